@@ -1,0 +1,162 @@
+/*
+ * uttt_amd.h -- C ABI of the MI355X (gfx950) uTTT hot-path library (libuttt_amd.so).
+ *
+ * Plain C: device pointers, int64 sizes/strides, scalars and a HIP stream.
+ * Nothing here allocates or frees device memory and no call synchronises the
+ * stream; every call only enqueues kernels on the stream it is given, so calls
+ * are stream-ordered and safe to record into a HIP graph.  Buffers (including
+ * workspace) belong to the caller.  Every entry point returns UTTT_OK (0) or an
+ * error code; uttt_last_error() then describes the failure (per host thread).
+ *
+ * Shapes follow the reference PyTorch modules of Phova/uTTTCompanion
+ * (model/uttt_layer.py).  "Row" = one batch row / one request, each with its own
+ * fp32 fast-weight state.  Layouts: activations (B, T, D) with the feature dim
+ * contiguous and a token stride of D; state W_up/W_gate (B, D, F), W_down (B, F, D)
+ * contiguous per row (row stride given separately; 0 = one matrix shared by all rows).
+ */
+#ifndef UTTT_AMD_H
+#define UTTT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* uttt_stream_t; /* a hipStream_t; NULL = the default stream */
+
+enum { UTTT_DTYPE_F32 = 0, UTTT_DTYPE_BF16 = 1 };
+enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE = 3 };
+
+/* Text of the last error on this host thread ("" when none). */
+const char* uttt_last_error(void);
+/* ABI version of the structures below; the Python binding checks it. */
+int uttt_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * 1. Fused chunk fast-weight update + causal readout.
+ *    Replaces fused_chunk_ttt_step (model/uttt_layer.py:414-534), i.e.
+ *    analytical_swiglu_chunk_grad (:279-411) + clip (:468-489) + momentum and
+ *    decay (:493-511) + inactive-row select (:513-520) + readout (:525-533),
+ *    as called by SharedFastWeightPool.chunk_step (:697-771).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch;      /* B rows */
+  int64_t tokens;     /* C tokens in this chunk, 1..64 */
+  int64_t d_model;    /* D, multiple of 64 */
+  int64_t d_ff;       /* F, multiple of 64 */
+  int32_t act_dtype;  /* UTTT_DTYPE_F32 or UTTT_DTYPE_BF16: q/k/v/eta/alpha/out */
+  int32_t normalize_by_dim;
+  float momentum_beta, max_inner_grad_norm, eps;
+  /* chunk inputs, act_dtype; token stride D (eta/alpha: 1); row strides in elements */
+  const void* q; int64_t q_row_stride;
+  const void* k; int64_t k_row_stride;
+  const void* v; int64_t v_row_stride;
+  const void* eta; int64_t eta_row_stride;
+  const void* alpha; int64_t alpha_row_stride;
+  const float* token_mask; int64_t mask_row_stride; /* (B, C) fp32 or NULL */
+  /* write cursor (fp32 master state), row stride = D*F */
+  const float* w_up; const float* w_gate; const float* w_down;
+  const float* s_up; const float* s_gate; const float* s_down;
+  /* read snapshot for the readout (may equal the cursor); row stride 0 = shared */
+  const float* r_up; const float* r_gate; const float* r_down; int64_t r_row_stride;
+  const float* ln_weight; const float* ln_bias; /* (D,) fp32 */
+  /* outputs: new state (may alias the cursor for in-place), readout, surprise */
+  float* w_up_out; float* w_gate_out; float* w_down_out;
+  float* s_up_out; float* s_gate_out; float* s_down_out;
+  void* out; int64_t out_row_stride; /* (B, C, D) act_dtype */
+  float* surprise;                   /* device scalar (fp32) */
+} uttt_chunk_update_args;
+
+size_t uttt_chunk_update_workspace(int64_t batch, int64_t d_model, int64_t d_ff, int32_t act_dtype);
+int uttt_chunk_update(const uttt_chunk_update_args* args, void* workspace, size_t workspace_bytes,
+                      uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 2. Frozen fast-weight readout f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down).
+ *    Replaces swiglu_fast_forward (model/uttt_layer.py:211-247) as used by
+ *    SharedFastWeightPool.forward_readout (:670-695) and the packed inference
+ *    readout swiglu_packed_forward (:250-257) / CUDAGraphDecoder (engine/inference.py:263-276).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch, tokens, d_model, d_ff; /* tokens: any T >= 1 */
+  int32_t act_dtype;
+  float eps;
+  const void* x; int64_t x_row_stride;
+  const float* w_up; const float* w_gate; const float* w_down; int64_t w_row_stride; /* 0 = shared */
+  const float* ln_weight; const float* ln_bias;
+  void* out; int64_t out_row_stride;
+} uttt_readout_args;
+
+size_t uttt_readout_workspace(int64_t batch, int64_t tokens, int64_t d_model, int64_t d_ff, int32_t act_dtype);
+int uttt_swiglu_readout(const uttt_readout_args* args, void* workspace, size_t workspace_bytes,
+                        uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 3. RoPE on q/k + KV append.  Replaces RotaryEmbedding.forward + apply_rope
+ *    (model/uttt_layer.py:935-958) and the cache concatenation (:1082-1102).
+ *    q is rotated in place; rotated k and v are written into the caller's KV
+ *    buffers at time index kv_offset + t.  Position of token t = start_pos + t.
+ *    cos/sin: fp32 tables (positions, head_dim) built as in RotaryEmbedding._build_cache (:910-933).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch, tokens, n_heads, n_kv_heads, head_dim;
+  int32_t act_dtype;
+  int64_t start_pos, table_len;
+  const float* cos_table; const float* sin_table;
+  void* q; int64_t q_stride_b, q_stride_t, q_stride_h;       /* rotated in place */
+  const void* k; int64_t k_stride_b, k_stride_t, k_stride_h;
+  const void* v; int64_t v_stride_b, v_stride_t, v_stride_h;
+  void* k_cache; void* v_cache; int64_t kv_stride_b, kv_stride_h, kv_stride_t; int64_t kv_offset;
+} uttt_rope_append_args;
+
+int uttt_rope_kv_append(const uttt_rope_append_args* args, uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 4. Sliding-window GQA attention for prefill / multi-token steps.
+ *    Replaces the SDPA / FlexAttention dispatch of SlidingWindowAttention.forward
+ *    (model/uttt_layer.py:1119-1165) with its mask (:1028-1056): query i (absolute
+ *    key index q_offset + i) sees key j iff 0 <= q_offset + i - j < window and
+ *    j < kv_len; kv head = h / (n_heads / n_kv_heads); softmax scale 1/sqrt(head_dim).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch, n_heads, n_kv_heads, q_len, kv_len, head_dim; /* head_dim 64 or 128 */
+  int64_t q_offset, window;
+  int32_t act_dtype; /* bf16 or fp32 */
+  float scale;
+  const void* q; int64_t q_stride_b, q_stride_h, q_stride_t;
+  const void* k; int64_t k_stride_b, k_stride_h, k_stride_t;
+  const void* v; int64_t v_stride_b, v_stride_h, v_stride_t;
+  void* out; int64_t o_stride_b, o_stride_h, o_stride_t;
+} uttt_swa_prefill_args;
+
+int uttt_swa_prefill(const uttt_swa_prefill_args* args, uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 5. One decode step over ring-buffer SWA KV caches for N independent requests.
+ *    Replaces CUDAGraphDecoder._forward's per-layer ring write + masked SDPA
+ *    (engine/inference.py:244-259) and the eager seq_len==1 branch
+ *    (model/uttt_layer.py:1082-1124).  Request n at position p = positions[n]:
+ *    RoPE at p (when tables are given), k/v written to slot p mod window, then
+ *    attention over slots < min(p + 1, window).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t n_req, n_heads, n_kv_heads, head_dim, window;
+  int32_t act_dtype;
+  float scale;
+  const int64_t* positions;                      /* device, (N,) */
+  const float* cos_table; const float* sin_table; int64_t table_len; /* NULL: inputs pre-rotated */
+  const void* q; int64_t q_stride_n;             /* (N, H, hd), head stride hd */
+  const void* k_new; const void* v_new; int64_t kv_new_stride_n; /* (N, Hkv, hd) */
+  void* k_ring; void* v_ring; int64_t ring_stride_n; /* (N, Hkv, window, hd) */
+  void* out; int64_t o_stride_n;                 /* (N, H, hd) */
+} uttt_swa_decode_args;
+
+int uttt_swa_decode(const uttt_swa_decode_args* args, uttt_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UTTT_AMD_H */

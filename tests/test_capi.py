@@ -1,0 +1,88 @@
+"""The C-ABI library loads, exports every function include/uttt_amd.h declares, and the
+ctypes structures match the C layout (checked against gcc's offsetof on the header).
+No kernel is launched: only host-side calls that return before touching a GPU."""
+import ctypes as C
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from utttcompanion_amd import _native as N
+from utttcompanion_amd import build
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "uttt_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(uttt_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(build.LIB_PATH):
+        build.build()
+    return N.load_library()
+
+
+def test_every_declared_symbol_is_exported_and_typed(lib):
+    names = declared_functions()
+    assert len(names) >= 9
+    for name in names:
+        assert name in N.SIGNATURES, f"{name} has no ctypes signature"
+        assert hasattr(lib, name), f"{name} not exported"
+    assert set(N.SIGNATURES) == set(names)
+
+
+def test_struct_layouts_match_the_c_header(tmp_path):
+    structs = {"uttt_chunk_update_args": N.ChunkUpdateArgs, "uttt_readout_args": N.ReadoutArgs,
+               "uttt_rope_append_args": N.RopeAppendArgs, "uttt_swa_prefill_args": N.SwaPrefillArgs,
+               "uttt_swa_decode_args": N.SwaDecodeArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], check=True, stdout=subprocess.PIPE, text=True).stdout.split("\n")
+    got = {}
+    for line in out:
+        if line:
+            cname, field, value = line.split()
+            got[(cname, field)] = int(value)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == C.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[(cname, field)] == getattr(py, field).offset, f"{cname}.{field}"
+
+
+def test_host_side_calls(lib):
+    assert lib.uttt_abi_version() == N.ABI_VERSION
+    ws = lib.uttt_chunk_update_workspace(8, 768, 2048, N.DTYPE_BF16)
+    assert ws > 8 * 64 * 2048 * 4
+    assert lib.uttt_chunk_update_workspace(8, 770, 2048, N.DTYPE_BF16) == 0  # invalid d_model
+    assert lib.uttt_readout_workspace(2, 100, 512, 1024, N.DTYPE_F32) > 0
+
+
+def test_invalid_arguments_are_rejected_before_any_launch(lib):
+    a = N.ChunkUpdateArgs()
+    a.batch, a.tokens, a.d_model, a.d_ff = 1, 0, 512, 1024
+    rc = lib.uttt_chunk_update(C.byref(a), None, 0, None)
+    assert rc == 1
+    assert b"tokens per chunk" in lib.uttt_last_error()
+    p = N.SwaPrefillArgs()
+    p.batch, p.n_heads, p.n_kv_heads, p.head_dim = 1, 4, 3, 64
+    assert lib.uttt_swa_prefill(C.byref(p), None) == 1
+    assert b"n_kv_heads" in lib.uttt_last_error()
+    d = N.SwaDecodeArgs()
+    d.head_dim = 96
+    assert lib.uttt_swa_decode(C.byref(d), None) == 1
+    assert b"head_dim" in lib.uttt_last_error()

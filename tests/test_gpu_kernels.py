@@ -1,0 +1,278 @@
+"""GPU parity of the HIP kernels against the CPU oracle (same seeded inputs).
+
+Tolerances (north star): fp32 paths <= 1e-5 relative error, measured as
+max|gpu - oracle| / max|oracle| per tensor; updated fp32 fast weights from bf16
+activations <= 2e-2 max-abs against the fp32 oracle.  bf16 *activations* (readouts)
+are stored with an 8-bit mantissa, so one unit in the last place at |x| in [4, 8) is
+already 0.031: they must satisfy |gpu - fp32| <= 2e-2 + 2^-7 |fp32| elementwise AND be
+no less accurate than the reference's own bf16 arithmetic (the oracle run on bf16
+inputs, which rounds u, g, h, z to bf16 as the reference does):
+max|gpu - fp32| <= 1.5 max|ref_bf16 - fp32| + 1e-3.  RoPE is bit-exact (the kernel
+reproduces the reference's operation order and rounding).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import uttt_math as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+F32_REL = 1e-5
+BF16_ABS = 2e-2
+
+
+def rel_err(actual, expected):
+    actual = actual.detach().double().cpu()
+    expected = expected.detach().double().cpu()
+    scale = expected.abs().max().item()
+    return (actual - expected).abs().max().item() / max(scale, 1e-30)
+
+
+def max_abs(actual, expected):
+    return (actual.detach().double().cpu() - expected.detach().double().cpu()).abs().max().item()
+
+
+def check_bf16_activation(name, got, fp32_ref, bf16_ref):
+    got, fp32_ref, bf16_ref = (t.detach().double().cpu() for t in (got, fp32_ref, bf16_ref))
+    diff = (got - fp32_ref).abs()
+    bound = 2e-2 + 2.0 ** -7 * fp32_ref.abs()
+    worst = (diff - bound).max().item()
+    assert worst <= 0, f"{name}: exceeds 2e-2 + 2^-7|x| by {worst:.3e}"
+    ours, theirs = diff.max().item(), (bf16_ref - fp32_ref).abs().max().item()
+    assert ours <= 1.5 * theirs + 1e-3, f"{name}: max err {ours:.3e} vs reference-bf16 {theirs:.3e}"
+
+
+def kernels():
+    from utttcompanion_amd import kernels as K
+    return K
+
+
+def make_chunk(b, c, d, f, seed, scale_w=None):
+    g = torch.Generator().manual_seed(seed)
+    sw = scale_w if scale_w is not None else 1.0 / math.sqrt(d)
+    q, k, v = (torch.randn(b, c, d, generator=g) for _ in range(3))
+    eta = 0.01 * torch.sigmoid(torch.randn(b, c, 1, generator=g))
+    alpha = 0.005 * torch.sigmoid(torch.randn(b, c, 1, generator=g) - 1.386)
+    w = (torch.randn(b, d, f, generator=g) * sw, torch.randn(b, d, f, generator=g) * sw,
+         torch.randn(b, f, d, generator=g) * 0.1 / math.sqrt(f))
+    s = tuple(torch.randn(t.shape, generator=g) * 1e-3 for t in w)
+    ln_w = 1.0 + 0.1 * torch.randn(d, generator=g)
+    ln_b = 0.05 * torch.randn(d, generator=g)
+    return q, k, v, eta, alpha, w, s, ln_w, ln_b
+
+
+def to_dev(*ts):
+    return [t.to(DEV) if t is not None else None for t in ts]
+
+
+@pytest.mark.parametrize("case", [
+    dict(b=1, c=64, d=512, f=1024, mask=False, read=False, clip=1.0, norm=True),   # config-1 chunk shape
+    dict(b=2, c=40, d=128, f=256, mask=True, read=True, clip=1.0, norm=True),     # tail chunk, mask, snapshot
+    dict(b=3, c=64, d=192, f=320, mask=True, read=False, clip=0.0, norm=False),   # no clip, 1/1 scale
+    dict(b=2, c=64, d=64, f=128, mask=False, read=True, clip=1e-4, norm=True),    # clip active
+])
+def test_chunk_update_fp32_matches_oracle(case):
+    K = kernels()
+    b, c, d, f = case["b"], case["c"], case["d"], case["f"]
+    print(f"case {case}", flush=True)
+    q, k, v, eta, alpha, w, s, ln_w, ln_b = make_chunk(b, c, d, f, seed=11 + b + c)
+    mask = None
+    if case["mask"]:
+        mask = torch.ones(b, c)
+        mask[0, c // 2:] = 0
+        if b > 2:
+            mask[2] = 0  # a row with no valid token keeps W and S
+    read = None
+    if case["read"]:
+        read = tuple(t + 0.01 * torch.randn_like(t) for t in w)
+    ref = om.fused_chunk_ttt_step(q, k, v, eta, alpha, *w, *s, ln_w, ln_b, mask, 0.9, case["clip"], case["norm"],
+                                  1e-5, *(read if read else (None, None, None)))
+    dev_in = to_dev(q, k, v, eta, alpha, *w, *s, ln_w, ln_b, mask)
+    dev_read = to_dev(*read) if read else (None, None, None)
+    with torch.no_grad():
+        got = K.chunk_update(*dev_in[:13], dev_in[13], 0.9, case["clip"], case["norm"], 1e-5, *dev_read)
+    torch.cuda.synchronize()
+    names = ("readout", "w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down", "surprise")
+    for name, a, e in zip(names, got, ref):
+        err = rel_err(a, e)
+        assert err <= F32_REL, f"{name}: rel err {err:.3e}"
+    if case["mask"] and b > 2:
+        for a, o in zip(got[1:7], w + s):
+            assert torch.equal(a[2].cpu(), o[2]), "inactive row changed"
+
+
+def test_chunk_update_fp32_sixteen_chunks_config1():
+    """Config 1: B=1, T=1024 as 16 sequential chunks; each chunk reads its pre-update W."""
+    K = kernels()
+    b, d, f, T = 1, 512, 1024, 1024
+    q, k, v, eta, alpha, w, s, ln_w, ln_b = make_chunk(b, T, d, f, seed=5, scale_w=0.02)
+    s = tuple(torch.zeros_like(t) for t in w)
+    ref_w, ref_s, ref_outs = w, s, []
+    dev = to_dev(q, k, v, eta, alpha, ln_w, ln_b)
+    cur = to_dev(*w, *s)
+    outs, surprises = [], []
+    with torch.no_grad():
+        for i in range(T // 64):
+            sl = slice(64 * i, 64 * (i + 1))
+            r = om.fused_chunk_ttt_step(q[:, sl], k[:, sl], v[:, sl], eta[:, sl], alpha[:, sl], *ref_w, *ref_s,
+                                        ln_w, ln_b, None, 0.9, 1.0, True, 1e-5)
+            ref_outs.append(r[0])
+            ref_w, ref_s = r[1:4], r[4:7]
+            g = K.chunk_update(dev[0][:, sl], dev[1][:, sl], dev[2][:, sl], dev[3][:, sl], dev[4][:, sl], *cur,
+                               dev[5], dev[6], None, 0.9, 1.0, True, 1e-5)
+            outs.append(g[0])
+            surprises.append(g[7])
+            cur = list(g[1:7])
+    torch.cuda.synchronize()
+    assert rel_err(torch.cat(outs, 1), torch.cat(ref_outs, 1)) <= F32_REL
+    for a, e in zip(cur, ref_w + ref_s):
+        assert rel_err(a, e) <= F32_REL
+
+
+def test_chunk_update_in_place_equals_out_of_place():
+    K = kernels()
+    q, k, v, eta, alpha, w, s, ln_w, ln_b = make_chunk(2, 64, 128, 192, seed=3)
+    dev = to_dev(q, k, v, eta, alpha, *w, *s, ln_w, ln_b)
+    with torch.no_grad():
+        fresh = K.chunk_update(*dev[:13], None, 0.9, 1.0, True, 1e-5)
+        state = [t.clone() for t in dev[5:11]]
+        inplace = K.chunk_update(*dev[:5], *state, *dev[11:13], None, 0.9, 1.0, True, 1e-5, out_state=state)
+    torch.cuda.synchronize()
+    for a, e in zip(inplace[:7], fresh[:7]):
+        assert torch.equal(a, e)
+    assert inplace[1].data_ptr() == state[0].data_ptr()
+
+
+@pytest.mark.parametrize("b,c,d,f", [(1, 64, 512, 1024), (2, 64, 768, 2048), (2, 37, 256, 512)])
+def test_chunk_update_bf16_within_tolerance_of_fp32_oracle(b, c, d, f):
+    K = kernels()
+    print(f"bf16 chunk b={b} c={c} d={d} f={f}", flush=True)
+    q, k, v, eta, alpha, w, s, ln_w, ln_b = make_chunk(b, c, d, f, seed=17 + d)
+    q16, k16, v16, e16, a16 = (t.bfloat16() for t in (q, k, v, eta, alpha))
+    ref = om.fused_chunk_ttt_step(q16.float(), k16.float(), v16.float(), e16.float(), a16.float(), *w, *s,
+                                  ln_w, ln_b, None, 0.9, 1.0, True, 1e-5)
+    ref16 = om.fused_chunk_ttt_step(q16, k16, v16, e16, a16, *w, *s, ln_w, ln_b, None, 0.9, 1.0, True, 1e-5)
+    with torch.no_grad():
+        got = K.chunk_update(*to_dev(q16, k16, v16, e16, a16, *w, *s, ln_w, ln_b), None, 0.9, 1.0, True, 1e-5)
+    torch.cuda.synchronize()
+    assert got[0].dtype == torch.bfloat16 and got[1].dtype == torch.float32
+    check_bf16_activation("readout", got[0], ref[0], ref16[0])
+    for name, a, e in zip(("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down"), got[1:7], ref[1:7]):
+        err = max_abs(a, e)
+        assert err <= BF16_ABS, f"{name}: max abs {err:.3e}"
+    assert abs(got[7].item() - ref[7].item()) <= 2e-2 * max(1.0, abs(ref[7].item()))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shared", [False, True])
+def test_swiglu_readout_matches_oracle(dtype, shared):
+    K = kernels()
+    b, t, d, f = 3, 150, 256, 512
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(b, t, d, generator=g).to(dtype)
+    wb = 1 if shared else b
+    w = (torch.randn(wb, d, f, generator=g) / 16, torch.randn(wb, d, f, generator=g) / 16,
+         torch.randn(wb, f, d, generator=g) / 64)
+    ln_w, ln_b = 1 + 0.1 * torch.randn(d, generator=g), 0.1 * torch.randn(d, generator=g)
+    ref = om.swiglu_fast_forward(x.float(), *(t_.expand(b, -1, -1) for t_ in w), ln_w, ln_b, 1e-5)
+    with torch.no_grad():
+        got = K.swiglu_readout(*to_dev(x, *(t_.expand(b, -1, -1) for t_ in w), ln_w, ln_b), eps=1e-5)
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert rel_err(got, ref) <= F32_REL
+    else:
+        ref16 = om.swiglu_fast_forward(x, *(t_.expand(b, -1, -1) for t_ in w), ln_w, ln_b, 1e-5)
+        check_bf16_activation("readout", got, ref, ref16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rope_append_is_bit_exact(dtype):
+    K = kernels()
+    b, t, h, hkv, hd = 2, 7, 4, 2, 64
+    g = torch.Generator().manual_seed(29)
+    q = torch.randn(b, t, h, hd, generator=g).to(dtype)
+    k = torch.randn(b, t, hkv, hd, generator=g).to(dtype)
+    v = torch.randn(b, t, hkv, hd, generator=g).to(dtype)
+    cos, sin = om.rope_tables(hd, 64)
+    start = 9
+    ref_q = om.apply_rope(q.transpose(1, 2), cos[start:start + t], sin[start:start + t])
+    ref_k = om.apply_rope(k.transpose(1, 2), cos[start:start + t], sin[start:start + t])
+    dq, dk, dv, dcos, dsin = to_dev(q.clone(), k, v, cos, sin)
+    kc = torch.zeros(b, hkv, 20, hd, dtype=dtype, device=DEV)
+    vc = torch.zeros_like(kc)
+    K.rope_kv_append(dq, dk, dv, dcos, dsin, start, kc, vc, 5)
+    torch.cuda.synchronize()
+    assert torch.equal(dq.transpose(1, 2).cpu(), ref_q)
+    assert torch.equal(kc[:, :, 5:5 + t].cpu(), ref_k)
+    assert torch.equal(vc[:, :, 5:5 + t].cpu(), v.transpose(1, 2))
+    assert kc[:, :, :5].abs().sum().item() == 0 and kc[:, :, 5 + t:].abs().sum().item() == 0
+
+
+@pytest.mark.parametrize("case", [
+    dict(b=2, h=12, hkv=4, tq=300, tkv=300, hd=64, win=128),     # multi-tile window, ragged tail
+    dict(b=1, h=4, hkv=4, tq=64, tkv=575, hd=64, win=512),       # chunk step over a cache (C2 shape)
+    dict(b=1, h=16, hkv=4, tq=130, tkv=400, hd=128, win=1024),   # hd 128, window > kv (causal)
+    dict(b=2, h=4, hkv=1, tq=70, tkv=70, hd=64, win=1),          # window 1: self only
+])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_swa_prefill_matches_oracle(case, dtype):
+    K = kernels()
+    print(f"swa prefill {case} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(31)
+    b, h, hkv, tq, tkv, hd, win = (case[k] for k in ("b", "h", "hkv", "tq", "tkv", "hd", "win"))
+    q = torch.randn(b, tq, h, hd, generator=g).to(dtype).transpose(1, 2)
+    k = torch.randn(b, hkv, tkv, hd, generator=g).to(dtype)
+    v = torch.randn(b, hkv, tkv, hd, generator=g).to(dtype)
+    off = tkv - tq
+    ref = om.sliding_window_attention(q.float(), k.float(), v.float(), win, off)
+    with torch.no_grad():
+        got = K.swa_prefill(*to_dev(q, k, v), win, off)
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert rel_err(got, ref) <= F32_REL
+    else:
+        assert max_abs(got, ref) <= BF16_ABS
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("hd", [64, 128])
+def test_swa_decode_ring_matches_full_prefix(dtype, hd):
+    """Ragged positions, several window wraps; RoPE applied inside the kernel."""
+    K = kernels()
+    n, h, hkv, win, steps = 5, 12, 4, 16, 40
+    g = torch.Generator().manual_seed(37)
+    starts = [0, 3, 15, 16, 33]
+    total = max(starts) + steps
+    qs = torch.randn(n, total, h, hd, generator=g).to(dtype)
+    ks = torch.randn(n, total, hkv, hd, generator=g).to(dtype)
+    vs = torch.randn(n, total, hkv, hd, generator=g).to(dtype)
+    cos, sin = om.rope_tables(hd, 256)
+    rq = om.apply_rope(qs.transpose(1, 2), cos[:total], sin[:total])  # (n, h, total, hd)
+    rk = om.apply_rope(ks.transpose(1, 2), cos[:total], sin[:total])
+    rv = vs.transpose(1, 2)
+    k_ring = torch.zeros(n, hkv, win, hd, dtype=dtype)
+    v_ring = torch.zeros_like(k_ring)
+    for r, p0 in enumerate(starts):  # history before the first step, already rotated
+        for j in range(max(0, p0 - win), p0):
+            k_ring[r, :, j % win] = rk[r, :, j]
+            v_ring[r, :, j % win] = rv[r, :, j]
+    dk_ring, dv_ring, dcos, dsin = to_dev(k_ring, v_ring, cos, sin)
+    with torch.no_grad():
+        for step in range(steps):
+            pos = [p0 + step for p0 in starts]
+            q = torch.stack([qs[r, p] for r, p in enumerate(pos)])
+            kn = torch.stack([ks[r, p] for r, p in enumerate(pos)])
+            vn = torch.stack([vs[r, p] for r, p in enumerate(pos)])
+            positions = torch.tensor(pos, dtype=torch.int64, device=DEV)
+            got = K.swa_decode(*to_dev(q, kn, vn), dk_ring, dv_ring, positions, dcos, dsin)
+            for r, p in enumerate(pos):
+                want = om.sliding_window_attention(rq[r:r + 1, :, p:p + 1].float(), rk[r:r + 1, :, :p + 1].float(),
+                                                   rv[r:r + 1, :, :p + 1].float(), win, p)[0, :, 0]
+                a = got[r].float().cpu()
+                if dtype == torch.float32:
+                    assert rel_err(a, want) <= F32_REL, f"step {step} req {r}"
+                else:
+                    assert max_abs(a, want) <= BF16_ABS, f"step {step} req {r}"
+    torch.cuda.synchronize()

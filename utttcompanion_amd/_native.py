@@ -1,0 +1,140 @@
+"""ctypes binding of libuttt_amd.so (the C ABI declared in include/uttt_amd.h).
+
+The library is loaded lazily on first use and there is no fallback: a missing or
+stale library raises ``RuntimeError`` naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+from .build import LIB_PATH
+
+ABI_VERSION = 1
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+_P = C.c_void_p
+_I64 = C.c_int64
+_I32 = C.c_int32
+_F = C.c_float
+
+
+class ChunkUpdateArgs(C.Structure):
+    _fields_ = [
+        ("batch", _I64), ("tokens", _I64), ("d_model", _I64), ("d_ff", _I64),
+        ("act_dtype", _I32), ("normalize_by_dim", _I32),
+        ("momentum_beta", _F), ("max_inner_grad_norm", _F), ("eps", _F),
+        ("q", _P), ("q_row_stride", _I64),
+        ("k", _P), ("k_row_stride", _I64),
+        ("v", _P), ("v_row_stride", _I64),
+        ("eta", _P), ("eta_row_stride", _I64),
+        ("alpha", _P), ("alpha_row_stride", _I64),
+        ("token_mask", _P), ("mask_row_stride", _I64),
+        ("w_up", _P), ("w_gate", _P), ("w_down", _P),
+        ("s_up", _P), ("s_gate", _P), ("s_down", _P),
+        ("r_up", _P), ("r_gate", _P), ("r_down", _P), ("r_row_stride", _I64),
+        ("ln_weight", _P), ("ln_bias", _P),
+        ("w_up_out", _P), ("w_gate_out", _P), ("w_down_out", _P),
+        ("s_up_out", _P), ("s_gate_out", _P), ("s_down_out", _P),
+        ("out", _P), ("out_row_stride", _I64),
+        ("surprise", _P),
+    ]
+
+
+class ReadoutArgs(C.Structure):
+    _fields_ = [
+        ("batch", _I64), ("tokens", _I64), ("d_model", _I64), ("d_ff", _I64),
+        ("act_dtype", _I32), ("eps", _F),
+        ("x", _P), ("x_row_stride", _I64),
+        ("w_up", _P), ("w_gate", _P), ("w_down", _P), ("w_row_stride", _I64),
+        ("ln_weight", _P), ("ln_bias", _P),
+        ("out", _P), ("out_row_stride", _I64),
+    ]
+
+
+class RopeAppendArgs(C.Structure):
+    _fields_ = [
+        ("batch", _I64), ("tokens", _I64), ("n_heads", _I64), ("n_kv_heads", _I64), ("head_dim", _I64),
+        ("act_dtype", _I32),
+        ("start_pos", _I64), ("table_len", _I64),
+        ("cos_table", _P), ("sin_table", _P),
+        ("q", _P), ("q_stride_b", _I64), ("q_stride_t", _I64), ("q_stride_h", _I64),
+        ("k", _P), ("k_stride_b", _I64), ("k_stride_t", _I64), ("k_stride_h", _I64),
+        ("v", _P), ("v_stride_b", _I64), ("v_stride_t", _I64), ("v_stride_h", _I64),
+        ("k_cache", _P), ("v_cache", _P), ("kv_stride_b", _I64), ("kv_stride_h", _I64), ("kv_stride_t", _I64),
+        ("kv_offset", _I64),
+    ]
+
+
+class SwaPrefillArgs(C.Structure):
+    _fields_ = [
+        ("batch", _I64), ("n_heads", _I64), ("n_kv_heads", _I64), ("q_len", _I64), ("kv_len", _I64),
+        ("head_dim", _I64), ("q_offset", _I64), ("window", _I64),
+        ("act_dtype", _I32), ("scale", _F),
+        ("q", _P), ("q_stride_b", _I64), ("q_stride_h", _I64), ("q_stride_t", _I64),
+        ("k", _P), ("k_stride_b", _I64), ("k_stride_h", _I64), ("k_stride_t", _I64),
+        ("v", _P), ("v_stride_b", _I64), ("v_stride_h", _I64), ("v_stride_t", _I64),
+        ("out", _P), ("o_stride_b", _I64), ("o_stride_h", _I64), ("o_stride_t", _I64),
+    ]
+
+
+class SwaDecodeArgs(C.Structure):
+    _fields_ = [
+        ("n_req", _I64), ("n_heads", _I64), ("n_kv_heads", _I64), ("head_dim", _I64), ("window", _I64),
+        ("act_dtype", _I32), ("scale", _F),
+        ("positions", _P),
+        ("cos_table", _P), ("sin_table", _P), ("table_len", _I64),
+        ("q", _P), ("q_stride_n", _I64),
+        ("k_new", _P), ("v_new", _P), ("kv_new_stride_n", _I64),
+        ("k_ring", _P), ("v_ring", _P), ("ring_stride_n", _I64),
+        ("out", _P), ("o_stride_n", _I64),
+    ]
+
+
+# exported symbol -> (restype, argtypes)
+SIGNATURES = {
+    "uttt_last_error": (C.c_char_p, []),
+    "uttt_abi_version": (C.c_int, []),
+    "uttt_chunk_update_workspace": (C.c_size_t, [_I64, _I64, _I64, _I32]),
+    "uttt_chunk_update": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _P]),
+    "uttt_readout_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
+    "uttt_swiglu_readout": (C.c_int, [C.POINTER(ReadoutArgs), _P, C.c_size_t, _P]),
+    "uttt_rope_kv_append": (C.c_int, [C.POINTER(RopeAppendArgs), _P]),
+    "uttt_swa_prefill": (C.c_int, [C.POINTER(SwaPrefillArgs), _P]),
+    "uttt_swa_decode": (C.c_int, [C.POINTER(SwaDecodeArgs), _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Load (once) and type the HIP library; raise if it is absent or of another ABI."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"{path} is missing: the uTTT HIP kernels are not built "
+                "(run `python -m utttcompanion_amd.build`); there is no fallback path")
+        lib = C.CDLL(path)
+        for name, (res, argt) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = argt
+        version = lib.uttt_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}: rebuild it")
+        _lib = lib
+        return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load_library().uttt_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {status}): {msg}")

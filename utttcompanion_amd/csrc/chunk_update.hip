@@ -1,0 +1,702 @@
+// Fused chunk fast-weight update and frozen readout for the uTTT shared fast-weight
+// pool, written for gfx950 (MI355X).
+//
+// Math (per row b; K, V, Q are C x D chunk activations, W fp32 master state):
+//   U = K W_up, G = K W_gate, H = SiLU(G) * U, Z = H W_down
+//   Zh = LN(Z) (fp32 stats), E = K + gamma*Zh + beta - V, loss_t = 0.5 |E_t|^2 / s
+//   dZh = (w_t / s) E gamma, dZ = rstd (dZh - mean(dZh) - Zh mean(dZh Zh))
+//   gW_down = H^T dZ, dH = dZ W_down^T, dU = dH G sig(G), dG = dH U sig(G)(1 + G(1 - sig(G)))
+//   gW_up = K^T dU, gW_gate = K^T dG
+//   clip c = min(1, tau / sqrt(|g|^2 + 1e-8)); S' = beta S - c g; W' = (1 - mean alpha) W + S'
+//   readout O = Q + LN((SiLU(Q R_gate) * Q R_up) R_down)   (R = read snapshot)
+// (reference: model/uttt_layer.py:279-534)
+//
+// Kernel sequence for one chunk (all rows in each launch):
+//   1. k_up_gate      U/G/H for the K path (cursor W) and the Q path (read W), per F tile
+//   2. k_down_partial Z partial sums over F splits, per D tile
+//   3. k_ln_grad      LN + loss + dZ per token (K path)
+//   4. k_ln_readout   LN + residual readout per token (Q path)
+//   5. k_backward     dH, dU, dG per F tile + the per-row squared gradient norm partial
+//   6. k_apply        recompute each gradient tile from the small activations and apply
+//                     clip / momentum / decay / inactive-row select to W and S in one pass
+// Steps 1, 2 and 4 alone are the frozen readout.
+#include "uttt_device.h"
+#include "uttt_host.h"
+
+namespace uttt {
+
+constexpr int KT = 64;  // K depth of one LDS stage
+
+template <typename T> constexpr int lds_ld() { return KT + Mma<T>::kPad; }
+
+struct FwdArgs {
+  int B, D, F, ntok, ntb, tok_pad, nsplit;
+  const void* x[2];
+  int64_t x_rs[2];
+  const float* wu[2];
+  const float* wg[2];
+  const float* wd[2];
+  int64_t w_rs[2];
+  float* u_store;  // fp32 (B, tok_pad, F), path 0 only; may be null
+  float* g_store;
+  void* h[2];      // act dtype (B, tok_pad, F)
+  float* zp;       // fp32 (paths, nsplit, B, tok_pad, D)
+};
+
+// ---------------------------------------------------------------------------
+// 1. U, G, H for one (F tile, row, path, token block)
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ T xs[64 * LD];
+  __shared__ T us[64 * LD];
+  __shared__ T gs[64 * LD];
+  const int ft = blockIdx.x, b = blockIdx.y;
+  const int path = blockIdx.z / a.ntb, tb = blockIdx.z - path * a.ntb;
+  const int f0 = ft * 64, t0 = tb * 64;
+  const int rows = min(64, a.ntok - t0);
+  const T* x = static_cast<const T*>(a.x[path]) + (int64_t)b * a.x_rs[path] + (int64_t)t0 * a.D;
+  const float* wu = a.wu[path] + (int64_t)b * a.w_rs[path] + f0;
+  const float* wg = a.wg[path] + (int64_t)b * a.w_rs[path] + f0;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+
+  f32x16 au, ag;
+  zero(au);
+  zero(ag);
+  for (int d0 = 0; d0 < a.D; d0 += KT) {
+    stage_rows<T, T, KT>(xs, LD, x + d0, a.D, rows);
+    stage_cols<T, float, KT>(us, LD, wu + (int64_t)d0 * a.F, a.F, KT);
+    stage_cols<T, float, KT>(gs, LD, wg + (int64_t)d0 * a.F, a.F, KT);
+    __syncthreads();
+    wave_mma<T, KT>(au, xs + wr * LD, LD, us + wc * LD, LD);
+    wave_mma<T, KT>(ag, xs + wr * LD, LD, gs + wc * LD, LD);
+    __syncthreads();
+  }
+
+  const int64_t base = ((int64_t)b * a.tok_pad + t0) * a.F + f0;
+  T* h = static_cast<T*>(a.h[path]) + base;
+  const bool store_ug = path == 0 && a.u_store != nullptr;
+  const int col = wc + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = wr + acc_row(i);
+    const float u = au[i], g = ag[i];
+    const int64_t off = (int64_t)row * a.F + col;
+    h[off] = from_f32<T>((g * sigmoidf_acc(g)) * u);
+    if (store_ug) {
+      a.u_store[base + off] = u;
+      a.g_store[base + off] = g;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. Z partial = H[:, split] W_down[split, D tile]
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_down_partial(const FwdArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ T hs[64 * LD];
+  __shared__ T ws[64 * LD];
+  const int dt = blockIdx.x, split = blockIdx.y;
+  const int b = blockIdx.z % a.B, pt = blockIdx.z / a.B;
+  const int path = pt / a.ntb, tb = pt - path * a.ntb;
+  const int d0 = dt * 64, t0 = tb * 64;
+  const int nF = a.F / 64;
+  const int f_begin = (nF * split / a.nsplit) * 64, f_end = (nF * (split + 1) / a.nsplit) * 64;
+  const T* h = static_cast<const T*>(a.h[path]) + ((int64_t)b * a.tok_pad + t0) * a.F;
+  const float* wd = a.wd[path] + (int64_t)b * a.w_rs[path] + d0;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+
+  f32x16 acc;
+  zero(acc);
+  for (int f0 = f_begin; f0 < f_end; f0 += KT) {
+    stage_rows<T, T, KT>(hs, LD, h + f0, a.F, 64);
+    stage_cols<T, float, KT>(ws, LD, wd + (int64_t)f0 * a.D, a.D, KT);
+    __syncthreads();
+    wave_mma<T, KT>(acc, hs + wr * LD, LD, ws + wc * LD, LD);
+    __syncthreads();
+  }
+  float* zp = a.zp + ((((int64_t)path * a.nsplit + split) * a.B + b) * a.tok_pad + t0) * a.D + d0;
+  const int col = wc + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zp[(int64_t)(wr + acc_row(i)) * a.D + col] = acc[i];
+}
+
+// ---------------------------------------------------------------------------
+// 3. LayerNorm, reconstruction error, token loss and dZ (K path)
+// ---------------------------------------------------------------------------
+constexpr int kMaxPerThread = 16;  // D <= 4096
+
+struct LnGradArgs {
+  int B, C, D, nsplit, tok_pad, normalize;
+  float eps;
+  const float* zp;  // path-0 partials (nsplit, B, tok_pad, D)
+  const void* k; int64_t k_rs;
+  const void* v; int64_t v_rs;
+  const void* eta; int64_t eta_rs;
+  const float* mask; int64_t mask_rs;
+  const float* ln_w;
+  const float* ln_b;
+  void* dz;     // act dtype (B, 64, D)
+  float* loss;  // (B, 64): token loss times its mask value
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
+  __shared__ float red[4];
+  const int t = blockIdx.x, b = blockIdx.y;
+  T* dz = static_cast<T*>(a.dz) + ((int64_t)b * 64 + t) * a.D;
+  if (t >= a.C) {
+    for (int d = threadIdx.x; d < a.D; d += kThreads) dz[d] = from_f32<T>(0.f);
+    if (threadIdx.x == 0) a.loss[b * 64 + t] = 0.f;
+    return;
+  }
+  const T* kr = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs + (int64_t)t * a.D;
+  const T* vr = static_cast<const T*>(a.v) + (int64_t)b * a.v_rs + (int64_t)t * a.D;
+  const float inv_d = 1.0f / (float)a.D;
+
+  float z[kMaxPerThread];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    float acc = 0.f;
+    if (d < a.D) {
+      for (int sp = 0; sp < a.nsplit; ++sp)
+        acc += a.zp[(((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D + d];
+    }
+    z[i] = acc;
+    s += acc;
+  }
+  const float mean = block_sum(s, red) * inv_d;
+  float s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    if (d < a.D) {
+      const float c = z[i] - mean;
+      s2 += c * c;
+    }
+  }
+  const float var = block_sum(s2, red) * inv_d;
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+  const float inv_scale = a.normalize ? inv_d : 1.0f;
+
+  // z[] becomes z_hat, e[] the reconstruction error
+  float e[kMaxPerThread];
+  float se = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    e[i] = 0.f;
+    if (d < a.D) {
+      z[i] = (z[i] - mean) * rstd;
+      const float vhat = to_f32(kr[d]) + (z[i] * a.ln_w[d] + a.ln_b[d]);
+      e[i] = vhat - to_f32(vr[d]);
+      se += e[i] * e[i];
+    }
+  }
+  const float token_loss = 0.5f * block_sum(se, red) * inv_scale;
+
+  const float eta_t = to_f32(static_cast<const T*>(a.eta)[(int64_t)b * a.eta_rs + t]);
+  float weight, m_t = 1.f;
+  if (a.mask != nullptr) {
+    const float* mr = a.mask + (int64_t)b * a.mask_rs;
+    m_t = mr[t];
+    float cnt = threadIdx.x < a.C ? mr[threadIdx.x] : 0.f;
+    cnt = fmaxf(block_sum(cnt, red), 1.0f);
+    weight = (eta_t * m_t) / cnt;
+  } else {
+    weight = eta_t * (1.0f / (float)a.C);
+  }
+  const float coef = weight * inv_scale;
+
+  float s3 = 0.f, s4 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    if (d < a.D) {
+      e[i] = coef * e[i] * a.ln_w[d];  // dZ_hat
+      s3 += e[i];
+      s4 += e[i] * z[i];
+    }
+  }
+  const float m1 = block_sum(s3, red) * inv_d;
+  const float m2 = block_sum(s4, red) * inv_d;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    if (d < a.D) dz[d] = from_f32<T>(rstd * (e[i] - m1 - z[i] * m2));
+  }
+  if (threadIdx.x == 0) a.loss[b * 64 + t] = a.mask != nullptr ? token_loss * m_t : token_loss;
+}
+
+// ---------------------------------------------------------------------------
+// 4. Readout: out = x + LN(Z) with LN parameters rounded to the activation dtype
+// ---------------------------------------------------------------------------
+struct LnOutArgs {
+  int B, ntok, D, nsplit, tok_pad;
+  float eps;
+  const float* zp;  // partials of the readout path (nsplit, B, tok_pad, D)
+  const void* x; int64_t x_rs;
+  const float* ln_w;
+  const float* ln_b;
+  void* out; int64_t out_rs;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
+  __shared__ float red[4];
+  const int t = blockIdx.x, b = blockIdx.y;
+  if (t >= a.ntok) return;
+  const float inv_d = 1.0f / (float)a.D;
+  float z[kMaxPerThread];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    float acc = 0.f;
+    if (d < a.D) {
+      for (int sp = 0; sp < a.nsplit; ++sp)
+        acc += a.zp[(((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D + d];
+    }
+    z[i] = acc;
+    s += acc;
+  }
+  const float mean = block_sum(s, red) * inv_d;
+  float s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    if (d < a.D) {
+      const float c = z[i] - mean;
+      s2 += c * c;
+    }
+  }
+  const float rstd = 1.0f / sqrtf(block_sum(s2, red) * inv_d + a.eps);
+  const T* xr = static_cast<const T*>(a.x) + (int64_t)b * a.x_rs + (int64_t)t * a.D;
+  T* o = static_cast<T*>(a.out) + (int64_t)b * a.out_rs + (int64_t)t * a.D;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    if (d < a.D) {
+      const float g = to_f32(from_f32<T>(a.ln_w[d]));
+      const float be = to_f32(from_f32<T>(a.ln_b[d]));
+      o[d] = from_f32<T>(to_f32(xr[d]) + ((z[i] - mean) * rstd * g + be));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 5. dH = dZ W_down^T per F tile; dU, dG; squared-norm partial of all three gradients
+// ---------------------------------------------------------------------------
+struct BwdArgs {
+  int B, C, D, F;
+  const void* k; int64_t k_rs;
+  const float* wd; int64_t w_rs;
+  const float* u_store;
+  const float* g_store;
+  const void* h;   // K-path H (B, 64, F)
+  const void* dz;  // (B, 64, D)
+  void* du;        // (B, 64, F)
+  void* dg;
+  float* nrm;      // (B, F/64)
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_backward(const BwdArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ T buf0[64 * LD];  // dZ rows -> K^T tile -> H^T tile
+  __shared__ T buf1[64 * LD];  // W_down rows -> dZ^T tile
+  __shared__ T dus[64 * LD];   // dU^T  [f][t]
+  __shared__ T dgs[64 * LD];   // dG^T  [f][t]
+  __shared__ float red[4];
+  const int ft = blockIdx.x, b = blockIdx.y;
+  const int f0 = ft * 64;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  const T* dz = static_cast<const T*>(a.dz) + (int64_t)b * 64 * a.D;
+  const float* wd = a.wd + (int64_t)b * a.w_rs + (int64_t)f0 * a.D;
+
+  // dH tile [t][f] over the full D
+  f32x16 acc;
+  zero(acc);
+  for (int d0 = 0; d0 < a.D; d0 += KT) {
+    stage_rows<T, T, KT>(buf0, LD, dz + d0, a.D, 64);
+    stage_rows<T, float, KT>(buf1, LD, wd + d0, a.D, 64);
+    __syncthreads();
+    wave_mma<T, KT>(acc, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
+    __syncthreads();
+  }
+
+  const int64_t rowbase = (int64_t)b * 64 * a.F + f0;
+  {
+    const int f = wc + acc_col();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int t = wr + acc_row(i);
+      const int64_t off = rowbase + (int64_t)t * a.F + f;
+      const float u = a.u_store[off], g = a.g_store[off];
+      const float sg = sigmoidf_acc(g);
+      const float dh = acc[i];
+      const T du = from_f32<T>(dh * (g * sg));
+      const T dg = from_f32<T>(dh * u * (sg * (1.0f + g * (1.0f - sg))));
+      static_cast<T*>(a.du)[off] = du;
+      static_cast<T*>(a.dg)[off] = dg;
+      dus[f * LD + t] = du;
+      dgs[f * LD + t] = dg;
+    }
+  }
+  __syncthreads();
+
+  const T* kr = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs;
+  float sq = 0.f;
+  // |gW_up[:, tile]|^2 + |gW_gate[:, tile]|^2: rows d, cols f
+  for (int d0 = 0; d0 < a.D; d0 += 64) {
+    stage_cols<T, T, 64>(buf0, LD, kr + d0, a.D, a.C);  // K^T  [d][t]
+    __syncthreads();
+    f32x16 au, ag;
+    zero(au);
+    zero(ag);
+    wave_mma<T, 64>(au, buf0 + wr * LD, LD, dus + wc * LD, LD);
+    wave_mma<T, 64>(ag, buf0 + wr * LD, LD, dgs + wc * LD, LD);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sq += au[i] * au[i] + ag[i] * ag[i];
+    __syncthreads();
+  }
+  // |gW_down[tile, :]|^2: rows f, cols d
+  stage_cols<T, T, 64>(buf0, LD, static_cast<const T*>(a.h) + rowbase, a.F, 64);  // H^T [f][t]
+  for (int d0 = 0; d0 < a.D; d0 += 64) {
+    stage_cols<T, T, 64>(buf1, LD, dz + d0, a.D, 64);  // dZ^T [d][t]
+    __syncthreads();
+    f32x16 ad;
+    zero(ad);
+    wave_mma<T, 64>(ad, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sq += ad[i] * ad[i];
+    __syncthreads();
+  }
+  const float total = block_sum(sq, red);
+  if (threadIdx.x == 0) a.nrm[b * (a.F / 64) + ft] = total;
+}
+
+// ---------------------------------------------------------------------------
+// 6. Apply: recompute one gradient tile (K = the chunk's 64 token slots), then
+//    S' = beta S - c g, W' = (1 - alpha_bar) W + S', inactive rows copied through.
+// ---------------------------------------------------------------------------
+struct ApplyArgs {
+  int B, C, D, F;
+  float beta, max_norm;
+  const void* k; int64_t k_rs;
+  const void* alpha; int64_t alpha_rs;
+  const float* mask; int64_t mask_rs;
+  const void* h;
+  const void* dz;
+  const void* du;
+  const void* dg;
+  const float* nrm;
+  const float* loss;
+  const float* w[3];
+  const float* s[3];
+  float* w_out[3];
+  float* s_out[3];
+  float* surprise;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ T as[64 * LD];
+  __shared__ T bs[64 * LD];
+  __shared__ float row_scalar[3];
+  const int nD = a.D / 64, nF = a.F / 64;
+  const int per = nD * nF;
+  const int m = blockIdx.x / per, j = blockIdx.x - m * per, b = blockIdx.y;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    float n2 = 0.f;
+    for (int i = lane; i < nF; i += 64) n2 += a.nrm[b * nF + i];
+    n2 = wave_sum(n2);
+    float asum = 0.f, msum = 0.f, any = 0.f;
+    const T* al = static_cast<const T*>(a.alpha) + (int64_t)b * a.alpha_rs;
+    for (int t = lane; t < a.C; t += 64) {
+      if (a.mask != nullptr) {
+        const float mt = a.mask[(int64_t)b * a.mask_rs + t];
+        asum += to_f32(al[t]) * mt;
+        msum += mt;
+        any += (mt != 0.f) ? 1.f : 0.f;
+      } else {
+        asum += to_f32(al[t]);
+      }
+    }
+    asum = wave_sum(asum);
+    msum = wave_sum(msum);
+    any = wave_sum(any);
+    if (lane == 0) {
+      const float abar = a.mask != nullptr ? asum / fmaxf(msum, 1.f) : asum / (float)a.C;
+      row_scalar[0] = a.max_norm > 0.f ? fminf(a.max_norm * (1.0f / sqrtf(n2 + 1e-8f)), 1.0f) : 1.0f;
+      row_scalar[1] = 1.0f - abar;
+      row_scalar[2] = (a.mask == nullptr || any > 0.f) ? 1.f : 0.f;
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      // batch-global surprise: sum of masked token losses over all rows / valid tokens
+      float num = 0.f, den = 0.f;
+      for (int i = lane; i < a.B * 64; i += 64) {
+        const int bb = i >> 6, t = i & 63;
+        num += a.loss[i];
+        if (t < a.C) den += a.mask != nullptr ? a.mask[(int64_t)bb * a.mask_rs + t] : 1.f;
+      }
+      num = wave_sum(num);
+      den = wave_sum(den);
+      if (lane == 0) *a.surprise = a.mask != nullptr ? num / fmaxf(den, 1.f) : num / den;
+    }
+  }
+
+  int r0, c0, ld_out;
+  if (m < 2) {  // W_up / W_gate tile (d, f) = K^T dU / K^T dG
+    const int dt = j / nF, ft = j - dt * nF;
+    r0 = dt * 64;
+    c0 = ft * 64;
+    ld_out = a.F;
+    stage_cols<T, T, 64>(as, LD, static_cast<const T*>(a.k) + (int64_t)b * a.k_rs + r0, a.D, a.C);
+    const T* src = static_cast<const T*>(m == 0 ? a.du : a.dg) + (int64_t)b * 64 * a.F + c0;
+    stage_cols<T, T, 64>(bs, LD, src, a.F, 64);
+  } else {      // W_down tile (f, d) = H^T dZ
+    const int ft = j / nD, dt = j - ft * nD;
+    r0 = ft * 64;
+    c0 = dt * 64;
+    ld_out = a.D;
+    stage_cols<T, T, 64>(as, LD, static_cast<const T*>(a.h) + (int64_t)b * 64 * a.F + r0, a.F, 64);
+    stage_cols<T, T, 64>(bs, LD, static_cast<const T*>(a.dz) + (int64_t)b * 64 * a.D + c0, a.D, 64);
+  }
+  __syncthreads();
+  f32x16 acc;
+  zero(acc);
+  wave_mma<T, 64>(acc, as + wr * LD, LD, bs + wc * LD, LD);
+
+  const float clip = row_scalar[0], decay = row_scalar[1];
+  const bool active = row_scalar[2] != 0.f;
+  const int64_t mat = (int64_t)a.D * a.F;
+  const float* wsrc = a.w[m] + b * mat;
+  const float* ssrc = a.s[m] + b * mat;
+  float* wdst = a.w_out[m] + b * mat;
+  float* sdst = a.s_out[m] + b * mat;
+  const int col = c0 + wc + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
+    const float wv = wsrc[off], sv = ssrc[off];
+    float s_new, w_new;
+    {
+#pragma clang fp contract(off)
+      const float step = acc[i] * clip;
+      s_new = a.beta * sv - step;
+      w_new = decay * wv + s_new;
+    }
+    wdst[off] = active ? w_new : wv;
+    sdst[off] = active ? s_new : sv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+static int pick_nsplit(int64_t blocks_without_split, int64_t nF) {
+  int64_t s = (512 + blocks_without_split - 1) / blocks_without_split;
+  if (s < 1) s = 1;
+  if (s > nF) s = nF;
+  return (int)s;
+}
+
+static size_t act_bytes(int32_t dtype) { return dtype == UTTT_DTYPE_BF16 ? 2 : 4; }
+
+struct UpdateLayout {
+  size_t u, g, h0, h1, zp, dz, du, dg, loss, nrm, total;
+  int nsplit;
+};
+
+static UpdateLayout update_layout(int64_t B, int64_t D, int64_t F, int32_t dtype) {
+  UpdateLayout L;
+  const size_t e = act_bytes(dtype);
+  L.nsplit = pick_nsplit((D / 64) * B * 2, F / 64);
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t at = off; off += align_up(bytes); return at; };
+  L.u = take(sizeof(float) * B * 64 * F);
+  L.g = take(sizeof(float) * B * 64 * F);
+  L.h0 = take(e * B * 64 * F);
+  L.h1 = take(e * B * 64 * F);
+  L.zp = take(sizeof(float) * 2 * L.nsplit * B * 64 * D);
+  L.dz = take(e * B * 64 * D);
+  L.du = take(e * B * 64 * F);
+  L.dg = take(e * B * 64 * F);
+  L.loss = take(sizeof(float) * B * 64);
+  L.nrm = take(sizeof(float) * B * (F / 64));
+  L.total = off;
+  return L;
+}
+
+template <typename T>
+static void launch_update(const uttt_chunk_update_args& a, char* ws, const UpdateLayout& L, hipStream_t st) {
+  const int B = (int)a.batch, C = (int)a.tokens, D = (int)a.d_model, F = (int)a.d_ff;
+  FwdArgs f{};
+  f.B = B; f.D = D; f.F = F; f.ntok = C; f.ntb = 1; f.tok_pad = 64; f.nsplit = L.nsplit;
+  f.x[0] = a.k; f.x_rs[0] = a.k_row_stride;
+  f.x[1] = a.q; f.x_rs[1] = a.q_row_stride;
+  f.wu[0] = a.w_up; f.wg[0] = a.w_gate; f.wd[0] = a.w_down; f.w_rs[0] = (int64_t)D * F;
+  f.wu[1] = a.r_up; f.wg[1] = a.r_gate; f.wd[1] = a.r_down; f.w_rs[1] = a.r_row_stride;
+  f.u_store = reinterpret_cast<float*>(ws + L.u);
+  f.g_store = reinterpret_cast<float*>(ws + L.g);
+  f.h[0] = ws + L.h0;
+  f.h[1] = ws + L.h1;
+  f.zp = reinterpret_cast<float*>(ws + L.zp);
+
+  const dim3 blk(kThreads);
+  hipLaunchKernelGGL(k_up_gate<T>, dim3(F / 64, B, 2), blk, 0, st, f);
+  hipLaunchKernelGGL(k_down_partial<T>, dim3(D / 64, L.nsplit, 2 * B), blk, 0, st, f);
+
+  LnGradArgs g{};
+  g.B = B; g.C = C; g.D = D; g.nsplit = L.nsplit; g.tok_pad = 64; g.normalize = a.normalize_by_dim;
+  g.eps = a.eps; g.zp = f.zp;
+  g.k = a.k; g.k_rs = a.k_row_stride; g.v = a.v; g.v_rs = a.v_row_stride;
+  g.eta = a.eta; g.eta_rs = a.eta_row_stride; g.mask = a.token_mask; g.mask_rs = a.mask_row_stride;
+  g.ln_w = a.ln_weight; g.ln_b = a.ln_bias;
+  g.dz = ws + L.dz; g.loss = reinterpret_cast<float*>(ws + L.loss);
+  hipLaunchKernelGGL(k_ln_grad<T>, dim3(64, B), blk, 0, st, g);
+
+  LnOutArgs o{};
+  o.B = B; o.ntok = C; o.D = D; o.nsplit = L.nsplit; o.tok_pad = 64; o.eps = a.eps;
+  o.zp = f.zp + (size_t)L.nsplit * B * 64 * D;
+  o.x = a.q; o.x_rs = a.q_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
+  o.out = a.out; o.out_rs = a.out_row_stride;
+  hipLaunchKernelGGL(k_ln_readout<T>, dim3(C, B), blk, 0, st, o);
+
+  BwdArgs bw{};
+  bw.B = B; bw.C = C; bw.D = D; bw.F = F;
+  bw.k = a.k; bw.k_rs = a.k_row_stride; bw.wd = a.w_down; bw.w_rs = (int64_t)D * F;
+  bw.u_store = f.u_store; bw.g_store = f.g_store; bw.h = f.h[0]; bw.dz = g.dz;
+  bw.du = ws + L.du; bw.dg = ws + L.dg; bw.nrm = reinterpret_cast<float*>(ws + L.nrm);
+  hipLaunchKernelGGL(k_backward<T>, dim3(F / 64, B), blk, 0, st, bw);
+
+  ApplyArgs ap{};
+  ap.B = B; ap.C = C; ap.D = D; ap.F = F; ap.beta = a.momentum_beta; ap.max_norm = a.max_inner_grad_norm;
+  ap.k = a.k; ap.k_rs = a.k_row_stride; ap.alpha = a.alpha; ap.alpha_rs = a.alpha_row_stride;
+  ap.mask = a.token_mask; ap.mask_rs = a.mask_row_stride;
+  ap.h = f.h[0]; ap.dz = g.dz; ap.du = bw.du; ap.dg = bw.dg; ap.nrm = bw.nrm; ap.loss = g.loss;
+  ap.w[0] = a.w_up; ap.w[1] = a.w_gate; ap.w[2] = a.w_down;
+  ap.s[0] = a.s_up; ap.s[1] = a.s_gate; ap.s[2] = a.s_down;
+  ap.w_out[0] = a.w_up_out; ap.w_out[1] = a.w_gate_out; ap.w_out[2] = a.w_down_out;
+  ap.s_out[0] = a.s_up_out; ap.s_out[1] = a.s_gate_out; ap.s_out[2] = a.s_down_out;
+  ap.surprise = a.surprise;
+  hipLaunchKernelGGL(k_apply<T>, dim3(3 * (D / 64) * (F / 64), B), blk, 0, st, ap);
+}
+
+struct ReadoutLayout {
+  size_t h, zp, total;
+  int nsplit, ntb;
+};
+
+static ReadoutLayout readout_layout(int64_t B, int64_t T, int64_t D, int64_t F, int32_t dtype) {
+  ReadoutLayout L;
+  L.ntb = (int)((T + 63) / 64);
+  L.nsplit = pick_nsplit((D / 64) * B * L.ntb, F / 64);
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t at = off; off += align_up(bytes); return at; };
+  L.h = take(act_bytes(dtype) * B * L.ntb * 64 * F);
+  L.zp = take(sizeof(float) * L.nsplit * B * L.ntb * 64 * D);
+  L.total = off;
+  return L;
+}
+
+template <typename T>
+static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLayout& L, hipStream_t st) {
+  const int B = (int)a.batch, D = (int)a.d_model, F = (int)a.d_ff;
+  FwdArgs f{};
+  f.B = B; f.D = D; f.F = F; f.ntok = (int)a.tokens; f.ntb = L.ntb; f.tok_pad = L.ntb * 64; f.nsplit = L.nsplit;
+  f.x[0] = a.x; f.x_rs[0] = a.x_row_stride;
+  f.wu[0] = a.w_up; f.wg[0] = a.w_gate; f.wd[0] = a.w_down; f.w_rs[0] = a.w_row_stride;
+  f.u_store = nullptr; f.g_store = nullptr;
+  f.h[0] = ws + L.h;
+  f.zp = reinterpret_cast<float*>(ws + L.zp);
+  const dim3 blk(kThreads);
+  hipLaunchKernelGGL(k_up_gate<T>, dim3(F / 64, B, L.ntb), blk, 0, st, f);
+  hipLaunchKernelGGL(k_down_partial<T>, dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
+  LnOutArgs o{};
+  o.B = B; o.ntok = (int)a.tokens; o.D = D; o.nsplit = L.nsplit; o.tok_pad = f.tok_pad; o.eps = a.eps;
+  o.zp = f.zp; o.x = a.x; o.x_rs = a.x_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
+  o.out = a.out; o.out_rs = a.out_row_stride;
+  hipLaunchKernelGGL(k_ln_readout<T>, dim3(f.tok_pad, B), blk, 0, st, o);
+}
+
+static int check_dims(int64_t B, int64_t D, int64_t F, int32_t dtype) {
+  UTTT_REQUIRE(B >= 1, "batch must be >= 1 (got %lld)", (long long)B);
+  UTTT_REQUIRE(D >= 64 && D % 64 == 0 && D <= 4096, "d_model must be a multiple of 64 in [64, 4096] (got %lld)", (long long)D);
+  UTTT_REQUIRE(F >= 64 && F % 64 == 0, "d_ff must be a positive multiple of 64 (got %lld)", (long long)F);
+  UTTT_REQUIRE(dtype == UTTT_DTYPE_F32 || dtype == UTTT_DTYPE_BF16, "act_dtype must be F32 or BF16 (got %d)", dtype);
+  UTTT_REQUIRE(B <= 65535, "batch must be <= 65535");
+  return UTTT_OK;
+}
+
+}  // namespace uttt
+
+using namespace uttt;
+
+extern "C" size_t uttt_chunk_update_workspace(int64_t batch, int64_t d_model, int64_t d_ff, int32_t act_dtype) {
+  if (check_dims(batch, d_model, d_ff, act_dtype) != UTTT_OK) return 0;
+  return update_layout(batch, d_model, d_ff, act_dtype).total;
+}
+
+extern "C" int uttt_chunk_update(const uttt_chunk_update_args* a, void* workspace, size_t workspace_bytes,
+                                 uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  int rc = check_dims(a->batch, a->d_model, a->d_ff, a->act_dtype);
+  if (rc != UTTT_OK) return rc;
+  UTTT_REQUIRE(a->tokens >= 1 && a->tokens <= 64, "tokens per chunk must be in [1, 64] (got %lld)", (long long)a->tokens);
+  UTTT_REQUIRE(a->q && a->k && a->v && a->eta && a->alpha, "q/k/v/eta/alpha must be non-NULL");
+  UTTT_REQUIRE(a->w_up && a->w_gate && a->w_down && a->s_up && a->s_gate && a->s_down, "state pointers must be non-NULL");
+  UTTT_REQUIRE(a->r_up && a->r_gate && a->r_down, "read-state pointers must be non-NULL");
+  UTTT_REQUIRE(a->ln_weight && a->ln_bias, "ln_weight/ln_bias must be non-NULL");
+  UTTT_REQUIRE(a->w_up_out && a->w_gate_out && a->w_down_out && a->s_up_out && a->s_gate_out && a->s_down_out,
+               "output state pointers must be non-NULL");
+  UTTT_REQUIRE(a->out && a->surprise, "out/surprise must be non-NULL");
+  UTTT_REQUIRE(a->r_row_stride == 0 || a->r_row_stride == a->d_model * a->d_ff,
+               "read-state row stride must be 0 (shared) or d_model*d_ff");
+  const UpdateLayout L = update_layout(a->batch, a->d_model, a->d_ff, a->act_dtype);
+  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,
+               "workspace too small: need %zu bytes, got %zu", L.total, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->act_dtype == UTTT_DTYPE_BF16)
+    launch_update<bf16>(*a, static_cast<char*>(workspace), L, st);
+  else
+    launch_update<float>(*a, static_cast<char*>(workspace), L, st);
+  return launch_status("uttt_chunk_update");
+}
+
+extern "C" size_t uttt_readout_workspace(int64_t batch, int64_t tokens, int64_t d_model, int64_t d_ff, int32_t act_dtype) {
+  if (check_dims(batch, d_model, d_ff, act_dtype) != UTTT_OK || tokens < 1) return 0;
+  return readout_layout(batch, tokens, d_model, d_ff, act_dtype).total;
+}
+
+extern "C" int uttt_swiglu_readout(const uttt_readout_args* a, void* workspace, size_t workspace_bytes,
+                                   uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  int rc = check_dims(a->batch, a->d_model, a->d_ff, a->act_dtype);
+  if (rc != UTTT_OK) return rc;
+  UTTT_REQUIRE(a->tokens >= 1 && a->tokens <= (1 << 20), "tokens must be in [1, 2^20]");
+  UTTT_REQUIRE(a->x && a->out && a->w_up && a->w_gate && a->w_down && a->ln_weight && a->ln_bias,
+               "pointers must be non-NULL");
+  UTTT_REQUIRE(a->w_row_stride == 0 || a->w_row_stride == a->d_model * a->d_ff,
+               "weight row stride must be 0 (shared) or d_model*d_ff");
+  const ReadoutLayout L = readout_layout(a->batch, a->tokens, a->d_model, a->d_ff, a->act_dtype);
+  UTTT_REQUIRE((int64_t)L.ntb * a->batch <= 65535, "batch * ceil(tokens / 64) must be <= 65535");
+  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,
+               "workspace too small: need %zu bytes, got %zu", L.total, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->act_dtype == UTTT_DTYPE_BF16)
+    launch_readout<bf16>(*a, static_cast<char*>(workspace), L, st);
+  else
+    launch_readout<float>(*a, static_cast<char*>(workspace), L, st);
+  return launch_status("uttt_swiglu_readout");
+}

@@ -1,0 +1,409 @@
+// Sliding-window GQA attention for the uTTT blocks on gfx950 (MI355X):
+//   * k_rope_append  -- RoPE on q (in place) and k, append rotated k and v to a KV buffer
+//   * k_swa_prefill  -- flash-style attention: 64 queries per workgroup, 64-key LDS tiles,
+//                       only the key tiles that intersect the window are visited
+//   * k_swa_decode   -- one token per request over a ring-buffer KV cache
+// Visibility rule (reference model/uttt_layer.py:1028-1037): query at absolute key index p
+// sees key j iff 0 <= p - j < window; kv head = h / (n_heads / n_kv_heads).
+#include <math.h>
+
+#include "uttt_device.h"
+#include "uttt_host.h"
+
+namespace uttt {
+
+// ---------------------------------------------------------------------------
+// 16x16 MFMA wave tiles (used by attention)
+//   fp32: v_mfma_f32_16x16x4f32      (K = 4, lane supplies A[l%16][k0 + l/16])
+//   bf16: v_mfma_f32_16x16x32_bf16   (K = 32, lane supplies A[l%16][k0 + 8*(l/16) + 0..7])
+//   result: acc[i] = C[4*(l/16) + i][l%16]
+// ---------------------------------------------------------------------------
+template <typename T> struct Mma16;
+template <> struct Mma16<float> {
+  static constexpr int kK = 4;
+  static constexpr int kPad = 1;
+  __device__ __forceinline__ static void step(f32x4& acc, const float* a_row, const float* b_row, int k0, int g) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a_row[k0 + g], b_row[k0 + g], acc, 0, 0, 0);
+  }
+};
+template <> struct Mma16<bf16> {
+  static constexpr int kK = 32;
+  static constexpr int kPad = 8;
+  __device__ __forceinline__ static void step(f32x4& acc, const bf16* a_row, const bf16* b_row, int k0, int g) {
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(a_row + k0 + 8 * g);
+    const bf16x8 b = *reinterpret_cast<const bf16x8*>(b_row + k0 + 8 * g);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+};
+
+// acc(16x16) += A(16 x KTOT) B(KTOT x 16); A rows at `a` ([16][lda]), B^T rows at `b` ([16][ldb])
+template <typename T, int KTOT>
+__device__ __forceinline__ void wave_mma16(f32x4& acc, const T* a, int lda, const T* b, int ldb) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const T* a_row = a + r * lda;
+  const T* b_row = b + r * ldb;
+#pragma unroll
+  for (int k0 = 0; k0 < KTOT; k0 += Mma16<T>::kK) Mma16<T>::step(acc, a_row, b_row, k0, g);
+}
+
+// RoPE for one element pair, rounding like the reference's activation-dtype ops:
+// out_lo = x_lo*cos - x_hi*sin, out_hi = x_hi*cos + x_lo*sin (model/uttt_layer.py:946-958).
+template <typename T>
+__device__ __forceinline__ void rope_pair(float x_lo, float x_hi, float c, float s, T& out_lo, T& out_hi) {
+#pragma clang fp contract(off)
+  const float cr = to_f32(from_f32<T>(c)), sr = to_f32(from_f32<T>(s));
+  const float a0 = to_f32(from_f32<T>(x_lo * cr)), b0 = to_f32(from_f32<T>(-x_hi * sr));
+  const float a1 = to_f32(from_f32<T>(x_hi * cr)), b1 = to_f32(from_f32<T>(x_lo * sr));
+  out_lo = from_f32<T>(a0 + b0);
+  out_hi = from_f32<T>(a1 + b1);
+}
+
+// ---------------------------------------------------------------------------
+// RoPE + KV append: grid (tokens, batch)
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_rope_append(const uttt_rope_append_args a) {
+  const int t = blockIdx.x, b = blockIdx.y;
+  const int hd = (int)a.head_dim, half = hd / 2;
+  const int64_t pos = a.start_pos + t;
+  const float* cr = a.cos_table + pos * hd;
+  const float* sr = a.sin_table + pos * hd;
+  T* q = static_cast<T*>(a.q) + b * a.q_stride_b + t * a.q_stride_t;
+  const T* k = static_cast<const T*>(a.k) + b * a.k_stride_b + t * a.k_stride_t;
+  const T* v = static_cast<const T*>(a.v) + b * a.v_stride_b + t * a.v_stride_t;
+  T* kc = static_cast<T*>(a.k_cache) + b * a.kv_stride_b + (a.kv_offset + t) * a.kv_stride_t;
+  T* vc = static_cast<T*>(a.v_cache) + b * a.kv_stride_b + (a.kv_offset + t) * a.kv_stride_t;
+  const int nq = (int)a.n_heads * half;
+  for (int idx = threadIdx.x; idx < nq; idx += kThreads) {
+    const int h = idx / half, e = idx - h * half;
+    T* qh = q + h * a.q_stride_h;
+    T lo, hi;
+    rope_pair<T>(to_f32(qh[e]), to_f32(qh[e + half]), cr[e], sr[e], lo, hi);
+    qh[e] = lo;
+    qh[e + half] = hi;
+  }
+  const int nk = (int)a.n_kv_heads * half;
+  for (int idx = threadIdx.x; idx < nk; idx += kThreads) {
+    const int h = idx / half, e = idx - h * half;
+    const T* kh = k + h * a.k_stride_h;
+    T lo, hi;
+    rope_pair<T>(to_f32(kh[e]), to_f32(kh[e + half]), cr[e], sr[e], lo, hi);
+    kc[h * a.kv_stride_h + e] = lo;
+    kc[h * a.kv_stride_h + e + half] = hi;
+  }
+  const int nv = (int)a.n_kv_heads * hd;
+  for (int idx = threadIdx.x; idx < nv; idx += kThreads) {
+    const int h = idx / hd, e = idx - h * hd;
+    vc[h * a.kv_stride_h + e] = v[h * a.v_stride_h + e];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill: grid (ceil(q_len / 64), n_heads, batch); wave w owns queries 16w..16w+15
+// ---------------------------------------------------------------------------
+template <typename T, int HD>
+__global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill_args a) {
+  constexpr int PAD = Mma16<T>::kPad;
+  constexpr int LQ = HD + PAD;   // q/k rows [token][e]
+  constexpr int LV = 64 + PAD;   // v^T rows [e][key], p rows [query][key]
+  __shared__ T qs[64 * LQ];
+  __shared__ T ks[64 * LQ];
+  __shared__ T vt[HD * LV];
+  __shared__ T ps[64 * LV];
+  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int rep = (int)(a.n_heads / a.n_kv_heads);
+  const int kvh = h / rep;
+  const int q0 = qt * 64;
+  const int qn = (int)min((int64_t)64, a.q_len - q0);
+  const int64_t p_first = a.q_offset + q0, p_last = a.q_offset + q0 + qn - 1;
+  const int64_t lo = max((int64_t)0, p_first - a.window + 1);
+  const int64_t hi = min(a.kv_len, p_last + 1);  // exclusive
+
+  const T* qg = static_cast<const T*>(a.q) + b * a.q_stride_b + h * a.q_stride_h;
+  const T* kg = static_cast<const T*>(a.k) + b * a.k_stride_b + kvh * a.k_stride_h;
+  const T* vg = static_cast<const T*>(a.v) + b * a.v_stride_b + kvh * a.v_stride_h;
+
+  for (int idx = threadIdx.x; idx < 64 * HD; idx += kThreads) {
+    const int r = idx / HD, e = idx - r * HD;
+    qs[r * LQ + e] = r < qn ? qg[(q0 + r) * a.q_stride_t + e] : from_f32<T>(0.f);
+  }
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  float m_run[4], l_run[4];
+  f32x4 o[HD / 16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
+  }
+#pragma unroll
+  for (int t = 0; t < HD / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t kt0 = lo; kt0 < hi; kt0 += 64) {
+    const int kn = (int)min((int64_t)64, hi - kt0);
+    __syncthreads();  // previous tile fully consumed
+    for (int idx = threadIdx.x; idx < 64 * HD; idx += kThreads) {
+      const int j = idx / HD, e = idx - j * HD;
+      const bool in = j < kn;
+      ks[j * LQ + e] = in ? kg[(kt0 + j) * a.k_stride_t + e] : from_f32<T>(0.f);
+      vt[e * LV + j] = in ? vg[(kt0 + j) * a.v_stride_t + e] : from_f32<T>(0.f);
+    }
+    __syncthreads();
+
+    // S = Q K^T for this wave's 16 queries x 64 keys (4 tiles of 16 keys)
+    f32x4 s[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      wave_mma16<T, HD>(s[n], qs + (16 * w) * LQ, LQ, ks + (16 * n) * LQ, LQ);
+    }
+    // scale, mask, online softmax (rows 4g+i of the wave's 16)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qi = q0 + 16 * w + 4 * g + i;
+      const int64_t p = a.q_offset + qi;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int64_t key = kt0 + 16 * n + c;
+        const bool vis = qi < a.q_len && key < hi && p - key >= 0 && p - key < a.window;
+        const float val = vis ? s[n][i] * a.scale : -INFINITY;
+        s[n][i] = val;
+        mx = fmaxf(mx, val);
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float m_new = fmaxf(m_run[i], mx);
+      const float corr = m_new == -INFINITY ? 1.f : expf(m_run[i] - m_new);
+      float rs = 0.f;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const float pv = s[n][i] == -INFINITY ? 0.f : expf(s[n][i] - m_new);
+        s[n][i] = pv;
+        rs += pv;
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, 64);
+      l_run[i] = l_run[i] * corr + rs;
+      m_run[i] = m_new;
+#pragma unroll
+      for (int t = 0; t < HD / 16; ++t) o[t][i] *= corr;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) ps[(16 * w + 4 * g + i) * LV + 16 * n + c] = from_f32<T>(s[n][i]);
+    }
+    __syncthreads();
+    // O += P V : A = P rows [query][key], B^T = V^T rows [e][key]
+#pragma unroll
+    for (int t = 0; t < HD / 16; ++t) wave_mma16<T, 64>(o[t], ps + (16 * w) * LV, LV, vt + (16 * t) * LV, LV);
+  }
+
+  T* og = static_cast<T*>(a.out) + b * a.o_stride_b + h * a.o_stride_h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int qi = q0 + 16 * w + 4 * g + i;
+    if (qi >= a.q_len) continue;
+    const float inv = l_run[i] > 0.f ? 1.0f / l_run[i] : 0.f;
+#pragma unroll
+    for (int t = 0; t < HD / 16; ++t) og[(int64_t)qi * a.o_stride_t + 16 * t + c] = from_f32<T>(o[t][i] * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode: grid (n_req, n_kv_heads); one workgroup serves the rep query heads of one kv head
+// ---------------------------------------------------------------------------
+template <typename T, int HD>
+__global__ void __launch_bounds__(kThreads) k_swa_decode(const uttt_swa_decode_args a) {
+  extern __shared__ float dyn[];  // rep * window scores
+  __shared__ float qf[8 * HD];
+  __shared__ float knew[HD], vnew[HD];
+  __shared__ float red[4];
+  __shared__ float part[kThreads / HD][8][HD];
+  const int n = blockIdx.x, kvh = blockIdx.y;
+  const int rep = (int)(a.n_heads / a.n_kv_heads);
+  const int64_t W = a.window;
+  const int64_t pos = a.positions[n];
+  const bool bad = pos < 0 || (a.cos_table != nullptr && pos >= a.table_len);
+  T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
+  if (bad) {  // position outside the RoPE table: loud NaN output, cache untouched
+    for (int idx = threadIdx.x; idx < rep * HD; idx += kThreads) og[idx] = from_f32<T>(NAN);
+    return;
+  }
+  const int64_t slot = pos % W;
+  const int valid = (int)min(pos + 1, W);
+  const T* qg = static_cast<const T*>(a.q) + n * a.q_stride_n + (int64_t)kvh * rep * HD;
+  const T* kn = static_cast<const T*>(a.k_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
+  const T* vn = static_cast<const T*>(a.v_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
+  T* kr = static_cast<T*>(a.k_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
+  T* vr = static_cast<T*>(a.v_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
+  constexpr int half = HD / 2;
+
+  // RoPE (activation-dtype rounding as the reference) and ring write of the new token
+  for (int idx = threadIdx.x; idx < (rep + 1) * half; idx += kThreads) {
+    const int r = idx / half, e = idx - r * half;
+    const T* src = r < rep ? qg + r * HD : kn;
+    T lo = src[e], hi = src[e + half];
+    if (a.cos_table != nullptr)
+      rope_pair<T>(to_f32(lo), to_f32(hi), a.cos_table[pos * HD + e], a.sin_table[pos * HD + e], lo, hi);
+    if (r < rep) {
+      qf[r * HD + e] = to_f32(lo);
+      qf[r * HD + e + half] = to_f32(hi);
+    } else {
+      knew[e] = to_f32(lo);
+      knew[e + half] = to_f32(hi);
+      kr[slot * HD + e] = lo;
+      kr[slot * HD + e + half] = hi;
+    }
+  }
+  for (int e = threadIdx.x; e < HD; e += kThreads) {
+    const T v = vn[e];
+    vnew[e] = to_f32(v);
+    vr[slot * HD + e] = v;
+  }
+  __syncthreads();
+
+  // scores
+  float* sc = dyn;
+  for (int j = threadIdx.x; j < valid; j += kThreads) {
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+    if (j == slot) {
+      for (int e = 0; e < HD; ++e) {
+        const float kv = knew[e];
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          if (r < rep) acc[r] += qf[r * HD + e] * kv;
+      }
+    } else {
+      const T* krow = kr + (int64_t)j * HD;
+      for (int e = 0; e < HD; ++e) {
+        const float kv = to_f32(krow[e]);
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          if (r < rep) acc[r] += qf[r * HD + e] * kv;
+      }
+    }
+    for (int r = 0; r < rep; ++r) sc[r * W + j] = acc[r] * a.scale;
+  }
+  __syncthreads();
+  // softmax per head
+  for (int r = 0; r < rep; ++r) {
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < valid; j += kThreads) mx = fmaxf(mx, sc[r * W + j]);
+    mx = block_max(mx, red);
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < valid; j += kThreads) {
+      const float pv = expf(sc[r * W + j] - mx);
+      sc[r * W + j] = pv;
+      sum += pv;
+    }
+    sum = block_sum(sum, red);
+    const float inv = 1.0f / sum;
+    for (int j = threadIdx.x; j < valid; j += kThreads) sc[r * W + j] *= inv;
+    __syncthreads();
+  }
+  // weighted V: thread -> (group, e)
+  constexpr int G = kThreads / HD;
+  const int e = threadIdx.x % HD, grp = threadIdx.x / HD;
+  float acc[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+  for (int j = grp; j < valid; j += G) {
+    const float vv = j == slot ? vnew[e] : to_f32(vr[(int64_t)j * HD + e]);
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      if (r < rep) acc[r] += sc[r * W + j] * vv;
+  }
+  for (int r = 0; r < rep; ++r) part[grp][r][e] = acc[r];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < rep * HD; idx += kThreads) {
+    const int r = idx / HD, ee = idx - r * HD;
+    float s = 0.f;
+    for (int gg = 0; gg < G; ++gg) s += part[gg][r][ee];
+    og[idx] = from_f32<T>(s);
+  }
+}
+
+template <typename T, int HD>
+static void launch_prefill(const uttt_swa_prefill_args& a, hipStream_t st) {
+  const dim3 grid((unsigned)((a.q_len + 63) / 64), (unsigned)a.n_heads, (unsigned)a.batch);
+  hipLaunchKernelGGL((k_swa_prefill<T, HD>), grid, dim3(kThreads), 0, st, a);
+}
+
+template <typename T, int HD>
+static void launch_decode(const uttt_swa_decode_args& a, hipStream_t st) {
+  const size_t smem = sizeof(float) * (size_t)(a.n_heads / a.n_kv_heads) * (size_t)a.window;
+  hipLaunchKernelGGL((k_swa_decode<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads), dim3(kThreads), smem,
+                     st, a);
+}
+
+}  // namespace uttt
+
+using namespace uttt;
+
+extern "C" int uttt_rope_kv_append(const uttt_rope_append_args* a, uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  UTTT_REQUIRE(a->batch >= 1 && a->batch <= 65535 && a->tokens >= 1, "batch/tokens out of range");
+  UTTT_REQUIRE(a->head_dim >= 2 && a->head_dim % 2 == 0, "head_dim must be even");
+  UTTT_REQUIRE(a->n_heads >= 1 && a->n_kv_heads >= 1, "head counts must be >= 1");
+  UTTT_REQUIRE(a->start_pos >= 0 && a->start_pos + a->tokens <= a->table_len,
+               "positions [%lld, %lld) exceed the RoPE table (%lld rows)", (long long)a->start_pos,
+               (long long)(a->start_pos + a->tokens), (long long)a->table_len);
+  UTTT_REQUIRE(a->cos_table && a->sin_table && a->q && a->k && a->v && a->k_cache && a->v_cache,
+               "pointers must be non-NULL");
+  UTTT_REQUIRE(a->kv_offset >= 0, "kv_offset must be >= 0");
+  UTTT_REQUIRE(a->act_dtype == UTTT_DTYPE_F32 || a->act_dtype == UTTT_DTYPE_BF16, "bad act_dtype");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)a->tokens, (unsigned)a->batch);
+  if (a->act_dtype == UTTT_DTYPE_BF16)
+    hipLaunchKernelGGL(k_rope_append<bf16>, grid, dim3(kThreads), 0, st, *a);
+  else
+    hipLaunchKernelGGL(k_rope_append<float>, grid, dim3(kThreads), 0, st, *a);
+  return launch_status("uttt_rope_kv_append");
+}
+
+extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  UTTT_REQUIRE(a->head_dim == 64 || a->head_dim == 128, "head_dim must be 64 or 128 (got %lld)", (long long)a->head_dim);
+  UTTT_REQUIRE(a->batch >= 1 && a->batch <= 65535 && a->n_heads >= 1 && a->n_heads <= 65535,
+               "batch / n_heads out of range");
+  UTTT_REQUIRE(a->n_kv_heads >= 1 && a->n_heads % a->n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
+  UTTT_REQUIRE(a->q_len >= 1 && a->kv_len >= 1 && a->window >= 1, "q_len, kv_len and window must be >= 1");
+  UTTT_REQUIRE(a->q_offset >= 0 && a->q_offset + a->q_len <= a->kv_len,
+               "queries must index keys inside [0, kv_len): q_offset %lld + q_len %lld > kv_len %lld",
+               (long long)a->q_offset, (long long)a->q_len, (long long)a->kv_len);
+  UTTT_REQUIRE(a->q && a->k && a->v && a->out, "pointers must be non-NULL");
+  UTTT_REQUIRE(a->act_dtype == UTTT_DTYPE_F32 || a->act_dtype == UTTT_DTYPE_BF16, "bad act_dtype");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool b16 = a->act_dtype == UTTT_DTYPE_BF16;
+  if (a->head_dim == 64) {
+    if (b16) launch_prefill<bf16, 64>(*a, st); else launch_prefill<float, 64>(*a, st);
+  } else {
+    if (b16) launch_prefill<bf16, 128>(*a, st); else launch_prefill<float, 128>(*a, st);
+  }
+  return launch_status("uttt_swa_prefill");
+}
+
+extern "C" int uttt_swa_decode(const uttt_swa_decode_args* a, uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  UTTT_REQUIRE(a->head_dim == 64 || a->head_dim == 128, "head_dim must be 64 or 128 (got %lld)", (long long)a->head_dim);
+  UTTT_REQUIRE(a->n_req >= 1 && a->n_kv_heads >= 1 && a->n_kv_heads <= 65535 && a->n_heads % a->n_kv_heads == 0,
+               "bad request / head counts");
+  UTTT_REQUIRE(a->n_heads / a->n_kv_heads <= 8, "at most 8 query heads per kv head");
+  UTTT_REQUIRE(a->window >= 1 && a->window * (a->n_heads / a->n_kv_heads) * 4 <= 64 * 1024,
+               "window too large for the decode score buffer");
+  UTTT_REQUIRE(a->positions && a->q && a->k_new && a->v_new && a->k_ring && a->v_ring && a->out,
+               "pointers must be non-NULL");
+  UTTT_REQUIRE((a->cos_table == nullptr) == (a->sin_table == nullptr), "cos/sin tables must both be given or both NULL");
+  UTTT_REQUIRE(a->act_dtype == UTTT_DTYPE_F32 || a->act_dtype == UTTT_DTYPE_BF16, "bad act_dtype");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool b16 = a->act_dtype == UTTT_DTYPE_BF16;
+  if (a->head_dim == 64) {
+    if (b16) launch_decode<bf16, 64>(*a, st); else launch_decode<float, 64>(*a, st);
+  } else {
+    if (b16) launch_decode<bf16, 128>(*a, st); else launch_decode<float, 128>(*a, st);
+  }
+  return launch_status("uttt_swa_decode");
+}

@@ -1,0 +1,41 @@
+// Host-side helpers shared by the C-ABI entry points: error text, status codes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/uttt_amd.h"
+
+namespace uttt {
+
+char* last_error_buffer();
+
+inline int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(last_error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+inline int ok() {
+  last_error_buffer()[0] = '\0';
+  return UTTT_OK;
+}
+
+// Status after a group of launches.
+inline int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(UTTT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
+
+}  // namespace uttt
+
+#define UTTT_REQUIRE(cond, ...)                              \
+  do {                                                       \
+    if (!(cond)) return ::uttt::fail(UTTT_ERR_INVALID, __VA_ARGS__); \
+  } while (0)

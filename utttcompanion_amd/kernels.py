@@ -1,0 +1,381 @@
+"""Torch-tensor front end of the HIP kernels in libuttt_amd.so.
+
+Each function validates shapes, dtypes and devices the way the reference modules
+do (``ValueError``), hands raw device pointers, strides and the current HIP
+stream to the C ABI, and raises ``RuntimeError`` when the library reports an
+error.  Nothing here computes on the host: CPU tensors are rejected.  The HIP
+path is forward-only, so inputs that require grad under grad mode are rejected
+as well (the reference's update is differentiable; meta-training stays on the
+reference's PyTorch path).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _native as N
+
+Tensor = torch.Tensor
+_ACT = {torch.float32: N.DTYPE_F32, torch.bfloat16: N.DTYPE_BF16}
+
+
+def _act_code(dtype: torch.dtype) -> int:
+    try:
+        return _ACT[dtype]
+    except KeyError:
+        raise ValueError(f"the uTTT HIP kernels take float32 or bfloat16 activations, got {dtype}") from None
+
+
+def _require_device(device: torch.device, *tensors: Optional[Tensor]) -> None:
+    if device.type != "cuda":
+        raise ValueError("the uTTT HIP kernels need GPU (ROCm) tensors; there is no CPU path")
+    for t in tensors:
+        if t is not None and t.device != device:
+            raise ValueError(f"all tensors must be on {device}, found one on {t.device}")
+
+
+def _forward_only(*tensors: Optional[Tensor]) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise ValueError("the HIP fast-weight path is forward-only: run it under torch.no_grad() "
+                         "or pass tensors that do not require grad")
+
+
+def _p(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _rows(x: Tensor) -> Tensor:
+    """(B, T, D) with feature stride 1 and token stride D (row stride free)."""
+    if x.stride(2) != 1 or (x.shape[1] > 1 and x.stride(1) != x.shape[2]):
+        x = x.contiguous()
+    return x
+
+
+def _row_vector(x: Tensor, act: torch.dtype) -> Tensor:
+    """(B, T) or (B, T, 1) per-token scalars with token stride 1, in ``act``."""
+    if x.dim() == 3:
+        x = x[..., 0]
+    if x.dtype != act:
+        x = x.to(act)
+    if x.shape[1] > 1 and x.stride(1) != 1:
+        x = x.contiguous()
+    return x
+
+
+def _state(t: Tensor, name: str) -> Tensor:
+    if t.dtype == torch.float64:
+        raise ValueError(f"{name}: float64 fast-weight state is not supported by the HIP path")
+    if t.dtype != torch.float32:
+        t = t.float()  # exact widening of a bf16/fp16 state to the fp32 master
+    return t.contiguous()
+
+
+def _read_weight(t: Tensor, bsz: int, name: str) -> Tuple[Tensor, int]:
+    """A read-only weight of shape (B|1, r, c): returns (tensor, row stride in elements)."""
+    if t.dtype == torch.float64:
+        raise ValueError(f"{name}: float64 weights are not supported by the HIP path")
+    if t.dtype != torch.float32:
+        t = t.float()
+    shared = t.shape[0] == 1 or t.stride(0) == 0
+    if shared:
+        base = t[:1]
+        if not base.is_contiguous():
+            base = base.contiguous()
+        return base, 0
+    if t.shape[0] != bsz:
+        raise ValueError(f"{name}: batch {t.shape[0]} does not match {bsz}")
+    return t.contiguous(), t.shape[1] * t.shape[2]
+
+
+# ---------------------------------------------------------------------------
+# fast-weight chunk update (reference fused_chunk_ttt_step, model/uttt_layer.py:414-534)
+# ---------------------------------------------------------------------------
+
+def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
+                 w_up: Tensor, w_gate: Tensor, w_down: Tensor,
+                 s_up: Tensor, s_gate: Tensor, s_down: Tensor,
+                 ln_weight: Tensor, ln_bias: Tensor, token_mask: Optional[Tensor],
+                 momentum_beta: float, max_inner_grad_norm: float, normalize_by_dim: bool, eps: float,
+                 read_w_up: Optional[Tensor] = None, read_w_gate: Optional[Tensor] = None,
+                 read_w_down: Optional[Tensor] = None,
+                 out_state: Optional[Sequence[Tensor]] = None,
+                 out: Optional[Tensor] = None,
+                 surprise: Optional[Tensor] = None) -> Tuple[Tensor, ...]:
+    """One chunk of the shared fast-weight update on the GPU.
+
+    Returns ``(readout, W_up', W_gate', W_down', S_up', S_gate', S_down', surprise)``
+    like the reference.  ``out_state`` (six fp32 tensors) receives the new state
+    and may be the input state itself for an in-place update; by default new
+    tensors are allocated.  ``surprise`` is a 0-d fp32 device tensor (no sync).
+    """
+    if q.dim() != 3 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"q/k/v must share one (B, C, D) shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    bsz, tokens, dim = q.shape
+    if not 1 <= tokens <= 64:
+        raise ValueError(f"a chunk holds 1..64 tokens on the HIP path, got {tokens}")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("q, k and v must share one dtype")
+    act = q.dtype
+    code = _act_code(act)
+    dev = q.device
+    ff = w_up.shape[-1]
+    if w_up.shape != (bsz, dim, ff) or w_gate.shape != (bsz, dim, ff) or w_down.shape != (bsz, ff, dim):
+        raise ValueError(f"state shapes {tuple(w_up.shape)}, {tuple(w_gate.shape)}, {tuple(w_down.shape)} "
+                         f"do not match B={bsz}, D={dim}, F={ff}")
+    for s, w in ((s_up, w_up), (s_gate, w_gate), (s_down, w_down)):
+        if s.shape != w.shape:
+            raise ValueError("momentum buffers must match the weight shapes")
+    if dim % 64 or ff % 64 or dim > 4096:
+        raise ValueError(f"d_model and d_ff must be multiples of 64 (d_model <= 4096); got {dim}, {ff}")
+    _require_device(dev, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias,
+                    token_mask, read_w_up, read_w_gate, read_w_down)
+    _forward_only(q, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias)
+
+    q, k, v = _rows(q), _rows(k), _rows(v)
+    eta, alpha = _row_vector(eta, act), _row_vector(alpha, act)
+    mask = None
+    if token_mask is not None:
+        mask = token_mask.to(torch.float32)
+        if tokens > 1 and mask.stride(1) != 1:
+            mask = mask.contiguous()
+    ws = [_state(t, n) for t, n in ((w_up, "w_up"), (w_gate, "w_gate"), (w_down, "w_down"),
+                                     (s_up, "s_up"), (s_gate, "s_gate"), (s_down, "s_down"))]
+    if read_w_up is None and read_w_gate is None and read_w_down is None:
+        rw, r_stride = ws[:3], dim * ff
+    else:
+        if read_w_up is None or read_w_gate is None or read_w_down is None:
+            raise ValueError("read weights must be given all three or none")
+        parts = [_read_weight(t, bsz, n) for t, n in ((read_w_up, "read_w_up"), (read_w_gate, "read_w_gate"),
+                                                        (read_w_down, "read_w_down"))]
+        strides = {p[1] for p in parts}
+        if len(strides) != 1:
+            raise ValueError("read weights must all be shared (batch 1) or all per-row")
+        rw, r_stride = [p[0] for p in parts], parts[0][1]
+    ln_w = ln_weight.to(torch.float32).contiguous()
+    ln_b = ln_bias.to(torch.float32).contiguous()
+    if ln_w.numel() != dim or ln_b.numel() != dim:
+        raise ValueError("ln_weight / ln_bias must have d_model elements")
+
+    if out_state is None:
+        outs = [torch.empty_like(t) for t in ws]
+    else:
+        outs = list(out_state)
+        if len(outs) != 6 or any(o.dtype != torch.float32 or not o.is_contiguous() or o.shape != t.shape
+                                 for o, t in zip(outs, ws)):
+            raise ValueError("out_state must be six contiguous fp32 tensors shaped like the state")
+    if out is None:
+        out = torch.empty((bsz, tokens, dim), dtype=act, device=dev)
+    elif out.shape != (bsz, tokens, dim) or out.dtype != act or out.stride(2) != 1 or (tokens > 1 and out.stride(1) != dim):
+        raise ValueError("out must be (B, C, D) in the activation dtype with token stride D")
+    if surprise is None:
+        surprise = torch.empty((), dtype=torch.float32, device=dev)
+
+    lib = N.load_library()
+    nbytes = lib.uttt_chunk_update_workspace(bsz, dim, ff, code)
+    workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    a = N.ChunkUpdateArgs()
+    a.batch, a.tokens, a.d_model, a.d_ff = bsz, tokens, dim, ff
+    a.act_dtype, a.normalize_by_dim = code, int(bool(normalize_by_dim))
+    a.momentum_beta, a.max_inner_grad_norm, a.eps = float(momentum_beta), float(max_inner_grad_norm or 0.0), float(eps)
+    a.q, a.q_row_stride = _p(q), q.stride(0)
+    a.k, a.k_row_stride = _p(k), k.stride(0)
+    a.v, a.v_row_stride = _p(v), v.stride(0)
+    a.eta, a.eta_row_stride = _p(eta), eta.stride(0)
+    a.alpha, a.alpha_row_stride = _p(alpha), alpha.stride(0)
+    a.token_mask, a.mask_row_stride = _p(mask), (mask.stride(0) if mask is not None else 0)
+    a.w_up, a.w_gate, a.w_down, a.s_up, a.s_gate, a.s_down = (_p(t) for t in ws)
+    a.r_up, a.r_gate, a.r_down = (_p(t) for t in rw)
+    a.r_row_stride = r_stride
+    a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
+    a.w_up_out, a.w_gate_out, a.w_down_out, a.s_up_out, a.s_gate_out, a.s_down_out = (_p(t) for t in outs)
+    a.out, a.out_row_stride = _p(out), out.stride(0)
+    a.surprise = _p(surprise)
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_chunk_update(C.byref(a), _p(workspace), workspace.numel(), _stream(dev)),
+                "uttt_chunk_update")
+    return (out, *outs, surprise)
+
+
+# ---------------------------------------------------------------------------
+# frozen readout (reference swiglu_fast_forward, model/uttt_layer.py:211-247)
+# ---------------------------------------------------------------------------
+
+def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_weight: Tensor,
+                   ln_bias: Tensor, eps: float = 1e-5, out: Optional[Tensor] = None) -> Tensor:
+    """f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down) with per-row (or shared) fp32 W."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, T, D), got {tuple(x.shape)}")
+    bsz, tokens, dim = x.shape
+    code = _act_code(x.dtype)
+    ff = w_up.shape[-1]
+    if w_up.shape[-2:] != (dim, ff) or w_gate.shape[-2:] != (dim, ff) or w_down.shape[-2:] != (ff, dim):
+        raise ValueError("fast weights do not match x's d_model")
+    if dim % 64 or ff % 64 or dim > 4096:
+        raise ValueError(f"d_model and d_ff must be multiples of 64 (d_model <= 4096); got {dim}, {ff}")
+    dev = x.device
+    _require_device(dev, w_up, w_gate, w_down, ln_weight, ln_bias)
+    _forward_only(x, w_up, w_gate, w_down, ln_weight, ln_bias)
+    x = _rows(x)
+    parts = [_read_weight(t, bsz, n) for t, n in ((w_up, "w_up"), (w_gate, "w_gate"), (w_down, "w_down"))]
+    if len({p[1] for p in parts}) != 1:
+        raise ValueError("fast weights must all be shared (batch 1) or all per-row")
+    ln_w = ln_weight.to(torch.float32).contiguous()
+    ln_b = ln_bias.to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty((bsz, tokens, dim), dtype=x.dtype, device=dev)
+    lib = N.load_library()
+    nbytes = lib.uttt_readout_workspace(bsz, tokens, dim, ff, code)
+    workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    a = N.ReadoutArgs()
+    a.batch, a.tokens, a.d_model, a.d_ff, a.act_dtype, a.eps = bsz, tokens, dim, ff, code, float(eps)
+    a.x, a.x_row_stride = _p(x), x.stride(0)
+    a.w_up, a.w_gate, a.w_down = (_p(p[0]) for p in parts)
+    a.w_row_stride = parts[0][1]
+    a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
+    a.out, a.out_row_stride = _p(out), out.stride(0)
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_swiglu_readout(C.byref(a), _p(workspace), workspace.numel(), _stream(dev)),
+                "uttt_swiglu_readout")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# RoPE + KV append (reference apply_rope + cache concat, model/uttt_layer.py:935-958, 1079-1102)
+# ---------------------------------------------------------------------------
+
+def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, start_pos: int,
+                   k_cache: Tensor, v_cache: Tensor, kv_offset: int) -> None:
+    """Rotate ``q`` (B, T, H, hd) in place; write rotated ``k`` and ``v`` (B, T, Hkv, hd) into
+    ``k_cache``/``v_cache`` (B, Hkv, L, hd) at time ``kv_offset + t``.  RoPE position of
+    token t is ``start_pos + t``; cos/sin are fp32 (positions, hd) tables."""
+    bsz, tokens, heads, hd = q.shape
+    hkv = k.shape[2]
+    if k.shape != (bsz, tokens, hkv, hd) or v.shape != k.shape:
+        raise ValueError("k/v must be (B, T, Hkv, hd) matching q")
+    if k_cache.shape[0] != bsz or k_cache.shape[1] != hkv or k_cache.shape[3] != hd or v_cache.shape != k_cache.shape:
+        raise ValueError("kv caches must be (B, Hkv, L, hd)")
+    if kv_offset < 0 or kv_offset + tokens > k_cache.shape[2]:
+        raise ValueError("kv_offset + tokens exceeds the cache length")
+    if start_pos < 0:
+        raise ValueError("RoPE start_pos must be nonnegative")
+    if start_pos + tokens > cos.shape[0]:
+        raise ValueError("positions exceed the RoPE table")
+    if any(t.dtype != q.dtype for t in (k, v, k_cache, v_cache)):
+        raise ValueError("q/k/v and the caches must share one dtype")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or not cos.is_contiguous() or not sin.is_contiguous():
+        raise ValueError("RoPE tables must be contiguous fp32")
+    for t in (q, k, v, k_cache, v_cache):
+        if t.stride(-1) != 1:
+            raise ValueError("the head dimension must be contiguous")
+    dev = q.device
+    _require_device(dev, k, v, cos, sin, k_cache, v_cache)
+    a = N.RopeAppendArgs()
+    a.batch, a.tokens, a.n_heads, a.n_kv_heads, a.head_dim = bsz, tokens, heads, hkv, hd
+    a.act_dtype = _act_code(q.dtype)
+    a.start_pos, a.table_len = int(start_pos), cos.shape[0]
+    a.cos_table, a.sin_table = _p(cos), _p(sin)
+    a.q, a.q_stride_b, a.q_stride_t, a.q_stride_h = _p(q), q.stride(0), q.stride(1), q.stride(2)
+    a.k, a.k_stride_b, a.k_stride_t, a.k_stride_h = _p(k), k.stride(0), k.stride(1), k.stride(2)
+    a.v, a.v_stride_b, a.v_stride_t, a.v_stride_h = _p(v), v.stride(0), v.stride(1), v.stride(2)
+    a.k_cache, a.v_cache = _p(k_cache), _p(v_cache)
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share strides")
+    a.kv_stride_b, a.kv_stride_h, a.kv_stride_t = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.kv_offset = int(kv_offset)
+    lib = N.load_library()
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_rope_kv_append(C.byref(a), _stream(dev)), "uttt_rope_kv_append")
+
+
+# ---------------------------------------------------------------------------
+# sliding-window attention (reference SDPA / FlexAttention dispatch, model/uttt_layer.py:1119-1165)
+# ---------------------------------------------------------------------------
+
+def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
+                out: Optional[Tensor] = None, kv_len: Optional[int] = None) -> Tensor:
+    """q (B, H, Tq, hd), k/v (B, Hkv, Tkv, hd) (any strides with hd contiguous).  Query i sits
+    at key index q_offset + i and sees key j iff 0 <= q_offset + i - j < window.  ``out``
+    (B, H, Tq, hd) may be a strided view, e.g. of a (B, Tq, H, hd) buffer."""
+    bsz, heads, tq, hd = q.shape
+    hkv, tkv = k.shape[1], k.shape[2] if kv_len is None else kv_len
+    if k.shape[0] != bsz or k.shape[3] != hd or v.shape != k.shape or heads % hkv:
+        raise ValueError("k/v must be (B, Hkv, Tkv, hd) with n_heads a multiple of n_kv_heads")
+    if hd not in (64, 128):
+        raise ValueError(f"head_dim must be 64 or 128 on the HIP path, got {hd}")
+    if q_offset < 0 or q_offset + tq > tkv or tkv > k.shape[2]:
+        raise ValueError("queries must index keys inside the kv range")
+    if window < 1:
+        raise ValueError("window must be >= 1")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q/k/v must share one dtype")
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            raise ValueError("the head dimension must be contiguous")
+    dev = q.device
+    _require_device(dev, k, v)
+    _forward_only(q, k, v)
+    if out is None:
+        out = torch.empty((bsz, tq, heads, hd), dtype=q.dtype, device=dev).transpose(1, 2)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype with hd contiguous")
+    a = N.SwaPrefillArgs()
+    a.batch, a.n_heads, a.n_kv_heads, a.q_len, a.kv_len, a.head_dim = bsz, heads, hkv, tq, tkv, hd
+    a.q_offset, a.window, a.act_dtype, a.scale = int(q_offset), int(window), _act_code(q.dtype), 1.0 / math.sqrt(hd)
+    a.q, a.q_stride_b, a.q_stride_h, a.q_stride_t = _p(q), q.stride(0), q.stride(1), q.stride(2)
+    a.k, a.k_stride_b, a.k_stride_h, a.k_stride_t = _p(k), k.stride(0), k.stride(1), k.stride(2)
+    a.v, a.v_stride_b, a.v_stride_h, a.v_stride_t = _p(v), v.stride(0), v.stride(1), v.stride(2)
+    a.out, a.o_stride_b, a.o_stride_h, a.o_stride_t = _p(out), out.stride(0), out.stride(1), out.stride(2)
+    lib = N.load_library()
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_swa_prefill(C.byref(a), _stream(dev)), "uttt_swa_prefill")
+    return out
+
+
+def swa_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_ring: Tensor, v_ring: Tensor, positions: Tensor,
+               cos: Optional[Tensor] = None, sin: Optional[Tensor] = None, out: Optional[Tensor] = None) -> Tensor:
+    """One decode step for N requests.  q (N, H, hd), k_new/v_new (N, Hkv, hd) (un-rotated when
+    tables are given), rings (N, Hkv, W, hd), positions (N,) int64 on the device."""
+    n, heads, hd = q.shape
+    hkv, window = k_ring.shape[1], k_ring.shape[2]
+    if k_new.shape != (n, hkv, hd) or v_new.shape != k_new.shape:
+        raise ValueError("k_new / v_new must be (N, Hkv, hd)")
+    if k_ring.shape != (n, hkv, window, hd) or v_ring.shape != k_ring.shape:
+        raise ValueError("rings must be (N, Hkv, W, hd)")
+    if positions.shape != (n,) or positions.dtype != torch.int64:
+        raise ValueError("positions must be an int64 (N,) device tensor")
+    if hd not in (64, 128) or heads % hkv or heads // hkv > 8:
+        raise ValueError("head_dim must be 64/128 and n_heads / n_kv_heads <= 8")
+    if any(t.dtype != q.dtype for t in (k_new, v_new, k_ring, v_ring)):
+        raise ValueError("q, new k/v and rings must share one dtype")
+    for t, shape_tail in ((q, (heads, hd)), (k_new, (hkv, hd)), (v_new, (hkv, hd)), (k_ring, (hkv, window, hd))):
+        if not t[0].is_contiguous():
+            raise ValueError("per-request slices of q, k_new, v_new and the rings must be contiguous")
+    if k_new.stride(0) != v_new.stride(0) or k_ring.stride(0) != v_ring.stride(0):
+        raise ValueError("k and v tensors must share their request stride")
+    dev = q.device
+    _require_device(dev, k_new, v_new, k_ring, v_ring, positions, cos, sin)
+    if (cos is None) != (sin is None):
+        raise ValueError("cos and sin must both be given or both omitted")
+    if out is None:
+        out = torch.empty_like(q)
+    a = N.SwaDecodeArgs()
+    a.n_req, a.n_heads, a.n_kv_heads, a.head_dim, a.window = n, heads, hkv, hd, window
+    a.act_dtype, a.scale = _act_code(q.dtype), 1.0 / math.sqrt(hd)
+    a.positions = _p(positions)
+    a.cos_table, a.sin_table = _p(cos), _p(sin)
+    a.table_len = 0 if cos is None else cos.shape[0]
+    a.q, a.q_stride_n = _p(q), q.stride(0)
+    a.k_new, a.v_new, a.kv_new_stride_n = _p(k_new), _p(v_new), k_new.stride(0)
+    a.k_ring, a.v_ring, a.ring_stride_n = _p(k_ring), _p(v_ring), k_ring.stride(0)
+    a.out, a.o_stride_n = _p(out), out.stride(0)
+    lib = N.load_library()
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_swa_decode(C.byref(a), _stream(dev)), "uttt_swa_decode")
+    return out
