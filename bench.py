@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""Benchmark of the uTTT hot path on one MI355X; prints one JSON line on stdout.
+
+Workload: the ~151M-label uTTT model (12 layers, d_model 768,
+12 x 64 heads, 4 kv heads, window 512, shared SwiGLU fast weights F = 2048, chunk 64,
+vocab 32000), bf16 activations with fp32 fast-weight masters, random-init weights, token
+ids uniform over the vocabulary, batch 8 x 2048.  One step = one full prefill with the
+per-chunk fast-weight writes of every layer (the chunk-first schedule), recorded once
+into a HIP graph and replayed.  ``value`` = tokens / s over the timed steps.
+
+Also reported:
+* ``roofline``: the dominant kernel of the fused update, timed live with HIP events
+  between the update's stream-ordered phases at the config-2 update shape (8 rows,
+  C 64, D 768, F 2048), against its algorithmic bytes (HBM bound) or flops (MFMA);
+* ``update``: the whole update (all phases) against 48 D F bytes per row;
+* ``decode``: the ring-buffer SWA decode kernel at the config-4 shape (32 requests,
+  4 kv heads x 64, window 512, bf16) against its K/V bytes;
+* ``cpu_baseline``: the CPU oracle (tests-only restatement) on a bounded sample of the
+  same workload, on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+METRIC = "chunk-TTT layer prefill tok/s + SWA decode tok/s; % of MFMA/HBM roofline"
+PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
+
+C2 = dict(vocab_size=32000, d_model=768, n_layers=12, n_heads=12, n_kv_heads=4, d_ff_fast=2048,
+          sliding_window_size=512, chunk_size=64, max_seq_len=4096)
+C2_BATCH, C2_SEQ = 8, 2048
+PHASES = ("k_up_gate", "k_down_partial", "k_ln_grad+k_ln_readout", "k_backward", "k_apply")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--phase-iters", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--cpu-tokens", type=int, default=256, help="tokens of the CPU baseline sample (1 row)")
+    return ap.parse_args()
+
+
+def build_model():
+    import torch
+    from utttcompanion_amd import uTTTConfig, uTTTModel
+    torch.manual_seed(0)
+    model = uTTTModel(uTTTConfig(**C2)).eval()
+    model = model.to("cuda").to(torch.bfloat16)
+    model.fast_weight_pool.float()
+    return model
+
+
+def bench_prefill(model, steps: int, warmup: int):
+    import torch
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, C2["vocab_size"], (C2_BATCH, C2_SEQ), generator=g).to("cuda")
+    state = model.init_fast_state(C2_BATCH, device="cuda", dtype=torch.float32, detach=True)
+    with torch.no_grad():
+        log("eager warmup prefill")
+        model.prefill_with_writes(ids, state)
+        torch.cuda.synchronize()
+        log("capturing the prefill into a HIP graph")
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = model.prefill_with_writes(ids, state)
+        torch.cuda.synchronize()
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        log(f"timing {steps} replays")
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+    finite = bool(torch.isfinite(out[0]).all().item()) and bool(torch.isfinite(out[2]).all().item())
+    return ms, finite
+
+
+def bench_update_phases(iters: int):
+    """HIP-event timing of each update phase at the config-2 shape (read snapshot distinct
+    from the cursor, as for layers 1..L-1 of a chunk; state updated in place)."""
+    import torch
+    from utttcompanion_amd import kernels as K
+    from utttcompanion_amd import _native as N
+    B, C, D, F = C2_BATCH, C2["chunk_size"], C2["d_model"], C2["d_ff_fast"]
+    g = torch.Generator(device="cuda").manual_seed(2)
+    act = lambda *s: torch.randn(*s, device="cuda", generator=g).to(torch.bfloat16)
+    q, k, v = act(B, C, D), act(B, C, D), act(B, C, D)
+    eta = torch.full((B, C, 1), 0.005, device="cuda").to(torch.bfloat16)
+    alpha = torch.full((B, C, 1), 0.001, device="cuda").to(torch.bfloat16)
+    w = [torch.randn(B, D, F, device="cuda", generator=g) * 0.03, torch.randn(B, D, F, device="cuda", generator=g) * 0.03,
+         torch.randn(B, F, D, device="cuda", generator=g) * 0.003]
+    s = [torch.zeros_like(t) for t in w]
+    r = [t.clone() for t in w]
+    ln_w, ln_b = torch.ones(D, device="cuda"), torch.zeros(D, device="cuda")
+    with torch.no_grad():
+        prep = K.prepare_chunk_update(q, k, v, eta, alpha, *w, *s, ln_w, ln_b, None, 0.9, 1.0, True, 1e-5,
+                                      *r, out_state=w + s)
+        for _ in range(3):
+            prep.launch()
+        torch.cuda.synchronize()
+        n = N.UPDATE_PHASES
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(n + 1)] for _ in range(iters)]
+        for it in range(iters):
+            events[it][0].record()
+            for p in range(n):
+                prep.launch(p)
+                events[it][p + 1].record()
+        torch.cuda.synchronize()
+    per = [sum(events[it][p].elapsed_time(events[it][p + 1]) for it in range(iters)) / iters for p in range(n)]
+    return per, dict(B=B, C=C, D=D, F=F)
+
+
+def phase_work(p: int, B: int, C: int, D: int, F: int):
+    """Algorithmic (bytes, flops) of one launch of phase p (two read paths: K through the
+    cursor, Q through a distinct snapshot).  Bytes count the fp32 state each phase must
+    stream once; activations (<= 64 tokens per row) are second order and left out."""
+    DF = D * F
+    if p == 0:
+        return 16 * DF * B, 8 * C * DF * B
+    if p == 1:
+        return 8 * DF * B, 4 * C * DF * B
+    if p == 2:
+        return 0, 0
+    if p == 3:
+        return 4 * DF * B, 8 * C * DF * B
+    return 48 * DF * B, 6 * C * DF * B
+
+
+def bench_decode(iters: int):
+    import torch
+    from utttcompanion_amd import kernels as K
+    N_REQ, H, HKV, HD, W = 32, 12, 4, 64, 512
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn(N_REQ, H, HD, device="cuda", generator=g).to(torch.bfloat16)
+    kn = torch.randn(N_REQ, HKV, HD, device="cuda", generator=g).to(torch.bfloat16)
+    vn = torch.randn_like(kn)
+    kr = torch.randn(N_REQ, HKV, W, HD, device="cuda", generator=g).to(torch.bfloat16)
+    vr = torch.randn_like(kr)
+    pos = torch.randint(W, 4 * W, (N_REQ,), device="cuda", generator=g)
+    with torch.no_grad():
+        out = K.swa_decode(q, kn, vn, kr, vr, pos)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            K.swa_decode(q, kn, vn, kr, vr, pos, out=out)
+        end.record()
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / iters
+    kv_bytes = 2 * N_REQ * HKV * W * HD * 2 + 2 * N_REQ * HKV * HD * 2 + 2 * N_REQ * H * HD * 2
+    return ms, kv_bytes, dict(requests=N_REQ, heads=H, kv_heads=HKV, head_dim=HD, window=W)
+
+
+def cpu_baseline(model, tokens: int):
+    """The CPU oracle (PyTorch-CPU fp32 restatement) on 1 row x ``tokens`` of config 2 with writes."""
+    import torch
+    from oracle import uttt_math as om
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    weights = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    ocfg = om.OracleConfig(**{k: C2[k] for k in ("d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff_fast",
+                                                 "sliding_window_size", "vocab_size", "chunk_size")},
+                           base_inner_lr=model.config.base_inner_lr,
+                           base_weight_decay=model.config.base_weight_decay)
+    oracle = om.OracleModel(ocfg, weights)
+    ids = torch.randint(0, C2["vocab_size"], (1, tokens), generator=torch.Generator().manual_seed(4))
+    t0 = time.perf_counter()
+    oracle.forward(ids, None, None, update_fast_weights=True, logits_to_keep=-1)
+    dt = time.perf_counter() - t0
+    return {"value": round(tokens / dt, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle.OracleModel fp32 on the host CPU: 1 row x {tokens} tokens "
+                      f"({tokens // C2['chunk_size']} chunks) x 12 layers of config 2 with writes; "
+                      f"{dt:.1f} s; tok/s scales linearly in rows and chunks"}
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: every workload here fits one MI355X and the build has no "
+              f"multi-GPU path (requested --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
+        return 1
+    model = build_model()
+    ms, finite = bench_prefill(model, args.steps, args.warmup)
+    tokens = C2_BATCH * C2_SEQ
+    log(f"prefill {ms:.2f} ms/step -> {tokens / ms * 1e3:.0f} tok/s (finite={finite})")
+
+    per, shape = bench_update_phases(args.phase_iters)
+    total_ms = sum(per)
+    B, C, D, F = shape["B"], shape["C"], shape["D"], shape["F"]
+    dom = max(range(len(per)), key=lambda p: per[p])
+    dbytes, dflops = phase_work(dom, B, C, D, F)
+    d_gbs = dbytes / (per[dom] * 1e-3) / 1e9
+    d_tfl = dflops / (per[dom] * 1e-3) / 1e12
+    hbm_bound = dbytes > 0 and dflops / dbytes < PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    roofline = ({"bound": "hbm", "achieved": round(d_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                 "frac": round(d_gbs / PEAK_HBM_GBS, 4)} if hbm_bound else
+                {"bound": "mfma", "achieved": round(d_tfl, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                 "frac": round(d_tfl / PEAK_BF16_TFLOPS, 4)})
+    roofline.update(kernel=PHASES[dom], traffic=None,
+                    per_launch={"algorithmic_bytes": dbytes, "algorithmic_flops": dflops, "avg_ms": round(per[dom], 4),
+                                "shape": shape})
+    upd_bytes, upd_flops = 48 * D * F * B, 20 * C * D * F * B
+    update = {"ms": round(total_ms, 4), "phase_ms": dict(zip(PHASES, [round(x, 4) for x in per])),
+              "hbm_frac_min_state_bytes": round(upd_bytes / (total_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+              "mfma_frac": round(upd_flops / (total_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    log(f"update phases (ms): {update['phase_ms']}")
+
+    dec_ms, dec_bytes, dec_shape = bench_decode(200)
+    dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
+    decode = {"kernel": "k_swa_decode", "us_per_layer_step": round(dec_ms * 1e3, 2), "achieved_gbs": round(dec_gbs, 1),
+              "hbm_frac": round(dec_gbs / PEAK_HBM_GBS, 4), "shape": dec_shape,
+              "attention_only_tok_s_12_layers": round(dec_shape["requests"] / (12 * dec_ms * 1e-3), 1)}
+    log(f"decode kernel {dec_ms * 1e3:.1f} us -> {dec_gbs:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle baseline")
+        cpu = cpu_baseline(model, args.cpu_tokens)
+        log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
+
+    line = {"metric": METRIC, "value": round(tokens / ms * 1e3, 1), "unit": "tok/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic: uniform token ids, random-init weights (reference init), fp32 fast-weight masters",
+            "config": {"workload": "config2_prefill_with_fast_weight_writes", "global_batch": C2_BATCH,
+                       "seq_len": C2_SEQ, "layers": C2["n_layers"], "d_model": C2["d_model"],
+                       "d_ff_fast": C2["d_ff_fast"], "window": C2["sliding_window_size"], "chunk": C2["chunk_size"],
+                       "parallelism": "none (1 GPU)", "hip_graph": True, "finite": finite},
+            "roofline": roofline, "update": update, "decode": decode, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

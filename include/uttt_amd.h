@@ -73,6 +73,15 @@ size_t uttt_chunk_update_workspace(int64_t batch, int64_t d_model, int64_t d_ff,
 int uttt_chunk_update(const uttt_chunk_update_args* args, void* workspace, size_t workspace_bytes,
                       uttt_stream_t stream);
 
+/* The same update as UTTT_UPDATE_PHASES stream-ordered launches, one per call, in order
+ * 0..4 on one stream with one workspace: 0 U/G/H (both paths), 1 Z partial sums,
+ * 2 LayerNorm + loss + dZ + readout, 3 dH/dU/dG + gradient-norm partials, 4 clip/momentum/
+ * decay/select applied to W and S.  Running all five equals uttt_chunk_update; it exists
+ * so a caller can place timing events (or other stream work) between the phases. */
+#define UTTT_UPDATE_PHASES 5
+int uttt_chunk_update_phase(const uttt_chunk_update_args* args, void* workspace, size_t workspace_bytes,
+                            int32_t phase, uttt_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * 2. Frozen fast-weight readout f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down).
  *    Replaces swiglu_fast_forward (model/uttt_layer.py:211-247) as used by
@@ -154,6 +163,32 @@ typedef struct {
 } uttt_swa_decode_args;
 
 int uttt_swa_decode(const uttt_swa_decode_args* args, uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 6. Slow-anchor elastic pull W <- (1 - lambda) W + lambda W_0 with an optional
+ *    per-row drift ceiling |W - W_0| <= ratio |W_0|.  Replaces
+ *    SharedFastWeightPool.apply_elastic_pull (model/uttt_layer.py:773-832).
+ *    ratio <= 0 disables the ceiling.  out_* may alias w_* (in place).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch, d_model, d_ff;
+  float anchor_lambda, max_drift_ratio;
+  const float* w_up; const float* w_gate; const float* w_down;    /* (B, D, F), (B, D, F), (B, F, D) */
+  const float* w0_up; const float* w0_gate; const float* w0_down; /* (D, F), (D, F), (F, D) */
+  float* out_up; float* out_gate; float* out_down;
+} uttt_elastic_pull_args;
+
+size_t uttt_elastic_pull_workspace(int64_t batch);
+int uttt_elastic_pull(const uttt_elastic_pull_args* args, void* workspace, size_t workspace_bytes,
+                      uttt_stream_t stream);
+
+/* 7. Squared drift norms for SharedFastWeightPool.compute_drift (model/uttt_layer.py:834-874):
+ *    out6[0..2] = sum over rows of |W_m - W0_m|^2 (up, gate, down), out6[3..5] = |W0_m|^2.
+ *    Uses the elastic-pull workspace size. */
+int uttt_fast_weight_drift(int64_t batch, int64_t d_model, int64_t d_ff,
+                           const float* w_up, const float* w_gate, const float* w_down,
+                           const float* w0_up, const float* w0_gate, const float* w0_down,
+                           float* out6, void* workspace, size_t workspace_bytes, uttt_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -41,7 +41,7 @@ def test_every_declared_symbol_is_exported_and_typed(lib):
 def test_struct_layouts_match_the_c_header(tmp_path):
     structs = {"uttt_chunk_update_args": N.ChunkUpdateArgs, "uttt_readout_args": N.ReadoutArgs,
                "uttt_rope_append_args": N.RopeAppendArgs, "uttt_swa_prefill_args": N.SwaPrefillArgs,
-               "uttt_swa_decode_args": N.SwaDecodeArgs}
+               "uttt_swa_decode_args": N.SwaDecodeArgs, "uttt_elastic_pull_args": N.ElasticPullArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')

@@ -1,0 +1,319 @@
+"""GPU parity of the drop-in modules (utttcompanion_amd.layer / .model) against the CPU oracle.
+
+The oracle's compositions are pinned to the reference by tests/golden (see
+test_oracle_golden.py); here the HIP path runs the same seeded weights and inputs at
+kernel-supported sizes (d_model and d_ff multiples of 64, head_dim 64/128).
+Tolerances: fp32 <= 1e-5 relative (max|err| / max|ref|) for fast-weight state and
+surprise, <= 2e-5 relative for logits and activations (these pass through several
+PyTorch GEMMs and RMSNorms besides the kernels); bf16 <= 2e-2 max-abs for logits and
+updated fast weights.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import uttt_math as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAMES = ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")
+
+
+def rel_err(a, e):
+    a, e = a.detach().double().cpu(), e.detach().double().cpu()
+    return (a - e).abs().max().item() / max(e.abs().max().item(), 1e-30)
+
+
+def max_abs(a, e):
+    return (a.detach().double().cpu() - e.detach().double().cpu()).abs().max().item()
+
+
+def draw(sd, seed):
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for name, t in sd.items():
+        if name == "lm_head.weight":
+            continue
+        shape = tuple(t.shape)
+        if name.endswith(("norm.weight", "ln_weight")):
+            v = 1.0 + 0.1 * torch.randn(shape, generator=g)
+        elif name.endswith("ln_bias"):
+            v = 0.05 * torch.randn(shape, generator=g)
+        elif name.endswith(("w_up_init", "w_gate_init")):
+            v = torch.randn(shape, generator=g) / shape[0] ** 0.5
+        elif name.endswith("w_down_init"):
+            v = 0.3 * torch.randn(shape, generator=g) / shape[0] ** 0.5
+        elif name.endswith(("w_eta.weight", "w_alpha.weight")):
+            v = 0.05 * torch.randn(shape, generator=g)
+        elif name.endswith("w_eta.bias"):
+            v = torch.zeros(shape)
+        elif name.endswith("w_alpha.bias"):
+            v = torch.full(shape, -1.386)
+        elif name == "tok_embeddings.weight":
+            v = torch.randn(shape, generator=g)
+        else:
+            v = 0.05 * torch.randn(shape, generator=g)
+        out[name] = v.float()
+    return out
+
+
+SMALL = dict(vocab_size=256, d_model=128, n_layers=3, n_heads=2, n_kv_heads=1, d_ff_fast=192, chunk_size=16,
+             sliding_window_size=24, max_seq_len=512, base_inner_lr=0.05, base_weight_decay=0.01)
+
+
+def build(cfg_kw=SMALL, seed=5, dtype=torch.float32):
+    from utttcompanion_amd import uTTTConfig, uTTTModel
+    cfg = uTTTConfig(**cfg_kw)
+    torch.manual_seed(0)
+    model = uTTTModel(cfg).eval()
+    weights = draw(model.state_dict(), seed)
+    sd = dict(weights)
+    sd["lm_head.weight"] = sd["tok_embeddings.weight"]
+    if dtype != torch.float32:  # round slow weights as the bf16 model will hold them
+        weights = {k: (v if k.startswith("fast_weight_pool.") else v.to(dtype).float()) for k, v in weights.items()}
+    model.load_state_dict(sd)
+    model = model.to(DEV)
+    if dtype != torch.float32:
+        model.to(dtype)
+        model.fast_weight_pool.float()
+    ocfg = om.OracleConfig(**{k: cfg_kw[k] for k in ("d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff_fast",
+                                                     "sliding_window_size", "vocab_size", "chunk_size",
+                                                     "base_inner_lr", "base_weight_decay")})
+    return model, om.OracleModel(ocfg, weights)
+
+
+def ids_and_mask(bsz, seq, vocab, seed=7):
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(6, vocab, (bsz, seq), generator=g)
+    mask = torch.ones(bsz, seq)
+    if bsz > 1:
+        mask[1, seq - 11:] = 0
+    return ids, mask
+
+
+def test_model_forward_with_writes_fp32_matches_oracle():
+    model, oracle = build()
+    ids, mask = ids_and_mask(2, 56, 256)
+    out = model(ids.to(DEV), attention_mask=mask.to(DEV), update_fast_weights=True)
+    logits, state, per_layer, caches = oracle.forward(ids, None, mask, update_fast_weights=True)
+    assert rel_err(out.logits, logits) <= 2e-5
+    for n in NAMES:
+        assert rel_err(getattr(out.fast_state, n), getattr(state, n)) <= 1e-5, n
+    assert rel_err(torch.tensor(out.layer_surprise_losses), per_layer) <= 1e-5
+    assert out.fast_state.step == state.step
+    for (k, v), (ok, ov) in zip(out.kv_caches, caches):
+        assert rel_err(k, ok) <= 2e-5 and rel_err(v, ov) <= 2e-5
+
+
+def test_model_forward_with_writes_bf16_within_tolerance():
+    """bf16 slow weights / activations with fp32 fast-weight masters, reference initialisation
+    (N(0, 0.02) slow weights, pool W_0 draws): logits and updated fast weights within 2e-2
+    max-abs of the fp32 oracle, and no further from it than the reference's own bf16
+    arithmetic (the oracle run in bf16) plus 50%."""
+    from utttcompanion_amd import uTTTConfig, uTTTModel
+    cfg_kw = dict(SMALL, d_ff_fast=256)
+    torch.manual_seed(3)
+    model = uTTTModel(uTTTConfig(**cfg_kw)).eval()
+    weights = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    rounded = {k: (v if k.startswith("fast_weight_pool.") else v.bfloat16().float()) for k, v in weights.items()}
+    model = model.to(DEV).to(torch.bfloat16)
+    model.fast_weight_pool.float()
+    ocfg = om.OracleConfig(**{k: cfg_kw[k] for k in ("d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff_fast",
+                                                     "sliding_window_size", "vocab_size", "chunk_size",
+                                                     "base_inner_lr", "base_weight_decay")})
+    oracle = om.OracleModel(ocfg, rounded)
+    oracle16 = om.OracleModel(ocfg, rounded, dtype=torch.bfloat16)
+    ids, mask = ids_and_mask(2, 64, 256, seed=9)
+    out = model(ids.to(DEV), attention_mask=mask.to(DEV), update_fast_weights=True)
+    logits, state, _, _ = oracle.forward(ids, None, mask, update_fast_weights=True)
+    logits16, state16, _, _ = oracle16.forward(ids, None, mask, update_fast_weights=True)
+    assert out.logits.dtype == torch.bfloat16 and out.fast_state.w_up.dtype == torch.float32
+    ours, theirs = max_abs(out.logits, logits), max_abs(logits16, logits)
+    assert ours <= 2e-2, f"logits max abs {ours:.3e} (reference bf16: {theirs:.3e})"
+    assert ours <= 1.5 * theirs + 1e-3, f"logits max abs {ours:.3e} vs reference bf16 {theirs:.3e}"
+    for n in NAMES[:3]:
+        assert max_abs(getattr(out.fast_state, n), getattr(state, n)) <= 2e-2, n
+
+
+def test_caller_state_is_not_modified_and_split_prefill_matches():
+    model, _ = build()
+    ids, _ = ids_and_mask(1, 48, 256, seed=3)
+    d_ids = ids.to(DEV)
+    state = model.init_fast_state(1, device=DEV, dtype=torch.float32, detach=True)
+    before = [t.clone() for t in state.tensors()]
+    full = model(d_ids, fast_state=state)
+    for a, b in zip(state.tensors(), before):
+        assert torch.equal(a, b)
+    first = model(d_ids[:, :32], fast_state=state)
+    second = model(d_ids[:, 32:], fast_state=first.fast_state, kv_caches=first.kv_caches, start_pos=32)
+    both = torch.cat([first.logits, second.logits], 1)
+    assert rel_err(both, full.logits) <= 2e-5
+    for n in NAMES:
+        assert rel_err(getattr(second.fast_state, n), getattr(full.fast_state, n)) <= 1e-5
+
+
+def test_no_future_leakage_with_writes_on_gpu():
+    model, _ = build()
+    ids, _ = ids_and_mask(2, 48, 256, seed=4)
+    changed = ids.clone()
+    changed[:, 20:] = (changed[:, 20:] + 37) % 250 + 6
+    a = model(ids.to(DEV)).logits
+    b = model(changed.to(DEV)).logits
+    assert torch.equal(a[:, :20], b[:, :20])
+
+
+def test_test_time_update_pull_and_drift_match_oracle():
+    model, oracle = build()
+    ids, mask = ids_and_mask(2, 40, 256, seed=12)
+    base = model.init_fast_state(1, device=DEV, dtype=torch.float32, detach=True)
+    cand, surprise, layers = model.test_time_update(ids[1:2].to(DEV), base, attention_mask=mask[1:2].to(DEV))
+    ocand, osurprise, olayers = oracle.test_time_update(ids[1:2], oracle.init_state(1), mask[1:2])
+    for n in NAMES:
+        assert rel_err(getattr(cand, n), getattr(ocand, n)) <= 1e-5, n
+    assert abs(surprise - osurprise) <= 1e-5 * max(1.0, abs(osurprise))
+    assert rel_err(torch.tensor(layers), torch.tensor(olayers)) <= 1e-5
+    w0 = tuple(oracle.pool[n] for n in ("w_up_init", "w_gate_init", "w_down_init"))
+    for ratio in (0.35, 1e-4, None):
+        pulled = model.fast_weight_pool.apply_elastic_pull(cand, 0.02, ratio)
+        opulled = om.apply_elastic_pull((ocand.w_up, ocand.w_gate, ocand.w_down), w0, 0.02, ratio)
+        for a, e in zip((pulled.w_up, pulled.w_gate, pulled.w_down), opulled):
+            assert rel_err(a, e) <= 1e-5, ratio
+    drift = model.fast_weight_pool.compute_drift(pulled)
+    odrift = om.compute_drift(opulled, w0)
+    for key in ("drift_frobenius", "base_frobenius", "w_up_drift", "w_down_drift_pct"):
+        assert abs(drift[key] - odrift[key]) <= 1e-4 * max(1.0, abs(odrift[key])), key
+
+
+def test_greedy_stream_generate_matches_oracle_tokens():
+    model, oracle = build()
+    ids, _ = ids_and_mask(1, 30, 256, seed=21)
+    state = model.init_fast_state(1, device=DEV, dtype=torch.float32, detach=True)
+    tokens = list(model.stream_generate(ids.to(DEV), state, max_new_tokens=16, temperature=0.0, eos_token_id=None))
+    want = oracle.greedy_generate(ids, oracle.init_state(1), 16)
+    assert tokens == want
+
+
+def test_incremental_decode_equals_full_prefix():
+    """reference tests/test_inference_edge_audit.py:48-62 on the HIP path."""
+    model, _ = build()
+    ids, _ = ids_and_mask(1, 40, 256, seed=22)
+    d_ids = ids.to(DEV)
+    state = model.init_fast_state(1, device=DEV, dtype=torch.float32, detach=True)
+    caches = None
+    for length in range(20, 41):
+        full = model(d_ids[:, :length], fast_state=state, update_fast_weights=False, logits_to_keep=1)
+        if caches is None:
+            step = full
+        else:
+            step = model(d_ids[:, length - 1:length], fast_state=state, kv_caches=caches, start_pos=length - 1,
+                         update_fast_weights=False, logits_to_keep=1)
+        caches = step.kv_caches
+        assert rel_err(step.logits, full.logits) <= 2e-5, length
+
+
+def test_cached_block_and_standalone_layer_match_oracle():
+    from utttcompanion_amd import uTTTBlock
+    torch.manual_seed(0)
+    block = uTTTBlock(0, 128, 2, 1, window_size=24, chunk_size=16, base_inner_lr=0.05, base_weight_decay=0.01).eval()
+    lw = draw(block.state_dict(), 99)
+    block.load_state_dict(lw)
+    block = block.to(DEV)
+    model, oracle = build()
+    pool = model.fast_weight_pool
+    cfg = om.OracleConfig(d_model=128, n_layers=1, n_heads=2, n_kv_heads=1, d_ff_fast=192, sliding_window_size=24,
+                          chunk_size=16, base_inner_lr=0.05, base_weight_decay=0.01)
+    g = torch.Generator().manual_seed(11)
+    x, x_prev = torch.randn(2, 40, 128, generator=g), torch.randn(2, 20, 128, generator=g)
+    mask = torch.ones(2, 40)
+    mask[0, 33:] = 0
+    ostate = oracle.init_state(2)
+    for n in ("s_up", "s_gate", "s_down"):
+        setattr(ostate, n, 0.01 * torch.randn(getattr(ostate, n).shape, generator=g))
+    state = pool.init_state(2, device=DEV, dtype=torch.float32, detach=True)
+    for n in ("s_up", "s_gate", "s_down"):
+        setattr(state, n, getattr(ostate, n).to(DEV))
+    with torch.no_grad():
+        out, st, sur = block.uttt(x.to(DEV), pool, state.clone(), attention_mask=mask.to(DEV))
+    oout, ost, osur = om.uttt_layer_forward(x, lw, cfg, ostate.clone(), mask)
+    assert rel_err(out, oout) <= 2e-5
+    for n in NAMES:
+        assert rel_err(getattr(st, n), getattr(ost, n)) <= 1e-5, n
+    assert rel_err(sur, osur) <= 1e-5
+    cos, sin = om.rope_tables(64, 512)
+    with torch.no_grad():
+        _, _, _, cache = block(x_prev.to(DEV), pool, state.clone(), update_fast_weights=False)
+        bout, bst, bsur, bcache = block(x.to(DEV), pool, state.clone(), mask.to(DEV), cache, 20)
+    _, _, _, ocache = om.block_forward(x_prev, lw, cfg, cos, sin, ostate.clone(), update_fast_weights=False)
+    obout, obst, obsur, obcache = om.block_forward(x, lw, cfg, cos, sin, ostate.clone(), mask, ocache, 20)
+    assert rel_err(bout, obout) <= 2e-5
+    for n in NAMES:
+        assert rel_err(getattr(bst, n), getattr(obst, n)) <= 1e-5, n
+    assert rel_err(bcache[0], obcache[0]) <= 2e-5 and rel_err(bcache[1], obcache[1]) <= 2e-5
+
+
+def test_config1_block_fp32_matches_oracle():
+    """Config 1: one uTTT block, fp32, B1 T1024 D512 8x64 heads, window 256, F1024, C64, 16 chunks."""
+    from utttcompanion_amd import SharedFastWeightPool, uTTTBlock
+    torch.manual_seed(0)
+    block = uTTTBlock(0, 512, 8, 4, window_size=256, chunk_size=64, base_inner_lr=0.01,
+                      base_weight_decay=0.005, max_seq_len=2048).eval()
+    pool = SharedFastWeightPool(512, 1024, normalize_loss_by_dim=True)
+    g = torch.Generator().manual_seed(1)
+    lw = {}
+    for k, t in block.state_dict().items():
+        if k.endswith("norm.weight"):
+            lw[k] = torch.ones(t.shape)
+        elif k.endswith(("w_eta.weight", "w_alpha.weight")):
+            lw[k] = torch.zeros(t.shape)
+        elif k.endswith("w_eta.bias"):
+            lw[k] = torch.zeros(t.shape)
+        elif k.endswith("w_alpha.bias"):
+            lw[k] = torch.full(t.shape, -1.386)
+        else:
+            lw[k] = 0.02 * torch.randn(t.shape, generator=g)
+    block.load_state_dict(lw)
+    w0 = [0.02 * torch.randn(512, 1024, generator=g), 0.02 * torch.randn(512, 1024, generator=g),
+          0.02 * torch.randn(1024, 512, generator=g)]
+    with torch.no_grad():
+        pool.w_up_init.copy_(w0[0]); pool.w_gate_init.copy_(w0[1]); pool.w_down_init.copy_(w0[2])
+    block, pool = block.to(DEV), pool.to(DEV)
+    x = torch.randn(1, 1024, 512, generator=g)
+    cfg = om.OracleConfig(d_model=512, n_layers=1, n_heads=8, n_kv_heads=4, d_ff_fast=1024, sliding_window_size=256,
+                          chunk_size=64, base_inner_lr=0.01, base_weight_decay=0.005)
+    ostate = om.init_state({"w_up_init": w0[0], "w_gate_init": w0[1], "w_down_init": w0[2],
+                            "ln_weight": torch.ones(512), "ln_bias": torch.zeros(512)}, 1)
+    cos, sin = om.rope_tables(64, 2048)
+    oout, ost, osur, _ = om.block_forward(x, lw, cfg, cos, sin, ostate)
+    state = pool.init_state(1, device=DEV, dtype=torch.float32, detach=True)
+    with torch.no_grad():
+        out, st, sur, _ = block(x.to(DEV), pool, state)
+    assert rel_err(out, oout) <= 2e-5
+    for n in NAMES:
+        assert rel_err(getattr(st, n), getattr(ost, n)) <= 1e-5, n
+    assert rel_err(sur, osur) <= 1e-5
+
+
+def test_prefill_graph_replays_match_eager():
+    """The whole prefill with writes recorded in one HIP graph; several replays with eager
+    work and syncs between them must each equal the eager result."""
+    model, _ = build()
+    ids, _ = ids_and_mask(2, 64, 256, seed=30)
+    d_ids = ids.to(DEV)
+    state = model.init_fast_state(2, device=DEV, dtype=torch.float32, detach=True)
+    with torch.no_grad():
+        h, tensors, per_layer, _ = model.prefill_with_writes(d_ids, state)
+        eager = (h.clone(), [t.clone() for t in tensors], per_layer.clone())
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gout = model.prefill_with_writes(d_ids, state)
+        for rep in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(gout[0], eager[0]), rep
+            for a, e in zip(gout[1], eager[1]):
+                assert torch.equal(a, e), rep
+            assert torch.equal(gout[2], eager[2]), rep
+            model(d_ids[:, :16], fast_state=state)  # unrelated eager work between replays
+            torch.cuda.synchronize()

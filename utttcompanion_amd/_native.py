@@ -14,6 +14,7 @@ from .build import LIB_PATH
 ABI_VERSION = 1
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+UPDATE_PHASES = 5
 
 _P = C.c_void_p
 _I64 = C.c_int64
@@ -93,17 +94,31 @@ class SwaDecodeArgs(C.Structure):
     ]
 
 
+class ElasticPullArgs(C.Structure):
+    _fields_ = [
+        ("batch", _I64), ("d_model", _I64), ("d_ff", _I64),
+        ("anchor_lambda", _F), ("max_drift_ratio", _F),
+        ("w_up", _P), ("w_gate", _P), ("w_down", _P),
+        ("w0_up", _P), ("w0_gate", _P), ("w0_down", _P),
+        ("out_up", _P), ("out_gate", _P), ("out_down", _P),
+    ]
+
+
 # exported symbol -> (restype, argtypes)
 SIGNATURES = {
     "uttt_last_error": (C.c_char_p, []),
     "uttt_abi_version": (C.c_int, []),
     "uttt_chunk_update_workspace": (C.c_size_t, [_I64, _I64, _I64, _I32]),
     "uttt_chunk_update": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _P]),
+    "uttt_chunk_update_phase": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _I32, _P]),
     "uttt_readout_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_swiglu_readout": (C.c_int, [C.POINTER(ReadoutArgs), _P, C.c_size_t, _P]),
     "uttt_rope_kv_append": (C.c_int, [C.POINTER(RopeAppendArgs), _P]),
     "uttt_swa_prefill": (C.c_int, [C.POINTER(SwaPrefillArgs), _P]),
     "uttt_swa_decode": (C.c_int, [C.POINTER(SwaDecodeArgs), _P]),
+    "uttt_elastic_pull_workspace": (C.c_size_t, [_I64]),
+    "uttt_elastic_pull": (C.c_int, [C.POINTER(ElasticPullArgs), _P, C.c_size_t, _P]),
+    "uttt_fast_weight_drift": (C.c_int, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P]),
 }
 
 _lib = None

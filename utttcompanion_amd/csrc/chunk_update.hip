@@ -539,7 +539,8 @@ static UpdateLayout update_layout(int64_t B, int64_t D, int64_t F, int32_t dtype
 }
 
 template <typename T>
-static void launch_update(const uttt_chunk_update_args& a, char* ws, const UpdateLayout& L, hipStream_t st) {
+static void launch_update(const uttt_chunk_update_args& a, char* ws, const UpdateLayout& L, hipStream_t st,
+                          int first_phase, int last_phase) {
   const int B = (int)a.batch, C = (int)a.tokens, D = (int)a.d_model, F = (int)a.d_ff;
   FwdArgs f{};
   f.B = B; f.D = D; f.F = F; f.ntok = C; f.ntb = 1; f.tok_pad = 64; f.nsplit = L.nsplit;
@@ -552,10 +553,11 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   f.h[0] = ws + L.h0;
   f.h[1] = ws + L.h1;
   f.zp = reinterpret_cast<float*>(ws + L.zp);
-
   const dim3 blk(kThreads);
-  hipLaunchKernelGGL(k_up_gate<T>, dim3(F / 64, B, 2), blk, 0, st, f);
-  hipLaunchKernelGGL(k_down_partial<T>, dim3(D / 64, L.nsplit, 2 * B), blk, 0, st, f);
+  auto want = [&](int phase) { return first_phase <= phase && phase <= last_phase; };
+
+  if (want(0)) hipLaunchKernelGGL(k_up_gate<T>, dim3(F / 64, B, 2), blk, 0, st, f);
+  if (want(1)) hipLaunchKernelGGL(k_down_partial<T>, dim3(D / 64, L.nsplit, 2 * B), blk, 0, st, f);
 
   LnGradArgs g{};
   g.B = B; g.C = C; g.D = D; g.nsplit = L.nsplit; g.tok_pad = 64; g.normalize = a.normalize_by_dim;
@@ -564,21 +566,22 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   g.eta = a.eta; g.eta_rs = a.eta_row_stride; g.mask = a.token_mask; g.mask_rs = a.mask_row_stride;
   g.ln_w = a.ln_weight; g.ln_b = a.ln_bias;
   g.dz = ws + L.dz; g.loss = reinterpret_cast<float*>(ws + L.loss);
-  hipLaunchKernelGGL(k_ln_grad<T>, dim3(64, B), blk, 0, st, g);
-
   LnOutArgs o{};
   o.B = B; o.ntok = C; o.D = D; o.nsplit = L.nsplit; o.tok_pad = 64; o.eps = a.eps;
   o.zp = f.zp + (size_t)L.nsplit * B * 64 * D;
   o.x = a.q; o.x_rs = a.q_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
   o.out = a.out; o.out_rs = a.out_row_stride;
-  hipLaunchKernelGGL(k_ln_readout<T>, dim3(C, B), blk, 0, st, o);
+  if (want(2)) {
+    hipLaunchKernelGGL(k_ln_grad<T>, dim3(64, B), blk, 0, st, g);
+    hipLaunchKernelGGL(k_ln_readout<T>, dim3(C, B), blk, 0, st, o);
+  }
 
   BwdArgs bw{};
   bw.B = B; bw.C = C; bw.D = D; bw.F = F;
   bw.k = a.k; bw.k_rs = a.k_row_stride; bw.wd = a.w_down; bw.w_rs = (int64_t)D * F;
   bw.u_store = f.u_store; bw.g_store = f.g_store; bw.h = f.h[0]; bw.dz = g.dz;
   bw.du = ws + L.du; bw.dg = ws + L.dg; bw.nrm = reinterpret_cast<float*>(ws + L.nrm);
-  hipLaunchKernelGGL(k_backward<T>, dim3(F / 64, B), blk, 0, st, bw);
+  if (want(3)) hipLaunchKernelGGL(k_backward<T>, dim3(F / 64, B), blk, 0, st, bw);
 
   ApplyArgs ap{};
   ap.B = B; ap.C = C; ap.D = D; ap.F = F; ap.beta = a.momentum_beta; ap.max_norm = a.max_inner_grad_norm;
@@ -590,7 +593,7 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   ap.w_out[0] = a.w_up_out; ap.w_out[1] = a.w_gate_out; ap.w_out[2] = a.w_down_out;
   ap.s_out[0] = a.s_up_out; ap.s_out[1] = a.s_gate_out; ap.s_out[2] = a.s_down_out;
   ap.surprise = a.surprise;
-  hipLaunchKernelGGL(k_apply<T>, dim3(3 * (D / 64) * (F / 64), B), blk, 0, st, ap);
+  if (want(4)) hipLaunchKernelGGL(k_apply<T>, dim3(3 * (D / 64) * (F / 64), B), blk, 0, st, ap);
 }
 
 struct ReadoutLayout {
@@ -648,8 +651,8 @@ extern "C" size_t uttt_chunk_update_workspace(int64_t batch, int64_t d_model, in
   return update_layout(batch, d_model, d_ff, act_dtype).total;
 }
 
-extern "C" int uttt_chunk_update(const uttt_chunk_update_args* a, void* workspace, size_t workspace_bytes,
-                                 uttt_stream_t stream) {
+static int validate_update(const uttt_chunk_update_args* a, void* workspace, size_t workspace_bytes,
+                           UpdateLayout& L) {
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   int rc = check_dims(a->batch, a->d_model, a->d_ff, a->act_dtype);
   if (rc != UTTT_OK) return rc;
@@ -663,15 +666,34 @@ extern "C" int uttt_chunk_update(const uttt_chunk_update_args* a, void* workspac
   UTTT_REQUIRE(a->out && a->surprise, "out/surprise must be non-NULL");
   UTTT_REQUIRE(a->r_row_stride == 0 || a->r_row_stride == a->d_model * a->d_ff,
                "read-state row stride must be 0 (shared) or d_model*d_ff");
-  const UpdateLayout L = update_layout(a->batch, a->d_model, a->d_ff, a->act_dtype);
+  L = update_layout(a->batch, a->d_model, a->d_ff, a->act_dtype);
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,
                "workspace too small: need %zu bytes, got %zu", L.total, workspace_bytes);
+  return UTTT_OK;
+}
+
+static int run_update(const uttt_chunk_update_args* a, void* workspace, size_t workspace_bytes,
+                      uttt_stream_t stream, int first_phase, int last_phase) {
+  UpdateLayout L;
+  const int rc = validate_update(a, workspace, workspace_bytes, L);
+  if (rc != UTTT_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (a->act_dtype == UTTT_DTYPE_BF16)
-    launch_update<bf16>(*a, static_cast<char*>(workspace), L, st);
+    launch_update<bf16>(*a, static_cast<char*>(workspace), L, st, first_phase, last_phase);
   else
-    launch_update<float>(*a, static_cast<char*>(workspace), L, st);
+    launch_update<float>(*a, static_cast<char*>(workspace), L, st, first_phase, last_phase);
   return launch_status("uttt_chunk_update");
+}
+
+extern "C" int uttt_chunk_update(const uttt_chunk_update_args* a, void* workspace, size_t workspace_bytes,
+                                 uttt_stream_t stream) {
+  return run_update(a, workspace, workspace_bytes, stream, 0, UTTT_UPDATE_PHASES - 1);
+}
+
+extern "C" int uttt_chunk_update_phase(const uttt_chunk_update_args* a, void* workspace, size_t workspace_bytes,
+                                       int32_t phase, uttt_stream_t stream) {
+  UTTT_REQUIRE(phase >= 0 && phase < UTTT_UPDATE_PHASES, "phase must be in [0, %d)", UTTT_UPDATE_PHASES);
+  return run_update(a, workspace, workspace_bytes, stream, phase, phase);
 }
 
 extern "C" size_t uttt_readout_workspace(int64_t batch, int64_t tokens, int64_t d_model, int64_t d_ff, int32_t act_dtype) {

@@ -98,23 +98,39 @@ def _read_weight(t: Tensor, bsz: int, name: str) -> Tuple[Tensor, int]:
 # fast-weight chunk update (reference fused_chunk_ttt_step, model/uttt_layer.py:414-534)
 # ---------------------------------------------------------------------------
 
-def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
-                 w_up: Tensor, w_gate: Tensor, w_down: Tensor,
-                 s_up: Tensor, s_gate: Tensor, s_down: Tensor,
-                 ln_weight: Tensor, ln_bias: Tensor, token_mask: Optional[Tensor],
-                 momentum_beta: float, max_inner_grad_norm: float, normalize_by_dim: bool, eps: float,
-                 read_w_up: Optional[Tensor] = None, read_w_gate: Optional[Tensor] = None,
-                 read_w_down: Optional[Tensor] = None,
-                 out_state: Optional[Sequence[Tensor]] = None,
-                 out: Optional[Tensor] = None,
-                 surprise: Optional[Tensor] = None) -> Tuple[Tensor, ...]:
-    """One chunk of the shared fast-weight update on the GPU.
+class PreparedUpdate:
+    """A validated ``uttt_chunk_update`` call: the argument block, the tensors it points to
+    and the result tuple.  ``launch()`` enqueues the whole update on the current stream;
+    ``launch(phase)`` enqueues one of its ``N.UPDATE_PHASES`` stream-ordered phases."""
 
-    Returns ``(readout, W_up', W_gate', W_down', S_up', S_gate', S_down', surprise)``
-    like the reference.  ``out_state`` (six fp32 tensors) receives the new state
-    and may be the input state itself for an in-place update; by default new
-    tensors are allocated.  ``surprise`` is a 0-d fp32 device tensor (no sync).
-    """
+    def __init__(self, args, keep, workspace, result, device):
+        self.args, self._keep, self.workspace, self.result, self.device = args, keep, workspace, result, device
+
+    def launch(self, phase: Optional[int] = None) -> Tuple[Tensor, ...]:
+        lib = N.load_library()
+        with torch.cuda.device(self.device):
+            if phase is None:
+                rc = lib.uttt_chunk_update(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
+                                           _stream(self.device))
+            else:
+                rc = lib.uttt_chunk_update_phase(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
+                                                 int(phase), _stream(self.device))
+        N.check(rc, "uttt_chunk_update")
+        return self.result
+
+
+def prepare_chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
+                         w_up: Tensor, w_gate: Tensor, w_down: Tensor,
+                         s_up: Tensor, s_gate: Tensor, s_down: Tensor,
+                         ln_weight: Tensor, ln_bias: Tensor, token_mask: Optional[Tensor],
+                         momentum_beta: float, max_inner_grad_norm: float, normalize_by_dim: bool, eps: float,
+                         read_w_up: Optional[Tensor] = None, read_w_gate: Optional[Tensor] = None,
+                         read_w_down: Optional[Tensor] = None,
+                         out_state: Optional[Sequence[Tensor]] = None,
+                         out: Optional[Tensor] = None,
+                         surprise: Optional[Tensor] = None,
+                         workspace: Optional[Tensor] = None) -> PreparedUpdate:
+    """Validate and marshal one chunk update (see ``chunk_update``) without launching it."""
     if q.dim() != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError(f"q/k/v must share one (B, C, D) shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     bsz, tokens, dim = q.shape
@@ -142,6 +158,8 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
     eta, alpha = _row_vector(eta, act), _row_vector(alpha, act)
     mask = None
     if token_mask is not None:
+        if token_mask.shape != (bsz, tokens):
+            raise ValueError(f"token_mask must be (B, C) = ({bsz}, {tokens})")
         mask = token_mask.to(torch.float32)
         if tokens > 1 and mask.stride(1) != 1:
             mask = mask.contiguous()
@@ -154,8 +172,7 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
             raise ValueError("read weights must be given all three or none")
         parts = [_read_weight(t, bsz, n) for t, n in ((read_w_up, "read_w_up"), (read_w_gate, "read_w_gate"),
                                                         (read_w_down, "read_w_down"))]
-        strides = {p[1] for p in parts}
-        if len(strides) != 1:
+        if len({p[1] for p in parts}) != 1:
             raise ValueError("read weights must all be shared (batch 1) or all per-row")
         rw, r_stride = [p[0] for p in parts], parts[0][1]
     ln_w = ln_weight.to(torch.float32).contiguous()
@@ -179,7 +196,8 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
 
     lib = N.load_library()
     nbytes = lib.uttt_chunk_update_workspace(bsz, dim, ff, code)
-    workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     a = N.ChunkUpdateArgs()
     a.batch, a.tokens, a.d_model, a.d_ff = bsz, tokens, dim, ff
     a.act_dtype, a.normalize_by_dim = code, int(bool(normalize_by_dim))
@@ -197,10 +215,34 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
     a.w_up_out, a.w_gate_out, a.w_down_out, a.s_up_out, a.s_gate_out, a.s_down_out = (_p(t) for t in outs)
     a.out, a.out_row_stride = _p(out), out.stride(0)
     a.surprise = _p(surprise)
-    with torch.cuda.device(dev):
-        N.check(lib.uttt_chunk_update(C.byref(a), _p(workspace), workspace.numel(), _stream(dev)),
-                "uttt_chunk_update")
-    return (out, *outs, surprise)
+    keep = (q, k, v, eta, alpha, mask, ws, rw, ln_w, ln_b)
+    return PreparedUpdate(a, keep, workspace, (out, *outs, surprise), dev)
+
+
+def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
+                 w_up: Tensor, w_gate: Tensor, w_down: Tensor,
+                 s_up: Tensor, s_gate: Tensor, s_down: Tensor,
+                 ln_weight: Tensor, ln_bias: Tensor, token_mask: Optional[Tensor],
+                 momentum_beta: float, max_inner_grad_norm: float, normalize_by_dim: bool, eps: float,
+                 read_w_up: Optional[Tensor] = None, read_w_gate: Optional[Tensor] = None,
+                 read_w_down: Optional[Tensor] = None,
+                 out_state: Optional[Sequence[Tensor]] = None,
+                 out: Optional[Tensor] = None,
+                 surprise: Optional[Tensor] = None,
+                 workspace: Optional[Tensor] = None) -> Tuple[Tensor, ...]:
+    """One chunk of the shared fast-weight update on the GPU.
+
+    Returns ``(readout, W_up', W_gate', W_down', S_up', S_gate', S_down', surprise)``
+    like the reference.  ``out_state`` (six fp32 tensors) receives the new state
+    and may be the input state itself for an in-place update; by default new
+    tensors are allocated.  ``surprise`` is a 0-d fp32 device tensor (no sync).
+    ``workspace`` (uint8, at least ``uttt_chunk_update_workspace`` bytes) is reused
+    when given; calls that share one workspace must be ordered on one stream.
+    """
+    return prepare_chunk_update(q, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight,
+                                ln_bias, token_mask, momentum_beta, max_inner_grad_norm, normalize_by_dim, eps,
+                                read_w_up, read_w_gate, read_w_down, out_state, out, surprise,
+                                workspace).launch()
 
 
 # ---------------------------------------------------------------------------
@@ -378,4 +420,58 @@ def swa_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_ring: Tensor, v_ring: 
     lib = N.load_library()
     with torch.cuda.device(dev):
         N.check(lib.uttt_swa_decode(C.byref(a), _stream(dev)), "uttt_swa_decode")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# elastic pull and drift (reference SharedFastWeightPool.apply_elastic_pull / compute_drift,
+# model/uttt_layer.py:773-874)
+# ---------------------------------------------------------------------------
+
+def _pull_operands(w: Sequence[Tensor], w0: Sequence[Tensor]):
+    if len(w) != 3 or len(w0) != 3:
+        raise ValueError("expected (W_up, W_gate, W_down) and three base matrices")
+    bsz, dim, ff = w[0].shape
+    if w[1].shape != (bsz, dim, ff) or w[2].shape != (bsz, ff, dim):
+        raise ValueError("fast weights must be (B, D, F), (B, D, F), (B, F, D)")
+    if w0[0].shape != (dim, ff) or w0[1].shape != (dim, ff) or w0[2].shape != (ff, dim):
+        raise ValueError("base weights must be (D, F), (D, F), (F, D)")
+    dev = w[0].device
+    _require_device(dev, *w, *w0)
+    ws = [_state(t, "w") for t in w]
+    bases = [t.detach().to(torch.float32).contiguous() for t in w0]
+    return bsz, dim, ff, dev, ws, bases
+
+
+def elastic_pull(w: Sequence[Tensor], w0: Sequence[Tensor], anchor_lambda: float,
+                 max_drift_ratio: Optional[float] = None, out: Optional[Sequence[Tensor]] = None):
+    """(1 - lambda) W + lambda W_0 with the optional per-row drift ceiling; new fp32 tensors
+    unless ``out`` (which may be ``w`` itself) is given."""
+    bsz, dim, ff, dev, ws, bases = _pull_operands(w, w0)
+    outs = [torch.empty_like(t) for t in ws] if out is None else list(out)
+    lib = N.load_library()
+    workspace = torch.empty(lib.uttt_elastic_pull_workspace(bsz), dtype=torch.uint8, device=dev)
+    a = N.ElasticPullArgs()
+    a.batch, a.d_model, a.d_ff = bsz, dim, ff
+    a.anchor_lambda = float(anchor_lambda)
+    a.max_drift_ratio = float(max_drift_ratio) if max_drift_ratio is not None and max_drift_ratio > 0 else 0.0
+    a.w_up, a.w_gate, a.w_down = (_p(t) for t in ws)
+    a.w0_up, a.w0_gate, a.w0_down = (_p(t) for t in bases)
+    a.out_up, a.out_gate, a.out_down = (_p(t) for t in outs)
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_elastic_pull(C.byref(a), _p(workspace), workspace.numel(), _stream(dev)),
+                "uttt_elastic_pull")
+    return tuple(outs)
+
+
+def drift_sums(w: Sequence[Tensor], w0: Sequence[Tensor]) -> Tensor:
+    """Device fp32 (6,): sum over rows of |W_m - W0_m|^2 per matrix, then |W0_m|^2 per matrix."""
+    bsz, dim, ff, dev, ws, bases = _pull_operands(w, w0)
+    lib = N.load_library()
+    workspace = torch.empty(lib.uttt_elastic_pull_workspace(bsz), dtype=torch.uint8, device=dev)
+    out = torch.empty(6, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_fast_weight_drift(bsz, dim, ff, *(_p(t) for t in ws), *(_p(t) for t in bases), _p(out),
+                                           _p(workspace), workspace.numel(), _stream(dev)),
+                "uttt_fast_weight_drift")
     return out

@@ -1,0 +1,431 @@
+"""Drop-in counterpart of the reference's ``model/uttt_model.py`` (uTTTConfig / uTTTModel).
+
+Parameter names and shapes match the reference, so its base checkpoints load with
+``load_dual_base_state`` / ``load_state_dict``.  The forward pass with fast-weight
+writes runs the reference's chunk-first shared schedule (every layer of a chunk
+reads the chunk-start snapshot; writes chain one cursor through the layers;
+reference ``uttt_model.py:453-608``) on the HIP kernels, with
+
+* the fp32 state double-buffered: layer 0 of a chunk writes the snapshot's update
+  into a fresh buffer set, layers 1..L-1 update that set in place, and it becomes
+  the next chunk's snapshot (the caller's state tensors are never written);
+* one linear KV buffer per layer for the whole call (rotated keys appended by the
+  RoPE kernel, the window enforced by the attention kernel);
+* per-(chunk, layer) surprise kept on the device; the only host sync is the
+  reference's end-of-forward surprise read, which ``prefill_with_writes`` skips so
+  the whole prefill can be recorded into a HIP graph.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import asdict, dataclass, field
+from pathlib import Path
+from typing import Any, Dict, Iterator, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import kernels as K
+from .layer import FastWeightState, RMSNorm, SharedFastWeightPool, uTTTBlock
+
+Tensor = torch.Tensor
+_NAMES = ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")
+
+# Special token ids of the reference's SimpleUTF8Tokenizer (uttt_model.py:140-151)
+PAD_ID, BOS_ID, EOS_ID, UNK_ID, USER_ID, ASSISTANT_ID = 0, 1, 2, 3, 4, 5
+ACTIVE_VOCAB_LIMIT = 21478
+
+
+@dataclass
+class uTTTConfig:
+    """Model and inner-loop configuration (reference uttt_model.py:44-111)."""
+    name: str = "uTTT-151M-Base"
+    vocab_size: int = 32000
+    d_model: int = 1024
+    n_layers: int = 16
+    n_heads: int = 16
+    n_kv_heads: int = 4
+    d_ff_fast: int = 2816
+    sliding_window_size: int = 512
+    max_seq_len: int = 4096
+    rope_theta: float = 10000.0
+    rms_norm_eps: float = 1e-5
+    dropout: float = 0.0
+    chunk_size: int = 64
+    base_inner_lr: float = 0.015
+    base_weight_decay: float = 0.005
+    momentum_beta: float = 0.90
+    max_inner_grad_norm: float = 1.0
+    normalize_loss_by_dim: bool = True
+    surprise_threshold: float = 0.25
+    elastic_anchor_lambda: float = 0.02
+    max_weight_drift_ratio: float = 0.35
+    gradient_checkpointing: bool = True
+    gradient_checkpointing_every: int = 1
+    meta_checkpoint_layers: int = 0
+    meta_checkpoint_time_chunks: bool = True
+    meta_checkpoint_reentrant: bool = False
+    tie_word_embeddings: bool = True
+    write_schedule: str = "sequential"
+    dspark_speculative_k: int = 0
+    dspark_conf_threshold: float = 0.82
+    tokenizer_json: Optional[str] = None
+    repetition_penalty: float = 1.0
+
+    def to_dict(self) -> Dict[str, Any]:
+        return asdict(self)
+
+    @classmethod
+    def from_dict(cls, data: Dict[str, Any]) -> "uTTTConfig":
+        merged: Dict[str, Any] = {}
+        if "model" in data or "uttt" in data:
+            merged.update(data.get("model", {}))
+            merged.update(data.get("uttt", {}))
+            for name in ("gradient_checkpointing", "gradient_checkpointing_every", "meta_checkpoint_layers",
+                         "meta_checkpoint_time_chunks", "meta_checkpoint_reentrant"):
+                if name in data.get("training", {}):
+                    merged[name] = data["training"][name]
+        else:
+            merged.update(data)
+        valid = {f for f in cls.__dataclass_fields__}
+        return cls(**{k: v for k, v in merged.items() if k in valid})
+
+    @classmethod
+    def from_yaml(cls, path: str | Path) -> "uTTTConfig":
+        import yaml
+        with open(path, "r", encoding="utf-8") as fh:
+            return cls.from_dict(yaml.safe_load(fh))
+
+
+@dataclass
+class uTTTModelOutput:
+    """Structured forward output (reference uttt_model.py:114-124)."""
+    logits: Tensor
+    fast_state: Optional[FastWeightState]
+    loss: Optional[Tensor] = None
+    ce_loss: Optional[Tensor] = None
+    surprise_loss: Optional[Tensor] = None
+    layer_surprise_losses: List[float] = field(default_factory=list)
+    kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None
+
+
+class uTTTModel(nn.Module):
+    """Embeddings, L x (SWA + uTTT) blocks, final norm and tied LM head around one shared
+    fast-weight pool (reference uttt_model.py:261-1271), inference on the HIP path."""
+
+    INNER_LOOP_PROTOCOL = "chunk_shared_fp32_exact_v2"
+
+    def __init__(self, config: uTTTConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.active_vocab_limit = ACTIVE_VOCAB_LIMIT if config.vocab_size >= 24000 else config.vocab_size
+        self.tok_embeddings = nn.Embedding(config.vocab_size, config.d_model)
+        self.fast_weight_pool = SharedFastWeightPool(config.d_model, config.d_ff_fast, config.momentum_beta,
+                                                     config.max_inner_grad_norm, config.normalize_loss_by_dim,
+                                                     config.rms_norm_eps)
+        self.layers = nn.ModuleList([
+            uTTTBlock(i, config.d_model, config.n_heads, config.n_kv_heads, config.sliding_window_size,
+                      config.chunk_size, config.base_inner_lr, config.base_weight_decay, config.max_seq_len,
+                      config.rope_theta, config.rms_norm_eps, config.dropout)
+            for i in range(config.n_layers)])
+        self.norm = RMSNorm(config.d_model, eps=config.rms_norm_eps)
+        self.lm_head = nn.Linear(config.d_model, config.vocab_size, bias=False)
+        self._init_slow_weights()
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.tok_embeddings.weight
+
+    def _init_slow_weights(self) -> None:
+        """N(0, 0.02) for slow Linear / Embedding weights except the eta / alpha routers
+        (reference uttt_model.py:340-352)."""
+        for name, module in self.named_modules():
+            if "fast_weight_pool" in name:
+                continue
+            if isinstance(module, nn.Linear) and not name.endswith(("w_eta", "w_alpha")):
+                nn.init.normal_(module.weight, mean=0.0, std=0.02)
+                if module.bias is not None:
+                    nn.init.zeros_(module.bias)
+            elif isinstance(module, nn.Embedding):
+                nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+    # ------------------------------------------------------------------ checkpoints
+    def get_slow_parameters(self) -> List[nn.Parameter]:
+        fast = {id(p) for p in self.fast_weight_pool.parameters()}
+        return [p for p in self.parameters() if id(p) not in fast]
+
+    def get_meta_fast_parameters(self) -> List[nn.Parameter]:
+        return list(self.fast_weight_pool.parameters())
+
+    def slow_state_dict(self) -> Dict[str, Tensor]:
+        return {k: v.detach().to("cpu", copy=True) for k, v in self.state_dict().items()
+                if not k.startswith("fast_weight_pool.")}
+
+    def init_fast_state_dict(self) -> Dict[str, Tensor]:
+        return {k: v.detach().to("cpu", copy=True) for k, v in self.fast_weight_pool.state_dict().items()}
+
+    def load_dual_base_state(self, slow_weights: Dict[str, Tensor], init_fast_weights: Dict[str, Tensor],
+                             strict: bool = True) -> None:
+        """Load a reference base checkpoint's two tracks (reference uttt_model.py:383-394)."""
+        merged = dict(slow_weights)
+        for k, v in init_fast_weights.items():
+            merged[k if k.startswith("fast_weight_pool.") else f"fast_weight_pool.{k}"] = v
+        self.load_state_dict(merged, strict=strict)
+
+    def freeze_slow_weights(self) -> None:
+        for p in self.parameters():
+            p.requires_grad_(False)
+
+    def init_fast_state(self, batch_size: int = 1, device=None, dtype=None, detach: bool = False) -> FastWeightState:
+        return self.fast_weight_pool.init_state(batch_size=batch_size, device=device, dtype=dtype, detach=detach)
+
+    def num_parameters(self) -> Dict[str, int]:
+        slow = sum(p.numel() for p in self.get_slow_parameters())
+        fast = sum(p.numel() for p in self.get_meta_fast_parameters())
+        return {"slow_weights": slow, "fast_weight_pool": fast, "total": slow + fast}
+
+    # ------------------------------------------------------------------ chunk-first schedule
+    def _compute_dtype(self) -> torch.dtype:
+        return self.tok_embeddings.weight.dtype
+
+    def prefill_with_writes(self, input_ids: Tensor, state: FastWeightState,
+                            attention_mask: Optional[Tensor] = None,
+                            kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0,
+                            out_state: Optional[FastWeightState] = None):
+        """Chunk-first forward with fast-weight writes, without any host synchronisation.
+
+        Returns (hidden (B, T, D), final state tensors (6,), per-layer surprise (L,) fp32
+        device tensor, per-layer KV caches (last <= window rotated keys/values)).
+        ``out_state`` may name a preallocated pair of buffer sets via its tensors (used by
+        graph capture); otherwise buffers are allocated here.
+        """
+        cfg = self.config
+        if cfg.write_schedule != "sequential":
+            raise ValueError("Only the causal sequential write schedule is implemented; aggregated writes must "
+                             "not be silently treated as sequential")
+        bsz, seq = input_ids.shape
+        dev = input_ids.device
+        h = F.embedding(input_ids, self.tok_embeddings.weight)
+        n_layers, c = len(self.layers), cfg.chunk_size
+        n_chunks = (seq + c - 1) // c
+        attn0 = self.layers[0].attn
+        hd, hkv, win = attn0.head_dim, attn0.n_kv_heads, attn0.window_size
+
+        hist = 0
+        if kv_caches is not None:
+            hist = min(kv_caches[0][0].shape[2], win - 1)
+        k_bufs, v_bufs = [], []
+        for li in range(n_layers):
+            kb = torch.empty((bsz, hkv, hist + seq, hd), dtype=h.dtype, device=dev)
+            vb = torch.empty_like(kb)
+            if hist:
+                kb[:, :, :hist].copy_(kv_caches[li][0][:, :, -hist:])
+                vb[:, :, :hist].copy_(kv_caches[li][1][:, :, -hist:])
+            k_bufs.append(kb)
+            v_bufs.append(vb)
+
+        snapshot = tuple(t.float().contiguous() for t in state.tensors())
+        ln_w, ln_b = state.ln_weight, state.ln_bias
+        sets = [tuple(torch.empty_like(t) for t in snapshot) for _ in range(2 if n_chunks > 1 else 1)]
+        surprises = torch.zeros((n_chunks, n_layers), dtype=torch.float32, device=dev)
+        counts = torch.full((n_chunks,), float(bsz * c), dtype=torch.float32, device=dev)
+        if seq % c:
+            counts[-1:].fill_(float(bsz * (seq % c)))
+        pool = self.fast_weight_pool
+        pieces = []
+        workspace = None
+        for ci in range(n_chunks):
+            off = ci * c
+            end = min(seq, off + c)
+            mask = attention_mask[:, off:end] if attention_mask is not None else None
+            if mask is not None:
+                counts[ci].copy_(mask.to(torch.float32).sum())
+            target = sets[ci % len(sets)]
+            hid = h[:, off:end]
+            for li, block in enumerate(self.layers):
+                attn = block.attn
+                x1 = block.attn_norm(hid)
+                q = attn.project(x1, start_pos + off, k_bufs[li], v_bufs[li], hist + off)
+                att = torch.empty((bsz, end - off, attn.n_heads, hd), dtype=h.dtype, device=dev)
+                K.swa_prefill(q.transpose(1, 2), k_bufs[li], v_bufs[li], win, hist + off,
+                              out=att.transpose(1, 2), kv_len=hist + end)
+                hid = hid + attn.wo(att.view(bsz, end - off, -1))
+                x2 = block.uttt_norm(hid)
+                uq, uk, uv, eta, alpha = block.uttt.projections(x2)
+                cursor = snapshot if li == 0 else target
+                prep = K.prepare_chunk_update(
+                    uq, uk, uv, eta, alpha, *cursor, ln_w, ln_b, mask, pool.momentum_beta,
+                    float(pool.max_inner_grad_norm or 0.0), pool.normalize_loss_by_dim, pool.eps,
+                    *((None, None, None) if li == 0 else snapshot[:3]),
+                    out_state=target, surprise=surprises[ci, li], workspace=workspace)
+                workspace = prep.workspace
+                res = prep.launch()
+                hid = hid + block.uttt.w_o(res[0])
+            snapshot = target
+            pieces.append(hid)
+        per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
+        caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win else (kb, vb)
+                  for kb, vb in zip(k_bufs, v_bufs)]
+        return torch.cat(pieces, dim=1), snapshot, per_layer, caches
+
+    # ------------------------------------------------------------------ forward
+    def _logits(self, h: Tensor) -> Tensor:
+        return F.linear(self.norm(h), self.lm_head.weight)
+
+    def forward(self, input_ids: Tensor, fast_state: Optional[FastWeightState] = None,
+                labels: Optional[Tensor] = None, attention_mask: Optional[Tensor] = None,
+                kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0,
+                update_fast_weights: bool = True, surprise_aux_weight: float = 0.10, logits_to_keep: int = 0,
+                return_fast_state: bool = True, **unsupported: Any) -> uTTTModelOutput:
+        """Inference forward with the reference's arguments (uttt_model.py:714-960).
+
+        Training-only options (meta-gradients through the writes, CE token index
+        selection) are not part of the HIP path and are rejected.
+        """
+        if unsupported:
+            raise ValueError(f"options not supported on the HIP inference path: {sorted(unsupported)}")
+        if self.training and torch.is_grad_enabled():
+            raise ValueError("uTTTModel on the HIP path is inference-only; call eval() / torch.no_grad()")
+        bsz, seq = input_ids.shape
+        if seq == 0 or self.config.chunk_size < 1:
+            raise ValueError("input sequence and chunk_size must be non-empty/positive")
+        dev = input_ids.device
+        dt = self._compute_dtype()
+        if fast_state is None:
+            if not update_fast_weights and not return_fast_state:
+                fast_state = self.fast_weight_pool.readonly_state(bsz, device=dev, dtype=dt, detach=True)
+            else:
+                state_dtype = torch.float32 if update_fast_weights else dt
+                fast_state = self.init_fast_state(bsz, device=dev, dtype=state_dtype, detach=True)
+        else:
+            fast_state = fast_state.ensure_batch_size(bsz)
+
+        with torch.no_grad():
+            if update_fast_weights:
+                h, tensors, per_layer, new_caches = self.prefill_with_writes(
+                    input_ids, fast_state, attention_mask, kv_caches, start_pos)
+                n_chunks = (seq + self.config.chunk_size - 1) // self.config.chunk_size
+                cur = FastWeightState(*tensors, fast_state.ln_weight, fast_state.ln_bias,
+                                      fast_state.step + n_chunks * len(self.layers),
+                                      fast_state.last_surprise_loss, list(fast_state.surprise_history))
+                floats = [float(x) for x in per_layer.tolist()]  # the reference's end-of-forward sync
+                cur.last_surprise_loss = sum(floats) / max(len(floats), 1)
+                cur.surprise_history = (list(cur.surprise_history) + floats)[-100:]
+                layer_tensors = per_layer
+            else:
+                h = self.tok_embeddings(input_ids)
+                cur = fast_state
+                new_caches = []
+                for li, block in enumerate(self.layers):
+                    cache = kv_caches[li] if kv_caches is not None else None
+                    h, cur, _, cache = block(h, self.fast_weight_pool, cur, attention_mask, cache, start_pos, False)
+                    new_caches.append(cache)
+                layer_tensors = torch.zeros(len(self.layers), dtype=torch.float32, device=dev)
+                floats = [0.0] * len(self.layers)
+            mean_surprise = layer_tensors.mean()
+
+            ce_loss = total = None
+            if labels is not None:
+                logits = self._logits(h)
+                shift = torch.full_like(labels, -100)
+                shift[:, :-1] = labels[:, 1:]
+                ce_loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]).float(), shift.reshape(-1),
+                                          ignore_index=-100, reduction="sum") / (shift != -100).sum().clamp_min(1)
+                total = ce_loss if surprise_aux_weight == 0.0 else ce_loss + surprise_aux_weight * mean_surprise
+            elif logits_to_keep < 0:
+                logits = torch.empty((bsz, 0, self.config.vocab_size), device=dev, dtype=h.dtype)
+            elif 0 < logits_to_keep < seq:
+                logits = self._logits(h[:, -logits_to_keep:])
+            else:
+                logits = self._logits(h)
+        return uTTTModelOutput(logits=logits, fast_state=cur if return_fast_state else None, loss=total,
+                               ce_loss=ce_loss, surprise_loss=mean_surprise, layer_surprise_losses=floats,
+                               kv_caches=new_caches)
+
+    # ------------------------------------------------------------------ interaction API
+    @torch.no_grad()
+    def test_time_update(self, interaction_ids: Tensor, fast_state: FastWeightState,
+                         attention_mask: Optional[Tensor] = None) -> Tuple[FastWeightState, float, List[float]]:
+        """Writes over [prompt + reply] on a copy of the state (reference uttt_model.py:1237-1271)."""
+        was = self.training
+        self.eval()
+        try:
+            out = self.forward(interaction_ids, fast_state=fast_state, attention_mask=attention_mask,
+                               update_fast_weights=True, logits_to_keep=-1)
+            cand = out.fast_state
+            return cand, float(cand.last_surprise_loss), out.layer_surprise_losses
+        finally:
+            if was:
+                self.train()
+
+    @staticmethod
+    def _sample_next_token(logits: Tensor, temperature: float = 0.7, top_p: float = 0.9,
+                           recent_tokens: Optional[List[int]] = None, repetition_penalty: float = 1.18,
+                           active_vocab_limit: Optional[int] = None,
+                           generator: Optional[torch.Generator] = None) -> Tensor:
+        """Top-p sampling with repetition penalty and vocabulary masking (reference uttt_model.py:1181-1235)."""
+        if not math.isfinite(temperature) or temperature < 0:
+            raise ValueError("temperature must be finite and nonnegative")
+        if not math.isfinite(top_p) or not 0 < top_p <= 1:
+            raise ValueError("top_p must be finite and in (0, 1]")
+        if not math.isfinite(repetition_penalty):
+            raise ValueError("repetition_penalty must be finite")
+        if logits.ndim != 2 or logits.shape[-1] <= UNK_ID:
+            raise ValueError("Sampling logits must have batch and vocabulary dimensions")
+        if active_vocab_limit is not None and active_vocab_limit <= EOS_ID:
+            raise ValueError("Active vocabulary must include EOS")
+        work = logits.to(dtype=torch.float32, copy=True)
+        work[:, PAD_ID] = -torch.inf
+        work[:, BOS_ID] = -torch.inf
+        work[:, UNK_ID] = -torch.inf
+        if active_vocab_limit is not None and active_vocab_limit < work.shape[-1]:
+            work[:, active_vocab_limit:] = -torch.inf
+        if recent_tokens and repetition_penalty > 1.0:
+            idx = torch.tensor(list(set(recent_tokens[-48:])), dtype=torch.long, device=work.device)
+            score = work[:, idx]
+            work[:, idx] = torch.where(score < 0, score * repetition_penalty, score / repetition_penalty)
+        if temperature <= 1e-5:
+            return torch.argmax(work, dim=-1)
+        probs = F.softmax(work / temperature, dim=-1)
+        if 0.0 < top_p < 1.0:
+            sp, si = torch.sort(probs, descending=True, dim=-1)
+            cum = torch.cumsum(sp, dim=-1)
+            sp[cum - sp > top_p] = 0.0
+            sp = sp / sp.sum(dim=-1, keepdim=True).clamp_min(1e-8)
+            return si.gather(-1, torch.multinomial(sp, 1, generator=generator)).squeeze(-1)
+        return torch.multinomial(probs, 1, generator=generator).squeeze(-1)
+
+    @torch.no_grad()
+    def stream_generate(self, input_ids: Tensor, fast_state: FastWeightState, max_new_tokens: int = 128,
+                        temperature: float = 0.7, top_p: float = 0.9, eos_token_id: Optional[int] = EOS_ID,
+                        generator: Optional[torch.Generator] = None, **unused: Any) -> Iterator[int]:
+        """Frozen-state streaming generation for one prompt (reference uttt_model.py:966-1179,
+        without the experimental self-speculative branch)."""
+        if max_new_tokens < 0:
+            raise ValueError("max_new_tokens must be nonnegative")
+        if max_new_tokens == 0:
+            return
+        if input_ids.ndim != 2 or input_ids.shape[0] != 1 or input_ids.shape[1] == 0:
+            raise ValueError("Streaming generation requires one non-empty prompt")
+        was = self.training
+        self.eval()
+        try:
+            out = self.forward(input_ids, fast_state=fast_state, update_fast_weights=False, logits_to_keep=1)
+            caches, logits = out.kv_caches, out.logits[:, -1, :]
+            pos, recent = input_ids.shape[1], []
+            while len(recent) < max_new_tokens:
+                tok = self._sample_next_token(logits, temperature, top_p, recent, self.config.repetition_penalty,
+                                              self.active_vocab_limit, generator)
+                tid = int(tok.item())
+                if tid in (USER_ID, ASSISTANT_ID):
+                    break
+                recent.append(tid)
+                yield tid
+                if (eos_token_id is not None and tid == eos_token_id) or len(recent) >= max_new_tokens:
+                    break
+                step = self.forward(tok.view(1, 1), fast_state=fast_state, kv_caches=caches, start_pos=pos,
+                                    update_fast_weights=False)
+                caches, logits = step.kv_caches, step.logits[:, -1, :]
+                pos += 1
+        finally:
+            if was:
+                self.train()
