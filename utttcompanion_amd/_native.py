@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 UPDATE_PHASES = 5
@@ -91,6 +91,7 @@ class SwaDecodeArgs(C.Structure):
         ("k_new", _P), ("v_new", _P), ("kv_new_stride_n", _I64),
         ("k_ring", _P), ("v_ring", _P), ("ring_stride_n", _I64),
         ("out", _P), ("o_stride_n", _I64),
+        ("workspace", _P), ("workspace_bytes", C.c_size_t),
     ]
 
 
@@ -115,6 +116,7 @@ SIGNATURES = {
     "uttt_swiglu_readout": (C.c_int, [C.POINTER(ReadoutArgs), _P, C.c_size_t, _P]),
     "uttt_rope_kv_append": (C.c_int, [C.POINTER(RopeAppendArgs), _P]),
     "uttt_swa_prefill": (C.c_int, [C.POINTER(SwaPrefillArgs), _P]),
+    "uttt_swa_decode_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
     "uttt_swa_decode": (C.c_int, [C.POINTER(SwaDecodeArgs), _P]),
     "uttt_elastic_pull_workspace": (C.c_size_t, [_I64]),
     "uttt_elastic_pull": (C.c_int, [C.POINTER(ElasticPullArgs), _P, C.c_size_t, _P]),

@@ -49,26 +49,36 @@ struct FwdArgs {
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
   constexpr int LD = lds_ld<T>();
-  __shared__ T xs[64 * LD];
-  __shared__ T us[64 * LD];
-  __shared__ T gs[64 * LD];
+  __shared__ __align__(16) T xs[64 * LD];
+  __shared__ __align__(16) T us[64 * LD];
+  __shared__ __align__(16) T gs[64 * LD];
   const int ft = blockIdx.x, b = blockIdx.y;
   const int path = blockIdx.z / a.ntb, tb = blockIdx.z - path * a.ntb;
   const int f0 = ft * 64, t0 = tb * 64;
   const int rows = min(64, a.ntok - t0);
   const T* x = static_cast<const T*>(a.x[path]) + (int64_t)b * a.x_rs[path] + (int64_t)t0 * a.D;
-  const float* wu = a.wu[path] + (int64_t)b * a.w_rs[path] + f0;
-  const float* wg = a.wg[path] + (int64_t)b * a.w_rs[path] + f0;
+  // threads [0, 128) stage W_up, [128, 256) W_gate (128 units of 8 rows x 4 floats)
+  const bool up_half = threadIdx.x < 128;
+  const float* wsrc = (up_half ? a.wu[path] : a.wg[path]) + (int64_t)b * a.w_rs[path] + f0;
+  T* wdst = up_half ? us : gs;
+  const int unit = threadIdx.x & 127;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
 
+  RowStage<T, KT> xst;
+  ColStage<float, KT> wst;
+  xst.load(x, a.D, rows);
+  wst.load(wsrc, a.F, KT, unit);
   f32x16 au, ag;
   zero(au);
   zero(ag);
   for (int d0 = 0; d0 < a.D; d0 += KT) {
-    stage_rows<T, T, KT>(xs, LD, x + d0, a.D, rows);
-    stage_cols<T, float, KT>(us, LD, wu + (int64_t)d0 * a.F, a.F, KT);
-    stage_cols<T, float, KT>(gs, LD, wg + (int64_t)d0 * a.F, a.F, KT);
+    xst.template store<T>(xs, LD);
+    wst.template store<T>(wdst, LD);
     __syncthreads();
+    if (d0 + KT < a.D) {
+      xst.load(x + d0 + KT, a.D, rows);
+      wst.load(wsrc + (int64_t)(d0 + KT) * a.F, a.F, KT, unit);
+    }
     wave_mma<T, KT>(au, xs + wr * LD, LD, us + wc * LD, LD);
     wave_mma<T, KT>(ag, xs + wr * LD, LD, gs + wc * LD, LD);
     __syncthreads();
@@ -97,8 +107,8 @@ __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_down_partial(const FwdArgs a) {
   constexpr int LD = lds_ld<T>();
-  __shared__ T hs[64 * LD];
-  __shared__ T ws[64 * LD];
+  __shared__ __align__(16) T hs[64 * LD];
+  __shared__ __align__(16) T ws[64 * LD];
   const int dt = blockIdx.x, split = blockIdx.y;
   const int b = blockIdx.z % a.B, pt = blockIdx.z / a.B;
   const int path = pt / a.ntb, tb = pt - path * a.ntb;
@@ -109,12 +119,22 @@ __global__ void __launch_bounds__(kThreads) k_down_partial(const FwdArgs a) {
   const float* wd = a.wd[path] + (int64_t)b * a.w_rs[path] + d0;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
 
+  RowStage<T, KT> hst;
+  ColStage<float, KT> wst;  // W_down rows f, columns d -> [d][f]
   f32x16 acc;
   zero(acc);
+  if (f_begin < f_end) {
+    hst.load(h + f_begin, a.F, 64);
+    wst.load(wd + (int64_t)f_begin * a.D, a.D, KT, threadIdx.x);
+  }
   for (int f0 = f_begin; f0 < f_end; f0 += KT) {
-    stage_rows<T, T, KT>(hs, LD, h + f0, a.F, 64);
-    stage_cols<T, float, KT>(ws, LD, wd + (int64_t)f0 * a.D, a.D, KT);
+    hst.template store<T>(hs, LD);
+    wst.template store<T>(ws, LD);
     __syncthreads();
+    if (f0 + KT < f_end) {
+      hst.load(h + f0 + KT, a.F, 64);
+      wst.load(wd + (int64_t)(f0 + KT) * a.D, a.D, KT, threadIdx.x);
+    }
     wave_mma<T, KT>(acc, hs + wr * LD, LD, ws + wc * LD, LD);
     __syncthreads();
   }
@@ -308,30 +328,39 @@ struct BwdArgs {
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_backward(const BwdArgs a) {
   constexpr int LD = lds_ld<T>();
-  __shared__ T buf0[64 * LD];  // dZ rows -> K^T tile -> H^T tile
-  __shared__ T buf1[64 * LD];  // W_down rows -> dZ^T tile
-  __shared__ T dus[64 * LD];   // dU^T  [f][t]
-  __shared__ T dgs[64 * LD];   // dG^T  [f][t]
+  __shared__ __align__(16) T buf0[64 * LD];  // dZ rows, then K^T tiles
+  __shared__ __align__(16) T buf1[64 * LD];  // W_down rows, then dZ^T tiles
+  __shared__ __align__(16) T hts[64 * LD];   // H^T  [f][t]
+  __shared__ __align__(16) T dus[64 * LD];   // dU^T [f][t]
+  __shared__ __align__(16) T dgs[64 * LD];   // dG^T [f][t]
   __shared__ float red[4];
   const int ft = blockIdx.x, b = blockIdx.y;
   const int f0 = ft * 64;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const T* dz = static_cast<const T*>(a.dz) + (int64_t)b * 64 * a.D;
   const float* wd = a.wd + (int64_t)b * a.w_rs + (int64_t)f0 * a.D;
-
-  // dH tile [t][f] over the full D
-  f32x16 acc;
-  zero(acc);
-  for (int d0 = 0; d0 < a.D; d0 += KT) {
-    stage_rows<T, T, KT>(buf0, LD, dz + d0, a.D, 64);
-    stage_rows<T, float, KT>(buf1, LD, wd + d0, a.D, 64);
-    __syncthreads();
-    wave_mma<T, KT>(acc, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
-    __syncthreads();
-  }
-
+  const T* kr = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs;
   const int64_t rowbase = (int64_t)b * 64 * a.F + f0;
+
+  // dH tile [t][f] over the full D (A = dZ rows, B^T = W_down rows)
   {
+    RowStage<T, KT> zst;
+    RowStage<float, KT> wst;
+    zst.load(dz, a.D, 64);
+    wst.load(wd, a.D, 64);
+    f32x16 acc;
+    zero(acc);
+    for (int d0 = 0; d0 < a.D; d0 += KT) {
+      zst.template store<T>(buf0, LD);
+      wst.template store<T>(buf1, LD);
+      __syncthreads();
+      if (d0 + KT < a.D) {
+        zst.load(dz + d0 + KT, a.D, 64);
+        wst.load(wd + d0 + KT, a.D, 64);
+      }
+      wave_mma<T, KT>(acc, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
+      __syncthreads();
+    }
     const int f = wc + acc_col();
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -348,34 +377,37 @@ __global__ void __launch_bounds__(kThreads) k_backward(const BwdArgs a) {
       dgs[f * LD + t] = dg;
     }
   }
-  __syncthreads();
+  // H^T for this F tile
+  {
+    ColStage<T, 64> hst;
+    hst.load(static_cast<const T*>(a.h) + rowbase, a.F, 64, threadIdx.x);
+    hst.template store<T>(hts, LD);
+  }
 
-  const T* kr = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs;
+  // |gW_up[:, tile]|^2 + |gW_gate[:, tile]|^2 (rows d) and |gW_down[tile, :]|^2 (cols d)
+  constexpr int kUnits = ColStage<T, 64>::kUnits;  // 64 (bf16) or 128 (fp32)
+  const bool k_part = threadIdx.x < kUnits;
+  const int unit = k_part ? threadIdx.x : threadIdx.x - kUnits;
+  ColStage<T, 64> cst;
+  const T* csrc = k_part ? kr : dz;
+  const int cvalid = k_part ? a.C : 64;
+  T* cdst = k_part ? buf0 : buf1;
+  cst.load(csrc, a.D, cvalid, unit < kUnits ? unit : kUnits);
   float sq = 0.f;
-  // |gW_up[:, tile]|^2 + |gW_gate[:, tile]|^2: rows d, cols f
   for (int d0 = 0; d0 < a.D; d0 += 64) {
-    stage_cols<T, T, 64>(buf0, LD, kr + d0, a.D, a.C);  // K^T  [d][t]
     __syncthreads();
-    f32x16 au, ag;
+    cst.template store<T>(cdst, LD);
+    __syncthreads();
+    if (d0 + 64 < a.D) cst.load(csrc + d0 + 64, a.D, cvalid, unit < kUnits ? unit : kUnits);
+    f32x16 au, ag, ad;
     zero(au);
     zero(ag);
+    zero(ad);
     wave_mma<T, 64>(au, buf0 + wr * LD, LD, dus + wc * LD, LD);
     wave_mma<T, 64>(ag, buf0 + wr * LD, LD, dgs + wc * LD, LD);
+    wave_mma<T, 64>(ad, hts + wr * LD, LD, buf1 + wc * LD, LD);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sq += au[i] * au[i] + ag[i] * ag[i];
-    __syncthreads();
-  }
-  // |gW_down[tile, :]|^2: rows f, cols d
-  stage_cols<T, T, 64>(buf0, LD, static_cast<const T*>(a.h) + rowbase, a.F, 64);  // H^T [f][t]
-  for (int d0 = 0; d0 < a.D; d0 += 64) {
-    stage_cols<T, T, 64>(buf1, LD, dz + d0, a.D, 64);  // dZ^T [d][t]
-    __syncthreads();
-    f32x16 ad;
-    zero(ad);
-    wave_mma<T, 64>(ad, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sq += ad[i] * ad[i];
-    __syncthreads();
+    for (int i = 0; i < 16; ++i) sq += au[i] * au[i] + ag[i] * ag[i] + ad[i] * ad[i];
   }
   const float total = block_sum(sq, red);
   if (threadIdx.x == 0) a.nrm[b * (a.F / 64) + ft] = total;
@@ -407,16 +439,62 @@ struct ApplyArgs {
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
   constexpr int LD = lds_ld<T>();
-  __shared__ T as[64 * LD];
-  __shared__ T bs[64 * LD];
+  __shared__ __align__(16) T as[64 * LD];
+  __shared__ __align__(16) T bs[64 * LD];
   __shared__ float row_scalar[3];
   const int nD = a.D / 64, nF = a.F / 64;
   const int per = nD * nF;
   const int m = blockIdx.x / per, j = blockIdx.x - m * per, b = blockIdx.y;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
 
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
+  int r0, c0, ld_out;
+  const T *asrc, *bsrc;
+  int64_t a_ld, b_ld;
+  int a_valid;
+  if (m < 2) {  // W_up / W_gate tile (d, f) = K^T dU / K^T dG
+    const int dt = j / nF, ft = j - dt * nF;
+    r0 = dt * 64;
+    c0 = ft * 64;
+    ld_out = a.F;
+    asrc = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs + r0;
+    a_ld = a.D;
+    a_valid = a.C;
+    bsrc = static_cast<const T*>(m == 0 ? a.du : a.dg) + (int64_t)b * 64 * a.F + c0;
+    b_ld = a.F;
+  } else {      // W_down tile (f, d) = H^T dZ
+    const int ft = j / nD, dt = j - ft * nD;
+    r0 = ft * 64;
+    c0 = dt * 64;
+    ld_out = a.D;
+    asrc = static_cast<const T*>(a.h) + (int64_t)b * 64 * a.F + r0;
+    a_ld = a.F;
+    a_valid = 64;
+    bsrc = static_cast<const T*>(a.dz) + (int64_t)b * 64 * a.D + c0;
+    b_ld = a.D;
+  }
+  // the state tile is the bulk of the traffic: issue its loads first
+  const int64_t mat = (int64_t)a.D * a.F;
+  const float* wsrc = a.w[m] + b * mat;
+  const float* ssrc = a.s[m] + b * mat;
+  const int col = c0 + wc + acc_col();
+  float wv[16], sv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
+    wv[i] = wsrc[off];
+    sv[i] = ssrc[off];
+  }
+  constexpr int kUnits = ColStage<T, 64>::kUnits;
+  {
+    ColStage<T, 64> cst;
+    const bool a_part = threadIdx.x < kUnits;
+    const int unit = a_part ? threadIdx.x : threadIdx.x - kUnits;
+    cst.load(a_part ? asrc : bsrc, a_part ? a_ld : b_ld, a_part ? a_valid : 64, unit < kUnits ? unit : kUnits);
+    cst.template store<T>(a_part ? as : bs, LD);
+  }
+
+  if (threadIdx.x >= 192) {  // the last wave derives this row's clip / decay / active flag
+    const int lane = threadIdx.x - 192;
     float n2 = 0.f;
     for (int i = lane; i < nF; i += 64) n2 += a.nrm[b * nF + i];
     n2 = wave_sum(n2);
@@ -454,24 +532,6 @@ __global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
       if (lane == 0) *a.surprise = a.mask != nullptr ? num / fmaxf(den, 1.f) : num / den;
     }
   }
-
-  int r0, c0, ld_out;
-  if (m < 2) {  // W_up / W_gate tile (d, f) = K^T dU / K^T dG
-    const int dt = j / nF, ft = j - dt * nF;
-    r0 = dt * 64;
-    c0 = ft * 64;
-    ld_out = a.F;
-    stage_cols<T, T, 64>(as, LD, static_cast<const T*>(a.k) + (int64_t)b * a.k_rs + r0, a.D, a.C);
-    const T* src = static_cast<const T*>(m == 0 ? a.du : a.dg) + (int64_t)b * 64 * a.F + c0;
-    stage_cols<T, T, 64>(bs, LD, src, a.F, 64);
-  } else {      // W_down tile (f, d) = H^T dZ
-    const int ft = j / nD, dt = j - ft * nD;
-    r0 = ft * 64;
-    c0 = dt * 64;
-    ld_out = a.D;
-    stage_cols<T, T, 64>(as, LD, static_cast<const T*>(a.h) + (int64_t)b * 64 * a.F + r0, a.F, 64);
-    stage_cols<T, T, 64>(bs, LD, static_cast<const T*>(a.dz) + (int64_t)b * 64 * a.D + c0, a.D, 64);
-  }
   __syncthreads();
   f32x16 acc;
   zero(acc);
@@ -479,25 +539,20 @@ __global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
 
   const float clip = row_scalar[0], decay = row_scalar[1];
   const bool active = row_scalar[2] != 0.f;
-  const int64_t mat = (int64_t)a.D * a.F;
-  const float* wsrc = a.w[m] + b * mat;
-  const float* ssrc = a.s[m] + b * mat;
   float* wdst = a.w_out[m] + b * mat;
   float* sdst = a.s_out[m] + b * mat;
-  const int col = c0 + wc + acc_col();
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
-    const float wv = wsrc[off], sv = ssrc[off];
     float s_new, w_new;
     {
 #pragma clang fp contract(off)
       const float step = acc[i] * clip;
-      s_new = a.beta * sv - step;
-      w_new = decay * wv + s_new;
+      s_new = a.beta * sv[i] - step;
+      w_new = decay * wv[i] + s_new;
     }
-    wdst[off] = active ? w_new : wv;
-    sdst[off] = active ? s_new : sv;
+    wdst[off] = active ? w_new : wv[i];
+    sdst[off] = active ? s_new : sv[i];
   }
 }
 
@@ -666,6 +721,13 @@ static int validate_update(const uttt_chunk_update_args* a, void* workspace, siz
   UTTT_REQUIRE(a->out && a->surprise, "out/surprise must be non-NULL");
   UTTT_REQUIRE(a->r_row_stride == 0 || a->r_row_stride == a->d_model * a->d_ff,
                "read-state row stride must be 0 (shared) or d_model*d_ff");
+  const int64_t vec = a->act_dtype == UTTT_DTYPE_BF16 ? 8 : 4;
+  UTTT_REQUIRE(aligned16(a->q) && aligned16(a->k) && aligned16(a->v) && aligned16(a->w_up) && aligned16(a->w_gate) &&
+               aligned16(a->w_down) && aligned16(a->s_up) && aligned16(a->s_gate) && aligned16(a->s_down) &&
+               aligned16(a->r_up) && aligned16(a->r_gate) && aligned16(a->r_down),
+               "activation and state pointers must be 16-byte aligned");
+  UTTT_REQUIRE(a->q_row_stride % vec == 0 && a->k_row_stride % vec == 0 && a->v_row_stride % vec == 0,
+               "q/k/v row strides must be multiples of 16 bytes");
   L = update_layout(a->batch, a->d_model, a->d_ff, a->act_dtype);
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,
                "workspace too small: need %zu bytes, got %zu", L.total, workspace_bytes);
@@ -711,6 +773,10 @@ extern "C" int uttt_swiglu_readout(const uttt_readout_args* a, void* workspace, 
                "pointers must be non-NULL");
   UTTT_REQUIRE(a->w_row_stride == 0 || a->w_row_stride == a->d_model * a->d_ff,
                "weight row stride must be 0 (shared) or d_model*d_ff");
+  UTTT_REQUIRE(aligned16(a->x) && aligned16(a->w_up) && aligned16(a->w_gate) && aligned16(a->w_down),
+               "x and weight pointers must be 16-byte aligned");
+  UTTT_REQUIRE(a->x_row_stride % (a->act_dtype == UTTT_DTYPE_BF16 ? 8 : 4) == 0,
+               "x row stride must be a multiple of 16 bytes");
   const ReadoutLayout L = readout_layout(a->batch, a->tokens, a->d_model, a->d_ff, a->act_dtype);
   UTTT_REQUIRE((int64_t)L.ntb * a->batch <= 65535, "batch * ceil(tokens / 64) must be <= 65535");
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,

@@ -211,35 +211,72 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
 }
 
 // ---------------------------------------------------------------------------
-// Decode: grid (n_req, n_kv_heads); one workgroup serves the rep query heads of one kv head
+// Decode, split over the window: k_swa_decode_part handles kDecodeKeys ring slots of one
+// (request, kv head) and writes softmax partials (max, sum, unnormalised output) per
+// query head; k_swa_decode_combine merges the splits.  Lanes cooperate on a key row with
+// 16-byte loads (HD/8 lanes per key).
 // ---------------------------------------------------------------------------
+constexpr int kDecodeKeys = 128;
+constexpr int kMaxRep = 8;
+
+struct DecodeDims {
+  int rep, nsplit;
+};
+
+__host__ __device__ __forceinline__ int decode_splits(int64_t window) {
+  return (int)((window + kDecodeKeys - 1) / kDecodeKeys);
+}
+
 template <typename T, int HD>
-__global__ void __launch_bounds__(kThreads) k_swa_decode(const uttt_swa_decode_args a) {
-  extern __shared__ float dyn[];  // rep * window scores
-  __shared__ float qf[8 * HD];
+__device__ __forceinline__ void load8(float (&dst)[8], const T* src) {
+  const uint4 v = *reinterpret_cast<const uint4*>(src);
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = Lanes16<bf16>::get(v, i);
+  } else {
+    const uint4 v2 = *reinterpret_cast<const uint4*>(src + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dst[i] = Lanes16<float>::get(v, i);
+      dst[i + 4] = Lanes16<float>::get(v2, i);
+    }
+  }
+}
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_decode_args a, float* part) {
+  constexpr int L = HD / 8;            // lanes per key row (8 elements each)
+  constexpr int KPP = kThreads / L;    // keys per pass
+  __shared__ float qf[kMaxRep * HD];
   __shared__ float knew[HD], vnew[HD];
-  __shared__ float red[4];
-  __shared__ float part[kThreads / HD][8][HD];
-  const int n = blockIdx.x, kvh = blockIdx.y;
+  __shared__ float sc[kMaxRep * kDecodeKeys];
+  __shared__ float wred[4][kMaxRep * HD];
+  const int n = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int rep = (int)(a.n_heads / a.n_kv_heads);
+  const int nsplit = gridDim.z;
   const int64_t W = a.window;
   const int64_t pos = a.positions[n];
-  const bool bad = pos < 0 || (a.cos_table != nullptr && pos >= a.table_len);
-  T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
-  if (bad) {  // position outside the RoPE table: loud NaN output, cache untouched
-    for (int idx = threadIdx.x; idx < rep * HD; idx += kThreads) og[idx] = from_f32<T>(NAN);
-    return;
-  }
+  if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) return;  // combine writes NaN
   const int64_t slot = pos % W;
   const int valid = (int)min(pos + 1, W);
+  const int j_lo = sp * kDecodeKeys, j_hi = min(valid, j_lo + kDecodeKeys);
+  float* pr = part + (((int64_t)n * a.n_kv_heads + kvh) * nsplit + sp) * rep * (HD + 2);
+  if (j_lo >= j_hi) {
+    for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += kThreads) {
+      const int e = idx % (HD + 2);
+      pr[idx] = e == 0 ? -INFINITY : 0.f;
+    }
+    return;
+  }
   const T* qg = static_cast<const T*>(a.q) + n * a.q_stride_n + (int64_t)kvh * rep * HD;
   const T* kn = static_cast<const T*>(a.k_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
   const T* vn = static_cast<const T*>(a.v_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
   T* kr = static_cast<T*>(a.k_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
   T* vr = static_cast<T*>(a.v_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
+  const bool owns_slot = slot >= j_lo && slot < j_hi;
   constexpr int half = HD / 2;
 
-  // RoPE (activation-dtype rounding as the reference) and ring write of the new token
+  // RoPE (activation-dtype rounding as the reference); the split holding the slot writes the ring
   for (int idx = threadIdx.x; idx < (rep + 1) * half; idx += kThreads) {
     const int r = idx / half, e = idx - r * half;
     const T* src = r < rep ? qg + r * HD : kn;
@@ -252,77 +289,146 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode(const uttt_swa_decode_a
     } else {
       knew[e] = to_f32(lo);
       knew[e + half] = to_f32(hi);
-      kr[slot * HD + e] = lo;
-      kr[slot * HD + e + half] = hi;
+      if (owns_slot) {
+        kr[slot * HD + e] = lo;
+        kr[slot * HD + e + half] = hi;
+      }
     }
   }
   for (int e = threadIdx.x; e < HD; e += kThreads) {
     const T v = vn[e];
     vnew[e] = to_f32(v);
-    vr[slot * HD + e] = v;
+    if (owns_slot) vr[slot * HD + e] = v;
   }
   __syncthreads();
 
-  // scores
-  float* sc = dyn;
-  for (int j = threadIdx.x; j < valid; j += kThreads) {
-    float acc[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) acc[r] = 0.f;
+  const int sub = threadIdx.x % L, grp = threadIdx.x / L;
+  const int e0 = sub * 8;
+  // scores for keys j_lo + grp, + KPP, ...
+  for (int j = j_lo + grp; j < j_hi; j += KPP) {
+    float kv[8];
     if (j == slot) {
-      for (int e = 0; e < HD; ++e) {
-        const float kv = knew[e];
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
-          if (r < rep) acc[r] += qf[r * HD + e] * kv;
-      }
+      for (int i = 0; i < 8; ++i) kv[i] = knew[e0 + i];
     } else {
-      const T* krow = kr + (int64_t)j * HD;
-      for (int e = 0; e < HD; ++e) {
-        const float kv = to_f32(krow[e]);
-#pragma unroll
-        for (int r = 0; r < 8; ++r)
-          if (r < rep) acc[r] += qf[r * HD + e] * kv;
-      }
+      load8<T, HD>(kv, kr + (int64_t)j * HD + e0);
     }
-    for (int r = 0; r < rep; ++r) sc[r * W + j] = acc[r] * a.scale;
+    float acc[kMaxRep];
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+      float s = 0.f;
+      if (r < rep) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += qf[r * HD + e0 + i] * kv[i];
+      }
+      acc[r] = s;
+    }
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+#pragma unroll
+      for (int off = 1; off < L; off <<= 1) acc[r] += __shfl_xor(acc[r], off, 64);
+    }
+    if (sub == 0) {
+      for (int r = 0; r < rep; ++r) sc[r * kDecodeKeys + (j - j_lo)] = acc[r] * a.scale;
+    }
   }
   __syncthreads();
-  // softmax per head
-  for (int r = 0; r < rep; ++r) {
+  // per-head max and exp over this split's keys (one wave per head, looping)
+  const int cnt = j_hi - j_lo;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ float stat[kMaxRep][2];
+  for (int r = wave; r < rep; r += 4) {
     float mx = -INFINITY;
-    for (int j = threadIdx.x; j < valid; j += kThreads) mx = fmaxf(mx, sc[r * W + j]);
-    mx = block_max(mx, red);
+    for (int j = lane; j < cnt; j += 64) mx = fmaxf(mx, sc[r * kDecodeKeys + j]);
+    mx = wave_max(mx);
     float sum = 0.f;
-    for (int j = threadIdx.x; j < valid; j += kThreads) {
-      const float pv = expf(sc[r * W + j] - mx);
-      sc[r * W + j] = pv;
-      sum += pv;
+    for (int j = lane; j < cnt; j += 64) {
+      const float p = expf(sc[r * kDecodeKeys + j] - mx);
+      sc[r * kDecodeKeys + j] = p;
+      sum += p;
     }
-    sum = block_sum(sum, red);
-    const float inv = 1.0f / sum;
-    for (int j = threadIdx.x; j < valid; j += kThreads) sc[r * W + j] *= inv;
-    __syncthreads();
+    sum = wave_sum(sum);
+    if (lane == 0) {
+      stat[r][0] = mx;
+      stat[r][1] = sum;
+    }
   }
-  // weighted V: thread -> (group, e)
-  constexpr int G = kThreads / HD;
-  const int e = threadIdx.x % HD, grp = threadIdx.x / HD;
-  float acc[8];
+  __syncthreads();
+  // unnormalised output: lane covers 8 dims of the V rows of its key group
+  float o[kMaxRep][8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) acc[r] = 0.f;
-  for (int j = grp; j < valid; j += G) {
-    const float vv = j == slot ? vnew[e] : to_f32(vr[(int64_t)j * HD + e]);
+  for (int r = 0; r < kMaxRep; ++r)
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
-      if (r < rep) acc[r] += sc[r * W + j] * vv;
+    for (int i = 0; i < 8; ++i) o[r][i] = 0.f;
+  for (int j = j_lo + grp; j < j_hi; j += KPP) {
+    float vv[8];
+    if (j == slot) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vv[i] = vnew[e0 + i];
+    } else {
+      load8<T, HD>(vv, vr + (int64_t)j * HD + e0);
+    }
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+      if (r < rep) {
+        const float p = sc[r * kDecodeKeys + (j - j_lo)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[r][i] += p * vv[i];
+      }
+    }
   }
-  for (int r = 0; r < rep; ++r) part[grp][r][e] = acc[r];
+  // reduce the key groups of a wave (lanes with equal sub), then across the 4 waves
+#pragma unroll
+  for (int r = 0; r < kMaxRep; ++r) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int off = L; off < 64; off <<= 1) o[r][i] += __shfl_xor(o[r][i], off, 64);
+    }
+  }
+  if (lane < L) {
+    for (int r = 0; r < rep; ++r)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wred[wave][r * HD + e0 + i] = o[r][i];
+  }
   __syncthreads();
   for (int idx = threadIdx.x; idx < rep * HD; idx += kThreads) {
-    const int r = idx / HD, ee = idx - r * HD;
-    float s = 0.f;
-    for (int gg = 0; gg < G; ++gg) s += part[gg][r][ee];
-    og[idx] = from_f32<T>(s);
+    const int r = idx / HD, e = idx - r * HD;
+    pr[r * (HD + 2) + 2 + e] = wred[0][idx] + wred[1][idx] + wred[2][idx] + wred[3][idx];
+    if (e == 0) {
+      pr[r * (HD + 2)] = stat[r][0];
+      pr[r * (HD + 2) + 1] = stat[r][1];
+    }
+  }
+}
+
+// grid (n_req, n_kv_heads)
+template <typename T, int HD>
+__global__ void __launch_bounds__(kThreads) k_swa_decode_combine(const uttt_swa_decode_args a, const float* part,
+                                                                 int nsplit) {
+  const int n = blockIdx.x, kvh = blockIdx.y;
+  const int rep = (int)(a.n_heads / a.n_kv_heads);
+  const int64_t pos = a.positions[n];
+  T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
+  const bool bad = pos < 0 || (a.cos_table != nullptr && pos >= a.table_len);
+  const float* pr = part + ((int64_t)n * a.n_kv_heads + kvh) * nsplit * rep * (HD + 2);
+  for (int idx = threadIdx.x; idx < rep * HD; idx += kThreads) {
+    if (bad) {  // position outside the RoPE table: loud NaN output, cache untouched
+      og[idx] = from_f32<T>(NAN);
+      continue;
+    }
+    const int r = idx / HD, e = idx - r * HD;
+    float mx = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, pr[(s * rep + r) * (HD + 2)]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float* q = pr + (s * rep + r) * (HD + 2);
+      if (q[0] == -INFINITY) continue;
+      const float f = expf(q[0] - mx);
+      den += q[1] * f;
+      num += q[2 + e] * f;
+    }
+    og[idx] = from_f32<T>(num / den);
   }
 }
 
@@ -334,9 +440,12 @@ static void launch_prefill(const uttt_swa_prefill_args& a, hipStream_t st) {
 
 template <typename T, int HD>
 static void launch_decode(const uttt_swa_decode_args& a, hipStream_t st) {
-  const size_t smem = sizeof(float) * (size_t)(a.n_heads / a.n_kv_heads) * (size_t)a.window;
-  hipLaunchKernelGGL((k_swa_decode<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads), dim3(kThreads), smem,
-                     st, a);
+  const int nsplit = decode_splits(a.window);
+  float* part = static_cast<float*>(a.workspace);
+  hipLaunchKernelGGL((k_swa_decode_part<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, (unsigned)nsplit),
+                     dim3(kThreads), 0, st, a, part);
+  hipLaunchKernelGGL((k_swa_decode_combine<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads), dim3(kThreads), 0,
+                     st, a, (const float*)part, nsplit);
 }
 
 }  // namespace uttt
@@ -386,14 +495,25 @@ extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t st
   return launch_status("uttt_swa_prefill");
 }
 
+extern "C" size_t uttt_swa_decode_workspace(int64_t n_req, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                            int64_t window) {
+  if (n_req < 1 || n_kv_heads < 1 || n_heads < n_kv_heads || window < 1 || head_dim < 1) return 0;
+  return sizeof(float) * (size_t)n_req * (size_t)n_heads * (size_t)decode_splits(window) * (size_t)(head_dim + 2);
+}
+
 extern "C" int uttt_swa_decode(const uttt_swa_decode_args* a, uttt_stream_t stream) {
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   UTTT_REQUIRE(a->head_dim == 64 || a->head_dim == 128, "head_dim must be 64 or 128 (got %lld)", (long long)a->head_dim);
-  UTTT_REQUIRE(a->n_req >= 1 && a->n_kv_heads >= 1 && a->n_kv_heads <= 65535 && a->n_heads % a->n_kv_heads == 0,
-               "bad request / head counts");
-  UTTT_REQUIRE(a->n_heads / a->n_kv_heads <= 8, "at most 8 query heads per kv head");
-  UTTT_REQUIRE(a->window >= 1 && a->window * (a->n_heads / a->n_kv_heads) * 4 <= 64 * 1024,
-               "window too large for the decode score buffer");
+  UTTT_REQUIRE(a->n_req >= 1 && a->n_req <= 2147483647 && a->n_kv_heads >= 1 && a->n_kv_heads <= 65535 &&
+               a->n_heads % a->n_kv_heads == 0, "bad request / head counts");
+  UTTT_REQUIRE(a->n_heads / a->n_kv_heads <= kMaxRep, "at most %d query heads per kv head", kMaxRep);
+  UTTT_REQUIRE(a->window >= 1 && decode_splits(a->window) <= 65535, "window out of range");
+  UTTT_REQUIRE(a->workspace != nullptr &&
+               a->workspace_bytes >= uttt_swa_decode_workspace(a->n_req, a->n_heads, a->n_kv_heads, a->head_dim,
+                                                               a->window),
+               "decode workspace too small");
+  UTTT_REQUIRE(aligned16(a->k_ring) && aligned16(a->v_ring) && a->ring_stride_n % 8 == 0,
+               "rings must be 16-byte aligned with a 16-byte multiple request stride");
   UTTT_REQUIRE(a->positions && a->q && a->k_new && a->v_new && a->k_ring && a->v_ring && a->out,
                "pointers must be non-NULL");
   UTTT_REQUIRE((a->cos_table == nullptr) == (a->sin_table == nullptr), "cos/sin tables must both be given or both NULL");

@@ -39,7 +39,7 @@ template <typename T> struct Mma;
 template <> struct Mma<float> {
   static constexpr int kK = 2;     // K per instruction
   static constexpr int kPerLane = 1;
-  static constexpr int kPad = 1;   // LDS row padding (elements)
+  static constexpr int kPad = 4;   // LDS row padding (elements); keeps rows 16-byte aligned
   __device__ __forceinline__ static void step(f32x16& acc, const float* a_row, const float* b_row, int k0, int h) {
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a_row[k0 + h], b_row[k0 + h], acc, 0, 0, 0);
   }
@@ -103,6 +103,114 @@ __device__ __forceinline__ void stage_cols(T* dst, int ldd, const S* src, int64_
     dst[col * ldd + k] = from_f32<T>(v);
   }
 }
+
+// ---------------------------------------------------------------------------
+// Register-staged tiles with 16-byte global loads.  `load` issues every global read of
+// a tile into registers (so a stage can be loaded while the previous one is consumed);
+// `store` converts to the MFMA operand type and writes the LDS tile.  Sources must be
+// 16-byte aligned with row strides that are multiples of 16 bytes.
+// ---------------------------------------------------------------------------
+template <typename S> struct Lanes16;
+template <> struct Lanes16<float> {
+  static constexpr int kVec = 4;
+  __device__ __forceinline__ static float get(const uint4& v, int i) {
+    return __uint_as_float(i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w);
+  }
+};
+template <> struct Lanes16<bf16> {
+  static constexpr int kVec = 8;
+  __device__ __forceinline__ static float get(const uint4& v, int i) {
+    const uint32_t w = i < 2 ? v.x : i < 4 ? v.y : i < 6 ? v.z : v.w;
+    return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+  }
+};
+
+// store kVec source elements of one 16-byte chunk as T, contiguous at dst
+template <typename S, typename T>
+__device__ __forceinline__ void store_chunk(T* dst, const uint4& v) {
+  if constexpr (sizeof(S) == sizeof(T)) {
+    *reinterpret_cast<uint4*>(dst) = v;  // same type: raw copy (dst 16-byte aligned)
+  } else {
+#pragma unroll
+    for (int i = 0; i < Lanes16<S>::kVec; ++i) dst[i] = from_f32<T>(Lanes16<S>::get(v, i));
+  }
+}
+
+// 64 rows x KT columns, row-major source; LDS tile [row][k]
+template <typename S, int KT>
+struct RowStage {
+  static constexpr int kVec = Lanes16<S>::kVec;
+  static constexpr int kPerRow = KT / kVec;
+  static constexpr int kN = 64 * kPerRow / kThreads;
+  static_assert((64 * kPerRow) % kThreads == 0, "tile must split evenly over the workgroup");
+  uint4 r[kN];
+
+  __device__ __forceinline__ void load(const S* src, int64_t ld, int rows_valid) {
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int row = idx / kPerRow, c = idx - row * kPerRow;
+      r[j] = row < rows_valid ? *reinterpret_cast<const uint4*>(src + (int64_t)row * ld + c * kVec)
+                              : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  template <typename T>
+  __device__ __forceinline__ void store(T* dst, int ldd) const {
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int row = idx / kPerRow, c = idx - row * kPerRow;
+      store_chunk<S, T>(dst + row * ldd + c * kVec, r[j]);
+    }
+  }
+};
+
+// KT source rows (k) x 64 columns; LDS tile transposed to [col][k].  One unit loads 8
+// consecutive rows of one 16-byte column group and writes 8 consecutive k per column.
+template <typename S, int KT>
+struct ColStage {
+  static constexpr int kVec = Lanes16<S>::kVec;
+  static constexpr int kColGroups = 64 / kVec;
+  static constexpr int kUnits = (KT / 8) * kColGroups;
+  uint4 r[8];
+  int unit;
+
+  __device__ __forceinline__ void load(const S* src, int64_t ld, int k_valid, int u) {
+    unit = u;
+    if (u >= kUnits) return;
+    const int kg = u / kColGroups, cg = u - kg * kColGroups;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int k = kg * 8 + i;
+      r[i] = k < k_valid ? *reinterpret_cast<const uint4*>(src + (int64_t)k * ld + cg * kVec)
+                         : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  template <typename T>
+  __device__ __forceinline__ void store(T* dst, int ldd) const {
+    if (unit >= kUnits) return;
+    const int kg = unit / kColGroups, cg = unit - kg * kColGroups;
+#pragma unroll
+    for (int v = 0; v < kVec; ++v) {
+      T* d = dst + (cg * kVec + v) * ldd + kg * 8;
+      if constexpr (sizeof(T) == 2) {
+        bf16x8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(Lanes16<S>::get(r[i], v));
+        *reinterpret_cast<bf16x8*>(d) = o;
+      } else {
+        f32x4 o0, o1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o0[i] = Lanes16<S>::get(r[i], v);
+          o1[i] = Lanes16<S>::get(r[i + 4], v);
+        }
+        *reinterpret_cast<f32x4*>(d) = o0;
+        *reinterpret_cast<f32x4*>(d + 4) = o1;
+      }
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Reductions

@@ -33,6 +33,8 @@ inline int launch_status(const char* what) {
 
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
 
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 }  // namespace uttt
 
 #define UTTT_REQUIRE(cond, ...)                              \

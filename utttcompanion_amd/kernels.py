@@ -52,8 +52,11 @@ def _stream(device: torch.device) -> int:
 
 
 def _rows(x: Tensor) -> Tensor:
-    """(B, T, D) with feature stride 1 and token stride D (row stride free)."""
-    if x.stride(2) != 1 or (x.shape[1] > 1 and x.stride(1) != x.shape[2]):
+    """(B, T, D) with feature stride 1, token stride D and a 16-byte aligned base and row
+    stride (the kernels read activations with 16-byte vector loads)."""
+    vec = 16 // x.element_size()
+    if (x.stride(2) != 1 or (x.shape[1] > 1 and x.stride(1) != x.shape[2])
+            or x.data_ptr() % 16 or (x.shape[0] > 1 and x.stride(0) % vec)):
         x = x.contiguous()
     return x
 
@@ -74,7 +77,8 @@ def _state(t: Tensor, name: str) -> Tensor:
         raise ValueError(f"{name}: float64 fast-weight state is not supported by the HIP path")
     if t.dtype != torch.float32:
         t = t.float()  # exact widening of a bf16/fp16 state to the fp32 master
-    return t.contiguous()
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def _read_weight(t: Tensor, bsz: int, name: str) -> Tuple[Tensor, int]:
@@ -86,12 +90,13 @@ def _read_weight(t: Tensor, bsz: int, name: str) -> Tuple[Tensor, int]:
     shared = t.shape[0] == 1 or t.stride(0) == 0
     if shared:
         base = t[:1]
-        if not base.is_contiguous():
-            base = base.contiguous()
+        if not base.is_contiguous() or base.data_ptr() % 16:
+            base = base.contiguous() if not base.is_contiguous() else base.clone()
         return base, 0
     if t.shape[0] != bsz:
         raise ValueError(f"{name}: batch {t.shape[0]} does not match {bsz}")
-    return t.contiguous(), t.shape[1] * t.shape[2]
+    t = t.contiguous()
+    return (t if t.data_ptr() % 16 == 0 else t.clone()), t.shape[1] * t.shape[2]
 
 
 # ---------------------------------------------------------------------------
@@ -381,7 +386,8 @@ def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
 
 
 def swa_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_ring: Tensor, v_ring: Tensor, positions: Tensor,
-               cos: Optional[Tensor] = None, sin: Optional[Tensor] = None, out: Optional[Tensor] = None) -> Tensor:
+               cos: Optional[Tensor] = None, sin: Optional[Tensor] = None, out: Optional[Tensor] = None,
+               workspace: Optional[Tensor] = None) -> Tensor:
     """One decode step for N requests.  q (N, H, hd), k_new/v_new (N, Hkv, hd) (un-rotated when
     tables are given), rings (N, Hkv, W, hd), positions (N,) int64 on the device."""
     n, heads, hd = q.shape
@@ -418,6 +424,10 @@ def swa_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_ring: Tensor, v_ring: 
     a.k_ring, a.v_ring, a.ring_stride_n = _p(k_ring), _p(v_ring), k_ring.stride(0)
     a.out, a.o_stride_n = _p(out), out.stride(0)
     lib = N.load_library()
+    nbytes = lib.uttt_swa_decode_workspace(n, heads, hkv, hd, window)
+    if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = _p(workspace), workspace.numel()
     with torch.cuda.device(dev):
         N.check(lib.uttt_swa_decode(C.byref(a), _stream(dev)), "uttt_swa_decode")
     return out
