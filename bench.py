@@ -48,6 +48,8 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--phase-iters", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--sections", default="prefill,update,decode,cpu",
+                    help="comma list of prefill, update, decode, cpu (profiling runs pick a subset)")
     ap.add_argument("--cpu-tokens", type=int, default=256, help="tokens of the CPU baseline sample (1 row)")
     return ap.parse_args()
 
@@ -144,26 +146,37 @@ def phase_work(p: int, B: int, C: int, D: int, F: int):
 
 
 def bench_decode(iters: int):
+    """The ring-buffer decode kernel at the config-4 shape: one decode step's 12 layer calls
+    (each layer its own rings) recorded in a HIP graph, replayed ``iters`` times."""
     import torch
     from utttcompanion_amd import kernels as K
-    N_REQ, H, HKV, HD, W = 32, 12, 4, 64, 512
+    N_REQ, H, HKV, HD, W, LAYERS = 32, 12, 4, 64, 512, 12
     g = torch.Generator(device="cuda").manual_seed(3)
     q = torch.randn(N_REQ, H, HD, device="cuda", generator=g).to(torch.bfloat16)
     kn = torch.randn(N_REQ, HKV, HD, device="cuda", generator=g).to(torch.bfloat16)
     vn = torch.randn_like(kn)
-    kr = torch.randn(N_REQ, HKV, W, HD, device="cuda", generator=g).to(torch.bfloat16)
-    vr = torch.randn_like(kr)
+    rings = [(torch.randn(N_REQ, HKV, W, HD, device="cuda", generator=g).to(torch.bfloat16),
+              torch.randn(N_REQ, HKV, W, HD, device="cuda", generator=g).to(torch.bfloat16)) for _ in range(LAYERS)]
     pos = torch.randint(W, 4 * W, (N_REQ,), device="cuda", generator=g)
+    out = torch.empty_like(q)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
     with torch.no_grad():
-        out = K.swa_decode(q, kn, vn, kr, vr, pos)
+        for kr, vr in rings:
+            K.swa_decode(q, kn, vn, kr, vr, pos, out=out, workspace=ws)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for kr, vr in rings:
+                K.swa_decode(q, kn, vn, kr, vr, pos, out=out, workspace=ws)
+        graph.replay()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(iters):
-            K.swa_decode(q, kn, vn, kr, vr, pos, out=out)
+            graph.replay()
         end.record()
         torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / iters
+    ms = start.elapsed_time(end) / (iters * LAYERS)
     kv_bytes = 2 * N_REQ * HKV * W * HD * 2 + 2 * N_REQ * HKV * HD * 2 + 2 * N_REQ * H * HD * 2
     return ms, kv_bytes, dict(requests=N_REQ, heads=H, kv_heads=HKV, head_dim=HD, window=W)
 
@@ -200,10 +213,17 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
         return 1
+    sections = set(args.sections.split(","))
     model = build_model()
-    ms, finite = bench_prefill(model, args.steps, args.warmup)
     tokens = C2_BATCH * C2_SEQ
-    log(f"prefill {ms:.2f} ms/step -> {tokens / ms * 1e3:.0f} tok/s (finite={finite})")
+    ms, finite = float("nan"), False
+    if "prefill" in sections:
+        ms, finite = bench_prefill(model, args.steps, args.warmup)
+        log(f"prefill {ms:.2f} ms/step -> {tokens / ms * 1e3:.0f} tok/s (finite={finite})")
+    if "update" not in sections:
+        print(json.dumps({"metric": METRIC, "value": round(tokens / ms * 1e3, 1), "unit": "tok/s",
+                          "ms_per_step": round(ms, 3), "partial_sections": sorted(sections)}), flush=True)
+        return 0
 
     per, shape = bench_update_phases(args.phase_iters)
     total_ms = sum(per)
@@ -226,7 +246,7 @@ def main() -> int:
               "mfma_frac": round(upd_flops / (total_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
     log(f"update phases (ms): {update['phase_ms']}")
 
-    dec_ms, dec_bytes, dec_shape = bench_decode(200)
+    dec_ms, dec_bytes, dec_shape = bench_decode(20) if "decode" in sections else (float("nan"), 1, {})
     dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
     decode = {"kernel": "k_swa_decode", "us_per_layer_step": round(dec_ms * 1e3, 2), "achieved_gbs": round(dec_gbs, 1),
               "hbm_frac": round(dec_gbs / PEAK_HBM_GBS, 4), "shape": dec_shape,
@@ -234,7 +254,7 @@ def main() -> int:
     log(f"decode kernel {dec_ms * 1e3:.1f} us -> {dec_gbs:.0f} GB/s")
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and "cpu" in sections:
         log("timing the CPU oracle baseline")
         cpu = cpu_baseline(model, args.cpu_tokens)
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")

@@ -215,6 +215,7 @@ def test_rope_append_is_bit_exact(dtype):
     dict(b=1, h=4, hkv=4, tq=64, tkv=575, hd=64, win=512),       # chunk step over a cache (C2 shape)
     dict(b=1, h=16, hkv=4, tq=130, tkv=400, hd=128, win=1024),   # hd 128, window > kv (causal)
     dict(b=2, h=4, hkv=1, tq=70, tkv=70, hd=64, win=1),          # window 1: self only
+    dict(b=4, h=8, hkv=4, tq=1024, tkv=1024, hd=64, win=256),    # config-1 attention: no key split
 ])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_swa_prefill_matches_oracle(case, dtype):
@@ -234,6 +235,27 @@ def test_swa_prefill_matches_oracle(case, dtype):
         assert rel_err(got, ref) <= F32_REL
     else:
         assert max_abs(got, ref) <= BF16_ABS
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_swa_prefill_ignores_stale_workspace_contents(dtype):
+    """Splits with no visible key leave their partial rows unwritten; a workspace full of
+    NaN (reused memory) must not leak into the output.  Single-query steps exercise it."""
+    K = kernels()
+    g = torch.Generator().manual_seed(41)
+    for tkv, win in ((21, 24), (70, 8), (300, 128)):
+        q = torch.randn(1, 1, 2, 64, generator=g).to(dtype).transpose(1, 2)
+        k = torch.randn(1, 1, tkv, 64, generator=g).to(dtype)
+        v = torch.randn(1, 1, tkv, 64, generator=g).to(dtype)
+        ref = om.sliding_window_attention(q.float(), k.float(), v.float(), win, tkv - 1)
+        ws = torch.full((1 << 22,), float("nan"), device=DEV).view(torch.uint8)
+        with torch.no_grad():
+            got = K.swa_prefill(*to_dev(q, k, v), win, tkv - 1, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got).all(), (tkv, win)
+        tol = F32_REL if dtype == torch.float32 else BF16_ABS
+        err = rel_err(got, ref) if dtype == torch.float32 else max_abs(got, ref)
+        assert err <= tol, (tkv, win, err)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 UPDATE_PHASES = 5
@@ -78,6 +78,7 @@ class SwaPrefillArgs(C.Structure):
         ("k", _P), ("k_stride_b", _I64), ("k_stride_h", _I64), ("k_stride_t", _I64),
         ("v", _P), ("v_stride_b", _I64), ("v_stride_h", _I64), ("v_stride_t", _I64),
         ("out", _P), ("o_stride_b", _I64), ("o_stride_h", _I64), ("o_stride_t", _I64),
+        ("workspace", _P), ("workspace_bytes", C.c_size_t),
     ]
 
 
@@ -115,6 +116,7 @@ SIGNATURES = {
     "uttt_readout_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_swiglu_readout": (C.c_int, [C.POINTER(ReadoutArgs), _P, C.c_size_t, _P]),
     "uttt_rope_kv_append": (C.c_int, [C.POINTER(RopeAppendArgs), _P]),
+    "uttt_swa_prefill_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "uttt_swa_prefill": (C.c_int, [C.POINTER(SwaPrefillArgs), _P]),
     "uttt_swa_decode_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
     "uttt_swa_decode": (C.c_int, [C.POINTER(SwaDecodeArgs), _P]),

@@ -178,18 +178,19 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
   const float inv_d = 1.0f / (float)a.D;
 
   float z[kMaxPerThread];
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) z[i] = 0.f;
+  for (int sp = 0; sp < a.nsplit; ++sp) {  // one round trip per split: the row's loads go out together
+    const float* src = a.zp + (((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D;
+#pragma unroll
+    for (int i = 0; i < kMaxPerThread; ++i) {
+      const int d = threadIdx.x + i * kThreads;
+      if (d < a.D) z[i] += src[d];
+    }
+  }
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
-    const int d = threadIdx.x + i * kThreads;
-    float acc = 0.f;
-    if (d < a.D) {
-      for (int sp = 0; sp < a.nsplit; ++sp)
-        acc += a.zp[(((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D + d];
-    }
-    z[i] = acc;
-    s += acc;
-  }
+  for (int i = 0; i < kMaxPerThread; ++i) s += z[i];
   const float mean = block_sum(s, red) * inv_d;
   float s2 = 0.f;
 #pragma unroll
@@ -273,18 +274,19 @@ __global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
   if (t >= a.ntok) return;
   const float inv_d = 1.0f / (float)a.D;
   float z[kMaxPerThread];
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) z[i] = 0.f;
+  for (int sp = 0; sp < a.nsplit; ++sp) {  // one round trip per split: the row's loads go out together
+    const float* src = a.zp + (((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D;
+#pragma unroll
+    for (int i = 0; i < kMaxPerThread; ++i) {
+      const int d = threadIdx.x + i * kThreads;
+      if (d < a.D) z[i] += src[d];
+    }
+  }
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
-    const int d = threadIdx.x + i * kThreads;
-    float acc = 0.f;
-    if (d < a.D) {
-      for (int sp = 0; sp < a.nsplit; ++sp)
-        acc += a.zp[(((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D + d];
-    }
-    z[i] = acc;
-    s += acc;
-  }
+  for (int i = 0; i < kMaxPerThread; ++i) s += z[i];
   const float mean = block_sum(s, red) * inv_d;
   float s2 = 0.f;
 #pragma unroll

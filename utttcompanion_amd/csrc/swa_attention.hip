@@ -21,7 +21,7 @@ namespace uttt {
 template <typename T> struct Mma16;
 template <> struct Mma16<float> {
   static constexpr int kK = 4;
-  static constexpr int kPad = 1;
+  static constexpr int kPad = 4;  // rows stay 16-byte aligned
   __device__ __forceinline__ static void step(f32x4& acc, const float* a_row, const float* b_row, int k0, int g) {
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a_row[k0 + g], b_row[k0 + g], acc, 0, 0, 0);
   }
@@ -100,18 +100,109 @@ __global__ void __launch_bounds__(kThreads) k_rope_append(const uttt_rope_append
 }
 
 // ---------------------------------------------------------------------------
-// Prefill: grid (ceil(q_len / 64), n_heads, batch); wave w owns queries 16w..16w+15
+// Prefill.  grid (q tiles of 64, n_heads, batch * nsplit): the key tiles that intersect a
+// q tile's window are divided among `nsplit` workgroups; each wave owns 16 queries.  With
+// nsplit > 1 the workgroups write fp32 partials (row max, row sum, unnormalised output)
+// and k_swa_prefill_combine merges them.  Q / K rows are staged with 16-byte loads, V is
+// transposed in registers to [e][key]; the next key tile is loaded while the current one
+// is consumed.
 // ---------------------------------------------------------------------------
 template <typename T, int HD>
-__global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill_args a) {
+struct AttnStage {
+  static constexpr int kVec = 16 / (int)sizeof(T);
+  static constexpr int kChunksPerRow = HD / kVec;
+  static constexpr int kRowChunks = 64 * kChunksPerRow / kThreads;  // per thread, for a 64-row tile
+  static constexpr int kVUnits = 8 * kChunksPerRow;                 // 8 keys x one chunk per unit
+  uint4 kr[kRowChunks];
+  uint4 vr[8];
+
+  __device__ __forceinline__ void load(const T* k, const T* v, int64_t st_k, int64_t st_v, int n) {
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int row = idx / kChunksPerRow, c = idx - row * kChunksPerRow;
+      kr[j] = row < n ? *reinterpret_cast<const uint4*>(k + row * st_k + c * kVec) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (threadIdx.x < kVUnits) {
+      const int kg = threadIdx.x / kChunksPerRow, c = threadIdx.x - kg * kChunksPerRow;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = kg * 8 + i;
+        vr[i] = row < n ? *reinterpret_cast<const uint4*>(v + row * st_v + c * kVec) : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+  template <int LQ, int LV>
+  __device__ __forceinline__ void store(T* ks, T* vt) const {
+#pragma unroll
+    for (int j = 0; j < kRowChunks; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int row = idx / kChunksPerRow, c = idx - row * kChunksPerRow;
+      *reinterpret_cast<uint4*>(ks + row * LQ + c * kVec) = kr[j];
+    }
+    if (threadIdx.x < kVUnits) {
+      const int kg = threadIdx.x / kChunksPerRow, c = threadIdx.x - kg * kChunksPerRow;
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        T* d = vt + (c * kVec + e) * LV + kg * 8;
+        if constexpr (sizeof(T) == 2) {
+          bf16x8 o;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(Lanes16<bf16>::get(vr[i], e));
+          *reinterpret_cast<bf16x8*>(d) = o;
+        } else {
+          f32x4 o0, o1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            o0[i] = Lanes16<float>::get(vr[i], e);
+            o1[i] = Lanes16<float>::get(vr[i + 4], e);
+          }
+          *reinterpret_cast<f32x4*>(d) = o0;
+          *reinterpret_cast<f32x4*>(d + 4) = o1;
+        }
+      }
+    }
+  }
+};
+
+struct PrefillPlan {
+  int nqt, nsplit, tiles_per_split, q_pad;
+};
+
+constexpr int kMaxPrefillSplits = 16;
+
+__host__ __device__ __forceinline__ int prefill_max_tiles(int64_t kv_len, int64_t window) {
+  const int64_t span = min(kv_len, window + 63);
+  return (int)((span + 63) / 64) + 1;
+}
+
+static PrefillPlan prefill_plan(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len, int64_t window) {
+  PrefillPlan p;
+  p.nqt = (int)((q_len + 63) / 64);
+  p.q_pad = p.nqt * 64;
+  const int64_t base = (int64_t)p.nqt * heads * batch;
+  const int max_tiles = prefill_max_tiles(kv_len, window);
+  int64_t ns = (512 + base - 1) / base;
+  if (ns > max_tiles) ns = max_tiles;
+  if (ns > kMaxPrefillSplits) ns = kMaxPrefillSplits;
+  if (ns < 1) ns = 1;
+  p.tiles_per_split = (max_tiles + (int)ns - 1) / (int)ns;
+  p.nsplit = (max_tiles + p.tiles_per_split - 1) / p.tiles_per_split;
+  return p;
+}
+
+template <typename T, int HD>
+__global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill_args a, float* part, int nsplit,
+                                                          int tiles_per_split, int q_pad) {
   constexpr int PAD = Mma16<T>::kPad;
   constexpr int LQ = HD + PAD;   // q/k rows [token][e]
   constexpr int LV = 64 + PAD;   // v^T rows [e][key], p rows [query][key]
-  __shared__ T qs[64 * LQ];
-  __shared__ T ks[64 * LQ];
-  __shared__ T vt[HD * LV];
-  __shared__ T ps[64 * LV];
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  __shared__ __align__(16) T qs[64 * LQ];
+  __shared__ __align__(16) T ks[64 * LQ];
+  __shared__ __align__(16) T vt[HD * LV];
+  __shared__ __align__(16) T ps[64 * LV];
+  const int qt = blockIdx.x, h = blockIdx.y;
+  const int b = blockIdx.z / nsplit, sp = blockIdx.z - b * nsplit;
   const int rep = (int)(a.n_heads / a.n_kv_heads);
   const int kvh = h / rep;
   const int q0 = qt * 64;
@@ -119,18 +210,32 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
   const int64_t p_first = a.q_offset + q0, p_last = a.q_offset + q0 + qn - 1;
   const int64_t lo = max((int64_t)0, p_first - a.window + 1);
   const int64_t hi = min(a.kv_len, p_last + 1);  // exclusive
+  const int ntiles = (int)((hi - lo + 63) / 64);
+  const int t_begin = sp * tiles_per_split, t_end = min(ntiles, t_begin + tiles_per_split);
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int g = lane >> 4, c = lane & 15;
+  float* pr = part + ((((int64_t)b * a.n_heads + h) * nsplit + sp) * q_pad + q0) * (HD + 2);
+  if (t_begin >= t_end) {  // nothing in this split's range (only with nsplit > 1)
+    for (int idx = threadIdx.x; idx < 64; idx += kThreads) {
+      pr[idx * (HD + 2)] = -INFINITY;
+      pr[idx * (HD + 2) + 1] = 0.f;
+    }
+    return;
+  }
 
   const T* qg = static_cast<const T*>(a.q) + b * a.q_stride_b + h * a.q_stride_h;
   const T* kg = static_cast<const T*>(a.k) + b * a.k_stride_b + kvh * a.k_stride_h;
   const T* vg = static_cast<const T*>(a.v) + b * a.v_stride_b + kvh * a.v_stride_h;
-
-  for (int idx = threadIdx.x; idx < 64 * HD; idx += kThreads) {
-    const int r = idx / HD, e = idx - r * HD;
-    qs[r * LQ + e] = r < qn ? qg[(q0 + r) * a.q_stride_t + e] : from_f32<T>(0.f);
+  {
+    constexpr int kVec = 16 / (int)sizeof(T), kCpr = HD / kVec;
+    for (int idx = threadIdx.x; idx < 64 * kCpr; idx += kThreads) {
+      const int r = idx / kCpr, cc = idx - r * kCpr;
+      *reinterpret_cast<uint4*>(qs + r * LQ + cc * kVec) =
+          r < qn ? *reinterpret_cast<const uint4*>(qg + (q0 + r) * a.q_stride_t + cc * kVec) : make_uint4(0u, 0u, 0u, 0u);
+    }
   }
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int g = lane >> 4, c = lane & 15;
   float m_run[4], l_run[4];
   f32x4 o[HD / 16];
 #pragma unroll
@@ -141,16 +246,22 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
 #pragma unroll
   for (int t = 0; t < HD / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t kt0 = lo; kt0 < hi; kt0 += 64) {
-    const int kn = (int)min((int64_t)64, hi - kt0);
+  AttnStage<T, HD> stg;
+  {
+    const int64_t kt0 = lo + (int64_t)t_begin * 64;
+    stg.load(kg + kt0 * a.k_stride_t, vg + kt0 * a.v_stride_t, a.k_stride_t, a.v_stride_t,
+             (int)min((int64_t)64, hi - kt0));
+  }
+  for (int kt = t_begin; kt < t_end; ++kt) {
+    const int64_t kt0 = lo + (int64_t)kt * 64;
     __syncthreads();  // previous tile fully consumed
-    for (int idx = threadIdx.x; idx < 64 * HD; idx += kThreads) {
-      const int j = idx / HD, e = idx - j * HD;
-      const bool in = j < kn;
-      ks[j * LQ + e] = in ? kg[(kt0 + j) * a.k_stride_t + e] : from_f32<T>(0.f);
-      vt[e * LV + j] = in ? vg[(kt0 + j) * a.v_stride_t + e] : from_f32<T>(0.f);
-    }
+    stg.template store<LQ, LV>(ks, vt);
     __syncthreads();
+    if (kt + 1 < t_end) {
+      const int64_t nx = kt0 + 64;
+      stg.load(kg + nx * a.k_stride_t, vg + nx * a.v_stride_t, a.k_stride_t, a.v_stride_t,
+               (int)min((int64_t)64, hi - nx));
+    }
 
     // S = Q K^T for this wave's 16 queries x 64 keys (4 tiles of 16 keys)
     f32x4 s[4];
@@ -159,7 +270,6 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
       s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
       wave_mma16<T, HD>(s[n], qs + (16 * w) * LQ, LQ, ks + (16 * n) * LQ, LQ);
     }
-    // scale, mask, online softmax (rows 4g+i of the wave's 16)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int qi = q0 + 16 * w + 4 * g + i;
@@ -194,20 +304,77 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
       for (int n = 0; n < 4; ++n) ps[(16 * w + 4 * g + i) * LV + 16 * n + c] = from_f32<T>(s[n][i]);
     }
     __syncthreads();
-    // O += P V : A = P rows [query][key], B^T = V^T rows [e][key]
 #pragma unroll
     for (int t = 0; t < HD / 16; ++t) wave_mma16<T, 64>(o[t], ps + (16 * w) * LV, LV, vt + (16 * t) * LV, LV);
   }
 
-  T* og = static_cast<T*>(a.out) + b * a.o_stride_b + h * a.o_stride_h;
+  if (nsplit == 1) {
+    T* og = static_cast<T*>(a.out) + b * a.o_stride_b + h * a.o_stride_h;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int qi = q0 + 16 * w + 4 * g + i;
-    if (qi >= a.q_len) continue;
-    const float inv = l_run[i] > 0.f ? 1.0f / l_run[i] : 0.f;
+    for (int i = 0; i < 4; ++i) {
+      const int qi = q0 + 16 * w + 4 * g + i;
+      if (qi >= a.q_len) continue;
+      const float inv = l_run[i] > 0.f ? 1.0f / l_run[i] : 0.f;
 #pragma unroll
-    for (int t = 0; t < HD / 16; ++t) og[(int64_t)qi * a.o_stride_t + 16 * t + c] = from_f32<T>(o[t][i] * inv);
+      for (int t = 0; t < HD / 16; ++t) og[(int64_t)qi * a.o_stride_t + 16 * t + c] = from_f32<T>(o[t][i] * inv);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * w + 4 * g + i;
+      float* row = pr + r * (HD + 2);
+      if (c == 0) {
+        row[0] = m_run[i];
+        row[1] = l_run[i];
+      }
+#pragma unroll
+      for (int t = 0; t < HD / 16; ++t) row[2 + 16 * t + c] = o[t][i];
+    }
   }
+}
+
+// grid (q_pad * HD / 256, n_heads, batch): one output element per thread; the split
+// partials of its row are loaded together (at most kMaxPrefillSplits).
+template <typename T, int HD>
+__global__ void __launch_bounds__(kThreads) k_swa_prefill_combine(const uttt_swa_prefill_args a, const float* part,
+                                                                  int nsplit, int q_pad) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int idx = blockIdx.x * kThreads + threadIdx.x;
+  const int qi = idx / HD, e = idx - qi * HD;
+  if (qi >= a.q_len) return;
+  const float* base = part + (((int64_t)b * a.n_heads + h) * nsplit) * q_pad * (HD + 2) + (int64_t)qi * (HD + 2);
+  const int64_t sstride = (int64_t)q_pad * (HD + 2);
+  float m[kMaxPrefillSplits], l[kMaxPrefillSplits], o[kMaxPrefillSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxPrefillSplits; ++s) {
+    if (s < nsplit) {
+      const float* row = base + s * sstride;
+      m[s] = row[0];
+      l[s] = row[1];
+      o[s] = row[2 + e];
+    } else {
+      m[s] = -INFINITY;
+      l[s] = 0.f;
+      o[s] = 0.f;
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxPrefillSplits; ++s) mx = fmaxf(mx, m[s]);
+  float num = 0.f, den = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll
+    for (int s = 0; s < kMaxPrefillSplits; ++s) {
+      // a split with no visible key leaves its output partial unwritten: skip it, do not scale it
+      if (m[s] != -INFINITY) {
+        const float f = expf(m[s] - mx);
+        den += l[s] * f;
+        num += o[s] * f;
+      }
+    }
+  }
+  T* og = static_cast<T*>(a.out) + b * a.o_stride_b + h * a.o_stride_h;
+  og[(int64_t)qi * a.o_stride_t + e] = from_f32<T>(den > 0.f ? num / den : 0.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -216,41 +383,39 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
 // query head; k_swa_decode_combine merges the splits.  Lanes cooperate on a key row with
 // 16-byte loads (HD/8 lanes per key).
 // ---------------------------------------------------------------------------
-constexpr int kDecodeKeys = 128;
+constexpr int kDecodeKeys = 64;
 constexpr int kMaxRep = 8;
-
-struct DecodeDims {
-  int rep, nsplit;
-};
 
 __host__ __device__ __forceinline__ int decode_splits(int64_t window) {
   return (int)((window + kDecodeKeys - 1) / kDecodeKeys);
 }
 
-template <typename T, int HD>
-__device__ __forceinline__ void load8(float (&dst)[8], const T* src) {
-  const uint4 v = *reinterpret_cast<const uint4*>(src);
+template <typename T>
+__device__ __forceinline__ void unpack8(float (&dst)[8], const uint4* v) {
   if constexpr (sizeof(T) == 2) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i] = Lanes16<bf16>::get(v, i);
+    for (int i = 0; i < 8; ++i) dst[i] = Lanes16<bf16>::get(v[0], i);
   } else {
-    const uint4 v2 = *reinterpret_cast<const uint4*>(src + 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      dst[i] = Lanes16<float>::get(v, i);
-      dst[i + 4] = Lanes16<float>::get(v2, i);
+      dst[i] = Lanes16<float>::get(v[0], i);
+      dst[i + 4] = Lanes16<float>::get(v[1], i);
     }
   }
 }
 
+// grid (n_req, n_kv_heads, splits of kDecodeKeys slots)
 template <typename T, int HD>
 __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_decode_args a, float* part) {
-  constexpr int L = HD / 8;            // lanes per key row (8 elements each)
-  constexpr int KPP = kThreads / L;    // keys per pass
+  constexpr int L = HD / 8;                  // lanes per key row (8 elements each)
+  constexpr int KPP = kThreads / L;          // keys per pass
+  constexpr int PASSES = kDecodeKeys / KPP;  // 2 (HD 64) or 4 (HD 128)
+  constexpr int CH = sizeof(T) == 2 ? 1 : 2; // 16-byte chunks per 8 elements
   __shared__ float qf[kMaxRep * HD];
   __shared__ float knew[HD], vnew[HD];
   __shared__ float sc[kMaxRep * kDecodeKeys];
   __shared__ float wred[4][kMaxRep * HD];
+  __shared__ float stat[kMaxRep][2];
   const int n = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int rep = (int)(a.n_heads / a.n_kv_heads);
   const int nsplit = gridDim.z;
@@ -268,14 +433,27 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
     }
     return;
   }
+  T* kr = static_cast<T*>(a.k_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
+  T* vr = static_cast<T*>(a.v_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
+  const int sub = threadIdx.x % L, grp = threadIdx.x / L;
+  const int e0 = sub * 8;
+  // every K / V load of this thread first (the slot being written is read from LDS instead)
+  uint4 kraw[PASSES][CH], vraw[PASSES][CH];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int j = j_lo + grp + p * KPP;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const bool ld = j < j_hi && j != slot;
+      kraw[p][c] = ld ? *reinterpret_cast<const uint4*>(kr + (int64_t)j * HD + e0 + c * (8 / CH)) : make_uint4(0u, 0u, 0u, 0u);
+      vraw[p][c] = ld ? *reinterpret_cast<const uint4*>(vr + (int64_t)j * HD + e0 + c * (8 / CH)) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
   const T* qg = static_cast<const T*>(a.q) + n * a.q_stride_n + (int64_t)kvh * rep * HD;
   const T* kn = static_cast<const T*>(a.k_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
   const T* vn = static_cast<const T*>(a.v_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
-  T* kr = static_cast<T*>(a.k_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
-  T* vr = static_cast<T*>(a.v_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
   const bool owns_slot = slot >= j_lo && slot < j_hi;
   constexpr int half = HD / 2;
-
   // RoPE (activation-dtype rounding as the reference); the split holding the slot writes the ring
   for (int idx = threadIdx.x; idx < (rep + 1) * half; idx += kThreads) {
     const int r = idx / half, e = idx - r * half;
@@ -302,16 +480,15 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
   }
   __syncthreads();
 
-  const int sub = threadIdx.x % L, grp = threadIdx.x / L;
-  const int e0 = sub * 8;
-  // scores for keys j_lo + grp, + KPP, ...
-  for (int j = j_lo + grp; j < j_hi; j += KPP) {
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int j = j_lo + grp + p * KPP;
     float kv[8];
     if (j == slot) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) kv[i] = knew[e0 + i];
     } else {
-      load8<T, HD>(kv, kr + (int64_t)j * HD + e0);
+      unpack8<T>(kv, kraw[p]);
     }
     float acc[kMaxRep];
 #pragma unroll
@@ -320,70 +497,64 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
       if (r < rep) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) s += qf[r * HD + e0 + i] * kv[i];
+#pragma unroll
+        for (int off = 1; off < L; off <<= 1) s += __shfl_xor(s, off, 64);
       }
       acc[r] = s;
     }
-#pragma unroll
-    for (int r = 0; r < kMaxRep; ++r) {
-#pragma unroll
-      for (int off = 1; off < L; off <<= 1) acc[r] += __shfl_xor(acc[r], off, 64);
-    }
-    if (sub == 0) {
+    if (sub == 0 && j < j_hi) {
       for (int r = 0; r < rep; ++r) sc[r * kDecodeKeys + (j - j_lo)] = acc[r] * a.scale;
     }
   }
   __syncthreads();
-  // per-head max and exp over this split's keys (one wave per head, looping)
   const int cnt = j_hi - j_lo;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __shared__ float stat[kMaxRep][2];
   for (int r = wave; r < rep; r += 4) {
-    float mx = -INFINITY;
-    for (int j = lane; j < cnt; j += 64) mx = fmaxf(mx, sc[r * kDecodeKeys + j]);
-    mx = wave_max(mx);
-    float sum = 0.f;
-    for (int j = lane; j < cnt; j += 64) {
-      const float p = expf(sc[r * kDecodeKeys + j] - mx);
-      sc[r * kDecodeKeys + j] = p;
-      sum += p;
-    }
-    sum = wave_sum(sum);
+    const float v0 = lane < cnt ? sc[r * kDecodeKeys + lane] : -INFINITY;
+    const float mx = wave_max(v0);
+    const float p0 = lane < cnt ? expf(v0 - mx) : 0.f;
+    if (lane < cnt) sc[r * kDecodeKeys + lane] = p0;
+    const float sum = wave_sum(p0);
     if (lane == 0) {
       stat[r][0] = mx;
       stat[r][1] = sum;
     }
   }
   __syncthreads();
-  // unnormalised output: lane covers 8 dims of the V rows of its key group
   float o[kMaxRep][8];
 #pragma unroll
   for (int r = 0; r < kMaxRep; ++r)
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[r][i] = 0.f;
-  for (int j = j_lo + grp; j < j_hi; j += KPP) {
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int j = j_lo + grp + p * KPP;
+    if (j >= j_hi) continue;
     float vv[8];
     if (j == slot) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) vv[i] = vnew[e0 + i];
     } else {
-      load8<T, HD>(vv, vr + (int64_t)j * HD + e0);
+      unpack8<T>(vv, vraw[p]);
     }
 #pragma unroll
     for (int r = 0; r < kMaxRep; ++r) {
       if (r < rep) {
-        const float p = sc[r * kDecodeKeys + (j - j_lo)];
+        const float pw = sc[r * kDecodeKeys + (j - j_lo)];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[r][i] += p * vv[i];
+        for (int i = 0; i < 8; ++i) o[r][i] += pw * vv[i];
       }
     }
   }
   // reduce the key groups of a wave (lanes with equal sub), then across the 4 waves
 #pragma unroll
   for (int r = 0; r < kMaxRep; ++r) {
+    if (r < rep) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 8; ++i) {
 #pragma unroll
-      for (int off = L; off < 64; off <<= 1) o[r][i] += __shfl_xor(o[r][i], off, 64);
+        for (int off = L; off < 64; off <<= 1) o[r][i] += __shfl_xor(o[r][i], off, 64);
+      }
     }
   }
   if (lane < L) {
@@ -402,7 +573,9 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
   }
 }
 
-// grid (n_req, n_kv_heads)
+constexpr int kMaxDecodeSplits = 64;
+
+// grid (n_req, n_kv_heads): one output element per thread, splits loaded together
 template <typename T, int HD>
 __global__ void __launch_bounds__(kThreads) k_swa_decode_combine(const uttt_swa_decode_args a, const float* part,
                                                                  int nsplit) {
@@ -412,30 +585,55 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_combine(const uttt_swa_
   T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
   const bool bad = pos < 0 || (a.cos_table != nullptr && pos >= a.table_len);
   const float* pr = part + ((int64_t)n * a.n_kv_heads + kvh) * nsplit * rep * (HD + 2);
+  const int used = bad ? 0 : (int)((min(pos + 1, a.window) + kDecodeKeys - 1) / kDecodeKeys);
   for (int idx = threadIdx.x; idx < rep * HD; idx += kThreads) {
     if (bad) {  // position outside the RoPE table: loud NaN output, cache untouched
       og[idx] = from_f32<T>(NAN);
       continue;
     }
     const int r = idx / HD, e = idx - r * HD;
-    float mx = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, pr[(s * rep + r) * (HD + 2)]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* q = pr + (s * rep + r) * (HD + 2);
-      if (q[0] == -INFINITY) continue;
-      const float f = expf(q[0] - mx);
-      den += q[1] * f;
-      num += q[2 + e] * f;
+    float m[16], l[16], o[16];
+    float mx = -INFINITY, num = 0.f, den = 0.f;
+    for (int s0 = 0; s0 < used; s0 += 16) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int s = s0 + k;
+        const float* q = pr + (s * rep + r) * (HD + 2);
+        m[k] = s < used ? q[0] : -INFINITY;
+        l[k] = s < used ? q[1] : 0.f;
+        o[k] = s < used ? q[2 + e] : 0.f;
+      }
+      float cm = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) cm = fmaxf(cm, m[k]);
+      const float nm = fmaxf(mx, cm);
+      const float scale_old = mx == -INFINITY ? 0.f : expf(mx - nm);
+      num *= scale_old;
+      den *= scale_old;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (m[k] != -INFINITY) {
+          const float f = expf(m[k] - nm);
+          den += l[k] * f;
+          num += o[k] * f;
+        }
+      }
+      mx = nm;
     }
     og[idx] = from_f32<T>(num / den);
   }
 }
 
 template <typename T, int HD>
-static void launch_prefill(const uttt_swa_prefill_args& a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.q_len + 63) / 64), (unsigned)a.n_heads, (unsigned)a.batch);
-  hipLaunchKernelGGL((k_swa_prefill<T, HD>), grid, dim3(kThreads), 0, st, a);
+static void launch_prefill(const uttt_swa_prefill_args& a, const PrefillPlan& p, hipStream_t st) {
+  float* part = static_cast<float*>(a.workspace);
+  const dim3 grid((unsigned)p.nqt, (unsigned)a.n_heads, (unsigned)(a.batch * p.nsplit));
+  hipLaunchKernelGGL((k_swa_prefill<T, HD>), grid, dim3(kThreads), 0, st, a, part, p.nsplit, p.tiles_per_split,
+                     p.q_pad);
+  if (p.nsplit > 1)
+    hipLaunchKernelGGL((k_swa_prefill_combine<T, HD>),
+                       dim3((unsigned)((int64_t)p.q_pad * HD / kThreads), (unsigned)a.n_heads, (unsigned)a.batch),
+                       dim3(kThreads), 0, st, a, (const float*)part, p.nsplit, p.q_pad);
 }
 
 template <typename T, int HD>
@@ -473,11 +671,18 @@ extern "C" int uttt_rope_kv_append(const uttt_rope_append_args* a, uttt_stream_t
   return launch_status("uttt_rope_kv_append");
 }
 
+extern "C" size_t uttt_swa_prefill_workspace(int64_t batch, int64_t n_heads, int64_t q_len, int64_t kv_len,
+                                             int64_t head_dim, int64_t window) {
+  if (batch < 1 || n_heads < 1 || q_len < 1 || kv_len < 1 || window < 1 || head_dim < 1) return 0;
+  const PrefillPlan p = prefill_plan(batch, n_heads, q_len, kv_len, window);
+  if (p.nsplit == 1) return 16;
+  return sizeof(float) * (size_t)p.nsplit * (size_t)batch * (size_t)n_heads * (size_t)p.q_pad * (size_t)(head_dim + 2);
+}
+
 extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t stream) {
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   UTTT_REQUIRE(a->head_dim == 64 || a->head_dim == 128, "head_dim must be 64 or 128 (got %lld)", (long long)a->head_dim);
-  UTTT_REQUIRE(a->batch >= 1 && a->batch <= 65535 && a->n_heads >= 1 && a->n_heads <= 65535,
-               "batch / n_heads out of range");
+  UTTT_REQUIRE(a->batch >= 1 && a->n_heads >= 1 && a->n_heads <= 65535, "batch / n_heads out of range");
   UTTT_REQUIRE(a->n_kv_heads >= 1 && a->n_heads % a->n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
   UTTT_REQUIRE(a->q_len >= 1 && a->kv_len >= 1 && a->window >= 1, "q_len, kv_len and window must be >= 1");
   UTTT_REQUIRE(a->q_offset >= 0 && a->q_offset + a->q_len <= a->kv_len,
@@ -485,12 +690,24 @@ extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t st
                (long long)a->q_offset, (long long)a->q_len, (long long)a->kv_len);
   UTTT_REQUIRE(a->q && a->k && a->v && a->out, "pointers must be non-NULL");
   UTTT_REQUIRE(a->act_dtype == UTTT_DTYPE_F32 || a->act_dtype == UTTT_DTYPE_BF16, "bad act_dtype");
+  const int64_t vec = a->act_dtype == UTTT_DTYPE_BF16 ? 8 : 4;
+  UTTT_REQUIRE(aligned16(a->q) && aligned16(a->k) && aligned16(a->v), "q/k/v must be 16-byte aligned");
+  UTTT_REQUIRE(a->q_stride_b % vec == 0 && a->q_stride_h % vec == 0 && a->q_stride_t % vec == 0 &&
+               a->k_stride_b % vec == 0 && a->k_stride_h % vec == 0 && a->k_stride_t % vec == 0 &&
+               a->v_stride_b % vec == 0 && a->v_stride_h % vec == 0 && a->v_stride_t % vec == 0,
+               "q/k/v strides must be multiples of 16 bytes");
+  const PrefillPlan p = prefill_plan(a->batch, a->n_heads, a->q_len, a->kv_len, a->window);
+  UTTT_REQUIRE(a->batch * p.nsplit <= 65535, "batch too large for the attention grid");
+  UTTT_REQUIRE(p.nsplit == 1 || (a->workspace != nullptr &&
+                                 a->workspace_bytes >= uttt_swa_prefill_workspace(a->batch, a->n_heads, a->q_len,
+                                                                                  a->kv_len, a->head_dim, a->window)),
+               "attention workspace too small");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool b16 = a->act_dtype == UTTT_DTYPE_BF16;
   if (a->head_dim == 64) {
-    if (b16) launch_prefill<bf16, 64>(*a, st); else launch_prefill<float, 64>(*a, st);
+    if (b16) launch_prefill<bf16, 64>(*a, p, st); else launch_prefill<float, 64>(*a, p, st);
   } else {
-    if (b16) launch_prefill<bf16, 128>(*a, st); else launch_prefill<float, 128>(*a, st);
+    if (b16) launch_prefill<bf16, 128>(*a, p, st); else launch_prefill<float, 128>(*a, p, st);
   }
   return launch_status("uttt_swa_prefill");
 }

@@ -346,7 +346,8 @@ def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, st
 # ---------------------------------------------------------------------------
 
 def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
-                out: Optional[Tensor] = None, kv_len: Optional[int] = None) -> Tensor:
+                out: Optional[Tensor] = None, kv_len: Optional[int] = None,
+                workspace: Optional[Tensor] = None) -> Tensor:
     """q (B, H, Tq, hd), k/v (B, Hkv, Tkv, hd) (any strides with hd contiguous).  Query i sits
     at key index q_offset + i and sees key j iff 0 <= q_offset + i - j < window.  ``out``
     (B, H, Tq, hd) may be a strided view, e.g. of a (B, Tq, H, hd) buffer."""
@@ -362,9 +363,15 @@ def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
         raise ValueError("window must be >= 1")
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q/k/v must share one dtype")
+    vec = 16 // q.element_size()
+    fixed = []
     for t in (q, k, v):
         if t.stride(-1) != 1:
             raise ValueError("the head dimension must be contiguous")
+        if t.data_ptr() % 16 or any(st % vec for st in t.stride()[:3]):
+            t = t.contiguous()  # the kernel reads 16-byte vectors
+        fixed.append(t)
+    q, k, v = fixed
     dev = q.device
     _require_device(dev, k, v)
     _forward_only(q, k, v)
@@ -380,6 +387,10 @@ def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
     a.v, a.v_stride_b, a.v_stride_h, a.v_stride_t = _p(v), v.stride(0), v.stride(1), v.stride(2)
     a.out, a.o_stride_b, a.o_stride_h, a.o_stride_t = _p(out), out.stride(0), out.stride(1), out.stride(2)
     lib = N.load_library()
+    nbytes = lib.uttt_swa_prefill_workspace(bsz, heads, tq, tkv, hd, window)
+    if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = _p(workspace), workspace.numel()
     with torch.cuda.device(dev):
         N.check(lib.uttt_swa_prefill(C.byref(a), _stream(dev)), "uttt_swa_prefill")
     return out
