@@ -503,7 +503,9 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
       acc[r] = s;
     }
     if (sub == 0 && j < j_hi) {
-      for (int r = 0; r < rep; ++r) sc[r * kDecodeKeys + (j - j_lo)] = acc[r] * a.scale;
+#pragma unroll
+      for (int r = 0; r < kMaxRep; ++r)
+        if (r < rep) sc[r * kDecodeKeys + (j - j_lo)] = acc[r] * a.scale;
     }
   }
   __syncthreads();
@@ -558,9 +560,13 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
     }
   }
   if (lane < L) {
-    for (int r = 0; r < rep; ++r)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) wred[wave][r * HD + e0 + i] = o[r][i];
+    for (int r = 0; r < kMaxRep; ++r) {
+      if (r < rep) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wred[wave][r * HD + e0 + i] = o[r][i];
+      }
+    }
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < rep * HD; idx += kThreads) {
