@@ -91,9 +91,10 @@ int uttt_chunk_update_phase(const uttt_chunk_update_args* args, void* workspace,
 typedef struct {
   int64_t batch, tokens, d_model, d_ff; /* tokens: any T >= 1 */
   int32_t act_dtype;
+  int32_t w_dtype;   /* UTTT_DTYPE_F32 masters, or UTTT_DTYPE_BF16 read copies (bf16 activations only) */
   float eps;
   const void* x; int64_t x_row_stride;
-  const float* w_up; const float* w_gate; const float* w_down; int64_t w_row_stride; /* 0 = shared */
+  const void* w_up; const void* w_gate; const void* w_down; int64_t w_row_stride; /* 0 = shared */
   const float* ln_weight; const float* ln_bias;
   void* out; int64_t out_row_stride;
 } uttt_readout_args;

@@ -187,6 +187,25 @@ def test_swiglu_readout_matches_oracle(dtype, shared):
         check_bf16_activation("readout", got, ref, ref16)
 
 
+def test_swiglu_readout_with_bf16_weight_copies():
+    """bf16 read copies of W give the operands the fp32 path rounds to (same readout)."""
+    K = kernels()
+    b, t, d, f = 4, 1, 768, 2048
+    g = torch.Generator().manual_seed(27)
+    x = torch.randn(b, t, d, generator=g).bfloat16()
+    w = (torch.randn(b, d, f, generator=g) * 0.03, torch.randn(b, d, f, generator=g) * 0.03,
+         torch.randn(b, f, d, generator=g) * 0.02)
+    ln_w, ln_b = 1 + 0.1 * torch.randn(d, generator=g), 0.1 * torch.randn(d, generator=g)
+    with torch.no_grad():
+        from_f32 = K.swiglu_readout(*to_dev(x, *w, ln_w, ln_b))
+        from_bf16 = K.swiglu_readout(*to_dev(x, *(t_.bfloat16() for t_ in w), ln_w, ln_b))
+    torch.cuda.synchronize()
+    assert torch.equal(from_f32, from_bf16)
+    ref = om.swiglu_fast_forward(x.float(), *(t_.bfloat16().float() for t_ in w), ln_w, ln_b, 1e-5)
+    ref16 = om.swiglu_fast_forward(x, *w, ln_w, ln_b, 1e-5)
+    check_bf16_activation("readout", from_bf16, ref, ref16)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_rope_append_is_bit_exact(dtype):
     K = kernels()

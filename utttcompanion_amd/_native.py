@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 UPDATE_PHASES = 5
@@ -47,7 +47,7 @@ class ChunkUpdateArgs(C.Structure):
 class ReadoutArgs(C.Structure):
     _fields_ = [
         ("batch", _I64), ("tokens", _I64), ("d_model", _I64), ("d_ff", _I64),
-        ("act_dtype", _I32), ("eps", _F),
+        ("act_dtype", _I32), ("w_dtype", _I32), ("eps", _F),
         ("x", _P), ("x_row_stride", _I64),
         ("w_up", _P), ("w_gate", _P), ("w_down", _P), ("w_row_stride", _I64),
         ("ln_weight", _P), ("ln_bias", _P),

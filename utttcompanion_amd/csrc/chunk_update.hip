@@ -33,9 +33,9 @@ struct FwdArgs {
   int B, D, F, ntok, ntb, tok_pad, nsplit;
   const void* x[2];
   int64_t x_rs[2];
-  const float* wu[2];
-  const float* wg[2];
-  const float* wd[2];
+  const void* wu[2];  // fp32 (update) or the weight type WT of the readout
+  const void* wg[2];
+  const void* wd[2];
   int64_t w_rs[2];
   float* u_store;  // fp32 (B, tok_pad, F), path 0 only; may be null
   float* g_store;
@@ -46,7 +46,7 @@ struct FwdArgs {
 // ---------------------------------------------------------------------------
 // 1. U, G, H for one (F tile, row, path, token block)
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, typename WT>
 __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T xs[64 * LD];
@@ -57,15 +57,16 @@ __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
   const int f0 = ft * 64, t0 = tb * 64;
   const int rows = min(64, a.ntok - t0);
   const T* x = static_cast<const T*>(a.x[path]) + (int64_t)b * a.x_rs[path] + (int64_t)t0 * a.D;
-  // threads [0, 128) stage W_up, [128, 256) W_gate (128 units of 8 rows x 4 floats)
-  const bool up_half = threadIdx.x < 128;
-  const float* wsrc = (up_half ? a.wu[path] : a.wg[path]) + (int64_t)b * a.w_rs[path] + f0;
+  // threads [0, U) stage W_up, [U, 2U) W_gate (U units of 8 rows x one 16-byte chunk)
+  constexpr int U = ColStage<WT, KT>::kUnits;
+  const bool up_half = threadIdx.x < U;
+  const WT* wsrc = static_cast<const WT*>(up_half ? a.wu[path] : a.wg[path]) + (int64_t)b * a.w_rs[path] + f0;
   T* wdst = up_half ? us : gs;
-  const int unit = threadIdx.x & 127;
+  const int unit = up_half ? (int)threadIdx.x : min((int)threadIdx.x - U, U);
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
 
   RowStage<T, KT> xst;
-  ColStage<float, KT> wst;
+  ColStage<WT, KT> wst;
   xst.load(x, a.D, rows);
   wst.load(wsrc, a.F, KT, unit);
   f32x16 au, ag;
@@ -104,7 +105,7 @@ __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
 // ---------------------------------------------------------------------------
 // 2. Z partial = H[:, split] W_down[split, D tile]
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, typename WT>
 __global__ void __launch_bounds__(kThreads) k_down_partial(const FwdArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T hs[64 * LD];
@@ -116,11 +117,11 @@ __global__ void __launch_bounds__(kThreads) k_down_partial(const FwdArgs a) {
   const int nF = a.F / 64;
   const int f_begin = (nF * split / a.nsplit) * 64, f_end = (nF * (split + 1) / a.nsplit) * 64;
   const T* h = static_cast<const T*>(a.h[path]) + ((int64_t)b * a.tok_pad + t0) * a.F;
-  const float* wd = a.wd[path] + (int64_t)b * a.w_rs[path] + d0;
+  const WT* wd = static_cast<const WT*>(a.wd[path]) + (int64_t)b * a.w_rs[path] + d0;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
 
   RowStage<T, KT> hst;
-  ColStage<float, KT> wst;  // W_down rows f, columns d -> [d][f]
+  ColStage<WT, KT> wst;  // W_down rows f, columns d -> [d][f]
   f32x16 acc;
   zero(acc);
   if (f_begin < f_end) {
@@ -613,8 +614,8 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   const dim3 blk(kThreads);
   auto want = [&](int phase) { return first_phase <= phase && phase <= last_phase; };
 
-  if (want(0)) hipLaunchKernelGGL(k_up_gate<T>, dim3(F / 64, B, 2), blk, 0, st, f);
-  if (want(1)) hipLaunchKernelGGL(k_down_partial<T>, dim3(D / 64, L.nsplit, 2 * B), blk, 0, st, f);
+  if (want(0)) hipLaunchKernelGGL((k_up_gate<T, float>), dim3(F / 64, B, 2), blk, 0, st, f);
+  if (want(1)) hipLaunchKernelGGL((k_down_partial<T, float>), dim3(D / 64, L.nsplit, 2 * B), blk, 0, st, f);
 
   LnGradArgs g{};
   g.B = B; g.C = C; g.D = D; g.nsplit = L.nsplit; g.tok_pad = 64; g.normalize = a.normalize_by_dim;
@@ -670,7 +671,7 @@ static ReadoutLayout readout_layout(int64_t B, int64_t T, int64_t D, int64_t F, 
   return L;
 }
 
-template <typename T>
+template <typename T, typename WT>
 static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLayout& L, hipStream_t st) {
   const int B = (int)a.batch, D = (int)a.d_model, F = (int)a.d_ff;
   FwdArgs f{};
@@ -681,8 +682,8 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   f.h[0] = ws + L.h;
   f.zp = reinterpret_cast<float*>(ws + L.zp);
   const dim3 blk(kThreads);
-  hipLaunchKernelGGL(k_up_gate<T>, dim3(F / 64, B, L.ntb), blk, 0, st, f);
-  hipLaunchKernelGGL(k_down_partial<T>, dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
+  hipLaunchKernelGGL((k_up_gate<T, WT>), dim3(F / 64, B, L.ntb), blk, 0, st, f);
+  hipLaunchKernelGGL((k_down_partial<T, WT>), dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
   LnOutArgs o{};
   o.B = B; o.ntok = (int)a.tokens; o.D = D; o.nsplit = L.nsplit; o.tok_pad = f.tok_pad; o.eps = a.eps;
   o.zp = f.zp; o.x = a.x; o.x_rs = a.x_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
@@ -783,10 +784,17 @@ extern "C" int uttt_swiglu_readout(const uttt_readout_args* a, void* workspace, 
   UTTT_REQUIRE((int64_t)L.ntb * a->batch <= 65535, "batch * ceil(tokens / 64) must be <= 65535");
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,
                "workspace too small: need %zu bytes, got %zu", L.total, workspace_bytes);
+  UTTT_REQUIRE(a->w_dtype == UTTT_DTYPE_F32 || (a->w_dtype == UTTT_DTYPE_BF16 && a->act_dtype == UTTT_DTYPE_BF16),
+               "w_dtype must be F32, or BF16 with BF16 activations");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (a->act_dtype == UTTT_DTYPE_BF16)
-    launch_readout<bf16>(*a, static_cast<char*>(workspace), L, st);
-  else
-    launch_readout<float>(*a, static_cast<char*>(workspace), L, st);
+  char* ws = static_cast<char*>(workspace);
+  if (a->act_dtype == UTTT_DTYPE_BF16) {
+    if (a->w_dtype == UTTT_DTYPE_BF16)
+      launch_readout<bf16, bf16>(*a, ws, L, st);
+    else
+      launch_readout<bf16, float>(*a, ws, L, st);
+  } else {
+    launch_readout<float, float>(*a, ws, L, st);
+  }
   return launch_status("uttt_swiglu_readout");
 }

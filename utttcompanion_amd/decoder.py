@@ -1,0 +1,195 @@
+"""Batched frozen-state decoding over ring-buffer SWA caches.
+
+The reference decodes one request at a time, either eagerly (``uTTTModel.stream_generate``,
+``model/uttt_model.py:966-1179``) or through ``CUDAGraphDecoder`` (``engine/inference.py:71-302``),
+whose captured step writes the new key/value into ring slot ``pos mod window``, masks the slots
+that are not yet valid and reads each layer's fast weights through activation-dtype copies.
+
+``BatchedDecoder`` runs N independent requests in one step: every request keeps its own fp32
+fast-weight master state (read through per-request activation-dtype copies), its own position
+and its own ring slots.  One step is, per layer: RMSNorm -> packed QKV GEMM -> ``uttt_swa_decode``
+(RoPE at each request's position, ring write, window attention) -> output GEMM -> RMSNorm ->
+query projection -> per-request fast-weight readout (``uttt_swiglu_readout`` over the stacked
+copies) -> output GEMM; then the final norm, the LM head and greedy selection, all on the
+device, so ``capture()`` can record the whole step into one HIP graph.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels as K
+from .layer import FastWeightState
+from .model import BOS_ID, PAD_ID, UNK_ID, uTTTModel
+
+Tensor = torch.Tensor
+
+
+class BatchedDecoder:
+    """N requests, one token each per step, frozen fast weights (decode never writes them)."""
+
+    def __init__(self, model: uTTTModel, states: Sequence[FastWeightState], max_positions: int = 8192):
+        if model.training:
+            raise ValueError("call model.eval() before decoding")
+        if not states:
+            raise ValueError("need at least one request state")
+        self.model = model
+        self.n = len(states)
+        dev = model.tok_embeddings.weight.device
+        if dev.type != "cuda":
+            raise ValueError("BatchedDecoder needs the model on the GPU")
+        self.device = dev
+        self.dtype = model.tok_embeddings.weight.dtype
+        for st in states:
+            if st.w_up.shape[0] != 1:
+                raise ValueError("each request state must hold one row (batch 1)")
+        ln_w, ln_b = states[0].ln_weight, states[0].ln_bias
+        for st in states[1:]:
+            if not (torch.equal(st.ln_weight, ln_w) and torch.equal(st.ln_bias, ln_b)):
+                raise ValueError("batched decoding needs one shared LayerNorm pair for all requests")
+        self.ln_weight = ln_w.detach().float().contiguous()
+        self.ln_bias = ln_b.detach().float().contiguous()
+        # per-request read copies in the activation dtype (reference inference_read_weights,
+        # model/uttt_layer.py:648-668): same operands the reference's bf16 matmuls see
+        with torch.no_grad():
+            self.w_up = torch.cat([st.w_up.detach() for st in states]).to(self.dtype).contiguous()
+            self.w_gate = torch.cat([st.w_gate.detach() for st in states]).to(self.dtype).contiguous()
+            self.w_down = torch.cat([st.w_down.detach() for st in states]).to(self.dtype).contiguous()
+        attn = model.layers[0].attn
+        self.window, self.hkv, self.hd, self.heads = attn.window_size, attn.n_kv_heads, attn.head_dim, attn.n_heads
+        self.rings = [(torch.zeros((self.n, self.hkv, self.window, self.hd), dtype=self.dtype, device=dev),
+                       torch.zeros((self.n, self.hkv, self.window, self.hd), dtype=self.dtype, device=dev))
+                      for _ in model.layers]
+        self.cos, self.sin = attn.rope.tables(max_positions, dev)
+        self.positions = torch.zeros(self.n, dtype=torch.int64, device=dev)
+        self.host_positions = [0] * self.n
+        self.tokens = torch.zeros(self.n, dtype=torch.int64, device=dev)
+        self.logits: Optional[Tensor] = None
+        self.next_tokens: Optional[Tensor] = None
+        self._graph = None
+        self._ws_attn = torch.zeros(1, dtype=torch.uint8, device=dev)
+        self._ws_read = torch.zeros(1, dtype=torch.uint8, device=dev)
+        self._states = list(states)
+
+    # ------------------------------------------------------------------ prefill
+    @torch.no_grad()
+    def prefill(self, prompts: Sequence[Tensor]) -> Tensor:
+        """Frozen prefill of each request's prompt (its own state), then load the last
+        ``window`` keys/values into the ring slots.  Returns the next-token logits (N, V)."""
+        if len(prompts) != self.n:
+            raise ValueError(f"expected {self.n} prompts, got {len(prompts)}")
+        out_logits = []
+        for i, (ids, st) in enumerate(zip(prompts, self._states)):
+            ids = ids.to(self.device).view(1, -1)
+            if ids.shape[1] == 0:
+                raise ValueError("prompts must be non-empty")
+            out = self.model(ids, fast_state=st, update_fast_weights=False, logits_to_keep=1)
+            length = ids.shape[1]
+            for (kr, vr), (k, v) in zip(self.rings, out.kv_caches):
+                cached = k.shape[2]
+                slots = torch.arange(length - cached, length, device=self.device) % self.window
+                kr[i].index_copy_(1, slots, k[0])
+                vr[i].index_copy_(1, slots, v[0])
+            self.host_positions[i] = length
+            out_logits.append(out.logits[:, -1, :])
+        self.positions.copy_(torch.tensor(self.host_positions, dtype=torch.int64))
+        return torch.cat(out_logits, dim=0)
+
+    # ------------------------------------------------------------------ one step
+    def _step_body(self) -> None:
+        m = self.model
+        n = self.n
+        h = F.embedding(self.tokens, m.tok_embeddings.weight)  # (N, D)
+        for li, block in enumerate(m.layers):
+            attn = block.attn
+            x = block.attn_norm(h)
+            qkv = F.linear(x, attn.packed_qkv().to(x.dtype))  # (N, (H + 2 Hkv) hd)
+            hq = self.heads * self.hd
+            hk = self.hkv * self.hd
+            q = qkv[:, :hq].view(n, self.heads, self.hd)
+            k = qkv[:, hq:hq + hk].view(n, self.hkv, self.hd)
+            v = qkv[:, hq + hk:].view(n, self.hkv, self.hd)
+            kr, vr = self.rings[li]
+            att = K.swa_decode(q, k, v, kr, vr, self.positions, self.cos, self.sin, workspace=self._ws_attn)
+            h = h + attn.wo(att.reshape(n, -1))
+            x2 = block.uttt_norm(h)
+            uq = F.rms_norm(F.linear(x2, block.uttt.w_q.weight), (x2.shape[-1],),
+                            block.uttt.q_norm.weight.to(x2.dtype), block.uttt.q_norm.eps)
+            r = K.swiglu_readout(uq.view(n, 1, -1), self.w_up, self.w_gate, self.w_down, self.ln_weight,
+                                 self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read)
+            h = h + block.uttt.w_o(r.view(n, -1))
+        logits = F.linear(m.norm(h), m.lm_head.weight)
+        self.positions.add_(1)
+        work = logits.float()
+        work[:, PAD_ID] = float("-inf")
+        work[:, BOS_ID] = float("-inf")
+        work[:, UNK_ID] = float("-inf")
+        if m.active_vocab_limit < work.shape[-1]:
+            work[:, m.active_vocab_limit:] = float("-inf")
+        self.logits = logits
+        self.next_tokens = work.argmax(dim=-1)
+
+    def _warm_workspaces(self) -> None:
+        lib_ws_attn = 1 << 20
+        nbytes = max(lib_ws_attn, self.n * self.heads * ((self.window + 63) // 64) * (self.hd + 2) * 4)
+        self._ws_attn = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        d = self.model.config.d_model
+        ff = self.model.config.d_ff_fast
+        from . import _native as N
+        code = N.DTYPE_BF16 if self.dtype == torch.bfloat16 else N.DTYPE_F32
+        self._ws_read = torch.zeros(max(N.load_library().uttt_readout_workspace(self.n, 1, d, ff, code), 1),
+                                    dtype=torch.uint8, device=self.device)
+
+    @torch.no_grad()
+    def capture(self) -> None:
+        """Record one step into a HIP graph (after ``prefill``); ``step`` then replays it."""
+        self._warm_workspaces()
+        saved = (self.positions.clone(), [(k.clone(), v.clone()) for k, v in self.rings])
+        self._step_body()  # warm-up outside the graph (packs, tables, allocator)
+        torch.cuda.synchronize()
+        self.positions.copy_(saved[0])
+        for (k, v), (k0, v0) in zip(self.rings, saved[1]):
+            k.copy_(k0)
+            v.copy_(v0)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._step_body()
+        torch.cuda.synchronize()
+        # capture ran no kernels; positions and rings are as before
+        self._graph = graph
+
+    @torch.no_grad()
+    def step(self, tokens: Tensor) -> Tensor:
+        """Append one token per request; returns the logits (N, V) for the next position."""
+        if tokens.shape != (self.n,):
+            raise ValueError(f"tokens must be ({self.n},)")
+        limit = self.cos.shape[0]
+        if max(self.host_positions) >= limit:
+            raise ValueError("a request reached the end of the RoPE table")
+        self.tokens.copy_(tokens)
+        if self._graph is not None:
+            self._graph.replay()
+        else:
+            if self._ws_attn.numel() == 1:
+                self._warm_workspaces()
+            self._step_body()
+        self.host_positions = [p + 1 for p in self.host_positions]
+        return self.logits
+
+    @torch.no_grad()
+    def generate_greedy(self, first_logits: Tensor, steps: int) -> Tensor:
+        """Greedy tokens (N, steps) continuing from ``first_logits`` (no EOS stop)."""
+        m = self.model
+        work = first_logits.float().clone()
+        work[:, [PAD_ID, BOS_ID, UNK_ID]] = float("-inf")
+        if m.active_vocab_limit < work.shape[-1]:
+            work[:, m.active_vocab_limit:] = float("-inf")
+        tok = work.argmax(dim=-1)
+        out = [tok]
+        for _ in range(steps - 1):
+            self.step(tok)
+            tok = self.next_tokens.clone()
+            out.append(tok)
+        return torch.stack(out, dim=1)

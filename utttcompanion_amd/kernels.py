@@ -81,11 +81,12 @@ def _state(t: Tensor, name: str) -> Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
-def _read_weight(t: Tensor, bsz: int, name: str) -> Tuple[Tensor, int]:
-    """A read-only weight of shape (B|1, r, c): returns (tensor, row stride in elements)."""
+def _read_weight(t: Tensor, bsz: int, name: str, keep_bf16: bool = False) -> Tuple[Tensor, int]:
+    """A read-only weight of shape (B|1, r, c): returns (tensor, row stride in elements).
+    fp32 is the default; ``keep_bf16`` passes bf16 read copies through unchanged."""
     if t.dtype == torch.float64:
         raise ValueError(f"{name}: float64 weights are not supported by the HIP path")
-    if t.dtype != torch.float32:
+    if t.dtype != torch.float32 and not (keep_bf16 and t.dtype == torch.bfloat16):
         t = t.float()
     shared = t.shape[0] == 1 or t.stride(0) == 0
     if shared:
@@ -255,8 +256,13 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
 # ---------------------------------------------------------------------------
 
 def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_weight: Tensor,
-                   ln_bias: Tensor, eps: float = 1e-5, out: Optional[Tensor] = None) -> Tensor:
-    """f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down) with per-row (or shared) fp32 W."""
+                   ln_bias: Tensor, eps: float = 1e-5, out: Optional[Tensor] = None,
+                   workspace: Optional[Tensor] = None) -> Tensor:
+    """f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down) with per-row (or shared) W.
+
+    W is read as fp32 masters, or -- when x and all three weights are bf16 -- as bf16 read
+    copies (the reference casts W to the activation dtype for these matmuls, so a bf16
+    copy yields the same operands at half the bytes)."""
     if x.dim() != 3:
         raise ValueError(f"x must be (B, T, D), got {tuple(x.shape)}")
     bsz, tokens, dim = x.shape
@@ -270,7 +276,9 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
     _require_device(dev, w_up, w_gate, w_down, ln_weight, ln_bias)
     _forward_only(x, w_up, w_gate, w_down, ln_weight, ln_bias)
     x = _rows(x)
-    parts = [_read_weight(t, bsz, n) for t, n in ((w_up, "w_up"), (w_gate, "w_gate"), (w_down, "w_down"))]
+    bf16_copies = x.dtype == torch.bfloat16 and all(t.dtype == torch.bfloat16 for t in (w_up, w_gate, w_down))
+    parts = [_read_weight(t, bsz, n, bf16_copies) for t, n in ((w_up, "w_up"), (w_gate, "w_gate"),
+                                                               (w_down, "w_down"))]
     if len({p[1] for p in parts}) != 1:
         raise ValueError("fast weights must all be shared (batch 1) or all per-row")
     ln_w = ln_weight.to(torch.float32).contiguous()
@@ -279,9 +287,11 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
         out = torch.empty((bsz, tokens, dim), dtype=x.dtype, device=dev)
     lib = N.load_library()
     nbytes = lib.uttt_readout_workspace(bsz, tokens, dim, ff, code)
-    workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     a = N.ReadoutArgs()
     a.batch, a.tokens, a.d_model, a.d_ff, a.act_dtype, a.eps = bsz, tokens, dim, ff, code, float(eps)
+    a.w_dtype = N.DTYPE_BF16 if bf16_copies else N.DTYPE_F32
     a.x, a.x_row_stride = _p(x), x.stride(0)
     a.w_up, a.w_gate, a.w_down = (_p(p[0]) for p in parts)
     a.w_row_stride = parts[0][1]
