@@ -50,7 +50,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--sections", default="prefill,update,decode,cpu",
                     help="comma list of prefill, update, decode, cpu (profiling runs pick a subset)")
-    ap.add_argument("--cpu-tokens", type=int, default=256, help="tokens of the CPU baseline sample (1 row)")
+    ap.add_argument("--cpu-tokens", type=int, default=2048, help="tokens per row of the CPU baseline sample")
+    ap.add_argument("--cpu-rows", type=int, default=4, help="rows of the CPU baseline sample")
+    ap.add_argument("--decode-steps", type=int, default=256)
     return ap.parse_args()
 
 
@@ -181,8 +183,55 @@ def bench_decode(iters: int):
     return ms, kv_bytes, dict(requests=N_REQ, heads=H, kv_heads=HKV, head_dim=HD, window=W)
 
 
-def cpu_baseline(model, tokens: int):
-    """The CPU oracle (PyTorch-CPU fp32 restatement) on 1 row x ``tokens`` of config 2 with writes."""
+def bench_decode_step(model, steps: int):
+    """Config 4: 32 requests on the config-2 model, each with its own fp32 fast weights
+    (W_up/W_gate/W_down ~ N(0, 0.02) drawn from a generator seeded with the request id,
+    S = 0), ragged prompts with lengths uniform in [64, 2048], frozen prefill into ring
+    caches (window 512, bf16 K/V), then ``steps`` greedy steps of one token per request
+    replayed from one HIP graph (no EOS stop).  Returns (decode tok/s, ms per step, info)."""
+    import torch
+    from utttcompanion_amd.decoder import BatchedDecoder
+    from utttcompanion_amd.layer import FastWeightState
+    N_REQ = 32
+    D, F = C2["d_model"], C2["d_ff_fast"]
+    ln_w = model.fast_weight_pool.ln_weight.detach().float()
+    ln_b = model.fast_weight_pool.ln_bias.detach().float()
+    states = []
+    for rid in range(N_REQ):
+        g = torch.Generator().manual_seed(rid)
+        w = [torch.randn(1, D, F, generator=g) * 0.02, torch.randn(1, D, F, generator=g) * 0.02,
+             torch.randn(1, F, D, generator=g) * 0.02]
+        w = [t.to("cuda") for t in w]
+        states.append(FastWeightState(*w, *(torch.zeros_like(t) for t in w), ln_w, ln_b))
+    g = torch.Generator().manual_seed(5)
+    lengths = torch.randint(64, 2049, (N_REQ,), generator=g).tolist()
+    prompts = [torch.randint(0, C2["vocab_size"], (n,), generator=g) for n in lengths]
+    with torch.no_grad():
+        dec = BatchedDecoder(model, states)
+        log("decode: frozen prefill of 32 ragged prompts")
+        first = dec.prefill(prompts)
+        dec.capture()
+        tok = first.float().argmax(-1)
+        for _ in range(3):
+            dec.step(tok)
+            tok = dec.next_tokens.clone()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            dec.step(tok)
+            tok = dec.next_tokens
+        end.record()
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    readout_bytes = 3 * D * F * 2 * N_REQ * C2["n_layers"]  # bf16 read copies, once per step
+    return N_REQ / (ms * 1e-3), ms, {"requests": N_REQ, "steps": steps, "prompt_lengths": [min(lengths), max(lengths)],
+                                      "readout_bytes_per_step": readout_bytes,
+                                      "readout_hbm_gbs": round(readout_bytes / (ms * 1e-3) / 1e9, 1)}
+
+
+def cpu_baseline(model, tokens: int, rows: int):
+    """The CPU oracle (PyTorch-CPU fp32 restatement) on ``rows`` x ``tokens`` of config 2 with writes."""
     import torch
     from oracle import uttt_math as om
     threads = min(16, os.cpu_count() or 1)
@@ -193,14 +242,14 @@ def cpu_baseline(model, tokens: int):
                            base_inner_lr=model.config.base_inner_lr,
                            base_weight_decay=model.config.base_weight_decay)
     oracle = om.OracleModel(ocfg, weights)
-    ids = torch.randint(0, C2["vocab_size"], (1, tokens), generator=torch.Generator().manual_seed(4))
+    ids = torch.randint(0, C2["vocab_size"], (rows, tokens), generator=torch.Generator().manual_seed(4))
     t0 = time.perf_counter()
     oracle.forward(ids, None, None, update_fast_weights=True, logits_to_keep=-1)
     dt = time.perf_counter() - t0
-    return {"value": round(tokens / dt, 2), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"oracle.OracleModel fp32 on the host CPU: 1 row x {tokens} tokens "
-                      f"({tokens // C2['chunk_size']} chunks) x 12 layers of config 2 with writes; "
-                      f"{dt:.1f} s; tok/s scales linearly in rows and chunks"}
+    return {"value": round(rows * tokens / dt, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle.OracleModel fp32 on the host CPU: {rows} rows x {tokens} tokens "
+                      f"({tokens // C2['chunk_size']} chunks) x 12 layers of config 2 with writes "
+                      f"(half the config-2 batch); {dt:.1f} s"}
 
 
 def main() -> int:
@@ -249,14 +298,17 @@ def main() -> int:
     dec_ms, dec_bytes, dec_shape = bench_decode(20) if "decode" in sections else (float("nan"), 1, {})
     dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
     decode = {"kernel": "k_swa_decode", "us_per_layer_step": round(dec_ms * 1e3, 2), "achieved_gbs": round(dec_gbs, 1),
-              "hbm_frac": round(dec_gbs / PEAK_HBM_GBS, 4), "shape": dec_shape,
-              "attention_only_tok_s_12_layers": round(dec_shape["requests"] / (12 * dec_ms * 1e-3), 1)}
+              "hbm_frac": round(dec_gbs / PEAK_HBM_GBS, 4), "shape": dec_shape}
     log(f"decode kernel {dec_ms * 1e3:.1f} us -> {dec_gbs:.0f} GB/s")
+    if "decode" in sections:
+        tps, step_ms, info = bench_decode_step(model, args.decode_steps)
+        decode.update(decode_tok_s=round(tps, 1), ms_per_decode_step=round(step_ms, 4), workload=info)
+        log(f"decode step {step_ms:.3f} ms -> {tps:.0f} tok/s")
 
     cpu = None
     if not args.no_cpu_baseline and "cpu" in sections:
         log("timing the CPU oracle baseline")
-        cpu = cpu_baseline(model, args.cpu_tokens)
+        cpu = cpu_baseline(model, args.cpu_tokens, args.cpu_rows)
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
 
     line = {"metric": METRIC, "value": round(tokens / ms * 1e3, 1), "unit": "tok/s", "n_gpus": 1,

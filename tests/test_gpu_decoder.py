@@ -14,14 +14,16 @@ CFG = dict(vocab_size=256, d_model=128, n_layers=3, n_heads=2, n_kv_heads=1, d_f
            sliding_window_size=24, max_seq_len=512)
 
 
-def make(dtype=torch.float32, seed=0):
+def make(dtype=torch.float32, seed=0, slow_std=0.08):
+    """``slow_std`` 0.08 (larger than the reference's 0.02 init) makes greedy tokens vary in
+    the token-equality test; the bf16 logits test uses the reference init."""
     from utttcompanion_amd import uTTTConfig, uTTTModel
     torch.manual_seed(seed)
     model = uTTTModel(uTTTConfig(**CFG)).eval()
-    with torch.no_grad():  # larger slow weights than the 0.02 init, so greedy tokens vary
+    with torch.no_grad():
         for name, p in model.named_parameters():
             if p.dim() == 2 and "fast_weight_pool" not in name and "w_eta" not in name and "w_alpha" not in name:
-                p.normal_(0, 0.08)
+                p.normal_(0, slow_std)
     model = model.to(DEV)
     if dtype != torch.float32:
         model.to(dtype)
@@ -75,7 +77,7 @@ def test_decoder_logits_match_eager_frozen_forward_bf16():
     reference tests/test_inference_cuda_graph.py:54-90): the batched GEMMs and the ring
     change bf16 reduction orders, so the two need not be bitwise equal."""
     from utttcompanion_amd.decoder import BatchedDecoder
-    model, states, prompts = make(torch.bfloat16, seed=3)
+    model, states, prompts = make(torch.bfloat16, seed=3, slow_std=0.02)
     dec = BatchedDecoder(model, states)
     first = dec.prefill(prompts)
     tok = first.float().argmax(-1)
