@@ -66,7 +66,12 @@ typedef struct {
   float* w_up_out; float* w_gate_out; float* w_down_out;
   float* s_up_out; float* s_gate_out; float* s_down_out;
   void* out; int64_t out_row_stride; /* (B, C, D) act_dtype */
-  float* surprise;                   /* device scalar (fp32) */
+  float* surprise;                   /* device scalar (fp32): batch-global mean token loss (L:369-380) */
+  float* row_loss;                   /* optional (B, 2) fp32: per row [sum of masked token losses,
+                                        valid tokens], for per-request surprise; NULL to skip */
+  float min_row_surprise;            /* > 0: a row whose masked mean token loss in this chunk is
+                                        below it keeps W and S (per-chunk surprise gate; not in the
+                                        reference, whose gate is per turn, P:524-551); 0 = off */
 } uttt_chunk_update_args;
 
 size_t uttt_chunk_update_workspace(int64_t batch, int64_t d_model, int64_t d_ff, int32_t act_dtype);

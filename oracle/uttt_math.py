@@ -129,12 +129,17 @@ def fused_chunk_ttt_step(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
                          momentum_beta: float, max_inner_grad_norm: float, normalize_by_dim: bool,
                          eps: float, read_w_up: Optional[Tensor] = None,
                          read_w_gate: Optional[Tensor] = None,
-                         read_w_down: Optional[Tensor] = None) -> Tuple[Tensor, ...]:
+                         read_w_down: Optional[Tensor] = None,
+                         min_row_surprise: float = 0.0) -> Tuple[Tensor, ...]:
     """One chunk: gradient -> per-row Frobenius clip -> momentum -> decay -> masked
     select -> readout through the read weights.  Follows L:414-534.
 
     Returns (readout, W_up', W_gate', W_down', S_up', S_gate', S_down', surprise)
     with W/S in the master dtype (fp32, or fp64 for fp64 state).
+
+    ``min_row_surprise`` > 0 is the per-chunk surprise gate of BASELINE config 5, which
+    the reference does not have (its gate is per turn, P:524-551): a row whose masked mean
+    token loss in this chunk is below the threshold keeps W and S, like an all-padding row.
     """
     bsz = q.shape[0]
     g_up, g_gate, g_down, surprise = analytical_swiglu_chunk_grad(
@@ -161,8 +166,14 @@ def fused_chunk_ttt_step(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
     decay = 1.0 - alpha_bar
     new_w = tuple(decay * w.to(mdt) + s for w, s in zip((w_up, w_gate, w_down), new_s))
 
+    active = None
     if token_mask is not None:
         active = token_mask.any(dim=1).view(bsz, 1, 1)
+    if min_row_surprise and min_row_surprise > 0.0:
+        row_mean = row_surprise(k, v, w_up, w_gate, w_down, ln_weight, ln_bias, token_mask, normalize_by_dim, eps)
+        keep = (row_mean >= min_row_surprise).view(bsz, 1, 1)
+        active = keep if active is None else (active & keep)
+    if active is not None:
         new_w = tuple(torch.where(active, n, o) for n, o in zip(new_w, (w_up, w_gate, w_down)))
         new_s = tuple(torch.where(active, n, o) for n, o in zip(new_s, (s_up, s_gate, s_down)))
 
@@ -173,6 +184,21 @@ def fused_chunk_ttt_step(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
         w_down if read_w_down is None else read_w_down,
         ln_weight, ln_bias, eps)
     return (out,) + new_w + new_s + (surprise,)
+
+
+def row_surprise(k: Tensor, v: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_weight: Tensor,
+                 ln_bias: Tensor, token_mask: Optional[Tensor], normalize_by_dim: bool, eps: float) -> Tensor:
+    """Per-row masked mean token loss of a chunk (the batch-global surprise of L:369-380
+    restricted to one row): sum_t l_t m_t / max(1, sum_t m_t), or the row mean unmasked."""
+    act = k.dtype
+    cdt = _math_dtype(act)
+    dim = k.shape[-1]
+    pred = swiglu_fast_forward(k, w_up, w_gate, w_down, ln_weight, ln_bias, eps).to(cdt)
+    loss = 0.5 * (pred - v.to(cdt)).square().sum(-1) * ((1.0 / dim) if normalize_by_dim else 1.0)
+    if token_mask is None:
+        return loss.mean(dim=1)
+    m = token_mask.to(cdt)
+    return (loss * m).sum(dim=1) / m.sum(dim=1).clamp_min(1.0)
 
 
 def apply_elastic_pull(w: Sequence[Tensor], w0: Sequence[Tensor], anchor_lambda: float,
@@ -352,6 +378,8 @@ class OracleConfig:
     momentum_beta: float = 0.9
     max_inner_grad_norm: float = 1.0
     normalize_loss_by_dim: bool = True
+    # not a reference option: the per-chunk surprise gate of BASELINE config 5 (0 = off)
+    min_chunk_surprise: float = 0.0
 
     @property
     def head_dim(self) -> int:
@@ -430,7 +458,7 @@ def uttt_layer_forward(x: Tensor, lw: Dict[str, Tensor], cfg: OracleConfig, stat
             cur.ln_weight, cur.ln_bias,
             None if attention_mask is None else attention_mask[:, sl],
             cfg.momentum_beta, float(cfg.max_inner_grad_norm or 0.0), cfg.normalize_loss_by_dim,
-            cfg.rms_norm_eps, r.w_up, r.w_gate, r.w_down)
+            cfg.rms_norm_eps, r.w_up, r.w_gate, r.w_down, cfg.min_chunk_surprise)
         outs.append(res[0])
         losses.append(res[7])
         cur = OracleState(*res[1:7], cur.ln_weight, cur.ln_bias, cur.step + 1,

@@ -313,3 +313,49 @@ def test_elastic_pull_closed_forms():
         assert drift <= ratio * base * (1 + 1e-5)
     d = om.compute_drift(capped, w0)
     assert abs(d["base_frobenius"] - base) < 1e-4
+
+
+def test_row_surprise_is_each_rows_batch1_surprise():
+    """Per-row chunk surprise = the batch-global surprise (L:369-380) of that row alone,
+    and = the masked mean of 0.5 |f_W(k) - v|^2 / d written as a per-token loop."""
+    b, c, d, f = 3, 6, 8, 12
+    k, v = torch.randn(b, c, d, dtype=torch.float64), torch.randn(b, c, d, dtype=torch.float64)
+    ws = _weights(b, d, f)
+    ln_w, ln_b = torch.randn(d, dtype=torch.float64), torch.randn(d, dtype=torch.float64)
+    mask = torch.tensor([[1, 1, 1, 1, 1, 1], [1, 0, 1, 0, 0, 0], [0, 0, 0, 0, 0, 0]], dtype=torch.float64)
+    eta = torch.full((b, c, 1), 0.01, dtype=torch.float64)
+    rows = om.row_surprise(k, v, *ws, ln_w, ln_b, mask, True, 1e-5)
+    for r in range(b):
+        one = om.analytical_swiglu_chunk_grad(k[r:r + 1], v[r:r + 1], eta[r:r + 1], *(w[r:r + 1] for w in ws),
+                                              ln_w, ln_b, mask[r:r + 1], True, 1e-5)[3]
+        assert abs(float(rows[r]) - float(one)) < 1e-12
+        pred = om.swiglu_fast_forward(k[r:r + 1], *(w[r:r + 1] for w in ws), ln_w, ln_b, 1e-5)[0]
+        num = sum(0.5 * float((pred[t] - v[r, t]).square().sum()) / d * float(mask[r, t]) for t in range(c))
+        assert abs(float(rows[r]) - num / max(1.0, float(mask[r].sum()))) < 1e-12
+    assert float(rows[2]) == 0.0
+
+
+def test_chunk_gate_keeps_rows_whose_surprise_is_below_threshold():
+    """Rows under the per-chunk gate keep W and S bit for bit; rows over it take the
+    ungated step; a zero threshold is the ungated step."""
+    d, f = 16, 24
+    ws = _weights(3, d, f, dtype=torch.float32, scale=0.2)
+    ms = tuple(torch.randn_like(w) * 1e-3 for w in ws)
+    q, k = torch.randn(3, 5, d), torch.randn(3, 5, d)
+    v = torch.randn(3, 5, d) * torch.tensor([0.1, 1.0, 10.0]).view(3, 1, 1)  # row losses far apart
+    eta, alpha = torch.rand(3, 5, 1) * 0.01, torch.rand(3, 5, 1) * 0.01
+    ln = (torch.ones(d), torch.zeros(d))
+    rows = om.row_surprise(k, v, *ws, *ln, None, True, 1e-5)
+    assert rows[0] < rows[1] < rows[2]
+    plain = om.fused_chunk_ttt_step(q, k, v, eta, alpha, *ws, *ms, *ln, None, 0.9, 1.0, True, 1e-5)
+    zero = om.fused_chunk_ttt_step(q, k, v, eta, alpha, *ws, *ms, *ln, None, 0.9, 1.0, True, 1e-5,
+                                   min_row_surprise=0.0)
+    for x, y in zip(plain, zero):
+        assert torch.equal(x, y)
+    thr = float(rows[1] + rows[2]) / 2
+    gated = om.fused_chunk_ttt_step(q, k, v, eta, alpha, *ws, *ms, *ln, None, 0.9, 1.0, True, 1e-5,
+                                    min_row_surprise=thr)
+    for x, p, o in zip(gated[1:7], plain[1:7], ws + ms):
+        assert torch.equal(x[0], o[0]) and torch.equal(x[1], o[1])
+        assert torch.equal(x[2], p[2])
+    torch.testing.assert_close(gated[0], plain[0])  # the readout is the same either way

@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 4
+ABI_VERSION = 6
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 UPDATE_PHASES = 5
@@ -40,7 +40,7 @@ class ChunkUpdateArgs(C.Structure):
         ("w_up_out", _P), ("w_gate_out", _P), ("w_down_out", _P),
         ("s_up_out", _P), ("s_gate_out", _P), ("s_down_out", _P),
         ("out", _P), ("out_row_stride", _I64),
-        ("surprise", _P),
+        ("surprise", _P), ("row_loss", _P), ("min_row_surprise", _F),
     ]
 
 

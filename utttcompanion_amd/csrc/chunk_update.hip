@@ -437,6 +437,8 @@ struct ApplyArgs {
   float* w_out[3];
   float* s_out[3];
   float* surprise;
+  float* row_loss;  // optional (B, 2): per row sum of masked token losses, number of valid tokens
+  float min_row_surprise;  // > 0: rows whose chunk surprise is below it keep W and S
 };
 
 template <typename T>
@@ -516,11 +518,24 @@ __global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
     asum = wave_sum(asum);
     msum = wave_sum(msum);
     any = wave_sum(any);
+    // this row's chunk surprise (masked mean token loss), for the optional update gate
+    const float lsum = wave_sum(lane < a.C ? a.loss[b * 64 + lane] : 0.f);
+    const float row_mean = lsum / fmaxf(a.mask != nullptr ? msum : (float)a.C, 1.f);
     if (lane == 0) {
       const float abar = a.mask != nullptr ? asum / fmaxf(msum, 1.f) : asum / (float)a.C;
       row_scalar[0] = a.max_norm > 0.f ? fminf(a.max_norm * (1.0f / sqrtf(n2 + 1e-8f)), 1.0f) : 1.0f;
       row_scalar[1] = 1.0f - abar;
-      row_scalar[2] = (a.mask == nullptr || any > 0.f) ? 1.f : 0.f;
+      const bool gated_off = a.min_row_surprise > 0.f && row_mean < a.min_row_surprise;
+      row_scalar[2] = ((a.mask == nullptr || any > 0.f) && !gated_off) ? 1.f : 0.f;
+    }
+    if (blockIdx.x == 0 && a.row_loss != nullptr) {
+      const float lt = lane < a.C ? a.loss[b * 64 + lane] : 0.f;
+      const float mt = lane < a.C ? (a.mask != nullptr ? a.mask[(int64_t)b * a.mask_rs + lane] : 1.f) : 0.f;
+      const float sl = wave_sum(lt), sm = wave_sum(mt);
+      if (lane == 0) {
+        a.row_loss[2 * b] = sl;
+        a.row_loss[2 * b + 1] = sm;
+      }
     }
     if (blockIdx.x == 0 && blockIdx.y == 0) {
       // batch-global surprise: sum of masked token losses over all rows / valid tokens
@@ -651,6 +666,8 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   ap.w_out[0] = a.w_up_out; ap.w_out[1] = a.w_gate_out; ap.w_out[2] = a.w_down_out;
   ap.s_out[0] = a.s_up_out; ap.s_out[1] = a.s_gate_out; ap.s_out[2] = a.s_down_out;
   ap.surprise = a.surprise;
+  ap.row_loss = a.row_loss;
+  ap.min_row_surprise = a.min_row_surprise;
   if (want(4)) hipLaunchKernelGGL(k_apply<T>, dim3(3 * (D / 64) * (F / 64), B), blk, 0, st, ap);
 }
 

@@ -135,7 +135,9 @@ def prepare_chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
                          out_state: Optional[Sequence[Tensor]] = None,
                          out: Optional[Tensor] = None,
                          surprise: Optional[Tensor] = None,
-                         workspace: Optional[Tensor] = None) -> PreparedUpdate:
+                         workspace: Optional[Tensor] = None,
+                         row_loss: Optional[Tensor] = None,
+                         min_row_surprise: float = 0.0) -> PreparedUpdate:
     """Validate and marshal one chunk update (see ``chunk_update``) without launching it."""
     if q.dim() != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError(f"q/k/v must share one (B, C, D) shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
@@ -221,7 +223,12 @@ def prepare_chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
     a.w_up_out, a.w_gate_out, a.w_down_out, a.s_up_out, a.s_gate_out, a.s_down_out = (_p(t) for t in outs)
     a.out, a.out_row_stride = _p(out), out.stride(0)
     a.surprise = _p(surprise)
-    keep = (q, k, v, eta, alpha, mask, ws, rw, ln_w, ln_b)
+    if row_loss is not None:
+        if row_loss.shape != (bsz, 2) or row_loss.dtype != torch.float32 or not row_loss.is_contiguous():
+            raise ValueError("row_loss must be a contiguous fp32 (B, 2) tensor")
+        a.row_loss = _p(row_loss)
+    a.min_row_surprise = float(min_row_surprise or 0.0)
+    keep = (q, k, v, eta, alpha, mask, ws, rw, ln_w, ln_b, row_loss)
     return PreparedUpdate(a, keep, workspace, (out, *outs, surprise), dev)
 
 

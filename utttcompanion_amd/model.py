@@ -357,6 +357,13 @@ class uTTTModel(nn.Module):
             if was:
                 self.train()
 
+    def test_time_update_batched(self, interactions, fast_states, attention_masks=None,
+                                 min_chunk_surprise: float = 0.0):
+        """``test_time_update`` for N ragged requests in one chunk loop; one
+        (candidate, surprise, per-layer surprise) tuple per request (see ``evolve``)."""
+        from .evolve import ragged_test_time_update
+        return ragged_test_time_update(self, interactions, fast_states, attention_masks, min_chunk_surprise)
+
     @staticmethod
     def _sample_next_token(logits: Tensor, temperature: float = 0.7, top_p: float = 0.9,
                            recent_tokens: Optional[List[int]] = None, repetition_penalty: float = 1.18,
