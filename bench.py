@@ -34,7 +34,26 @@ PEAK_BF16_TFLOPS = 2500.0
 C2 = dict(vocab_size=32000, d_model=768, n_layers=12, n_heads=12, n_kv_heads=4, d_ff_fast=2048,
           sliding_window_size=512, chunk_size=64, max_seq_len=4096)
 C2_BATCH, C2_SEQ = 8, 2048
+C3 = dict(vocab_size=32000, d_model=2048, n_layers=24, n_heads=16, n_kv_heads=4, d_ff_fast=5504,
+          sliding_window_size=1024, chunk_size=64, max_seq_len=4096)
+C3_BATCH, C3_SEQ = 4, 4096
+C5_REQUESTS, C5_LENGTHS = 16, (128, 4096)
 PHASES = ("k_up_gate", "k_down_partial", "k_ln_grad+k_ln_readout", "k_backward", "k_apply")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` at the config-2 update shape, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (scaled by a copy kernel of known size), or
+    None when no summary for that kernel is present."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{kernel}_c2_traffic.md")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
 
 
 def log(msg: str) -> None:
@@ -48,8 +67,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--phase-iters", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
-    ap.add_argument("--sections", default="prefill,update,decode,cpu",
-                    help="comma list of prefill, update, decode, cpu (profiling runs pick a subset)")
+    ap.add_argument("--sections", default="prefill,update,decode,cpu,c3,evolve",
+                    help="comma list of prefill, update, decode, cpu, c3, evolve, copyref "
+                         "(profiling runs pick a subset)")
+    ap.add_argument("--c3-steps", type=int, default=2, help="timed config-3 prefills / config-5 updates")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="tokens per row of the CPU baseline sample")
     ap.add_argument("--cpu-rows", type=int, default=4, help="rows of the CPU baseline sample")
     ap.add_argument("--decode-steps", type=int, default=256)
@@ -230,6 +251,99 @@ def bench_decode_step(model, steps: int):
                                       "readout_hbm_gbs": round(readout_bytes / (ms * 1e-3) / 1e9, 1)}
 
 
+def build_c3_model():
+    """The config-3 model (1.58B-label: 24 layers, d 2048, 16 x 128 heads, 4 kv heads, window
+    1024, F 5504), initialised directly on the GPU, bf16 with fp32 fast-weight masters."""
+    import torch
+    from utttcompanion_amd import uTTTConfig, uTTTModel
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = uTTTModel(uTTTConfig(**C3)).eval()
+    model = model.to(torch.bfloat16)
+    model.fast_weight_pool.float()
+    return model
+
+
+def bench_c3_prefill(model, steps: int):
+    """Config 3: batch 4 x 4096 uniform token ids, full prefill with the per-chunk writes
+    (64 chunks x 24 layers), launched eagerly (each chunk-layer's update moves ~2 GB of
+    state, so launch overhead is hidden).  Returns (tok/s, ms per prefill)."""
+    import torch
+    g = torch.Generator().manual_seed(6)
+    ids = torch.randint(0, C3["vocab_size"], (C3_BATCH, C3_SEQ), generator=g).to("cuda")
+    state = model.init_fast_state(C3_BATCH, device="cuda", dtype=torch.float32, detach=True)
+    with torch.no_grad():
+        log("config 3: warm-up prefill")
+        model.prefill_with_writes(ids, state)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            out = model.prefill_with_writes(ids, state)
+            log(f"config 3: prefill {i + 1}/{steps} launched")
+        end.record()
+        torch.cuda.synchronize()
+        finite = bool(torch.isfinite(out[2]).all().item())
+    ms = start.elapsed_time(end) / steps
+    return C3_BATCH * C3_SEQ / (ms * 1e-3), ms, finite
+
+
+def bench_evolve(model, steps: int):
+    """Config 5: 16 requests with [prompt + reply] lengths uniform in [128, 4096] on the
+    config-3 model, each with its own fp32 state (W ~ N(0, 0.02) from a generator seeded with
+    the request id, S = 0); one step = ``evolve_batched``: the ragged chunk-wise updates of all
+    requests in one chunk loop (per-chunk surprise gate 0.5), the turn gate (surprise > 0.5) and
+    the elastic pull (lambda 1e-3, drift ceiling 0.35) of the gated requests.  Returns
+    (valid tok/s, ms per step, info)."""
+    import torch
+    from utttcompanion_amd.evolve import evolve_batched
+    from utttcompanion_amd.layer import FastWeightState
+    D, F = C3["d_model"], C3["d_ff_fast"]
+    ln_w = model.fast_weight_pool.ln_weight.detach().float()
+    ln_b = model.fast_weight_pool.ln_bias.detach().float()
+    states = []
+    for rid in range(C5_REQUESTS):
+        g = torch.Generator(device="cuda").manual_seed(rid)
+        w = [torch.randn(1, D, F, device="cuda", generator=g) * 0.02,
+             torch.randn(1, D, F, device="cuda", generator=g) * 0.02,
+             torch.randn(1, F, D, device="cuda", generator=g) * 0.02]
+        states.append(FastWeightState(*w, *(torch.zeros_like(t) for t in w), ln_w, ln_b))
+    g = torch.Generator().manual_seed(8)
+    lengths = torch.randint(C5_LENGTHS[0], C5_LENGTHS[1] + 1, (C5_REQUESTS,), generator=g).tolist()
+    turns = [torch.randint(6, C3["vocab_size"], (n,), generator=g).to("cuda") for n in lengths]
+    kw = dict(surprise_threshold=0.5, anchor_lambda=1e-3, max_drift_ratio=0.35, min_chunk_surprise=0.5)
+    with torch.no_grad():
+        log("config 5: warm-up ragged update")
+        res = evolve_batched(model, turns, states, **kw)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            res = evolve_batched(model, turns, states, **kw)
+            log(f"config 5: step {i + 1}/{steps} done")
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+    tokens = sum(lengths)
+    chunks = sum((n + 63) // 64 for n in lengths)
+    info = {"requests": C5_REQUESTS, "lengths": [min(lengths), max(lengths)], "valid_tokens": tokens,
+            "row_chunks": chunks, "turn_gate_fired": sum(int(r.gate_triggered) for r in res),
+            "mean_surprise": round(sum(r.surprise for r in res) / len(res), 4),
+            "min_state_bytes_per_step": 48 * D * F * chunks * C3["n_layers"]}
+    info["state_hbm_gbs"] = round(info["min_state_bytes_per_step"] / (ms * 1e-3) / 1e9, 1)
+    return tokens / (ms * 1e-3), ms, info
+
+
+def bench_copy_reference(iters: int = 5, nbytes: int = 1 << 30):
+    """A plain device copy of known size (torch copy_), the scale for rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters in the traffic figure."""
+    import torch
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return nbytes
+
+
 def cpu_baseline(model, tokens: int, rows: int):
     """The CPU oracle (PyTorch-CPU fp32 restatement) on ``rows`` x ``tokens`` of config 2 with writes."""
     import torch
@@ -263,44 +377,43 @@ def main() -> int:
         print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
         return 1
     sections = set(args.sections.split(","))
+    if "copyref" in sections:
+        log(f"copy reference: {bench_copy_reference()} bytes x 5")
     model = build_model()
     tokens = C2_BATCH * C2_SEQ
     ms, finite = float("nan"), False
     if "prefill" in sections:
         ms, finite = bench_prefill(model, args.steps, args.warmup)
         log(f"prefill {ms:.2f} ms/step -> {tokens / ms * 1e3:.0f} tok/s (finite={finite})")
-    if "update" not in sections:
-        print(json.dumps({"metric": METRIC, "value": round(tokens / ms * 1e3, 1), "unit": "tok/s",
-                          "ms_per_step": round(ms, 3), "partial_sections": sorted(sections)}), flush=True)
-        return 0
+    roofline = update = decode = None
+    if "update" in sections:
+        per, shape = bench_update_phases(args.phase_iters)
+        total_ms = sum(per)
+        B, C, D, F = shape["B"], shape["C"], shape["D"], shape["F"]
+        dom = max(range(len(per)), key=lambda p: per[p])
+        dbytes, dflops = phase_work(dom, B, C, D, F)
+        d_gbs = dbytes / (per[dom] * 1e-3) / 1e9
+        d_tfl = dflops / (per[dom] * 1e-3) / 1e12
+        hbm_bound = dbytes > 0 and dflops / dbytes < PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+        roofline = ({"bound": "hbm", "achieved": round(d_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(d_gbs / PEAK_HBM_GBS, 4)} if hbm_bound else
+                    {"bound": "mfma", "achieved": round(d_tfl, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(d_tfl / PEAK_BF16_TFLOPS, 4)})
+        roofline.update(kernel=PHASES[dom], traffic=measured_traffic(PHASES[dom]),
+                        per_launch={"algorithmic_bytes": dbytes, "algorithmic_flops": dflops,
+                                    "avg_ms": round(per[dom], 4), "shape": shape})
+        upd_bytes, upd_flops = 48 * D * F * B, 20 * C * D * F * B
+        update = {"ms": round(total_ms, 4), "phase_ms": dict(zip(PHASES, [round(x, 4) for x in per])),
+                  "hbm_frac_min_state_bytes": round(upd_bytes / (total_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                  "mfma_frac": round(upd_flops / (total_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+        log(f"update phases (ms): {update['phase_ms']}")
 
-    per, shape = bench_update_phases(args.phase_iters)
-    total_ms = sum(per)
-    B, C, D, F = shape["B"], shape["C"], shape["D"], shape["F"]
-    dom = max(range(len(per)), key=lambda p: per[p])
-    dbytes, dflops = phase_work(dom, B, C, D, F)
-    d_gbs = dbytes / (per[dom] * 1e-3) / 1e9
-    d_tfl = dflops / (per[dom] * 1e-3) / 1e12
-    hbm_bound = dbytes > 0 and dflops / dbytes < PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
-    roofline = ({"bound": "hbm", "achieved": round(d_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                 "frac": round(d_gbs / PEAK_HBM_GBS, 4)} if hbm_bound else
-                {"bound": "mfma", "achieved": round(d_tfl, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                 "frac": round(d_tfl / PEAK_BF16_TFLOPS, 4)})
-    roofline.update(kernel=PHASES[dom], traffic=None,
-                    per_launch={"algorithmic_bytes": dbytes, "algorithmic_flops": dflops, "avg_ms": round(per[dom], 4),
-                                "shape": shape})
-    upd_bytes, upd_flops = 48 * D * F * B, 20 * C * D * F * B
-    update = {"ms": round(total_ms, 4), "phase_ms": dict(zip(PHASES, [round(x, 4) for x in per])),
-              "hbm_frac_min_state_bytes": round(upd_bytes / (total_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-              "mfma_frac": round(upd_flops / (total_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
-    log(f"update phases (ms): {update['phase_ms']}")
-
-    dec_ms, dec_bytes, dec_shape = bench_decode(20) if "decode" in sections else (float("nan"), 1, {})
-    dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
-    decode = {"kernel": "k_swa_decode", "us_per_layer_step": round(dec_ms * 1e3, 2), "achieved_gbs": round(dec_gbs, 1),
-              "hbm_frac": round(dec_gbs / PEAK_HBM_GBS, 4), "shape": dec_shape}
-    log(f"decode kernel {dec_ms * 1e3:.1f} us -> {dec_gbs:.0f} GB/s")
     if "decode" in sections:
+        dec_ms, dec_bytes, dec_shape = bench_decode(20)
+        dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
+        decode = {"kernel": "k_swa_decode", "us_per_layer_step": round(dec_ms * 1e3, 2),
+                  "achieved_gbs": round(dec_gbs, 1), "hbm_frac": round(dec_gbs / PEAK_HBM_GBS, 4), "shape": dec_shape}
+        log(f"decode kernel {dec_ms * 1e3:.1f} us -> {dec_gbs:.0f} GB/s")
         tps, step_ms, info = bench_decode_step(model, args.decode_steps)
         decode.update(decode_tok_s=round(tps, 1), ms_per_decode_step=round(step_ms, 4), workload=info)
         log(f"decode step {step_ms:.3f} ms -> {tps:.0f} tok/s")
@@ -311,6 +424,25 @@ def main() -> int:
         cpu = cpu_baseline(model, args.cpu_tokens, args.cpu_rows)
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
 
+    big = {}
+    if sections & {"c3", "evolve"}:
+        del model
+        torch.cuda.empty_cache()
+        log("building the config-3 model on the GPU")
+        model3 = build_c3_model()
+        if "c3" in sections:
+            tps, c3_ms, fin = bench_c3_prefill(model3, args.c3_steps)
+            big["config3_prefill"] = {"tok_s": round(tps, 1), "ms_per_prefill": round(c3_ms, 2), "finite": fin,
+                                      "batch": C3_BATCH, "seq_len": C3_SEQ, "layers": C3["n_layers"],
+                                      "d_model": C3["d_model"], "d_ff_fast": C3["d_ff_fast"]}
+            log(f"config 3 prefill {c3_ms:.1f} ms -> {tps:.0f} tok/s")
+        if "evolve" in sections:
+            tps, ev_ms, info = bench_evolve(model3, args.c3_steps)
+            big["config5_evolve"] = {"tok_s": round(tps, 1), "ms_per_step": round(ev_ms, 2), **info}
+            log(f"config 5 ragged update {ev_ms:.1f} ms -> {tps:.0f} tok/s")
+        del model3
+        torch.cuda.empty_cache()
+
     line = {"metric": METRIC, "value": round(tokens / ms * 1e3, 1), "unit": "tok/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
@@ -319,7 +451,7 @@ def main() -> int:
                        "seq_len": C2_SEQ, "layers": C2["n_layers"], "d_model": C2["d_model"],
                        "d_ff_fast": C2["d_ff_fast"], "window": C2["sliding_window_size"], "chunk": C2["chunk_size"],
                        "parallelism": "none (1 GPU)", "hip_graph": True, "finite": finite},
-            "roofline": roofline, "update": update, "decode": decode, "cpu_baseline": cpu}
+            "roofline": roofline, "update": update, "decode": decode, **big, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
     return 0
 
