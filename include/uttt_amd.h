@@ -88,6 +88,43 @@ int uttt_chunk_update_phase(const uttt_chunk_update_args* args, void* workspace,
                             int32_t phase, uttt_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * 1b. One chunk's updates for all L layers of the chunk-first shared schedule.
+ *     Replaces the per-layer chunk_step calls that uTTTModel._run_shared_chunk /
+ *     _run_shared_layer_segment (model/uttt_model.py:519-608) make for one chunk: layer l's
+ *     update (model/uttt_layer.py:414-534, loss / clip / momentum / decay / inactive rows as
+ *     in uttt_chunk_update) is applied to the state left by layers 0..l-1, starting from the
+ *     chunk-start state.  Every layer's readout reads the chunk-start state, so readouts are
+ *     not part of this call (uttt_swiglu_readout over that state or its bf16 copies).
+ *     The state is updated in place, once.  Layer l's inputs are given per layer:
+ *     k/v (batch, tokens, d_model) with token stride d_model and row stride kv_row_stride,
+ *     eta/alpha (batch, tokens) with token stride 1 and row stride ea_row_stride.
+ * ------------------------------------------------------------------------- */
+#define UTTT_MAX_CHAIN 64
+typedef struct {
+  int64_t batch, layers, tokens, d_model, d_ff; /* layers <= UTTT_MAX_CHAIN, tokens <= 64 */
+  int32_t act_dtype, normalize_by_dim;
+  float momentum_beta, max_inner_grad_norm, eps;
+  float min_row_surprise;            /* > 0: per-chunk surprise gate per layer (not in the reference) */
+  const void* k[UTTT_MAX_CHAIN];
+  const void* v[UTTT_MAX_CHAIN];
+  int64_t kv_row_stride;
+  const void* eta[UTTT_MAX_CHAIN];
+  const void* alpha[UTTT_MAX_CHAIN];
+  int64_t ea_row_stride;
+  const float* token_mask; int64_t mask_row_stride; /* optional (batch, >= tokens) fp32, all layers */
+  float* w_up; float* w_gate; float* w_down;        /* fp32 (B, D, F), (B, D, F), (B, F, D); in/out */
+  float* s_up; float* s_gate; float* s_down;
+  const float* ln_weight; const float* ln_bias;     /* (D,) fp32 */
+  void* w_up_copy; void* w_gate_copy; void* w_down_copy; /* optional bf16 copies of the final W */
+  float* surprise;                   /* (layers,) batch-global surprise of each layer */
+  float* row_loss;                   /* optional (layers, batch, 2): [sum of masked token losses, valid tokens] */
+} uttt_chunk_chain_args;
+
+size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff, int32_t act_dtype);
+int uttt_chunk_chain(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
+                     uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * 2. Frozen fast-weight readout f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down).
  *    Replaces swiglu_fast_forward (model/uttt_layer.py:211-247) as used by
  *    SharedFastWeightPool.forward_readout (:670-695) and the packed inference

@@ -41,7 +41,8 @@ def test_every_declared_symbol_is_exported_and_typed(lib):
 def test_struct_layouts_match_the_c_header(tmp_path):
     structs = {"uttt_chunk_update_args": N.ChunkUpdateArgs, "uttt_readout_args": N.ReadoutArgs,
                "uttt_rope_append_args": N.RopeAppendArgs, "uttt_swa_prefill_args": N.SwaPrefillArgs,
-               "uttt_swa_decode_args": N.SwaDecodeArgs, "uttt_elastic_pull_args": N.ElasticPullArgs}
+               "uttt_swa_decode_args": N.SwaDecodeArgs, "uttt_elastic_pull_args": N.ElasticPullArgs,
+               "uttt_chunk_chain_args": N.ChunkChainArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -70,6 +71,8 @@ def test_host_side_calls(lib):
     assert ws > 8 * 64 * 2048 * 4
     assert lib.uttt_chunk_update_workspace(8, 770, 2048, N.DTYPE_BF16) == 0  # invalid d_model
     assert lib.uttt_readout_workspace(2, 100, 512, 1024, N.DTYPE_F32) > 0
+    assert lib.uttt_chunk_chain_workspace(8, 12, 768, 2048, N.DTYPE_BF16) > 12 * 8 * 64 * 2048 * 2 * 7
+    assert lib.uttt_chunk_chain_workspace(8, N.MAX_CHAIN + 1, 768, 2048, N.DTYPE_BF16) == 0  # too many layers
 
 
 def test_invalid_arguments_are_rejected_before_any_launch(lib):
@@ -82,6 +85,13 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     p.batch, p.n_heads, p.n_kv_heads, p.head_dim = 1, 4, 3, 64
     assert lib.uttt_swa_prefill(C.byref(p), None) == 1
     assert b"n_kv_heads" in lib.uttt_last_error()
+    ch = N.ChunkChainArgs()
+    ch.batch, ch.layers, ch.tokens, ch.d_model, ch.d_ff = 2, 3, 64, 512, 1024
+    assert lib.uttt_chunk_chain(C.byref(ch), None, 0, None) == 1
+    assert b"layer 0 must be non-NULL" in lib.uttt_last_error()
+    ch.layers = 0
+    assert lib.uttt_chunk_chain(C.byref(ch), None, 0, None) == 1
+    assert b"layers must be in" in lib.uttt_last_error()
     d = N.SwaDecodeArgs()
     d.head_dim = 96
     assert lib.uttt_swa_decode(C.byref(d), None) == 1

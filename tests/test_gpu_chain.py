@@ -1,0 +1,169 @@
+"""GPU parity of the layer chain (``uttt_chunk_chain``) with L sequential updates.
+
+The chain computes one chunk's updates of all L layers at once: layer l's update is
+applied to the state left by layers 0..l-1.  The expected state is the oracle's
+``fused_chunk_ttt_step`` applied L times in sequence (reference model/uttt_layer.py:414-534
+inside the chunk-first schedule of model/uttt_model.py:453-608).  Tolerances as for the
+single update: fp32 <= 1e-5 relative (max|err| / max|ref|) for W, S and the per-layer
+surprise; bf16 activations <= 2e-2 max-abs for the fp32 state against the fp32 oracle.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import uttt_math as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAMES = ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")
+
+
+def rel_err(actual, expected):
+    actual = actual.detach().double().cpu()
+    expected = expected.detach().double().cpu()
+    return (actual - expected).abs().max().item() / max(expected.abs().max().item(), 1e-30)
+
+
+def make_layers(n_layers, b, c, d, f, seed, w_scale=None):
+    g = torch.Generator().manual_seed(seed)
+    sw = w_scale if w_scale is not None else 1.0 / math.sqrt(d)
+    layers = []
+    for _ in range(n_layers):
+        k, v = torch.randn(b, c, d, generator=g), torch.randn(b, c, d, generator=g)
+        eta = 0.02 * torch.sigmoid(torch.randn(b, c, 1, generator=g))
+        alpha = 0.01 * torch.sigmoid(torch.randn(b, c, 1, generator=g) - 1.386)
+        layers.append((k, v, eta, alpha))
+    w = (torch.randn(b, d, f, generator=g) * sw, torch.randn(b, d, f, generator=g) * sw,
+         torch.randn(b, f, d, generator=g) * 0.3 / math.sqrt(f))
+    s = tuple(torch.randn(t.shape, generator=g) * 1e-3 for t in w)
+    ln_w = 1.0 + 0.1 * torch.randn(d, generator=g)
+    ln_b = 0.05 * torch.randn(d, generator=g)
+    return layers, w, s, ln_w, ln_b
+
+
+def oracle_chain(layers, w, s, ln_w, ln_b, mask, beta, clip, norm, gate=0.0):
+    surprises = []
+    for k, v, eta, alpha in layers:
+        res = om.fused_chunk_ttt_step(k, k, v, eta, alpha, *w, *s, ln_w, ln_b, mask, beta, clip, norm, 1e-5,
+                                      min_row_surprise=gate)
+        w, s = res[1:4], res[4:7]
+        surprises.append(res[7])
+    return w + s, torch.stack(surprises)
+
+
+def run_chain(layers, w, s, ln_w, ln_b, mask, beta, clip, norm, dtype, gate=0.0, copies=False, row_loss=False):
+    from utttcompanion_amd import kernels as K
+    b, c, d = layers[0][0].shape
+    state = [t.clone().to(DEV) for t in w + s]
+    ks = [x[0].to(DEV, dtype) for x in layers]
+    vs = [x[1].to(DEV, dtype) for x in layers]
+    etas = [x[2].to(DEV, dtype) for x in layers]
+    alphas = [x[3].to(DEV, dtype) for x in layers]
+    cps = [torch.empty_like(t, dtype=torch.bfloat16) for t in state[:3]] if copies else None
+    rl = torch.full((len(layers), b, 2), float("nan"), device=DEV) if row_loss else None
+    with torch.no_grad():
+        surprise, _ = K.chunk_chain(ks, vs, etas, alphas, state, ln_w.to(DEV), ln_b.to(DEV),
+                                    None if mask is None else mask.to(DEV), beta, clip, norm, 1e-5, copies=cps,
+                                    row_loss=rl, min_row_surprise=gate)
+    torch.cuda.synchronize()
+    return state, surprise, cps, rl
+
+
+CASES = [
+    dict(L=3, b=2, c=64, d=128, f=192, mask=False, clip=1.0, norm=True, beta=0.9),
+    dict(L=5, b=3, c=40, d=64, f=128, mask=True, clip=1e-3, norm=True, beta=0.9),    # tail chunk, clip active
+    dict(L=12, b=1, c=64, d=256, f=512, mask=False, clip=1.0, norm=False, beta=0.95),  # 12 layers, 1 row
+    dict(L=2, b=4, c=17, d=192, f=320, mask=True, clip=0.0, norm=True, beta=0.0),     # no clip, no momentum
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_chain_fp32_matches_sequential_oracle(case):
+    print(f"chain case {case}", flush=True)
+    layers, w, s, ln_w, ln_b = make_layers(case["L"], case["b"], case["c"], case["d"], case["f"], seed=3 + case["L"])
+    mask = None
+    if case["mask"]:
+        mask = torch.ones(case["b"], case["c"])
+        mask[0, case["c"] // 2:] = 0
+        if case["b"] > 2:
+            mask[2] = 0  # a row with no valid token keeps W and S through every layer
+    ref, ref_s = oracle_chain(layers, w, s, ln_w, ln_b, mask, case["beta"], case["clip"], case["norm"])
+    got, got_s, _, _ = run_chain(layers, w, s, ln_w, ln_b, mask, case["beta"], case["clip"], case["norm"],
+                                 torch.float32)
+    for name, a, e in zip(NAMES, got, ref):
+        err = rel_err(a, e)
+        assert err <= 1e-5, f"{name}: rel err {err:.3e}"
+    assert rel_err(got_s, ref_s) <= 1e-5
+    if case["mask"] and case["b"] > 2:
+        for a, o in zip(got, w + s):
+            assert torch.equal(a[2].cpu(), o[2]), "a row without tokens changed"
+
+
+def test_chain_bf16_within_tolerance_and_copies():
+    layers, w, s, ln_w, ln_b = make_layers(6, 2, 64, 256, 512, seed=41, w_scale=0.02)
+    ref, ref_s = oracle_chain(layers, w, s, ln_w, ln_b, None, 0.9, 1.0, True)
+    got, got_s, cps, _ = run_chain(layers, w, s, ln_w, ln_b, None, 0.9, 1.0, True, torch.bfloat16, copies=True)
+    for name, a, e in zip(NAMES, got, ref):
+        err = (a.cpu() - e).abs().max().item()
+        assert err <= 2e-2, f"{name}: max abs err {err:.3e}"
+    assert (got_s.cpu() - ref_s).abs().max().item() <= 2e-2 * max(1.0, ref_s.abs().max().item())
+    for cp, wt in zip(cps, got[:3]):
+        assert torch.equal(cp, wt.to(torch.bfloat16))
+
+
+def test_chain_equals_per_layer_hip_updates_bf16():
+    """The chain and L calls of the single-layer HIP update take the same bf16 operands."""
+    from utttcompanion_amd import kernels as K
+    layers, w, s, ln_w, ln_b = make_layers(4, 3, 64, 128, 256, seed=7, w_scale=0.05)
+    got, got_s, _, _ = run_chain(layers, w, s, ln_w, ln_b, None, 0.9, 1.0, True, torch.bfloat16)
+    state = [t.clone().to(DEV) for t in w + s]
+    surprises = []
+    with torch.no_grad():
+        for k, v, eta, alpha in layers:
+            kb = k.to(DEV, torch.bfloat16)
+            res = K.chunk_update(kb, kb, v.to(DEV, torch.bfloat16), eta.to(DEV, torch.bfloat16),
+                                 alpha.to(DEV, torch.bfloat16), *state, ln_w.to(DEV), ln_b.to(DEV), None, 0.9, 1.0,
+                                 True, 1e-5)
+            state = list(res[1:7])
+            surprises.append(res[7])
+    for name, a, e in zip(NAMES, got, state):
+        scale = e.abs().max().item()
+        err = (a - e).abs().max().item()
+        assert err <= 5e-3 * scale + 1e-6, f"{name}: {err:.3e} vs scale {scale:.3e}"
+    assert rel_err(got_s, torch.stack(surprises)) <= 1e-2
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_chain_row_loss_and_gate_match_oracle(masked):
+    layers, w, s, ln_w, ln_b = make_layers(3, 4, 64, 128, 192, seed=13)
+    for i, x in enumerate(layers):  # rows with losses far apart, so a threshold separates them
+        layers[i] = (x[0], x[1] * torch.tensor([0.3, 1.0, 3.0, 10.0]).view(4, 1, 1), x[2], x[3])
+    mask = None
+    if masked:
+        mask = torch.ones(4, 64)
+        mask[1, 40:] = 0
+        mask[3, ::3] = 0
+    means = [om.row_surprise(x[0], x[1], *w, ln_w, ln_b, mask, True, 1e-5) for x in layers[:1]]
+    thr = float(means[0][1] + means[0][2]) / 2
+    ref, ref_s = oracle_chain(layers, w, s, ln_w, ln_b, mask, 0.9, 1.0, True, gate=thr)
+    got, got_s, _, rl = run_chain(layers, w, s, ln_w, ln_b, mask, 0.9, 1.0, True, torch.float32, gate=thr,
+                                  row_loss=True)
+    for name, a, e in zip(NAMES, got, ref):
+        assert rel_err(a, e) <= 1e-5, name
+    assert rel_err(got_s, ref_s) <= 1e-5
+    counts = mask.sum(1) if masked else torch.full((4,), 64.0)
+    assert torch.equal(rl[0, :, 1].cpu(), counts)
+    assert rel_err(rl[0, :, 0].cpu() / counts, means[0]) <= 1e-5
+
+
+def test_chain_rejects_bad_input():
+    from utttcompanion_amd import kernels as K
+    layers, w, s, ln_w, ln_b = make_layers(2, 1, 8, 64, 64, seed=1)
+    state = [t.to(DEV) for t in w + s]
+    ks = [x[0].to(DEV) for x in layers]
+    with pytest.raises(ValueError):
+        K.chunk_chain(ks, ks[:1], ks, ks, state, ln_w.to(DEV), ln_b.to(DEV), None, 0.9, 1.0, True, 1e-5)
+    with pytest.raises(ValueError):  # in-place state must be fp32
+        K.chunk_chain(ks, ks, [x[2].to(DEV) for x in layers], [x[3].to(DEV) for x in layers],
+                      [t.double() for t in state], ln_w.to(DEV), ln_b.to(DEV), None, 0.9, 1.0, True, 1e-5)

@@ -11,7 +11,8 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 6
+ABI_VERSION = 7
+MAX_CHAIN = 64
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 UPDATE_PHASES = 5
@@ -41,6 +42,22 @@ class ChunkUpdateArgs(C.Structure):
         ("s_up_out", _P), ("s_gate_out", _P), ("s_down_out", _P),
         ("out", _P), ("out_row_stride", _I64),
         ("surprise", _P), ("row_loss", _P), ("min_row_surprise", _F),
+    ]
+
+
+class ChunkChainArgs(C.Structure):
+    _fields_ = [
+        ("batch", _I64), ("layers", _I64), ("tokens", _I64), ("d_model", _I64), ("d_ff", _I64),
+        ("act_dtype", _I32), ("normalize_by_dim", _I32),
+        ("momentum_beta", _F), ("max_inner_grad_norm", _F), ("eps", _F), ("min_row_surprise", _F),
+        ("k", _P * 64), ("v", _P * 64), ("kv_row_stride", _I64),
+        ("eta", _P * 64), ("alpha", _P * 64), ("ea_row_stride", _I64),
+        ("token_mask", _P), ("mask_row_stride", _I64),
+        ("w_up", _P), ("w_gate", _P), ("w_down", _P),
+        ("s_up", _P), ("s_gate", _P), ("s_down", _P),
+        ("ln_weight", _P), ("ln_bias", _P),
+        ("w_up_copy", _P), ("w_gate_copy", _P), ("w_down_copy", _P),
+        ("surprise", _P), ("row_loss", _P),
     ]
 
 
@@ -113,6 +130,8 @@ SIGNATURES = {
     "uttt_chunk_update_workspace": (C.c_size_t, [_I64, _I64, _I64, _I32]),
     "uttt_chunk_update": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_update_phase": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _I32, _P]),
+    "uttt_chunk_chain_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
+    "uttt_chunk_chain": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _P]),
     "uttt_readout_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_swiglu_readout": (C.c_int, [C.POINTER(ReadoutArgs), _P, C.c_size_t, _P]),
     "uttt_rope_kv_append": (C.c_int, [C.POINTER(RopeAppendArgs), _P]),

@@ -1,0 +1,889 @@
+// One chunk's fast-weight updates for all L layers of the chunk-first shared schedule,
+// written for gfx950 (MI355X).
+//
+// In the reference schedule (model/uttt_model.py:453-608) every layer of a chunk reads the
+// chunk-start snapshot (W_s, S_s) for its readout and layer l's update is applied to the
+// cursor left by layers 0..l-1 (model/uttt_layer.py:414-534 per layer).  Because every
+// readout reads the snapshot, all L layers' keys, values, eta and alpha are known before the
+// first update, and the L chained updates can be carried out without materialising the
+// intermediate states.  Per row, with g_j = (K_j^T dU_j, K_j^T dG_j, H_j^T dZ_j) the
+// gradient of layer j, clip c_j, decay d_j = 1 - mean(alpha_j) and momentum beta:
+//
+//   S_{l+1} = beta S_l - c_l g_l,   W_{l+1} = d_l W_l + S_{l+1}     (rows without tokens: no-op)
+//   =>  W_l = a_l W_s + b_l S_s + sum_{j<l} gam_{l,j} g_j,   S_l = e_l S_s + sum_{j<l} sig_{l,j} g_j
+//   e' = beta e, sig'_j = beta sig_j, sig'_l = -c_l, a' = d a, b' = d b + e', gam'_j = d gam_j + sig'_j
+//
+// so layer l's forward pass through W_l needs only products with the snapshot plus small
+// products with earlier layers' activations:
+//   U_l = a K_l W_up,s + b K_l S_up,s + sum_j gam_{l,j} (K_l K_j^T) dU_j          (G alike)
+//   Z_l = H_l (a W_down,s + b S_down,s) + sum_j gam_{l,j} (H_l H_j^T) dZ_j
+//   dH_l = dZ_l (a W_down,s + b S_down,s)^T + sum_j gam_{l,j} (dZ_l dZ_j^T) H_j
+//   |g_l|^2 = <K_l K_l^T, dU_l dU_l^T + dG_l dG_l^T> + <H_l H_l^T, dZ_l dZ_l^T>
+// and the state is written once, at the end of the chunk.  The (K W_s, K S_s) products of
+// all layers form one GEMM with L*64 rows, so W_up/W_gate/S_up/S_gate are read once per
+// chunk instead of once per layer, and W/S are written once per chunk instead of once per
+// layer.
+//
+// Launch sequence (one stream): init, pq, K-gram, then per layer l:
+//   up (U, G, H) -> H-gram -> down (Z partials) -> k_ln_grad (dZ, loss) -> dZ-gram
+//   -> back (dU, dG, norm partials) -> coef (clip, decay, recurrences);
+// then apply (final W, S and optional bf16 copies of W).
+#include "update_ln.h"
+#include "uttt_device.h"
+#include "uttt_host.h"
+
+namespace uttt {
+
+namespace {
+
+constexpr int KT = 64;
+constexpr int kMaxChain = UTTT_MAX_CHAIN;
+constexpr int kCoefStride = 4 + 2 * kMaxChain;  // a, b, e, -, gam[kMaxChain], sig[kMaxChain]
+constexpr int kGam = 4, kSig = 4 + kMaxChain;
+constexpr int kPqGroup = 4;                      // layers per workgroup in the P/Q GEMM
+
+template <typename T> constexpr int lds_ld() { return KT + Mma<T>::kPad; }
+
+struct LayerPtrs {
+  const void* p[kMaxChain];
+};
+
+// Per-layer activations: row b, token t of layer l at ptr[l] + b * row_stride + t * tok_stride.
+struct Acts {
+  LayerPtrs k, v, eta, alpha;
+  int64_t kv_rs, kv_ts;     // k / v strides (elements)
+  int64_t ea_rs, ea_ts;     // eta / alpha strides
+};
+
+template <typename T>
+__device__ __forceinline__ const T* layer_row(const LayerPtrs& lp, int l, int b, int64_t rs) {
+  return static_cast<const T*>(lp.p[l]) + (int64_t)b * rs;
+}
+
+// stage dst[row][k] = scale * src[row * ld + k] (64 x 64, fp32 source, summed over nothing)
+template <typename T>
+__device__ __forceinline__ void stage_scaled(T* dst, int ldd, const float* src, int64_t ld, float scale) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    const int row = idx >> 6, c = idx & 63;
+    dst[row * ldd + c] = from_f32<T>(scale * src[(int64_t)row * ld + c]);
+  }
+}
+
+// Register-staged K x 64 (KT rows) tile of ca * X + cb * Y (fp32 sources), transposed to [col][k].
+struct CombColStage {
+  static constexpr int kUnits = (KT / 8) * 16;  // 128: 8 rows x 4 floats per unit
+  uint4 rx[8], ry[8];
+  __device__ __forceinline__ void load(const float* x, const float* y, int64_t ld, bool with_y) {
+    if (threadIdx.x >= kUnits) return;
+    const int kg = threadIdx.x >> 4, cg = threadIdx.x & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t off = (int64_t)(kg * 8 + i) * ld + cg * 4;
+      rx[i] = *reinterpret_cast<const uint4*>(x + off);
+      ry[i] = with_y ? *reinterpret_cast<const uint4*>(y + off) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  template <typename T>
+  __device__ __forceinline__ void store(T* dst, int ldd, float ca, float cb) const {
+    if (threadIdx.x >= kUnits) return;
+    const int kg = threadIdx.x >> 4, cg = threadIdx.x & 15;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      T* d = dst + (cg * 4 + v) * ldd + kg * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        d[i] = from_f32<T>(ca * Lanes16<float>::get(rx[i], v) + cb * Lanes16<float>::get(ry[i], v));
+    }
+  }
+};
+
+// Register-staged 64 x KT tile of ca * X + cb * Y (fp32 sources, row-major), LDS [row][k].
+struct CombRowStage {
+  static constexpr int kN = 64 * (KT / 4) / kThreads;  // 4
+  uint4 rx[kN], ry[kN];
+  __device__ __forceinline__ void load(const float* x, const float* y, int64_t ld, bool with_y) {
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int row = idx >> 4, c = idx & 15;
+      const int64_t off = (int64_t)row * ld + c * 4;
+      rx[j] = *reinterpret_cast<const uint4*>(x + off);
+      ry[j] = with_y ? *reinterpret_cast<const uint4*>(y + off) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  template <typename T>
+  __device__ __forceinline__ void store(T* dst, int ldd, float ca, float cb) const {
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int row = idx >> 4, c = idx & 15;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        dst[row * ldd + c * 4 + v] =
+            from_f32<T>(ca * Lanes16<float>::get(rx[j], v) + cb * Lanes16<float>::get(ry[j], v));
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// 0. coefficient tables: a = e = 1, everything else 0 (a fill kernel, safe in graphs)
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads) k_chain_init(float* coef, int n) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int slot = i % kCoefStride;
+  coef[i] = (slot == 0 || slot == 2) ? 1.f : 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// 1. P/Q: pq[m][l][b] = K_l X_m for X = (W_up, S_up, W_gate, S_gate) of the snapshot,
+//    kPqGroup layers per workgroup sharing each staged X tile.
+// ---------------------------------------------------------------------------
+struct PqArgs {
+  int B, L, C, D, F;
+  Acts acts;
+  const float* x[4];
+  void* pq;  // (4, L, B, 64, F) act dtype
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ __align__(16) T bs[64 * LD];
+  __shared__ __align__(16) T as[kPqGroup * 64 * LD];
+  const int ft = blockIdx.x, m = blockIdx.z & 3, b = blockIdx.z >> 2;
+  const int f0 = ft * 64, l0 = blockIdx.y * kPqGroup;
+  const int nl = min(kPqGroup, a.L - l0);
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  const float* xs = a.x[m] + (int64_t)b * a.D * a.F + f0;
+  const T* kr[kPqGroup];
+#pragma unroll
+  for (int g = 0; g < kPqGroup; ++g)
+    kr[g] = layer_row<T>(a.acts.k, g < nl ? l0 + g : l0, b, a.acts.kv_rs);
+
+  ColStage<float, KT> xst;
+  RowStage<T, KT> kst[kPqGroup];
+  xst.load(xs, a.F, KT, threadIdx.x);
+#pragma unroll
+  for (int g = 0; g < kPqGroup; ++g)
+    if (g < nl) kst[g].load(kr[g], a.acts.kv_ts, a.C);
+  f32x16 acc[kPqGroup];
+#pragma unroll
+  for (int g = 0; g < kPqGroup; ++g) zero(acc[g]);
+  for (int d0 = 0; d0 < a.D; d0 += KT) {
+    xst.template store<T>(bs, LD);
+#pragma unroll
+    for (int g = 0; g < kPqGroup; ++g)
+      if (g < nl) kst[g].template store<T>(as + g * 64 * LD, LD);
+    __syncthreads();
+    if (d0 + KT < a.D) {
+      xst.load(xs + (int64_t)(d0 + KT) * a.F, a.F, KT, threadIdx.x);
+#pragma unroll
+      for (int g = 0; g < kPqGroup; ++g)
+        if (g < nl) kst[g].load(kr[g] + d0 + KT, a.acts.kv_ts, a.C);
+    }
+#pragma unroll
+    for (int g = 0; g < kPqGroup; ++g)
+      if (g < nl) wave_mma<T, KT>(acc[g], as + g * 64 * LD + wr * LD, LD, bs + wc * LD, LD);
+    __syncthreads();
+  }
+  const int col = f0 + wc + acc_col();
+#pragma unroll
+  for (int g = 0; g < kPqGroup; ++g) {
+    if (g >= nl) continue;
+    T* out = static_cast<T*>(a.pq) + (((int64_t)m * a.L + l0 + g) * a.B + b) * 64 * a.F;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[(int64_t)(wr + acc_row(i)) * a.F + col] = from_f32<T>(acc[g][i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. Gram blocks G[l][j] = X_l X_j^T over the feature dimension, one 32 x 32 block per
+//    single-wave workgroup, operands loaded straight from global memory (rows >= C are 0).
+//    Row mode (layer >= 0): blocks (layer, j) for j <= layer into out (B, 64, LL);
+//    all-pairs mode: every j <= l into out (B, LL, LL).
+// ---------------------------------------------------------------------------
+struct GramArgs {
+  int B, C, kd, LL, layer;
+  int64_t rs, ts;  // row / token strides of X (elements)
+  LayerPtrs x;
+  float* out;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(64) k_chain_gram(const GramArgs a) {
+  const int q = blockIdx.x & 3;  // 32 x 32 quadrant of the 64 x 64 block
+  const int blk = blockIdx.x >> 2, b = blockIdx.y;
+  int l, j;
+  if (a.layer >= 0) {
+    l = a.layer;
+    j = blk;
+  } else {
+    l = (int)((sqrtf(8.f * (float)blk + 1.f) - 1.f) * 0.5f);
+    while ((l + 1) * (l + 2) / 2 <= blk) ++l;
+    while (l * (l + 1) / 2 > blk) --l;
+    j = blk - l * (l + 1) / 2;
+  }
+  const int lane = threadIdx.x, r = lane & 31, h = lane >> 5;
+  const int ti = (q >> 1) * 32 + r, tj = (q & 1) * 32 + r;
+  const T* xa = layer_row<T>(a.x, l, b, a.rs) + (int64_t)ti * a.ts;
+  const T* xb = layer_row<T>(a.x, j, b, a.rs) + (int64_t)tj * a.ts;
+  const bool va = ti < a.C, vb = tj < a.C;
+  f32x16 acc;
+  zero(acc);
+  if constexpr (sizeof(T) == 2) {
+    for (int k0 = 0; k0 < a.kd; k0 += 16) {
+      bf16x8 av, bv;
+      const uint4 ra = va ? *reinterpret_cast<const uint4*>(xa + k0 + h * 8) : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 rb = vb ? *reinterpret_cast<const uint4*>(xb + k0 + h * 8) : make_uint4(0u, 0u, 0u, 0u);
+      av = *reinterpret_cast<const bf16x8*>(&ra);
+      bv = *reinterpret_cast<const bf16x8*>(&rb);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+    }
+  } else {
+    for (int k0 = 0; k0 < a.kd; k0 += 8) {
+      const f32x4 av = va ? *reinterpret_cast<const f32x4*>(xa + k0 + h * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 bv = vb ? *reinterpret_cast<const f32x4*>(xb + k0 + h * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc, 0, 0, 0);
+    }
+  }
+  float* out = a.layer >= 0 ? a.out + (int64_t)b * 64 * a.LL
+                            : a.out + ((int64_t)b * a.LL + l * 64) * a.LL;
+  const int c = j * 64 + (q & 1) * 32 + r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = (q >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+    out[(int64_t)row * a.LL + c] = acc[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. Layer l forward through W_l: U, G (fp32, kept for the backward), H (act dtype)
+// ---------------------------------------------------------------------------
+struct UpArgs {
+  int B, L, C, D, F, LL, l;
+  const float* coef;
+  const void* pq;
+  const float* kk;  // (B, LL, LL)
+  const void* du_all;
+  const void* dg_all;  // (L, B, 64, F)
+  float* u_cur;
+  float* g_cur;  // (B, 64, F)
+  void* h_all;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_chain_up(const UpArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ __align__(16) T as[64 * LD];
+  __shared__ __align__(16) T bu[64 * LD];
+  __shared__ __align__(16) T bg[64 * LD];
+  const int ft = blockIdx.x, b = blockIdx.y, f0 = ft * 64;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  const float* cf = a.coef + (int64_t)b * kCoefStride;
+  const float ca = cf[0], cb = cf[1];
+  f32x16 au, ag;
+  zero(au);
+  zero(ag);
+  constexpr int U = ColStage<T, 64>::kUnits;
+  const bool up_half = threadIdx.x < U;
+  const int unit = up_half ? (int)threadIdx.x : min((int)threadIdx.x - U, U);
+  for (int j = 0; j < a.l; ++j) {
+    const float gj = cf[kGam + j];
+    if (gj == 0.f) continue;
+    const int64_t tile = ((int64_t)j * a.B + b) * 64 * a.F + f0;
+    ColStage<T, 64> st;
+    st.load(static_cast<const T*>(up_half ? a.du_all : a.dg_all) + tile, a.F, 64, unit);
+    stage_scaled<T>(as, LD, a.kk + ((int64_t)b * a.LL + a.l * 64) * a.LL + j * 64, a.LL, gj);
+    st.template store<T>(up_half ? bu : bg, LD);
+    __syncthreads();
+    wave_mma<T, 64>(au, as + wr * LD, LD, bu + wc * LD, LD);
+    wave_mma<T, 64>(ag, as + wr * LD, LD, bg + wc * LD, LD);
+    __syncthreads();
+  }
+  const int64_t lane_base = (int64_t)b * 64 * a.F + f0;
+  const int64_t plane = (int64_t)a.L * a.B * 64 * a.F;
+  const T* pl = static_cast<const T*>(a.pq) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
+  T* h = static_cast<T*>(a.h_all) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
+  const int col = wc + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
+    float u = ca * to_f32(pl[off]) + au[i];
+    float g = ca * to_f32(pl[2 * plane + off]) + ag[i];
+    if (cb != 0.f) {
+      u += cb * to_f32(pl[plane + off]);
+      g += cb * to_f32(pl[3 * plane + off]);
+    }
+    a.u_cur[lane_base + off] = u;
+    a.g_cur[lane_base + off] = g;
+    h[off] = from_f32<T>((g * sigmoidf_acc(g)) * u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. Z partials: splits < nsplit take H_l (a W_down,s + b S_down,s) over an F range;
+//    split nsplit (l > 0) takes sum_j gam_j (H_l H_j^T) dZ_j.
+// ---------------------------------------------------------------------------
+struct DownArgs {
+  int B, L, C, D, F, LL, l, nsplit;
+  const float* coef;
+  const void* h_all;
+  const float* wd;
+  const float* sd;  // (B, F, D)
+  const float* hh;  // (B, 64, LL): H_l H_j^T
+  const void* dz_all;  // (L, B, 64, D)
+  float* zp;           // (nsplit + 1, B, 64, D)
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_chain_down(const DownArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ __align__(16) T hs[64 * LD];
+  __shared__ __align__(16) T ws[64 * LD];
+  const int dt = blockIdx.x, split = blockIdx.y, b = blockIdx.z, d0 = dt * 64;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  const float* cf = a.coef + (int64_t)b * kCoefStride;
+  f32x16 acc;
+  zero(acc);
+  if (split < a.nsplit) {
+    const float ca = cf[0], cb = cf[1];
+    const bool with_s = cb != 0.f;
+    const int nF = a.F / 64;
+    const int f_begin = (nF * split / a.nsplit) * 64, f_end = (nF * (split + 1) / a.nsplit) * 64;
+    const T* h = static_cast<const T*>(a.h_all) + ((int64_t)a.l * a.B + b) * 64 * a.F;
+    const int64_t mat = (int64_t)a.F * a.D;
+    const float* wd = a.wd + b * mat + d0;
+    const float* sd = a.sd + b * mat + d0;
+    RowStage<T, KT> hst;
+    CombColStage wst;
+    if (f_begin < f_end) {
+      hst.load(h + f_begin, a.F, 64);
+      wst.load(wd + (int64_t)f_begin * a.D, sd + (int64_t)f_begin * a.D, a.D, with_s);
+    }
+    for (int f0 = f_begin; f0 < f_end; f0 += KT) {
+      hst.template store<T>(hs, LD);
+      wst.template store<T>(ws, LD, ca, cb);
+      __syncthreads();
+      if (f0 + KT < f_end) {
+        hst.load(h + f0 + KT, a.F, 64);
+        wst.load(wd + (int64_t)(f0 + KT) * a.D, sd + (int64_t)(f0 + KT) * a.D, a.D, with_s);
+      }
+      wave_mma<T, KT>(acc, hs + wr * LD, LD, ws + wc * LD, LD);
+      __syncthreads();
+    }
+  } else {
+    for (int j = 0; j < a.l; ++j) {
+      const float gj = cf[kGam + j];
+      if (gj == 0.f) continue;
+      ColStage<T, 64> st;
+      st.load(static_cast<const T*>(a.dz_all) + ((int64_t)j * a.B + b) * 64 * a.D + d0, a.D, 64, threadIdx.x);
+      stage_scaled<T>(hs, LD, a.hh + (int64_t)b * 64 * a.LL + j * 64, a.LL, gj);
+      st.template store<T>(ws, LD);
+      __syncthreads();
+      wave_mma<T, 64>(acc, hs + wr * LD, LD, ws + wc * LD, LD);
+      __syncthreads();
+    }
+  }
+  float* zp = a.zp + (((int64_t)split * a.B + b) * 64) * a.D + d0;
+  const int col = wc + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zp[(int64_t)(wr + acc_row(i)) * a.D + col] = acc[i];
+}
+
+// ---------------------------------------------------------------------------
+// 5. dH = dZ_l (a W_down,s + b S_down,s)^T + sum_j gam_j (dZ_l dZ_j^T) H_j per F tile;
+//    dU, dG; this tile's share of <K K^T, dU dU^T + dG dG^T>.
+// ---------------------------------------------------------------------------
+struct BackArgs {
+  int B, L, C, D, F, LL, l;
+  const float* coef;
+  const void* dz_all;
+  const float* wd;
+  const float* sd;
+  const float* zz;  // (B, 64, LL): dZ_l dZ_j^T
+  const void* h_all;
+  const float* u_cur;
+  const float* g_cur;
+  const float* kk;
+  void* du_all;
+  void* dg_all;
+  float* npart;  // (B, F / 64)
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ __align__(16) T buf0[64 * LD];
+  __shared__ __align__(16) T buf1[64 * LD];
+  __shared__ __align__(16) T dus[64 * LD];  // [t][f]
+  __shared__ __align__(16) T dgs[64 * LD];
+  __shared__ float red[4];
+  const int ft = blockIdx.x, b = blockIdx.y, f0 = ft * 64;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  const float* cf = a.coef + (int64_t)b * kCoefStride;
+  const float ca = cf[0], cb = cf[1];
+  const bool with_s = cb != 0.f;
+  const T* dz = static_cast<const T*>(a.dz_all) + ((int64_t)a.l * a.B + b) * 64 * a.D;
+  const int64_t mat = (int64_t)a.F * a.D;
+  const float* wd = a.wd + b * mat + (int64_t)f0 * a.D;
+  const float* sd = a.sd + b * mat + (int64_t)f0 * a.D;
+  f32x16 acc;
+  zero(acc);
+  {
+    RowStage<T, KT> zst;
+    CombRowStage wst;
+    zst.load(dz, a.D, 64);
+    wst.load(wd, sd, a.D, with_s);
+    for (int d0 = 0; d0 < a.D; d0 += KT) {
+      zst.template store<T>(buf0, LD);
+      wst.template store<T>(buf1, LD, ca, cb);
+      __syncthreads();
+      if (d0 + KT < a.D) {
+        zst.load(dz + d0 + KT, a.D, 64);
+        wst.load(wd + d0 + KT, sd + d0 + KT, a.D, with_s);
+      }
+      wave_mma<T, KT>(acc, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
+      __syncthreads();
+    }
+  }
+  for (int j = 0; j < a.l; ++j) {
+    const float gj = cf[kGam + j];
+    if (gj == 0.f) continue;
+    ColStage<T, 64> st;
+    st.load(static_cast<const T*>(a.h_all) + ((int64_t)j * a.B + b) * 64 * a.F + f0, a.F, 64, threadIdx.x);
+    stage_scaled<T>(buf0, LD, a.zz + (int64_t)b * 64 * a.LL + j * 64, a.LL, gj);
+    st.template store<T>(buf1, LD);
+    __syncthreads();
+    wave_mma<T, 64>(acc, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
+    __syncthreads();
+  }
+  const int64_t base = (int64_t)b * 64 * a.F + f0;
+  const int64_t lbase = ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
+  const int f = wc + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = wr + acc_row(i);
+    const int64_t off = (int64_t)t * a.F + f;
+    const float u = a.u_cur[base + off], g = a.g_cur[base + off];
+    const float sg = sigmoidf_acc(g);
+    const T du = from_f32<T>(acc[i] * (g * sg));
+    const T dg = from_f32<T>(acc[i] * u * (sg * (1.0f + g * (1.0f - sg))));
+    static_cast<T*>(a.du_all)[lbase + off] = du;
+    static_cast<T*>(a.dg_all)[lbase + off] = dg;
+    dus[t * LD + f] = du;
+    dgs[t * LD + f] = dg;
+  }
+  __syncthreads();
+  f32x16 gu, gg;
+  zero(gu);
+  zero(gg);
+  wave_mma<T, 64>(gu, dus + wr * LD, LD, dus + wc * LD, LD);
+  wave_mma<T, 64>(gg, dgs + wr * LD, LD, dgs + wc * LD, LD);
+  const float* kk = a.kk + ((int64_t)b * a.LL + a.l * 64) * a.LL + a.l * 64;
+  float part = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) part += (gu[i] + gg[i]) * kk[(int64_t)(wr + acc_row(i)) * a.LL + wc + acc_col()];
+  const float total = block_sum(part, red);
+  if (threadIdx.x == 0) a.npart[(int64_t)b * (a.F / 64) + ft] = total;
+}
+
+// ---------------------------------------------------------------------------
+// 6. Per row: |g_l|^2, clip, decay, active flag, surprise; advance the recurrences.
+// ---------------------------------------------------------------------------
+struct CoefArgs {
+  int B, C, LL, l, nF;
+  float beta, max_norm, min_row_surprise;
+  const float* npart;
+  const float* hh;
+  const float* zz;
+  Acts acts;
+  const float* mask;
+  int64_t mask_rs;
+  const float* loss;  // (B, 64)
+  float* coef;
+  float* surprise;  // (L,)
+  float* row_loss;  // optional (L, B, 2)
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_chain_coef(const CoefArgs a) {
+  __shared__ float red[4];
+  __shared__ float sc[3];
+  const int b = blockIdx.x;
+  float n2 = 0.f;
+  for (int i = threadIdx.x; i < a.nF; i += kThreads) n2 += a.npart[(int64_t)b * a.nF + i];
+  const float* hh = a.hh + (int64_t)b * 64 * a.LL + a.l * 64;
+  const float* zz = a.zz + (int64_t)b * 64 * a.LL + a.l * 64;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    const int64_t off = (int64_t)(idx >> 6) * a.LL + (idx & 63);
+    n2 += hh[off] * zz[off];
+  }
+  n2 = block_sum(n2, red);
+  const int t = threadIdx.x;
+  const T* al = layer_row<T>(a.acts.alpha, a.l, b, a.acts.ea_rs);
+  float mt = 0.f, at = 0.f;
+  if (t < a.C) {
+    mt = a.mask != nullptr ? a.mask[(int64_t)b * a.mask_rs + t] : 1.f;
+    at = to_f32(al[(int64_t)t * a.acts.ea_ts]);
+  }
+  const float lt = t < 64 ? a.loss[b * 64 + t] : 0.f;
+  const float asum = block_sum(at * mt, red);
+  const float msum = block_sum(mt, red);
+  const float any = block_sum(mt != 0.f ? 1.f : 0.f, red);
+  const float lsum = block_sum(lt, red);
+  if (threadIdx.x == 0) {
+    const float denom = a.mask != nullptr ? fmaxf(msum, 1.f) : (float)a.C;
+    const float row_mean = lsum / fmaxf(a.mask != nullptr ? msum : (float)a.C, 1.f);
+    const bool gated_off = a.min_row_surprise > 0.f && row_mean < a.min_row_surprise;
+    const bool active = (a.mask == nullptr || any > 0.f) && !gated_off;
+    sc[0] = a.max_norm > 0.f ? fminf(a.max_norm * (1.0f / sqrtf(n2 + 1e-8f)), 1.0f) : 1.0f;
+    sc[1] = 1.0f - asum / denom;
+    sc[2] = active ? 1.f : 0.f;
+    if (a.row_loss != nullptr) {
+      a.row_loss[((int64_t)a.l * a.B + b) * 2] = lsum;
+      a.row_loss[((int64_t)a.l * a.B + b) * 2 + 1] = a.mask != nullptr ? msum : (float)a.C;
+    }
+  }
+  if (b == 0 && threadIdx.x >= 192) {
+    // batch-global surprise of this layer: masked token losses over all rows / valid tokens
+    const int lane = threadIdx.x - 192;
+    float num = 0.f, den = 0.f;
+    for (int i = lane; i < a.B * 64; i += 64) {
+      const int bb = i >> 6, tt = i & 63;
+      num += a.loss[i];
+      if (tt < a.C) den += a.mask != nullptr ? a.mask[(int64_t)bb * a.mask_rs + tt] : 1.f;
+    }
+    num = wave_sum(num);
+    den = wave_sum(den);
+    if (lane == 0) a.surprise[a.l] = a.mask != nullptr ? num / fmaxf(den, 1.f) : num / den;
+  }
+  __syncthreads();
+  if (sc[2] == 0.f) return;  // no tokens, or gated off: this layer leaves the row unchanged
+  const float c = sc[0], d = sc[1];
+  float* cf = a.coef + (int64_t)b * kCoefStride;
+  // read every old value before any thread writes
+  const float a_old = cf[0], b_old = cf[1], e_old = cf[2];
+  const int j = threadIdx.x;
+  const float sig_old = j < a.l ? cf[kSig + j] : 0.f;
+  const float gam_old = j < a.l ? cf[kGam + j] : 0.f;
+  __syncthreads();
+  const float e_new = a.beta * e_old;
+  if (j <= a.l) {
+    const float s_new = j < a.l ? a.beta * sig_old : -c;
+    cf[kSig + j] = s_new;
+    cf[kGam + j] = d * gam_old + s_new;
+  }
+  if (threadIdx.x == 0) {
+    cf[0] = d * a_old;
+    cf[1] = d * b_old + e_new;
+    cf[2] = e_new;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 7. Final state: W' = a W_s + b S_s + sum_j gam_j g_j, S' = e S_s + sum_j sig_j g_j per
+//    64 x 64 tile, with g_j tiles rebuilt from the small activations (K = 64 per layer).
+// ---------------------------------------------------------------------------
+struct ApplyChainArgs {
+  int B, L, C, D, F;
+  const float* coef;
+  Acts acts;
+  const void* h_all;
+  const void* du_all;
+  const void* dg_all;
+  const void* dz_all;
+  float* w[3];
+  float* s[3];
+  bf16* wc[3];  // optional bf16 copies of W'
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_chain_apply(const ApplyChainArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ __align__(16) T as[64 * LD];
+  __shared__ __align__(16) T bs[64 * LD];
+  const int nD = a.D / 64, nF = a.F / 64;
+  const int per = nD * nF;
+  const int m = blockIdx.x / per, jt = blockIdx.x - m * per, b = blockIdx.y;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  int r0, c0, ld_out;
+  if (m < 2) {
+    const int dt = jt / nF, ft = jt - dt * nF;
+    r0 = dt * 64;
+    c0 = ft * 64;
+    ld_out = a.F;
+  } else {
+    const int ft = jt / nD, dt = jt - ft * nD;
+    r0 = ft * 64;
+    c0 = dt * 64;
+    ld_out = a.D;
+  }
+  const int64_t mat = (int64_t)a.D * a.F;
+  float* wdst = a.w[m] + b * mat;
+  float* sdst = a.s[m] + b * mat;
+  const int col = c0 + wc + acc_col();
+  float wv[16], sv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
+    wv[i] = wdst[off];
+    sv[i] = sdst[off];
+  }
+  const float* cf = a.coef + (int64_t)b * kCoefStride;
+  f32x16 accw, accs;
+  zero(accw);
+  zero(accs);
+  constexpr int kUnits = ColStage<T, 64>::kUnits;
+  const bool a_part = threadIdx.x < kUnits;
+  const int unit = a_part ? (int)threadIdx.x : min((int)threadIdx.x - kUnits, kUnits);
+  const int64_t lstride_f = (int64_t)a.B * 64 * a.F, lstride_d = (int64_t)a.B * 64 * a.D;
+  for (int j = 0; j < a.L; ++j) {
+    const float gj = cf[kGam + j], sj = cf[kSig + j];
+    if (gj == 0.f && sj == 0.f) continue;
+    ColStage<T, 64> cst;
+    if (m < 2) {
+      if (a_part)
+        cst.load(layer_row<T>(a.acts.k, j, b, a.acts.kv_rs) + r0, a.acts.kv_ts, a.C, unit);
+      else
+        cst.load(static_cast<const T*>(m == 0 ? a.du_all : a.dg_all) + j * lstride_f + (int64_t)b * 64 * a.F + c0,
+                 a.F, 64, unit);
+    } else {
+      if (a_part)
+        cst.load(static_cast<const T*>(a.h_all) + j * lstride_f + (int64_t)b * 64 * a.F + r0, a.F, 64, unit);
+      else
+        cst.load(static_cast<const T*>(a.dz_all) + j * lstride_d + (int64_t)b * 64 * a.D + c0, a.D, 64, unit);
+    }
+    cst.template store<T>(a_part ? as : bs, LD);
+    __syncthreads();
+    f32x16 t;
+    zero(t);
+    wave_mma<T, 64>(t, as + wr * LD, LD, bs + wc * LD, LD);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      accw[i] += gj * t[i];
+      accs[i] += sj * t[i];
+    }
+    __syncthreads();
+  }
+  const float ca = cf[0], cb = cf[1], ce = cf[2];
+  bf16* cdst = a.wc[m] != nullptr ? a.wc[m] + b * mat : nullptr;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
+    const float w_new = ca * wv[i] + cb * sv[i] + accw[i];
+    const float s_new = ce * sv[i] + accs[i];
+    wdst[off] = w_new;
+    sdst[off] = s_new;
+    if (cdst != nullptr) cdst[off] = static_cast<bf16>(w_new);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+size_t act_size(int32_t dtype) { return dtype == UTTT_DTYPE_BF16 ? 2 : 4; }
+
+struct ChainLayout {
+  size_t pq, kk, hh, zz, h_all, du_all, dg_all, dz_all, u_cur, g_cur, zp, loss, npart, coef, total;
+  int nsplit;
+};
+
+ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dtype) {
+  ChainLayout c;
+  const size_t e = act_size(dtype);
+  const int64_t LL = L * 64, nF = F / 64;
+  int64_t s = (512 + (D / 64) * B - 1) / ((D / 64) * B);
+  c.nsplit = (int)(s < 1 ? 1 : (s > nF ? nF : s));
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t at = off; off += align_up(bytes); return at; };
+  c.pq = take(e * 4 * L * B * 64 * F);
+  c.kk = take(sizeof(float) * B * LL * LL);
+  c.hh = take(sizeof(float) * B * 64 * LL);
+  c.zz = take(sizeof(float) * B * 64 * LL);
+  c.h_all = take(e * L * B * 64 * F);
+  c.du_all = take(e * L * B * 64 * F);
+  c.dg_all = take(e * L * B * 64 * F);
+  c.dz_all = take(e * L * B * 64 * D);
+  c.u_cur = take(sizeof(float) * B * 64 * F);
+  c.g_cur = take(sizeof(float) * B * 64 * F);
+  c.zp = take(sizeof(float) * (c.nsplit + 1) * B * 64 * D);
+  c.loss = take(sizeof(float) * B * 64);
+  c.npart = take(sizeof(float) * B * nF);
+  c.coef = take(sizeof(float) * B * kCoefStride);
+  c.total = off;
+  return c;
+}
+
+template <typename T>
+void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c, hipStream_t st) {
+  const int B = (int)a.batch, L = (int)a.layers, C = (int)a.tokens, D = (int)a.d_model, F = (int)a.d_ff;
+  const int LL = L * 64, nF = F / 64;
+  const dim3 blk(kThreads);
+  Acts acts{};
+  for (int l = 0; l < L; ++l) {
+    acts.k.p[l] = a.k[l];
+    acts.v.p[l] = a.v[l];
+    acts.eta.p[l] = a.eta[l];
+    acts.alpha.p[l] = a.alpha[l];
+  }
+  acts.kv_rs = a.kv_row_stride;
+  acts.kv_ts = D;
+  acts.ea_rs = a.ea_row_stride;
+  acts.ea_ts = 1;
+  float* coef = reinterpret_cast<float*>(ws + c.coef);
+  float* kk = reinterpret_cast<float*>(ws + c.kk);
+  float* hh = reinterpret_cast<float*>(ws + c.hh);
+  float* zz = reinterpret_cast<float*>(ws + c.zz);
+  float* u_cur = reinterpret_cast<float*>(ws + c.u_cur);
+  float* g_cur = reinterpret_cast<float*>(ws + c.g_cur);
+  float* zp = reinterpret_cast<float*>(ws + c.zp);
+  float* loss = reinterpret_cast<float*>(ws + c.loss);
+  float* npart = reinterpret_cast<float*>(ws + c.npart);
+  void* h_all = ws + c.h_all;
+  void* du_all = ws + c.du_all;
+  void* dg_all = ws + c.dg_all;
+  void* dz_all = ws + c.dz_all;
+  const int64_t lf = (int64_t)B * 64 * F, ld = (int64_t)B * 64 * D;
+  const size_t e = sizeof(T);
+
+  const int ncoef = B * kCoefStride;
+  hipLaunchKernelGGL(k_chain_init, dim3((ncoef + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef);
+
+  PqArgs pa{};
+  pa.B = B; pa.L = L; pa.C = C; pa.D = D; pa.F = F; pa.acts = acts;
+  pa.x[0] = a.w_up; pa.x[1] = a.s_up; pa.x[2] = a.w_gate; pa.x[3] = a.s_gate;
+  pa.pq = ws + c.pq;
+  hipLaunchKernelGGL(k_chain_pq<T>, dim3(nF, (L + kPqGroup - 1) / kPqGroup, 4 * B), blk, 0, st, pa);
+
+  GramArgs ka{};
+  ka.B = B; ka.C = C; ka.kd = D; ka.LL = LL; ka.layer = -1; ka.rs = a.kv_row_stride; ka.ts = D;
+  ka.x = acts.k; ka.out = kk;
+  hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (L * (L + 1) / 2), B), dim3(64), 0, st, ka);
+
+  GramArgs ha{};  // H_l H_j^T and dZ_l dZ_j^T: the layer buffers have stride 64 rows per row b
+  ha.B = B; ha.C = C; ha.LL = LL;
+  GramArgs za = ha;
+  ha.kd = F; ha.rs = (int64_t)64 * F; ha.ts = F; ha.out = hh;
+  za.kd = D; za.rs = (int64_t)64 * D; za.ts = D; za.out = zz;
+  for (int l = 0; l < L; ++l) {
+    ha.x.p[l] = static_cast<char*>(h_all) + e * l * lf;
+    za.x.p[l] = static_cast<char*>(dz_all) + e * l * ld;
+  }
+
+  for (int l = 0; l < L; ++l) {
+    UpArgs ua{};
+    ua.B = B; ua.L = L; ua.C = C; ua.D = D; ua.F = F; ua.LL = LL; ua.l = l;
+    ua.coef = coef; ua.pq = ws + c.pq; ua.kk = kk; ua.du_all = du_all; ua.dg_all = dg_all;
+    ua.u_cur = u_cur; ua.g_cur = g_cur; ua.h_all = h_all;
+    hipLaunchKernelGGL(k_chain_up<T>, dim3(nF, B), blk, 0, st, ua);
+
+    ha.layer = l;
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (l + 1), B), dim3(64), 0, st, ha);
+
+    DownArgs da{};
+    da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
+    da.coef = coef; da.h_all = h_all; da.wd = a.w_down; da.sd = a.s_down; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
+    hipLaunchKernelGGL(k_chain_down<T>, dim3(D / 64, c.nsplit + (l > 0 ? 1 : 0), B), blk, 0, st, da);
+
+    LnGradArgs g{};
+    g.B = B; g.C = C; g.D = D; g.nsplit = c.nsplit + (l > 0 ? 1 : 0); g.tok_pad = 64;
+    g.normalize = a.normalize_by_dim; g.eps = a.eps; g.zp = zp;
+    g.k = a.k[l]; g.k_rs = a.kv_row_stride; g.v = a.v[l]; g.v_rs = a.kv_row_stride;
+    g.eta = a.eta[l]; g.eta_rs = a.ea_row_stride;
+    g.mask = a.token_mask; g.mask_rs = a.mask_row_stride;
+    g.ln_w = a.ln_weight; g.ln_b = a.ln_bias;
+    g.dz = static_cast<char*>(dz_all) + e * l * ld;
+    g.loss = loss;
+    hipLaunchKernelGGL(k_ln_grad<T>, dim3(64, B), blk, 0, st, g);
+
+    za.layer = l;
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (l + 1), B), dim3(64), 0, st, za);
+
+    BackArgs ba{};
+    ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
+    ba.coef = coef; ba.dz_all = dz_all; ba.wd = a.w_down; ba.sd = a.s_down; ba.zz = zz; ba.h_all = h_all;
+    ba.u_cur = u_cur; ba.g_cur = g_cur; ba.kk = kk; ba.du_all = du_all; ba.dg_all = dg_all; ba.npart = npart;
+    hipLaunchKernelGGL(k_chain_back<T>, dim3(nF, B), blk, 0, st, ba);
+
+    CoefArgs ca{};
+    ca.B = B; ca.C = C; ca.LL = LL; ca.l = l; ca.nF = nF;
+    ca.beta = a.momentum_beta; ca.max_norm = a.max_inner_grad_norm; ca.min_row_surprise = a.min_row_surprise;
+    ca.npart = npart; ca.hh = hh; ca.zz = zz; ca.acts = acts;
+    ca.mask = a.token_mask; ca.mask_rs = a.mask_row_stride; ca.loss = loss; ca.coef = coef;
+    ca.surprise = a.surprise; ca.row_loss = a.row_loss;
+    hipLaunchKernelGGL(k_chain_coef<T>, dim3(B), blk, 0, st, ca);
+  }
+
+  ApplyChainArgs aa{};
+  aa.B = B; aa.L = L; aa.C = C; aa.D = D; aa.F = F; aa.coef = coef; aa.acts = acts;
+  aa.h_all = h_all; aa.du_all = du_all; aa.dg_all = dg_all; aa.dz_all = dz_all;
+  aa.w[0] = a.w_up; aa.w[1] = a.w_gate; aa.w[2] = a.w_down;
+  aa.s[0] = a.s_up; aa.s[1] = a.s_gate; aa.s[2] = a.s_down;
+  aa.wc[0] = static_cast<bf16*>(a.w_up_copy);
+  aa.wc[1] = static_cast<bf16*>(a.w_gate_copy);
+  aa.wc[2] = static_cast<bf16*>(a.w_down_copy);
+  hipLaunchKernelGGL(k_chain_apply<T>, dim3(3 * (D / 64) * nF, B), blk, 0, st, aa);
+}
+
+int check_chain_dims(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dtype) {
+  UTTT_REQUIRE(B >= 1 && B <= 65535, "batch must be in [1, 65535] (got %lld)", (long long)B);
+  UTTT_REQUIRE(L >= 1 && L <= kMaxChain, "layers must be in [1, %d] (got %lld)", kMaxChain, (long long)L);
+  UTTT_REQUIRE(D >= 64 && D % 64 == 0 && D <= 4096, "d_model must be a multiple of 64 in [64, 4096] (got %lld)",
+               (long long)D);
+  UTTT_REQUIRE(F >= 64 && F % 64 == 0, "d_ff must be a positive multiple of 64 (got %lld)", (long long)F);
+  UTTT_REQUIRE(dtype == UTTT_DTYPE_F32 || dtype == UTTT_DTYPE_BF16, "act_dtype must be F32 or BF16 (got %d)", dtype);
+  UTTT_REQUIRE(3 * (D / 64) * (F / 64) <= 2147483647LL, "state too large");
+  return UTTT_OK;
+}
+
+}  // namespace
+
+}  // namespace uttt
+
+using namespace uttt;
+
+extern "C" size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff,
+                                             int32_t act_dtype) {
+  if (check_chain_dims(batch, layers, d_model, d_ff, act_dtype) != UTTT_OK) return 0;
+  return chain_layout(batch, layers, d_model, d_ff, act_dtype).total;
+}
+
+extern "C" int uttt_chunk_chain(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes,
+                                uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  int rc = check_chain_dims(a->batch, a->layers, a->d_model, a->d_ff, a->act_dtype);
+  if (rc != UTTT_OK) return rc;
+  UTTT_REQUIRE(a->tokens >= 1 && a->tokens <= 64, "tokens per chunk must be in [1, 64] (got %lld)",
+               (long long)a->tokens);
+  const int64_t vec = a->act_dtype == UTTT_DTYPE_BF16 ? 8 : 4;
+  for (int64_t l = 0; l < a->layers; ++l) {
+    UTTT_REQUIRE(a->k[l] && a->v[l] && a->eta[l] && a->alpha[l], "k/v/eta/alpha of layer %lld must be non-NULL",
+                 (long long)l);
+    UTTT_REQUIRE(aligned16(a->k[l]) && aligned16(a->v[l]), "k/v of layer %lld must be 16-byte aligned", (long long)l);
+  }
+  UTTT_REQUIRE(a->kv_row_stride % vec == 0, "k/v row stride must be a multiple of 16 bytes");
+  UTTT_REQUIRE(a->batch == 1 || (a->kv_row_stride >= a->tokens * a->d_model && a->ea_row_stride >= a->tokens),
+               "k/v and eta/alpha row strides must cover the chunk's tokens");
+  UTTT_REQUIRE(a->w_up && a->w_gate && a->w_down && a->s_up && a->s_gate && a->s_down, "state pointers must be non-NULL");
+  UTTT_REQUIRE(aligned16(a->w_up) && aligned16(a->w_gate) && aligned16(a->w_down) && aligned16(a->s_up) &&
+               aligned16(a->s_gate) && aligned16(a->s_down), "state pointers must be 16-byte aligned");
+  UTTT_REQUIRE(a->ln_weight && a->ln_bias && a->surprise, "ln_weight/ln_bias/surprise must be non-NULL");
+  UTTT_REQUIRE(a->momentum_beta >= 0.f && a->max_inner_grad_norm >= 0.f && a->min_row_surprise >= 0.f,
+               "momentum_beta, max_inner_grad_norm and min_row_surprise must be >= 0");
+  const ChainLayout c = chain_layout(a->batch, a->layers, a->d_model, a->d_ff, a->act_dtype);
+  UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= c.total, "workspace too small: need %zu bytes, got %zu",
+               c.total, workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  if (a->act_dtype == UTTT_DTYPE_BF16)
+    launch_chain<bf16>(*a, ws, c, st);
+  else
+    launch_chain<float>(*a, ws, c, st);
+  return launch_status("uttt_chunk_chain");
+}

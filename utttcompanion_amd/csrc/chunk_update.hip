@@ -20,6 +20,7 @@
 //   6. k_apply        recompute each gradient tile from the small activations and apply
 //                     clip / momentum / decay / inactive-row select to W and S in one pass
 // Steps 1, 2 and 4 alone are the frozen readout.
+#include "update_ln.h"
 #include "uttt_device.h"
 #include "uttt_host.h"
 
@@ -146,114 +147,8 @@ __global__ void __launch_bounds__(kThreads) k_down_partial(const FwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 3. LayerNorm, reconstruction error, token loss and dZ (K path)
+// 3. LayerNorm, reconstruction error, token loss and dZ (K path): k_ln_grad, update_ln.h
 // ---------------------------------------------------------------------------
-constexpr int kMaxPerThread = 16;  // D <= 4096
-
-struct LnGradArgs {
-  int B, C, D, nsplit, tok_pad, normalize;
-  float eps;
-  const float* zp;  // path-0 partials (nsplit, B, tok_pad, D)
-  const void* k; int64_t k_rs;
-  const void* v; int64_t v_rs;
-  const void* eta; int64_t eta_rs;
-  const float* mask; int64_t mask_rs;
-  const float* ln_w;
-  const float* ln_b;
-  void* dz;     // act dtype (B, 64, D)
-  float* loss;  // (B, 64): token loss times its mask value
-};
-
-template <typename T>
-__global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
-  __shared__ float red[4];
-  const int t = blockIdx.x, b = blockIdx.y;
-  T* dz = static_cast<T*>(a.dz) + ((int64_t)b * 64 + t) * a.D;
-  if (t >= a.C) {
-    for (int d = threadIdx.x; d < a.D; d += kThreads) dz[d] = from_f32<T>(0.f);
-    if (threadIdx.x == 0) a.loss[b * 64 + t] = 0.f;
-    return;
-  }
-  const T* kr = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs + (int64_t)t * a.D;
-  const T* vr = static_cast<const T*>(a.v) + (int64_t)b * a.v_rs + (int64_t)t * a.D;
-  const float inv_d = 1.0f / (float)a.D;
-
-  float z[kMaxPerThread];
-#pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) z[i] = 0.f;
-  for (int sp = 0; sp < a.nsplit; ++sp) {  // one round trip per split: the row's loads go out together
-    const float* src = a.zp + (((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D;
-#pragma unroll
-    for (int i = 0; i < kMaxPerThread; ++i) {
-      const int d = threadIdx.x + i * kThreads;
-      if (d < a.D) z[i] += src[d];
-    }
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) s += z[i];
-  const float mean = block_sum(s, red) * inv_d;
-  float s2 = 0.f;
-#pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
-    const int d = threadIdx.x + i * kThreads;
-    if (d < a.D) {
-      const float c = z[i] - mean;
-      s2 += c * c;
-    }
-  }
-  const float var = block_sum(s2, red) * inv_d;
-  const float rstd = 1.0f / sqrtf(var + a.eps);
-  const float inv_scale = a.normalize ? inv_d : 1.0f;
-
-  // z[] becomes z_hat, e[] the reconstruction error
-  float e[kMaxPerThread];
-  float se = 0.f;
-#pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
-    const int d = threadIdx.x + i * kThreads;
-    e[i] = 0.f;
-    if (d < a.D) {
-      z[i] = (z[i] - mean) * rstd;
-      const float vhat = to_f32(kr[d]) + (z[i] * a.ln_w[d] + a.ln_b[d]);
-      e[i] = vhat - to_f32(vr[d]);
-      se += e[i] * e[i];
-    }
-  }
-  const float token_loss = 0.5f * block_sum(se, red) * inv_scale;
-
-  const float eta_t = to_f32(static_cast<const T*>(a.eta)[(int64_t)b * a.eta_rs + t]);
-  float weight, m_t = 1.f;
-  if (a.mask != nullptr) {
-    const float* mr = a.mask + (int64_t)b * a.mask_rs;
-    m_t = mr[t];
-    float cnt = threadIdx.x < a.C ? mr[threadIdx.x] : 0.f;
-    cnt = fmaxf(block_sum(cnt, red), 1.0f);
-    weight = (eta_t * m_t) / cnt;
-  } else {
-    weight = eta_t * (1.0f / (float)a.C);
-  }
-  const float coef = weight * inv_scale;
-
-  float s3 = 0.f, s4 = 0.f;
-#pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
-    const int d = threadIdx.x + i * kThreads;
-    if (d < a.D) {
-      e[i] = coef * e[i] * a.ln_w[d];  // dZ_hat
-      s3 += e[i];
-      s4 += e[i] * z[i];
-    }
-  }
-  const float m1 = block_sum(s3, red) * inv_d;
-  const float m2 = block_sum(s4, red) * inv_d;
-#pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
-    const int d = threadIdx.x + i * kThreads;
-    if (d < a.D) dz[d] = from_f32<T>(rstd * (e[i] - m1 - z[i] * m2));
-  }
-  if (threadIdx.x == 0) a.loss[b * 64 + t] = a.mask != nullptr ? token_loss * m_t : token_loss;
-}
 
 // ---------------------------------------------------------------------------
 // 4. Readout: out = x + LN(Z) with LN parameters rounded to the activation dtype

@@ -259,6 +259,137 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
 
 
 # ---------------------------------------------------------------------------
+# one chunk, all layers (the chunk-first shared schedule, model/uttt_model.py:453-608)
+# ---------------------------------------------------------------------------
+
+class PreparedChain:
+    """A validated ``uttt_chunk_chain`` call; ``launch()`` enqueues it on the current stream."""
+
+    def __init__(self, args, keep, workspace, result, device):
+        self.args, self._keep, self.workspace, self.result, self.device = args, keep, workspace, result, device
+
+    def launch(self) -> Tuple[Tensor, Optional[Tensor]]:
+        lib = N.load_library()
+        with torch.cuda.device(self.device):
+            rc = lib.uttt_chunk_chain(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
+                                      _stream(self.device))
+        N.check(rc, "uttt_chunk_chain")
+        return self.result
+
+
+def _inplace_state(t: Tensor, name: str) -> Tensor:
+    if t.dtype != torch.float32 or not t.is_contiguous() or t.data_ptr() % 16:
+        raise ValueError(f"{name}: the layer chain updates the state in place and needs contiguous, "
+                         f"16-byte aligned fp32 tensors")
+    return t
+
+
+def prepare_chunk_chain(ks: Sequence[Tensor], vs: Sequence[Tensor], etas: Sequence[Tensor],
+                        alphas: Sequence[Tensor], state: Sequence[Tensor], ln_weight: Tensor, ln_bias: Tensor,
+                        token_mask: Optional[Tensor], momentum_beta: float, max_inner_grad_norm: float,
+                        normalize_by_dim: bool, eps: float, copies: Optional[Sequence[Tensor]] = None,
+                        surprise: Optional[Tensor] = None, row_loss: Optional[Tensor] = None,
+                        min_row_surprise: float = 0.0, workspace: Optional[Tensor] = None) -> PreparedChain:
+    """Validate and marshal the L chained layer updates of one chunk (``uttt_chunk_chain``).
+
+    ``ks[l]``/``vs[l]`` (B, C, D), ``etas[l]``/``alphas[l]`` (B, C) or (B, C, 1) are layer l's
+    update inputs; ``state`` = (w_up, w_gate, w_down, s_up, s_gate, s_down), fp32, updated in
+    place; ``copies`` optional bf16 (w_up, w_gate, w_down) tensors that receive the final W."""
+    n_layers = len(ks)
+    if not 1 <= n_layers <= N.MAX_CHAIN or not (len(vs) == len(etas) == len(alphas) == n_layers):
+        raise ValueError(f"need 1..{N.MAX_CHAIN} layers with k, v, eta and alpha each")
+    bsz, tokens, dim = ks[0].shape
+    if not 1 <= tokens <= 64:
+        raise ValueError(f"a chunk holds 1..64 tokens on the HIP path, got {tokens}")
+    act = ks[0].dtype
+    code = _act_code(act)
+    dev = ks[0].device
+    w_up, w_gate, w_down, s_up, s_gate, s_down = (_inplace_state(t, n) for t, n in zip(
+        state, ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")))
+    ff = w_up.shape[-1]
+    if w_up.shape != (bsz, dim, ff) or w_gate.shape != (bsz, dim, ff) or w_down.shape != (bsz, ff, dim) \
+            or s_up.shape != w_up.shape or s_gate.shape != w_gate.shape or s_down.shape != w_down.shape:
+        raise ValueError(f"state shapes do not match B={bsz}, D={dim}, F={ff}")
+    if dim % 64 or ff % 64 or dim > 4096:
+        raise ValueError(f"d_model and d_ff must be multiples of 64 (d_model <= 4096); got {dim}, {ff}")
+    _require_device(dev, *ks, *vs, *etas, *alphas, *state, ln_weight, ln_bias, token_mask)
+    _forward_only(*ks, *vs, *etas, *alphas, *state)
+    a = N.ChunkChainArgs()
+    keep = []
+    kv_rs = ea_rs = None
+    for l in range(n_layers):
+        k, v = ks[l], vs[l]
+        if k.shape != (bsz, tokens, dim) or v.shape != k.shape or k.dtype != act or v.dtype != act:
+            raise ValueError(f"layer {l}: k/v must be ({bsz}, {tokens}, {dim}) {act}")
+        k, v = _rows(k), _rows(v)
+        if k.stride(0) != v.stride(0) or (kv_rs is not None and k.stride(0) != kv_rs):
+            k, v = k.contiguous(), v.contiguous()
+            if kv_rs is not None and k.stride(0) != kv_rs:
+                raise ValueError("all layers' k/v must share one row stride")
+        kv_rs = k.stride(0)
+        e, al = _row_vector(etas[l], act), _row_vector(alphas[l], act)
+        if e.shape != (bsz, tokens) or al.shape != (bsz, tokens):
+            raise ValueError(f"layer {l}: eta/alpha must be ({bsz}, {tokens}) or ({bsz}, {tokens}, 1)")
+        if e.stride(0) != al.stride(0) or (ea_rs is not None and e.stride(0) != ea_rs):
+            e, al = e.contiguous(), al.contiguous()
+            if ea_rs is not None and e.stride(0) != ea_rs:
+                raise ValueError("all layers' eta/alpha must share one row stride")
+        ea_rs = e.stride(0)
+        a.k[l], a.v[l], a.eta[l], a.alpha[l] = _p(k), _p(v), _p(e), _p(al)
+        keep += [k, v, e, al]
+    mask = None
+    if token_mask is not None:
+        if token_mask.shape != (bsz, tokens):
+            raise ValueError(f"token_mask must be (B, C) = ({bsz}, {tokens})")
+        mask = token_mask.to(torch.float32)
+        if tokens > 1 and mask.stride(1) != 1:
+            mask = mask.contiguous()
+        keep.append(mask)
+    ln_w = ln_weight.to(torch.float32).contiguous()
+    ln_b = ln_bias.to(torch.float32).contiguous()
+    if ln_w.numel() != dim or ln_b.numel() != dim:
+        raise ValueError("ln_weight / ln_bias must have d_model elements")
+    if copies is not None:
+        if len(copies) != 3 or any(c.dtype != torch.bfloat16 or not c.is_contiguous() or c.shape != w.shape
+                                   or c.device != dev for c, w in zip(copies, (w_up, w_gate, w_down))):
+            raise ValueError("copies must be three contiguous bf16 tensors shaped like w_up, w_gate, w_down")
+    if surprise is None:
+        surprise = torch.empty(n_layers, dtype=torch.float32, device=dev)
+    elif surprise.shape != (n_layers,) or surprise.dtype != torch.float32 or not surprise.is_contiguous():
+        raise ValueError("surprise must be a contiguous fp32 (layers,) tensor")
+    if row_loss is not None and (row_loss.shape != (n_layers, bsz, 2) or row_loss.dtype != torch.float32
+                                 or not row_loss.is_contiguous()):
+        raise ValueError("row_loss must be a contiguous fp32 (layers, B, 2) tensor")
+    if not math.isfinite(min_row_surprise) or min_row_surprise < 0:
+        raise ValueError("min_row_surprise must be finite and >= 0")
+    lib = N.load_library()
+    nbytes = lib.uttt_chunk_chain_workspace(bsz, n_layers, dim, ff, code)
+    if nbytes == 0:
+        raise ValueError("unsupported layer chain dimensions")
+    if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    a.batch, a.layers, a.tokens, a.d_model, a.d_ff = bsz, n_layers, tokens, dim, ff
+    a.act_dtype, a.normalize_by_dim = code, int(bool(normalize_by_dim))
+    a.momentum_beta, a.max_inner_grad_norm, a.eps = float(momentum_beta), float(max_inner_grad_norm or 0.0), float(eps)
+    a.min_row_surprise = float(min_row_surprise)
+    a.kv_row_stride, a.ea_row_stride = kv_rs, ea_rs
+    a.token_mask, a.mask_row_stride = _p(mask), (mask.stride(0) if mask is not None else 0)
+    a.w_up, a.w_gate, a.w_down, a.s_up, a.s_gate, a.s_down = (_p(t) for t in
+                                                              (w_up, w_gate, w_down, s_up, s_gate, s_down))
+    a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
+    if copies is not None:
+        a.w_up_copy, a.w_gate_copy, a.w_down_copy = (_p(c) for c in copies)
+    a.surprise, a.row_loss = _p(surprise), _p(row_loss)
+    keep += [ln_w, ln_b, state, copies]
+    return PreparedChain(a, keep, workspace, (surprise, row_loss), dev)
+
+
+def chunk_chain(*args, **kwargs) -> Tuple[Tensor, Optional[Tensor]]:
+    """Run ``prepare_chunk_chain(...)`` and launch it; returns (per-layer surprise, row_loss)."""
+    return prepare_chunk_chain(*args, **kwargs).launch()
+
+
+# ---------------------------------------------------------------------------
 # frozen readout (reference swiglu_fast_forward, model/uttt_layer.py:211-247)
 # ---------------------------------------------------------------------------
 
