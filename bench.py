@@ -68,7 +68,7 @@ def parse_args():
     ap.add_argument("--phase-iters", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--sections", default="prefill,update,decode,cpu,c3,evolve",
-                    help="comma list of prefill, update, decode, cpu, c3, evolve, copyref "
+                    help="comma list of prefill, update, chain, decode, cpu, c3, evolve, copyref "
                          "(profiling runs pick a subset)")
     ap.add_argument("--c3-steps", type=int, default=2, help="timed config-3 prefills / config-5 updates")
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="tokens per row of the CPU baseline sample")
@@ -150,6 +150,42 @@ def bench_update_phases(iters: int):
         torch.cuda.synchronize()
     per = [sum(events[it][p].elapsed_time(events[it][p + 1]) for it in range(iters)) / iters for p in range(n)]
     return per, dict(B=B, C=C, D=D, F=F)
+
+
+def bench_chain(iters: int, B: int = None, L: int = None, D: int = None, F: int = None):
+    """HIP-event timing of one chunk's layer chain (``uttt_chunk_chain``) at the config-2
+    shape (8 rows, 12 layers, C 64, D 768, F 2048), bf16 activations, fp32 state in place."""
+    import torch
+    from utttcompanion_amd import kernels as K
+    B = B or C2_BATCH
+    L = L or C2["n_layers"]
+    D = D or C2["d_model"]
+    F = F or C2["d_ff_fast"]
+    C = C2["chunk_size"]
+    g = torch.Generator(device="cuda").manual_seed(9)
+    act = lambda *s: (torch.randn(*s, device="cuda", generator=g)).to(torch.bfloat16)
+    ks = [act(B, C, D) for _ in range(L)]
+    vs = [act(B, C, D) for _ in range(L)]
+    etas = [torch.full((B, C), 0.005, device="cuda").to(torch.bfloat16) for _ in range(L)]
+    alphas = [torch.full((B, C), 0.001, device="cuda").to(torch.bfloat16) for _ in range(L)]
+    state = [torch.randn(B, D, F, device="cuda", generator=g) * 0.03, torch.randn(B, D, F, device="cuda", generator=g) * 0.03,
+             torch.randn(B, F, D, device="cuda", generator=g) * 0.003]
+    state += [torch.zeros_like(t) for t in state]
+    copies = [t.to(torch.bfloat16) for t in state]
+    ln_w, ln_b = torch.ones(D, device="cuda"), torch.zeros(D, device="cuda")
+    with torch.no_grad():
+        prep = K.prepare_chunk_chain(ks, vs, etas, alphas, state, ln_w, ln_b, None, 0.9, 1.0, True, 1e-5,
+                                     copies=copies)
+        for _ in range(2):
+            prep.launch()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            prep.launch()
+        end.record()
+        torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters, dict(B=B, L=L, C=C, D=D, F=F)
 
 
 def phase_work(p: int, B: int, C: int, D: int, F: int):
@@ -424,6 +460,14 @@ def main() -> int:
         cpu = cpu_baseline(model, args.cpu_tokens, args.cpu_rows)
         log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads")
 
+    chain = None
+    if "chain" in sections:
+        ch_ms, ch_shape = bench_chain(args.phase_iters)
+        Bc, Lc, Dc, Fc = ch_shape["B"], ch_shape["L"], ch_shape["D"], ch_shape["F"]
+        chain = {"ms": round(ch_ms, 4), "shape": ch_shape, "us_per_layer": round(ch_ms * 1e3 / Lc, 2),
+                 "min_state_bytes_frac": round(48 * Dc * Fc * Bc / (ch_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        log(f"layer chain {ch_ms:.3f} ms per chunk ({ch_ms * 1e3 / Lc:.1f} us per layer)")
+
     big = {}
     if sections & {"c3", "evolve"}:
         del model
@@ -451,7 +495,7 @@ def main() -> int:
                        "seq_len": C2_SEQ, "layers": C2["n_layers"], "d_model": C2["d_model"],
                        "d_ff_fast": C2["d_ff_fast"], "window": C2["sliding_window_size"], "chunk": C2["chunk_size"],
                        "parallelism": "none (1 GPU)", "hip_graph": True, "finite": finite},
-            "roofline": roofline, "update": update, "decode": decode, **big, "cpu_baseline": cpu}
+            "roofline": roofline, "update": update, "chain": chain, "decode": decode, **big, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
     return 0
 

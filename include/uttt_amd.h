@@ -115,7 +115,12 @@ typedef struct {
   float* w_up; float* w_gate; float* w_down;        /* fp32 (B, D, F), (B, D, F), (B, F, D); in/out */
   float* s_up; float* s_gate; float* s_down;
   const float* ln_weight; const float* ln_bias;     /* (D,) fp32 */
-  void* w_up_copy; void* w_gate_copy; void* w_down_copy; /* optional bf16 copies of the final W */
+  /* optional bf16 copies of the state (bf16 activations only, all six or none): on entry they
+     hold the chunk-start state rounded to bf16 and are what the kernels read in place of the
+     fp32 masters (the reference rounds W to the activation dtype for these products); on exit
+     they hold the final state rounded to bf16 */
+  void* w_up_copy; void* w_gate_copy; void* w_down_copy;
+  void* s_up_copy; void* s_gate_copy; void* s_down_copy;
   float* surprise;                   /* (layers,) batch-global surprise of each layer */
   float* row_loss;                   /* optional (layers, batch, 2): [sum of masked token losses, valid tokens] */
 } uttt_chunk_chain_args;

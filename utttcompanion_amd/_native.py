@@ -57,6 +57,7 @@ class ChunkChainArgs(C.Structure):
         ("s_up", _P), ("s_gate", _P), ("s_down", _P),
         ("ln_weight", _P), ("ln_bias", _P),
         ("w_up_copy", _P), ("w_gate_copy", _P), ("w_down_copy", _P),
+        ("s_up_copy", _P), ("s_gate_copy", _P), ("s_down_copy", _P),
         ("surprise", _P), ("row_loss", _P),
     ]
 

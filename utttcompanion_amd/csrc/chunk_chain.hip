@@ -38,7 +38,7 @@ namespace {
 
 constexpr int KT = 64;
 constexpr int kMaxChain = UTTT_MAX_CHAIN;
-constexpr int kCoefStride = 4 + 2 * kMaxChain;  // a, b, e, -, gam[kMaxChain], sig[kMaxChain]
+constexpr int kCoefStride = 4 + 2 * kMaxChain;  // a, b, e, #updating layers, gam[], sig[]
 constexpr int kGam = 4, kSig = 4 + kMaxChain;
 constexpr int kPqGroup = 4;                      // layers per workgroup in the P/Q GEMM
 
@@ -60,27 +60,32 @@ __device__ __forceinline__ const T* layer_row(const LayerPtrs& lp, int l, int b,
   return static_cast<const T*>(lp.p[l]) + (int64_t)b * rs;
 }
 
-// stage dst[row][k] = scale * src[row * ld + k] (64 x 64, fp32 source, summed over nothing)
+// dst[row][k] = scale * (register-staged fp32 64 x 64 tile), converted to T
 template <typename T>
-__device__ __forceinline__ void stage_scaled(T* dst, int ldd, const float* src, int64_t ld, float scale) {
+__device__ __forceinline__ void store_scaled(const RowStage<float, 64>& st, T* dst, int ldd, float scale) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int idx = threadIdx.x + i * kThreads;
-    const int row = idx >> 6, c = idx & 63;
-    dst[row * ldd + c] = from_f32<T>(scale * src[(int64_t)row * ld + c]);
+  for (int j = 0; j < RowStage<float, 64>::kN; ++j) {
+    const int idx = threadIdx.x + j * kThreads;
+    const int row = idx >> 4, c = idx & 15;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dst[row * ldd + c * 4 + v] = from_f32<T>(scale * Lanes16<float>::get(st.r[j], v));
   }
 }
 
-// Register-staged K x 64 (KT rows) tile of ca * X + cb * Y (fp32 sources), transposed to [col][k].
+// Register-staged KT x 64 tile (KT source rows) of ca * X + cb * Y, source type S (fp32
+// masters or their bf16 copies), transposed to [col][k].  One unit: 8 rows x 16 bytes.
+template <typename S>
 struct CombColStage {
-  static constexpr int kUnits = (KT / 8) * 16;  // 128: 8 rows x 4 floats per unit
+  static constexpr int kVec = Lanes16<S>::kVec;
+  static constexpr int kColGroups = 64 / kVec;
+  static constexpr int kUnits = (KT / 8) * kColGroups;  // 128 (fp32) or 64 (bf16)
   uint4 rx[8], ry[8];
-  __device__ __forceinline__ void load(const float* x, const float* y, int64_t ld, bool with_y) {
+  __device__ __forceinline__ void load(const S* x, const S* y, int64_t ld, bool with_y) {
     if (threadIdx.x >= kUnits) return;
-    const int kg = threadIdx.x >> 4, cg = threadIdx.x & 15;
+    const int kg = threadIdx.x / kColGroups, cg = threadIdx.x % kColGroups;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int64_t off = (int64_t)(kg * 8 + i) * ld + cg * 4;
+      const int64_t off = (int64_t)(kg * 8 + i) * ld + cg * kVec;
       rx[i] = *reinterpret_cast<const uint4*>(x + off);
       ry[i] = with_y ? *reinterpret_cast<const uint4*>(y + off) : make_uint4(0u, 0u, 0u, 0u);
     }
@@ -88,27 +93,30 @@ struct CombColStage {
   template <typename T>
   __device__ __forceinline__ void store(T* dst, int ldd, float ca, float cb) const {
     if (threadIdx.x >= kUnits) return;
-    const int kg = threadIdx.x >> 4, cg = threadIdx.x & 15;
+    const int kg = threadIdx.x / kColGroups, cg = threadIdx.x % kColGroups;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      T* d = dst + (cg * 4 + v) * ldd + kg * 8;
+    for (int v = 0; v < kVec; ++v) {
+      T* d = dst + (cg * kVec + v) * ldd + kg * 8;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        d[i] = from_f32<T>(ca * Lanes16<float>::get(rx[i], v) + cb * Lanes16<float>::get(ry[i], v));
+        d[i] = from_f32<T>(ca * Lanes16<S>::get(rx[i], v) + cb * Lanes16<S>::get(ry[i], v));
     }
   }
 };
 
-// Register-staged 64 x KT tile of ca * X + cb * Y (fp32 sources, row-major), LDS [row][k].
+// Register-staged 64 x KT tile of ca * X + cb * Y (row-major source of type S), LDS [row][k].
+template <typename S>
 struct CombRowStage {
-  static constexpr int kN = 64 * (KT / 4) / kThreads;  // 4
+  static constexpr int kVec = Lanes16<S>::kVec;
+  static constexpr int kPerRow = KT / kVec;
+  static constexpr int kN = 64 * kPerRow / kThreads;  // 4 (fp32) or 2 (bf16)
   uint4 rx[kN], ry[kN];
-  __device__ __forceinline__ void load(const float* x, const float* y, int64_t ld, bool with_y) {
+  __device__ __forceinline__ void load(const S* x, const S* y, int64_t ld, bool with_y) {
 #pragma unroll
     for (int j = 0; j < kN; ++j) {
       const int idx = threadIdx.x + j * kThreads;
-      const int row = idx >> 4, c = idx & 15;
-      const int64_t off = (int64_t)row * ld + c * 4;
+      const int row = idx / kPerRow, c = idx % kPerRow;
+      const int64_t off = (int64_t)row * ld + c * kVec;
       rx[j] = *reinterpret_cast<const uint4*>(x + off);
       ry[j] = with_y ? *reinterpret_cast<const uint4*>(y + off) : make_uint4(0u, 0u, 0u, 0u);
     }
@@ -118,11 +126,11 @@ struct CombRowStage {
 #pragma unroll
     for (int j = 0; j < kN; ++j) {
       const int idx = threadIdx.x + j * kThreads;
-      const int row = idx >> 4, c = idx & 15;
+      const int row = idx / kPerRow, c = idx % kPerRow;
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        dst[row * ldd + c * 4 + v] =
-            from_f32<T>(ca * Lanes16<float>::get(rx[j], v) + cb * Lanes16<float>::get(ry[j], v));
+      for (int v = 0; v < kVec; ++v)
+        dst[row * ldd + c * kVec + v] =
+            from_f32<T>(ca * Lanes16<S>::get(rx[j], v) + cb * Lanes16<S>::get(ry[j], v));
     }
   }
 };
@@ -144,11 +152,11 @@ __global__ void __launch_bounds__(kThreads) k_chain_init(float* coef, int n) {
 struct PqArgs {
   int B, L, C, D, F;
   Acts acts;
-  const float* x[4];
+  const void* x[4];  // fp32 state or its bf16 copies
   void* pq;  // (4, L, B, 64, F) act dtype
 };
 
-template <typename T>
+template <typename T, typename WT>
 __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T bs[64 * LD];
@@ -157,13 +165,13 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
   const int f0 = ft * 64, l0 = blockIdx.y * kPqGroup;
   const int nl = min(kPqGroup, a.L - l0);
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
-  const float* xs = a.x[m] + (int64_t)b * a.D * a.F + f0;
+  const WT* xs = static_cast<const WT*>(a.x[m]) + (int64_t)b * a.D * a.F + f0;
   const T* kr[kPqGroup];
 #pragma unroll
   for (int g = 0; g < kPqGroup; ++g)
     kr[g] = layer_row<T>(a.acts.k, g < nl ? l0 + g : l0, b, a.acts.kv_rs);
 
-  ColStage<float, KT> xst;
+  ColStage<WT, KT> xst;
   RowStage<T, KT> kst[kPqGroup];
   xst.load(xs, a.F, KT, threadIdx.x);
 #pragma unroll
@@ -212,8 +220,11 @@ struct GramArgs {
   float* out;
 };
 
+// One 32 x 32 quadrant per workgroup; the 4 waves take a quarter of the feature range each
+// and their partial sums meet in LDS.
 template <typename T>
-__global__ void __launch_bounds__(64) k_chain_gram(const GramArgs a) {
+__global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
+  __shared__ float part[3 * 16 * 64];
   const int q = blockIdx.x & 3;  // 32 x 32 quadrant of the 64 x 64 block
   const int blk = blockIdx.x >> 2, b = blockIdx.y;
   int l, j;
@@ -226,37 +237,57 @@ __global__ void __launch_bounds__(64) k_chain_gram(const GramArgs a) {
     while (l * (l + 1) / 2 > blk) --l;
     j = blk - l * (l + 1) / 2;
   }
-  const int lane = threadIdx.x, r = lane & 31, h = lane >> 5;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
   const int ti = (q >> 1) * 32 + r, tj = (q & 1) * 32 + r;
+  const int kq = a.kd / 4, kb = wave * kq, ke = kb + kq;
   const T* xa = layer_row<T>(a.x, l, b, a.rs) + (int64_t)ti * a.ts;
   const T* xb = layer_row<T>(a.x, j, b, a.rs) + (int64_t)tj * a.ts;
   const bool va = ti < a.C, vb = tj < a.C;
   f32x16 acc;
   zero(acc);
   if constexpr (sizeof(T) == 2) {
-    for (int k0 = 0; k0 < a.kd; k0 += 16) {
-      bf16x8 av, bv;
-      const uint4 ra = va ? *reinterpret_cast<const uint4*>(xa + k0 + h * 8) : make_uint4(0u, 0u, 0u, 0u);
-      const uint4 rb = vb ? *reinterpret_cast<const uint4*>(xb + k0 + h * 8) : make_uint4(0u, 0u, 0u, 0u);
-      av = *reinterpret_cast<const bf16x8*>(&ra);
-      bv = *reinterpret_cast<const bf16x8*>(&rb);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+    for (int k0 = kb; k0 < ke; k0 += 128) {  // kq is a multiple of 16; 8 steps of 16 in flight
+      uint4 ra[8], rb[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const bool in = k0 + u * 16 < ke;
+        ra[u] = va && in ? *reinterpret_cast<const uint4*>(xa + k0 + u * 16 + h * 8) : make_uint4(0u, 0u, 0u, 0u);
+        rb[u] = vb && in ? *reinterpret_cast<const uint4*>(xb + k0 + u * 16 + h * 8) : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(&ra[u]),
+                                                      *reinterpret_cast<const bf16x8*>(&rb[u]), acc, 0, 0, 0);
     }
   } else {
-    for (int k0 = 0; k0 < a.kd; k0 += 8) {
-      const f32x4 av = va ? *reinterpret_cast<const f32x4*>(xa + k0 + h * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 bv = vb ? *reinterpret_cast<const f32x4*>(xb + k0 + h * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = kb; k0 < ke; k0 += 32) {  // 4 groups of 8 (each lane 4 consecutive k)
+      f32x4 av[4], bv[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc, 0, 0, 0);
+      for (int u = 0; u < 4; ++u) {
+        const bool in = k0 + u * 8 < ke;
+        av[u] = va && in ? *reinterpret_cast<const f32x4*>(xa + k0 + u * 8 + h * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        bv[u] = vb && in ? *reinterpret_cast<const f32x4*>(xb + k0 + u * 8 + h * 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u][e], bv[u][e], acc, 0, 0, 0);
     }
   }
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) part[((wave - 1) * 16 + i) * 64 + lane] = acc[i];
+  }
+  __syncthreads();
+  if (wave != 0) return;
   float* out = a.layer >= 0 ? a.out + (int64_t)b * 64 * a.LL
                             : a.out + ((int64_t)b * a.LL + l * 64) * a.LL;
   const int c = j * 64 + (q & 1) * 32 + r;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
+    const float v = acc[i] + part[i * 64 + lane] + part[(16 + i) * 64 + lane] + part[(32 + i) * 64 + lane];
     const int row = (q >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-    out[(int64_t)row * a.LL + c] = acc[i];
+    out[(int64_t)row * a.LL + c] = v;
   }
 }
 
@@ -278,46 +309,66 @@ struct UpArgs {
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_chain_up(const UpArgs a) {
   constexpr int LD = lds_ld<T>();
-  __shared__ __align__(16) T as[64 * LD];
-  __shared__ __align__(16) T bu[64 * LD];
-  __shared__ __align__(16) T bg[64 * LD];
+  __shared__ __align__(16) T as[2][64 * LD];
+  __shared__ __align__(16) T bu[2][64 * LD];
+  __shared__ __align__(16) T bg[2][64 * LD];
   const int ft = blockIdx.x, b = blockIdx.y, f0 = ft * 64;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const float* cf = a.coef + (int64_t)b * kCoefStride;
   const float ca = cf[0], cb = cf[1];
-  f32x16 au, ag;
-  zero(au);
-  zero(ag);
-  constexpr int U = ColStage<T, 64>::kUnits;
-  const bool up_half = threadIdx.x < U;
-  const int unit = up_half ? (int)threadIdx.x : min((int)threadIdx.x - U, U);
-  for (int j = 0; j < a.l; ++j) {
-    const float gj = cf[kGam + j];
-    if (gj == 0.f) continue;
-    const int64_t tile = ((int64_t)j * a.B + b) * 64 * a.F + f0;
-    ColStage<T, 64> st;
-    st.load(static_cast<const T*>(up_half ? a.du_all : a.dg_all) + tile, a.F, 64, unit);
-    stage_scaled<T>(as, LD, a.kk + ((int64_t)b * a.LL + a.l * 64) * a.LL + j * 64, a.LL, gj);
-    st.template store<T>(up_half ? bu : bg, LD);
-    __syncthreads();
-    wave_mma<T, 64>(au, as + wr * LD, LD, bu + wc * LD, LD);
-    wave_mma<T, 64>(ag, as + wr * LD, LD, bg + wc * LD, LD);
-    __syncthreads();
-  }
-  const int64_t lane_base = (int64_t)b * 64 * a.F + f0;
+  // the snapshot products of this tile: loads issued before the correction loop
   const int64_t plane = (int64_t)a.L * a.B * 64 * a.F;
   const T* pl = static_cast<const T*>(a.pq) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
-  T* h = static_cast<T*>(a.h_all) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
   const int col = wc + acc_col();
+  float pu[16], pg[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
-    float u = ca * to_f32(pl[off]) + au[i];
-    float g = ca * to_f32(pl[2 * plane + off]) + ag[i];
-    if (cb != 0.f) {
-      u += cb * to_f32(pl[plane + off]);
-      g += cb * to_f32(pl[3 * plane + off]);
+    pu[i] = ca * to_f32(pl[off]);
+    pg[i] = ca * to_f32(pl[2 * plane + off]);
+  }
+  if (cb != 0.f) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
+      pu[i] += cb * to_f32(pl[plane + off]);
+      pg[i] += cb * to_f32(pl[3 * plane + off]);
     }
+  }
+  f32x16 au, ag;
+  zero(au);
+  zero(ag);
+  if (a.l > 0) {
+    constexpr int U = ColStage<T, 64>::kUnits;
+    const bool up_half = threadIdx.x < U;
+    const int unit = up_half ? (int)threadIdx.x : min((int)threadIdx.x - U, U);
+    const T* dsrc = static_cast<const T*>(up_half ? a.du_all : a.dg_all) + (int64_t)b * 64 * a.F + f0;
+    const int64_t lstride = (int64_t)a.B * 64 * a.F;
+    const float* kk = a.kk + ((int64_t)b * a.LL + a.l * 64) * a.LL;
+    RowStage<float, 64> kst;
+    ColStage<T, 64> st;
+    kst.load(kk, a.LL, 64);
+    st.load(dsrc, a.F, 64, unit);
+    for (int j = 0; j < a.l; ++j) {
+      const int buf = j & 1;
+      store_scaled<T>(kst, as[buf], LD, cf[kGam + j]);
+      st.template store<T>(up_half ? bu[buf] : bg[buf], LD);
+      __syncthreads();
+      if (j + 1 < a.l) {
+        kst.load(kk + (j + 1) * 64, a.LL, 64);
+        st.load(dsrc + (j + 1) * lstride, a.F, 64, unit);
+      }
+      wave_mma<T, 64>(au, as[buf] + wr * LD, LD, bu[buf] + wc * LD, LD);
+      wave_mma<T, 64>(ag, as[buf] + wr * LD, LD, bg[buf] + wc * LD, LD);
+    }
+  }
+  const int64_t lane_base = (int64_t)b * 64 * a.F + f0;
+  T* h = static_cast<T*>(a.h_all) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
+    const float u = pu[i] + au[i];
+    const float g = pg[i] + ag[i];
     a.u_cur[lane_base + off] = u;
     a.g_cur[lane_base + off] = g;
     h[off] = from_f32<T>((g * sigmoidf_acc(g)) * u);
@@ -332,18 +383,20 @@ struct DownArgs {
   int B, L, C, D, F, LL, l, nsplit;
   const float* coef;
   const void* h_all;
-  const float* wd;
-  const float* sd;  // (B, F, D)
+  const void* wd;
+  const void* sd;  // (B, F, D): fp32 state or its bf16 copies
   const float* hh;  // (B, 64, LL): H_l H_j^T
   const void* dz_all;  // (L, B, 64, D)
-  float* zp;           // (nsplit + 1, B, 64, D)
+  float* zp;           // (nsplit + correction splits, B, 64, D)
 };
 
-template <typename T>
+constexpr int kCorrPerSplit = 2;  // layers j per correction split
+
+template <typename T, typename WT>
 __global__ void __launch_bounds__(kThreads) k_chain_down(const DownArgs a) {
   constexpr int LD = lds_ld<T>();
-  __shared__ __align__(16) T hs[64 * LD];
-  __shared__ __align__(16) T ws[64 * LD];
+  __shared__ __align__(16) T hs[2][64 * LD];
+  __shared__ __align__(16) T ws[2][64 * LD];
   const int dt = blockIdx.x, split = blockIdx.y, b = blockIdx.z, d0 = dt * 64;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const float* cf = a.coef + (int64_t)b * kCoefStride;
@@ -356,36 +409,47 @@ __global__ void __launch_bounds__(kThreads) k_chain_down(const DownArgs a) {
     const int f_begin = (nF * split / a.nsplit) * 64, f_end = (nF * (split + 1) / a.nsplit) * 64;
     const T* h = static_cast<const T*>(a.h_all) + ((int64_t)a.l * a.B + b) * 64 * a.F;
     const int64_t mat = (int64_t)a.F * a.D;
-    const float* wd = a.wd + b * mat + d0;
-    const float* sd = a.sd + b * mat + d0;
+    const WT* wd = static_cast<const WT*>(a.wd) + b * mat + d0;
+    const WT* sd = static_cast<const WT*>(a.sd) + b * mat + d0;
     RowStage<T, KT> hst;
-    CombColStage wst;
+    CombColStage<WT> wst;
     if (f_begin < f_end) {
       hst.load(h + f_begin, a.F, 64);
       wst.load(wd + (int64_t)f_begin * a.D, sd + (int64_t)f_begin * a.D, a.D, with_s);
     }
-    for (int f0 = f_begin; f0 < f_end; f0 += KT) {
-      hst.template store<T>(hs, LD);
-      wst.template store<T>(ws, LD, ca, cb);
+    int buf = 0;
+    for (int f0 = f_begin; f0 < f_end; f0 += KT, buf ^= 1) {
+      hst.template store<T>(hs[buf], LD);
+      wst.template store<T>(ws[buf], LD, ca, cb);
       __syncthreads();
       if (f0 + KT < f_end) {
         hst.load(h + f0 + KT, a.F, 64);
         wst.load(wd + (int64_t)(f0 + KT) * a.D, sd + (int64_t)(f0 + KT) * a.D, a.D, with_s);
       }
-      wave_mma<T, KT>(acc, hs + wr * LD, LD, ws + wc * LD, LD);
-      __syncthreads();
+      wave_mma<T, KT>(acc, hs[buf] + wr * LD, LD, ws[buf] + wc * LD, LD);
     }
   } else {
-    for (int j = 0; j < a.l; ++j) {
-      const float gj = cf[kGam + j];
-      if (gj == 0.f) continue;
-      ColStage<T, 64> st;
-      st.load(static_cast<const T*>(a.dz_all) + ((int64_t)j * a.B + b) * 64 * a.D + d0, a.D, 64, threadIdx.x);
-      stage_scaled<T>(hs, LD, a.hh + (int64_t)b * 64 * a.LL + j * 64, a.LL, gj);
-      st.template store<T>(ws, LD);
+    const int j_begin = (split - a.nsplit) * kCorrPerSplit;
+    const int j_end = min(a.l, j_begin + kCorrPerSplit);
+    const T* dsrc = static_cast<const T*>(a.dz_all) + (int64_t)b * 64 * a.D + d0;
+    const int64_t lstride = (int64_t)a.B * 64 * a.D;
+    const float* hh = a.hh + (int64_t)b * 64 * a.LL;
+    RowStage<float, 64> hst;
+    ColStage<T, 64> st;
+    if (j_begin < j_end) {
+      hst.load(hh + j_begin * 64, a.LL, 64);
+      st.load(dsrc + j_begin * lstride, a.D, 64, threadIdx.x);
+    }
+    for (int j = j_begin; j < j_end; ++j) {
+      const int buf = (j - j_begin) & 1;
+      store_scaled<T>(hst, hs[buf], LD, cf[kGam + j]);
+      st.template store<T>(ws[buf], LD);
       __syncthreads();
-      wave_mma<T, 64>(acc, hs + wr * LD, LD, ws + wc * LD, LD);
-      __syncthreads();
+      if (j + 1 < j_end) {
+        hst.load(hh + (j + 1) * 64, a.LL, 64);
+        st.load(dsrc + (j + 1) * lstride, a.D, 64, threadIdx.x);
+      }
+      wave_mma<T, 64>(acc, hs[buf] + wr * LD, LD, ws[buf] + wc * LD, LD);
     }
   }
   float* zp = a.zp + (((int64_t)split * a.B + b) * 64) * a.D + d0;
@@ -402,8 +466,8 @@ struct BackArgs {
   int B, L, C, D, F, LL, l;
   const float* coef;
   const void* dz_all;
-  const float* wd;
-  const float* sd;
+  const void* wd;
+  const void* sd;   // fp32 state or its bf16 copies
   const float* zz;  // (B, 64, LL): dZ_l dZ_j^T
   const void* h_all;
   const float* u_cur;
@@ -414,7 +478,7 @@ struct BackArgs {
   float* npart;  // (B, F / 64)
 };
 
-template <typename T>
+template <typename T, typename WT>
 __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T buf0[64 * LD];
@@ -429,13 +493,13 @@ __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
   const bool with_s = cb != 0.f;
   const T* dz = static_cast<const T*>(a.dz_all) + ((int64_t)a.l * a.B + b) * 64 * a.D;
   const int64_t mat = (int64_t)a.F * a.D;
-  const float* wd = a.wd + b * mat + (int64_t)f0 * a.D;
-  const float* sd = a.sd + b * mat + (int64_t)f0 * a.D;
+  const WT* wd = static_cast<const WT*>(a.wd) + b * mat + (int64_t)f0 * a.D;
+  const WT* sd = static_cast<const WT*>(a.sd) + b * mat + (int64_t)f0 * a.D;
   f32x16 acc;
   zero(acc);
   {
     RowStage<T, KT> zst;
-    CombRowStage wst;
+    CombRowStage<WT> wst;
     zst.load(dz, a.D, 64);
     wst.load(wd, sd, a.D, with_s);
     for (int d0 = 0; d0 < a.D; d0 += KT) {
@@ -450,16 +514,27 @@ __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
       __syncthreads();
     }
   }
-  for (int j = 0; j < a.l; ++j) {
-    const float gj = cf[kGam + j];
-    if (gj == 0.f) continue;
+  if (a.l > 0) {  // sum_j gam_j (dZ_l dZ_j^T) H_j, double-buffered through dus / dgs
+    const T* hsrc = static_cast<const T*>(a.h_all) + (int64_t)b * 64 * a.F + f0;
+    const int64_t lstride = (int64_t)a.B * 64 * a.F;
+    const float* zz = a.zz + (int64_t)b * 64 * a.LL;
+    RowStage<float, 64> zst;
     ColStage<T, 64> st;
-    st.load(static_cast<const T*>(a.h_all) + ((int64_t)j * a.B + b) * 64 * a.F + f0, a.F, 64, threadIdx.x);
-    stage_scaled<T>(buf0, LD, a.zz + (int64_t)b * 64 * a.LL + j * 64, a.LL, gj);
-    st.template store<T>(buf1, LD);
-    __syncthreads();
-    wave_mma<T, 64>(acc, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
-    __syncthreads();
+    zst.load(zz, a.LL, 64);
+    st.load(hsrc, a.F, 64, threadIdx.x);
+    for (int j = 0; j < a.l; ++j) {
+      T* abuf = (j & 1) ? dus : buf0;
+      T* bbuf = (j & 1) ? dgs : buf1;
+      store_scaled<T>(zst, abuf, LD, cf[kGam + j]);
+      st.template store<T>(bbuf, LD);
+      __syncthreads();
+      if (j + 1 < a.l) {
+        zst.load(zz + (j + 1) * 64, a.LL, 64);
+        st.load(hsrc + (j + 1) * lstride, a.F, 64, threadIdx.x);
+      }
+      wave_mma<T, 64>(acc, abuf + wr * LD, LD, bbuf + wc * LD, LD);
+    }
+    __syncthreads();  // dus / dgs are rewritten below
   }
   const int64_t base = (int64_t)b * 64 * a.F + f0;
   const int64_t lbase = ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
@@ -583,6 +658,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_coef(const CoefArgs a) {
     cf[0] = d * a_old;
     cf[1] = d * b_old + e_new;
     cf[2] = e_new;
+    cf[3] += 1.f;
   }
 }
 
@@ -600,18 +676,22 @@ struct ApplyChainArgs {
   const void* dz_all;
   float* w[3];
   float* s[3];
-  bf16* wc[3];  // optional bf16 copies of W'
+  bf16* wc[3];  // optional bf16 copies of W' and S'
+  bf16* sc[3];
 };
 
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_chain_apply(const ApplyChainArgs a) {
   constexpr int LD = lds_ld<T>();
-  __shared__ __align__(16) T as[64 * LD];
-  __shared__ __align__(16) T bs[64 * LD];
+  __shared__ __align__(16) T as[2][64 * LD];
+  __shared__ __align__(16) T bs[2][64 * LD];
   const int nD = a.D / 64, nF = a.F / 64;
   const int per = nD * nF;
   const int m = blockIdx.x / per, jt = blockIdx.x - m * per, b = blockIdx.y;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  const float* cf = a.coef + (int64_t)b * kCoefStride;
+  const float ca = cf[0], cb = cf[1], ce = cf[2];
+  if (cf[3] == 0.f) return;  // no layer updated this row: W and S stay as they are
   int r0, c0, ld_out;
   if (m < 2) {
     const int dt = jt / nF, ft = jt - dt * nF;
@@ -628,59 +708,76 @@ __global__ void __launch_bounds__(kThreads) k_chain_apply(const ApplyChainArgs a
   float* wdst = a.w[m] + b * mat;
   float* sdst = a.s[m] + b * mat;
   const int col = c0 + wc + acc_col();
-  float wv[16], sv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
-    wv[i] = wdst[off];
-    sv[i] = sdst[off];
-  }
-  const float* cf = a.coef + (int64_t)b * kCoefStride;
-  f32x16 accw, accs;
-  zero(accw);
-  zero(accs);
+  // operand sources of layer j: A^T rows are tokens (k), columns this tile's rows
   constexpr int kUnits = ColStage<T, 64>::kUnits;
   const bool a_part = threadIdx.x < kUnits;
   const int unit = a_part ? (int)threadIdx.x : min((int)threadIdx.x - kUnits, kUnits);
-  const int64_t lstride_f = (int64_t)a.B * 64 * a.F, lstride_d = (int64_t)a.B * 64 * a.D;
-  for (int j = 0; j < a.L; ++j) {
-    const float gj = cf[kGam + j], sj = cf[kSig + j];
-    if (gj == 0.f && sj == 0.f) continue;
-    ColStage<T, 64> cst;
-    if (m < 2) {
-      if (a_part)
-        cst.load(layer_row<T>(a.acts.k, j, b, a.acts.kv_rs) + r0, a.acts.kv_ts, a.C, unit);
-      else
-        cst.load(static_cast<const T*>(m == 0 ? a.du_all : a.dg_all) + j * lstride_f + (int64_t)b * 64 * a.F + c0,
-                 a.F, 64, unit);
+  const T* src;
+  int64_t src_ld, src_lstride;
+  int k_valid;
+  if (m < 2) {
+    if (a_part) {
+      src = layer_row<T>(a.acts.k, 0, b, a.acts.kv_rs) + r0;
+      src_ld = a.acts.kv_ts;
+      src_lstride = 0;  // per-layer pointers
+      k_valid = a.C;
     } else {
-      if (a_part)
-        cst.load(static_cast<const T*>(a.h_all) + j * lstride_f + (int64_t)b * 64 * a.F + r0, a.F, 64, unit);
-      else
-        cst.load(static_cast<const T*>(a.dz_all) + j * lstride_d + (int64_t)b * 64 * a.D + c0, a.D, 64, unit);
+      src = static_cast<const T*>(m == 0 ? a.du_all : a.dg_all) + (int64_t)b * 64 * a.F + c0;
+      src_ld = a.F;
+      src_lstride = (int64_t)a.B * 64 * a.F;
+      k_valid = 64;
     }
-    cst.template store<T>(a_part ? as : bs, LD);
+  } else {
+    src = a_part ? static_cast<const T*>(a.h_all) + (int64_t)b * 64 * a.F + r0
+                 : static_cast<const T*>(a.dz_all) + (int64_t)b * 64 * a.D + c0;
+    src_ld = a_part ? a.F : a.D;
+    src_lstride = a_part ? (int64_t)a.B * 64 * a.F : (int64_t)a.B * 64 * a.D;
+    k_valid = 64;
+  }
+  const bool per_layer_ptr = m < 2 && a_part;
+  auto layer_src = [&](int j) -> const T* {
+    return per_layer_ptr ? layer_row<T>(a.acts.k, j, b, a.acts.kv_rs) + r0 : src + j * src_lstride;
+  };
+  f32x16 accw, accs;
+  zero(accw);
+  zero(accs);
+  ColStage<T, 64> cst;
+  cst.load(layer_src(0), src_ld, k_valid, unit);
+  for (int j = 0; j < a.L; ++j) {
+    const int buf = j & 1;
+    cst.template store<T>(a_part ? as[buf] : bs[buf], LD);
     __syncthreads();
+    if (j + 1 < a.L) cst.load(layer_src(j + 1), src_ld, k_valid, unit);
     f32x16 t;
     zero(t);
-    wave_mma<T, 64>(t, as + wr * LD, LD, bs + wc * LD, LD);
+    wave_mma<T, 64>(t, as[buf] + wr * LD, LD, bs[buf] + wc * LD, LD);
+    const float gj = cf[kGam + j], sj = cf[kSig + j];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       accw[i] += gj * t[i];
       accs[i] += sj * t[i];
     }
-    __syncthreads();
   }
-  const float ca = cf[0], cb = cf[1], ce = cf[2];
-  bf16* cdst = a.wc[m] != nullptr ? a.wc[m] + b * mat : nullptr;
+  bf16* cw = a.wc[m] != nullptr ? a.wc[m] + b * mat : nullptr;
+  bf16* cs = a.sc[m] != nullptr ? a.sc[m] + b * mat : nullptr;
+  float* wrow = wdst + (int64_t)(r0 + wr) * ld_out + col;
+  float* srow = sdst + (int64_t)(r0 + wr) * ld_out + col;
+  float wv[16], sv[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
+    wv[i] = wrow[(int64_t)acc_row(i) * ld_out];
+    sv[i] = srow[(int64_t)acc_row(i) * ld_out];
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)acc_row(i) * ld_out;
     const float w_new = ca * wv[i] + cb * sv[i] + accw[i];
     const float s_new = ce * sv[i] + accs[i];
-    wdst[off] = w_new;
-    sdst[off] = s_new;
-    if (cdst != nullptr) cdst[off] = static_cast<bf16>(w_new);
+    wrow[off] = w_new;
+    srow[off] = s_new;
+    const int64_t coff = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
+    if (cw != nullptr) cw[coff] = static_cast<bf16>(w_new);
+    if (cs != nullptr) cs[coff] = static_cast<bf16>(s_new);
   }
 }
 
@@ -712,7 +809,7 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
   c.dz_all = take(e * L * B * 64 * D);
   c.u_cur = take(sizeof(float) * B * 64 * F);
   c.g_cur = take(sizeof(float) * B * 64 * F);
-  c.zp = take(sizeof(float) * (c.nsplit + 1) * B * 64 * D);
+  c.zp = take(sizeof(float) * (c.nsplit + (L - 1 + kCorrPerSplit - 1) / kCorrPerSplit + 1) * B * 64 * D);
   c.loss = take(sizeof(float) * B * 64);
   c.npart = take(sizeof(float) * B * nF);
   c.coef = take(sizeof(float) * B * kCoefStride);
@@ -755,16 +852,28 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   const int ncoef = B * kCoefStride;
   hipLaunchKernelGGL(k_chain_init, dim3((ncoef + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef);
 
+  // the chunk-start state the bf16 kernels read: its bf16 copies when given, else the masters
+  const bool bf16_src = a.w_up_copy != nullptr;
   PqArgs pa{};
   pa.B = B; pa.L = L; pa.C = C; pa.D = D; pa.F = F; pa.acts = acts;
-  pa.x[0] = a.w_up; pa.x[1] = a.s_up; pa.x[2] = a.w_gate; pa.x[3] = a.s_gate;
+  if (bf16_src) {
+    pa.x[0] = a.w_up_copy; pa.x[1] = a.s_up_copy; pa.x[2] = a.w_gate_copy; pa.x[3] = a.s_gate_copy;
+  } else {
+    pa.x[0] = a.w_up; pa.x[1] = a.s_up; pa.x[2] = a.w_gate; pa.x[3] = a.s_gate;
+  }
   pa.pq = ws + c.pq;
-  hipLaunchKernelGGL(k_chain_pq<T>, dim3(nF, (L + kPqGroup - 1) / kPqGroup, 4 * B), blk, 0, st, pa);
+  const dim3 pq_grid(nF, (L + kPqGroup - 1) / kPqGroup, 4 * B);
+  if (bf16_src)
+    hipLaunchKernelGGL((k_chain_pq<T, bf16>), pq_grid, blk, 0, st, pa);
+  else
+    hipLaunchKernelGGL((k_chain_pq<T, float>), pq_grid, blk, 0, st, pa);
+  const void* wd_src = bf16_src ? a.w_down_copy : static_cast<const void*>(a.w_down);
+  const void* sd_src = bf16_src ? a.s_down_copy : static_cast<const void*>(a.s_down);
 
   GramArgs ka{};
   ka.B = B; ka.C = C; ka.kd = D; ka.LL = LL; ka.layer = -1; ka.rs = a.kv_row_stride; ka.ts = D;
   ka.x = acts.k; ka.out = kk;
-  hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (L * (L + 1) / 2), B), dim3(64), 0, st, ka);
+  hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (L * (L + 1) / 2), B), blk, 0, st, ka);
 
   GramArgs ha{};  // H_l H_j^T and dZ_l dZ_j^T: the layer buffers have stride 64 rows per row b
   ha.B = B; ha.C = C; ha.LL = LL;
@@ -784,15 +893,20 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     hipLaunchKernelGGL(k_chain_up<T>, dim3(nF, B), blk, 0, st, ua);
 
     ha.layer = l;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (l + 1), B), dim3(64), 0, st, ha);
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (l + 1), B), blk, 0, st, ha);
 
     DownArgs da{};
     da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
-    da.coef = coef; da.h_all = h_all; da.wd = a.w_down; da.sd = a.s_down; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
-    hipLaunchKernelGGL(k_chain_down<T>, dim3(D / 64, c.nsplit + (l > 0 ? 1 : 0), B), blk, 0, st, da);
+    da.coef = coef; da.h_all = h_all; da.wd = wd_src; da.sd = sd_src; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
+    const int ncorr = (l + kCorrPerSplit - 1) / kCorrPerSplit;
+    const dim3 down_grid(D / 64, c.nsplit + ncorr, B);
+    if (bf16_src)
+      hipLaunchKernelGGL((k_chain_down<T, bf16>), down_grid, blk, 0, st, da);
+    else
+      hipLaunchKernelGGL((k_chain_down<T, float>), down_grid, blk, 0, st, da);
 
     LnGradArgs g{};
-    g.B = B; g.C = C; g.D = D; g.nsplit = c.nsplit + (l > 0 ? 1 : 0); g.tok_pad = 64;
+    g.B = B; g.C = C; g.D = D; g.nsplit = c.nsplit + ncorr; g.tok_pad = 64;
     g.normalize = a.normalize_by_dim; g.eps = a.eps; g.zp = zp;
     g.k = a.k[l]; g.k_rs = a.kv_row_stride; g.v = a.v[l]; g.v_rs = a.kv_row_stride;
     g.eta = a.eta[l]; g.eta_rs = a.ea_row_stride;
@@ -800,16 +914,19 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     g.ln_w = a.ln_weight; g.ln_b = a.ln_bias;
     g.dz = static_cast<char*>(dz_all) + e * l * ld;
     g.loss = loss;
-    hipLaunchKernelGGL(k_ln_grad<T>, dim3(64, B), blk, 0, st, g);
+    launch_ln_grad<T>(dim3(64, B), st, g);
 
     za.layer = l;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (l + 1), B), dim3(64), 0, st, za);
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (l + 1), B), blk, 0, st, za);
 
     BackArgs ba{};
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
-    ba.coef = coef; ba.dz_all = dz_all; ba.wd = a.w_down; ba.sd = a.s_down; ba.zz = zz; ba.h_all = h_all;
+    ba.coef = coef; ba.dz_all = dz_all; ba.wd = wd_src; ba.sd = sd_src; ba.zz = zz; ba.h_all = h_all;
     ba.u_cur = u_cur; ba.g_cur = g_cur; ba.kk = kk; ba.du_all = du_all; ba.dg_all = dg_all; ba.npart = npart;
-    hipLaunchKernelGGL(k_chain_back<T>, dim3(nF, B), blk, 0, st, ba);
+    if (bf16_src)
+      hipLaunchKernelGGL((k_chain_back<T, bf16>), dim3(nF, B), blk, 0, st, ba);
+    else
+      hipLaunchKernelGGL((k_chain_back<T, float>), dim3(nF, B), blk, 0, st, ba);
 
     CoefArgs ca{};
     ca.B = B; ca.C = C; ca.LL = LL; ca.l = l; ca.nF = nF;
@@ -828,6 +945,9 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   aa.wc[0] = static_cast<bf16*>(a.w_up_copy);
   aa.wc[1] = static_cast<bf16*>(a.w_gate_copy);
   aa.wc[2] = static_cast<bf16*>(a.w_down_copy);
+  aa.sc[0] = static_cast<bf16*>(a.s_up_copy);
+  aa.sc[1] = static_cast<bf16*>(a.s_gate_copy);
+  aa.sc[2] = static_cast<bf16*>(a.s_down_copy);
   hipLaunchKernelGGL(k_chain_apply<T>, dim3(3 * (D / 64) * nF, B), blk, 0, st, aa);
 }
 
@@ -874,6 +994,15 @@ extern "C" int uttt_chunk_chain(const uttt_chunk_chain_args* a, void* workspace,
   UTTT_REQUIRE(aligned16(a->w_up) && aligned16(a->w_gate) && aligned16(a->w_down) && aligned16(a->s_up) &&
                aligned16(a->s_gate) && aligned16(a->s_down), "state pointers must be 16-byte aligned");
   UTTT_REQUIRE(a->ln_weight && a->ln_bias && a->surprise, "ln_weight/ln_bias/surprise must be non-NULL");
+  const bool any_copy = a->w_up_copy || a->w_gate_copy || a->w_down_copy || a->s_up_copy || a->s_gate_copy ||
+                        a->s_down_copy;
+  const bool all_copy = a->w_up_copy && a->w_gate_copy && a->w_down_copy && a->s_up_copy && a->s_gate_copy &&
+                        a->s_down_copy;
+  UTTT_REQUIRE(!any_copy || (all_copy && a->act_dtype == UTTT_DTYPE_BF16),
+               "bf16 state copies must be given all six or none, and only with bf16 activations");
+  UTTT_REQUIRE(!any_copy || (aligned16(a->w_up_copy) && aligned16(a->w_gate_copy) && aligned16(a->w_down_copy) &&
+                             aligned16(a->s_up_copy) && aligned16(a->s_gate_copy) && aligned16(a->s_down_copy)),
+               "bf16 state copies must be 16-byte aligned");
   UTTT_REQUIRE(a->momentum_beta >= 0.f && a->max_inner_grad_norm >= 0.f && a->min_row_surprise >= 0.f,
                "momentum_beta, max_inner_grad_norm and min_row_surprise must be >= 0");
   const ChainLayout c = chain_layout(a->batch, a->layers, a->d_model, a->d_ff, a->act_dtype);

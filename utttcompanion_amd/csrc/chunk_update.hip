@@ -540,7 +540,7 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   o.x = a.q; o.x_rs = a.q_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
   o.out = a.out; o.out_rs = a.out_row_stride;
   if (want(2)) {
-    hipLaunchKernelGGL(k_ln_grad<T>, dim3(64, B), blk, 0, st, g);
+    launch_ln_grad<T>(dim3(64, B), st, g);
     hipLaunchKernelGGL(k_ln_readout<T>, dim3(C, B), blk, 0, st, o);
   }
 

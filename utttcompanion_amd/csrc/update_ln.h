@@ -11,7 +11,7 @@
 namespace uttt {
 namespace {  // each translation unit that launches it owns its copy
 
-constexpr int kMaxPerThread = 16;  // D <= 4096
+constexpr int kMaxPerThread = 16;  // D <= 4096 with 256 threads
 
 struct LnGradArgs {
   int B, C, D, nsplit, tok_pad, normalize;
@@ -27,7 +27,9 @@ struct LnGradArgs {
   float* loss;  // (B, 64): token loss times its mask value
 };
 
-template <typename T>
+// kPer features per thread (D <= 256 kPer); the split partials of a token are read
+// 16 / kPer splits at a time so that many loads are in flight together.
+template <typename T, int kPer>
 __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
   __shared__ float red[4];
   const int t = blockIdx.x, b = blockIdx.y;
@@ -41,24 +43,34 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
   const T* vr = static_cast<const T*>(a.v) + (int64_t)b * a.v_rs + (int64_t)t * a.D;
   const float inv_d = 1.0f / (float)a.D;
 
-  float z[kMaxPerThread];
+  constexpr int kGroup = 16 / kPer;
+  float z[kPer];
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) z[i] = 0.f;
-  for (int sp = 0; sp < a.nsplit; ++sp) {  // one round trip per split: the row's loads go out together
-    const float* src = a.zp + (((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D;
+  for (int i = 0; i < kPer; ++i) z[i] = 0.f;
+  for (int sp = 0; sp < a.nsplit; sp += kGroup) {
+    float part[kGroup][kPer];
 #pragma unroll
-    for (int i = 0; i < kMaxPerThread; ++i) {
-      const int d = threadIdx.x + i * kThreads;
-      if (d < a.D) z[i] += src[d];
+    for (int g = 0; g < kGroup; ++g) {
+      const bool in = sp + g < a.nsplit;
+      const float* src = a.zp + (((int64_t)(sp + g) * a.B + b) * a.tok_pad + t) * a.D;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int d = threadIdx.x + i * kThreads;
+        part[g][i] = (in && d < a.D) ? src[d] : 0.f;
+      }
     }
+#pragma unroll
+    for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) z[i] += part[g][i];
   }
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) s += z[i];
+  for (int i = 0; i < kPer; ++i) s += z[i];
   const float mean = block_sum(s, red) * inv_d;
   float s2 = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const int d = threadIdx.x + i * kThreads;
     if (d < a.D) {
       const float c = z[i] - mean;
@@ -70,10 +82,10 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
   const float inv_scale = a.normalize ? inv_d : 1.0f;
 
   // z[] becomes z_hat, e[] the reconstruction error
-  float e[kMaxPerThread];
+  float e[kPer];
   float se = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const int d = threadIdx.x + i * kThreads;
     e[i] = 0.f;
     if (d < a.D) {
@@ -100,7 +112,7 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
 
   float s3 = 0.f, s4 = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const int d = threadIdx.x + i * kThreads;
     if (d < a.D) {
       e[i] = coef * e[i] * a.ln_w[d];  // dZ_hat
@@ -111,11 +123,22 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
   const float m1 = block_sum(s3, red) * inv_d;
   const float m2 = block_sum(s4, red) * inv_d;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const int d = threadIdx.x + i * kThreads;
     if (d < a.D) dz[d] = from_f32<T>(rstd * (e[i] - m1 - z[i] * m2));
   }
   if (threadIdx.x == 0) a.loss[b * 64 + t] = a.mask != nullptr ? token_loss * m_t : token_loss;
+}
+
+// Launch k_ln_grad with the narrowest per-thread width that covers d_model.
+template <typename T>
+void launch_ln_grad(dim3 grid, hipStream_t st, const LnGradArgs& g) {
+  if (g.D <= 4 * kThreads)
+    hipLaunchKernelGGL((k_ln_grad<T, 4>), grid, dim3(kThreads), 0, st, g);
+  else if (g.D <= 8 * kThreads)
+    hipLaunchKernelGGL((k_ln_grad<T, 8>), grid, dim3(kThreads), 0, st, g);
+  else
+    hipLaunchKernelGGL((k_ln_grad<T, 16>), grid, dim3(kThreads), 0, st, g);
 }
 
 }  // namespace

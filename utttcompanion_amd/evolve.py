@@ -9,10 +9,10 @@ runs ``uTTTModel.test_time_update`` on a clone of that user's state (``model/utt
 
 ``ragged_test_time_update`` runs N such updates together.  Requests are ordered by chunk
 count, longest first, so the requests still running at chunk ``c`` are a leading block of
-rows: every kernel of chunk ``c`` (attention, the projections, the fast-weight update phases)
-runs over just those rows, and a request costs its own chunks and nothing more.  A
-request's state rows are its own (the update kernels index the state per row), and a row
-leaves the chunk loop once its last chunk is written.  Each request's result equals its
+rows: every kernel of chunk ``c`` (attention, projections, readouts and the layer chain that
+applies the chunk's L updates) runs over just those rows, and a request costs its own chunks
+and nothing more.  A request's state rows are its own (the kernels index the state per row),
+and its rows keep their final state once its last chunk is written.  Each request's result equals its
 batch-1 ``test_time_update`` on the same padded turn: the chunk-first schedule, the token
 masking, the per-layer surprise weighting (``uttt_model.py:598-607``) and the step count are
 all per row.
@@ -125,23 +125,26 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
     k_bufs = [torch.empty((n, hkv, seq, hd), dtype=dt, device=dev) for _ in range(n_layers)]
     v_bufs = [torch.empty_like(kb) for kb in k_bufs]
 
-    snapshot = tuple(torch.cat([getattr(fast_states[i], name).detach().to(dev, torch.float32) for i in order])
-                     .contiguous() for name in ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down"))
+    # the requests' states, stacked in order; each chunk's chain updates the leading rows in
+    # place, so a finished request's rows keep its final state
+    cur = tuple(torch.cat([getattr(fast_states[i], name).detach().to(dev, torch.float32) for i in order])
+                .contiguous() for name in ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down"))
     ln_w = ln_w.to(dev)
     ln_b = ln_b.to(dev)
-    sets = [tuple(torch.empty_like(t) for t in snapshot) for _ in range(2 if n_chunks > 1 else 1)]
-    row_loss = torch.zeros((n_chunks, n_layers, n, 2), dtype=torch.float32, device=dev)
+    copies = [t.to(torch.bfloat16) for t in cur] if dt == torch.bfloat16 else None
+    read = copies[:3] if copies is not None else cur[:3]
+    row_loss = torch.zeros((n_layers, n, 2), dtype=torch.float32, device=dev)
     surprise = torch.empty((n_chunks, n_layers), dtype=torch.float32, device=dev)
     pool = model.fast_weight_pool
     clip = float(pool.max_inner_grad_norm or 0.0)
-    workspace = None
+    ws_chain = ws_read = None
     for ci in range(n_chunks):
         rows, off = active[ci], ci * c
         end = off + c
-        target = tuple(t[:rows] for t in sets[ci % len(sets)])
-        read = tuple(t[:rows] for t in snapshot[:3])
         cur_mask = mask[:rows, off:end]
         hid = h[:rows, off:end]
+        rd = [t[:rows] for t in read]
+        ks, vs, etas, alphas = [], [], [], []
         for li, block in enumerate(model.layers):
             attn = block.attn
             kb, vb = k_bufs[li][:rows], v_bufs[li][:rows]
@@ -150,28 +153,25 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
             K.swa_prefill(q.transpose(1, 2), kb, vb, win, off, out=att.transpose(1, 2), kv_len=end)
             hid = hid + attn.wo(att.view(rows, c, -1))
             uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
-            cursor = tuple(t[:rows] for t in snapshot) if li == 0 else target
-            prep = K.prepare_chunk_update(
-                uq, uk, uv, eta, alpha, *cursor, ln_w, ln_b, cur_mask, pool.momentum_beta, clip,
-                pool.normalize_loss_by_dim, pool.eps, *((None, None, None) if li == 0 else read),
-                out_state=target, surprise=surprise[ci, li], workspace=workspace,
-                row_loss=row_loss[ci, li, :rows], min_row_surprise=min_chunk_surprise)
-            workspace = prep.workspace
-            res = prep.launch()
-            hid = hid + block.uttt.w_o(res[0])
-        snapshot = sets[ci % len(sets)]
+            if ws_read is None:
+                ws_read = K.readout_workspace(uq, rd[0])
+            hid = hid + block.uttt.w_o(K.swiglu_readout(uq, *rd, ln_w, ln_b, pool.eps, workspace=ws_read))
+            ks.append(uk)
+            vs.append(uv)
+            etas.append(eta)
+            alphas.append(alpha)
+        chunk_rl = torch.empty((n_layers, rows, 2), dtype=torch.float32, device=dev)
+        chain = K.prepare_chunk_chain(ks, vs, etas, alphas, [t[:rows] for t in cur], ln_w, ln_b, cur_mask,
+                                      pool.momentum_beta, clip, pool.normalize_loss_by_dim, pool.eps,
+                                      copies=None if copies is None else [t[:rows] for t in copies],
+                                      surprise=surprise[ci], row_loss=chunk_rl,
+                                      min_row_surprise=min_chunk_surprise, workspace=ws_chain)
+        ws_chain = chain.workspace
+        chain.launch()
+        row_loss[:, :rows] += chunk_rl
 
-    # a request's final state sits in the buffer set its last chunk wrote; later chunks only
-    # write the leading rows of the longer requests, so it is never overwritten
-    final = sets[0]
-    if len(sets) == 2:
-        odd = torch.tensor([row for row, i in enumerate(order) if (chunks[i] - 1) % 2 == 1],
-                           dtype=torch.long, device=dev)
-        if odd.numel():
-            for dst, src in zip(sets[0], sets[1]):
-                dst.index_copy_(0, odd, src.index_select(0, odd))
-    sums = row_loss.sum(dim=0)  # (L, N, 2)
-    per_layer = (sums[..., 0] / sums[..., 1].clamp_min(1.0)).t()  # (N, L)
+    final = cur
+    per_layer = (row_loss[..., 0] / row_loss[..., 1].clamp_min(1.0)).t()  # (N, L)
     floats = per_layer.tolist()  # the reference's end-of-forward read, once for all requests
 
     results: List[Optional[Tuple[FastWeightState, float, List[float]]]] = [None] * n

@@ -294,7 +294,9 @@ def prepare_chunk_chain(ks: Sequence[Tensor], vs: Sequence[Tensor], etas: Sequen
 
     ``ks[l]``/``vs[l]`` (B, C, D), ``etas[l]``/``alphas[l]`` (B, C) or (B, C, 1) are layer l's
     update inputs; ``state`` = (w_up, w_gate, w_down, s_up, s_gate, s_down), fp32, updated in
-    place; ``copies`` optional bf16 (w_up, w_gate, w_down) tensors that receive the final W."""
+    place; ``copies`` optional bf16 tensors shaped like the six state tensors (bf16 activations
+    only): on entry the chunk-start state rounded to bf16, which the kernels then read instead
+    of the fp32 masters; on exit the final state rounded to bf16."""
     n_layers = len(ks)
     if not 1 <= n_layers <= N.MAX_CHAIN or not (len(vs) == len(etas) == len(alphas) == n_layers):
         raise ValueError(f"need 1..{N.MAX_CHAIN} layers with k, v, eta and alpha each")
@@ -350,9 +352,12 @@ def prepare_chunk_chain(ks: Sequence[Tensor], vs: Sequence[Tensor], etas: Sequen
     if ln_w.numel() != dim or ln_b.numel() != dim:
         raise ValueError("ln_weight / ln_bias must have d_model elements")
     if copies is not None:
-        if len(copies) != 3 or any(c.dtype != torch.bfloat16 or not c.is_contiguous() or c.shape != w.shape
-                                   or c.device != dev for c, w in zip(copies, (w_up, w_gate, w_down))):
-            raise ValueError("copies must be three contiguous bf16 tensors shaped like w_up, w_gate, w_down")
+        if act != torch.bfloat16:
+            raise ValueError("bf16 state copies go with bf16 activations only")
+        if len(copies) != 6 or any(c.dtype != torch.bfloat16 or not c.is_contiguous() or c.shape != w.shape
+                                   or c.device != dev or c.data_ptr() % 16
+                                   for c, w in zip(copies, (w_up, w_gate, w_down, s_up, s_gate, s_down))):
+            raise ValueError("copies must be six contiguous, aligned bf16 tensors shaped like the state")
     if surprise is None:
         surprise = torch.empty(n_layers, dtype=torch.float32, device=dev)
     elif surprise.shape != (n_layers,) or surprise.dtype != torch.float32 or not surprise.is_contiguous():
@@ -378,7 +383,8 @@ def prepare_chunk_chain(ks: Sequence[Tensor], vs: Sequence[Tensor], etas: Sequen
                                                               (w_up, w_gate, w_down, s_up, s_gate, s_down))
     a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
     if copies is not None:
-        a.w_up_copy, a.w_gate_copy, a.w_down_copy = (_p(c) for c in copies)
+        (a.w_up_copy, a.w_gate_copy, a.w_down_copy,
+         a.s_up_copy, a.s_gate_copy, a.s_down_copy) = (_p(c) for c in copies)
     a.surprise, a.row_loss = _p(surprise), _p(row_loss)
     keep += [ln_w, ln_b, state, copies]
     return PreparedChain(a, keep, workspace, (surprise, row_loss), dev)
@@ -392,6 +398,14 @@ def chunk_chain(*args, **kwargs) -> Tuple[Tensor, Optional[Tensor]]:
 # ---------------------------------------------------------------------------
 # frozen readout (reference swiglu_fast_forward, model/uttt_layer.py:211-247)
 # ---------------------------------------------------------------------------
+
+def readout_workspace(x: Tensor, w_up: Tensor) -> Tensor:
+    """A workspace for ``swiglu_readout`` of x (B, T, D) through weights shaped like ``w_up``,
+    reusable by every later call with the same or smaller shapes."""
+    bsz, tokens, dim = x.shape
+    nbytes = N.load_library().uttt_readout_workspace(bsz, tokens, dim, w_up.shape[-1], _act_code(x.dtype))
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+
 
 def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_weight: Tensor,
                    ln_bias: Tensor, eps: float = 1e-5, out: Optional[Tensor] = None,

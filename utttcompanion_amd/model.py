@@ -6,9 +6,10 @@ writes runs the reference's chunk-first shared schedule (every layer of a chunk
 reads the chunk-start snapshot; writes chain one cursor through the layers;
 reference ``uttt_model.py:453-608``) on the HIP kernels, with
 
-* the fp32 state double-buffered: layer 0 of a chunk writes the snapshot's update
-  into a fresh buffer set, layers 1..L-1 update that set in place, and it becomes
-  the next chunk's snapshot (the caller's state tensors are never written);
+* per chunk, every layer's attention, projections and readout first (the readouts read
+  the chunk-start state, through bf16 copies on the bf16 path), then one layer-chain
+  launch (``uttt_chunk_chain``) that applies all L chained updates to one fp32 state set
+  in place (a copy of the caller's state, whose tensors are never written);
 * one linear KV buffer per layer for the whole call (rotated keys appended by the
   RoPE kernel, the window enforced by the attention kernel);
 * per-(chunk, layer) surprise kept on the device; the only host sync is the
@@ -189,14 +190,14 @@ class uTTTModel(nn.Module):
 
     def prefill_with_writes(self, input_ids: Tensor, state: FastWeightState,
                             attention_mask: Optional[Tensor] = None,
-                            kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0,
-                            out_state: Optional[FastWeightState] = None):
+                            kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0):
         """Chunk-first forward with fast-weight writes, without any host synchronisation.
 
+        Per chunk: every layer's attention, projections and fast-weight readout run first
+        (all readouts read the chunk-start state, reference uttt_model.py:519-608), then one
+        ``uttt_chunk_chain`` launch applies the layers' chained updates to the state in place.
         Returns (hidden (B, T, D), final state tensors (6,), per-layer surprise (L,) fp32
         device tensor, per-layer KV caches (last <= window rotated keys/values)).
-        ``out_state`` may name a preallocated pair of buffer sets via its tensors (used by
-        graph capture); otherwise buffers are allocated here.
         """
         cfg = self.config
         if cfg.write_schedule != "sequential":
@@ -223,49 +224,56 @@ class uTTTModel(nn.Module):
             k_bufs.append(kb)
             v_bufs.append(vb)
 
-        snapshot = tuple(t.float().contiguous() for t in state.tensors())
+        # one fp32 state set, updated in place chunk by chunk (the caller's tensors are not written)
+        cur = tuple(t.detach().to(device=dev, dtype=torch.float32).clone(memory_format=torch.contiguous_format)
+                    for t in state.tensors())
         ln_w, ln_b = state.ln_weight, state.ln_bias
-        sets = [tuple(torch.empty_like(t) for t in snapshot) for _ in range(2 if n_chunks > 1 else 1)]
+        # bf16 copies of the state on the bf16 path (the reference casts W to the activation
+        # dtype for these matmuls): the readouts and the chain read them; each chain refreshes them
+        copies = [t.to(torch.bfloat16) for t in cur] if h.dtype == torch.bfloat16 else None
+        read = copies[:3] if copies is not None else cur[:3]
         surprises = torch.zeros((n_chunks, n_layers), dtype=torch.float32, device=dev)
         counts = torch.full((n_chunks,), float(bsz * c), dtype=torch.float32, device=dev)
         if seq % c:
             counts[-1:].fill_(float(bsz * (seq % c)))
         pool = self.fast_weight_pool
+        clip = float(pool.max_inner_grad_norm or 0.0)
         pieces = []
-        workspace = None
+        ws_chain = ws_read = None
         for ci in range(n_chunks):
             off = ci * c
             end = min(seq, off + c)
             mask = attention_mask[:, off:end] if attention_mask is not None else None
             if mask is not None:
                 counts[ci].copy_(mask.to(torch.float32).sum())
-            target = sets[ci % len(sets)]
             hid = h[:, off:end]
+            ks, vs, etas, alphas = [], [], [], []
             for li, block in enumerate(self.layers):
                 attn = block.attn
-                x1 = block.attn_norm(hid)
-                q = attn.project(x1, start_pos + off, k_bufs[li], v_bufs[li], hist + off)
+                q = attn.project(block.attn_norm(hid), start_pos + off, k_bufs[li], v_bufs[li], hist + off)
                 att = torch.empty((bsz, end - off, attn.n_heads, hd), dtype=h.dtype, device=dev)
                 K.swa_prefill(q.transpose(1, 2), k_bufs[li], v_bufs[li], win, hist + off,
                               out=att.transpose(1, 2), kv_len=hist + end)
                 hid = hid + attn.wo(att.view(bsz, end - off, -1))
-                x2 = block.uttt_norm(hid)
-                uq, uk, uv, eta, alpha = block.uttt.projections(x2)
-                cursor = snapshot if li == 0 else target
-                prep = K.prepare_chunk_update(
-                    uq, uk, uv, eta, alpha, *cursor, ln_w, ln_b, mask, pool.momentum_beta,
-                    float(pool.max_inner_grad_norm or 0.0), pool.normalize_loss_by_dim, pool.eps,
-                    *((None, None, None) if li == 0 else snapshot[:3]),
-                    out_state=target, surprise=surprises[ci, li], workspace=workspace)
-                workspace = prep.workspace
-                res = prep.launch()
-                hid = hid + block.uttt.w_o(res[0])
-            snapshot = target
+                uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
+                if ws_read is None:
+                    ws_read = K.readout_workspace(uq, read[0])
+                r = K.swiglu_readout(uq, *read, ln_w, ln_b, pool.eps, workspace=ws_read)
+                hid = hid + block.uttt.w_o(r)
+                ks.append(uk)
+                vs.append(uv)
+                etas.append(eta)
+                alphas.append(alpha)
+            chain = K.prepare_chunk_chain(ks, vs, etas, alphas, cur, ln_w, ln_b, mask, pool.momentum_beta, clip,
+                                          pool.normalize_loss_by_dim, pool.eps, copies=copies,
+                                          surprise=surprises[ci], workspace=ws_chain)
+            ws_chain = chain.workspace
+            chain.launch()
             pieces.append(hid)
         per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
         caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win else (kb, vb)
                   for kb, vb in zip(k_bufs, v_bufs)]
-        return torch.cat(pieces, dim=1), snapshot, per_layer, caches
+        return torch.cat(pieces, dim=1), cur, per_layer, caches
 
     # ------------------------------------------------------------------ forward
     def _logits(self, h: Tensor) -> Tensor:
