@@ -60,6 +60,29 @@ __device__ __forceinline__ const T* layer_row(const LayerPtrs& lp, int l, int b,
   return static_cast<const T*>(lp.p[l]) + (int64_t)b * rs;
 }
 
+// Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2.  With
+// at least 8 rows the row is the fastest-varying part of the id (rows padded to a multiple of
+// 8), so all workgroups of a row run on one XCD and share its activations in one L2; with
+// fewer rows the tiles vary fastest and every XCD works on every row.
+constexpr int kXcds = 8;
+
+struct RowTile {
+  int b, tile;
+  bool valid;
+};
+
+__device__ __forceinline__ RowTile row_tile(int bid, int B, int ntiles) {
+  if (B >= kXcds) {
+    const int b8 = (B + kXcds - 1) / kXcds * kXcds;
+    return {bid % b8, bid / b8, bid % b8 < B};
+  }
+  return {bid / ntiles, bid % ntiles, true};
+}
+
+inline int row_tile_blocks(int B, int ntiles) {
+  return (B >= kXcds ? (B + kXcds - 1) / kXcds * kXcds : B) * ntiles;
+}
+
 // dst[row][k] = scale * (register-staged fp32 64 x 64 tile), converted to T
 template <typename T>
 __device__ __forceinline__ void store_scaled(const RowStage<float, 64>& st, T* dst, int ldd, float scale) {
@@ -161,8 +184,12 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T bs[64 * LD];
   __shared__ __align__(16) T as[kPqGroup * 64 * LD];
-  const int ft = blockIdx.x, m = blockIdx.z & 3, b = blockIdx.z >> 2;
-  const int f0 = ft * 64, l0 = blockIdx.y * kPqGroup;
+  const int nlg = (a.L + kPqGroup - 1) / kPqGroup;
+  const RowTile rt = row_tile(blockIdx.x, a.B, 4 * (a.F / 64) * nlg);
+  if (!rt.valid) return;
+  // tile = (m, F tile, layer group) with the layer groups that share an X tile adjacent
+  const int b = rt.b, lg = rt.tile % nlg, ft = (rt.tile / nlg) % (a.F / 64), m = rt.tile / (nlg * (a.F / 64));
+  const int f0 = ft * 64, l0 = lg * kPqGroup;
   const int nl = min(kPqGroup, a.L - l0);
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const WT* xs = static_cast<const WT*>(a.x[m]) + (int64_t)b * a.D * a.F + f0;
@@ -214,7 +241,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
 //    all-pairs mode: every j <= l into out (B, LL, LL).
 // ---------------------------------------------------------------------------
 struct GramArgs {
-  int B, C, kd, LL, layer;
+  int B, L, C, kd, LL, layer;
   int64_t rs, ts;  // row / token strides of X (elements)
   LayerPtrs x;
   float* out;
@@ -225,8 +252,11 @@ struct GramArgs {
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
   __shared__ float part[3 * 16 * 64];
-  const int q = blockIdx.x & 3;  // 32 x 32 quadrant of the 64 x 64 block
-  const int blk = blockIdx.x >> 2, b = blockIdx.y;
+  const int npairs = a.layer >= 0 ? a.layer + 1 : a.L * (a.L + 1) / 2;
+  const RowTile rt = row_tile(blockIdx.x, a.B, 4 * npairs);
+  if (!rt.valid) return;
+  const int q = rt.tile & 3;  // 32 x 32 quadrant of the 64 x 64 block
+  const int blk = rt.tile >> 2, b = rt.b;
   int l, j;
   if (a.layer >= 0) {
     l = a.layer;
@@ -312,7 +342,9 @@ __global__ void __launch_bounds__(kThreads) k_chain_up(const UpArgs a) {
   __shared__ __align__(16) T as[2][64 * LD];
   __shared__ __align__(16) T bu[2][64 * LD];
   __shared__ __align__(16) T bg[2][64 * LD];
-  const int ft = blockIdx.x, b = blockIdx.y, f0 = ft * 64;
+  const RowTile rt = row_tile(blockIdx.x, a.B, a.F / 64);
+  if (!rt.valid) return;
+  const int ft = rt.tile, b = rt.b, f0 = ft * 64;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const float* cf = a.coef + (int64_t)b * kCoefStride;
   const float ca = cf[0], cb = cf[1];
@@ -397,7 +429,10 @@ __global__ void __launch_bounds__(kThreads) k_chain_down(const DownArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T hs[2][64 * LD];
   __shared__ __align__(16) T ws[2][64 * LD];
-  const int dt = blockIdx.x, split = blockIdx.y, b = blockIdx.z, d0 = dt * 64;
+  const int nsp = a.nsplit + (a.l + kCorrPerSplit - 1) / kCorrPerSplit;
+  const RowTile rt = row_tile(blockIdx.x, a.B, (a.D / 64) * nsp);
+  if (!rt.valid) return;
+  const int dt = rt.tile % (a.D / 64), split = rt.tile / (a.D / 64), b = rt.b, d0 = dt * 64;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const float* cf = a.coef + (int64_t)b * kCoefStride;
   f32x16 acc;
@@ -486,7 +521,9 @@ __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
   __shared__ __align__(16) T dus[64 * LD];  // [t][f]
   __shared__ __align__(16) T dgs[64 * LD];
   __shared__ float red[4];
-  const int ft = blockIdx.x, b = blockIdx.y, f0 = ft * 64;
+  const RowTile rt = row_tile(blockIdx.x, a.B, a.F / 64);
+  if (!rt.valid) return;
+  const int ft = rt.tile, b = rt.b, f0 = ft * 64;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const float* cf = a.coef + (int64_t)b * kCoefStride;
   const float ca = cf[0], cb = cf[1];
@@ -680,26 +717,35 @@ struct ApplyChainArgs {
   bf16* sc[3];
 };
 
+// 64 x 64 output tiles, one layer's token slab per stage (double-buffered); W and S are read
+// after the layer loop.  The kernel is bound by how many workgroups overlap their round trips,
+// so it is compiled for kApplyWaves waves per SIMD.
+constexpr int kApplyWaves = 3;
+
 template <typename T>
-__global__ void __launch_bounds__(kThreads) k_chain_apply(const ApplyChainArgs a) {
+__global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const ApplyChainArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T as[2][64 * LD];
   __shared__ __align__(16) T bs[2][64 * LD];
   const int nD = a.D / 64, nF = a.F / 64;
   const int per = nD * nF;
-  const int m = blockIdx.x / per, jt = blockIdx.x - m * per, b = blockIdx.y;
+  const RowTile rt = row_tile(blockIdx.x, a.B, 3 * per);
+  if (!rt.valid) return;
+  const int m = rt.tile / per, jt = rt.tile - m * per, b = rt.b;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const float* cf = a.coef + (int64_t)b * kCoefStride;
   const float ca = cf[0], cb = cf[1], ce = cf[2];
   if (cf[3] == 0.f) return;  // no layer updated this row: W and S stay as they are
+  // tiles sharing a small token slab run together: for every matrix the F tile is the outer
+  // index and the D tile the inner one, so the resident workgroups of a row need the slabs
+  // of a few F tiles plus the (small) D-wide slabs
   int r0, c0, ld_out;
+  const int ft = jt / nD, dt = jt - ft * nD;
   if (m < 2) {
-    const int dt = jt / nF, ft = jt - dt * nF;
     r0 = dt * 64;
     c0 = ft * 64;
     ld_out = a.F;
   } else {
-    const int ft = jt / nD, dt = jt - ft * nD;
     r0 = ft * 64;
     c0 = dt * 64;
     ld_out = a.D;
@@ -762,22 +808,24 @@ __global__ void __launch_bounds__(kThreads) k_chain_apply(const ApplyChainArgs a
   bf16* cs = a.sc[m] != nullptr ? a.sc[m] + b * mat : nullptr;
   float* wrow = wdst + (int64_t)(r0 + wr) * ld_out + col;
   float* srow = sdst + (int64_t)(r0 + wr) * ld_out + col;
+  // the state streams through once: non-temporal accesses keep it from evicting the token
+  // slabs that the other workgroups of the row still read from L2
   float wv[16], sv[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    wv[i] = wrow[(int64_t)acc_row(i) * ld_out];
-    sv[i] = srow[(int64_t)acc_row(i) * ld_out];
+    wv[i] = __builtin_nontemporal_load(wrow + (int64_t)acc_row(i) * ld_out);
+    sv[i] = __builtin_nontemporal_load(srow + (int64_t)acc_row(i) * ld_out);
   }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t off = (int64_t)acc_row(i) * ld_out;
     const float w_new = ca * wv[i] + cb * sv[i] + accw[i];
     const float s_new = ce * sv[i] + accs[i];
-    wrow[off] = w_new;
-    srow[off] = s_new;
+    __builtin_nontemporal_store(w_new, wrow + off);
+    __builtin_nontemporal_store(s_new, srow + off);
     const int64_t coff = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
-    if (cw != nullptr) cw[coff] = static_cast<bf16>(w_new);
-    if (cs != nullptr) cs[coff] = static_cast<bf16>(s_new);
+    if (cw != nullptr) __builtin_nontemporal_store(static_cast<bf16>(w_new), cw + coff);
+    if (cs != nullptr) __builtin_nontemporal_store(static_cast<bf16>(s_new), cs + coff);
   }
 }
 
@@ -862,7 +910,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     pa.x[0] = a.w_up; pa.x[1] = a.s_up; pa.x[2] = a.w_gate; pa.x[3] = a.s_gate;
   }
   pa.pq = ws + c.pq;
-  const dim3 pq_grid(nF, (L + kPqGroup - 1) / kPqGroup, 4 * B);
+  const dim3 pq_grid(row_tile_blocks(B, 4 * nF * ((L + kPqGroup - 1) / kPqGroup)));
   if (bf16_src)
     hipLaunchKernelGGL((k_chain_pq<T, bf16>), pq_grid, blk, 0, st, pa);
   else
@@ -871,12 +919,12 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   const void* sd_src = bf16_src ? a.s_down_copy : static_cast<const void*>(a.s_down);
 
   GramArgs ka{};
-  ka.B = B; ka.C = C; ka.kd = D; ka.LL = LL; ka.layer = -1; ka.rs = a.kv_row_stride; ka.ts = D;
+  ka.B = B; ka.L = L; ka.C = C; ka.kd = D; ka.LL = LL; ka.layer = -1; ka.rs = a.kv_row_stride; ka.ts = D;
   ka.x = acts.k; ka.out = kk;
-  hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (L * (L + 1) / 2), B), blk, 0, st, ka);
+  hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (L * (L + 1) / 2))), blk, 0, st, ka);
 
   GramArgs ha{};  // H_l H_j^T and dZ_l dZ_j^T: the layer buffers have stride 64 rows per row b
-  ha.B = B; ha.C = C; ha.LL = LL;
+  ha.B = B; ha.L = L; ha.C = C; ha.LL = LL;
   GramArgs za = ha;
   ha.kd = F; ha.rs = (int64_t)64 * F; ha.ts = F; ha.out = hh;
   za.kd = D; za.rs = (int64_t)64 * D; za.ts = D; za.out = zz;
@@ -890,16 +938,16 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     ua.B = B; ua.L = L; ua.C = C; ua.D = D; ua.F = F; ua.LL = LL; ua.l = l;
     ua.coef = coef; ua.pq = ws + c.pq; ua.kk = kk; ua.du_all = du_all; ua.dg_all = dg_all;
     ua.u_cur = u_cur; ua.g_cur = g_cur; ua.h_all = h_all;
-    hipLaunchKernelGGL(k_chain_up<T>, dim3(nF, B), blk, 0, st, ua);
+    hipLaunchKernelGGL(k_chain_up<T>, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
 
     ha.layer = l;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (l + 1), B), blk, 0, st, ha);
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (l + 1))), blk, 0, st, ha);
 
     DownArgs da{};
     da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
     da.coef = coef; da.h_all = h_all; da.wd = wd_src; da.sd = sd_src; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
     const int ncorr = (l + kCorrPerSplit - 1) / kCorrPerSplit;
-    const dim3 down_grid(D / 64, c.nsplit + ncorr, B);
+    const dim3 down_grid(row_tile_blocks(B, (D / 64) * (c.nsplit + ncorr)));
     if (bf16_src)
       hipLaunchKernelGGL((k_chain_down<T, bf16>), down_grid, blk, 0, st, da);
     else
@@ -917,16 +965,16 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     launch_ln_grad<T>(dim3(64, B), st, g);
 
     za.layer = l;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(4 * (l + 1), B), blk, 0, st, za);
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (l + 1))), blk, 0, st, za);
 
     BackArgs ba{};
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
     ba.coef = coef; ba.dz_all = dz_all; ba.wd = wd_src; ba.sd = sd_src; ba.zz = zz; ba.h_all = h_all;
     ba.u_cur = u_cur; ba.g_cur = g_cur; ba.kk = kk; ba.du_all = du_all; ba.dg_all = dg_all; ba.npart = npart;
     if (bf16_src)
-      hipLaunchKernelGGL((k_chain_back<T, bf16>), dim3(nF, B), blk, 0, st, ba);
+      hipLaunchKernelGGL((k_chain_back<T, bf16>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
     else
-      hipLaunchKernelGGL((k_chain_back<T, float>), dim3(nF, B), blk, 0, st, ba);
+      hipLaunchKernelGGL((k_chain_back<T, float>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
 
     CoefArgs ca{};
     ca.B = B; ca.C = C; ca.LL = LL; ca.l = l; ca.nF = nF;
@@ -948,7 +996,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   aa.sc[0] = static_cast<bf16*>(a.s_up_copy);
   aa.sc[1] = static_cast<bf16*>(a.s_gate_copy);
   aa.sc[2] = static_cast<bf16*>(a.s_down_copy);
-  hipLaunchKernelGGL(k_chain_apply<T>, dim3(3 * (D / 64) * nF, B), blk, 0, st, aa);
+  hipLaunchKernelGGL(k_chain_apply<T>, dim3(row_tile_blocks(B, 3 * (D / 64) * nF)), blk, 0, st, aa);
 }
 
 int check_chain_dims(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dtype) {
