@@ -130,6 +130,26 @@ int uttt_chunk_chain(const uttt_chunk_chain_args* args, void* workspace, size_t 
                      uttt_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * 1c. Slow-projection epilogue.  Replaces the RMSNorm / sigmoid part of
+ *     fused_slow_projections (model/uttt_layer.py:1193-1231): from the packed product
+ *     y = x [W_q; W_k; W_v; w_eta; w_alpha]^T + bias, one row (3 d_model + 2 values) per token,
+ *     q = RMSNorm(y_q) * q_weight, k = RMSNorm(y_k) * k_weight, v = RMSNorm(y_v),
+ *     eta = inner_lr * sigmoid(y_eta), alpha = weight_decay * sigmoid(y_alpha).
+ *     q, k, v rows share out_row_stride; eta and alpha are contiguous (rows,).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t rows, d_model;             /* d_model <= 4096 */
+  int32_t act_dtype;
+  float eps, inner_lr, weight_decay;
+  const void* y; int64_t y_row_stride;
+  const void* q_weight; const void* k_weight; /* (d_model,) in the activation dtype */
+  void* q; void* k; void* v; int64_t out_row_stride;
+  void* eta; void* alpha;
+} uttt_proj_epilogue_args;
+
+int uttt_proj_epilogue(const uttt_proj_epilogue_args* args, uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * 2. Frozen fast-weight readout f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down).
  *    Replaces swiglu_fast_forward (model/uttt_layer.py:211-247) as used by
  *    SharedFastWeightPool.forward_readout (:670-695) and the packed inference

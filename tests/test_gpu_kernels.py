@@ -317,3 +317,26 @@ def test_swa_decode_ring_matches_full_prefix(dtype, hd):
                 else:
                     assert max_abs(a, want) <= BF16_ABS, f"step {step} req {r}"
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_proj_epilogue_matches_oracle(dtype):
+    """q/k/v RMSNorm and eta/alpha sigmoid of the packed projection (reference
+    fused_slow_projections, model/uttt_layer.py:1193-1231) against the oracle's ops in fp32:
+    fp32 <= 1e-6 relative; bf16 within one bf16 rounding of the fp32 result (2^-8 relative)."""
+    K = kernels()
+    g = torch.Generator().manual_seed(17)
+    rows, d = 37, 192
+    y = torch.randn(2, rows, 3 * d + 2, generator=g) * 3.0
+    qw, kw = 1.0 + 0.2 * torch.randn(d, generator=g), 1.0 + 0.2 * torch.randn(d, generator=g)
+    y_in = y.to(dtype)
+    yf = y_in.float()
+    ref = (om.rms_norm(yf[..., :d], qw.to(dtype).float(), 1e-5), om.rms_norm(yf[..., d:2 * d], kw.to(dtype).float(), 1e-5),
+           om.rms_norm(yf[..., 2 * d:3 * d], None, 1e-5), 0.01 * torch.sigmoid(yf[..., 3 * d:3 * d + 1]),
+           0.005 * torch.sigmoid(yf[..., 3 * d + 1:]))
+    with torch.no_grad():
+        got = K.proj_epilogue(y_in.to(DEV), d, qw.to(DEV, dtype), kw.to(DEV, dtype), 1e-5, 0.01, 0.005)
+    for name, a, e in zip(("q", "k", "v", "eta", "alpha"), got, ref):
+        assert a.shape == e.shape and a.dtype == dtype, name
+        err = ((a.float().cpu() - e).abs() / e.abs().clamp_min(1e-6)).max().item()
+        assert err <= (1e-6 if dtype == torch.float32 else 2.0 ** -8), f"{name}: rel err {err:.3e}"

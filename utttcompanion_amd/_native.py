@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 MAX_CHAIN = 64
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -59,6 +59,17 @@ class ChunkChainArgs(C.Structure):
         ("w_up_copy", _P), ("w_gate_copy", _P), ("w_down_copy", _P),
         ("s_up_copy", _P), ("s_gate_copy", _P), ("s_down_copy", _P),
         ("surprise", _P), ("row_loss", _P),
+    ]
+
+
+class ProjEpilogueArgs(C.Structure):
+    _fields_ = [
+        ("rows", _I64), ("d_model", _I64), ("act_dtype", _I32),
+        ("eps", _F), ("inner_lr", _F), ("weight_decay", _F),
+        ("y", _P), ("y_row_stride", _I64),
+        ("q_weight", _P), ("k_weight", _P),
+        ("q", _P), ("k", _P), ("v", _P), ("out_row_stride", _I64),
+        ("eta", _P), ("alpha", _P),
     ]
 
 
@@ -133,6 +144,7 @@ SIGNATURES = {
     "uttt_chunk_update_phase": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _I32, _P]),
     "uttt_chunk_chain_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_chunk_chain": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _P]),
+    "uttt_proj_epilogue": (C.c_int, [C.POINTER(ProjEpilogueArgs), _P]),
     "uttt_readout_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_swiglu_readout": (C.c_int, [C.POINTER(ReadoutArgs), _P, C.c_size_t, _P]),
     "uttt_rope_kv_append": (C.c_int, [C.POINTER(RopeAppendArgs), _P]),

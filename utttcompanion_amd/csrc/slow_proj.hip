@@ -1,0 +1,104 @@
+// Epilogue of the uTTT slow projections (reference fused_slow_projections,
+// model/uttt_layer.py:1193-1231), written for gfx950 (MI355X).
+//
+// Input: y = x [W_q; W_k; W_v; w_eta; w_alpha]^T + [0; 0; 0; b_eta; b_alpha] per token row,
+// (rows, 3 D + 2) in the activation dtype.  Output per row:
+//   q = RMSNorm(y[0:D]) * q_weight, k = RMSNorm(y[D:2D]) * k_weight, v = RMSNorm(y[2D:3D]),
+//   eta = inner_lr * sigmoid(y[3D]), alpha = weight_decay * sigmoid(y[3D + 1])
+// with RMSNorm(z) = z / sqrt(mean(z^2) + eps), statistics and products in fp32 and one
+// rounding to the activation dtype.  One 256-thread workgroup per row replaces the three
+// RMSNorm launches and the four elementwise launches of the eager form.
+#include "uttt_device.h"
+#include "uttt_host.h"
+
+namespace uttt {
+namespace {
+
+constexpr int kMaxPer = 16;  // d_model <= 4096
+
+struct ProjArgs {
+  int rows, D;
+  float eps, lr, wd;
+  const void* y;
+  int64_t y_rs;
+  const void* qw;  // activation dtype
+  const void* kw;
+  void* out[3];
+  int64_t out_rs;
+  void* eta;
+  void* alpha;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_proj_epilogue(const ProjArgs a) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const T* y = static_cast<const T*>(a.y) + (int64_t)r * a.y_rs;
+  const float inv_d = 1.0f / (float)a.D;
+#pragma unroll 1
+  for (int seg = 0; seg < 3; ++seg) {
+    float v[kMaxPer];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) {
+      const int d = threadIdx.x + i * kThreads;
+      v[i] = d < a.D ? to_f32(y[seg * a.D + d]) : 0.f;
+      ss += v[i] * v[i];
+    }
+    const float rstd = 1.0f / sqrtf(block_sum(ss, red) * inv_d + a.eps);
+    const T* wt = static_cast<const T*>(seg == 0 ? a.qw : seg == 1 ? a.kw : nullptr);
+    T* o = static_cast<T*>(a.out[seg]) + (int64_t)r * a.out_rs;
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) {
+      const int d = threadIdx.x + i * kThreads;
+      if (d < a.D) {
+        const float g = wt != nullptr ? to_f32(wt[d]) : 1.0f;
+        o[d] = from_f32<T>(v[i] * rstd * g);
+      }
+    }
+  }
+  if (threadIdx.x == 0) {
+    const float ye = to_f32(y[3 * a.D]), ya = to_f32(y[3 * a.D + 1]);
+    static_cast<T*>(a.eta)[r] = from_f32<T>(a.lr * sigmoidf_acc(ye));
+    static_cast<T*>(a.alpha)[r] = from_f32<T>(a.wd * sigmoidf_acc(ya));
+  }
+}
+
+}  // namespace
+}  // namespace uttt
+
+using namespace uttt;
+
+extern "C" int uttt_proj_epilogue(const uttt_proj_epilogue_args* a, uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  UTTT_REQUIRE(a->rows >= 1 && a->rows <= 2147483647LL, "rows must be >= 1 (got %lld)", (long long)a->rows);
+  UTTT_REQUIRE(a->d_model >= 1 && a->d_model <= kMaxPer * kThreads, "d_model must be in [1, %d] (got %lld)",
+               kMaxPer * kThreads, (long long)a->d_model);
+  UTTT_REQUIRE(a->act_dtype == UTTT_DTYPE_F32 || a->act_dtype == UTTT_DTYPE_BF16, "act_dtype must be F32 or BF16");
+  UTTT_REQUIRE(a->y && a->q_weight && a->k_weight && a->q && a->k && a->v && a->eta && a->alpha,
+               "pointers must be non-NULL");
+  UTTT_REQUIRE(a->y_row_stride >= 3 * a->d_model + 2 && a->out_row_stride >= a->d_model,
+               "row strides must cover a row");
+  ProjArgs p{};
+  p.rows = (int)a->rows;
+  p.D = (int)a->d_model;
+  p.eps = a->eps;
+  p.lr = a->inner_lr;
+  p.wd = a->weight_decay;
+  p.y = a->y;
+  p.y_rs = a->y_row_stride;
+  p.qw = a->q_weight;
+  p.kw = a->k_weight;
+  p.out[0] = a->q;
+  p.out[1] = a->k;
+  p.out[2] = a->v;
+  p.out_rs = a->out_row_stride;
+  p.eta = a->eta;
+  p.alpha = a->alpha;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (a->act_dtype == UTTT_DTYPE_BF16)
+    hipLaunchKernelGGL(k_proj_epilogue<bf16>, dim3(p.rows), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(k_proj_epilogue<float>, dim3(p.rows), dim3(kThreads), 0, st, p);
+  return launch_status("uttt_proj_epilogue");
+}

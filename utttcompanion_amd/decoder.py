@@ -21,7 +21,7 @@ import torch
 import torch.nn.functional as F
 
 from . import kernels as K
-from .layer import FastWeightState
+from .layer import FastWeightState, linear_residual
 from .model import BOS_ID, PAD_ID, UNK_ID, uTTTModel
 
 Tensor = torch.Tensor
@@ -113,13 +113,13 @@ class BatchedDecoder:
             v = qkv[:, hq + hk:].view(n, self.hkv, self.hd)
             kr, vr = self.rings[li]
             att = K.swa_decode(q, k, v, kr, vr, self.positions, self.cos, self.sin, workspace=self._ws_attn)
-            h = h + attn.wo(att.reshape(n, -1))
+            h = linear_residual(h, att.reshape(n, -1), attn.wo.weight)
             x2 = block.uttt_norm(h)
             uq = F.rms_norm(F.linear(x2, block.uttt.w_q.weight), (x2.shape[-1],),
                             block.uttt.q_norm.weight.to(x2.dtype), block.uttt.q_norm.eps)
             r = K.swiglu_readout(uq.view(n, 1, -1), self.w_up, self.w_gate, self.w_down, self.ln_weight,
                                  self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read)
-            h = h + block.uttt.w_o(r.view(n, -1))
+            h = linear_residual(h, r.view(n, -1), block.uttt.w_o.weight)
         logits = F.linear(m.norm(h), m.lm_head.weight)
         self.positions.add_(1)
         work = logits.float()

@@ -31,7 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from . import kernels as K
-from .layer import FastWeightState
+from .layer import FastWeightState, linear_residual
 from .model import PAD_ID, uTTTModel
 
 Tensor = torch.Tensor
@@ -151,11 +151,12 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
             q = attn.project(block.attn_norm(hid), off, kb, vb, off)
             att = torch.empty((rows, c, attn.n_heads, hd), dtype=dt, device=dev)
             K.swa_prefill(q.transpose(1, 2), kb, vb, win, off, out=att.transpose(1, 2), kv_len=end)
-            hid = hid + attn.wo(att.view(rows, c, -1))
+            hid = linear_residual(hid, att.view(rows, c, -1), attn.wo.weight)
             uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
             if ws_read is None:
                 ws_read = K.readout_workspace(uq, rd[0])
-            hid = hid + block.uttt.w_o(K.swiglu_readout(uq, *rd, ln_w, ln_b, pool.eps, workspace=ws_read))
+            hid = linear_residual(hid, K.swiglu_readout(uq, *rd, ln_w, ln_b, pool.eps, workspace=ws_read),
+                                  block.uttt.w_o.weight)
             ks.append(uk)
             vs.append(uv)
             etas.append(eta)

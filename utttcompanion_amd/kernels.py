@@ -399,6 +399,40 @@ def chunk_chain(*args, **kwargs) -> Tuple[Tensor, Optional[Tensor]]:
 # frozen readout (reference swiglu_fast_forward, model/uttt_layer.py:211-247)
 # ---------------------------------------------------------------------------
 
+def proj_epilogue(y: Tensor, dim: int, q_weight: Tensor, k_weight: Tensor, eps: float, inner_lr: float,
+                  weight_decay: float) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """q, k, v, eta, alpha from the packed slow-projection product y (..., 3 D + 2)
+    (``uttt_proj_epilogue``; the RMSNorm / sigmoid part of reference fused_slow_projections,
+    model/uttt_layer.py:1193-1231).  Returns q, k, v (..., D) and eta, alpha (..., 1)."""
+    if y.shape[-1] != 3 * dim + 2:
+        raise ValueError(f"y must end in 3 * d_model + 2 = {3 * dim + 2} features, got {y.shape[-1]}")
+    code = _act_code(y.dtype)
+    dev = y.device
+    _require_device(dev, q_weight, k_weight)
+    _forward_only(y)
+    lead = y.shape[:-1]
+    y2 = y.reshape(-1, y.shape[-1])
+    if y2.stride(1) != 1:
+        y2 = y2.contiguous()
+    rows = y2.shape[0]
+    qkv = torch.empty((3, rows, dim), dtype=y.dtype, device=dev)
+    ea = torch.empty((2, rows), dtype=y.dtype, device=dev)
+    qw = q_weight.detach().to(y.dtype).contiguous()  # the reference casts the weights to x's dtype
+    kw = k_weight.detach().to(y.dtype).contiguous()
+    a = N.ProjEpilogueArgs()
+    a.rows, a.d_model, a.act_dtype = rows, dim, code
+    a.eps, a.inner_lr, a.weight_decay = float(eps), float(inner_lr), float(weight_decay)
+    a.y, a.y_row_stride = _p(y2), y2.stride(0)
+    a.q_weight, a.k_weight = _p(qw), _p(kw)
+    a.q, a.k, a.v, a.out_row_stride = _p(qkv[0]), _p(qkv[1]), _p(qkv[2]), dim
+    a.eta, a.alpha = _p(ea[0]), _p(ea[1])
+    lib = N.load_library()
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_proj_epilogue(C.byref(a), _stream(dev)), "uttt_proj_epilogue")
+    return (qkv[0].view(*lead, dim), qkv[1].view(*lead, dim), qkv[2].view(*lead, dim),
+            ea[0].view(*lead, 1), ea[1].view(*lead, 1))
+
+
 def readout_workspace(x: Tensor, w_up: Tensor) -> Tensor:
     """A workspace for ``swiglu_readout`` of x (B, T, D) through weights shaped like ``w_up``,
     reusable by every later call with the same or smaller shapes."""

@@ -376,6 +376,13 @@ def fused_fast_q_proj(x: Tensor, wq_w: Tensor, q_norm_w: Tensor, eps: float) -> 
     return F.rms_norm(q, (x.shape[-1],), q_norm_w.to(q.dtype), eps)
 
 
+def linear_residual(h: Tensor, x: Tensor, weight: Tensor) -> Tensor:
+    """h + x W^T as one GEMM with the residual as its C operand (the reference's
+    ``h + linear(x)``, model/uttt_layer.py:1528-1555, without a separate add kernel)."""
+    out = torch.addmm(h.reshape(-1, h.shape[-1]), x.reshape(-1, x.shape[-1]), weight.to(x.dtype).t())
+    return out.view(h.shape)
+
+
 def fused_slow_projections(x: Tensor, wq_w: Tensor, wk_w: Tensor, wv_w: Tensor, q_norm_w: Tensor,
                            k_norm_w: Tensor, w_eta_w: Tensor, w_eta_b: Tensor, w_alpha_w: Tensor,
                            w_alpha_b: Tensor, base_inner_lr: float, base_weight_decay: float,
@@ -433,16 +440,10 @@ class uTTTLayer(nn.Module):
 
     def projections(self, x: Tensor) -> Tuple[Tensor, ...]:
         """q, k, v, eta, alpha from one packed GEMM (same values as fused_slow_projections)."""
-        d = self.d_model
         w, b = self.packed_projection()
         y = F.linear(x, w.to(x.dtype), b.to(x.dtype))
-        eps = self.q_norm.eps
-        q = F.rms_norm(y[..., :d], (d,), self.q_norm.weight.to(x.dtype), eps)
-        k = F.rms_norm(y[..., d:2 * d], (d,), self.k_norm.weight.to(x.dtype), eps)
-        v = F.rms_norm(y[..., 2 * d:3 * d], (d,), None, eps)
-        eta = self.base_inner_lr * torch.sigmoid(y[..., 3 * d:3 * d + 1])
-        alpha = self.base_weight_decay * torch.sigmoid(y[..., 3 * d + 1:3 * d + 2])
-        return q, k, v, eta, alpha
+        return K.proj_epilogue(y, self.d_model, self.q_norm.weight, self.k_norm.weight, self.q_norm.eps,
+                               self.base_inner_lr, self.base_weight_decay)
 
     def forward(self, x: Tensor, fast_pool: SharedFastWeightPool, fast_state: FastWeightState,
                 attention_mask: Optional[Tensor] = None, update_fast_weights: bool = True,

@@ -28,7 +28,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import kernels as K
-from .layer import FastWeightState, RMSNorm, SharedFastWeightPool, uTTTBlock
+from .layer import FastWeightState, RMSNorm, SharedFastWeightPool, linear_residual, uTTTBlock
 
 Tensor = torch.Tensor
 _NAMES = ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")
@@ -254,12 +254,12 @@ class uTTTModel(nn.Module):
                 att = torch.empty((bsz, end - off, attn.n_heads, hd), dtype=h.dtype, device=dev)
                 K.swa_prefill(q.transpose(1, 2), k_bufs[li], v_bufs[li], win, hist + off,
                               out=att.transpose(1, 2), kv_len=hist + end)
-                hid = hid + attn.wo(att.view(bsz, end - off, -1))
+                hid = linear_residual(hid, att.view(bsz, end - off, -1), attn.wo.weight)
                 uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
                 if ws_read is None:
                     ws_read = K.readout_workspace(uq, read[0])
                 r = K.swiglu_readout(uq, *read, ln_w, ln_b, pool.eps, workspace=ws_read)
-                hid = hid + block.uttt.w_o(r)
+                hid = linear_residual(hid, r, block.uttt.w_o.weight)
                 ks.append(uk)
                 vs.append(uv)
                 etas.append(eta)
