@@ -8,11 +8,19 @@ ids uniform over the vocabulary, batch 8 x 2048.  One step = one full prefill wi
 per-chunk fast-weight writes of every layer (the chunk-first schedule), recorded once
 into a HIP graph and replayed.  ``value`` = tokens / s over the timed steps.
 
+Per chunk the prefill runs every layer's attention, projections and readout, then one layer
+chain (``uttt_chunk_chain``) that applies the chunk's 12 chained fast-weight updates.
+
 Also reported:
-* ``roofline``: the dominant kernel of the fused update, timed live with HIP events
-  between the update's stream-ordered phases at the config-2 update shape (8 rows,
-  C 64, D 768, F 2048), against its algorithmic bytes (HBM bound) or flops (MFMA);
-* ``update``: the whole update (all phases) against 48 D F bytes per row;
+* ``roofline``: the chain's state write (``k_chain_apply``, the largest single kernel of the
+  prefill), timed live with HIP events between the chain's stream-ordered stages at the
+  config-2 chunk shape (8 rows, 12 layers, C 64, D 768, F 2048), against 48 D F bytes per
+  row (W and S read and written once per chunk), with the HBM traffic rocprofv3 measured;
+* ``chain``: the whole chain per chunk and its stages;
+* ``update``: the single-chunk update (``uttt_chunk_update``, the per-layer drop-in for
+  ``fused_chunk_ttt_step``) phase by phase, with its own dominant kernel's roofline;
+* ``config3_prefill``, ``config5_evolve``: the 1.58B-label model's prefill and the ragged
+  per-request updates of 16 requests;
 * ``decode``: the ring-buffer SWA decode kernel at the config-4 shape (32 requests,
   4 kv heads x 64, window 512, bf16) against its K/V bytes;
 * ``cpu_baseline``: the CPU oracle (tests-only restatement) on a bounded sample of the
@@ -67,7 +75,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--phase-iters", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
-    ap.add_argument("--sections", default="prefill,update,decode,cpu,c3,evolve",
+    ap.add_argument("--sections", default="prefill,update,chain,decode,cpu,c3,evolve",
                     help="comma list of prefill, update, chain, decode, cpu, c3, evolve, copyref "
                          "(profiling runs pick a subset)")
     ap.add_argument("--c3-steps", type=int, default=2, help="timed config-3 prefills / config-5 updates")
@@ -185,7 +193,16 @@ def bench_chain(iters: int, B: int = None, L: int = None, D: int = None, F: int 
             prep.launch()
         end.record()
         torch.cuda.synchronize()
-    return start.elapsed_time(end) / iters, dict(B=B, L=L, C=C, D=D, F=F)
+        # the same chain stage by stage, with events between the stages (stream order kept)
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(L + 3)] for _ in range(iters)]
+        for it in range(iters):
+            ev[it][0].record()
+            for stg in range(L + 2):
+                prep.launch(stg)
+                ev[it][stg + 1].record()
+        torch.cuda.synchronize()
+    stage_ms = [sum(ev[it][k].elapsed_time(ev[it][k + 1]) for it in range(iters)) / iters for k in range(L + 2)]
+    return start.elapsed_time(end) / iters, stage_ms, dict(B=B, L=L, C=C, D=D, F=F)
 
 
 def phase_work(p: int, B: int, C: int, D: int, F: int):
@@ -363,7 +380,7 @@ def bench_evolve(model, steps: int):
     info = {"requests": C5_REQUESTS, "lengths": [min(lengths), max(lengths)], "valid_tokens": tokens,
             "row_chunks": chunks, "turn_gate_fired": sum(int(r.gate_triggered) for r in res),
             "mean_surprise": round(sum(r.surprise for r in res) / len(res), 4),
-            "min_state_bytes_per_step": 48 * D * F * chunks * C3["n_layers"]}
+            "min_state_bytes_per_step": 48 * D * F * chunks}  # W, S read + written once per row-chunk
     info["state_hbm_gbs"] = round(info["min_state_bytes_per_step"] / (ms * 1e-3) / 1e9, 1)
     return tokens / (ms * 1e-3), ms, info
 
@@ -431,17 +448,19 @@ def main() -> int:
         d_gbs = dbytes / (per[dom] * 1e-3) / 1e9
         d_tfl = dflops / (per[dom] * 1e-3) / 1e12
         hbm_bound = dbytes > 0 and dflops / dbytes < PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
-        roofline = ({"bound": "hbm", "achieved": round(d_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+        upd_roof = ({"bound": "hbm", "achieved": round(d_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(d_gbs / PEAK_HBM_GBS, 4)} if hbm_bound else
                     {"bound": "mfma", "achieved": round(d_tfl, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(d_tfl / PEAK_BF16_TFLOPS, 4)})
-        roofline.update(kernel=PHASES[dom], traffic=measured_traffic(PHASES[dom]),
+        upd_roof.update(kernel=PHASES[dom], traffic=measured_traffic(PHASES[dom]),
                         per_launch={"algorithmic_bytes": dbytes, "algorithmic_flops": dflops,
                                     "avg_ms": round(per[dom], 4), "shape": shape})
+        roofline = upd_roof
         upd_bytes, upd_flops = 48 * D * F * B, 20 * C * D * F * B
         update = {"ms": round(total_ms, 4), "phase_ms": dict(zip(PHASES, [round(x, 4) for x in per])),
                   "hbm_frac_min_state_bytes": round(upd_bytes / (total_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                  "mfma_frac": round(upd_flops / (total_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+                  "mfma_frac": round(upd_flops / (total_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                  "roofline": upd_roof}
         log(f"update phases (ms): {update['phase_ms']}")
 
     if "decode" in sections:
@@ -462,11 +481,25 @@ def main() -> int:
 
     chain = None
     if "chain" in sections:
-        ch_ms, ch_shape = bench_chain(args.phase_iters)
-        Bc, Lc, Dc, Fc = ch_shape["B"], ch_shape["L"], ch_shape["D"], ch_shape["F"]
-        chain = {"ms": round(ch_ms, 4), "shape": ch_shape, "us_per_layer": round(ch_ms * 1e3 / Lc, 2),
-                 "min_state_bytes_frac": round(48 * Dc * Fc * Bc / (ch_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-        log(f"layer chain {ch_ms:.3f} ms per chunk ({ch_ms * 1e3 / Lc:.1f} us per layer)")
+        ch_ms, stage_ms, ch_shape = bench_chain(args.phase_iters)
+        Bc, Lc, Cc, Dc, Fc = ch_shape["B"], ch_shape["L"], ch_shape["C"], ch_shape["D"], ch_shape["F"]
+        state_bytes = 48 * Dc * Fc * Bc  # W and S read and written once per chunk
+        chain = {"ms": round(ch_ms, 4), "shape": ch_shape,
+                 "stage_ms": {"prologue": round(stage_ms[0], 4),
+                              "layers_mean": round(sum(stage_ms[1:-1]) / Lc, 4),
+                              "apply": round(stage_ms[-1], 4)},
+                 "hbm_frac_min_state_bytes": round(state_bytes / (ch_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                 "mfma_frac_update_flops": round(20 * Cc * Dc * Fc * Lc * Bc / (ch_ms * 1e-3) / 1e12
+                                                 / PEAK_BF16_TFLOPS, 4)}
+        apply_ms = stage_ms[-1]
+        a_gbs = state_bytes / (apply_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(a_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(a_gbs / PEAK_HBM_GBS, 4), "kernel": "k_chain_apply",
+                    "traffic": measured_traffic("k_chain_apply"),
+                    "per_launch": {"algorithmic_bytes": state_bytes, "avg_ms": round(apply_ms, 4),
+                                   "unit_bytes": "48 D F per row per chunk (W and S read and written once)",
+                                   "shape": ch_shape}}
+        log(f"layer chain {ch_ms:.3f} ms per chunk; stages (ms) {chain['stage_ms']}")
 
     big = {}
     if sections & {"c3", "evolve"}:

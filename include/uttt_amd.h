@@ -128,6 +128,13 @@ typedef struct {
 size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff, int32_t act_dtype);
 int uttt_chunk_chain(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
                      uttt_stream_t stream);
+/* The same chain as layers + 2 stream-ordered stages, one per call, in order on one stream
+ * with one workspace: 0 coefficient init + products with the chunk-start state + key Gram
+ * blocks; 1 + l layer l's forward, backward and clip / decay recurrences; layers + 1 the
+ * state write.  Running every stage equals uttt_chunk_chain; it exists so a caller can
+ * place timing events between the stages. */
+int uttt_chunk_chain_stage(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
+                           int32_t stage, uttt_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * 1c. Slow-projection epilogue.  Replaces the RMSNorm / sigmoid part of

@@ -866,7 +866,8 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
 }
 
 template <typename T>
-void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c, hipStream_t st) {
+void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c, hipStream_t st, int first,
+                  int last) {
   const int B = (int)a.batch, L = (int)a.layers, C = (int)a.tokens, D = (int)a.d_model, F = (int)a.d_ff;
   const int LL = L * 64, nF = F / 64;
   const dim3 blk(kThreads);
@@ -897,8 +898,11 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   const int64_t lf = (int64_t)B * 64 * F, ld = (int64_t)B * 64 * D;
   const size_t e = sizeof(T);
 
+  // stage 0: coefficient init, snapshot products, key Gram; stage 1 + l: layer l; stage L + 1: apply
+  auto want = [&](int stage) { return first <= stage && stage <= last; };
   const int ncoef = B * kCoefStride;
-  hipLaunchKernelGGL(k_chain_init, dim3((ncoef + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef);
+  if (want(0))
+    hipLaunchKernelGGL(k_chain_init, dim3((ncoef + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef);
 
   // the chunk-start state the bf16 kernels read: its bf16 copies when given, else the masters
   const bool bf16_src = a.w_up_copy != nullptr;
@@ -911,17 +915,20 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   }
   pa.pq = ws + c.pq;
   const dim3 pq_grid(row_tile_blocks(B, 4 * nF * ((L + kPqGroup - 1) / kPqGroup)));
-  if (bf16_src)
-    hipLaunchKernelGGL((k_chain_pq<T, bf16>), pq_grid, blk, 0, st, pa);
-  else
-    hipLaunchKernelGGL((k_chain_pq<T, float>), pq_grid, blk, 0, st, pa);
+  if (want(0)) {
+    if (bf16_src)
+      hipLaunchKernelGGL((k_chain_pq<T, bf16>), pq_grid, blk, 0, st, pa);
+    else
+      hipLaunchKernelGGL((k_chain_pq<T, float>), pq_grid, blk, 0, st, pa);
+  }
   const void* wd_src = bf16_src ? a.w_down_copy : static_cast<const void*>(a.w_down);
   const void* sd_src = bf16_src ? a.s_down_copy : static_cast<const void*>(a.s_down);
 
   GramArgs ka{};
   ka.B = B; ka.L = L; ka.C = C; ka.kd = D; ka.LL = LL; ka.layer = -1; ka.rs = a.kv_row_stride; ka.ts = D;
   ka.x = acts.k; ka.out = kk;
-  hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (L * (L + 1) / 2))), blk, 0, st, ka);
+  if (want(0))
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (L * (L + 1) / 2))), blk, 0, st, ka);
 
   GramArgs ha{};  // H_l H_j^T and dZ_l dZ_j^T: the layer buffers have stride 64 rows per row b
   ha.B = B; ha.L = L; ha.C = C; ha.LL = LL;
@@ -934,6 +941,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   }
 
   for (int l = 0; l < L; ++l) {
+    if (!want(1 + l)) continue;
     UpArgs ua{};
     ua.B = B; ua.L = L; ua.C = C; ua.D = D; ua.F = F; ua.LL = LL; ua.l = l;
     ua.coef = coef; ua.pq = ws + c.pq; ua.kk = kk; ua.du_all = du_all; ua.dg_all = dg_all;
@@ -996,7 +1004,8 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   aa.sc[0] = static_cast<bf16*>(a.s_up_copy);
   aa.sc[1] = static_cast<bf16*>(a.s_gate_copy);
   aa.sc[2] = static_cast<bf16*>(a.s_down_copy);
-  hipLaunchKernelGGL(k_chain_apply<T>, dim3(row_tile_blocks(B, 3 * (D / 64) * nF)), blk, 0, st, aa);
+  if (want(L + 1))
+    hipLaunchKernelGGL(k_chain_apply<T>, dim3(row_tile_blocks(B, 3 * (D / 64) * nF)), blk, 0, st, aa);
 }
 
 int check_chain_dims(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dtype) {
@@ -1022,8 +1031,8 @@ extern "C" size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int6
   return chain_layout(batch, layers, d_model, d_ff, act_dtype).total;
 }
 
-extern "C" int uttt_chunk_chain(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes,
-                                uttt_stream_t stream) {
+static int run_chain(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes, uttt_stream_t stream,
+                     int first, int last) {
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   int rc = check_chain_dims(a->batch, a->layers, a->d_model, a->d_ff, a->act_dtype);
   if (rc != UTTT_OK) return rc;
@@ -1059,8 +1068,20 @@ extern "C" int uttt_chunk_chain(const uttt_chunk_chain_args* a, void* workspace,
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   if (a->act_dtype == UTTT_DTYPE_BF16)
-    launch_chain<bf16>(*a, ws, c, st);
+    launch_chain<bf16>(*a, ws, c, st, first, last);
   else
-    launch_chain<float>(*a, ws, c, st);
+    launch_chain<float>(*a, ws, c, st, first, last);
   return launch_status("uttt_chunk_chain");
+}
+
+extern "C" int uttt_chunk_chain(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes,
+                                uttt_stream_t stream) {
+  return run_chain(a, workspace, workspace_bytes, stream, 0, 1 << 30);
+}
+
+extern "C" int uttt_chunk_chain_stage(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes,
+                                      int32_t stage, uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  UTTT_REQUIRE(stage >= 0 && stage <= a->layers + 1, "stage must be in [0, layers + 1] (got %d)", stage);
+  return run_chain(a, workspace, workspace_bytes, stream, stage, stage);
 }

@@ -142,7 +142,7 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
         rows, off = active[ci], ci * c
         end = off + c
         cur_mask = mask[:rows, off:end]
-        hid = h[:rows, off:end]
+        hid = h[:rows, off:end].contiguous()  # this chunk's residual stream, updated in place
         rd = [t[:rows] for t in read]
         ks, vs, etas, alphas = [], [], [], []
         for li, block in enumerate(model.layers):

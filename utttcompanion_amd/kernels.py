@@ -268,11 +268,16 @@ class PreparedChain:
     def __init__(self, args, keep, workspace, result, device):
         self.args, self._keep, self.workspace, self.result, self.device = args, keep, workspace, result, device
 
-    def launch(self) -> Tuple[Tensor, Optional[Tensor]]:
+    def launch(self, stage: Optional[int] = None) -> Tuple[Tensor, Optional[Tensor]]:
+        """Enqueue the whole chain, or one of its ``layers + 2`` stream-ordered stages."""
         lib = N.load_library()
         with torch.cuda.device(self.device):
-            rc = lib.uttt_chunk_chain(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
-                                      _stream(self.device))
+            if stage is None:
+                rc = lib.uttt_chunk_chain(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
+                                          _stream(self.device))
+            else:
+                rc = lib.uttt_chunk_chain_stage(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
+                                                int(stage), _stream(self.device))
         N.check(rc, "uttt_chunk_chain")
         return self.result
 

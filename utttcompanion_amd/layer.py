@@ -377,10 +377,13 @@ def fused_fast_q_proj(x: Tensor, wq_w: Tensor, q_norm_w: Tensor, eps: float) -> 
 
 
 def linear_residual(h: Tensor, x: Tensor, weight: Tensor) -> Tensor:
-    """h + x W^T as one GEMM with the residual as its C operand (the reference's
-    ``h + linear(x)``, model/uttt_layer.py:1528-1555, without a separate add kernel)."""
-    out = torch.addmm(h.reshape(-1, h.shape[-1]), x.reshape(-1, x.shape[-1]), weight.to(x.dtype).t())
-    return out.view(h.shape)
+    """h += x W^T in place, as one GEMM that accumulates into the residual (the reference's
+    ``h + linear(x)``, model/uttt_layer.py:1528-1555, without a separate add kernel or copy).
+    ``h`` must be contiguous and owned by the caller."""
+    if not h.is_contiguous():
+        raise ValueError("the residual stream must be contiguous to be updated in place")
+    h.view(-1, h.shape[-1]).addmm_(x.reshape(-1, x.shape[-1]), weight.to(x.dtype).t())
+    return h
 
 
 def fused_slow_projections(x: Tensor, wq_w: Tensor, wk_w: Tensor, wv_w: Tensor, q_norm_w: Tensor,

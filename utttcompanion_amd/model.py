@@ -246,7 +246,7 @@ class uTTTModel(nn.Module):
             mask = attention_mask[:, off:end] if attention_mask is not None else None
             if mask is not None:
                 counts[ci].copy_(mask.to(torch.float32).sum())
-            hid = h[:, off:end]
+            hid = h[:, off:end].contiguous()  # this chunk's residual stream, updated in place
             ks, vs, etas, alphas = [], [], [], []
             for li, block in enumerate(self.layers):
                 attn = block.attn
