@@ -12,8 +12,9 @@ Per chunk the prefill runs every layer's attention, projections and readout, the
 chain (``uttt_chunk_chain``) that applies the chunk's 12 chained fast-weight updates.
 
 Also reported:
-* ``roofline``: the chain's state write (``k_chain_apply``, the largest single kernel of the
-  prefill), timed live with HIP events between the chain's stream-ordered stages at the
+* ``roofline``: the chain's state write (``k_chain_apply`` after the last layer's small
+  recurrence step; the largest single kernel of the prefill), timed live with HIP events
+  between the chain's stream-ordered stages at the
   config-2 chunk shape (8 rows, 12 layers, C 64, D 768, F 2048), against 48 D F bytes per
   row (W and S read and written once per chunk), with the HBM traffic rocprofv3 measured;
 * ``chain``: the whole chain per chunk and its stages;
@@ -194,14 +195,14 @@ def bench_chain(iters: int, B: int = None, L: int = None, D: int = None, F: int 
         end.record()
         torch.cuda.synchronize()
         # the same chain stage by stage, with events between the stages (stream order kept)
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(L + 3)] for _ in range(iters)]
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(L + 2)] for _ in range(iters)]
         for it in range(iters):
             ev[it][0].record()
-            for stg in range(L + 2):
+            for stg in range(L + 1):
                 prep.launch(stg)
                 ev[it][stg + 1].record()
         torch.cuda.synchronize()
-    stage_ms = [sum(ev[it][k].elapsed_time(ev[it][k + 1]) for it in range(iters)) / iters for k in range(L + 2)]
+    stage_ms = [sum(ev[it][k].elapsed_time(ev[it][k + 1]) for it in range(iters)) / iters for k in range(L + 1)]
     return start.elapsed_time(end) / iters, stage_ms, dict(B=B, L=L, C=C, D=D, F=F)
 
 
@@ -485,9 +486,8 @@ def main() -> int:
         Bc, Lc, Cc, Dc, Fc = ch_shape["B"], ch_shape["L"], ch_shape["C"], ch_shape["D"], ch_shape["F"]
         state_bytes = 48 * Dc * Fc * Bc  # W and S read and written once per chunk
         chain = {"ms": round(ch_ms, 4), "shape": ch_shape,
-                 "stage_ms": {"prologue": round(stage_ms[0], 4),
-                              "layers_mean": round(sum(stage_ms[1:-1]) / Lc, 4),
-                              "apply": round(stage_ms[-1], 4)},
+                 "stage_ms": {"layers_mean": round(sum(stage_ms[:-1]) / Lc, 4),
+                              "state_write": round(stage_ms[-1], 4)},
                  "hbm_frac_min_state_bytes": round(state_bytes / (ch_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                  "mfma_frac_update_flops": round(20 * Cc * Dc * Fc * Lc * Bc / (ch_ms * 1e-3) / 1e12
                                                  / PEAK_BF16_TFLOPS, 4)}

@@ -128,11 +128,16 @@ typedef struct {
 size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff, int32_t act_dtype);
 int uttt_chunk_chain(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
                      uttt_stream_t stream);
-/* The same chain as layers + 2 stream-ordered stages, one per call, in order on one stream
- * with one workspace: 0 coefficient init + products with the chunk-start state + key Gram
- * blocks; 1 + l layer l's forward, backward and clip / decay recurrences; layers + 1 the
- * state write.  Running every stage equals uttt_chunk_chain; it exists so a caller can
- * place timing events between the stages. */
+/* The same chain as layers + 1 stream-ordered stages, one per call, in order on one stream
+ * with one workspace.  Layers run in groups of 4: the stage of a group's last layer forms
+ * the group's products with the chunk-start state and runs each of its layers (key Gram row,
+ * forward / backward through the state left by the layers before it, the previous layer's
+ * clip / decay step); the other stages of a group launch nothing.  Stage `layers` is the last
+ * layer's step and the state write.
+ * Stage l reads only layers <= l, so only their k/v/eta/alpha pointers need to be set: a
+ * caller can run stage l (on a second stream) as soon as layer l's inputs exist, while it
+ * computes the next layers' forward passes.  The state write must follow every reader of the
+ * chunk-start state (the readouts).  Running every stage equals uttt_chunk_chain. */
 int uttt_chunk_chain_stage(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
                            int32_t stage, uttt_stream_t stream);
 

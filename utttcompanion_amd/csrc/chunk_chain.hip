@@ -24,10 +24,13 @@
 // chunk instead of once per layer, and W/S are written once per chunk instead of once per
 // layer.
 //
-// Launch sequence (one stream): init, pq, K-gram, then per layer l:
-//   up (U, G, H) -> H-gram -> down (Z partials) -> k_ln_grad (dZ, loss) -> dZ-gram
-//   -> back (dU, dG, norm partials) -> coef (clip, decay, recurrences);
-// then apply (final W, S and optional bf16 copies of W).
+// Launch sequence (one stream), layers in groups of kPqGroup: at the stage of a group's last
+// layer, pq (K_l W_s, K_l S_s for the group's layers), then per layer l of the group: K-gram
+// row l -> up (layer l - 1's clip / decay / recurrence step, then U, G, H) -> H-gram -> down
+// (Z partials) -> k_ln_grad (dZ, loss) -> dZ-gram -> back (dU, dG, norm partials); stage 0
+// first initialises the coefficient table; stage L: the last layer's recurrence step (coef) and
+// apply (final W, S and their bf16 copies).  Stage l reads only layers <= l, so a caller can
+// run it as soon as layer l's keys and values exist.
 #include "update_ln.h"
 #include "uttt_device.h"
 #include "uttt_host.h"
@@ -83,6 +86,21 @@ inline int row_tile_blocks(int B, int ntiles) {
   return (B >= kXcds ? (B + kXcds - 1) / kXcds * kXcds : B) * ntiles;
 }
 
+// Store N (4 or 8) consecutive values to LDS as T with one vector write (dst aligned to N * sizeof(T)).
+template <typename T, int N>
+__device__ __forceinline__ void store_vec(T* dst, const float* v) {
+  if constexpr (sizeof(T) == 2) {
+    typedef bf16 vec_t __attribute__((ext_vector_type(N)));
+    vec_t o;
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = from_f32<bf16>(v[i]);
+    *reinterpret_cast<vec_t*>(dst) = o;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) *reinterpret_cast<f32x4*>(dst + i) = f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]};
+  }
+}
+
 // dst[row][k] = scale * (register-staged fp32 64 x 64 tile), converted to T
 template <typename T>
 __device__ __forceinline__ void store_scaled(const RowStage<float, 64>& st, T* dst, int ldd, float scale) {
@@ -90,8 +108,10 @@ __device__ __forceinline__ void store_scaled(const RowStage<float, 64>& st, T* d
   for (int j = 0; j < RowStage<float, 64>::kN; ++j) {
     const int idx = threadIdx.x + j * kThreads;
     const int row = idx >> 4, c = idx & 15;
+    float v[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) dst[row * ldd + c * 4 + v] = from_f32<T>(scale * Lanes16<float>::get(st.r[j], v));
+    for (int q = 0; q < 4; ++q) v[q] = scale * Lanes16<float>::get(st.r[j], q);
+    store_vec<T, 4>(dst + row * ldd + c * 4, v);
   }
 }
 
@@ -119,10 +139,10 @@ struct CombColStage {
     const int kg = threadIdx.x / kColGroups, cg = threadIdx.x % kColGroups;
 #pragma unroll
     for (int v = 0; v < kVec; ++v) {
-      T* d = dst + (cg * kVec + v) * ldd + kg * 8;
+      float o[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        d[i] = from_f32<T>(ca * Lanes16<S>::get(rx[i], v) + cb * Lanes16<S>::get(ry[i], v));
+      for (int i = 0; i < 8; ++i) o[i] = ca * Lanes16<S>::get(rx[i], v) + cb * Lanes16<S>::get(ry[i], v);
+      store_vec<T, 8>(dst + (cg * kVec + v) * ldd + kg * 8, o);
     }
   }
 };
@@ -150,10 +170,10 @@ struct CombRowStage {
     for (int j = 0; j < kN; ++j) {
       const int idx = threadIdx.x + j * kThreads;
       const int row = idx / kPerRow, c = idx % kPerRow;
+      float o[kVec];
 #pragma unroll
-      for (int v = 0; v < kVec; ++v)
-        dst[row * ldd + c * kVec + v] =
-            from_f32<T>(ca * Lanes16<S>::get(rx[j], v) + cb * Lanes16<S>::get(ry[j], v));
+      for (int v = 0; v < kVec; ++v) o[v] = ca * Lanes16<S>::get(rx[j], v) + cb * Lanes16<S>::get(ry[j], v);
+      store_vec<T, kVec>(dst + row * ldd + c * kVec, o);
     }
   }
 };
@@ -174,6 +194,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_init(float* coef, int n) {
 // ---------------------------------------------------------------------------
 struct PqArgs {
   int B, L, C, D, F;
+  int l_begin, l_count;  // layers of this launch
   Acts acts;
   const void* x[4];  // fp32 state or its bf16 copies
   void* pq;  // (4, L, B, 64, F) act dtype
@@ -184,13 +205,13 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T bs[64 * LD];
   __shared__ __align__(16) T as[kPqGroup * 64 * LD];
-  const int nlg = (a.L + kPqGroup - 1) / kPqGroup;
+  const int nlg = (a.l_count + kPqGroup - 1) / kPqGroup;
   const RowTile rt = row_tile(blockIdx.x, a.B, 4 * (a.F / 64) * nlg);
   if (!rt.valid) return;
   // tile = (m, F tile, layer group) with the layer groups that share an X tile adjacent
   const int b = rt.b, lg = rt.tile % nlg, ft = (rt.tile / nlg) % (a.F / 64), m = rt.tile / (nlg * (a.F / 64));
-  const int f0 = ft * 64, l0 = lg * kPqGroup;
-  const int nl = min(kPqGroup, a.L - l0);
+  const int f0 = ft * 64, l0 = a.l_begin + lg * kPqGroup;
+  const int nl = min(kPqGroup, a.l_begin + a.l_count - l0);
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const WT* xs = static_cast<const WT*>(a.x[m]) + (int64_t)b * a.D * a.F + f0;
   const T* kr[kPqGroup];
@@ -235,16 +256,15 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. Gram blocks G[l][j] = X_l X_j^T over the feature dimension, one 32 x 32 block per
-//    single-wave workgroup, operands loaded straight from global memory (rows >= C are 0).
-//    Row mode (layer >= 0): blocks (layer, j) for j <= layer into out (B, 64, LL);
-//    all-pairs mode: every j <= l into out (B, LL, LL).
+// 2. Gram blocks G[l][j] = X_l X_j^T over the feature dimension for one layer l and every
+//    j <= l, operands loaded straight from global memory (rows >= C are 0).
 // ---------------------------------------------------------------------------
 struct GramArgs {
   int B, L, C, kd, LL, layer;
   int64_t rs, ts;  // row / token strides of X (elements)
   LayerPtrs x;
-  float* out;
+  float* out;      // row b's block row `layer` at out + (b * out_rows + out_r0) * LL
+  int out_rows, out_r0;
 };
 
 // One 32 x 32 quadrant per workgroup; the 4 waves take a quarter of the feature range each
@@ -252,21 +272,10 @@ struct GramArgs {
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
   __shared__ float part[3 * 16 * 64];
-  const int npairs = a.layer >= 0 ? a.layer + 1 : a.L * (a.L + 1) / 2;
-  const RowTile rt = row_tile(blockIdx.x, a.B, 4 * npairs);
+  const RowTile rt = row_tile(blockIdx.x, a.B, 4 * (a.layer + 1));
   if (!rt.valid) return;
   const int q = rt.tile & 3;  // 32 x 32 quadrant of the 64 x 64 block
-  const int blk = rt.tile >> 2, b = rt.b;
-  int l, j;
-  if (a.layer >= 0) {
-    l = a.layer;
-    j = blk;
-  } else {
-    l = (int)((sqrtf(8.f * (float)blk + 1.f) - 1.f) * 0.5f);
-    while ((l + 1) * (l + 2) / 2 <= blk) ++l;
-    while (l * (l + 1) / 2 > blk) --l;
-    j = blk - l * (l + 1) / 2;
-  }
+  const int j = rt.tile >> 2, b = rt.b, l = a.layer;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
   const int ti = (q >> 1) * 32 + r, tj = (q & 1) * 32 + r;
   const int kq = a.kd / 4, kb = wave * kq, ke = kb + kq;
@@ -310,8 +319,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
   }
   __syncthreads();
   if (wave != 0) return;
-  float* out = a.layer >= 0 ? a.out + (int64_t)b * 64 * a.LL
-                            : a.out + ((int64_t)b * a.LL + l * 64) * a.LL;
+  float* out = a.out + ((int64_t)b * a.out_rows + a.out_r0) * a.LL;
   const int c = j * 64 + (q & 1) * 32 + r;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -322,11 +330,120 @@ __global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// 3a. Per row: |g_l|^2, clip, decay, active flag, surprise; advance the recurrences.
+// ---------------------------------------------------------------------------
+struct CoefArgs {
+  int B, C, LL, l, nF;
+  float beta, max_norm, min_row_surprise;
+  const float* npart;
+  const float* hh;
+  const float* zz;
+  Acts acts;
+  const float* mask;
+  int64_t mask_rs;
+  const float* loss;  // (B, 64)
+  const float* src;   // coefficient table before layer l (B, kCoefStride)
+  float* dst;         // coefficient table after layer l
+  float* surprise;    // (L,)
+  float* row_loss;    // optional (L, B, 2)
+};
+
+// Layer l's clip, decay and active flag for row b, and the coefficient table after layer l,
+// left in `out` (LDS, kCoefStride floats).  All 256 threads call it.  With `publish` the
+// table goes to a.dst and the layer's surprise outputs are written.
+template <typename T>
+__device__ void advance_coef(const CoefArgs& a, int b, float* out, float* red, bool publish) {
+  __shared__ float sc[3];
+  const float* src = a.src + (int64_t)b * kCoefStride;
+  for (int i = threadIdx.x; i < kCoefStride; i += kThreads) out[i] = src[i];
+  float n2 = 0.f;
+  for (int i = threadIdx.x; i < a.nF; i += kThreads) n2 += a.npart[(int64_t)b * a.nF + i];
+  const float* hh = a.hh + (int64_t)b * 64 * a.LL + a.l * 64;
+  const float* zz = a.zz + (int64_t)b * 64 * a.LL + a.l * 64;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    const int64_t off = (int64_t)(idx >> 6) * a.LL + (idx & 63);
+    n2 += hh[off] * zz[off];
+  }
+  n2 = block_sum(n2, red);
+  const int t = threadIdx.x;
+  const T* al = layer_row<T>(a.acts.alpha, a.l, b, a.acts.ea_rs);
+  float mt = 0.f, at = 0.f;
+  if (t < a.C) {
+    mt = a.mask != nullptr ? a.mask[(int64_t)b * a.mask_rs + t] : 1.f;
+    at = to_f32(al[(int64_t)t * a.acts.ea_ts]);
+  }
+  const float lt = t < 64 ? a.loss[b * 64 + t] : 0.f;
+  const float asum = block_sum(at * mt, red);
+  const float msum = block_sum(mt, red);
+  const float any = block_sum(mt != 0.f ? 1.f : 0.f, red);
+  const float lsum = block_sum(lt, red);
+  if (threadIdx.x == 0) {
+    const float denom = a.mask != nullptr ? fmaxf(msum, 1.f) : (float)a.C;
+    const float row_mean = lsum / fmaxf(a.mask != nullptr ? msum : (float)a.C, 1.f);
+    const bool gated_off = a.min_row_surprise > 0.f && row_mean < a.min_row_surprise;
+    const bool active = (a.mask == nullptr || any > 0.f) && !gated_off;
+    sc[0] = a.max_norm > 0.f ? fminf(a.max_norm * (1.0f / sqrtf(n2 + 1e-8f)), 1.0f) : 1.0f;
+    sc[1] = 1.0f - asum / denom;
+    sc[2] = active ? 1.f : 0.f;
+    if (publish && a.row_loss != nullptr) {
+      a.row_loss[((int64_t)a.l * a.B + b) * 2] = lsum;
+      a.row_loss[((int64_t)a.l * a.B + b) * 2 + 1] = a.mask != nullptr ? msum : (float)a.C;
+    }
+  }
+  if (publish && b == 0 && threadIdx.x >= 192) {
+    // batch-global surprise of this layer: masked token losses over all rows / valid tokens
+    const int lane = threadIdx.x - 192;
+    float num = 0.f, den = 0.f;
+    for (int i = lane; i < a.B * 64; i += 64) {
+      const int bb = i >> 6, tt = i & 63;
+      num += a.loss[i];
+      if (tt < a.C) den += a.mask != nullptr ? a.mask[(int64_t)bb * a.mask_rs + tt] : 1.f;
+    }
+    num = wave_sum(num);
+    den = wave_sum(den);
+    if (lane == 0) a.surprise[a.l] = a.mask != nullptr ? num / fmaxf(den, 1.f) : num / den;
+  }
+  __syncthreads();
+  if (sc[2] != 0.f) {  // without tokens, or gated off, the layer leaves the row unchanged
+    const float c = sc[0], d = sc[1];
+    const int j = threadIdx.x;
+    const float e_new = a.beta * src[2];
+    if (j <= a.l) {
+      const float s_new = j < a.l ? a.beta * src[kSig + j] : -c;
+      out[kSig + j] = s_new;
+      out[kGam + j] = d * src[kGam + j] + s_new;
+    }
+    if (threadIdx.x == 0) {
+      out[0] = d * src[0];
+      out[1] = d * src[1] + e_new;
+      out[2] = e_new;
+      out[3] = src[3] + 1.f;
+    }
+  }
+  __syncthreads();
+  if (publish) {
+    float* dst = a.dst + (int64_t)b * kCoefStride;
+    for (int i = threadIdx.x; i < kCoefStride; i += kThreads) dst[i] = out[i];
+  }
+}
+
+// The last layer's recurrence step (every other layer's runs inside the next k_chain_up).
+template <typename T>
+__global__ void __launch_bounds__(kThreads) k_chain_coef(const CoefArgs a) {
+  __shared__ float red[4];
+  __shared__ float out[kCoefStride];
+  advance_coef<T>(a, blockIdx.x, out, red, true);
+}
+
+// ---------------------------------------------------------------------------
 // 3. Layer l forward through W_l: U, G (fp32, kept for the backward), H (act dtype)
 // ---------------------------------------------------------------------------
 struct UpArgs {
   int B, L, C, D, F, LL, l;
-  const float* coef;
+  CoefArgs prev;      // layer l - 1's recurrence step (l > 0): its table -> the table of layer l
+  const float* coef;  // table of layer l when l == 0
   const void* pq;
   const float* kk;  // (B, LL, LL)
   const void* du_all;
@@ -342,57 +459,65 @@ __global__ void __launch_bounds__(kThreads) k_chain_up(const UpArgs a) {
   __shared__ __align__(16) T as[2][64 * LD];
   __shared__ __align__(16) T bu[2][64 * LD];
   __shared__ __align__(16) T bg[2][64 * LD];
+  __shared__ float cf[kCoefStride];
+  __shared__ float red[4];
   const RowTile rt = row_tile(blockIdx.x, a.B, a.F / 64);
   if (!rt.valid) return;
   const int ft = rt.tile, b = rt.b, f0 = ft * 64;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
-  const float* cf = a.coef + (int64_t)b * kCoefStride;
-  const float ca = cf[0], cb = cf[1];
-  // the snapshot products of this tile: loads issued before the correction loop
+  // loads that do not depend on the coefficients go out first: this tile's snapshot products
+  // and the first correction tiles, so their latency overlaps the recurrence step below
   const int64_t plane = (int64_t)a.L * a.B * 64 * a.F;
   const T* pl = static_cast<const T*>(a.pq) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
   const int col = wc + acc_col();
-  float pu[16], pg[16];
+  T pw_u[16], pw_g[16], ps_u[16], ps_g[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
-    pu[i] = ca * to_f32(pl[off]);
-    pg[i] = ca * to_f32(pl[2 * plane + off]);
+    pw_u[i] = pl[off];
+    ps_u[i] = pl[plane + off];
+    pw_g[i] = pl[2 * plane + off];
+    ps_g[i] = pl[3 * plane + off];
   }
-  if (cb != 0.f) {
+  constexpr int U = ColStage<T, 64>::kUnits;
+  const bool up_half = threadIdx.x < U;
+  const int unit = up_half ? (int)threadIdx.x : min((int)threadIdx.x - U, U);
+  const T* dsrc = static_cast<const T*>(up_half ? a.du_all : a.dg_all) + (int64_t)b * 64 * a.F + f0;
+  const int64_t lstride = (int64_t)a.B * 64 * a.F;
+  const float* kk = a.kk + ((int64_t)b * a.LL + a.l * 64) * a.LL;
+  RowStage<float, 64> kst;
+  ColStage<T, 64> st;
+  if (a.l > 0) {
+    kst.load(kk, a.LL, 64);
+    st.load(dsrc, a.F, 64, unit);
+    // the previous layer's recurrence step: every F tile of the row derives the same table,
+    // the first one publishes it (and that layer's surprise) for the layer's later kernels
+    advance_coef<T>(a.prev, b, cf, red, ft == 0);
+  } else {
+    for (int i = threadIdx.x; i < kCoefStride; i += kThreads) cf[i] = a.coef[(int64_t)b * kCoefStride + i];
+    __syncthreads();
+  }
+  const float ca = cf[0], cb = cf[1];
+  float pu[16], pg[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
-      pu[i] += cb * to_f32(pl[plane + off]);
-      pg[i] += cb * to_f32(pl[3 * plane + off]);
-    }
+  for (int i = 0; i < 16; ++i) {
+    pu[i] = ca * to_f32(pw_u[i]) + cb * to_f32(ps_u[i]);
+    pg[i] = ca * to_f32(pw_g[i]) + cb * to_f32(ps_g[i]);
   }
   f32x16 au, ag;
   zero(au);
   zero(ag);
-  if (a.l > 0) {
-    constexpr int U = ColStage<T, 64>::kUnits;
-    const bool up_half = threadIdx.x < U;
-    const int unit = up_half ? (int)threadIdx.x : min((int)threadIdx.x - U, U);
-    const T* dsrc = static_cast<const T*>(up_half ? a.du_all : a.dg_all) + (int64_t)b * 64 * a.F + f0;
-    const int64_t lstride = (int64_t)a.B * 64 * a.F;
-    const float* kk = a.kk + ((int64_t)b * a.LL + a.l * 64) * a.LL;
-    RowStage<float, 64> kst;
-    ColStage<T, 64> st;
-    kst.load(kk, a.LL, 64);
-    st.load(dsrc, a.F, 64, unit);
-    for (int j = 0; j < a.l; ++j) {
-      const int buf = j & 1;
-      store_scaled<T>(kst, as[buf], LD, cf[kGam + j]);
-      st.template store<T>(up_half ? bu[buf] : bg[buf], LD);
-      __syncthreads();
-      if (j + 1 < a.l) {
-        kst.load(kk + (j + 1) * 64, a.LL, 64);
-        st.load(dsrc + (j + 1) * lstride, a.F, 64, unit);
-      }
-      wave_mma<T, 64>(au, as[buf] + wr * LD, LD, bu[buf] + wc * LD, LD);
-      wave_mma<T, 64>(ag, as[buf] + wr * LD, LD, bg[buf] + wc * LD, LD);
+  for (int j = 0; j < a.l; ++j) {
+    const int buf = j & 1;
+    store_scaled<T>(kst, as[buf], LD, cf[kGam + j]);
+    st.template store<T>(up_half ? bu[buf] : bg[buf], LD);
+    __syncthreads();
+    if (j + 1 < a.l) {
+      kst.load(kk + (j + 1) * 64, a.LL, 64);
+      st.load(dsrc + (j + 1) * lstride, a.F, 64, unit);
     }
+    wave_mma<T, 64>(au, as[buf] + wr * LD, LD, bu[buf] + wc * LD, LD);
+    wave_mma<T, 64>(ag, as[buf] + wr * LD, LD, bg[buf] + wc * LD, LD);
   }
   const int64_t lane_base = (int64_t)b * 64 * a.F + f0;
   T* h = static_cast<T*>(a.h_all) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
@@ -513,11 +638,16 @@ struct BackArgs {
   float* npart;  // (B, F / 64)
 };
 
+// Stages of the dH loop loaded per global round trip (the kernel runs about one workgroup per
+// CU, so registers are spent on loads in flight rather than on occupancy).
+template <typename T> constexpr int back_group() { return sizeof(T) == 2 ? 4 : 2; }
+
 template <typename T, typename WT>
 __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
   constexpr int LD = lds_ld<T>();
-  __shared__ __align__(16) T buf0[64 * LD];
-  __shared__ __align__(16) T buf1[64 * LD];
+  constexpr int NS = back_group<T>();
+  __shared__ __align__(16) T zs[NS * 64 * LD];  // dZ rows, then correction A tiles
+  __shared__ __align__(16) T ws[NS * 64 * LD];  // (a W_d + b S_d) rows, then H_j^T tiles
   __shared__ __align__(16) T dus[64 * LD];  // [t][f]
   __shared__ __align__(16) T dgs[64 * LD];
   __shared__ float red[4];
@@ -535,43 +665,66 @@ __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
   f32x16 acc;
   zero(acc);
   {
-    RowStage<T, KT> zst;
-    CombRowStage<WT> wst;
-    zst.load(dz, a.D, 64);
-    wst.load(wd, sd, a.D, with_s);
-    for (int d0 = 0; d0 < a.D; d0 += KT) {
-      zst.template store<T>(buf0, LD);
-      wst.template store<T>(buf1, LD, ca, cb);
-      __syncthreads();
-      if (d0 + KT < a.D) {
-        zst.load(dz + d0 + KT, a.D, 64);
-        wst.load(wd + d0 + KT, sd + d0 + KT, a.D, with_s);
+    RowStage<T, KT> zst[NS];
+    CombRowStage<WT> wst[NS];
+    auto load_group = [&](int d0) {
+#pragma unroll
+      for (int q = 0; q < NS; ++q) {
+        if (d0 + q * KT < a.D) {
+          zst[q].load(dz + d0 + q * KT, a.D, 64);
+          wst[q].load(wd + d0 + q * KT, sd + d0 + q * KT, a.D, with_s);
+        }
       }
-      wave_mma<T, KT>(acc, buf0 + wr * LD, LD, buf1 + wc * LD, LD);
+    };
+    load_group(0);
+    for (int d0 = 0; d0 < a.D; d0 += NS * KT) {
+#pragma unroll
+      for (int q = 0; q < NS; ++q) {
+        if (d0 + q * KT < a.D) {
+          zst[q].template store<T>(zs + q * 64 * LD, LD);
+          wst[q].template store<T>(ws + q * 64 * LD, LD, ca, cb);
+        }
+      }
+      __syncthreads();
+      if (d0 + NS * KT < a.D) load_group(d0 + NS * KT);
+#pragma unroll
+      for (int q = 0; q < NS; ++q)
+        if (d0 + q * KT < a.D) wave_mma<T, KT>(acc, zs + q * 64 * LD + wr * LD, LD, ws + q * 64 * LD + wc * LD, LD);
       __syncthreads();
     }
   }
-  if (a.l > 0) {  // sum_j gam_j (dZ_l dZ_j^T) H_j, double-buffered through dus / dgs
+  if (a.l > 0) {  // sum_j gam_j (dZ_l dZ_j^T) H_j, two layers per round trip
+    constexpr int NJ = 2;
     const T* hsrc = static_cast<const T*>(a.h_all) + (int64_t)b * 64 * a.F + f0;
     const int64_t lstride = (int64_t)a.B * 64 * a.F;
     const float* zz = a.zz + (int64_t)b * 64 * a.LL;
-    RowStage<float, 64> zst;
-    ColStage<T, 64> st;
-    zst.load(zz, a.LL, 64);
-    st.load(hsrc, a.F, 64, threadIdx.x);
-    for (int j = 0; j < a.l; ++j) {
-      T* abuf = (j & 1) ? dus : buf0;
-      T* bbuf = (j & 1) ? dgs : buf1;
-      store_scaled<T>(zst, abuf, LD, cf[kGam + j]);
-      st.template store<T>(bbuf, LD);
-      __syncthreads();
-      if (j + 1 < a.l) {
-        zst.load(zz + (j + 1) * 64, a.LL, 64);
-        st.load(hsrc + (j + 1) * lstride, a.F, 64, threadIdx.x);
+    RowStage<float, 64> zst[NJ];
+    ColStage<T, 64> st[NJ];
+    auto load_pair = [&](int j0) {
+#pragma unroll
+      for (int q = 0; q < NJ; ++q) {
+        if (j0 + q < a.l) {
+          zst[q].load(zz + (j0 + q) * 64, a.LL, 64);
+          st[q].load(hsrc + (j0 + q) * lstride, a.F, 64, threadIdx.x);
+        }
       }
-      wave_mma<T, 64>(acc, abuf + wr * LD, LD, bbuf + wc * LD, LD);
+    };
+    load_pair(0);
+    for (int j0 = 0; j0 < a.l; j0 += NJ) {
+#pragma unroll
+      for (int q = 0; q < NJ; ++q) {
+        if (j0 + q < a.l) {
+          store_scaled<T>(zst[q], zs + q * 64 * LD, LD, cf[kGam + j0 + q]);
+          st[q].template store<T>(ws + q * 64 * LD, LD);
+        }
+      }
+      __syncthreads();
+      if (j0 + NJ < a.l) load_pair(j0 + NJ);
+#pragma unroll
+      for (int q = 0; q < NJ; ++q)
+        if (j0 + q < a.l) wave_mma<T, 64>(acc, zs + q * 64 * LD + wr * LD, LD, ws + q * 64 * LD + wc * LD, LD);
+      __syncthreads();
     }
-    __syncthreads();  // dus / dgs are rewritten below
   }
   const int64_t base = (int64_t)b * 64 * a.F + f0;
   const int64_t lbase = ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
@@ -601,102 +754,6 @@ __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
   for (int i = 0; i < 16; ++i) part += (gu[i] + gg[i]) * kk[(int64_t)(wr + acc_row(i)) * a.LL + wc + acc_col()];
   const float total = block_sum(part, red);
   if (threadIdx.x == 0) a.npart[(int64_t)b * (a.F / 64) + ft] = total;
-}
-
-// ---------------------------------------------------------------------------
-// 6. Per row: |g_l|^2, clip, decay, active flag, surprise; advance the recurrences.
-// ---------------------------------------------------------------------------
-struct CoefArgs {
-  int B, C, LL, l, nF;
-  float beta, max_norm, min_row_surprise;
-  const float* npart;
-  const float* hh;
-  const float* zz;
-  Acts acts;
-  const float* mask;
-  int64_t mask_rs;
-  const float* loss;  // (B, 64)
-  float* coef;
-  float* surprise;  // (L,)
-  float* row_loss;  // optional (L, B, 2)
-};
-
-template <typename T>
-__global__ void __launch_bounds__(kThreads) k_chain_coef(const CoefArgs a) {
-  __shared__ float red[4];
-  __shared__ float sc[3];
-  const int b = blockIdx.x;
-  float n2 = 0.f;
-  for (int i = threadIdx.x; i < a.nF; i += kThreads) n2 += a.npart[(int64_t)b * a.nF + i];
-  const float* hh = a.hh + (int64_t)b * 64 * a.LL + a.l * 64;
-  const float* zz = a.zz + (int64_t)b * 64 * a.LL + a.l * 64;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int idx = threadIdx.x + i * kThreads;
-    const int64_t off = (int64_t)(idx >> 6) * a.LL + (idx & 63);
-    n2 += hh[off] * zz[off];
-  }
-  n2 = block_sum(n2, red);
-  const int t = threadIdx.x;
-  const T* al = layer_row<T>(a.acts.alpha, a.l, b, a.acts.ea_rs);
-  float mt = 0.f, at = 0.f;
-  if (t < a.C) {
-    mt = a.mask != nullptr ? a.mask[(int64_t)b * a.mask_rs + t] : 1.f;
-    at = to_f32(al[(int64_t)t * a.acts.ea_ts]);
-  }
-  const float lt = t < 64 ? a.loss[b * 64 + t] : 0.f;
-  const float asum = block_sum(at * mt, red);
-  const float msum = block_sum(mt, red);
-  const float any = block_sum(mt != 0.f ? 1.f : 0.f, red);
-  const float lsum = block_sum(lt, red);
-  if (threadIdx.x == 0) {
-    const float denom = a.mask != nullptr ? fmaxf(msum, 1.f) : (float)a.C;
-    const float row_mean = lsum / fmaxf(a.mask != nullptr ? msum : (float)a.C, 1.f);
-    const bool gated_off = a.min_row_surprise > 0.f && row_mean < a.min_row_surprise;
-    const bool active = (a.mask == nullptr || any > 0.f) && !gated_off;
-    sc[0] = a.max_norm > 0.f ? fminf(a.max_norm * (1.0f / sqrtf(n2 + 1e-8f)), 1.0f) : 1.0f;
-    sc[1] = 1.0f - asum / denom;
-    sc[2] = active ? 1.f : 0.f;
-    if (a.row_loss != nullptr) {
-      a.row_loss[((int64_t)a.l * a.B + b) * 2] = lsum;
-      a.row_loss[((int64_t)a.l * a.B + b) * 2 + 1] = a.mask != nullptr ? msum : (float)a.C;
-    }
-  }
-  if (b == 0 && threadIdx.x >= 192) {
-    // batch-global surprise of this layer: masked token losses over all rows / valid tokens
-    const int lane = threadIdx.x - 192;
-    float num = 0.f, den = 0.f;
-    for (int i = lane; i < a.B * 64; i += 64) {
-      const int bb = i >> 6, tt = i & 63;
-      num += a.loss[i];
-      if (tt < a.C) den += a.mask != nullptr ? a.mask[(int64_t)bb * a.mask_rs + tt] : 1.f;
-    }
-    num = wave_sum(num);
-    den = wave_sum(den);
-    if (lane == 0) a.surprise[a.l] = a.mask != nullptr ? num / fmaxf(den, 1.f) : num / den;
-  }
-  __syncthreads();
-  if (sc[2] == 0.f) return;  // no tokens, or gated off: this layer leaves the row unchanged
-  const float c = sc[0], d = sc[1];
-  float* cf = a.coef + (int64_t)b * kCoefStride;
-  // read every old value before any thread writes
-  const float a_old = cf[0], b_old = cf[1], e_old = cf[2];
-  const int j = threadIdx.x;
-  const float sig_old = j < a.l ? cf[kSig + j] : 0.f;
-  const float gam_old = j < a.l ? cf[kGam + j] : 0.f;
-  __syncthreads();
-  const float e_new = a.beta * e_old;
-  if (j <= a.l) {
-    const float s_new = j < a.l ? a.beta * sig_old : -c;
-    cf[kSig + j] = s_new;
-    cf[kGam + j] = d * gam_old + s_new;
-  }
-  if (threadIdx.x == 0) {
-    cf[0] = d * a_old;
-    cf[1] = d * b_old + e_new;
-    cf[2] = e_new;
-    cf[3] += 1.f;
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -860,7 +917,7 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
   c.zp = take(sizeof(float) * (c.nsplit + (L - 1 + kCorrPerSplit - 1) / kCorrPerSplit + 1) * B * 64 * D);
   c.loss = take(sizeof(float) * B * 64);
   c.npart = take(sizeof(float) * B * nF);
-  c.coef = take(sizeof(float) * B * kCoefStride);
+  c.coef = take(sizeof(float) * 2 * B * kCoefStride);  // tables of even / odd layers
   c.total = off;
   return c;
 }
@@ -898,9 +955,10 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   const int64_t lf = (int64_t)B * 64 * F, ld = (int64_t)B * 64 * D;
   const size_t e = sizeof(T);
 
-  // stage 0: coefficient init, snapshot products, key Gram; stage 1 + l: layer l; stage L + 1: apply
+  // stage l (< L): layer l (stage 0 also initialises the coefficient table); stage L: the last
+  // layer's recurrence step and the state write
   auto want = [&](int stage) { return first <= stage && stage <= last; };
-  const int ncoef = B * kCoefStride;
+  const int ncoef = B * kCoefStride;  // table of layer 0
   if (want(0))
     hipLaunchKernelGGL(k_chain_init, dim3((ncoef + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef);
 
@@ -914,24 +972,16 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     pa.x[0] = a.w_up; pa.x[1] = a.s_up; pa.x[2] = a.w_gate; pa.x[3] = a.s_gate;
   }
   pa.pq = ws + c.pq;
-  const dim3 pq_grid(row_tile_blocks(B, 4 * nF * ((L + kPqGroup - 1) / kPqGroup)));
-  if (want(0)) {
-    if (bf16_src)
-      hipLaunchKernelGGL((k_chain_pq<T, bf16>), pq_grid, blk, 0, st, pa);
-    else
-      hipLaunchKernelGGL((k_chain_pq<T, float>), pq_grid, blk, 0, st, pa);
-  }
+  const dim3 pq_grid(row_tile_blocks(B, 4 * nF));  // one layer group per launch
   const void* wd_src = bf16_src ? a.w_down_copy : static_cast<const void*>(a.w_down);
   const void* sd_src = bf16_src ? a.s_down_copy : static_cast<const void*>(a.s_down);
 
-  GramArgs ka{};
-  ka.B = B; ka.L = L; ka.C = C; ka.kd = D; ka.LL = LL; ka.layer = -1; ka.rs = a.kv_row_stride; ka.ts = D;
-  ka.x = acts.k; ka.out = kk;
-  if (want(0))
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (L * (L + 1) / 2))), blk, 0, st, ka);
+  GramArgs ka{};  // K_l K_j^T rows of the key Gram (B, LL, LL)
+  ka.B = B; ka.L = L; ka.C = C; ka.kd = D; ka.LL = LL; ka.rs = a.kv_row_stride; ka.ts = D;
+  ka.x = acts.k; ka.out = kk; ka.out_rows = LL;
 
   GramArgs ha{};  // H_l H_j^T and dZ_l dZ_j^T: the layer buffers have stride 64 rows per row b
-  ha.B = B; ha.L = L; ha.C = C; ha.LL = LL;
+  ha.B = B; ha.L = L; ha.C = C; ha.LL = LL; ha.out_rows = 64; ha.out_r0 = 0;
   GramArgs za = ha;
   ha.kd = F; ha.rs = (int64_t)64 * F; ha.ts = F; ha.out = hh;
   za.kd = D; za.rs = (int64_t)64 * D; za.ts = D; za.out = zz;
@@ -940,11 +990,42 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     za.x.p[l] = static_cast<char*>(dz_all) + e * l * ld;
   }
 
+  // coefficient table of layer l (the state before layer l's update) at table(l); layer l's
+  // recurrence step runs inside layer l + 1's k_chain_up, the last one in k_chain_coef
+  auto table = [&](int l) { return coef + (size_t)(l & 1) * B * kCoefStride; };
+  auto coef_step = [&](int l) {
+    CoefArgs ca{};
+    ca.B = B; ca.C = C; ca.LL = LL; ca.l = l; ca.nF = nF;
+    ca.beta = a.momentum_beta; ca.max_norm = a.max_inner_grad_norm; ca.min_row_surprise = a.min_row_surprise;
+    ca.npart = npart; ca.hh = hh; ca.zz = zz; ca.acts = acts;
+    ca.mask = a.token_mask; ca.mask_rs = a.mask_row_stride; ca.loss = loss;
+    ca.src = table(l); ca.dst = table(l + 1);
+    ca.surprise = a.surprise; ca.row_loss = a.row_loss;
+    return ca;
+  };
+  // Layers run in groups of kPqGroup: once a group's last layer is known (its stage), one
+  // launch forms the snapshot products of the whole group, then each layer of the group runs.
+  // Stages of the other layers of a group launch nothing.
   for (int l = 0; l < L; ++l) {
-    if (!want(1 + l)) continue;
+    const int g0 = l - l % kPqGroup, g1 = min(L, g0 + kPqGroup);  // this layer's group [g0, g1)
+    if (!want(g1 - 1)) continue;
+    if (l == g0) {
+      pa.l_begin = g0;
+      pa.l_count = g1 - g0;
+      if (bf16_src)
+        hipLaunchKernelGGL((k_chain_pq<T, bf16>), pq_grid, blk, 0, st, pa);
+      else
+        hipLaunchKernelGGL((k_chain_pq<T, float>), pq_grid, blk, 0, st, pa);
+    }
+    const float* cl = table(l);
+    ka.layer = l;  // key Gram row l
+    ka.out_r0 = l * 64;
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (l + 1))), blk, 0, st, ka);
+
     UpArgs ua{};
     ua.B = B; ua.L = L; ua.C = C; ua.D = D; ua.F = F; ua.LL = LL; ua.l = l;
-    ua.coef = coef; ua.pq = ws + c.pq; ua.kk = kk; ua.du_all = du_all; ua.dg_all = dg_all;
+    if (l > 0) ua.prev = coef_step(l - 1);
+    ua.coef = cl; ua.pq = ws + c.pq; ua.kk = kk; ua.du_all = du_all; ua.dg_all = dg_all;
     ua.u_cur = u_cur; ua.g_cur = g_cur; ua.h_all = h_all;
     hipLaunchKernelGGL(k_chain_up<T>, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
 
@@ -953,7 +1034,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
     DownArgs da{};
     da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
-    da.coef = coef; da.h_all = h_all; da.wd = wd_src; da.sd = sd_src; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
+    da.coef = cl; da.h_all = h_all; da.wd = wd_src; da.sd = sd_src; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
     const int ncorr = (l + kCorrPerSplit - 1) / kCorrPerSplit;
     const dim3 down_grid(row_tile_blocks(B, (D / 64) * (c.nsplit + ncorr)));
     if (bf16_src)
@@ -977,24 +1058,21 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
     BackArgs ba{};
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
-    ba.coef = coef; ba.dz_all = dz_all; ba.wd = wd_src; ba.sd = sd_src; ba.zz = zz; ba.h_all = h_all;
+    ba.coef = cl; ba.dz_all = dz_all; ba.wd = wd_src; ba.sd = sd_src; ba.zz = zz; ba.h_all = h_all;
     ba.u_cur = u_cur; ba.g_cur = g_cur; ba.kk = kk; ba.du_all = du_all; ba.dg_all = dg_all; ba.npart = npart;
     if (bf16_src)
       hipLaunchKernelGGL((k_chain_back<T, bf16>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
     else
       hipLaunchKernelGGL((k_chain_back<T, float>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
 
-    CoefArgs ca{};
-    ca.B = B; ca.C = C; ca.LL = LL; ca.l = l; ca.nF = nF;
-    ca.beta = a.momentum_beta; ca.max_norm = a.max_inner_grad_norm; ca.min_row_surprise = a.min_row_surprise;
-    ca.npart = npart; ca.hh = hh; ca.zz = zz; ca.acts = acts;
-    ca.mask = a.token_mask; ca.mask_rs = a.mask_row_stride; ca.loss = loss; ca.coef = coef;
-    ca.surprise = a.surprise; ca.row_loss = a.row_loss;
-    hipLaunchKernelGGL(k_chain_coef<T>, dim3(B), blk, 0, st, ca);
   }
 
+  if (want(L)) {
+    const CoefArgs last = coef_step(L - 1);
+    hipLaunchKernelGGL(k_chain_coef<T>, dim3(B), blk, 0, st, last);
+  }
   ApplyChainArgs aa{};
-  aa.B = B; aa.L = L; aa.C = C; aa.D = D; aa.F = F; aa.coef = coef; aa.acts = acts;
+  aa.B = B; aa.L = L; aa.C = C; aa.D = D; aa.F = F; aa.coef = table(L); aa.acts = acts;
   aa.h_all = h_all; aa.du_all = du_all; aa.dg_all = dg_all; aa.dz_all = dz_all;
   aa.w[0] = a.w_up; aa.w[1] = a.w_gate; aa.w[2] = a.w_down;
   aa.s[0] = a.s_up; aa.s[1] = a.s_gate; aa.s[2] = a.s_down;
@@ -1004,7 +1082,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   aa.sc[0] = static_cast<bf16*>(a.s_up_copy);
   aa.sc[1] = static_cast<bf16*>(a.s_gate_copy);
   aa.sc[2] = static_cast<bf16*>(a.s_down_copy);
-  if (want(L + 1))
+  if (want(L))
     hipLaunchKernelGGL(k_chain_apply<T>, dim3(row_tile_blocks(B, 3 * (D / 64) * nF)), blk, 0, st, aa);
 }
 
@@ -1039,7 +1117,8 @@ static int run_chain(const uttt_chunk_chain_args* a, void* workspace, size_t wor
   UTTT_REQUIRE(a->tokens >= 1 && a->tokens <= 64, "tokens per chunk must be in [1, 64] (got %lld)",
                (long long)a->tokens);
   const int64_t vec = a->act_dtype == UTTT_DTYPE_BF16 ? 8 : 4;
-  for (int64_t l = 0; l < a->layers; ++l) {
+  const int64_t known = last < a->layers ? (int64_t)last + 1 : a->layers;  // layers these stages read
+  for (int64_t l = 0; l < known; ++l) {
     UTTT_REQUIRE(a->k[l] && a->v[l] && a->eta[l] && a->alpha[l], "k/v/eta/alpha of layer %lld must be non-NULL",
                  (long long)l);
     UTTT_REQUIRE(aligned16(a->k[l]) && aligned16(a->v[l]), "k/v of layer %lld must be 16-byte aligned", (long long)l);
@@ -1082,6 +1161,6 @@ extern "C" int uttt_chunk_chain(const uttt_chunk_chain_args* a, void* workspace,
 extern "C" int uttt_chunk_chain_stage(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes,
                                       int32_t stage, uttt_stream_t stream) {
   UTTT_REQUIRE(a != nullptr, "args is NULL");
-  UTTT_REQUIRE(stage >= 0 && stage <= a->layers + 1, "stage must be in [0, layers + 1] (got %d)", stage);
+  UTTT_REQUIRE(stage >= 0 && stage <= a->layers, "stage must be in [0, layers] (got %d)", stage);
   return run_chain(a, workspace, workspace_bytes, stream, stage, stage);
 }

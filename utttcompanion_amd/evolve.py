@@ -138,13 +138,21 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
     pool = model.fast_weight_pool
     clip = float(pool.max_inner_grad_norm or 0.0)
     ws_chain = ws_read = None
+    main = torch.cuda.current_stream(dev)
+    side = model._chain_stream(dev)  # the layer chain runs one layer behind the forward pass
     for ci in range(n_chunks):
         rows, off = active[ci], ci * c
         end = off + c
         cur_mask = mask[:rows, off:end]
         hid = h[:rows, off:end].contiguous()  # this chunk's residual stream, updated in place
         rd = [t[:rows] for t in read]
-        ks, vs, etas, alphas = [], [], [], []
+        chunk_rl = torch.empty((n_layers, rows, 2), dtype=torch.float32, device=dev)
+        run = K.ChunkChainRun(n_layers, c, [t[:rows] for t in cur], ln_w, ln_b, cur_mask, pool.momentum_beta, clip,
+                              pool.normalize_loss_by_dim, pool.eps, dt,
+                              copies=None if copies is None else [t[:rows] for t in copies],
+                              surprise=surprise[ci], row_loss=chunk_rl, min_row_surprise=min_chunk_surprise,
+                              workspace=ws_chain)
+        ws_chain = run.workspace
         for li, block in enumerate(model.layers):
             attn = block.attn
             kb, vb = k_bufs[li][:rows], v_bufs[li][:rows]
@@ -153,22 +161,17 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
             K.swa_prefill(q.transpose(1, 2), kb, vb, win, off, out=att.transpose(1, 2), kv_len=end)
             hid = linear_residual(hid, att.view(rows, c, -1), attn.wo.weight)
             uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                run.add_layer(uk, uv, eta, alpha)
             if ws_read is None:
                 ws_read = K.readout_workspace(uq, rd[0])
             hid = linear_residual(hid, K.swiglu_readout(uq, *rd, ln_w, ln_b, pool.eps, workspace=ws_read),
                                   block.uttt.w_o.weight)
-            ks.append(uk)
-            vs.append(uv)
-            etas.append(eta)
-            alphas.append(alpha)
-        chunk_rl = torch.empty((n_layers, rows, 2), dtype=torch.float32, device=dev)
-        chain = K.prepare_chunk_chain(ks, vs, etas, alphas, [t[:rows] for t in cur], ln_w, ln_b, cur_mask,
-                                      pool.momentum_beta, clip, pool.normalize_loss_by_dim, pool.eps,
-                                      copies=None if copies is None else [t[:rows] for t in copies],
-                                      surprise=surprise[ci], row_loss=chunk_rl,
-                                      min_row_surprise=min_chunk_surprise, workspace=ws_chain)
-        ws_chain = chain.workspace
-        chain.launch()
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            run.finish()
+        main.wait_stream(side)
         row_loss[:, :rows] += chunk_rl
 
     final = cur

@@ -265,11 +265,12 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
 class PreparedChain:
     """A validated ``uttt_chunk_chain`` call; ``launch()`` enqueues it on the current stream."""
 
-    def __init__(self, args, keep, workspace, result, device):
+    def __init__(self, args, keep, workspace, result, device, n_layers):
         self.args, self._keep, self.workspace, self.result, self.device = args, keep, workspace, result, device
+        self.n_layers = n_layers
 
     def launch(self, stage: Optional[int] = None) -> Tuple[Tensor, Optional[Tensor]]:
-        """Enqueue the whole chain, or one of its ``layers + 2`` stream-ordered stages."""
+        """Enqueue the whole chain, or one of its ``layers + 1`` stream-ordered stages."""
         lib = N.load_library()
         with torch.cuda.device(self.device):
             if stage is None:
@@ -289,6 +290,132 @@ def _inplace_state(t: Tensor, name: str) -> Tensor:
     return t
 
 
+class ChunkChainRun(PreparedChain):
+    """One chunk's layer chain fed layer by layer (``uttt_chunk_chain_stage``).
+
+    ``add_layer(k, v, eta, alpha)`` records layer l's inputs and enqueues stage l on the
+    current stream; it reads only layers <= l, so it can run while the caller computes the
+    next layers.  ``finish()`` enqueues the last stage (the state write), which must follow
+    every reader of the chunk-start state and its copies.  Arguments as ``prepare_chunk_chain``
+    with the layer count and chunk length given up front."""
+
+    def __init__(self, n_layers: int, tokens: int, state: Sequence[Tensor], ln_weight: Tensor, ln_bias: Tensor,
+                 token_mask: Optional[Tensor], momentum_beta: float, max_inner_grad_norm: float,
+                 normalize_by_dim: bool, eps: float, act_dtype: torch.dtype,
+                 copies: Optional[Sequence[Tensor]] = None, surprise: Optional[Tensor] = None,
+                 row_loss: Optional[Tensor] = None, min_row_surprise: float = 0.0,
+                 workspace: Optional[Tensor] = None) -> None:
+        if not 1 <= n_layers <= N.MAX_CHAIN:
+            raise ValueError(f"need 1..{N.MAX_CHAIN} layers")
+        if not 1 <= tokens <= 64:
+            raise ValueError(f"a chunk holds 1..64 tokens on the HIP path, got {tokens}")
+        code = _act_code(act_dtype)
+        w_up, w_gate, w_down, s_up, s_gate, s_down = (_inplace_state(t, n) for t, n in zip(
+            state, ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")))
+        bsz, dim, ff = w_up.shape
+        dev = w_up.device
+        if w_gate.shape != (bsz, dim, ff) or w_down.shape != (bsz, ff, dim) \
+                or s_up.shape != w_up.shape or s_gate.shape != w_gate.shape or s_down.shape != w_down.shape:
+            raise ValueError(f"state shapes do not match B={bsz}, D={dim}, F={ff}")
+        if dim % 64 or ff % 64 or dim > 4096:
+            raise ValueError(f"d_model and d_ff must be multiples of 64 (d_model <= 4096); got {dim}, {ff}")
+        _require_device(dev, *state, ln_weight, ln_bias, token_mask)
+        _forward_only(*state)
+        mask = None
+        keep = []
+        if token_mask is not None:
+            if token_mask.shape != (bsz, tokens):
+                raise ValueError(f"token_mask must be (B, C) = ({bsz}, {tokens})")
+            mask = token_mask.to(torch.float32)
+            if tokens > 1 and mask.stride(1) != 1:
+                mask = mask.contiguous()
+            keep.append(mask)
+        ln_w = ln_weight.to(torch.float32).contiguous()
+        ln_b = ln_bias.to(torch.float32).contiguous()
+        if ln_w.numel() != dim or ln_b.numel() != dim:
+            raise ValueError("ln_weight / ln_bias must have d_model elements")
+        if copies is not None:
+            if act_dtype != torch.bfloat16:
+                raise ValueError("bf16 state copies go with bf16 activations only")
+            if len(copies) != 6 or any(c.dtype != torch.bfloat16 or not c.is_contiguous() or c.shape != w.shape
+                                       or c.device != dev or c.data_ptr() % 16
+                                       for c, w in zip(copies, (w_up, w_gate, w_down, s_up, s_gate, s_down))):
+                raise ValueError("copies must be six contiguous, aligned bf16 tensors shaped like the state")
+        if surprise is None:
+            surprise = torch.empty(n_layers, dtype=torch.float32, device=dev)
+        elif surprise.shape != (n_layers,) or surprise.dtype != torch.float32 or not surprise.is_contiguous():
+            raise ValueError("surprise must be a contiguous fp32 (layers,) tensor")
+        if row_loss is not None and (row_loss.shape != (n_layers, bsz, 2) or row_loss.dtype != torch.float32
+                                     or not row_loss.is_contiguous()):
+            raise ValueError("row_loss must be a contiguous fp32 (layers, B, 2) tensor")
+        if not math.isfinite(min_row_surprise) or min_row_surprise < 0:
+            raise ValueError("min_row_surprise must be finite and >= 0")
+        nbytes = N.load_library().uttt_chunk_chain_workspace(bsz, n_layers, dim, ff, code)
+        if nbytes == 0:
+            raise ValueError("unsupported layer chain dimensions")
+        if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        a = N.ChunkChainArgs()
+        a.batch, a.layers, a.tokens, a.d_model, a.d_ff = bsz, n_layers, tokens, dim, ff
+        a.act_dtype, a.normalize_by_dim = code, int(bool(normalize_by_dim))
+        a.momentum_beta, a.max_inner_grad_norm, a.eps = (float(momentum_beta), float(max_inner_grad_norm or 0.0),
+                                                         float(eps))
+        a.min_row_surprise = float(min_row_surprise)
+        a.token_mask, a.mask_row_stride = _p(mask), (mask.stride(0) if mask is not None else 0)
+        a.w_up, a.w_gate, a.w_down, a.s_up, a.s_gate, a.s_down = (_p(t) for t in
+                                                                  (w_up, w_gate, w_down, s_up, s_gate, s_down))
+        a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
+        if copies is not None:
+            (a.w_up_copy, a.w_gate_copy, a.w_down_copy,
+             a.s_up_copy, a.s_gate_copy, a.s_down_copy) = (_p(c) for c in copies)
+        a.surprise, a.row_loss = _p(surprise), _p(row_loss)
+        keep += [ln_w, ln_b, state, copies]
+        super().__init__(a, keep, workspace, (surprise, row_loss), dev, n_layers)
+        self._act, self._shape = act_dtype, (bsz, tokens, dim)
+        self.layers_added = 0
+
+    def set_layer(self, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor) -> int:
+        """Record the next layer's inputs without launching; returns its index."""
+        l = self.layers_added
+        if l >= self.n_layers:
+            raise ValueError("all layers of the chain were already given")
+        bsz, tokens, dim = self._shape
+        act = self._act
+        if k.shape != (bsz, tokens, dim) or v.shape != k.shape or k.dtype != act or v.dtype != act:
+            raise ValueError(f"layer {l}: k/v must be ({bsz}, {tokens}, {dim}) {act}")
+        _require_device(self.device, k, v, eta, alpha)
+        _forward_only(k, v, eta, alpha)
+        k, v = _rows(k), _rows(v)
+        e, al = _row_vector(eta, act), _row_vector(alpha, act)
+        if e.shape != (bsz, tokens) or al.shape != (bsz, tokens):
+            raise ValueError(f"layer {l}: eta/alpha must be ({bsz}, {tokens}) or ({bsz}, {tokens}, 1)")
+        a = self.args
+        if l == 0:
+            a.kv_row_stride, a.ea_row_stride = k.stride(0), e.stride(0)
+        if bsz > 1 and (k.stride(0) != a.kv_row_stride or v.stride(0) != a.kv_row_stride):
+            k, v = k.contiguous(), v.contiguous()
+            if k.stride(0) != a.kv_row_stride:
+                raise ValueError("all layers' k/v must share one row stride")
+        if bsz > 1 and (e.stride(0) != a.ea_row_stride or al.stride(0) != a.ea_row_stride):
+            e, al = e.contiguous(), al.contiguous()
+            if e.stride(0) != a.ea_row_stride:
+                raise ValueError("all layers' eta/alpha must share one row stride")
+        a.k[l], a.v[l], a.eta[l], a.alpha[l] = _p(k), _p(v), _p(e), _p(al)
+        self._keep += [k, v, e, al]
+        self.layers_added = l + 1
+        return l
+
+    def add_layer(self, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor) -> None:
+        """Record layer l's inputs and enqueue stage l on the current stream."""
+        self.launch(self.set_layer(k, v, eta, alpha))
+
+    def finish(self) -> Tuple[Tensor, Optional[Tensor]]:
+        """Enqueue the state write (after every layer was added)."""
+        if self.layers_added != self.n_layers:
+            raise ValueError(f"{self.layers_added} of {self.n_layers} layers were given")
+        return self.launch(self.n_layers)
+
+
 def prepare_chunk_chain(ks: Sequence[Tensor], vs: Sequence[Tensor], etas: Sequence[Tensor],
                         alphas: Sequence[Tensor], state: Sequence[Tensor], ln_weight: Tensor, ln_bias: Tensor,
                         token_mask: Optional[Tensor], momentum_beta: float, max_inner_grad_norm: float,
@@ -305,94 +432,14 @@ def prepare_chunk_chain(ks: Sequence[Tensor], vs: Sequence[Tensor], etas: Sequen
     n_layers = len(ks)
     if not 1 <= n_layers <= N.MAX_CHAIN or not (len(vs) == len(etas) == len(alphas) == n_layers):
         raise ValueError(f"need 1..{N.MAX_CHAIN} layers with k, v, eta and alpha each")
-    bsz, tokens, dim = ks[0].shape
-    if not 1 <= tokens <= 64:
-        raise ValueError(f"a chunk holds 1..64 tokens on the HIP path, got {tokens}")
-    act = ks[0].dtype
-    code = _act_code(act)
-    dev = ks[0].device
-    w_up, w_gate, w_down, s_up, s_gate, s_down = (_inplace_state(t, n) for t, n in zip(
-        state, ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")))
-    ff = w_up.shape[-1]
-    if w_up.shape != (bsz, dim, ff) or w_gate.shape != (bsz, dim, ff) or w_down.shape != (bsz, ff, dim) \
-            or s_up.shape != w_up.shape or s_gate.shape != w_gate.shape or s_down.shape != w_down.shape:
-        raise ValueError(f"state shapes do not match B={bsz}, D={dim}, F={ff}")
-    if dim % 64 or ff % 64 or dim > 4096:
-        raise ValueError(f"d_model and d_ff must be multiples of 64 (d_model <= 4096); got {dim}, {ff}")
-    _require_device(dev, *ks, *vs, *etas, *alphas, *state, ln_weight, ln_bias, token_mask)
-    _forward_only(*ks, *vs, *etas, *alphas, *state)
-    a = N.ChunkChainArgs()
-    keep = []
-    kv_rs = ea_rs = None
+    if ks[0].dim() != 3:
+        raise ValueError("k must be (B, C, D)")
+    run = ChunkChainRun(n_layers, ks[0].shape[1], state, ln_weight, ln_bias, token_mask, momentum_beta,
+                        max_inner_grad_norm, normalize_by_dim, eps, ks[0].dtype, copies=copies, surprise=surprise,
+                        row_loss=row_loss, min_row_surprise=min_row_surprise, workspace=workspace)
     for l in range(n_layers):
-        k, v = ks[l], vs[l]
-        if k.shape != (bsz, tokens, dim) or v.shape != k.shape or k.dtype != act or v.dtype != act:
-            raise ValueError(f"layer {l}: k/v must be ({bsz}, {tokens}, {dim}) {act}")
-        k, v = _rows(k), _rows(v)
-        if k.stride(0) != v.stride(0) or (kv_rs is not None and k.stride(0) != kv_rs):
-            k, v = k.contiguous(), v.contiguous()
-            if kv_rs is not None and k.stride(0) != kv_rs:
-                raise ValueError("all layers' k/v must share one row stride")
-        kv_rs = k.stride(0)
-        e, al = _row_vector(etas[l], act), _row_vector(alphas[l], act)
-        if e.shape != (bsz, tokens) or al.shape != (bsz, tokens):
-            raise ValueError(f"layer {l}: eta/alpha must be ({bsz}, {tokens}) or ({bsz}, {tokens}, 1)")
-        if e.stride(0) != al.stride(0) or (ea_rs is not None and e.stride(0) != ea_rs):
-            e, al = e.contiguous(), al.contiguous()
-            if ea_rs is not None and e.stride(0) != ea_rs:
-                raise ValueError("all layers' eta/alpha must share one row stride")
-        ea_rs = e.stride(0)
-        a.k[l], a.v[l], a.eta[l], a.alpha[l] = _p(k), _p(v), _p(e), _p(al)
-        keep += [k, v, e, al]
-    mask = None
-    if token_mask is not None:
-        if token_mask.shape != (bsz, tokens):
-            raise ValueError(f"token_mask must be (B, C) = ({bsz}, {tokens})")
-        mask = token_mask.to(torch.float32)
-        if tokens > 1 and mask.stride(1) != 1:
-            mask = mask.contiguous()
-        keep.append(mask)
-    ln_w = ln_weight.to(torch.float32).contiguous()
-    ln_b = ln_bias.to(torch.float32).contiguous()
-    if ln_w.numel() != dim or ln_b.numel() != dim:
-        raise ValueError("ln_weight / ln_bias must have d_model elements")
-    if copies is not None:
-        if act != torch.bfloat16:
-            raise ValueError("bf16 state copies go with bf16 activations only")
-        if len(copies) != 6 or any(c.dtype != torch.bfloat16 or not c.is_contiguous() or c.shape != w.shape
-                                   or c.device != dev or c.data_ptr() % 16
-                                   for c, w in zip(copies, (w_up, w_gate, w_down, s_up, s_gate, s_down))):
-            raise ValueError("copies must be six contiguous, aligned bf16 tensors shaped like the state")
-    if surprise is None:
-        surprise = torch.empty(n_layers, dtype=torch.float32, device=dev)
-    elif surprise.shape != (n_layers,) or surprise.dtype != torch.float32 or not surprise.is_contiguous():
-        raise ValueError("surprise must be a contiguous fp32 (layers,) tensor")
-    if row_loss is not None and (row_loss.shape != (n_layers, bsz, 2) or row_loss.dtype != torch.float32
-                                 or not row_loss.is_contiguous()):
-        raise ValueError("row_loss must be a contiguous fp32 (layers, B, 2) tensor")
-    if not math.isfinite(min_row_surprise) or min_row_surprise < 0:
-        raise ValueError("min_row_surprise must be finite and >= 0")
-    lib = N.load_library()
-    nbytes = lib.uttt_chunk_chain_workspace(bsz, n_layers, dim, ff, code)
-    if nbytes == 0:
-        raise ValueError("unsupported layer chain dimensions")
-    if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    a.batch, a.layers, a.tokens, a.d_model, a.d_ff = bsz, n_layers, tokens, dim, ff
-    a.act_dtype, a.normalize_by_dim = code, int(bool(normalize_by_dim))
-    a.momentum_beta, a.max_inner_grad_norm, a.eps = float(momentum_beta), float(max_inner_grad_norm or 0.0), float(eps)
-    a.min_row_surprise = float(min_row_surprise)
-    a.kv_row_stride, a.ea_row_stride = kv_rs, ea_rs
-    a.token_mask, a.mask_row_stride = _p(mask), (mask.stride(0) if mask is not None else 0)
-    a.w_up, a.w_gate, a.w_down, a.s_up, a.s_gate, a.s_down = (_p(t) for t in
-                                                              (w_up, w_gate, w_down, s_up, s_gate, s_down))
-    a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
-    if copies is not None:
-        (a.w_up_copy, a.w_gate_copy, a.w_down_copy,
-         a.s_up_copy, a.s_gate_copy, a.s_down_copy) = (_p(c) for c in copies)
-    a.surprise, a.row_loss = _p(surprise), _p(row_loss)
-    keep += [ln_w, ln_b, state, copies]
-    return PreparedChain(a, keep, workspace, (surprise, row_loss), dev)
+        run.set_layer(ks[l], vs[l], etas[l], alphas[l])
+    return run
 
 
 def chunk_chain(*args, **kwargs) -> Tuple[Tensor, Optional[Tensor]]:

@@ -239,6 +239,11 @@ class uTTTModel(nn.Module):
         pool = self.fast_weight_pool
         clip = float(pool.max_inner_grad_norm or 0.0)
         pieces = []
+        # the layer chain runs on a second stream, one layer behind the forward pass: stage l
+        # needs only layers <= l, and the forward of later layers needs nothing from it (every
+        # readout reads the chunk-start state); the state write joins after the last readout
+        main = torch.cuda.current_stream(dev)
+        side = self._chain_stream(dev)
         ws_chain = ws_read = None
         for ci in range(n_chunks):
             off = ci * c
@@ -247,7 +252,10 @@ class uTTTModel(nn.Module):
             if mask is not None:
                 counts[ci].copy_(mask.to(torch.float32).sum())
             hid = h[:, off:end].contiguous()  # this chunk's residual stream, updated in place
-            ks, vs, etas, alphas = [], [], [], []
+            run = K.ChunkChainRun(n_layers, end - off, cur, ln_w, ln_b, mask, pool.momentum_beta, clip,
+                                  pool.normalize_loss_by_dim, pool.eps, h.dtype, copies=copies,
+                                  surprise=surprises[ci], workspace=ws_chain)
+            ws_chain = run.workspace
             for li, block in enumerate(self.layers):
                 attn = block.attn
                 q = attn.project(block.attn_norm(hid), start_pos + off, k_bufs[li], v_bufs[li], hist + off)
@@ -256,24 +264,30 @@ class uTTTModel(nn.Module):
                               out=att.transpose(1, 2), kv_len=hist + end)
                 hid = linear_residual(hid, att.view(bsz, end - off, -1), attn.wo.weight)
                 uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    run.add_layer(uk, uv, eta, alpha)
                 if ws_read is None:
                     ws_read = K.readout_workspace(uq, read[0])
                 r = K.swiglu_readout(uq, *read, ln_w, ln_b, pool.eps, workspace=ws_read)
                 hid = linear_residual(hid, r, block.uttt.w_o.weight)
-                ks.append(uk)
-                vs.append(uv)
-                etas.append(eta)
-                alphas.append(alpha)
-            chain = K.prepare_chunk_chain(ks, vs, etas, alphas, cur, ln_w, ln_b, mask, pool.momentum_beta, clip,
-                                          pool.normalize_loss_by_dim, pool.eps, copies=copies,
-                                          surprise=surprises[ci], workspace=ws_chain)
-            ws_chain = chain.workspace
-            chain.launch()
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                run.finish()
+            main.wait_stream(side)
             pieces.append(hid)
         per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
         caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win else (kb, vb)
                   for kb, vb in zip(k_bufs, v_bufs)]
         return torch.cat(pieces, dim=1), cur, per_layer, caches
+
+    def _chain_stream(self, device: torch.device) -> "torch.cuda.Stream":
+        """The second stream the layer chain runs on (default priority, created once per device)."""
+        streams = self.__dict__.setdefault("_chain_streams", {})
+        key = torch.device(device).index or 0
+        if key not in streams:
+            streams[key] = torch.cuda.Stream(device=device)
+        return streams[key]
 
     # ------------------------------------------------------------------ forward
     def _logits(self, h: Tensor) -> Tensor:
