@@ -24,13 +24,14 @@
 // chunk instead of once per layer, and W/S are written once per chunk instead of once per
 // layer.
 //
-// Launch sequence (one stream), layers in groups of kPqGroup: at the stage of a group's last
-// layer, pq (K_l W_s, K_l S_s for the group's layers), then per layer l of the group: K-gram
-// row l -> up (layer l - 1's clip / decay / recurrence step, then U, G, H) -> H-gram -> down
-// (Z partials) -> k_ln_grad (dZ, loss) -> dZ-gram -> back (dU, dG, norm partials); stage 0
-// first initialises the coefficient table; stage L: the last layer's recurrence step (coef) and
-// apply (final W, S and their bf16 copies).  Stage l reads only layers <= l, so a caller can
-// run it as soon as layer l's keys and values exist.
+// Launch sequence (one stream), layers in groups (of kPqGroup, the last kPqTail layers alone):
+// at the stage of a group's last layer, pq (K_l W_s, K_l S_s for the group's layers) and the
+// key Gram rows of the group, then per layer l of the group: up (layer l - 1's clip / decay /
+// recurrence step, then U, G, H) -> H-gram -> down (Z partials) -> k_ln_grad (dZ, loss) ->
+// dZ-gram -> back (dU, dG, norm partials); stage 0 first initialises the coefficient table;
+// stage L: the last layer's recurrence step (coef) and apply (final W, S and their bf16
+// copies).  Stage l reads only layers <= l, so a caller can run it as soon as layer l's keys
+// and values exist.
 #include "update_ln.h"
 #include "uttt_device.h"
 #include "uttt_host.h"
@@ -43,7 +44,7 @@ constexpr int KT = 64;
 constexpr int kMaxChain = UTTT_MAX_CHAIN;
 constexpr int kCoefStride = 4 + 2 * kMaxChain;  // a, b, e, #updating layers, gam[], sig[]
 constexpr int kGam = 4, kSig = 4 + kMaxChain;
-constexpr int kPqGroup = 4;                      // layers per workgroup in the P/Q GEMM
+constexpr int kPqGroup = 4;  // layers per workgroup in the P/Q GEMM
 
 template <typename T> constexpr int lds_ld() { return KT + Mma<T>::kPad; }
 
@@ -190,7 +191,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_init(float* coef, int n) {
 
 // ---------------------------------------------------------------------------
 // 1. P/Q: pq[m][l][b] = K_l X_m for X = (W_up, S_up, W_gate, S_gate) of the snapshot,
-//    kPqGroup layers per workgroup sharing each staged X tile.
+//    G layers per workgroup sharing each staged X tile.
 // ---------------------------------------------------------------------------
 struct PqArgs {
   int B, L, C, D, F;
@@ -200,54 +201,54 @@ struct PqArgs {
   void* pq;  // (4, L, B, 64, F) act dtype
 };
 
-template <typename T, typename WT>
+template <typename T, typename WT, int G>
 __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T bs[64 * LD];
-  __shared__ __align__(16) T as[kPqGroup * 64 * LD];
-  const int nlg = (a.l_count + kPqGroup - 1) / kPqGroup;
+  __shared__ __align__(16) T as[G * 64 * LD];
+  const int nlg = (a.l_count + G - 1) / G;
   const RowTile rt = row_tile(blockIdx.x, a.B, 4 * (a.F / 64) * nlg);
   if (!rt.valid) return;
   // tile = (m, F tile, layer group) with the layer groups that share an X tile adjacent
   const int b = rt.b, lg = rt.tile % nlg, ft = (rt.tile / nlg) % (a.F / 64), m = rt.tile / (nlg * (a.F / 64));
-  const int f0 = ft * 64, l0 = a.l_begin + lg * kPqGroup;
-  const int nl = min(kPqGroup, a.l_begin + a.l_count - l0);
+  const int f0 = ft * 64, l0 = a.l_begin + lg * G;
+  const int nl = min(G, a.l_begin + a.l_count - l0);
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const WT* xs = static_cast<const WT*>(a.x[m]) + (int64_t)b * a.D * a.F + f0;
-  const T* kr[kPqGroup];
+  const T* kr[G];
 #pragma unroll
-  for (int g = 0; g < kPqGroup; ++g)
+  for (int g = 0; g < G; ++g)
     kr[g] = layer_row<T>(a.acts.k, g < nl ? l0 + g : l0, b, a.acts.kv_rs);
 
   ColStage<WT, KT> xst;
-  RowStage<T, KT> kst[kPqGroup];
+  RowStage<T, KT> kst[G];
   xst.load(xs, a.F, KT, threadIdx.x);
 #pragma unroll
-  for (int g = 0; g < kPqGroup; ++g)
+  for (int g = 0; g < G; ++g)
     if (g < nl) kst[g].load(kr[g], a.acts.kv_ts, a.C);
-  f32x16 acc[kPqGroup];
+  f32x16 acc[G];
 #pragma unroll
-  for (int g = 0; g < kPqGroup; ++g) zero(acc[g]);
+  for (int g = 0; g < G; ++g) zero(acc[g]);
   for (int d0 = 0; d0 < a.D; d0 += KT) {
     xst.template store<T>(bs, LD);
 #pragma unroll
-    for (int g = 0; g < kPqGroup; ++g)
+    for (int g = 0; g < G; ++g)
       if (g < nl) kst[g].template store<T>(as + g * 64 * LD, LD);
     __syncthreads();
     if (d0 + KT < a.D) {
       xst.load(xs + (int64_t)(d0 + KT) * a.F, a.F, KT, threadIdx.x);
 #pragma unroll
-      for (int g = 0; g < kPqGroup; ++g)
+      for (int g = 0; g < G; ++g)
         if (g < nl) kst[g].load(kr[g] + d0 + KT, a.acts.kv_ts, a.C);
     }
 #pragma unroll
-    for (int g = 0; g < kPqGroup; ++g)
+    for (int g = 0; g < G; ++g)
       if (g < nl) wave_mma<T, KT>(acc[g], as + g * 64 * LD + wr * LD, LD, bs + wc * LD, LD);
     __syncthreads();
   }
   const int col = f0 + wc + acc_col();
 #pragma unroll
-  for (int g = 0; g < kPqGroup; ++g) {
+  for (int g = 0; g < G; ++g) {
     if (g >= nl) continue;
     T* out = static_cast<T*>(a.pq) + (((int64_t)m * a.L + l0 + g) * a.B + b) * 64 * a.F;
 #pragma unroll
@@ -256,26 +257,35 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. Gram blocks G[l][j] = X_l X_j^T over the feature dimension for one layer l and every
-//    j <= l, operands loaded straight from global memory (rows >= C are 0).
+// 2. Gram blocks G[l][j] = X_l X_j^T over the feature dimension for the layers l in
+//    [layer, layer_end) and every j <= l, operands loaded straight from global memory (rows
+//    >= C are 0).
 // ---------------------------------------------------------------------------
 struct GramArgs {
-  int B, L, C, kd, LL, layer;
+  int B, L, C, kd, LL, layer, layer_end;
   int64_t rs, ts;  // row / token strides of X (elements)
   LayerPtrs x;
-  float* out;      // row b's block row `layer` at out + (b * out_rows + out_r0) * LL
-  int out_rows, out_r0;
+  float* out;      // row b's block row l at out + (b * out_rows + out_r0 + l * out_lstep) * LL
+  int out_rows, out_r0, out_lstep;
 };
+
+// 32 x 32 quadrant tiles of the block rows [l0, l1): row l has 4 (l + 1) of them
+__host__ __device__ inline int gram_tiles(int l0, int l1) { return 2 * (l1 * (l1 + 1) - l0 * (l0 + 1)); }
 
 // One 32 x 32 quadrant per workgroup; the 4 waves take a quarter of the feature range each
 // and their partial sums meet in LDS.
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
   __shared__ float part[3 * 16 * 64];
-  const RowTile rt = row_tile(blockIdx.x, a.B, 4 * (a.layer + 1));
+  const RowTile rt = row_tile(blockIdx.x, a.B, gram_tiles(a.layer, a.layer_end));
   if (!rt.valid) return;
-  const int q = rt.tile & 3;  // 32 x 32 quadrant of the 64 x 64 block
-  const int j = rt.tile >> 2, b = rt.b, l = a.layer;
+  int l = a.layer, rem = rt.tile;
+  while (rem >= 4 * (l + 1)) {  // at most layer_end - layer steps
+    rem -= 4 * (l + 1);
+    ++l;
+  }
+  const int q = rem & 3;  // 32 x 32 quadrant of the 64 x 64 block
+  const int j = rem >> 2, b = rt.b;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
   const int ti = (q >> 1) * 32 + r, tj = (q & 1) * 32 + r;
   const int kq = a.kd / 4, kb = wave * kq, ke = kb + kq;
@@ -319,7 +329,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
   }
   __syncthreads();
   if (wave != 0) return;
-  float* out = a.out + ((int64_t)b * a.out_rows + a.out_r0) * a.LL;
+  float* out = a.out + ((int64_t)b * a.out_rows + a.out_r0 + l * a.out_lstep) * a.LL;
   const int c = j * 64 + (q & 1) * 32 + r;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -922,6 +932,21 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
   return c;
 }
 
+constexpr int kPqTail = 1;
+
+// Layer groups of the snapshot products: [0, L - kPqTail) in groups of kPqGroup, then the last
+// kPqTail layers one by one, so that little of the chain is left when the forward pass ends.
+void pq_group(int l, int L, int& g0, int& g1) {
+  const int head = L - min(L, kPqTail);
+  if (l >= head) {
+    g0 = l;
+    g1 = l + 1;
+    return;
+  }
+  g0 = l - l % kPqGroup;
+  g1 = min(head, g0 + kPqGroup);
+}
+
 template <typename T>
 void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c, hipStream_t st, int first,
                   int last) {
@@ -978,10 +1003,10 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
   GramArgs ka{};  // K_l K_j^T rows of the key Gram (B, LL, LL)
   ka.B = B; ka.L = L; ka.C = C; ka.kd = D; ka.LL = LL; ka.rs = a.kv_row_stride; ka.ts = D;
-  ka.x = acts.k; ka.out = kk; ka.out_rows = LL;
+  ka.x = acts.k; ka.out = kk; ka.out_rows = LL; ka.out_r0 = 0; ka.out_lstep = 64;
 
   GramArgs ha{};  // H_l H_j^T and dZ_l dZ_j^T: the layer buffers have stride 64 rows per row b
-  ha.B = B; ha.L = L; ha.C = C; ha.LL = LL; ha.out_rows = 64; ha.out_r0 = 0;
+  ha.B = B; ha.L = L; ha.C = C; ha.LL = LL; ha.out_rows = 64; ha.out_r0 = 0; ha.out_lstep = 0;
   GramArgs za = ha;
   ha.kd = F; ha.rs = (int64_t)64 * F; ha.ts = F; ha.out = hh;
   za.kd = D; za.rs = (int64_t)64 * D; za.ts = D; za.out = zz;
@@ -1007,20 +1032,29 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   // launch forms the snapshot products of the whole group, then each layer of the group runs.
   // Stages of the other layers of a group launch nothing.
   for (int l = 0; l < L; ++l) {
-    const int g0 = l - l % kPqGroup, g1 = min(L, g0 + kPqGroup);  // this layer's group [g0, g1)
+    int g0, g1;  // this layer's group [g0, g1)
+    pq_group(l, L, g0, g1);
     if (!want(g1 - 1)) continue;
     if (l == g0) {
       pa.l_begin = g0;
       pa.l_count = g1 - g0;
-      if (bf16_src)
-        hipLaunchKernelGGL((k_chain_pq<T, bf16>), pq_grid, blk, 0, st, pa);
-      else
-        hipLaunchKernelGGL((k_chain_pq<T, float>), pq_grid, blk, 0, st, pa);
+      if (g1 - g0 == 1) {  // a single layer: one staged K tile, less LDS per workgroup
+        if (bf16_src)
+          hipLaunchKernelGGL((k_chain_pq<T, bf16, 1>), pq_grid, blk, 0, st, pa);
+        else
+          hipLaunchKernelGGL((k_chain_pq<T, float, 1>), pq_grid, blk, 0, st, pa);
+      } else if (bf16_src) {
+        hipLaunchKernelGGL((k_chain_pq<T, bf16, kPqGroup>), pq_grid, blk, 0, st, pa);
+      } else {
+        hipLaunchKernelGGL((k_chain_pq<T, float, kPqGroup>), pq_grid, blk, 0, st, pa);
+      }
+    }
+    if (l == g0) {  // key Gram rows of the whole group
+      ka.layer = g0;
+      ka.layer_end = g1;
+      hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(g0, g1))), blk, 0, st, ka);
     }
     const float* cl = table(l);
-    ka.layer = l;  // key Gram row l
-    ka.out_r0 = l * 64;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (l + 1))), blk, 0, st, ka);
 
     UpArgs ua{};
     ua.B = B; ua.L = L; ua.C = C; ua.D = D; ua.F = F; ua.LL = LL; ua.l = l;
@@ -1030,7 +1064,8 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     hipLaunchKernelGGL(k_chain_up<T>, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
 
     ha.layer = l;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (l + 1))), blk, 0, st, ha);
+    ha.layer_end = l + 1;
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l, l + 1))), blk, 0, st, ha);
 
     DownArgs da{};
     da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
@@ -1054,7 +1089,8 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     launch_ln_grad<T>(dim3(64, B), st, g);
 
     za.layer = l;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, 4 * (l + 1))), blk, 0, st, za);
+    za.layer_end = l + 1;
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l, l + 1))), blk, 0, st, za);
 
     BackArgs ba{};
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;

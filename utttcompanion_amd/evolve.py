@@ -161,13 +161,15 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
             K.swa_prefill(q.transpose(1, 2), kb, vb, win, off, out=att.transpose(1, 2), kv_len=end)
             hid = linear_residual(hid, att.view(rows, c, -1), attn.wo.weight)
             uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                run.add_layer(uk, uv, eta, alpha)
+            ready = torch.cuda.Event()
+            ready.record(main)
             if ws_read is None:
                 ws_read = K.readout_workspace(uq, rd[0])
             hid = linear_residual(hid, K.swiglu_readout(uq, *rd, ln_w, ln_b, pool.eps, workspace=ws_read),
                                   block.uttt.w_o.weight)
+            side.wait_event(ready)  # enqueued after the readout it overlaps
+            with torch.cuda.stream(side):
+                run.add_layer(uk, uv, eta, alpha)
         side.wait_stream(main)
         with torch.cuda.stream(side):
             run.finish()

@@ -264,13 +264,17 @@ class uTTTModel(nn.Module):
                               out=att.transpose(1, 2), kv_len=hist + end)
                 hid = linear_residual(hid, att.view(bsz, end - off, -1), attn.wo.weight)
                 uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
-                side.wait_stream(main)
-                with torch.cuda.stream(side):
-                    run.add_layer(uk, uv, eta, alpha)
+                ready = torch.cuda.Event()
+                ready.record(main)
                 if ws_read is None:
                     ws_read = K.readout_workspace(uq, read[0])
                 r = K.swiglu_readout(uq, *read, ln_w, ln_b, pool.eps, workspace=ws_read)
                 hid = linear_residual(hid, r, block.uttt.w_o.weight)
+                # the chain stage is enqueued after the readout it overlaps, so that a captured
+                # graph's executor keeps the forward pass on one in-order queue of its own
+                side.wait_event(ready)
+                with torch.cuda.stream(side):
+                    run.add_layer(uk, uv, eta, alpha)
             side.wait_stream(main)
             with torch.cuda.stream(side):
                 run.finish()
