@@ -784,14 +784,22 @@ struct ApplyChainArgs {
   bf16* sc[3];
 };
 
-// 64 x 64 output tiles, one layer's token slab per stage (double-buffered); W and S are read
-// after the layer loop.  The kernel is bound by how many workgroups overlap their round trips,
-// so it is compiled for kApplyWaves waves per SIMD.
-constexpr int kApplyWaves = 3;
+// 64 x 64 output tiles, one layer's token slabs per stage: double-buffered in LDS and loaded
+// two layers ahead into registers (bf16 slabs are staged by all 256 threads), so the slab
+// round trips overlap two layers of MFMA work.  The W and S tile loads are issued after the
+// last slab loads (memory counters retire in order) and overlap the last two layers.
+
+template <typename T> struct ApplyStage { using type = ColStage<T, 64>; };
+template <> struct ApplyStage<bf16> { using type = ColStage4<64>; };
+// waves per SIMD the kernel is compiled for (the latency hiding comes from resident tiles)
+template <typename T> constexpr int apply_waves() { return sizeof(T) == 2 ? 4 : 2; }
 
 template <typename T>
-__global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const ApplyChainArgs a) {
+__global__ void __launch_bounds__(kThreads, apply_waves<T>()) k_chain_apply(const ApplyChainArgs a) {
   constexpr int LD = lds_ld<T>();
+  using Stage = typename ApplyStage<T>::type;
+  constexpr int kUnits = Stage::kUnits;
+  static_assert(2 * kUnits == kThreads, "the two slabs of a stage take one thread each");
   __shared__ __align__(16) T as[2][64 * LD];
   __shared__ __align__(16) T bs[2][64 * LD];
   const int nD = a.D / 64, nF = a.F / 64;
@@ -801,7 +809,6 @@ __global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const App
   const int m = rt.tile / per, jt = rt.tile - m * per, b = rt.b;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
   const float* cf = a.coef + (int64_t)b * kCoefStride;
-  const float ca = cf[0], cb = cf[1], ce = cf[2];
   if (cf[3] == 0.f) return;  // no layer updated this row: W and S stay as they are
   // tiles sharing a small token slab run together: for every matrix the F tile is the outer
   // index and the D tile the inner one, so the resident workgroups of a row need the slabs
@@ -818,13 +825,9 @@ __global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const App
     ld_out = a.D;
   }
   const int64_t mat = (int64_t)a.D * a.F;
-  float* wdst = a.w[m] + b * mat;
-  float* sdst = a.s[m] + b * mat;
-  const int col = c0 + wc + acc_col();
   // operand sources of layer j: A^T rows are tokens (k), columns this tile's rows
-  constexpr int kUnits = ColStage<T, 64>::kUnits;
   const bool a_part = threadIdx.x < kUnits;
-  const int unit = a_part ? (int)threadIdx.x : min((int)threadIdx.x - kUnits, kUnits);
+  const int unit = a_part ? (int)threadIdx.x : (int)threadIdx.x - kUnits;
   const T* src;
   int64_t src_ld, src_lstride;
   int k_valid;
@@ -851,16 +854,35 @@ __global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const App
   auto layer_src = [&](int j) -> const T* {
     return per_layer_ptr ? layer_row<T>(a.acts.k, j, b, a.acts.kv_rs) + r0 : src + j * src_lstride;
   };
+  // element i of this lane's accumulator tile sits at the tile base + lane offset + the
+  // wave-uniform (8 (i / 4) + i % 4) rows: buffer accesses with one VGPR offset per lane and
+  // the row offsets in SGPRs
+  const uint32_t mat_bytes = (uint32_t)(mat * 4);
+  const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(a.w[m] + b * mat, mat_bytes);
+  const __amdgpu_buffer_rsrc_t sres = buffer_rsrc(a.s[m] + b * mat, mat_bytes);
+  const int64_t tile0 = (int64_t)(r0 + wr) * ld_out + c0 + wc;
+  const int lane_el = (int)tile0 + 4 * ((int)(threadIdx.x & 63) >> 5) * ld_out + acc_col();
+  auto row_el = [&](int i) { return (8 * (i >> 2) + (i & 3)) * ld_out; };
+  float wv[16], sv[16];
+  // the state streams through once: non-temporal accesses keep it from evicting the token
+  // slabs that the other workgroups of the row still read from L2
+  auto load_state = [&]() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      wv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wres, lane_el * 4, row_el(i) * 4,
+                                                                             kNonTemporal));
+      sv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sres, lane_el * 4, row_el(i) * 4,
+                                                                             kNonTemporal));
+    }
+  };
   f32x16 accw, accs;
   zero(accw);
   zero(accs);
-  ColStage<T, 64> cst;
-  cst.load(layer_src(0), src_ld, k_valid, unit);
-  for (int j = 0; j < a.L; ++j) {
+  auto step = [&](Stage& st, int j, bool refill) {
     const int buf = j & 1;
-    cst.template store<T>(a_part ? as[buf] : bs[buf], LD);
+    st.store(a_part ? as[buf] : bs[buf], LD);
     __syncthreads();
-    if (j + 1 < a.L) cst.load(layer_src(j + 1), src_ld, k_valid, unit);
+    if (refill) st.load(layer_src(j + 2), src_ld, k_valid, unit);
     f32x16 t;
     zero(t);
     wave_mma<T, 64>(t, as[buf] + wr * LD, LD, bs[buf] + wc * LD, LD);
@@ -870,29 +892,43 @@ __global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const App
       accw[i] += gj * t[i];
       accs[i] += sj * t[i];
     }
+  };
+  // layer j sits in register stage j & 1
+  Stage st0, st1;
+  st0.load(layer_src(0), src_ld, k_valid, unit);
+  if (a.L > 1) st1.load(layer_src(1), src_ld, k_valid, unit);
+  int j = 0;
+  for (; j + 3 < a.L; j += 2) {  // both steps load the layer two ahead
+    step(st0, j, true);
+    step(st1, j + 1, true);
   }
-  bf16* cw = a.wc[m] != nullptr ? a.wc[m] + b * mat : nullptr;
-  bf16* cs = a.sc[m] != nullptr ? a.sc[m] + b * mat : nullptr;
-  float* wrow = wdst + (int64_t)(r0 + wr) * ld_out + col;
-  float* srow = sdst + (int64_t)(r0 + wr) * ld_out + col;
-  // the state streams through once: non-temporal accesses keep it from evicting the token
-  // slabs that the other workgroups of the row still read from L2
-  float wv[16], sv[16];
+  if (j + 2 < a.L) step(st0, j++, true);
+  load_state();  // after the last slab loads
+  for (; j < a.L; ++j) {
+    if (j & 1)
+      step(st1, j, false);
+    else
+      step(st0, j, false);
+  }
+  const float ca = cf[0], cb = cf[1], ce = cf[2];
+  const bool copies = a.wc[m] != nullptr;  // W and S copies are given together or not at all
+  const __amdgpu_buffer_rsrc_t wcres = buffer_rsrc(copies ? a.wc[m] + b * mat : nullptr, copies ? mat_bytes / 2 : 0);
+  const __amdgpu_buffer_rsrc_t scres = buffer_rsrc(copies ? a.sc[m] + b * mat : nullptr, copies ? mat_bytes / 2 : 0);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    wv[i] = __builtin_nontemporal_load(wrow + (int64_t)acc_row(i) * ld_out);
-    sv[i] = __builtin_nontemporal_load(srow + (int64_t)acc_row(i) * ld_out);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t off = (int64_t)acc_row(i) * ld_out;
     const float w_new = ca * wv[i] + cb * sv[i] + accw[i];
     const float s_new = ce * sv[i] + accs[i];
-    __builtin_nontemporal_store(w_new, wrow + off);
-    __builtin_nontemporal_store(s_new, srow + off);
-    const int64_t coff = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
-    if (cw != nullptr) __builtin_nontemporal_store(static_cast<bf16>(w_new), cw + coff);
-    if (cs != nullptr) __builtin_nontemporal_store(static_cast<bf16>(s_new), cs + coff);
+    // the b32 / b16 buffer builtins move raw bits
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, w_new), wres, lane_el * 4, row_el(i) * 4,
+                                          kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s_new), sres, lane_el * 4, row_el(i) * 4,
+                                          kNonTemporal);
+    if (copies) {
+      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<bf16>(w_new)), wcres,
+                                            lane_el * 2, row_el(i) * 2, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<bf16>(s_new)), scres,
+                                            lane_el * 2, row_el(i) * 2, kNonTemporal);
+    }
   }
 }
 
@@ -1130,6 +1166,7 @@ int check_chain_dims(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dtype) 
   UTTT_REQUIRE(F >= 64 && F % 64 == 0, "d_ff must be a positive multiple of 64 (got %lld)", (long long)F);
   UTTT_REQUIRE(dtype == UTTT_DTYPE_F32 || dtype == UTTT_DTYPE_BF16, "act_dtype must be F32 or BF16 (got %d)", dtype);
   UTTT_REQUIRE(3 * (D / 64) * (F / 64) <= 2147483647LL, "state too large");
+  UTTT_REQUIRE(D * F * 4 <= 2147483647LL, "d_model * d_ff * 4 must fit 31 bits (got %lld)", (long long)(D * F * 4));
   return UTTT_OK;
 }
 

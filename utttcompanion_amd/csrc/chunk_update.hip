@@ -47,9 +47,9 @@ struct FwdArgs {
 // ---------------------------------------------------------------------------
 // 1. U, G, H for one (F tile, row, path, token block)
 // ---------------------------------------------------------------------------
-template <typename T, typename WT>
+template <typename T, typename WT, int KTL = KT>
 __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
-  constexpr int LD = lds_ld<T>();
+  constexpr int LD = KTL + Mma<T>::kPad;
   __shared__ __align__(16) T xs[64 * LD];
   __shared__ __align__(16) T us[64 * LD];
   __shared__ __align__(16) T gs[64 * LD];
@@ -59,30 +59,31 @@ __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
   const int rows = min(64, a.ntok - t0);
   const T* x = static_cast<const T*>(a.x[path]) + (int64_t)b * a.x_rs[path] + (int64_t)t0 * a.D;
   // threads [0, U) stage W_up, [U, 2U) W_gate (U units of 8 rows x one 16-byte chunk)
-  constexpr int U = ColStage<WT, KT>::kUnits;
+  constexpr int U = ColStage<WT, KTL>::kUnits;
+  static_assert(2 * U <= kThreads, "W_up and W_gate stage in separate halves of the workgroup");
   const bool up_half = threadIdx.x < U;
   const WT* wsrc = static_cast<const WT*>(up_half ? a.wu[path] : a.wg[path]) + (int64_t)b * a.w_rs[path] + f0;
   T* wdst = up_half ? us : gs;
   const int unit = up_half ? (int)threadIdx.x : min((int)threadIdx.x - U, U);
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
 
-  RowStage<T, KT> xst;
-  ColStage<WT, KT> wst;
+  RowStage<T, KTL> xst;
+  ColStage<WT, KTL> wst;
   xst.load(x, a.D, rows);
-  wst.load(wsrc, a.F, KT, unit);
+  wst.load(wsrc, a.F, KTL, unit);
   f32x16 au, ag;
   zero(au);
   zero(ag);
-  for (int d0 = 0; d0 < a.D; d0 += KT) {
+  for (int d0 = 0; d0 < a.D; d0 += KTL) {
     xst.template store<T>(xs, LD);
     wst.template store<T>(wdst, LD);
     __syncthreads();
-    if (d0 + KT < a.D) {
-      xst.load(x + d0 + KT, a.D, rows);
-      wst.load(wsrc + (int64_t)(d0 + KT) * a.F, a.F, KT, unit);
+    if (d0 + KTL < a.D) {
+      xst.load(x + d0 + KTL, a.D, rows);
+      wst.load(wsrc + (int64_t)(d0 + KTL) * a.F, a.F, KTL, unit);
     }
-    wave_mma<T, KT>(au, xs + wr * LD, LD, us + wc * LD, LD);
-    wave_mma<T, KT>(ag, xs + wr * LD, LD, gs + wc * LD, LD);
+    wave_mma<T, KTL>(au, xs + wr * LD, LD, us + wc * LD, LD);
+    wave_mma<T, KTL>(ag, xs + wr * LD, LD, gs + wc * LD, LD);
     __syncthreads();
   }
 
@@ -106,38 +107,38 @@ __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
 // ---------------------------------------------------------------------------
 // 2. Z partial = H[:, split] W_down[split, D tile]
 // ---------------------------------------------------------------------------
-template <typename T, typename WT>
+template <typename T, typename WT, int KTL = KT>
 __global__ void __launch_bounds__(kThreads) k_down_partial(const FwdArgs a) {
-  constexpr int LD = lds_ld<T>();
+  constexpr int LD = KTL + Mma<T>::kPad;
   __shared__ __align__(16) T hs[64 * LD];
   __shared__ __align__(16) T ws[64 * LD];
   const int dt = blockIdx.x, split = blockIdx.y;
   const int b = blockIdx.z % a.B, pt = blockIdx.z / a.B;
   const int path = pt / a.ntb, tb = pt - path * a.ntb;
   const int d0 = dt * 64, t0 = tb * 64;
-  const int nF = a.F / 64;
-  const int f_begin = (nF * split / a.nsplit) * 64, f_end = (nF * (split + 1) / a.nsplit) * 64;
+  const int nK = a.F / KTL;  // F ranges in whole K tiles
+  const int f_begin = (nK * split / a.nsplit) * KTL, f_end = (nK * (split + 1) / a.nsplit) * KTL;
   const T* h = static_cast<const T*>(a.h[path]) + ((int64_t)b * a.tok_pad + t0) * a.F;
   const WT* wd = static_cast<const WT*>(a.wd[path]) + (int64_t)b * a.w_rs[path] + d0;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
 
-  RowStage<T, KT> hst;
-  ColStage<WT, KT> wst;  // W_down rows f, columns d -> [d][f]
+  RowStage<T, KTL> hst;
+  ColStage<WT, KTL> wst;  // W_down rows f, columns d -> [d][f]
   f32x16 acc;
   zero(acc);
   if (f_begin < f_end) {
     hst.load(h + f_begin, a.F, 64);
-    wst.load(wd + (int64_t)f_begin * a.D, a.D, KT, threadIdx.x);
+    wst.load(wd + (int64_t)f_begin * a.D, a.D, KTL, threadIdx.x);
   }
-  for (int f0 = f_begin; f0 < f_end; f0 += KT) {
+  for (int f0 = f_begin; f0 < f_end; f0 += KTL) {
     hst.template store<T>(hs, LD);
     wst.template store<T>(ws, LD);
     __syncthreads();
-    if (f0 + KT < f_end) {
-      hst.load(h + f0 + KT, a.F, 64);
-      wst.load(wd + (int64_t)(f0 + KT) * a.D, a.D, KT, threadIdx.x);
+    if (f0 + KTL < f_end) {
+      hst.load(h + f0 + KTL, a.F, 64);
+      wst.load(wd + (int64_t)(f0 + KTL) * a.D, a.D, KTL, threadIdx.x);
     }
-    wave_mma<T, KT>(acc, hs + wr * LD, LD, ws + wc * LD, LD);
+    wave_mma<T, KTL>(acc, hs + wr * LD, LD, ws + wc * LD, LD);
     __syncthreads();
   }
   float* zp = a.zp + ((((int64_t)path * a.nsplit + split) * a.B + b) * a.tok_pad + t0) * a.D + d0;
@@ -594,8 +595,17 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   f.h[0] = ws + L.h;
   f.zp = reinterpret_cast<float*>(ws + L.zp);
   const dim3 blk(kThreads);
-  hipLaunchKernelGGL((k_up_gate<T, WT>), dim3(F / 64, B, L.ntb), blk, 0, st, f);
-  hipLaunchKernelGGL((k_down_partial<T, WT>), dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
+  // bf16 weights: K tiles of 128 halve the staged steps of these latency-bound loops where the
+  // shape allows
+  constexpr bool wide = sizeof(WT) == 2;
+  if (wide && D % 128 == 0)
+    hipLaunchKernelGGL((k_up_gate<T, WT, wide ? 128 : KT>), dim3(F / 64, B, L.ntb), blk, 0, st, f);
+  else
+    hipLaunchKernelGGL((k_up_gate<T, WT>), dim3(F / 64, B, L.ntb), blk, 0, st, f);
+  if (wide && F % 128 == 0)
+    hipLaunchKernelGGL((k_down_partial<T, WT, wide ? 128 : KT>), dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
+  else
+    hipLaunchKernelGGL((k_down_partial<T, WT>), dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
   LnOutArgs o{};
   o.B = B; o.ntok = (int)a.tokens; o.D = D; o.nsplit = L.nsplit; o.tok_pad = f.tok_pad; o.eps = a.eps;
   o.zp = f.zp; o.x = a.x; o.x_rs = a.x_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;

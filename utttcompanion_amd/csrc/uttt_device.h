@@ -212,6 +212,56 @@ struct ColStage {
   }
 };
 
+// bf16 KT x 64 tile transposed to [col][k] by 8 * KT / 8 units of 4 rows each (twice the
+// units of ColStage, half the registers per thread): two such tiles occupy all 256 threads.
+template <int KT>
+struct ColStage4 {
+  static constexpr int kColGroups = 8;  // 16-byte column groups of 8 bf16
+  static constexpr int kUnits = (KT / 4) * kColGroups;
+  uint4 r[4];
+  int unit;
+
+  __device__ __forceinline__ void load(const bf16* src, int64_t ld, int k_valid, int u) {
+    unit = u;
+    if (u >= kUnits) return;
+    const int kg = u / kColGroups, cg = u - kg * kColGroups;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = kg * 4 + i;
+      r[i] = k < k_valid ? *reinterpret_cast<const uint4*>(src + (int64_t)k * ld + cg * 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  // dst rows are 8-byte aligned (ldd a multiple of 4)
+  __device__ __forceinline__ void store(bf16* dst, int ldd) const {
+    if (unit >= kUnits) return;
+    const int kg = unit / kColGroups, cg = unit - kg * kColGroups;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      // column v of the 4 rows: the 16-bit halves of word v / 2 of each row
+      const int sh = (v & 1) * 16;
+      const uint32_t w0 = (v < 2 ? r[0].x : v < 4 ? r[0].y : v < 6 ? r[0].z : r[0].w) >> sh;
+      const uint32_t w1 = (v < 2 ? r[1].x : v < 4 ? r[1].y : v < 6 ? r[1].z : r[1].w) >> sh;
+      const uint32_t w2 = (v < 2 ? r[2].x : v < 4 ? r[2].y : v < 6 ? r[2].z : r[2].w) >> sh;
+      const uint32_t w3 = (v < 2 ? r[3].x : v < 4 ? r[3].y : v < 6 ? r[3].z : r[3].w) >> sh;
+      uint2 o;
+      o.x = (w0 & 0xffffu) | (w1 << 16);
+      o.y = (w2 & 0xffffu) | (w3 << 16);
+      *reinterpret_cast<uint2*>(dst + (cg * 8 + v) * ldd + kg * 4) = o;
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Buffer resources: one SGPR descriptor per array, 32-bit byte offsets per access; out-of-range
+// loads return 0 and out-of-range stores are dropped.
+// ---------------------------------------------------------------------------
+constexpr int kBufferFlags = 0x00020000;  // raw 32-bit data format (CDNA buffer descriptor word 3)
+constexpr int kNonTemporal = 2;           // cache policy of streaming accesses
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferFlags);
+}
+
 // ---------------------------------------------------------------------------
 // Reductions
 // ---------------------------------------------------------------------------
