@@ -785,17 +785,16 @@ struct ApplyChainArgs {
 };
 
 // 64 x 64 output tiles, one layer's token slabs per stage: double-buffered in LDS and loaded
-// two layers ahead into registers (bf16 slabs are staged by all 256 threads), so the slab
-// round trips overlap two layers of MFMA work.  The W and S tile loads are issued after the
-// last slab loads (memory counters retire in order) and overlap the last two layers.
+// two layers ahead into registers (bf16 slabs are staged by all 256 threads; fp32 slabs one
+// layer ahead), so the slab round trips overlap MFMA work.  The W and S tile loads are issued
+// after the last slab loads (memory counters retire in order) and overlap the last layers.
 
 template <typename T> struct ApplyStage { using type = ColStage<T, 64>; };
 template <> struct ApplyStage<bf16> { using type = ColStage4<64>; };
-// waves per SIMD the kernel is compiled for (the latency hiding comes from resident tiles)
-template <typename T> constexpr int apply_waves() { return sizeof(T) == 2 ? 4 : 2; }
+constexpr int kApplyWaves = 4;  // waves per SIMD: the latency hiding comes from resident tiles
 
 template <typename T>
-__global__ void __launch_bounds__(kThreads, apply_waves<T>()) k_chain_apply(const ApplyChainArgs a) {
+__global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const ApplyChainArgs a) {
   constexpr int LD = lds_ld<T>();
   using Stage = typename ApplyStage<T>::type;
   constexpr int kUnits = Stage::kUnits;
@@ -893,22 +892,44 @@ __global__ void __launch_bounds__(kThreads, apply_waves<T>()) k_chain_apply(cons
       accs[i] += sj * t[i];
     }
   };
-  // layer j sits in register stage j & 1
-  Stage st0, st1;
-  st0.load(layer_src(0), src_ld, k_valid, unit);
-  if (a.L > 1) st1.load(layer_src(1), src_ld, k_valid, unit);
-  int j = 0;
-  for (; j + 3 < a.L; j += 2) {  // both steps load the layer two ahead
-    step(st0, j, true);
-    step(st1, j + 1, true);
-  }
-  if (j + 2 < a.L) step(st0, j++, true);
-  load_state();  // after the last slab loads
-  for (; j < a.L; ++j) {
-    if (j & 1)
-      step(st1, j, false);
-    else
-      step(st0, j, false);
+  if constexpr (sizeof(T) == 2) {
+    // layer j sits in register stage j & 1
+    Stage st0, st1;
+    st0.load(layer_src(0), src_ld, k_valid, unit);
+    if (a.L > 1) st1.load(layer_src(1), src_ld, k_valid, unit);
+    int j = 0;
+    for (; j + 3 < a.L; j += 2) {  // both steps load the layer two ahead
+      step(st0, j, true);
+      step(st1, j + 1, true);
+    }
+    if (j + 2 < a.L) step(st0, j++, true);
+    load_state();  // after the last slab loads
+    for (; j < a.L; ++j) {
+      if (j & 1)
+        step(st1, j, false);
+      else
+        step(st0, j, false);
+    }
+  } else {
+    // fp32 slabs take twice the registers: one layer ahead
+    Stage st;
+    st.load(layer_src(0), src_ld, k_valid, unit);
+    for (int j = 0; j < a.L; ++j) {
+      const int buf = j & 1;
+      st.store(a_part ? as[buf] : bs[buf], LD);
+      __syncthreads();
+      if (j + 1 < a.L) st.load(layer_src(j + 1), src_ld, k_valid, unit);
+      if (j + 1 == a.L) load_state();
+      f32x16 t;
+      zero(t);
+      wave_mma<T, 64>(t, as[buf] + wr * LD, LD, bs[buf] + wc * LD, LD);
+      const float gj = cf[kGam + j], sj = cf[kSig + j];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        accw[i] += gj * t[i];
+        accs[i] += sj * t[i];
+      }
+    }
   }
   const float ca = cf[0], cb = cf[1], ce = cf[2];
   const bool copies = a.wc[m] != nullptr;  // W and S copies are given together or not at all
