@@ -191,7 +191,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_init(float* coef, int n) {
 
 // ---------------------------------------------------------------------------
 // 1. P/Q: pq[m][l][b] = K_l X_m for X = (W_up, S_up, W_gate, S_gate) of the snapshot,
-//    G layers per workgroup sharing each staged X tile.
+//    G layers per workgroup sharing each staged X tile (G = 4: one layer per wave).
 // ---------------------------------------------------------------------------
 struct PqArgs {
   int B, L, C, D, F;
@@ -202,7 +202,7 @@ struct PqArgs {
 };
 
 template <typename T, typename WT, int G>
-__global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
+__global__ void __launch_bounds__(kThreads, 2) k_chain_pq(const PqArgs a) {
   constexpr int LD = lds_ld<T>();
   __shared__ __align__(16) T bs[64 * LD];
   __shared__ __align__(16) T as[G * 64 * LD];
@@ -226,9 +226,9 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
 #pragma unroll
   for (int g = 0; g < G; ++g)
     if (g < nl) kst[g].load(kr[g], a.acts.kv_ts, a.C);
-  f32x16 acc[G];
+  f32x16 acc[G < 4 ? 4 : G];  // G == 4: the four 32 x 32 quadrants of this wave's layer
 #pragma unroll
-  for (int g = 0; g < G; ++g) zero(acc[g]);
+  for (int g = 0; g < (G < 4 ? 4 : G); ++g) zero(acc[g]);
   for (int d0 = 0; d0 < a.D; d0 += KT) {
     xst.template store<T>(bs, LD);
 #pragma unroll
@@ -241,18 +241,34 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq(const PqArgs a) {
       for (int g = 0; g < G; ++g)
         if (g < nl) kst[g].load(kr[g] + d0 + KT, a.acts.kv_ts, a.C);
     }
+    if constexpr (G == kThreads / 64) {
+      // one layer per wave, its whole 64 x 64 tile: the X fragments are read once per wave
+      if (w < nl) wave_mma64<T, KT>(acc, as + w * 64 * LD, LD, bs, LD);
+    } else {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-      if (g < nl) wave_mma<T, KT>(acc[g], as + g * 64 * LD + wr * LD, LD, bs + wc * LD, LD);
+      for (int g = 0; g < G; ++g)
+        if (g < nl) wave_mma<T, KT>(acc[g], as + g * 64 * LD + wr * LD, LD, bs + wc * LD, LD);
+    }
     __syncthreads();
   }
-  const int col = f0 + wc + acc_col();
+  if constexpr (G == kThreads / 64) {
+    if (w >= nl) return;
+    T* out = static_cast<T*>(a.pq) + (((int64_t)m * a.L + l0 + w) * a.B + b) * 64 * a.F + f0;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (g >= nl) continue;
-    T* out = static_cast<T*>(a.pq) + (((int64_t)m * a.L + l0 + g) * a.B + b) * 64 * a.F;
+    for (int q = 0; q < 4; ++q) {
+      const int row0 = (q >> 1) * 32, col = (q & 1) * 32 + acc_col();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) out[(int64_t)(wr + acc_row(i)) * a.F + col] = from_f32<T>(acc[g][i]);
+      for (int i = 0; i < 16; ++i) out[(int64_t)(row0 + acc_row(i)) * a.F + col] = from_f32<T>(acc[q][i]);
+    }
+  } else {
+    const int col = f0 + wc + acc_col();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (g >= nl) continue;
+      T* out = static_cast<T*>(a.pq) + (((int64_t)m * a.L + l0 + g) * a.B + b) * 64 * a.F;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) out[(int64_t)(wr + acc_row(i)) * a.F + col] = from_f32<T>(acc[g][i]);
+    }
   }
 }
 

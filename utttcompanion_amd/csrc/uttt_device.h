@@ -67,6 +67,39 @@ __device__ __forceinline__ void wave_mma(f32x16& acc, const T* a, int lda, const
   for (int k0 = 0; k0 < KT; k0 += Mma<T>::kK) Mma<T>::step(acc, a_row, b_row, k0, h);
 }
 
+// acc[2 rq + cq] (32x32 each) += A(rows 32 rq.., KT) * B(KT, cols 32 cq..): one wave takes a
+// 64 x 64 tile, each A and B fragment read from LDS once per k step and used twice.
+template <typename T, int KT>
+__device__ __forceinline__ void wave_mma64(f32x16 (&acc)[4], const T* a, int lda, const T* b, int ldb) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 31, h = lane >> 5;
+  const T* a0 = a + r * lda;
+  const T* a1 = a + (32 + r) * lda;
+  const T* b0 = b + r * ldb;
+  const T* b1 = b + (32 + r) * ldb;
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int k0 = 0; k0 < KT; k0 += 16) {
+      const bf16x8 fa0 = *reinterpret_cast<const bf16x8*>(a0 + k0 + h * 8);
+      const bf16x8 fa1 = *reinterpret_cast<const bf16x8*>(a1 + k0 + h * 8);
+      const bf16x8 fb0 = *reinterpret_cast<const bf16x8*>(b0 + k0 + h * 8);
+      const bf16x8 fb1 = *reinterpret_cast<const bf16x8*>(b1 + k0 + h * 8);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa0, fb0, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa0, fb1, acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa1, fb0, acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa1, fb1, acc[3], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int k0 = 0; k0 < KT; k0 += Mma<T>::kK) {
+      Mma<T>::step(acc[0], a0, b0, k0, h);
+      Mma<T>::step(acc[1], a0, b1, k0, h);
+      Mma<T>::step(acc[2], a1, b0, k0, h);
+      Mma<T>::step(acc[3], a1, b1, k0, h);
+    }
+  }
+}
+
 __device__ __forceinline__ void zero(f32x16& acc) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.f;
