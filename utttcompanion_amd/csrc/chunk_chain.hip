@@ -288,11 +288,13 @@ struct GramArgs {
 // 32 x 32 quadrant tiles of the block rows [l0, l1): row l has 4 (l + 1) of them
 __host__ __device__ inline int gram_tiles(int l0, int l1) { return 2 * (l1 * (l1 + 1) - l0 * (l0 + 1)); }
 
-// One 32 x 32 quadrant per workgroup; the 4 waves take a quarter of the feature range each
-// and their partial sums meet in LDS.
+// One 32 x 32 quadrant per workgroup; the kGramWaves waves take an equal share of the
+// feature range (in steps of 16) each and their partial sums meet in LDS.
+constexpr int kGramWaves = 8;
+
 template <typename T>
-__global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
-  __shared__ float part[3 * 16 * 64];
+__global__ void __launch_bounds__(kGramWaves * 64) k_chain_gram(const GramArgs a) {
+  __shared__ float part[(kGramWaves - 1) * 16 * 64];
   const RowTile rt = row_tile(blockIdx.x, a.B, gram_tiles(a.layer, a.layer_end));
   if (!rt.valid) return;
   int l = a.layer, rem = rt.tile;
@@ -304,14 +306,14 @@ __global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
   const int j = rem >> 2, b = rt.b;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
   const int ti = (q >> 1) * 32 + r, tj = (q & 1) * 32 + r;
-  const int kq = a.kd / 4, kb = wave * kq, ke = kb + kq;
+  const int nk = a.kd / 16, kb = 16 * (nk * wave / kGramWaves), ke = 16 * (nk * (wave + 1) / kGramWaves);
   const T* xa = layer_row<T>(a.x, l, b, a.rs) + (int64_t)ti * a.ts;
   const T* xb = layer_row<T>(a.x, j, b, a.rs) + (int64_t)tj * a.ts;
   const bool va = ti < a.C, vb = tj < a.C;
   f32x16 acc;
   zero(acc);
   if constexpr (sizeof(T) == 2) {
-    for (int k0 = kb; k0 < ke; k0 += 128) {  // kq is a multiple of 16; 8 steps of 16 in flight
+    for (int k0 = kb; k0 < ke; k0 += 128) {  // the range is a multiple of 16; 8 steps of 16 in flight
       uint4 ra[8], rb[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -349,7 +351,9 @@ __global__ void __launch_bounds__(kThreads) k_chain_gram(const GramArgs a) {
   const int c = j * 64 + (q & 1) * 32 + r;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const float v = acc[i] + part[i * 64 + lane] + part[(16 + i) * 64 + lane] + part[(32 + i) * 64 + lane];
+    float v = acc[i];
+#pragma unroll
+    for (int u = 0; u < kGramWaves - 1; ++u) v += part[(u * 16 + i) * 64 + lane];
     const int row = (q >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
     out[(int64_t)row * a.LL + c] = v;
   }
@@ -1125,7 +1129,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     if (l == g0) {  // key Gram rows of the whole group
       ka.layer = g0;
       ka.layer_end = g1;
-      hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(g0, g1))), blk, 0, st, ka);
+      hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(g0, g1))), dim3(kGramWaves * 64), 0, st, ka);
     }
     const float* cl = table(l);
 
@@ -1138,7 +1142,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
     ha.layer = l;
     ha.layer_end = l + 1;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l, l + 1))), blk, 0, st, ha);
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l, l + 1))), dim3(kGramWaves * 64), 0, st, ha);
 
     DownArgs da{};
     da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
@@ -1163,7 +1167,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
     za.layer = l;
     za.layer_end = l + 1;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l, l + 1))), blk, 0, st, za);
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l, l + 1))), dim3(kGramWaves * 64), 0, st, za);
 
     BackArgs ba{};
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
