@@ -157,6 +157,13 @@ typedef struct {
   const void* q_weight; const void* k_weight; /* (d_model,) in the activation dtype */
   void* q; void* k; void* v; int64_t out_row_stride;
   void* eta; void* alpha;
+  /* Optional RMSNorm of the projection input folded into this step (NULL x: none): y was
+   * projected from the un-normalised rows x (row stride x_row_stride, d_model wide) with the
+   * norm weight folded into the projection weight and without bias; row r of y is scaled by
+   * 1 / sqrt(mean(x_r^2) + x_eps), and the eta / alpha biases (2 values, activation dtype) are
+   * added to its last two entries, before the epilogue proper. */
+  const void* x; int64_t x_row_stride; float x_eps;
+  const void* eta_alpha_bias;
 } uttt_proj_epilogue_args;
 
 int uttt_proj_epilogue(const uttt_proj_epilogue_args* args, uttt_stream_t stream);
@@ -198,6 +205,10 @@ typedef struct {
   const void* k; int64_t k_stride_b, k_stride_t, k_stride_h;
   const void* v; int64_t v_stride_b, v_stride_t, v_stride_h;
   void* k_cache; void* v_cache; int64_t kv_stride_b, kv_stride_h, kv_stride_t; int64_t kv_offset;
+  /* Optional RMSNorm of the projection input folded into this step (NULL x: none).  q / k / v
+   * were projected from the un-normalised rows x with the norm weight folded into the
+   * projection weight; token t's q / k / v are scaled by 1 / sqrt(mean(x_t^2) + x_eps) first. */
+  const void* x; int64_t x_stride_b, x_stride_t, x_dim; float x_eps;
 } uttt_rope_append_args;
 
 int uttt_rope_kv_append(const uttt_rope_append_args* args, uttt_stream_t stream);

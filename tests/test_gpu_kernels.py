@@ -229,6 +229,40 @@ def test_rope_append_is_bit_exact(dtype):
     assert kc[:, :, :5].abs().sum().item() == 0 and kc[:, :, 5 + t:].abs().sum().item() == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rope_append_folded_norm(dtype):
+    """With the projection input x given, q / k / v of token t are scaled by
+    1 / sqrt(mean(x_t^2) + eps) before RoPE (the input RMSNorm folded into the projection):
+    against the oracle's RoPE of the scaled values, fp32 <= 1e-5 relative, bf16 within two bf16
+    roundings (2^-7) of the largest magnitude."""
+    K = kernels()
+    b, t, h, hkv, hd, d = 2, 5, 4, 2, 64, 96
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(b, t, h, hd, generator=g).to(dtype)
+    k = torch.randn(b, t, hkv, hd, generator=g).to(dtype)
+    v = torch.randn(b, t, hkv, hd, generator=g).to(dtype)
+    x = (torch.randn(b, t, d, generator=g) * torch.tensor([0.3, 3.0]).view(2, 1, 1)).to(dtype)
+    cos, sin = om.rope_tables(hd, 64)
+    start = 3
+    rstd = 1.0 / torch.sqrt(x.float().pow(2).mean(-1) + 1e-5)  # (b, t)
+    qs, ks, vs = (z.float() * rstd[:, :, None, None] for z in (q, k, v))
+    ref_q = om.apply_rope(qs.transpose(1, 2), cos[start:start + t], sin[start:start + t])
+    ref_k = om.apply_rope(ks.transpose(1, 2), cos[start:start + t], sin[start:start + t])
+    dq, dk, dv, dcos, dsin, dx = to_dev(q.clone(), k, v, cos, sin, x)
+    kc = torch.zeros(b, hkv, 12, hd, dtype=dtype, device=DEV)
+    vc = torch.zeros_like(kc)
+    K.rope_kv_append(dq, dk, dv, dcos, dsin, start, kc, vc, 2, x=dx, x_eps=1e-5)
+    torch.cuda.synchronize()
+    tol = 1e-5 if dtype == torch.float32 else 2.0 ** -7
+    for got, ref in ((dq.transpose(1, 2).cpu(), ref_q), (kc[:, :, 2:2 + t].cpu(), ref_k),
+                     (vc[:, :, 2:2 + t].cpu(), vs.transpose(1, 2))):
+        err = (got.float() - ref.float()).abs().max().item() / ref.float().abs().max().item()
+        assert err <= tol, f"rel err {err:.3e}"
+    assert kc[:, :, :2].abs().sum().item() == 0 and kc[:, :, 2 + t:].abs().sum().item() == 0
+    with pytest.raises(ValueError):
+        K.rope_kv_append(dq, dk, dv, dcos, dsin, start, kc, vc, 2, x=dx, x_eps=0.0)
+
+
 @pytest.mark.parametrize("case", [
     dict(b=2, h=12, hkv=4, tq=300, tkv=300, hd=64, win=128),     # multi-tile window, ragged tail
     dict(b=1, h=4, hkv=4, tq=64, tkv=575, hd=64, win=512),       # chunk step over a cache (C2 shape)
@@ -340,3 +374,31 @@ def test_proj_epilogue_matches_oracle(dtype):
         assert a.shape == e.shape and a.dtype == dtype, name
         err = ((a.float().cpu() - e).abs() / e.abs().clamp_min(1e-6)).max().item()
         assert err <= (1e-6 if dtype == torch.float32 else 2.0 ** -8), f"{name}: rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_proj_epilogue_folded_norm(dtype):
+    """With the GEMM input x given, y's rows are scaled by 1 / sqrt(mean(x^2) + eps) and the eta /
+    alpha biases added before the q/k/v RMSNorm and the sigmoids: against the same steps in fp32
+    from the same (rounded) y, fp32 <= 1e-5 relative, bf16 within 2^-7 relative."""
+    K = kernels()
+    g = torch.Generator().manual_seed(23)
+    rows, d = 29, 128
+    x = (torch.randn(rows, d, generator=g) * 2.0).to(dtype)
+    y = (torch.randn(rows, 3 * d + 2, generator=g) * 3.0).to(dtype)
+    qw, kw = 1.0 + 0.2 * torch.randn(d, generator=g), 1.0 + 0.2 * torch.randn(d, generator=g)
+    bias = torch.tensor([0.3, -1.386]).to(dtype)
+    rstd = 1.0 / torch.sqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-5)
+    yf = y.float() * rstd
+    yf[:, 3 * d] += bias[0].float()
+    yf[:, 3 * d + 1] += bias[1].float()
+    ref = (om.rms_norm(yf[:, :d], qw.to(dtype).float(), 1e-5), om.rms_norm(yf[:, d:2 * d], kw.to(dtype).float(), 1e-5),
+           om.rms_norm(yf[:, 2 * d:3 * d], None, 1e-5), 0.01 * torch.sigmoid(yf[:, 3 * d:3 * d + 1]),
+           0.005 * torch.sigmoid(yf[:, 3 * d + 1:]))
+    with torch.no_grad():
+        got = K.proj_epilogue(y.to(DEV), d, qw.to(DEV, dtype), kw.to(DEV, dtype), 1e-5, 0.01, 0.005,
+                              x=x.to(DEV), x_eps=1e-5, eta_alpha_bias=bias.to(DEV))
+    tol = 1e-5 if dtype == torch.float32 else 2.0 ** -7
+    for name, a, e in zip(("q", "k", "v", "eta", "alpha"), got, ref):
+        err = ((a.float().cpu() - e).abs() / e.abs().clamp_min(1e-6)).max().item()
+        assert err <= tol, f"{name}: rel err {err:.3e}"

@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 MAX_CHAIN = 64
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -70,6 +70,8 @@ class ProjEpilogueArgs(C.Structure):
         ("q_weight", _P), ("k_weight", _P),
         ("q", _P), ("k", _P), ("v", _P), ("out_row_stride", _I64),
         ("eta", _P), ("alpha", _P),
+        ("x", _P), ("x_row_stride", _I64), ("x_eps", _F),
+        ("eta_alpha_bias", _P),
     ]
 
 
@@ -95,6 +97,7 @@ class RopeAppendArgs(C.Structure):
         ("v", _P), ("v_stride_b", _I64), ("v_stride_t", _I64), ("v_stride_h", _I64),
         ("k_cache", _P), ("v_cache", _P), ("kv_stride_b", _I64), ("kv_stride_h", _I64), ("kv_stride_t", _I64),
         ("kv_offset", _I64),
+        ("x", _P), ("x_stride_b", _I64), ("x_stride_t", _I64), ("x_dim", _I64), ("x_eps", _F),
     ]
 
 

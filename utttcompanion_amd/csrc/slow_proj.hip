@@ -2,7 +2,9 @@
 // model/uttt_layer.py:1193-1231), written for gfx950 (MI355X).
 //
 // Input: y = x [W_q; W_k; W_v; w_eta; w_alpha]^T + [0; 0; 0; b_eta; b_alpha] per token row,
-// (rows, 3 D + 2) in the activation dtype.  Output per row:
+// (rows, 3 D + 2) in the activation dtype; or, with the block's input RMSNorm folded in,
+// y = h [W_q; ...]'^T of the un-normalised rows h with the norm weight folded into the weight
+// columns, scaled here by 1 / rms(h) per row before the biases.  Output per row:
 //   q = RMSNorm(y[0:D]) * q_weight, k = RMSNorm(y[D:2D]) * k_weight, v = RMSNorm(y[2D:3D]),
 //   eta = inner_lr * sigmoid(y[3D]), alpha = weight_decay * sigmoid(y[3D + 1])
 // with RMSNorm(z) = z / sqrt(mean(z^2) + eps), statistics and products in fp32 and one
@@ -27,7 +29,22 @@ struct ProjArgs {
   int64_t out_rs;
   void* eta;
   void* alpha;
+  const void* x;  // folded input RMSNorm: un-normalised rows, or null
+  int64_t x_rs;
+  float x_eps;
+  const void* ea_bias;  // eta / alpha biases with a folded norm
 };
+
+// 1 / sqrt(mean(x^2) + eps) of one d-wide row, all threads
+template <typename T>
+__device__ __forceinline__ float row_rstd(const T* x, int d, float eps, float* red) {
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < d; i += kThreads) {
+    const float v = to_f32(x[i]);
+    ss += v * v;
+  }
+  return 1.0f / sqrtf(block_sum(ss, red) / (float)d + eps);
+}
 
 template <typename T>
 __global__ void __launch_bounds__(kThreads) k_proj_epilogue(const ProjArgs a) {
@@ -35,6 +52,9 @@ __global__ void __launch_bounds__(kThreads) k_proj_epilogue(const ProjArgs a) {
   const int r = blockIdx.x;
   const T* y = static_cast<const T*>(a.y) + (int64_t)r * a.y_rs;
   const float inv_d = 1.0f / (float)a.D;
+  // folded input norm: every projected value of the row scales by the row's 1 / rms
+  const float xs = a.x != nullptr ? row_rstd<T>(static_cast<const T*>(a.x) + (int64_t)r * a.x_rs, a.D, a.x_eps, red)
+                                  : 1.0f;
 #pragma unroll 1
   for (int seg = 0; seg < 3; ++seg) {
     float v[kMaxPer];
@@ -42,7 +62,7 @@ __global__ void __launch_bounds__(kThreads) k_proj_epilogue(const ProjArgs a) {
 #pragma unroll
     for (int i = 0; i < kMaxPer; ++i) {
       const int d = threadIdx.x + i * kThreads;
-      v[i] = d < a.D ? to_f32(y[seg * a.D + d]) : 0.f;
+      v[i] = d < a.D ? xs * to_f32(y[seg * a.D + d]) : 0.f;
       ss += v[i] * v[i];
     }
     const float rstd = 1.0f / sqrtf(block_sum(ss, red) * inv_d + a.eps);
@@ -58,7 +78,9 @@ __global__ void __launch_bounds__(kThreads) k_proj_epilogue(const ProjArgs a) {
     }
   }
   if (threadIdx.x == 0) {
-    const float ye = to_f32(y[3 * a.D]), ya = to_f32(y[3 * a.D + 1]);
+    const T* eab = static_cast<const T*>(a.ea_bias);
+    const float be = eab != nullptr ? to_f32(eab[0]) : 0.f, ba = eab != nullptr ? to_f32(eab[1]) : 0.f;
+    const float ye = xs * to_f32(y[3 * a.D]) + be, ya = xs * to_f32(y[3 * a.D + 1]) + ba;
     static_cast<T*>(a.eta)[r] = from_f32<T>(a.lr * sigmoidf_acc(ye));
     static_cast<T*>(a.alpha)[r] = from_f32<T>(a.wd * sigmoidf_acc(ya));
   }
@@ -79,6 +101,8 @@ extern "C" int uttt_proj_epilogue(const uttt_proj_epilogue_args* a, uttt_stream_
                "pointers must be non-NULL");
   UTTT_REQUIRE(a->y_row_stride >= 3 * a->d_model + 2 && a->out_row_stride >= a->d_model,
                "row strides must cover a row");
+  UTTT_REQUIRE(a->x == nullptr || a->x_row_stride >= a->d_model, "x row stride must cover a row");
+  UTTT_REQUIRE(a->x == nullptr || a->x_eps > 0.f, "x_eps must be > 0 with a folded norm");
   ProjArgs p{};
   p.rows = (int)a->rows;
   p.D = (int)a->d_model;
@@ -95,6 +119,10 @@ extern "C" int uttt_proj_epilogue(const uttt_proj_epilogue_args* a, uttt_stream_
   p.out_rs = a->out_row_stride;
   p.eta = a->eta;
   p.alpha = a->alpha;
+  p.x = a->x;
+  p.x_rs = a->x_row_stride;
+  p.x_eps = a->x_eps;
+  p.ea_bias = a->eta_alpha_bias;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (a->act_dtype == UTTT_DTYPE_BF16)
     hipLaunchKernelGGL(k_proj_epilogue<bf16>, dim3(p.rows), dim3(kThreads), 0, st, p);

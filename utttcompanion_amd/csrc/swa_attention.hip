@@ -74,12 +74,24 @@ __global__ void __launch_bounds__(kThreads) k_rope_append(const uttt_rope_append
   const T* v = static_cast<const T*>(a.v) + b * a.v_stride_b + t * a.v_stride_t;
   T* kc = static_cast<T*>(a.k_cache) + b * a.kv_stride_b + (a.kv_offset + t) * a.kv_stride_t;
   T* vc = static_cast<T*>(a.v_cache) + b * a.kv_stride_b + (a.kv_offset + t) * a.kv_stride_t;
+  // folded input norm: q, k and v of the token scale by 1 / rms of its input row
+  float xs = 1.0f;
+  if (a.x != nullptr) {
+    __shared__ float red[4];
+    const T* xr = static_cast<const T*>(a.x) + b * a.x_stride_b + t * a.x_stride_t;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < a.x_dim; i += kThreads) {
+      const float xv = to_f32(xr[i]);
+      ss += xv * xv;
+    }
+    xs = 1.0f / sqrtf(block_sum(ss, red) / (float)a.x_dim + a.x_eps);
+  }
   const int nq = (int)a.n_heads * half;
   for (int idx = threadIdx.x; idx < nq; idx += kThreads) {
     const int h = idx / half, e = idx - h * half;
     T* qh = q + h * a.q_stride_h;
     T lo, hi;
-    rope_pair<T>(to_f32(qh[e]), to_f32(qh[e + half]), cr[e], sr[e], lo, hi);
+    rope_pair<T>(xs * to_f32(qh[e]), xs * to_f32(qh[e + half]), cr[e], sr[e], lo, hi);
     qh[e] = lo;
     qh[e + half] = hi;
   }
@@ -88,14 +100,15 @@ __global__ void __launch_bounds__(kThreads) k_rope_append(const uttt_rope_append
     const int h = idx / half, e = idx - h * half;
     const T* kh = k + h * a.k_stride_h;
     T lo, hi;
-    rope_pair<T>(to_f32(kh[e]), to_f32(kh[e + half]), cr[e], sr[e], lo, hi);
+    rope_pair<T>(xs * to_f32(kh[e]), xs * to_f32(kh[e + half]), cr[e], sr[e], lo, hi);
     kc[h * a.kv_stride_h + e] = lo;
     kc[h * a.kv_stride_h + e + half] = hi;
   }
   const int nv = (int)a.n_kv_heads * hd;
   for (int idx = threadIdx.x; idx < nv; idx += kThreads) {
     const int h = idx / hd, e = idx - h * hd;
-    vc[h * a.kv_stride_h + e] = v[h * a.v_stride_h + e];
+    const T vv = v[h * a.v_stride_h + e];
+    vc[h * a.kv_stride_h + e] = a.x != nullptr ? from_f32<T>(xs * to_f32(vv)) : vv;
   }
 }
 
@@ -668,6 +681,7 @@ extern "C" int uttt_rope_kv_append(const uttt_rope_append_args* a, uttt_stream_t
                "pointers must be non-NULL");
   UTTT_REQUIRE(a->kv_offset >= 0, "kv_offset must be >= 0");
   UTTT_REQUIRE(a->act_dtype == UTTT_DTYPE_F32 || a->act_dtype == UTTT_DTYPE_BF16, "bad act_dtype");
+  UTTT_REQUIRE(a->x == nullptr || (a->x_dim >= 1 && a->x_eps > 0.f), "a folded norm needs x_dim >= 1 and x_eps > 0");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)a->tokens, (unsigned)a->batch);
   if (a->act_dtype == UTTT_DTYPE_BF16)

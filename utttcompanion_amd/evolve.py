@@ -156,11 +156,11 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
         for li, block in enumerate(model.layers):
             attn = block.attn
             kb, vb = k_bufs[li][:rows], v_bufs[li][:rows]
-            q = attn.project(block.attn_norm(hid), off, kb, vb, off)
+            q = attn.project(hid, off, kb, vb, off, norm=block.attn_norm)
             att = torch.empty((rows, c, attn.n_heads, hd), dtype=dt, device=dev)
             K.swa_prefill(q.transpose(1, 2), kb, vb, win, off, out=att.transpose(1, 2), kv_len=end)
             hid = linear_residual(hid, att.view(rows, c, -1), attn.wo.weight)
-            uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
+            uq, uk, uv, eta, alpha = block.uttt.projections(hid, norm=block.uttt_norm)
             ready = torch.cuda.Event()
             ready.record(main)
             if ws_read is None:

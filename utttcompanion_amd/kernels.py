@@ -452,10 +452,14 @@ def chunk_chain(*args, **kwargs) -> Tuple[Tensor, Optional[Tensor]]:
 # ---------------------------------------------------------------------------
 
 def proj_epilogue(y: Tensor, dim: int, q_weight: Tensor, k_weight: Tensor, eps: float, inner_lr: float,
-                  weight_decay: float) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+                  weight_decay: float, x: Optional[Tensor] = None, x_eps: float = 0.0,
+                  eta_alpha_bias: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """q, k, v, eta, alpha from the packed slow-projection product y (..., 3 D + 2)
     (``uttt_proj_epilogue``; the RMSNorm / sigmoid part of reference fused_slow_projections,
-    model/uttt_layer.py:1193-1231).  Returns q, k, v (..., D) and eta, alpha (..., 1)."""
+    model/uttt_layer.py:1193-1231).  Returns q, k, v (..., D) and eta, alpha (..., 1).
+    With ``x`` (..., D), the un-normalised rows y was projected from by a weight with the input
+    RMSNorm weight folded in and no bias, y's rows are scaled by 1 / sqrt(mean(x^2) + x_eps)
+    and ``eta_alpha_bias`` (2,) is added to its last two entries first."""
     if y.shape[-1] != 3 * dim + 2:
         raise ValueError(f"y must end in 3 * d_model + 2 = {3 * dim + 2} features, got {y.shape[-1]}")
     code = _act_code(y.dtype)
@@ -478,9 +482,20 @@ def proj_epilogue(y: Tensor, dim: int, q_weight: Tensor, k_weight: Tensor, eps: 
     a.q_weight, a.k_weight = _p(qw), _p(kw)
     a.q, a.k, a.v, a.out_row_stride = _p(qkv[0]), _p(qkv[1]), _p(qkv[2]), dim
     a.eta, a.alpha = _p(ea[0]), _p(ea[1])
+    keep = None
+    if x is not None:
+        x2 = x.reshape(-1, x.shape[-1])
+        if x2.shape != (rows, dim) or x.dtype != y.dtype or x2.stride(1) != 1:
+            raise ValueError("x must hold one d_model-wide row per row of y, in y's dtype")
+        if not x_eps > 0.0 or eta_alpha_bias is None or eta_alpha_bias.numel() != 2:
+            raise ValueError("a folded norm needs eps > 0 and the two eta / alpha biases")
+        keep = eta_alpha_bias.detach().to(y.dtype).contiguous()
+        _require_device(dev, x, keep)
+        a.x, a.x_row_stride, a.x_eps, a.eta_alpha_bias = _p(x2), x2.stride(0), float(x_eps), _p(keep)
     lib = N.load_library()
     with torch.cuda.device(dev):
         N.check(lib.uttt_proj_epilogue(C.byref(a), _stream(dev)), "uttt_proj_epilogue")
+    del keep
     return (qkv[0].view(*lead, dim), qkv[1].view(*lead, dim), qkv[2].view(*lead, dim),
             ea[0].view(*lead, 1), ea[1].view(*lead, 1))
 
@@ -546,10 +561,13 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
 # ---------------------------------------------------------------------------
 
 def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, start_pos: int,
-                   k_cache: Tensor, v_cache: Tensor, kv_offset: int) -> None:
+                   k_cache: Tensor, v_cache: Tensor, kv_offset: int, x: Optional[Tensor] = None,
+                   x_eps: float = 0.0) -> None:
     """Rotate ``q`` (B, T, H, hd) in place; write rotated ``k`` and ``v`` (B, T, Hkv, hd) into
     ``k_cache``/``v_cache`` (B, Hkv, L, hd) at time ``kv_offset + t``.  RoPE position of
-    token t is ``start_pos + t``; cos/sin are fp32 (positions, hd) tables."""
+    token t is ``start_pos + t``; cos/sin are fp32 (positions, hd) tables.  With ``x`` (B, T, D),
+    the un-normalised input of a projection whose RMSNorm weight was folded into the weight,
+    token t's q / k / v are first scaled by 1 / sqrt(mean(x_t^2) + x_eps)."""
     bsz, tokens, heads, hd = q.shape
     hkv = k.shape[2]
     if k.shape != (bsz, tokens, hkv, hd) or v.shape != k.shape:
@@ -584,6 +602,13 @@ def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, st
         raise ValueError("k_cache and v_cache must share strides")
     a.kv_stride_b, a.kv_stride_h, a.kv_stride_t = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
     a.kv_offset = int(kv_offset)
+    if x is not None:
+        if x.dim() != 3 or x.shape[:2] != (bsz, tokens) or x.dtype != q.dtype or x.stride(-1) != 1:
+            raise ValueError("x must be (B, T, D) in q's dtype with a contiguous last dimension")
+        if not x_eps > 0.0:
+            raise ValueError("a folded norm needs eps > 0")
+        _require_device(dev, x)
+        a.x, a.x_stride_b, a.x_stride_t, a.x_dim, a.x_eps = _p(x), x.stride(0), x.stride(1), x.shape[2], float(x_eps)
     lib = N.load_library()
     with torch.cuda.device(dev):
         N.check(lib.uttt_rope_kv_append(C.byref(a), _stream(dev)), "uttt_rope_kv_append")

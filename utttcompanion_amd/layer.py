@@ -329,15 +329,30 @@ class SlidingWindowAttention(nn.Module):
             self._pack_key = key
         return self._pack
 
-    def project(self, x: Tensor, start_pos: int, k_buf: Tensor, v_buf: Tensor, kv_offset: int) -> Tensor:
+    def packed_qkv_folded(self, norm: "RMSNorm") -> Tensor:
+        """The packed QKV weight with an input RMSNorm's weight folded into its columns
+        (W diag(g), formed in fp32 and rounded once), rebuilt when any of them changes."""
+        w = self.packed_qkv()
+        key = (self._pack_key, norm.weight.data_ptr(), norm.weight._version, norm.weight.dtype)
+        if getattr(self, "_fold_key", None) != key:
+            self._fold = (w.float() * norm.weight.detach().float()[None, :]).to(w.dtype)
+            self._fold_key = key
+        return self._fold
+
+    def project(self, x: Tensor, start_pos: int, k_buf: Tensor, v_buf: Tensor, kv_offset: int,
+                norm: Optional["RMSNorm"] = None) -> Tensor:
         """QKV projection + RoPE; writes rotated k / v into the KV buffers at ``kv_offset`` and
-        returns rotated q as a (B, T, H, hd) view."""
+        returns rotated q as a (B, T, H, hd) view.  With ``norm``, ``x`` is the un-normalised
+        input of that RMSNorm: its weight is folded into the projection weight and the per-token
+        1 / rms scale is applied inside the RoPE kernel, so the norm needs no launch of its own."""
         bsz, seq, _ = x.shape
         hd, h, hkv = self.head_dim, self.n_heads, self.n_kv_heads
-        qkv = F.linear(x, self.packed_qkv().to(x.dtype)).view(bsz, seq, h + 2 * hkv, hd)
+        w = self.packed_qkv() if norm is None else self.packed_qkv_folded(norm)
+        qkv = F.linear(x, w.to(x.dtype)).view(bsz, seq, h + 2 * hkv, hd)
         q, k, v = qkv[:, :, :h], qkv[:, :, h:h + hkv], qkv[:, :, h + hkv:]
         cos, sin = self.rope.tables(start_pos + seq, x.device)
-        K.rope_kv_append(q, k, v, cos, sin, start_pos, k_buf, v_buf, kv_offset)
+        K.rope_kv_append(q, k, v, cos, sin, start_pos, k_buf, v_buf, kv_offset,
+                         x=None if norm is None else x, x_eps=0.0 if norm is None else norm.eps)
         return q
 
     def forward(self, x: Tensor, kv_cache: Optional[Tuple[Tensor, Tensor]] = None,
@@ -441,12 +456,30 @@ class uTTTLayer(nn.Module):
             self._pack_key = key
         return self._pack
 
-    def projections(self, x: Tensor) -> Tuple[Tensor, ...]:
-        """q, k, v, eta, alpha from one packed GEMM (same values as fused_slow_projections)."""
+    def packed_projection_folded(self, norm: "RMSNorm") -> Tuple[Tensor, Tensor]:
+        """(packed weight with an input RMSNorm's weight folded into its columns, the eta / alpha
+        biases), rebuilt when any of them changes."""
         w, b = self.packed_projection()
-        y = F.linear(x, w.to(x.dtype), b.to(x.dtype))
+        key = (self._pack_key, norm.weight.data_ptr(), norm.weight._version, norm.weight.dtype)
+        if getattr(self, "_fold_key", None) != key:
+            self._fold = ((w.float() * norm.weight.detach().float()[None, :]).to(w.dtype), b[-2:].contiguous())
+            self._fold_key = key
+        return self._fold
+
+    def projections(self, x: Tensor, norm: Optional["RMSNorm"] = None) -> Tuple[Tensor, ...]:
+        """q, k, v, eta, alpha from one packed GEMM (same values as fused_slow_projections).
+        With ``norm``, ``x`` is the un-normalised input of that RMSNorm, folded into the GEMM
+        weight and the epilogue (per-row 1 / rms scale, then the eta / alpha biases)."""
+        if norm is None:
+            w, b = self.packed_projection()
+            y = F.linear(x, w.to(x.dtype), b.to(x.dtype))
+            return K.proj_epilogue(y, self.d_model, self.q_norm.weight, self.k_norm.weight, self.q_norm.eps,
+                                   self.base_inner_lr, self.base_weight_decay)
+        w, eab = self.packed_projection_folded(norm)
+        y = F.linear(x, w.to(x.dtype))
         return K.proj_epilogue(y, self.d_model, self.q_norm.weight, self.k_norm.weight, self.q_norm.eps,
-                               self.base_inner_lr, self.base_weight_decay)
+                               self.base_inner_lr, self.base_weight_decay, x=x, x_eps=norm.eps,
+                               eta_alpha_bias=eab.to(x.dtype))
 
     def forward(self, x: Tensor, fast_pool: SharedFastWeightPool, fast_state: FastWeightState,
                 attention_mask: Optional[Tensor] = None, update_fast_weights: bool = True,

@@ -258,12 +258,12 @@ class uTTTModel(nn.Module):
             ws_chain = run.workspace
             for li, block in enumerate(self.layers):
                 attn = block.attn
-                q = attn.project(block.attn_norm(hid), start_pos + off, k_bufs[li], v_bufs[li], hist + off)
+                q = attn.project(hid, start_pos + off, k_bufs[li], v_bufs[li], hist + off, norm=block.attn_norm)
                 att = torch.empty((bsz, end - off, attn.n_heads, hd), dtype=h.dtype, device=dev)
                 K.swa_prefill(q.transpose(1, 2), k_bufs[li], v_bufs[li], win, hist + off,
                               out=att.transpose(1, 2), kv_len=hist + end)
                 hid = linear_residual(hid, att.view(bsz, end - off, -1), attn.wo.weight)
-                uq, uk, uv, eta, alpha = block.uttt.projections(block.uttt_norm(hid))
+                uq, uk, uv, eta, alpha = block.uttt.projections(hid, norm=block.uttt_norm)
                 ready = torch.cuda.Event()
                 ready.record(main)
                 if ws_read is None:
