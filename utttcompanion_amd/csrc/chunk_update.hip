@@ -164,30 +164,41 @@ struct LnOutArgs {
   void* out; int64_t out_rs;
 };
 
-template <typename T>
+// KPER values per thread (D <= KPER * 256); the splits' partial rows are loaded four at a time
+// with all their loads in flight before any is summed.
+template <typename T, int KPER>
 __global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
   __shared__ float red[4];
   const int t = blockIdx.x, b = blockIdx.y;
   if (t >= a.ntok) return;
   const float inv_d = 1.0f / (float)a.D;
-  float z[kMaxPerThread];
+  float z[KPER];
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) z[i] = 0.f;
-  for (int sp = 0; sp < a.nsplit; ++sp) {  // one round trip per split: the row's loads go out together
-    const float* src = a.zp + (((int64_t)sp * a.B + b) * a.tok_pad + t) * a.D;
+  for (int i = 0; i < KPER; ++i) z[i] = 0.f;
+  constexpr int kGroup = 4;
+  for (int sp0 = 0; sp0 < a.nsplit; sp0 += kGroup) {
+    float v[kGroup][KPER];
 #pragma unroll
-    for (int i = 0; i < kMaxPerThread; ++i) {
-      const int d = threadIdx.x + i * kThreads;
-      if (d < a.D) z[i] += src[d];
+    for (int u = 0; u < kGroup; ++u) {
+      const float* src = a.zp + (((int64_t)(sp0 + u) * a.B + b) * a.tok_pad + t) * a.D;
+#pragma unroll
+      for (int i = 0; i < KPER; ++i) {
+        const int d = threadIdx.x + i * kThreads;
+        v[u][i] = sp0 + u < a.nsplit && d < a.D ? src[d] : 0.f;
+      }
     }
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u)
+#pragma unroll
+      for (int i = 0; i < KPER; ++i) z[i] += v[u][i];
   }
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) s += z[i];
+  for (int i = 0; i < KPER; ++i) s += z[i];
   const float mean = block_sum(s, red) * inv_d;
   float s2 = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
+  for (int i = 0; i < KPER; ++i) {
     const int d = threadIdx.x + i * kThreads;
     if (d < a.D) {
       const float c = z[i] - mean;
@@ -198,7 +209,7 @@ __global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
   const T* xr = static_cast<const T*>(a.x) + (int64_t)b * a.x_rs + (int64_t)t * a.D;
   T* o = static_cast<T*>(a.out) + (int64_t)b * a.out_rs + (int64_t)t * a.D;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
+  for (int i = 0; i < KPER; ++i) {
     const int d = threadIdx.x + i * kThreads;
     if (d < a.D) {
       const float g = to_f32(from_f32<T>(a.ln_w[d]));
@@ -206,6 +217,16 @@ __global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
       o[d] = from_f32<T>(to_f32(xr[d]) + ((z[i] - mean) * rstd * g + be));
     }
   }
+}
+
+template <typename T>
+static void launch_ln_readout(dim3 grid, hipStream_t st, const LnOutArgs& o) {
+  if (o.D <= 4 * kThreads)
+    hipLaunchKernelGGL((k_ln_readout<T, 4>), grid, dim3(kThreads), 0, st, o);
+  else if (o.D <= 8 * kThreads)
+    hipLaunchKernelGGL((k_ln_readout<T, 8>), grid, dim3(kThreads), 0, st, o);
+  else
+    hipLaunchKernelGGL((k_ln_readout<T, 16>), grid, dim3(kThreads), 0, st, o);
 }
 
 // ---------------------------------------------------------------------------
@@ -542,7 +563,7 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   o.out = a.out; o.out_rs = a.out_row_stride;
   if (want(2)) {
     launch_ln_grad<T>(dim3(64, B), st, g);
-    hipLaunchKernelGGL(k_ln_readout<T>, dim3(C, B), blk, 0, st, o);
+    launch_ln_readout<T>(dim3(C, B), st, o);
   }
 
   BwdArgs bw{};
@@ -610,7 +631,7 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   o.B = B; o.ntok = (int)a.tokens; o.D = D; o.nsplit = L.nsplit; o.tok_pad = f.tok_pad; o.eps = a.eps;
   o.zp = f.zp; o.x = a.x; o.x_rs = a.x_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
   o.out = a.out; o.out_rs = a.out_row_stride;
-  hipLaunchKernelGGL(k_ln_readout<T>, dim3(f.tok_pad, B), blk, 0, st, o);
+  launch_ln_readout<T>(dim3(f.tok_pad, B), st, o);
 }
 
 static int check_dims(int64_t B, int64_t D, int64_t F, int32_t dtype) {

@@ -16,7 +16,7 @@
 namespace uttt {
 namespace {
 
-constexpr int kMaxPer = 16;  // d_model <= 4096
+constexpr int kMaxPer = 16;  // d_model <= 4096 (KPER of the widest instance)
 
 struct ProjArgs {
   int rows, D;
@@ -35,45 +35,60 @@ struct ProjArgs {
   const void* ea_bias;  // eta / alpha biases with a folded norm
 };
 
-// 1 / sqrt(mean(x^2) + eps) of one d-wide row, all threads
-template <typename T>
-__device__ __forceinline__ float row_rstd(const T* x, int d, float eps, float* red) {
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < d; i += kThreads) {
-    const float v = to_f32(x[i]);
-    ss += v * v;
-  }
-  return 1.0f / sqrtf(block_sum(ss, red) / (float)d + eps);
-}
-
-template <typename T>
+// One 256-thread workgroup per row, KPER values per thread and segment (D <= KPER * 256).  The
+// row's q, k, v (and folded-norm input) values are all loaded before any is used, and the four
+// sums of squares meet in one LDS reduction.
+template <typename T, int KPER>
 __global__ void __launch_bounds__(kThreads) k_proj_epilogue(const ProjArgs a) {
-  __shared__ float red[4];
+  __shared__ float red[4][kThreads / 64];
   const int r = blockIdx.x;
   const T* y = static_cast<const T*>(a.y) + (int64_t)r * a.y_rs;
+  const T* x = a.x != nullptr ? static_cast<const T*>(a.x) + (int64_t)r * a.x_rs : nullptr;
   const float inv_d = 1.0f / (float)a.D;
-  // folded input norm: every projected value of the row scales by the row's 1 / rms
-  const float xs = a.x != nullptr ? row_rstd<T>(static_cast<const T*>(a.x) + (int64_t)r * a.x_rs, a.D, a.x_eps, red)
-                                  : 1.0f;
-#pragma unroll 1
-  for (int seg = 0; seg < 3; ++seg) {
-    float v[kMaxPer];
-    float ss = 0.f;
+  float v[3][KPER], xv[KPER];
 #pragma unroll
-    for (int i = 0; i < kMaxPer; ++i) {
-      const int d = threadIdx.x + i * kThreads;
-      v[i] = d < a.D ? xs * to_f32(y[seg * a.D + d]) : 0.f;
-      ss += v[i] * v[i];
-    }
-    const float rstd = 1.0f / sqrtf(block_sum(ss, red) * inv_d + a.eps);
+  for (int i = 0; i < KPER; ++i) {
+    const int d = threadIdx.x + i * kThreads;
+    const bool in = d < a.D;
+#pragma unroll
+    for (int seg = 0; seg < 3; ++seg) v[seg][i] = in ? to_f32(y[seg * a.D + d]) : 0.f;
+    xv[i] = in && x != nullptr ? to_f32(x[d]) : 0.f;
+  }
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < KPER; ++i) {
+#pragma unroll
+    for (int seg = 0; seg < 3; ++seg) ss[seg] += v[seg][i] * v[seg][i];
+    ss[3] += xv[i] * xv[i];
+  }
+  const int w = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float t = wave_sum(ss[k]);
+    if ((threadIdx.x & 63) == 0) red[k][w] = t;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float t = 0.f;
+#pragma unroll
+    for (int u = 0; u < kThreads / 64; ++u) t += red[k][u];
+    ss[k] = t;
+  }
+  // folded input norm: every projected value of the row scales by the row's 1 / rms
+  const float xs = x != nullptr ? 1.0f / sqrtf(ss[3] * inv_d + a.x_eps) : 1.0f;
+#pragma unroll
+  for (int seg = 0; seg < 3; ++seg) {
+    // RMSNorm of the scaled segment: mean((xs z)^2) = xs^2 mean(z^2)
+    const float rstd = 1.0f / sqrtf(xs * xs * ss[seg] * inv_d + a.eps);
     const T* wt = static_cast<const T*>(seg == 0 ? a.qw : seg == 1 ? a.kw : nullptr);
     T* o = static_cast<T*>(a.out[seg]) + (int64_t)r * a.out_rs;
 #pragma unroll
-    for (int i = 0; i < kMaxPer; ++i) {
+    for (int i = 0; i < KPER; ++i) {
       const int d = threadIdx.x + i * kThreads;
       if (d < a.D) {
         const float g = wt != nullptr ? to_f32(wt[d]) : 1.0f;
-        o[d] = from_f32<T>(v[i] * rstd * g);
+        o[d] = from_f32<T>(xs * v[seg][i] * rstd * g);
       }
     }
   }
@@ -84,6 +99,16 @@ __global__ void __launch_bounds__(kThreads) k_proj_epilogue(const ProjArgs a) {
     static_cast<T*>(a.eta)[r] = from_f32<T>(a.lr * sigmoidf_acc(ye));
     static_cast<T*>(a.alpha)[r] = from_f32<T>(a.wd * sigmoidf_acc(ya));
   }
+}
+
+template <typename T>
+void launch_epilogue(const ProjArgs& p, hipStream_t st) {
+  if (p.D <= 4 * kThreads)
+    hipLaunchKernelGGL((k_proj_epilogue<T, 4>), dim3(p.rows), dim3(kThreads), 0, st, p);
+  else if (p.D <= 8 * kThreads)
+    hipLaunchKernelGGL((k_proj_epilogue<T, 8>), dim3(p.rows), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((k_proj_epilogue<T, 16>), dim3(p.rows), dim3(kThreads), 0, st, p);
 }
 
 }  // namespace
@@ -125,8 +150,8 @@ extern "C" int uttt_proj_epilogue(const uttt_proj_epilogue_args* a, uttt_stream_
   p.ea_bias = a->eta_alpha_bias;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (a->act_dtype == UTTT_DTYPE_BF16)
-    hipLaunchKernelGGL(k_proj_epilogue<bf16>, dim3(p.rows), dim3(kThreads), 0, st, p);
+    launch_epilogue<bf16>(p, st);
   else
-    hipLaunchKernelGGL(k_proj_epilogue<float>, dim3(p.rows), dim3(kThreads), 0, st, p);
+    launch_epilogue<float>(p, st);
   return launch_status("uttt_proj_epilogue");
 }
