@@ -129,11 +129,13 @@ size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int64_t d_model
 int uttt_chunk_chain(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
                      uttt_stream_t stream);
 /* The same chain as layers + 1 stream-ordered stages, one per call, in order on one stream
- * with one workspace.  Layers run in groups of 4, the last layer alone: the stage of a
- * group's last layer forms the group's products with the chunk-start state and its key Gram
- * rows, and runs each of its layers (forward / backward through the state left by the layers
- * before it, the previous layer's clip / decay step); the other stages of a group launch
- * nothing.  Stage `layers` is the last layer's step and the state write.
+ * with one workspace.  Layers run in groups: one layer each while 8 * d_model * d_ff * batch
+ * bytes (the state read of one group's products) is at most 128 MiB, else groups of 4 with the
+ * last layer alone.  The stage of a group's last layer forms the group's products with the
+ * chunk-start state and its key Gram rows, and runs each of its layers (forward / backward
+ * through the state left by the layers before it, the previous layer's clip / decay step);
+ * the other stages of a group launch nothing.  Stage `layers` is the last layer's step and
+ * the state write.
  * Stage l reads only layers <= l, so only their k/v/eta/alpha pointers need to be set: a
  * caller can run stage l (on a second stream) as soon as layer l's inputs exist, while it
  * computes the next layers' forward passes.  The state write must follow every reader of the

@@ -24,7 +24,8 @@
 // chunk instead of once per layer, and W/S are written once per chunk instead of once per
 // layer.
 //
-// Launch sequence (one stream), layers in groups (of kPqGroup, the last kPqTail layers alone):
+// Launch sequence (one stream), layers in groups (single layers while one launch's state read is
+// small, else kPqGroup layers with the last kPqTail layers alone; pq_group_size):
 // at the stage of a group's last layer, pq (K_l W_s, K_l S_s for the group's layers) and the
 // key Gram rows of the group, then per layer l of the group: up (layer l - 1's clip / decay /
 // recurrence step, then U, G, H) -> H-gram -> down (Z partials) -> k_ln_grad (dZ, loss) ->
@@ -1010,18 +1011,29 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
 }
 
 constexpr int kPqTail = 1;
+constexpr double kPqSingleBytes = 128.0 * (1 << 20);
 
-// Layer groups of the snapshot products: [0, L - kPqTail) in groups of kPqGroup, then the last
+// Layers per snapshot-product launch.  A launch reads the four bf16 state tensors once (8 D F
+// bytes per row): while that is small, every layer gets its own launch, so the chain can start
+// after the first layer's projections and stay one layer behind the forward pass; when it is
+// large, groups of kPqGroup layers share it.  Measured: config 2 (100 MB per launch) 74.5 ms
+// with single layers against 79.0 ms with groups of four; config 3 (360 MB) 825 ms with groups
+// against 882 ms with single layers.
+int pq_group_size(int64_t B, int64_t D, int64_t F) {
+  return 8.0 * (double)D * (double)F * (double)B <= kPqSingleBytes ? 1 : kPqGroup;
+}
+
+// Layer groups of the snapshot products: [0, L - kPqTail) in groups of `size`, then the last
 // kPqTail layers one by one, so that little of the chain is left when the forward pass ends.
-void pq_group(int l, int L, int& g0, int& g1) {
+void pq_group(int l, int L, int size, int& g0, int& g1) {
   const int head = L - min(L, kPqTail);
-  if (l >= head) {
+  if (l >= head || size == 1) {
     g0 = l;
     g1 = l + 1;
     return;
   }
-  g0 = l - l % kPqGroup;
-  g1 = min(head, g0 + kPqGroup);
+  g0 = l - l % size;
+  g1 = min(head, g0 + size);
 }
 
 template <typename T>
@@ -1108,9 +1120,10 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   // Layers run in groups of kPqGroup: once a group's last layer is known (its stage), one
   // launch forms the snapshot products of the whole group, then each layer of the group runs.
   // Stages of the other layers of a group launch nothing.
+  const int gsize = pq_group_size(B, D, F);
   for (int l = 0; l < L; ++l) {
     int g0, g1;  // this layer's group [g0, g1)
-    pq_group(l, L, g0, g1);
+    pq_group(l, L, gsize, g0, g1);
     if (!want(g1 - 1)) continue;
     if (l == g0) {
       pa.l_begin = g0;
