@@ -974,6 +974,204 @@ __global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const App
   }
 }
 
+// bf16 activations: the token slabs go straight from global memory into LDS (buffer loads with
+// the lds bit, no registers, no staging instructions) through a ring of kApplySlots layer slots,
+// and reach the MFMA through transposing LDS reads.  Waits are explicit: each wave issues 4 slab
+// loads per layer, and the count of loads still allowed in flight is known at every step.  The
+// W and S tile loads follow the loop: the layer loop holds no state registers (81 VGPRs), and
+// four workgroups per CU overlap one workgroup's state traffic with the others' layer loops
+// (measured: faster than deeper slab prefetch at fewer workgroups, or state loads ahead of the
+// loop).
+//
+// Slab layout in LDS: 64 token rows of 128 bytes (64 columns); 16-byte piece p of row t sits in
+// slot p ^ swz(t), swz(t) = 4 ((t >> 1) & 1), which keeps the transposing reads of four
+// consecutive rows on distinct banks.
+constexpr int kApplySlots = 2;
+constexpr int kApplyLdsWaves = 4;  // 32 KB of LDS per workgroup: four workgroups per CU
+
+// s_waitcnt for "this wave's slab loads of all but the `ahead` most recently issued layers"
+template <int A>
+__device__ __forceinline__ void wait_slabs(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      wait_vmcnt<4 * A>();
+      return;
+    }
+    wait_slabs<A - 1>(ahead);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+__device__ __forceinline__ int slab_swz(int t) { return ((t >> 1) & 1) << 2; }
+
+__global__ void __launch_bounds__(kThreads, kApplyLdsWaves) k_chain_apply_lds(const ApplyChainArgs a) {
+  __shared__ __align__(1024) bf16 slab[kApplySlots][2][64 * 64];
+  const int nD = a.D / 64, nF = a.F / 64;
+  const int per = nD * nF;
+  const RowTile rt = row_tile(blockIdx.x, a.B, 3 * per);
+  if (!rt.valid) return;
+  const int m = rt.tile / per, jt = rt.tile - m * per, b = rt.b;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  // the coefficients are read-only here: constant-address-space reads become scalar loads
+  const __attribute__((address_space(4))) float* cf =
+      (const __attribute__((address_space(4))) float*)(uintptr_t)(a.coef + (int64_t)b * kCoefStride);
+  if (cf[3] == 0.f) return;  // no layer updated this row: W and S stay as they are
+  int r0, c0, ld_out;
+  const int ft = jt / nD, dt = jt - ft * nD;
+  if (m < 2) {
+    r0 = dt * 64;
+    c0 = ft * 64;
+    ld_out = a.F;
+  } else {
+    r0 = ft * 64;
+    c0 = dt * 64;
+    ld_out = a.D;
+  }
+  const int64_t mat = (int64_t)a.D * a.F;
+  // slab sources of layer j (wave-uniform): A = tokens x this tile's rows, B = tokens x its columns
+  const bf16* a_src;
+  const bf16* b_src;
+  int64_t a_lstride, b_lstride;
+  int a_ld, b_ld, a_rows;
+  if (m < 2) {
+    a_src = nullptr;  // per-layer key pointers
+    a_lstride = 0;
+    a_ld = (int)a.acts.kv_ts;
+    a_rows = a.C;
+    b_src = static_cast<const bf16*>(m == 0 ? a.du_all : a.dg_all) + (int64_t)b * 64 * a.F + c0;
+    b_ld = a.F;
+    b_lstride = (int64_t)a.B * 64 * a.F;
+  } else {
+    a_src = static_cast<const bf16*>(a.h_all) + (int64_t)b * 64 * a.F + r0;
+    a_ld = a.F;
+    a_lstride = (int64_t)a.B * 64 * a.F;
+    a_rows = 64;
+    b_src = static_cast<const bf16*>(a.dz_all) + (int64_t)b * 64 * a.D + c0;
+    b_ld = a.D;
+    b_lstride = (int64_t)a.B * 64 * a.D;
+  }
+  auto a_layer = [&](int j) -> const bf16* {
+    return m < 2 ? layer_row<bf16>(a.acts.k, j, b, a.acts.kv_rs) + r0 : a_src + j * a_lstride;
+  };
+  // this wave's slab loads: row groups w and w + 4 (8 token rows each) of both slabs; lane ->
+  // (row t, slot q), loading piece q ^ swz(t) of its row
+  const int trow = lane >> 3, q = lane & 7;
+  int a_off[2], b_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int t = 8 * (w + 4 * i) + trow;
+    const int p = q ^ slab_swz(t);
+    a_off[i] = (t * a_ld + p * 8) * 2;  // rows past a_rows are out of the buffer range: zeros
+    b_off[i] = (t * b_ld + p * 8) * 2;
+  }
+  const uint32_t slab0 = lds_addr(&slab[0][0][0]);
+  // layer j's slabs into slot j % kApplySlots; past the last layer the buffers have no range,
+  // so those loads touch no memory and only write zeros (the prologue stays branch-free)
+  auto issue = [&](int j) {
+    const bool live = j < a.L;
+    const int jj = live ? j : a.L - 1;
+    const uint32_t base = slab0 + (uint32_t)((j % kApplySlots) * 2 * 64 * 64 * 2);
+    const __amdgpu_buffer_rsrc_t ar = buffer_rsrc(a_layer(jj), live ? (uint32_t)(a_rows * a_ld * 2) : 0u);
+    const __amdgpu_buffer_rsrc_t br = buffer_rsrc(b_src + jj * b_lstride, live ? (uint32_t)(64 * b_ld * 2) : 0u);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      buffer_load_lds_raw(ar, lds_ptr(base + (uint32_t)((w + 4 * i) * 1024)), 16, a_off[i], 0, 0, 0);
+      buffer_load_lds_raw(br, lds_ptr(base + 8192u + (uint32_t)((w + 4 * i) * 1024)), 16, b_off[i], 0, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < kApplySlots - 1; ++j) issue(j);
+  // transposing-read addresses: lane (group g, j16) points at token row 8 (g >> 1) + j16 / 4
+  // (+ 16 s + 4 r for k step s, read r) and columns cb + 16 (g & 1) + 4 (j16 % 4)
+  const int g = lane >> 4, j16 = lane & 15;
+  auto tr_addr = [&](int cb, int slab_i) {
+    const int t = 8 * (g >> 1) + (j16 >> 2);
+    const int c = cb + 16 * (g & 1) + 4 * (j16 & 3);
+    return slab0 + (uint32_t)(slab_i * 8192 + t * 128 + (((c >> 3) ^ slab_swz(t)) * 16) + (c & 7) * 2);
+  };
+  const uint32_t ta = tr_addr(wr, 0), tb = tr_addr(wc, 1);
+  f32x16 accw, accs;
+  zero(accw);
+  zero(accs);
+  for (int j = 0; j < a.L; ++j) {
+    // this wave's slab loads of layer j are done once those of the later issued layers remain
+    wait_slabs<kApplySlots - 2>(min(a.L - 1, j + kApplySlots - 2) - j);
+    __builtin_amdgcn_s_barrier();  // every wave's loads of layer j landed; layer j - 1's slot is free
+    if (j + kApplySlots - 1 < a.L) issue(j + kApplySlots - 1);
+    const uint32_t so = (uint32_t)((j % kApplySlots) * 2 * 64 * 64 * 2);
+    bf16x8 fa[4], fb[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      // immediate offsets: k step s = 16 rows (2048 bytes), read r = 4 rows (512 bytes)
+      i16x4 a0, a1, b0, b1;
+      switch (s) {
+        case 0: a0 = lds_read_tr16<0>(ta + so); a1 = lds_read_tr16<512>(ta + so);
+                b0 = lds_read_tr16<0>(tb + so); b1 = lds_read_tr16<512>(tb + so); break;
+        case 1: a0 = lds_read_tr16<2048>(ta + so); a1 = lds_read_tr16<2560>(ta + so);
+                b0 = lds_read_tr16<2048>(tb + so); b1 = lds_read_tr16<2560>(tb + so); break;
+        case 2: a0 = lds_read_tr16<4096>(ta + so); a1 = lds_read_tr16<4608>(ta + so);
+                b0 = lds_read_tr16<4096>(tb + so); b1 = lds_read_tr16<4608>(tb + so); break;
+        default: a0 = lds_read_tr16<6144>(ta + so); a1 = lds_read_tr16<6656>(ta + so);
+                 b0 = lds_read_tr16<6144>(tb + so); b1 = lds_read_tr16<6656>(tb + so); break;
+      }
+      fa[s] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
+      fb[s] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+    // the reads above are invisible to the compiler's wait insertion: wait for them here, tied
+    // to the fragments so that no use moves above the wait
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]), "+v"(fb[2]),
+                   "+v"(fb[3]));
+    f32x16 t;
+    zero(t);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s], fb[s], t, 0, 0, 0);
+    const float gj = cf[kGam + j], sj = cf[kSig + j];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      accw[i] += gj * t[i];
+      accs[i] += sj * t[i];
+    }
+  }
+  const uint32_t mat_bytes = (uint32_t)(mat * 4);
+  const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(a.w[m] + b * mat, mat_bytes);
+  const __amdgpu_buffer_rsrc_t sres = buffer_rsrc(a.s[m] + b * mat, mat_bytes);
+  const int64_t tile0 = (int64_t)(r0 + wr) * ld_out + c0 + wc;
+  const int lane_el = (int)tile0 + 4 * (lane >> 5) * ld_out + acc_col();
+  auto row_el = [&](int i) { return (8 * (i >> 2) + (i & 3)) * ld_out; };
+  float wv[16], sv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    wv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wres, lane_el * 4, row_el(i) * 4,
+                                                                           kNonTemporal));
+    sv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sres, lane_el * 4, row_el(i) * 4,
+                                                                           kNonTemporal));
+  }
+  const float ca = cf[0], cb = cf[1], ce = cf[2];
+  const bool copies = a.wc[m] != nullptr;
+  const __amdgpu_buffer_rsrc_t wcres = buffer_rsrc(copies ? a.wc[m] + b * mat : nullptr, copies ? mat_bytes / 2 : 0);
+  const __amdgpu_buffer_rsrc_t scres = buffer_rsrc(copies ? a.sc[m] + b * mat : nullptr, copies ? mat_bytes / 2 : 0);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float w_new = ca * wv[i] + cb * sv[i] + accw[i];
+    const float s_new = ce * sv[i] + accs[i];
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, w_new), wres, lane_el * 4, row_el(i) * 4,
+                                          kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s_new), sres, lane_el * 4, row_el(i) * 4,
+                                          kNonTemporal);
+    // the bf16 copies are what the next chunk reads first: default cache policy
+    if (copies) {
+      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<bf16>(w_new)), wcres,
+                                            lane_el * 2, row_el(i) * 2, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<bf16>(s_new)), scres,
+                                            lane_el * 2, row_el(i) * 2, 0);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -1208,8 +1406,13 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   aa.sc[0] = static_cast<bf16*>(a.s_up_copy);
   aa.sc[1] = static_cast<bf16*>(a.s_gate_copy);
   aa.sc[2] = static_cast<bf16*>(a.s_down_copy);
-  if (want(L))
-    hipLaunchKernelGGL(k_chain_apply<T>, dim3(row_tile_blocks(B, 3 * (D / 64) * nF)), blk, 0, st, aa);
+  if (want(L)) {
+    const dim3 grid(row_tile_blocks(B, 3 * (D / 64) * nF));
+    if constexpr (sizeof(T) == 2)
+      hipLaunchKernelGGL(k_chain_apply_lds, grid, blk, 0, st, aa);
+    else
+      hipLaunchKernelGGL(k_chain_apply<T>, grid, blk, 0, st, aa);
+  }
 }
 
 int check_chain_dims(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dtype) {

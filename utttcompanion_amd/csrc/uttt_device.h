@@ -296,6 +296,44 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 }
 
 // ---------------------------------------------------------------------------
+// Direct global -> LDS loads and transposing LDS reads (gfx950)
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// buffer_load_dword{,x4} ... lds: lane i's `size` bytes land at the LDS address + i * size
+// (the LDS address is wave-uniform); out-of-range lanes write zeros
+__device__ void buffer_load_lds_raw(__amdgpu_buffer_rsrc_t rsrc, lds_void_ptr lds, int size, int voffset, int soffset,
+                                    int offset, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.load.lds");
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>(p);  // the low half of a generic LDS address is its offset
+}
+__device__ __forceinline__ lds_void_ptr lds_ptr(uint32_t addr) { return (lds_void_ptr)(uintptr_t)addr; }
+
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives element (i & 3) of the 8 bytes
+// that lane 4 e + (i >> 2) addresses, for e = 0..3.  With lane j of the group pointing at row
+// r0 + j / 4, columns c0 + 4 (j % 4) .. + 3 of a row-major 16-bit matrix, lane i receives column
+// c0 + i of rows r0 .. r0 + 3.  Issued as inline assembly so that the compiler adds no wait on
+// outstanding direct-to-LDS loads; the caller waits for lgkmcnt before using the result.  It
+// stays ordered with the barrier and wait builtins (all have side effects); no memory clobber,
+// which would keep the compiler from reading uniform kernel data with scalar loads.
+template <int OFF>
+__device__ __forceinline__ i16x4 lds_read_tr16(uint32_t addr) {
+  i16x4 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
 // Reductions
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
