@@ -88,6 +88,71 @@ inline int row_tile_blocks(int B, int ntiles) {
   return (B >= kXcds ? (B + kXcds - 1) / kXcds * kXcds : B) * ntiles;
 }
 
+// ---------------------------------------------------------------------------
+// Operands in LDS without register staging (bf16 activations): buffer loads with the lds bit
+// write 1 KB per wave instruction (lane i at +16 i), and the MFMA reads them back, through
+// transposing LDS reads for token-major slabs.  Both go around the compiler's wait tracking
+// (explicit vmcnt / lgkmcnt waits), so a kernel counts its own loads per step.
+//
+// Token slab: 64 token rows of 128 bytes (64 bf16 columns); 16-byte piece p of row t sits in
+// slot p ^ slab_swz(t), which keeps the transposing reads of four consecutive rows on distinct
+// banks.  One load instruction covers a row group of 8 rows.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int slab_swz(int t) { return ((t >> 1) & 1) << 2; }
+
+// source byte offset of this lane's piece in row group rg (row stride ld elements)
+__device__ __forceinline__ int slab_src_off(int rg, int lane, int ld) {
+  const int t = 8 * rg + (lane >> 3);
+  return (t * ld + ((lane & 7) ^ slab_swz(t)) * 8) * 2;
+}
+
+// LDS address of this lane's first transposing read for MFMA operand columns cb .. cb + 31:
+// lane (group g, j16) points at row 8 (g >> 1) + j16 / 4, columns cb + 16 (g & 1) + 4 (j16 % 4)
+__device__ __forceinline__ uint32_t slab_tr_addr(uint32_t slab, int cb, int lane) {
+  const int g = lane >> 4, j16 = lane & 15;
+  const int t = 8 * (g >> 1) + (j16 >> 2);
+  const int c = cb + 16 * (g & 1) + 4 * (j16 & 3);
+  return slab + (uint32_t)(t * 128 + (((c >> 3) ^ slab_swz(t)) * 16) + (c & 7) * 2);
+}
+
+// the four K = 16 MFMA operand fragments of a slab (k step s = rows 16 s .., read r = + 4 r rows)
+__device__ __forceinline__ void slab_frags(uint32_t addr, bf16x8 (&f)[4]) {
+  i16x4 r[8];
+  r[0] = lds_read_tr16<0>(addr);
+  r[1] = lds_read_tr16<512>(addr);
+  r[2] = lds_read_tr16<2048>(addr);
+  r[3] = lds_read_tr16<2560>(addr);
+  r[4] = lds_read_tr16<4096>(addr);
+  r[5] = lds_read_tr16<4608>(addr);
+  r[6] = lds_read_tr16<6144>(addr);
+  r[7] = lds_read_tr16<6656>(addr);
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    f[k] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[2 * k], r[2 * k + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// s_waitcnt for "this wave's loads of all but the `ahead` (<= A) most recently issued steps",
+// PER loads per wave and step
+template <int PER, int A>
+__device__ __forceinline__ void wait_steps(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      wait_vmcnt<PER * A>();
+      return;
+    }
+    wait_steps<PER, A - 1>(ahead);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
+
+// the reads above are invisible to the compiler's wait insertion: wait for them, tied to the
+// fragments so that no use moves above the wait
+__device__ __forceinline__ void lds_wait_frags(bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
+}
+
 // Store N (4 or 8) consecutive values to LDS as T with one vector write (dst aligned to N * sizeof(T)).
 template <typename T, int N>
 __device__ __forceinline__ void store_vec(T* dst, const float* v) {
@@ -563,6 +628,142 @@ __global__ void __launch_bounds__(kThreads) k_chain_up(const UpArgs a) {
   }
 }
 
+// bf16 activations: the correction loop's operands go straight into LDS -- per layer j < l the
+// key Gram block K_l K_j^T (fp32, 16 KB; scaled by gam_j and rounded to bf16 as the A fragments
+// are read) and the du_j, dg_j slabs (8 KB each, transposing reads) -- through a ring of
+// kUpSlots slots: one workgroup per CU, loads run up to three layers ahead.
+constexpr int kUpSlots = 4;
+constexpr int kUpSlotBytes = 16384 + 2 * 8192;
+
+// Key Gram block in LDS: 64 rows of 64 fp32 (256 bytes); 16-byte piece p of row r sits in slot
+// p ^ (r & 15), so the 16 rows one read instruction serves per cycle hit distinct banks.  One
+// load instruction covers a row group of 4 rows.
+__device__ __forceinline__ int gram_src_off(int rg, int lane, int ld) {
+  const int r = 4 * rg + (lane >> 4);
+  return (r * ld + ((lane & 15) ^ (r & 15)) * 4) * 4;
+}
+
+__device__ __forceinline__ f32x4 lds_read_b128(uint32_t addr) {
+  f32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ float lds_read_b32(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+__global__ void __launch_bounds__(kThreads, 1) k_chain_up_lds(const UpArgs a) {
+  __shared__ __align__(1024) char ring[kUpSlots * kUpSlotBytes];
+  __shared__ float cf[kCoefStride];
+  __shared__ float red[4];
+  const RowTile rt = row_tile(blockIdx.x, a.B, a.F / 64);
+  if (!rt.valid) return;
+  const int ft = rt.tile, b = rt.b, f0 = ft * 64;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  // loads that do not depend on the coefficients go out first: this tile's snapshot products
+  // and the first correction layers, so their latency overlaps the recurrence step below
+  const int64_t plane = (int64_t)a.L * a.B * 64 * a.F;
+  const bf16* pl = static_cast<const bf16*>(a.pq) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
+  const int col = wc + acc_col();
+  bf16 pw_u[16], pw_g[16], ps_u[16], ps_g[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
+    pw_u[i] = pl[off];
+    ps_u[i] = pl[plane + off];
+    pw_g[i] = pl[2 * plane + off];
+    ps_g[i] = pl[3 * plane + off];
+  }
+  const int64_t lstride = (int64_t)a.B * 64 * a.F;
+  const bf16* du0 = static_cast<const bf16*>(a.du_all) + (int64_t)b * 64 * a.F + f0;
+  const bf16* dg0 = static_cast<const bf16*>(a.dg_all) + (int64_t)b * 64 * a.F + f0;
+  const float* kk0 = a.kk + ((int64_t)b * a.LL + a.l * 64) * a.LL;  // layer j's block at + 64 j
+  int kk_off[4], d_off[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kk_off[i] = gram_src_off(w + 4 * i, lane, a.LL);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) d_off[i] = slab_src_off(w + 4 * i, lane, a.F);
+  const uint32_t ring0 = lds_addr(ring);
+  auto issue = [&](int j) {  // 8 loads per wave
+    const uint32_t base = ring0 + (uint32_t)((j % kUpSlots) * kUpSlotBytes);
+    const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(kk0 + 64 * j, (uint32_t)(64 * a.LL * 4));
+    const __amdgpu_buffer_rsrc_t ur = buffer_rsrc(du0 + j * lstride, (uint32_t)(64 * a.F * 2));
+    const __amdgpu_buffer_rsrc_t gr = buffer_rsrc(dg0 + j * lstride, (uint32_t)(64 * a.F * 2));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      buffer_load_lds_raw(kr, lds_ptr(base + (uint32_t)((w + 4 * i) * 1024)), 16, kk_off[i], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      buffer_load_lds_raw(ur, lds_ptr(base + 16384u + (uint32_t)((w + 4 * i) * 1024)), 16, d_off[i], 0, 0, 0);
+      buffer_load_lds_raw(gr, lds_ptr(base + 24576u + (uint32_t)((w + 4 * i) * 1024)), 16, d_off[i], 0, 0, 0);
+    }
+  };
+  for (int j = 0; j < min(a.l, kUpSlots - 1); ++j) issue(j);
+  if (a.l > 0) {
+    // the previous layer's recurrence step: every F tile of the row derives the same table,
+    // the first one publishes it (and that layer's surprise) for the layer's later kernels
+    advance_coef<bf16>(a.prev, b, cf, red, ft == 0);
+  } else {
+    for (int i = threadIdx.x; i < kCoefStride; i += kThreads) cf[i] = a.coef[(int64_t)b * kCoefStride + i];
+    __syncthreads();
+  }
+  // A fragments (k step s): row i = wr + lane % 32, fp32 pieces 4 s + 2 h and + 1 (h = lane / 32)
+  const int ia = wr + (lane & 31), ha = lane >> 5;
+  uint32_t aaddr[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) aaddr[q] = ring0 + (uint32_t)(ia * 256 + (((2 * q + 2 * ha - (q & 1)) ^ (ia & 15)) * 16));
+  const uint32_t tu = slab_tr_addr(ring0 + 16384u, wc, lane), tg = slab_tr_addr(ring0 + 24576u, wc, lane);
+  const uint32_t cf_gam = lds_addr(cf) + 4u * kGam;
+  f32x16 au, ag;
+  zero(au);
+  zero(ag);
+  for (int j = 0; j < a.l; ++j) {
+    // this wave's loads of layer j are done once those of the later issued layers remain
+    wait_steps<8, kUpSlots - 2>(min(a.l - 1, j + kUpSlots - 2) - j);
+    __builtin_amdgcn_s_barrier();  // every wave's loads of layer j landed; layer j - 1's slot is free
+    if (j + kUpSlots - 1 < a.l) issue(j + kUpSlots - 1);
+    const uint32_t so = (uint32_t)((j % kUpSlots) * kUpSlotBytes);
+    bf16x8 fu[4], fg[4];
+    slab_frags(tu + so, fu);
+    slab_frags(tg + so, fg);
+    f32x4 kv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) kv[q] = lds_read_b128(aaddr[q] + so);
+    float gj = lds_read_b32(cf_gam + 4u * (uint32_t)j);
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fu[0]), "+v"(fu[1]), "+v"(fu[2]), "+v"(fu[3]), "+v"(fg[0]), "+v"(fg[1]), "+v"(fg[2]),
+                   "+v"(fg[3]), "+v"(kv[0]), "+v"(kv[1]), "+v"(kv[2]), "+v"(kv[3]), "+v"(kv[4]), "+v"(kv[5]),
+                   "+v"(kv[6]), "+v"(kv[7]), "+v"(gj));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      bf16x8 fa;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        fa[e] = static_cast<bf16>(gj * kv[2 * k][e]);
+        fa[4 + e] = static_cast<bf16>(gj * kv[2 * k + 1][e]);
+      }
+      au = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fu[k], au, 0, 0, 0);
+      ag = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fg[k], ag, 0, 0, 0);
+    }
+  }
+  const float ca = cf[0], cb = cf[1];
+  const int64_t lane_base = (int64_t)b * 64 * a.F + f0;
+  bf16* h = static_cast<bf16*>(a.h_all) + ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
+    const float u = (ca * to_f32(pw_u[i]) + cb * to_f32(ps_u[i])) + au[i];
+    const float g = (ca * to_f32(pw_g[i]) + cb * to_f32(ps_g[i])) + ag[i];
+    a.u_cur[lane_base + off] = u;
+    a.g_cur[lane_base + off] = g;
+    h[off] = from_f32<bf16>((g * sigmoidf_acc(g)) * u);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 4. Z partials: splits < nsplit take H_l (a W_down,s + b S_down,s) over an F range;
 //    split nsplit (l > 0) takes sum_j gam_j (H_l H_j^T) dZ_j.
@@ -983,27 +1184,8 @@ __global__ void __launch_bounds__(kThreads, kApplyWaves) k_chain_apply(const App
 // (measured: faster than deeper slab prefetch at fewer workgroups, or state loads ahead of the
 // loop).
 //
-// Slab layout in LDS: 64 token rows of 128 bytes (64 columns); 16-byte piece p of row t sits in
-// slot p ^ swz(t), swz(t) = 4 ((t >> 1) & 1), which keeps the transposing reads of four
-// consecutive rows on distinct banks.
 constexpr int kApplySlots = 2;
 constexpr int kApplyLdsWaves = 4;  // 32 KB of LDS per workgroup: four workgroups per CU
-
-// s_waitcnt for "this wave's slab loads of all but the `ahead` most recently issued layers"
-template <int A>
-__device__ __forceinline__ void wait_slabs(int ahead) {
-  if constexpr (A > 0) {
-    if (ahead >= A) {
-      wait_vmcnt<4 * A>();
-      return;
-    }
-    wait_slabs<A - 1>(ahead);
-  } else {
-    wait_vmcnt<0>();
-  }
-}
-
-__device__ __forceinline__ int slab_swz(int t) { return ((t >> 1) & 1) << 2; }
 
 __global__ void __launch_bounds__(kThreads, kApplyLdsWaves) k_chain_apply_lds(const ApplyChainArgs a) {
   __shared__ __align__(1024) bf16 slab[kApplySlots][2][64 * 64];
@@ -1056,16 +1238,12 @@ __global__ void __launch_bounds__(kThreads, kApplyLdsWaves) k_chain_apply_lds(co
   auto a_layer = [&](int j) -> const bf16* {
     return m < 2 ? layer_row<bf16>(a.acts.k, j, b, a.acts.kv_rs) + r0 : a_src + j * a_lstride;
   };
-  // this wave's slab loads: row groups w and w + 4 (8 token rows each) of both slabs; lane ->
-  // (row t, slot q), loading piece q ^ swz(t) of its row
-  const int trow = lane >> 3, q = lane & 7;
+  // this wave's slab loads: row groups w and w + 4 (8 token rows each) of both slabs
   int a_off[2], b_off[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int t = 8 * (w + 4 * i) + trow;
-    const int p = q ^ slab_swz(t);
-    a_off[i] = (t * a_ld + p * 8) * 2;  // rows past a_rows are out of the buffer range: zeros
-    b_off[i] = (t * b_ld + p * 8) * 2;
+    a_off[i] = slab_src_off(w + 4 * i, lane, a_ld);  // rows past a_rows are out of the buffer range: zeros
+    b_off[i] = slab_src_off(w + 4 * i, lane, b_ld);
   }
   const uint32_t slab0 = lds_addr(&slab[0][0][0]);
   // layer j's slabs into slot j % kApplySlots; past the last layer the buffers have no range,
@@ -1084,47 +1262,20 @@ __global__ void __launch_bounds__(kThreads, kApplyLdsWaves) k_chain_apply_lds(co
   };
 #pragma unroll
   for (int j = 0; j < kApplySlots - 1; ++j) issue(j);
-  // transposing-read addresses: lane (group g, j16) points at token row 8 (g >> 1) + j16 / 4
-  // (+ 16 s + 4 r for k step s, read r) and columns cb + 16 (g & 1) + 4 (j16 % 4)
-  const int g = lane >> 4, j16 = lane & 15;
-  auto tr_addr = [&](int cb, int slab_i) {
-    const int t = 8 * (g >> 1) + (j16 >> 2);
-    const int c = cb + 16 * (g & 1) + 4 * (j16 & 3);
-    return slab0 + (uint32_t)(slab_i * 8192 + t * 128 + (((c >> 3) ^ slab_swz(t)) * 16) + (c & 7) * 2);
-  };
-  const uint32_t ta = tr_addr(wr, 0), tb = tr_addr(wc, 1);
+  const uint32_t ta = slab_tr_addr(slab0, wr, lane), tb = slab_tr_addr(slab0 + 8192u, wc, lane);
   f32x16 accw, accs;
   zero(accw);
   zero(accs);
   for (int j = 0; j < a.L; ++j) {
     // this wave's slab loads of layer j are done once those of the later issued layers remain
-    wait_slabs<kApplySlots - 2>(min(a.L - 1, j + kApplySlots - 2) - j);
+    wait_steps<4, kApplySlots - 2>(min(a.L - 1, j + kApplySlots - 2) - j);
     __builtin_amdgcn_s_barrier();  // every wave's loads of layer j landed; layer j - 1's slot is free
     if (j + kApplySlots - 1 < a.L) issue(j + kApplySlots - 1);
     const uint32_t so = (uint32_t)((j % kApplySlots) * 2 * 64 * 64 * 2);
     bf16x8 fa[4], fb[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      // immediate offsets: k step s = 16 rows (2048 bytes), read r = 4 rows (512 bytes)
-      i16x4 a0, a1, b0, b1;
-      switch (s) {
-        case 0: a0 = lds_read_tr16<0>(ta + so); a1 = lds_read_tr16<512>(ta + so);
-                b0 = lds_read_tr16<0>(tb + so); b1 = lds_read_tr16<512>(tb + so); break;
-        case 1: a0 = lds_read_tr16<2048>(ta + so); a1 = lds_read_tr16<2560>(ta + so);
-                b0 = lds_read_tr16<2048>(tb + so); b1 = lds_read_tr16<2560>(tb + so); break;
-        case 2: a0 = lds_read_tr16<4096>(ta + so); a1 = lds_read_tr16<4608>(ta + so);
-                b0 = lds_read_tr16<4096>(tb + so); b1 = lds_read_tr16<4608>(tb + so); break;
-        default: a0 = lds_read_tr16<6144>(ta + so); a1 = lds_read_tr16<6656>(ta + so);
-                 b0 = lds_read_tr16<6144>(tb + so); b1 = lds_read_tr16<6656>(tb + so); break;
-      }
-      fa[s] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
-      fb[s] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7));
-    }
-    // the reads above are invisible to the compiler's wait insertion: wait for them here, tied
-    // to the fragments so that no use moves above the wait
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]), "+v"(fb[2]),
-                   "+v"(fb[3]));
+    slab_frags(ta + so, fa);
+    slab_frags(tb + so, fb);
+    lds_wait_frags(fa, fb);
     f32x16 t;
     zero(t);
 #pragma unroll
@@ -1349,7 +1500,10 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     if (l > 0) ua.prev = coef_step(l - 1);
     ua.coef = cl; ua.pq = ws + c.pq; ua.kk = kk; ua.du_all = du_all; ua.dg_all = dg_all;
     ua.u_cur = u_cur; ua.g_cur = g_cur; ua.h_all = h_all;
-    hipLaunchKernelGGL(k_chain_up<T>, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
+    if constexpr (sizeof(T) == 2)
+      hipLaunchKernelGGL(k_chain_up_lds, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
+    else
+      hipLaunchKernelGGL(k_chain_up<T>, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
 
     ha.layer = l;
     ha.layer_end = l + 1;
