@@ -123,6 +123,11 @@ typedef struct {
   void* s_up_copy; void* s_gate_copy; void* s_down_copy;
   float* surprise;                   /* (layers,) batch-global surprise of each layer */
   float* row_loss;                   /* optional (layers, batch, 2): [sum of masked token losses, valid tokens] */
+  /* nonzero (bf16 copies only): layer l's products k_l W_up and k_l W_gate with the chunk-start
+   * state are written by the caller into the workspace slots uttt_chunk_chain_w_products names
+   * (uttt_swiglu_readout with keys) before stage l's second part runs; the stages form only the
+   * S products */
+  int32_t w_products_given;
 } uttt_chunk_chain_args;
 
 size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff, int32_t act_dtype);
@@ -142,6 +147,17 @@ int uttt_chunk_chain(const uttt_chunk_chain_args* args, void* workspace, size_t 
  * chunk-start state (the readouts).  Running every stage equals uttt_chunk_chain. */
 int uttt_chunk_chain_stage(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
                            int32_t stage, uttt_stream_t stream);
+/* One part of stage `stage`: part 1 launches its snapshot products and key Gram rows (they read
+ * only the keys of layers <= stage and the chunk-start state), part 2 the rest; part 1 then part
+ * 2 on one stream equals uttt_chunk_chain_stage (part 0).  Part 1 of stage l may run beside
+ * part 2 of stage l - 1 (on another stream): they touch disjoint workspace slots.  With
+ * w_products_given, part 2 of stage l must follow the caller's writes of layer l's products. */
+int uttt_chunk_chain_stage_part(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
+                                int32_t stage, int32_t part, uttt_stream_t stream);
+/* Byte offsets in the chain workspace of layer `layer`'s k W_up and k W_gate products
+ * ((batch, 64, d_ff) in the activation dtype, row stride 64 * d_ff). */
+int uttt_chunk_chain_w_products(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff, int32_t act_dtype,
+                                int32_t layer, size_t* up_offset, size_t* gate_offset);
 
 /* ---------------------------------------------------------------------------
  * 1c. Slow-projection epilogue.  Replaces the RMSNorm / sigmoid part of
@@ -185,6 +201,15 @@ typedef struct {
   const void* w_up; const void* w_gate; const void* w_down; int64_t w_row_stride; /* 0 = shared */
   const float* ln_weight; const float* ln_bias;
   void* out; int64_t out_row_stride;
+  /* Optional key products for the layer chain (NULL keys: none; bf16 activations, tokens <= 64):
+   * keys (batch, tokens, d_model), token stride d_model, row stride keys_row_stride; the call
+   * also writes keys W_up and keys W_gate (batch, 64, d_ff) in the activation dtype at
+   * key_up_out / key_gate_out (rows past tokens are 0), from the same weight reads as the readout,
+   * equal to the products uttt_chunk_chain forms itself (no counterpart in the reference: the
+   * snapshot products of SharedFastWeightPool.update_fast_weights' dual form, shared with the
+   * readout's reads of the same chunk-start weights). */
+  const void* keys; int64_t keys_row_stride;
+  void* key_up_out; void* key_gate_out;
 } uttt_readout_args;
 
 size_t uttt_readout_workspace(int64_t batch, int64_t tokens, int64_t d_model, int64_t d_ff, int32_t act_dtype);

@@ -171,3 +171,76 @@ def test_chain_rejects_bad_input():
     with pytest.raises(ValueError):  # in-place state must be fp32
         K.chunk_chain(ks, ks, [x[2].to(DEV) for x in layers], [x[3].to(DEV) for x in layers],
                       [t.double() for t in state], ln_w.to(DEV), ln_b.to(DEV), None, 0.9, 1.0, True, 1e-5)
+
+
+def _chain_run(layers, w, s, ln_w, ln_b, shared):
+    """Chunk-start state (fp32 + bf16 copies) and a stage-by-stage ChunkChainRun over it."""
+    from utttcompanion_amd import kernels as K
+    state = [t.clone().to(DEV) for t in w + s]
+    cps = [t.to(torch.bfloat16) for t in state]
+    b, c, _ = layers[0][0].shape
+    run = K.ChunkChainRun(len(layers), c, state, ln_w.to(DEV), ln_b.to(DEV), None, 0.9, 1.0, True, 1e-5,
+                          torch.bfloat16, copies=cps, w_products_given=shared)
+    return run, state, cps
+
+
+def _layer_inputs(layer):
+    return tuple(x.to(DEV, torch.bfloat16) for x in layer)
+
+
+@pytest.mark.parametrize("c, d", [(64, 256), (40, 192)])
+def test_readout_key_products_equal_chain_products(c, d):
+    """The readout's key block forms k W_up and k W_gate bit for bit as the chain's own
+    snapshot products (same operands, same MFMA order), and leaves the readout unchanged."""
+    from utttcompanion_amd import kernels as K
+    print(f"key products c={c} d={d}", flush=True)
+    layers, w, s, ln_w, ln_b = make_layers(1, 3, c, d, 384, seed=91, w_scale=0.05)
+    run, state, cps = _chain_run(layers, w, s, ln_w, ln_b, shared=False)
+    k, v, eta, alpha = _layer_inputs(layers[0])
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(3, c, d, generator=g).to(DEV, torch.bfloat16)
+    out_up = torch.full((3, 64, 384), float("nan"), dtype=torch.bfloat16, device=DEV)
+    out_gate = torch.full_like(out_up, float("nan"))
+    with torch.no_grad():
+        layer = run.set_layer(k, v, eta, alpha)
+        run.launch(layer, part=1)  # all four snapshot products of layer 0
+        plain = K.swiglu_readout(q, *cps[:3], ln_w.to(DEV), ln_b.to(DEV), 1e-5)
+        with_keys = K.swiglu_readout(q, *cps[:3], ln_w.to(DEV), ln_b.to(DEV), 1e-5, keys=k,
+                                     key_outputs=(out_up, out_gate))
+    torch.cuda.synchronize()
+    ref_up, ref_gate = run.w_product_outputs(0)
+    assert torch.equal(with_keys, plain)
+    assert torch.equal(out_up, ref_up)
+    assert torch.equal(out_gate, ref_gate)
+    assert torch.all(out_up[:, c:] == 0) and torch.all(out_gate[:, c:] == 0)
+    expect = (k.float() @ cps[0].float())  # loose check of the products themselves
+    assert (out_up[:, :c].float() - expect).abs().max().item() <= 2e-2 * expect.abs().max().item()
+
+
+def test_chain_with_shared_products_equals_plain_chain():
+    """Stage parts with the W products from the readouts give the same chunk, bit for bit, as
+    the whole stages forming every product themselves."""
+    from utttcompanion_amd import kernels as K
+    layers, w, s, ln_w, ln_b = make_layers(4, 3, 64, 256, 384, seed=23, w_scale=0.05)
+    g = torch.Generator().manual_seed(8)
+    qs = [torch.randn(3, 64, 256, generator=g).to(DEV, torch.bfloat16) for _ in layers]
+    run_a, state_a, cps_a = _chain_run(layers, w, s, ln_w, ln_b, shared=False)
+    run_b, state_b, cps_b = _chain_run(layers, w, s, ln_w, ln_b, shared=True)
+    with torch.no_grad():
+        for layer in layers:
+            run_a.add_layer(*_layer_inputs(layer))
+        surprise_a, _ = run_a.finish()
+        for l, layer in enumerate(layers):
+            k, v, eta, alpha = _layer_inputs(layer)
+            run_b.set_layer(k, v, eta, alpha)
+            run_b.launch(l, part=1)
+            K.swiglu_readout(qs[l], *cps_b[:3], ln_w.to(DEV), ln_b.to(DEV), 1e-5, keys=k,
+                             key_outputs=run_b.w_product_outputs(l))
+            run_b.launch(l, part=2)
+        surprise_b, _ = run_b.finish()
+    torch.cuda.synchronize()
+    for name, a, b_ in zip(NAMES, state_a, state_b):
+        assert torch.equal(a, b_), name
+    for a, b_ in zip(cps_a, cps_b):
+        assert torch.equal(a, b_)
+    assert torch.equal(surprise_a, surprise_b)

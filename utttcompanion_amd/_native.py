@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 MAX_CHAIN = 64
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -59,6 +59,7 @@ class ChunkChainArgs(C.Structure):
         ("w_up_copy", _P), ("w_gate_copy", _P), ("w_down_copy", _P),
         ("s_up_copy", _P), ("s_gate_copy", _P), ("s_down_copy", _P),
         ("surprise", _P), ("row_loss", _P),
+        ("w_products_given", _I32),
     ]
 
 
@@ -83,6 +84,8 @@ class ReadoutArgs(C.Structure):
         ("w_up", _P), ("w_gate", _P), ("w_down", _P), ("w_row_stride", _I64),
         ("ln_weight", _P), ("ln_bias", _P),
         ("out", _P), ("out_row_stride", _I64),
+        ("keys", _P), ("keys_row_stride", _I64),
+        ("key_up_out", _P), ("key_gate_out", _P),
     ]
 
 
@@ -148,6 +151,9 @@ SIGNATURES = {
     "uttt_chunk_chain_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_chunk_chain": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_chain_stage": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _P]),
+    "uttt_chunk_chain_stage_part": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _I32, _P]),
+    "uttt_chunk_chain_w_products": (C.c_int, [_I64, _I64, _I64, _I64, _I32, _I32, C.POINTER(C.c_size_t),
+                                              C.POINTER(C.c_size_t)]),
     "uttt_proj_epilogue": (C.c_int, [C.POINTER(ProjEpilogueArgs), _P]),
     "uttt_readout_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_swiglu_readout": (C.c_int, [C.POINTER(ReadoutArgs), _P, C.c_size_t, _P]),

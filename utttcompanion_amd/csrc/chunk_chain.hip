@@ -265,6 +265,7 @@ struct PqArgs {
   Acts acts;
   const void* x[4];  // fp32 state or its bf16 copies
   void* pq;  // (4, L, B, 64, F) act dtype
+  int s_only;  // products with S_up and S_gate only (m = 1, 3): the caller gave the W products
 };
 
 template <typename T, typename WT, int G>
@@ -273,10 +274,12 @@ __global__ void __launch_bounds__(kThreads, 2) k_chain_pq(const PqArgs a) {
   __shared__ __align__(16) T bs[64 * LD];
   __shared__ __align__(16) T as[G * 64 * LD];
   const int nlg = (a.l_count + G - 1) / G;
-  const RowTile rt = row_tile(blockIdx.x, a.B, 4 * (a.F / 64) * nlg);
+  const int nm = a.s_only ? 2 : 4;  // matrices of this launch (the launch grid holds nm * F / 64 tiles per row)
+  const RowTile rt = row_tile(blockIdx.x, a.B, nm * (a.F / 64) * nlg);
   if (!rt.valid) return;
   // tile = (m, F tile, layer group) with the layer groups that share an X tile adjacent
-  const int b = rt.b, lg = rt.tile % nlg, ft = (rt.tile / nlg) % (a.F / 64), m = rt.tile / (nlg * (a.F / 64));
+  const int mi = rt.tile / (nlg * (a.F / 64));
+  const int b = rt.b, lg = rt.tile % nlg, ft = (rt.tile / nlg) % (a.F / 64), m = a.s_only ? 2 * mi + 1 : mi;
   const int f0 = ft * 64, l0 = a.l_begin + lg * G;
   const int nl = min(G, a.l_begin + a.l_count - l0);
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
@@ -1386,8 +1389,9 @@ void pq_group(int l, int L, int size, int& g0, int& g1) {
 }
 
 template <typename T>
+// parts: bit 0 the snapshot products and key Gram rows of the stages, bit 1 the rest
 void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c, hipStream_t st, int first,
-                  int last) {
+                  int last, int parts) {
   const int B = (int)a.batch, L = (int)a.layers, C = (int)a.tokens, D = (int)a.d_model, F = (int)a.d_ff;
   const int LL = L * 64, nF = F / 64;
   const dim3 blk(kThreads);
@@ -1421,8 +1425,9 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   // stage l (< L): layer l (stage 0 also initialises the coefficient table); stage L: the last
   // layer's recurrence step and the state write
   auto want = [&](int stage) { return first <= stage && stage <= last; };
+  const bool keys_part = parts & 1, rest_part = parts & 2;
   const int ncoef = B * kCoefStride;  // table of layer 0
-  if (want(0))
+  if (want(0) && rest_part)
     hipLaunchKernelGGL(k_chain_init, dim3((ncoef + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef);
 
   // the chunk-start state the bf16 kernels read: its bf16 copies when given, else the masters
@@ -1435,7 +1440,8 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     pa.x[0] = a.w_up; pa.x[1] = a.s_up; pa.x[2] = a.w_gate; pa.x[3] = a.s_gate;
   }
   pa.pq = ws + c.pq;
-  const dim3 pq_grid(row_tile_blocks(B, 4 * nF));  // one layer group per launch
+  pa.s_only = a.w_products_given != 0;
+  const dim3 pq_grid(row_tile_blocks(B, (pa.s_only ? 2 : 4) * nF));  // one layer group per launch
   const void* wd_src = bf16_src ? a.w_down_copy : static_cast<const void*>(a.w_down);
   const void* sd_src = bf16_src ? a.s_down_copy : static_cast<const void*>(a.s_down);
 
@@ -1474,7 +1480,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     int g0, g1;  // this layer's group [g0, g1)
     pq_group(l, L, gsize, g0, g1);
     if (!want(g1 - 1)) continue;
-    if (l == g0) {
+    if (l == g0 && keys_part) {
       pa.l_begin = g0;
       pa.l_count = g1 - g0;
       if (g1 - g0 == 1) {  // a single layer: one staged K tile, less LDS per workgroup
@@ -1488,11 +1494,12 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
         hipLaunchKernelGGL((k_chain_pq<T, float, kPqGroup>), pq_grid, blk, 0, st, pa);
       }
     }
-    if (l == g0) {  // key Gram rows of the whole group
+    if (l == g0 && keys_part) {  // key Gram rows of the whole group
       ka.layer = g0;
       ka.layer_end = g1;
       hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(g0, g1))), dim3(kGramWaves * 64), 0, st, ka);
     }
+    if (!rest_part) continue;
     const float* cl = table(l);
 
     UpArgs ua{};
@@ -1545,7 +1552,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
   }
 
-  if (want(L)) {
+  if (want(L) && rest_part) {
     const CoefArgs last = coef_step(L - 1);
     hipLaunchKernelGGL(k_chain_coef<T>, dim3(B), blk, 0, st, last);
   }
@@ -1560,7 +1567,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   aa.sc[0] = static_cast<bf16*>(a.s_up_copy);
   aa.sc[1] = static_cast<bf16*>(a.s_gate_copy);
   aa.sc[2] = static_cast<bf16*>(a.s_down_copy);
-  if (want(L)) {
+  if (want(L) && rest_part) {
     const dim3 grid(row_tile_blocks(B, 3 * (D / 64) * nF));
     if constexpr (sizeof(T) == 2)
       hipLaunchKernelGGL(k_chain_apply_lds, grid, blk, 0, st, aa);
@@ -1594,7 +1601,7 @@ extern "C" size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int6
 }
 
 static int run_chain(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes, uttt_stream_t stream,
-                     int first, int last) {
+                     int first, int last, int parts = 3) {
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   int rc = check_chain_dims(a->batch, a->layers, a->d_model, a->d_ff, a->act_dtype);
   if (rc != UTTT_OK) return rc;
@@ -1625,15 +1632,16 @@ static int run_chain(const uttt_chunk_chain_args* a, void* workspace, size_t wor
                "bf16 state copies must be 16-byte aligned");
   UTTT_REQUIRE(a->momentum_beta >= 0.f && a->max_inner_grad_norm >= 0.f && a->min_row_surprise >= 0.f,
                "momentum_beta, max_inner_grad_norm and min_row_surprise must be >= 0");
+  UTTT_REQUIRE(!a->w_products_given || all_copy, "w_products_given needs the bf16 state copies");
   const ChainLayout c = chain_layout(a->batch, a->layers, a->d_model, a->d_ff, a->act_dtype);
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= c.total, "workspace too small: need %zu bytes, got %zu",
                c.total, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   if (a->act_dtype == UTTT_DTYPE_BF16)
-    launch_chain<bf16>(*a, ws, c, st, first, last);
+    launch_chain<bf16>(*a, ws, c, st, first, last, parts);
   else
-    launch_chain<float>(*a, ws, c, st, first, last);
+    launch_chain<float>(*a, ws, c, st, first, last, parts);
   return launch_status("uttt_chunk_chain");
 }
 
@@ -1647,4 +1655,25 @@ extern "C" int uttt_chunk_chain_stage(const uttt_chunk_chain_args* a, void* work
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   UTTT_REQUIRE(stage >= 0 && stage <= a->layers, "stage must be in [0, layers] (got %d)", stage);
   return run_chain(a, workspace, workspace_bytes, stream, stage, stage);
+}
+
+extern "C" int uttt_chunk_chain_stage_part(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes,
+                                           int32_t stage, int32_t part, uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  UTTT_REQUIRE(stage >= 0 && stage <= a->layers, "stage must be in [0, layers] (got %d)", stage);
+  UTTT_REQUIRE(part >= 0 && part <= 2, "part must be 0 (whole stage), 1 or 2 (got %d)", part);
+  return run_chain(a, workspace, workspace_bytes, stream, stage, stage, part == 0 ? 3 : part);
+}
+
+extern "C" int uttt_chunk_chain_w_products(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff,
+                                           int32_t act_dtype, int32_t layer, size_t* up_offset, size_t* gate_offset) {
+  int rc = check_chain_dims(batch, layers, d_model, d_ff, act_dtype);
+  if (rc != UTTT_OK) return rc;
+  UTTT_REQUIRE(layer >= 0 && layer < layers, "layer must be in [0, layers) (got %d)", layer);
+  UTTT_REQUIRE(up_offset != nullptr && gate_offset != nullptr, "offset outputs must be non-NULL");
+  const ChainLayout c = chain_layout(batch, layers, d_model, d_ff, act_dtype);
+  const size_t slot = act_size(act_dtype) * (size_t)batch * 64 * (size_t)d_ff;  // one (m, layer) slot
+  *up_offset = c.pq + slot * (size_t)(0 * layers + layer);
+  *gate_offset = c.pq + slot * (size_t)(2 * layers + layer);
+  return UTTT_OK;
 }

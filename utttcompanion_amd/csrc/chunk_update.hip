@@ -42,6 +42,12 @@ struct FwdArgs {
   float* g_store;
   void* h[2];      // act dtype (B, tok_pad, F)
   float* zp;       // fp32 (paths, nsplit, B, tok_pad, D)
+  // optional key block (readout only): the last z block multiplies these rows (token stride D)
+  // by path 0's W_up / W_gate and writes both products (act dtype, (B, 64, F)) instead of H
+  const void* kx;
+  int64_t kx_rs;
+  void* ku;
+  void* kg;
 };
 
 // ---------------------------------------------------------------------------
@@ -54,10 +60,12 @@ __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
   __shared__ __align__(16) T us[64 * LD];
   __shared__ __align__(16) T gs[64 * LD];
   const int ft = blockIdx.x, b = blockIdx.y;
-  const int path = blockIdx.z / a.ntb, tb = blockIdx.z - path * a.ntb;
+  const bool key_block = a.kx != nullptr && blockIdx.z == gridDim.z - 1;
+  const int path = key_block ? 0 : blockIdx.z / a.ntb, tb = key_block ? 0 : blockIdx.z - path * a.ntb;
   const int f0 = ft * 64, t0 = tb * 64;
   const int rows = min(64, a.ntok - t0);
-  const T* x = static_cast<const T*>(a.x[path]) + (int64_t)b * a.x_rs[path] + (int64_t)t0 * a.D;
+  const T* x = key_block ? static_cast<const T*>(a.kx) + (int64_t)b * a.kx_rs
+                         : static_cast<const T*>(a.x[path]) + (int64_t)b * a.x_rs[path] + (int64_t)t0 * a.D;
   // threads [0, U) stage W_up, [U, 2U) W_gate (U units of 8 rows x one 16-byte chunk)
   constexpr int U = ColStage<WT, KTL>::kUnits;
   static_assert(2 * U <= kThreads, "W_up and W_gate stage in separate halves of the workgroup");
@@ -87,10 +95,21 @@ __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
     __syncthreads();
   }
 
+  const int col = wc + acc_col();
+  if (key_block) {  // both products, rows past ntok are 0 (zero-filled key rows)
+    T* ku = static_cast<T*>(a.ku) + (int64_t)b * 64 * a.F + f0;
+    T* kg = static_cast<T*>(a.kg) + (int64_t)b * 64 * a.F + f0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
+      ku[off] = from_f32<T>(au[i]);
+      kg[off] = from_f32<T>(ag[i]);
+    }
+    return;
+  }
   const int64_t base = ((int64_t)b * a.tok_pad + t0) * a.F + f0;
   T* h = static_cast<T*>(a.h[path]) + base;
   const bool store_ug = path == 0 && a.u_store != nullptr;
-  const int col = wc + acc_col();
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int row = wr + acc_row(i);
@@ -615,14 +634,17 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   f.u_store = nullptr; f.g_store = nullptr;
   f.h[0] = ws + L.h;
   f.zp = reinterpret_cast<float*>(ws + L.zp);
+  f.kx = a.keys; f.kx_rs = a.keys_row_stride; f.ku = a.key_up_out; f.kg = a.key_gate_out;
   const dim3 blk(kThreads);
   // bf16 weights: K tiles of 128 halve the staged steps of these latency-bound loops where the
-  // shape allows
+  // shape allows.  The key block (when asked for) is one more z block: it runs beside the token
+  // blocks of the same F tile and row, on the same XCD, so its weight tiles come from that L2.
   constexpr bool wide = sizeof(WT) == 2;
+  const dim3 ug_grid(F / 64, B, L.ntb + (a.keys != nullptr ? 1 : 0));
   if (wide && D % 128 == 0)
-    hipLaunchKernelGGL((k_up_gate<T, WT, wide ? 128 : KT>), dim3(F / 64, B, L.ntb), blk, 0, st, f);
+    hipLaunchKernelGGL((k_up_gate<T, WT, wide ? 128 : KT>), ug_grid, blk, 0, st, f);
   else
-    hipLaunchKernelGGL((k_up_gate<T, WT>), dim3(F / 64, B, L.ntb), blk, 0, st, f);
+    hipLaunchKernelGGL((k_up_gate<T, WT>), ug_grid, blk, 0, st, f);
   if (wide && F % 128 == 0)
     hipLaunchKernelGGL((k_down_partial<T, WT, wide ? 128 : KT>), dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
   else
@@ -729,6 +751,13 @@ extern "C" int uttt_swiglu_readout(const uttt_readout_args* a, void* workspace, 
                "workspace too small: need %zu bytes, got %zu", L.total, workspace_bytes);
   UTTT_REQUIRE(a->w_dtype == UTTT_DTYPE_F32 || (a->w_dtype == UTTT_DTYPE_BF16 && a->act_dtype == UTTT_DTYPE_BF16),
                "w_dtype must be F32, or BF16 with BF16 activations");
+  if (a->keys != nullptr) {
+    UTTT_REQUIRE(a->act_dtype == UTTT_DTYPE_BF16, "key products need bf16 activations");
+    UTTT_REQUIRE(a->tokens <= 64, "key products need tokens <= 64 (got %lld)", (long long)a->tokens);
+    UTTT_REQUIRE(a->key_up_out != nullptr && a->key_gate_out != nullptr, "key product outputs must be non-NULL");
+    UTTT_REQUIRE(aligned16(a->keys) && a->keys_row_stride % 8 == 0,
+                 "keys must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   if (a->act_dtype == UTTT_DTYPE_BF16) {

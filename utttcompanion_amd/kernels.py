@@ -269,13 +269,18 @@ class PreparedChain:
         self.args, self._keep, self.workspace, self.result, self.device = args, keep, workspace, result, device
         self.n_layers = n_layers
 
-    def launch(self, stage: Optional[int] = None) -> Tuple[Tensor, Optional[Tensor]]:
-        """Enqueue the whole chain, or one of its ``layers + 1`` stream-ordered stages."""
+    def launch(self, stage: Optional[int] = None, part: int = 0) -> Tuple[Tensor, Optional[Tensor]]:
+        """Enqueue the whole chain, or one of its ``layers + 1`` stream-ordered stages, or one
+        part of a stage (1: its snapshot products and key Gram rows, 2: the rest)."""
         lib = N.load_library()
         with torch.cuda.device(self.device):
             if stage is None:
                 rc = lib.uttt_chunk_chain(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
                                           _stream(self.device))
+            elif part:
+                rc = lib.uttt_chunk_chain_stage_part(C.byref(self.args), _p(self.workspace),
+                                                     self.workspace.numel(), int(stage), int(part),
+                                                     _stream(self.device))
             else:
                 rc = lib.uttt_chunk_chain_stage(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
                                                 int(stage), _stream(self.device))
@@ -297,16 +302,23 @@ class ChunkChainRun(PreparedChain):
     current stream; it reads only layers <= l, so it can run while the caller computes the
     next layers.  ``finish()`` enqueues the last stage (the state write), which must follow
     every reader of the chunk-start state and its copies.  Arguments as ``prepare_chunk_chain``
-    with the layer count and chunk length given up front."""
+    with the layer count and chunk length given up front.
+
+    With ``w_products_given`` (bf16 copies only) the caller forms layer l's products
+    k_l W_up and k_l W_gate with the chunk-start copies itself, into ``w_product_outputs(l)``
+    (``swiglu_readout(..., keys=k_l, key_outputs=...)`` shares the readout's weight reads),
+    before stage l's second part (``launch(l, part=2)``) runs."""
 
     def __init__(self, n_layers: int, tokens: int, state: Sequence[Tensor], ln_weight: Tensor, ln_bias: Tensor,
                  token_mask: Optional[Tensor], momentum_beta: float, max_inner_grad_norm: float,
                  normalize_by_dim: bool, eps: float, act_dtype: torch.dtype,
                  copies: Optional[Sequence[Tensor]] = None, surprise: Optional[Tensor] = None,
                  row_loss: Optional[Tensor] = None, min_row_surprise: float = 0.0,
-                 workspace: Optional[Tensor] = None) -> None:
+                 workspace: Optional[Tensor] = None, w_products_given: bool = False) -> None:
         if not 1 <= n_layers <= N.MAX_CHAIN:
             raise ValueError(f"need 1..{N.MAX_CHAIN} layers")
+        if w_products_given and copies is None:
+            raise ValueError("w_products_given needs the bf16 state copies")
         if not 1 <= tokens <= 64:
             raise ValueError(f"a chunk holds 1..64 tokens on the HIP path, got {tokens}")
         code = _act_code(act_dtype)
@@ -369,10 +381,24 @@ class ChunkChainRun(PreparedChain):
             (a.w_up_copy, a.w_gate_copy, a.w_down_copy,
              a.s_up_copy, a.s_gate_copy, a.s_down_copy) = (_p(c) for c in copies)
         a.surprise, a.row_loss = _p(surprise), _p(row_loss)
+        a.w_products_given = int(bool(w_products_given))
         keep += [ln_w, ln_b, state, copies]
         super().__init__(a, keep, workspace, (surprise, row_loss), dev, n_layers)
-        self._act, self._shape = act_dtype, (bsz, tokens, dim)
+        self._act, self._shape, self._ff, self._code = act_dtype, (bsz, tokens, dim), ff, code
         self.layers_added = 0
+
+    def w_product_outputs(self, layer: int) -> Tuple[Tensor, Tensor]:
+        """Workspace views (B, 64, d_ff) that take layer ``layer``'s k W_up and k W_gate."""
+        bsz, _, dim = self._shape
+        up, gate = C.c_size_t(0), C.c_size_t(0)
+        N.check(N.load_library().uttt_chunk_chain_w_products(bsz, self.n_layers, dim, self._ff, self._code,
+                                                               int(layer), C.byref(up), C.byref(gate)),
+                "uttt_chunk_chain_w_products")
+        n = bsz * 64 * self._ff * torch.empty((), dtype=self._act).element_size()
+
+        def view(off: int) -> Tensor:
+            return self.workspace[off:off + n].view(self._act).view(bsz, 64, self._ff)
+        return view(up.value), view(gate.value)
 
     def set_layer(self, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor) -> int:
         """Record the next layer's inputs without launching; returns its index."""
@@ -510,12 +536,16 @@ def readout_workspace(x: Tensor, w_up: Tensor) -> Tensor:
 
 def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_weight: Tensor,
                    ln_bias: Tensor, eps: float = 1e-5, out: Optional[Tensor] = None,
-                   workspace: Optional[Tensor] = None) -> Tensor:
+                   workspace: Optional[Tensor] = None, keys: Optional[Tensor] = None,
+                   key_outputs: Optional[Tuple[Tensor, Tensor]] = None) -> Tensor:
     """f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down) with per-row (or shared) W.
 
     W is read as fp32 masters, or -- when x and all three weights are bf16 -- as bf16 read
     copies (the reference casts W to the activation dtype for these matmuls, so a bf16
-    copy yields the same operands at half the bytes)."""
+    copy yields the same operands at half the bytes).  With ``keys`` (B, T <= 64, D) bf16 the
+    same weight reads also give keys W_up and keys W_gate, written to ``key_outputs``
+    ((B, 64, d_ff) each, rows past T zero): the layer chain's products with the chunk-start
+    copies (``ChunkChainRun.w_product_outputs``)."""
     if x.dim() != 3:
         raise ValueError(f"x must be (B, T, D), got {tuple(x.shape)}")
     bsz, tokens, dim = x.shape
@@ -550,6 +580,20 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
     a.w_row_stride = parts[0][1]
     a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
     a.out, a.out_row_stride = _p(out), out.stride(0)
+    if keys is not None:
+        if not bf16_copies or tokens > 64:
+            raise ValueError("key products need bf16 activations and weights and at most 64 tokens")
+        if keys.shape != (bsz, tokens, dim) or keys.dtype != x.dtype:
+            raise ValueError(f"keys must be ({bsz}, {tokens}, {dim}) {x.dtype}")
+        _require_device(dev, keys)
+        _forward_only(keys)
+        keys = _rows(keys)
+        if key_outputs is None or len(key_outputs) != 2 or any(
+                t.shape != (bsz, 64, ff) or t.dtype != x.dtype or not t.is_contiguous() or t.device != dev
+                for t in key_outputs):
+            raise ValueError(f"key_outputs must be two contiguous ({bsz}, 64, {ff}) {x.dtype} tensors")
+        a.keys, a.keys_row_stride = _p(keys), keys.stride(0)
+        a.key_up_out, a.key_gate_out = _p(key_outputs[0]), _p(key_outputs[1])
     with torch.cuda.device(dev):
         N.check(lib.uttt_swiglu_readout(C.byref(a), _p(workspace), workspace.numel(), _stream(dev)),
                 "uttt_swiglu_readout")

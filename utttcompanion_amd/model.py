@@ -245,6 +245,11 @@ class uTTTModel(nn.Module):
         main = torch.cuda.current_stream(dev)
         side = self._chain_stream(dev)
         ws_chain = ws_read = None
+        # bf16: each layer's readout also forms the chain's products of that layer's keys with
+        # W_up / W_gate (one read of those weights for both), and the chain stage runs in two
+        # parts: the S products and key Gram rows as soon as the keys exist, the rest after the
+        # readout
+        shared = copies is not None
         for ci in range(n_chunks):
             off = ci * c
             end = min(seq, off + c)
@@ -254,7 +259,7 @@ class uTTTModel(nn.Module):
             hid = h[:, off:end].contiguous()  # this chunk's residual stream, updated in place
             run = K.ChunkChainRun(n_layers, end - off, cur, ln_w, ln_b, mask, pool.momentum_beta, clip,
                                   pool.normalize_loss_by_dim, pool.eps, h.dtype, copies=copies,
-                                  surprise=surprises[ci], workspace=ws_chain)
+                                  surprise=surprises[ci], workspace=ws_chain, w_products_given=shared)
             ws_chain = run.workspace
             for li, block in enumerate(self.layers):
                 attn = block.attn
@@ -268,13 +273,24 @@ class uTTTModel(nn.Module):
                 ready.record(main)
                 if ws_read is None:
                     ws_read = K.readout_workspace(uq, read[0])
-                r = K.swiglu_readout(uq, *read, ln_w, ln_b, pool.eps, workspace=ws_read)
+                r = K.swiglu_readout(uq, *read, ln_w, ln_b, pool.eps, workspace=ws_read,
+                                     keys=uk if shared else None,
+                                     key_outputs=run.w_product_outputs(li) if shared else None)
+                if shared:
+                    read_done = torch.cuda.Event()
+                    read_done.record(main)
                 hid = linear_residual(hid, r, block.uttt.w_o.weight)
                 # the chain stage is enqueued after the readout it overlaps, so that a captured
                 # graph's executor keeps the forward pass on one in-order queue of its own
                 side.wait_event(ready)
                 with torch.cuda.stream(side):
-                    run.add_layer(uk, uv, eta, alpha)
+                    if shared:
+                        layer = run.set_layer(uk, uv, eta, alpha)
+                        run.launch(layer, part=1)
+                        side.wait_event(read_done)
+                        run.launch(layer, part=2)
+                    else:
+                        run.add_layer(uk, uv, eta, alpha)
             side.wait_stream(main)
             with torch.cuda.stream(side):
                 run.finish()
