@@ -88,70 +88,6 @@ inline int row_tile_blocks(int B, int ntiles) {
   return (B >= kXcds ? (B + kXcds - 1) / kXcds * kXcds : B) * ntiles;
 }
 
-// ---------------------------------------------------------------------------
-// Operands in LDS without register staging (bf16 activations): buffer loads with the lds bit
-// write 1 KB per wave instruction (lane i at +16 i), and the MFMA reads them back, through
-// transposing LDS reads for token-major slabs.  Both go around the compiler's wait tracking
-// (explicit vmcnt / lgkmcnt waits), so a kernel counts its own loads per step.
-//
-// Token slab: 64 token rows of 128 bytes (64 bf16 columns); 16-byte piece p of row t sits in
-// slot p ^ slab_swz(t), which keeps the transposing reads of four consecutive rows on distinct
-// banks.  One load instruction covers a row group of 8 rows.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int slab_swz(int t) { return ((t >> 1) & 1) << 2; }
-
-// source byte offset of this lane's piece in row group rg (row stride ld elements)
-__device__ __forceinline__ int slab_src_off(int rg, int lane, int ld) {
-  const int t = 8 * rg + (lane >> 3);
-  return (t * ld + ((lane & 7) ^ slab_swz(t)) * 8) * 2;
-}
-
-// LDS address of this lane's first transposing read for MFMA operand columns cb .. cb + 31:
-// lane (group g, j16) points at row 8 (g >> 1) + j16 / 4, columns cb + 16 (g & 1) + 4 (j16 % 4)
-__device__ __forceinline__ uint32_t slab_tr_addr(uint32_t slab, int cb, int lane) {
-  const int g = lane >> 4, j16 = lane & 15;
-  const int t = 8 * (g >> 1) + (j16 >> 2);
-  const int c = cb + 16 * (g & 1) + 4 * (j16 & 3);
-  return slab + (uint32_t)(t * 128 + (((c >> 3) ^ slab_swz(t)) * 16) + (c & 7) * 2);
-}
-
-// the four K = 16 MFMA operand fragments of a slab (k step s = rows 16 s .., read r = + 4 r rows)
-__device__ __forceinline__ void slab_frags(uint32_t addr, bf16x8 (&f)[4]) {
-  i16x4 r[8];
-  r[0] = lds_read_tr16<0>(addr);
-  r[1] = lds_read_tr16<512>(addr);
-  r[2] = lds_read_tr16<2048>(addr);
-  r[3] = lds_read_tr16<2560>(addr);
-  r[4] = lds_read_tr16<4096>(addr);
-  r[5] = lds_read_tr16<4608>(addr);
-  r[6] = lds_read_tr16<6144>(addr);
-  r[7] = lds_read_tr16<6656>(addr);
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    f[k] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(r[2 * k], r[2 * k + 1], 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-// s_waitcnt for "this wave's loads of all but the `ahead` (<= A) most recently issued steps",
-// PER loads per wave and step
-template <int PER, int A>
-__device__ __forceinline__ void wait_steps(int ahead) {
-  if constexpr (A > 0) {
-    if (ahead >= A) {
-      wait_vmcnt<PER * A>();
-      return;
-    }
-    wait_steps<PER, A - 1>(ahead);
-  } else {
-    wait_vmcnt<0>();
-  }
-}
-
-// the reads above are invisible to the compiler's wait insertion: wait for them, tied to the
-// fragments so that no use moves above the wait
-__device__ __forceinline__ void lds_wait_frags(bf16x8 (&a)[4], bf16x8 (&b)[4]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]));
-}
 
 // Store N (4 or 8) consecutive values to LDS as T with one vector write (dst aligned to N * sizeof(T)).
 template <typename T, int N>
@@ -646,16 +582,6 @@ __device__ __forceinline__ int gram_src_off(int rg, int lane, int ld) {
   return (r * ld + ((lane & 15) ^ (r & 15)) * 4) * 4;
 }
 
-__device__ __forceinline__ f32x4 lds_read_b128(uint32_t addr) {
-  f32x4 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
-}
-__device__ __forceinline__ float lds_read_b32(uint32_t addr) {
-  float v;
-  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
-  return v;
-}
 
 __global__ void __launch_bounds__(kThreads, 1) k_chain_up_lds(const UpArgs a) {
   __shared__ __align__(1024) char ring[kUpSlots * kUpSlotBytes];
