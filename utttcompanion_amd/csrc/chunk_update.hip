@@ -265,6 +265,70 @@ __global__ void __launch_bounds__(kThreads) k_down_partial(const FwdArgs a) {
   for (int i = 0; i < 16; ++i) zp[(int64_t)(wr + acc_row(i)) * a.D + col] = acc[i];
 }
 
+// bf16 activations and weights: the H rows and W_down tiles of each F step go straight into LDS
+// through a ring of kDpSlots steps of 64 (W_down rows f hold 64 d columns: transposing reads);
+// the same split boundaries and the same accumulation order as k_down_partial.
+constexpr int kDpSlots = 4;
+
+__global__ void __launch_bounds__(kThreads) k_down_partial_lds(const FwdArgs a, int kb) {
+  constexpr int kSlot = 2 * 8192;  // H tile, W_down tile
+  constexpr int PER = 4;           // 16 row groups per step over 4 waves
+  __shared__ __align__(1024) char ring[kDpSlots * kSlot];
+  const int dt = blockIdx.x, split = blockIdx.y;
+  const int b = blockIdx.z % a.B, pt = blockIdx.z / a.B;
+  const int path = pt / a.ntb, tb = pt - path * a.ntb;
+  const int d0 = dt * 64, t0 = tb * 64;
+  const int nK = a.F / kb;  // F ranges in whole blocks of kb, as k_down_partial<.., kb>
+  const int f_begin = (nK * split / a.nsplit) * kb, f_end = (nK * (split + 1) / a.nsplit) * kb;
+  const int nsteps = (f_end - f_begin) / 64;
+  const bf16* h = static_cast<const bf16*>(a.h[path]) + ((int64_t)b * a.tok_pad + t0) * a.F + f_begin;
+  const bf16* wd = static_cast<const bf16*>(a.wd[path]) + (int64_t)b * a.w_rs[path] + (int64_t)f_begin * a.D + d0;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  int voff[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int g = w + 4 * i;  // groups 0..7: H rows, 8..15: W_down rows
+    voff[i] = g < 8 ? row_src_off(g & 7, lane, a.F) : slab_src_off(g & 7, lane, a.D);
+  }
+  const uint32_t ring0 = lds_addr(ring);
+  auto issue = [&](int step) {
+    const uint32_t base = ring0 + (uint32_t)((step % kDpSlots) * kSlot);
+    const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(h + step * 64, (uint32_t)(64 * a.F * 2));
+    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wd + (int64_t)step * 64 * a.D, (uint32_t)(64 * a.D * 2));
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int g = w + 4 * i;
+      buffer_load_lds_raw(g < 8 ? rh : rw, lds_ptr(base + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
+    }
+  };
+  for (int j = 0; j < min(nsteps, kDpSlots - 1); ++j) issue(j);
+  uint32_t ta[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ta[k] = row_frag_addr(ring0, wr, lane, k);
+  const uint32_t tw = slab_tr_addr(ring0 + 8192u, wc, lane);
+  f32x16 acc;
+  zero(acc);
+  for (int step = 0; step < nsteps; ++step) {
+    wait_steps<PER, kDpSlots - 2>(min(nsteps - 1, step + kDpSlots - 2) - step);
+    __builtin_amdgcn_s_barrier();  // every wave's loads of this step landed; the last step's slot is free
+    if (step + kDpSlots - 1 < nsteps) issue(step + kDpSlots - 1);
+    const uint32_t so = (uint32_t)((step % kDpSlots) * kSlot);
+    bf16x8 fa[4], fw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) fa[k] = lds_read_bf16x8<0>(ta[k] + so);
+    slab_frags(tw + so, fw);
+    lds_wait_frags(fa, fw);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fw[k], acc, 0, 0, 0);
+  }
+  float* zp = a.zp + ((((int64_t)path * a.nsplit + split) * a.B + b) * a.tok_pad + t0) * a.D + d0;
+  const int col = wc + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zp[(int64_t)(wr + acc_row(i)) * a.D + col] = acc[i];
+}
+
 // ---------------------------------------------------------------------------
 // 3. LayerNorm, reconstruction error, token loss and dZ (K path): k_ln_grad, update_ln.h
 // ---------------------------------------------------------------------------
@@ -756,10 +820,13 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   } else {
     hipLaunchKernelGGL((k_up_gate<T, WT>), ug_grid, blk, 0, st, f);
   }
-  if (wide && F % 128 == 0)
-    hipLaunchKernelGGL((k_down_partial<T, WT, wide ? 128 : KT>), dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
+  const dim3 dp_grid(D / 64, L.nsplit, L.ntb * B);
+  if constexpr (sizeof(T) == 2 && sizeof(WT) == 2)
+    hipLaunchKernelGGL(k_down_partial_lds, dp_grid, blk, 0, st, f, F % 128 == 0 ? 128 : KT);
+  else if (wide && F % 128 == 0)
+    hipLaunchKernelGGL((k_down_partial<T, WT, wide ? 128 : KT>), dp_grid, blk, 0, st, f);
   else
-    hipLaunchKernelGGL((k_down_partial<T, WT>), dim3(D / 64, L.nsplit, L.ntb * B), blk, 0, st, f);
+    hipLaunchKernelGGL((k_down_partial<T, WT>), dp_grid, blk, 0, st, f);
   LnOutArgs o{};
   o.B = B; o.ntok = (int)a.tokens; o.D = D; o.nsplit = L.nsplit; o.tok_pad = f.tok_pad; o.eps = a.eps;
   o.zp = f.zp; o.x = a.x; o.x_rs = a.x_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
