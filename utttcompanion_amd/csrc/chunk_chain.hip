@@ -364,6 +364,93 @@ __global__ void __launch_bounds__(kGramWaves * 64) k_chain_gram(const GramArgs a
   }
 }
 
+// bf16 activations: one workgroup per 64 x 64 block (b, l, j) -- each operand row read once
+// per block, not once per quadrant.  Eight waves: the four 32 x 32 quadrants times two halves of
+// the feature range, each half streaming coalesced 64-wide row tiles of X_l and X_j straight into
+// LDS through its own ring of kGramSlots steps; the halves' sums meet in LDS.
+constexpr int kGramSlots = 3;
+
+__host__ __device__ inline int gram_blocks(int l0, int l1) { return (l1 * (l1 + 1) - l0 * (l0 + 1)) / 2; }
+
+__global__ void __launch_bounds__(512) k_chain_gram_lds(const GramArgs a) {
+  constexpr int kSlot = 16384;  // X_l rows, X_j rows (64 x 64 bf16 each)
+  constexpr int kHalf = kGramSlots * kSlot;
+  constexpr int PER = 4;        // 16 row groups per step over the 4 waves of a half
+  __shared__ __align__(1024) char ring[2 * kHalf];
+  const RowTile rt = row_tile(blockIdx.x, a.B, gram_blocks(a.layer, a.layer_end));
+  if (!rt.valid) return;
+  int l = a.layer, j = rt.tile;
+  while (j >= l + 1) {  // at most layer_end - layer steps
+    j -= l + 1;
+    ++l;
+  }
+  const int b = rt.b;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int kh = w >> 2, q = w & 3;
+  const int n = a.kd / 64, nh = (n + 1) / 2;
+  const int s_begin = kh * nh, mine = min(n, s_begin + nh) - s_begin;  // this half's steps
+  const bf16* xa = layer_row<bf16>(a.x, l, b, a.rs);
+  const bf16* xb = layer_row<bf16>(a.x, j, b, a.rs);
+  const int ts = (int)a.ts;
+  int voff[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) voff[i] = row_src_off((q + 4 * i) & 7, lane, ts);
+  const uint32_t ring0 = lds_addr(ring) + (uint32_t)(kh * kHalf);
+  auto issue = [&](int t) {  // this half's step t; rows past C are out of the buffer range: zeros
+    const int k0 = (s_begin + t) * 64;
+    const uint32_t base = ring0 + (uint32_t)((t % kGramSlots) * kSlot);
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(xa + k0, (uint32_t)(a.C * ts * 2));
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(xb + k0, (uint32_t)(a.C * ts * 2));
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int g = q + 4 * i;  // groups 0..7: X_l rows, 8..15: X_j rows
+      buffer_load_lds_raw(g < 8 ? ra : rb, lds_ptr(base + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
+    }
+  };
+  for (int t = 0; t < min(mine, kGramSlots - 1); ++t) issue(t);
+  uint32_t ta[4], tb[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    ta[k] = row_frag_addr(ring0, (q >> 1) * 32, lane, k);
+    tb[k] = row_frag_addr(ring0 + 8192u, (q & 1) * 32, lane, k);
+  }
+  f32x16 acc;
+  zero(acc);
+  for (int t = 0; t < nh; ++t) {  // both halves run nh rounds: the barriers match
+    if (t < mine) wait_steps<PER, kGramSlots - 2>(min(mine - 1, t + kGramSlots - 2) - t);
+    __builtin_amdgcn_s_barrier();
+    if (t + kGramSlots - 1 < mine) issue(t + kGramSlots - 1);
+    if (t < mine) {
+      const uint32_t so = (uint32_t)((t % kGramSlots) * kSlot);
+      bf16x8 fa[4], fb[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        fa[k] = lds_read_bf16x8<0>(ta[k] + so);
+        fb[k] = lds_read_bf16x8<0>(tb[k] + so);
+      }
+      lds_wait_frags(fa, fb);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fb[k], acc, 0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_barrier();  // every read of the rings is done: half 0's ring takes the sums
+  float* red = reinterpret_cast<float*>(ring);
+  if (kh == 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[(q * 16 + i) * 64 + lane] = acc[i];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  float* out = a.out + ((int64_t)b * a.out_rows + a.out_r0 + l * a.out_lstep) * a.LL;
+  const int c = j * 64 + (q & 1) * 32 + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int row = (q >> 1) * 32 + acc_row(i);
+    out[(int64_t)row * a.LL + c] = acc[i] + red[(q * 16 + i) * 64 + lane];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 3a. Per row: |g_l|^2, clip, decay, active flag, surprise; advance the recurrences.
 // ---------------------------------------------------------------------------
@@ -1314,6 +1401,17 @@ void pq_group(int l, int L, int size, int& g0, int& g1) {
   g1 = min(head, g0 + size);
 }
 
+// Gram block rows [l0, l1) of every row b
+template <typename T>
+void launch_gram(int B, int l0, int l1, GramArgs g, hipStream_t st) {
+  g.layer = l0;
+  g.layer_end = l1;
+  if constexpr (sizeof(T) == 2)
+    hipLaunchKernelGGL(k_chain_gram_lds, dim3(row_tile_blocks(B, gram_blocks(l0, l1))), dim3(512), 0, st, g);
+  else
+    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l0, l1))), dim3(kGramWaves * 64), 0, st, g);
+}
+
 template <typename T>
 // parts: bit 0 the snapshot products and key Gram rows of the stages, bit 1 the rest
 void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c, hipStream_t st, int first,
@@ -1423,7 +1521,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     if (l == g0 && keys_part) {  // key Gram rows of the whole group
       ka.layer = g0;
       ka.layer_end = g1;
-      hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(g0, g1))), dim3(kGramWaves * 64), 0, st, ka);
+      launch_gram<T>(B, g0, g1, ka, st);
     }
     if (!rest_part) continue;
     const float* cl = table(l);
@@ -1440,7 +1538,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
     ha.layer = l;
     ha.layer_end = l + 1;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l, l + 1))), dim3(kGramWaves * 64), 0, st, ha);
+    launch_gram<T>(B, l, l + 1, ha, st);
 
     DownArgs da{};
     da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
@@ -1465,7 +1563,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
     za.layer = l;
     za.layer_end = l + 1;
-    hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l, l + 1))), dim3(kGramWaves * 64), 0, st, za);
+    launch_gram<T>(B, l, l + 1, za, st);
 
     BackArgs ba{};
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
