@@ -277,6 +277,71 @@ __global__ void __launch_bounds__(kThreads, 2) k_chain_pq(const PqArgs a) {
   }
 }
 
+// bf16 activations and copies, one layer: the key rows and the X tiles go straight into LDS
+// through a ring of kPqSlots d steps of 64 (X rows d hold 64 f columns: transposing reads); the
+// products accumulate over d in the same order as the readout's key products.
+constexpr int kPqSlots = 3;
+
+__global__ void __launch_bounds__(kThreads) k_chain_pq_lds(const PqArgs a) {
+  constexpr int kSlot = 2 * 8192;  // key rows, X tile
+  constexpr int PER = 4;           // 16 row groups per step over 4 waves
+  __shared__ __align__(1024) char ring[kPqSlots * kSlot];
+  const int nF = a.F / 64, nm = a.s_only ? 2 : 4;
+  const RowTile rt = row_tile(blockIdx.x, a.B, nm * nF);
+  if (!rt.valid) return;
+  const int mi = rt.tile / nF, ft = rt.tile - mi * nF, b = rt.b;
+  const int m = a.s_only ? 2 * mi + 1 : mi, f0 = ft * 64, l = a.l_begin;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  const bf16* kr = layer_row<bf16>(a.acts.k, l, b, a.acts.kv_rs);
+  const bf16* xs = static_cast<const bf16*>(a.x[m]) + (int64_t)b * a.D * a.F + f0;
+  const int kts = (int)a.acts.kv_ts;
+  int voff[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int g = w + 4 * i;  // groups 0..7: key rows, 8..15: X rows
+    voff[i] = g < 8 ? row_src_off(g & 7, lane, kts) : slab_src_off(g & 7, lane, a.F);
+  }
+  const uint32_t ring0 = lds_addr(ring);
+  const int nsteps = a.D / 64;
+  auto issue = [&](int step) {  // key rows past C are out of the buffer range: zeros
+    const int d0 = step * 64;
+    const uint32_t base = ring0 + (uint32_t)((step % kPqSlots) * kSlot);
+    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kr + d0, (uint32_t)(a.C * kts * 2));
+    const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(xs + (int64_t)d0 * a.F, (uint32_t)(64 * a.F * 2));
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int g = w + 4 * i;
+      buffer_load_lds_raw(g < 8 ? rk : rx, lds_ptr(base + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
+    }
+  };
+  for (int j = 0; j < min(nsteps, kPqSlots - 1); ++j) issue(j);
+  uint32_t ta[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ta[k] = row_frag_addr(ring0, wr, lane, k);
+  const uint32_t tx = slab_tr_addr(ring0 + 8192u, wc, lane);
+  f32x16 acc;
+  zero(acc);
+  for (int step = 0; step < nsteps; ++step) {
+    wait_steps<PER, kPqSlots - 2>(min(nsteps - 1, step + kPqSlots - 2) - step);
+    __builtin_amdgcn_s_barrier();  // every wave's loads of this step landed; the last step's slot is free
+    if (step + kPqSlots - 1 < nsteps) issue(step + kPqSlots - 1);
+    const uint32_t so = (uint32_t)((step % kPqSlots) * kSlot);
+    bf16x8 fa[4], fx[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) fa[k] = lds_read_bf16x8<0>(ta[k] + so);
+    slab_frags(tx + so, fx);
+    lds_wait_frags(fa, fx);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fx[k], acc, 0, 0, 0);
+  }
+  bf16* out = static_cast<bf16*>(a.pq) + (((int64_t)m * a.L + l) * a.B + b) * 64 * a.F + f0;
+  const int col = wc + acc_col();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) out[(int64_t)(wr + acc_row(i)) * a.F + col] = from_f32<bf16>(acc[i]);
+}
+
 // ---------------------------------------------------------------------------
 // 2. Gram blocks G[l][j] = X_l X_j^T over the feature dimension for the layers l in
 //    [layer, layer_end) and every j <= l, operands loaded straight from global memory (rows
@@ -1508,7 +1573,9 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
       pa.l_begin = g0;
       pa.l_count = g1 - g0;
       if (g1 - g0 == 1) {  // a single layer: one staged K tile, less LDS per workgroup
-        if (bf16_src)
+        if (sizeof(T) == 2 && bf16_src)
+          hipLaunchKernelGGL(k_chain_pq_lds, pq_grid, blk, 0, st, pa);
+        else if (bf16_src)
           hipLaunchKernelGGL((k_chain_pq<T, bf16, 1>), pq_grid, blk, 0, st, pa);
         else
           hipLaunchKernelGGL((k_chain_pq<T, float, 1>), pq_grid, blk, 0, st, pa);
