@@ -1069,6 +1069,175 @@ __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
   if (threadIdx.x == 0) a.npart[(int64_t)b * (a.F / 64) + ft] = total;
 }
 
+// bf16 activations and copies: both loops' operands go straight into LDS through one ring of
+// kBackSlots steps -- D/64 steps of dZ_l rows with the W_down and S_down rows of this F tile
+// (k = d along every row), then l steps of the scaled dZ Gram block (fp32, as in k_chain_up_lds)
+// with the H_j slab (transposing reads).  dZ (a W_d + b S_d)^T is formed as a dZ W_d^T + b dZ S_d^T
+// with two accumulators, the combined weights never rounded to bf16.
+constexpr int kBackSlots = 4;
+
+__global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a) {
+  constexpr int kSlot = 24576;  // dZ, W_d, S_d tiles; or the Gram block (16 KB) and the H slab
+  constexpr int PER = 6;        // 24 row groups per step over 4 waves
+  constexpr int LD = lds_ld<bf16>();
+  __shared__ __align__(1024) char ring[kBackSlots * kSlot];
+  __shared__ __align__(16) bf16 dus[64 * LD];  // [t][f]
+  __shared__ __align__(16) bf16 dgs[64 * LD];
+  __shared__ float red[4];
+  const RowTile rt = row_tile(blockIdx.x, a.B, a.F / 64);
+  if (!rt.valid) return;
+  const int ft = rt.tile, b = rt.b, f0 = ft * 64;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  // the coefficients are read-only here: constant-address-space reads become scalar loads
+  const __attribute__((address_space(4))) float* cf =
+      (const __attribute__((address_space(4))) float*)(uintptr_t)(a.coef + (int64_t)b * kCoefStride);
+  const float ca = cf[0], cb = cf[1];
+  const bool with_s = cb != 0.f;
+  // the epilogue's cursor values go out first
+  const int64_t base = (int64_t)b * 64 * a.F + f0;
+  const int f = wc + acc_col();
+  float uc[16], gc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + f;
+    uc[i] = a.u_cur[base + off];
+    gc[i] = a.g_cur[base + off];
+  }
+  const bf16* dz = static_cast<const bf16*>(a.dz_all) + ((int64_t)a.l * a.B + b) * 64 * a.D;
+  const int64_t mat = (int64_t)a.F * a.D;
+  const bf16* wd = static_cast<const bf16*>(a.wd) + b * mat + (int64_t)f0 * a.D;
+  const bf16* sd = static_cast<const bf16*>(a.sd) + b * mat + (int64_t)f0 * a.D;
+  const float* zz = a.zz + (int64_t)b * 64 * a.LL;  // layer j's block at + 64 j
+  const bf16* hsrc = static_cast<const bf16*>(a.h_all) + (int64_t)b * 64 * a.F + f0;
+  const int64_t lstride = (int64_t)a.B * 64 * a.F;
+  const int n1 = a.D / 64, nst = n1 + a.l;
+  // row group g of a step: phase 1: 0..7 dZ rows, 8..15 W_d rows, 16..23 S_d rows (8 rows each);
+  // phase 2: 0..15 Gram rows (4 rows each), 16..23 H rows; wave w takes groups w, w + 4, ...
+  int v1[PER], v2[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int g = w + 4 * i;
+    v1[i] = row_src_off(g & 7, lane, a.D);
+    v2[i] = g < 16 ? gram_src_off(g, lane, a.LL) : slab_src_off(g & 7, lane, a.F);
+  }
+  const uint32_t ring0 = lds_addr(ring);
+  auto issue = [&](int step) {
+    const uint32_t slot = ring0 + (uint32_t)((step % kBackSlots) * kSlot);
+    if (step < n1) {
+      const int d0 = step * 64;
+      const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(dz + d0, (uint32_t)(64 * a.D * 2));
+      const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wd + d0, (uint32_t)(64 * a.D * 2));
+      // without S the S loads have no range: they move no data and keep the per-step count
+      const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(sd + d0, with_s ? (uint32_t)(64 * a.D * 2) : 0u);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int g = w + 4 * i;
+        buffer_load_lds_raw(g < 8 ? rz : (g < 16 ? rw : rs), lds_ptr(slot + (uint32_t)(g * 1024)), 16, v1[i], 0,
+                            0, 0);
+      }
+    } else {
+      const int j = step - n1;
+      const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(zz + 64 * j, (uint32_t)(64 * a.LL * 4));
+      const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(hsrc + j * lstride, (uint32_t)(64 * a.F * 2));
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int g = w + 4 * i;
+        buffer_load_lds_raw(g < 16 ? rg : rh, lds_ptr(slot + (uint32_t)(g * 1024)), 16, v2[i], 0, 0, 0);
+      }
+    }
+  };
+  for (int j = 0; j < min(nst, kBackSlots - 1); ++j) issue(j);
+  uint32_t tz[4], tw[4], ts[4], tg[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    tz[k] = row_frag_addr(ring0, wr, lane, k);
+    tw[k] = row_frag_addr(ring0 + 8192u, wc, lane, k);
+    ts[k] = row_frag_addr(ring0 + 16384u, wc, lane, k);
+  }
+  // Gram A fragments: row wr + lane % 32, fp32 pieces 4 s + 2 h and + 1 (h = lane / 32)
+  const int ia = wr + (lane & 31), ha = lane >> 5;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) tg[q] = ring0 + (uint32_t)(ia * 256 + (((2 * q + 2 * ha - (q & 1)) ^ (ia & 15)) * 16));
+  const uint32_t th = slab_tr_addr(ring0 + 16384u, wc, lane);
+  f32x16 accw, accs, accg;
+  zero(accw);
+  zero(accs);
+  zero(accg);
+  for (int step = 0; step < nst; ++step) {
+    wait_steps<PER, kBackSlots - 2>(min(nst - 1, step + kBackSlots - 2) - step);
+    __builtin_amdgcn_s_barrier();  // every wave's loads of this step landed; the last step's slot is free
+    if (step + kBackSlots - 1 < nst) issue(step + kBackSlots - 1);
+    const uint32_t so = (uint32_t)((step % kBackSlots) * kSlot);
+    if (step < n1) {
+      bf16x8 fz[4], fw[4], fs[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        fz[k] = lds_read_bf16x8<0>(tz[k] + so);
+        fw[k] = lds_read_bf16x8<0>(tw[k] + so);
+        fs[k] = lds_read_bf16x8<0>(ts[k] + so);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(fz[0]), "+v"(fz[1]), "+v"(fz[2]), "+v"(fz[3]), "+v"(fw[0]), "+v"(fw[1]), "+v"(fw[2]),
+                     "+v"(fw[3]), "+v"(fs[0]), "+v"(fs[1]), "+v"(fs[2]), "+v"(fs[3]));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        accw = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fz[k], fw[k], accw, 0, 0, 0);
+        if (with_s) accs = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fz[k], fs[k], accs, 0, 0, 0);
+      }
+    } else {
+      const int j = step - n1;
+      bf16x8 fh[4];
+      slab_frags(th + so, fh);
+      f32x4 kv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) kv[q] = lds_read_b128(tg[q] + so);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(fh[0]), "+v"(fh[1]), "+v"(fh[2]), "+v"(fh[3]), "+v"(kv[0]), "+v"(kv[1]), "+v"(kv[2]),
+                     "+v"(kv[3]), "+v"(kv[4]), "+v"(kv[5]), "+v"(kv[6]), "+v"(kv[7]));
+      const float gj = cf[kGam + j];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        bf16x8 fa;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          fa[e] = static_cast<bf16>(gj * kv[2 * k][e]);
+          fa[4 + e] = static_cast<bf16>(gj * kv[2 * k + 1][e]);
+        }
+        accg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fh[k], accg, 0, 0, 0);
+      }
+    }
+  }
+  const int64_t lbase = ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int t = wr + acc_row(i);
+    const int64_t off = (int64_t)t * a.F + f;
+    const float dh = (ca * accw[i] + cb * accs[i]) + accg[i];
+    const float u = uc[i], g = gc[i];
+    const float sg = sigmoidf_acc(g);
+    const bf16 du = from_f32<bf16>(dh * (g * sg));
+    const bf16 dg = from_f32<bf16>(dh * u * (sg * (1.0f + g * (1.0f - sg))));
+    static_cast<bf16*>(a.du_all)[lbase + off] = du;
+    static_cast<bf16*>(a.dg_all)[lbase + off] = dg;
+    dus[t * LD + f] = du;
+    dgs[t * LD + f] = dg;
+  }
+  __syncthreads();
+  f32x16 gu, gg;
+  zero(gu);
+  zero(gg);
+  wave_mma<bf16, 64>(gu, dus + wr * LD, LD, dus + wc * LD, LD);
+  wave_mma<bf16, 64>(gg, dgs + wr * LD, LD, dgs + wc * LD, LD);
+  const float* kk = a.kk + ((int64_t)b * a.LL + a.l * 64) * a.LL + a.l * 64;
+  float part = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) part += (gu[i] + gg[i]) * kk[(int64_t)(wr + acc_row(i)) * a.LL + wc + acc_col()];
+  const float total = block_sum(part, red);
+  if (threadIdx.x == 0) a.npart[(int64_t)b * (a.F / 64) + ft] = total;
+}
+
 // ---------------------------------------------------------------------------
 // 7. Final state: W' = a W_s + b S_s + sum_j gam_j g_j, S' = e S_s + sum_j sig_j g_j per
 //    64 x 64 tile, with g_j tiles rebuilt from the small activations (K = 64 per layer).
@@ -1636,7 +1805,9 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
     ba.coef = cl; ba.dz_all = dz_all; ba.wd = wd_src; ba.sd = sd_src; ba.zz = zz; ba.h_all = h_all;
     ba.u_cur = u_cur; ba.g_cur = g_cur; ba.kk = kk; ba.du_all = du_all; ba.dg_all = dg_all; ba.npart = npart;
-    if (bf16_src)
+    if (sizeof(T) == 2 && bf16_src)
+      hipLaunchKernelGGL(k_chain_back_lds, dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
+    else if (bf16_src)
       hipLaunchKernelGGL((k_chain_back<T, bf16>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
     else
       hipLaunchKernelGGL((k_chain_back<T, float>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
