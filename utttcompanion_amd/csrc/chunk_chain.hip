@@ -931,6 +931,140 @@ __global__ void __launch_bounds__(kThreads) k_chain_down(const DownArgs a) {
   for (int i = 0; i < 16; ++i) zp[(int64_t)(wr + acc_row(i)) * a.D + col] = acc[i];
 }
 
+
+// bf16 activations and copies: a main split streams H_l rows (k = f) with the W_down and S_down
+// tiles of its F range (rows f hold 64 d columns: transposing reads), a correction split the
+// scaled H Gram blocks (fp32, as in k_chain_up_lds) with the dZ_j slabs, straight into LDS
+// through a ring of kDownSlots steps.  H (a W_d + b S_d) is formed as a H W_d + b H S_d.
+constexpr int kDownSlots = 3;
+
+__global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
+  constexpr int kSlot = 24576;  // H, W_d, S_d tiles; or the Gram block (16 KB) and the dZ slab
+  constexpr int PER = 6;        // 24 row groups per step over 4 waves
+  __shared__ __align__(1024) char ring[kDownSlots * kSlot];
+  const int nsp = a.nsplit + (a.l + kCorrPerSplit - 1) / kCorrPerSplit;
+  const RowTile rt = row_tile(blockIdx.x, a.B, (a.D / 64) * nsp);
+  if (!rt.valid) return;
+  const int dt = rt.tile % (a.D / 64), split = rt.tile / (a.D / 64), b = rt.b, d0 = dt * 64;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
+  const __attribute__((address_space(4))) float* cf =
+      (const __attribute__((address_space(4))) float*)(uintptr_t)(a.coef + (int64_t)b * kCoefStride);
+  const bool main_split = split < a.nsplit;
+  const float ca = cf[0], cb = cf[1];
+  const bool with_s = cb != 0.f;
+  // main split: F steps [s0, s1); correction split: layers [s0, s1)
+  int s0, s1;
+  if (main_split) {
+    const int nF = a.F / 64;
+    s0 = nF * split / a.nsplit;
+    s1 = nF * (split + 1) / a.nsplit;
+  } else {
+    s0 = (split - a.nsplit) * kCorrPerSplit;
+    s1 = min(a.l, s0 + kCorrPerSplit);
+  }
+  const int nst = s1 - s0;
+  const bf16* h = static_cast<const bf16*>(a.h_all) + ((int64_t)a.l * a.B + b) * 64 * a.F;
+  const int64_t mat = (int64_t)a.F * a.D;
+  const bf16* wd = static_cast<const bf16*>(a.wd) + b * mat + d0;
+  const bf16* sd = static_cast<const bf16*>(a.sd) + b * mat + d0;
+  const bf16* dsrc = static_cast<const bf16*>(a.dz_all) + (int64_t)b * 64 * a.D + d0;
+  const int64_t lstride = (int64_t)a.B * 64 * a.D;
+  const float* hh = a.hh + (int64_t)b * 64 * a.LL;  // layer j's block at + 64 j
+  int voff[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int g = w + 4 * i;  // main: 0..7 H rows, 8..15 W_d rows, 16..23 S_d rows;
+                              // correction: 0..15 Gram rows (4 each), 16..23 dZ rows
+    voff[i] = main_split ? (g < 8 ? row_src_off(g & 7, lane, a.F) : slab_src_off(g & 7, lane, a.D))
+                         : (g < 16 ? gram_src_off(g, lane, a.LL) : slab_src_off(g & 7, lane, a.D));
+  }
+  const uint32_t ring0 = lds_addr(ring);
+  auto issue = [&](int t) {
+    const uint32_t slot = ring0 + (uint32_t)((t % kDownSlots) * kSlot);
+    if (main_split) {
+      const int f0 = (s0 + t) * 64;
+      const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(h + f0, (uint32_t)(64 * a.F * 2));
+      const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wd + (int64_t)f0 * a.D, (uint32_t)(64 * a.D * 2));
+      // without S the S loads have no range: they move no data and keep the per-step count
+      const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(sd + (int64_t)f0 * a.D, with_s ? (uint32_t)(64 * a.D * 2) : 0u);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int g = w + 4 * i;
+        buffer_load_lds_raw(g < 8 ? rh : (g < 16 ? rw : rs), lds_ptr(slot + (uint32_t)(g * 1024)), 16, voff[i], 0,
+                            0, 0);
+      }
+    } else {
+      const int j = s0 + t;
+      const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(hh + 64 * j, (uint32_t)(64 * a.LL * 4));
+      const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(dsrc + j * lstride, (uint32_t)(64 * a.D * 2));
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int g = w + 4 * i;
+        buffer_load_lds_raw(g < 16 ? rg : rz, lds_ptr(slot + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
+      }
+    }
+  };
+  for (int t = 0; t < min(nst, kDownSlots - 1); ++t) issue(t);
+  uint32_t th[4], tg[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) th[k] = row_frag_addr(ring0, wr, lane, k);
+  const int ia = wr + (lane & 31), ha = lane >> 5;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) tg[q] = ring0 + (uint32_t)(ia * 256 + (((2 * q + 2 * ha - (q & 1)) ^ (ia & 15)) * 16));
+  const uint32_t tw = slab_tr_addr(ring0 + 8192u, wc, lane), ts = slab_tr_addr(ring0 + 16384u, wc, lane);
+  const uint32_t tz = slab_tr_addr(ring0 + 16384u, wc, lane);
+  f32x16 accw, accs;
+  zero(accw);
+  zero(accs);
+  for (int t = 0; t < nst; ++t) {
+    wait_steps<PER, kDownSlots - 2>(min(nst - 1, t + kDownSlots - 2) - t);
+    __builtin_amdgcn_s_barrier();  // every wave's loads of this step landed; the last step's slot is free
+    if (t + kDownSlots - 1 < nst) issue(t + kDownSlots - 1);
+    const uint32_t so = (uint32_t)((t % kDownSlots) * kSlot);
+    if (main_split) {
+      bf16x8 fh[4], fw[4], fs[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) fh[k] = lds_read_bf16x8<0>(th[k] + so);
+      slab_frags(tw + so, fw);
+      slab_frags(ts + so, fs);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(fh[0]), "+v"(fh[1]), "+v"(fh[2]), "+v"(fh[3]), "+v"(fw[0]), "+v"(fw[1]), "+v"(fw[2]),
+                     "+v"(fw[3]), "+v"(fs[0]), "+v"(fs[1]), "+v"(fs[2]), "+v"(fs[3]));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        accw = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[k], fw[k], accw, 0, 0, 0);
+        if (with_s) accs = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[k], fs[k], accs, 0, 0, 0);
+      }
+    } else {
+      bf16x8 fz[4];
+      slab_frags(tz + so, fz);
+      f32x4 kv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) kv[q] = lds_read_b128(tg[q] + so);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(fz[0]), "+v"(fz[1]), "+v"(fz[2]), "+v"(fz[3]), "+v"(kv[0]), "+v"(kv[1]), "+v"(kv[2]),
+                     "+v"(kv[3]), "+v"(kv[4]), "+v"(kv[5]), "+v"(kv[6]), "+v"(kv[7]));
+      const float gj = cf[kGam + s0 + t];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        bf16x8 fa;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          fa[e] = static_cast<bf16>(gj * kv[2 * k][e]);
+          fa[4 + e] = static_cast<bf16>(gj * kv[2 * k + 1][e]);
+        }
+        accw = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fz[k], accw, 0, 0, 0);
+      }
+    }
+  }
+  float* zp = a.zp + (((int64_t)split * a.B + b) * 64) * a.D + d0;
+  const int col = wc + acc_col();
+  const float wa = main_split ? ca : 1.f, sb = main_split ? cb : 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zp[(int64_t)(wr + acc_row(i)) * a.D + col] = wa * accw[i] + sb * accs[i];
+}
 // ---------------------------------------------------------------------------
 // 5. dH = dZ_l (a W_down,s + b S_down,s)^T + sum_j gam_j (dZ_l dZ_j^T) H_j per F tile;
 //    dU, dG; this tile's share of <K K^T, dU dU^T + dG dG^T>.
@@ -1781,7 +1915,9 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     da.coef = cl; da.h_all = h_all; da.wd = wd_src; da.sd = sd_src; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
     const int ncorr = (l + kCorrPerSplit - 1) / kCorrPerSplit;
     const dim3 down_grid(row_tile_blocks(B, (D / 64) * (c.nsplit + ncorr)));
-    if (bf16_src)
+    if (sizeof(T) == 2 && bf16_src)
+      hipLaunchKernelGGL(k_chain_down_lds, down_grid, blk, 0, st, da);
+    else if (bf16_src)
       hipLaunchKernelGGL((k_chain_down<T, bf16>), down_grid, blk, 0, st, da);
     else
       hipLaunchKernelGGL((k_chain_down<T, float>), down_grid, blk, 0, st, da);
