@@ -12,7 +12,7 @@ Per chunk the prefill runs every layer's attention, projections and readout, the
 chain (``uttt_chunk_chain``) that applies the chunk's 12 chained fast-weight updates.
 
 Also reported:
-* ``roofline``: the chain's state write (``k_chain_apply`` after the last layer's small
+* ``roofline``: the chain's state write (``k_chain_apply_lds`` after the last layer's small
   recurrence step; the largest single kernel of the prefill), timed live with HIP events
   between the chain's stream-ordered stages at the
   config-2 chunk shape (8 rows, 12 layers, C 64, D 768, F 2048), against 48 D F bytes per
@@ -494,7 +494,7 @@ def main() -> int:
         apply_ms = stage_ms[-1]
         a_gbs = state_bytes / (apply_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(a_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": round(a_gbs / PEAK_HBM_GBS, 4), "kernel": "k_chain_apply",
+                    "frac": round(a_gbs / PEAK_HBM_GBS, 4), "kernel": "k_chain_apply_lds",
                     "traffic": measured_traffic("k_chain_apply"),
                     "per_launch": {"algorithmic_bytes": state_bytes, "avg_ms": round(apply_ms, 4),
                                    "unit_bytes": "48 D F per row per chunk (W and S read and written once)",
