@@ -553,7 +553,6 @@ __device__ void advance_coef(const CoefArgs& a, int b, float* out, float* red, b
     const int64_t off = (int64_t)(idx >> 6) * a.LL + (idx & 63);
     n2 += hh[off] * zz[off];
   }
-  n2 = block_sum(n2, red);
   const int t = threadIdx.x;
   const T* al = layer_row<T>(a.acts.alpha, a.l, b, a.acts.ea_rs);
   float mt = 0.f, at = 0.f;
@@ -562,10 +561,11 @@ __device__ void advance_coef(const CoefArgs& a, int b, float* out, float* red, b
     at = to_f32(al[(int64_t)t * a.acts.ea_ts]);
   }
   const float lt = t < 64 ? a.loss[b * 64 + t] : 0.f;
-  const float asum = block_sum(at * mt, red);
-  const float msum = block_sum(mt, red);
-  const float any = block_sum(mt != 0.f ? 1.f : 0.f, red);
-  const float lsum = block_sum(lt, red);
+  __shared__ float red5[20];
+  float sums[5] = {n2, at * mt, mt, mt != 0.f ? 1.f : 0.f, lt};
+  block_sums<5>(sums, red5);
+  n2 = sums[0];
+  const float asum = sums[1], msum = sums[2], any = sums[3], lsum = sums[4];
   if (threadIdx.x == 0) {
     const float denom = a.mask != nullptr ? fmaxf(msum, 1.f) : (float)a.C;
     const float row_mean = lsum / fmaxf(a.mask != nullptr ? msum : (float)a.C, 1.f);

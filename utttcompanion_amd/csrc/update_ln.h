@@ -95,16 +95,18 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
       se += e[i] * e[i];
     }
   }
-  const float token_loss = 0.5f * block_sum(se, red) * inv_scale;
+  // the loss and the mask's token count in one reduction
+  __shared__ float red2[8];
+  const float* mr = a.mask != nullptr ? a.mask + (int64_t)b * a.mask_rs : nullptr;
+  float sums[2] = {se, (mr != nullptr && threadIdx.x < a.C) ? mr[threadIdx.x] : 0.f};
+  block_sums<2>(sums, red2);
+  const float token_loss = 0.5f * sums[0] * inv_scale;
 
   const float eta_t = to_f32(static_cast<const T*>(a.eta)[(int64_t)b * a.eta_rs + t]);
   float weight, m_t = 1.f;
-  if (a.mask != nullptr) {
-    const float* mr = a.mask + (int64_t)b * a.mask_rs;
+  if (mr != nullptr) {
     m_t = mr[t];
-    float cnt = threadIdx.x < a.C ? mr[threadIdx.x] : 0.f;
-    cnt = fmaxf(block_sum(cnt, red), 1.0f);
-    weight = (eta_t * m_t) / cnt;
+    weight = (eta_t * m_t) / fmaxf(sums[1], 1.0f);
   } else {
     weight = eta_t * (1.0f / (float)a.C);
   }
@@ -120,8 +122,9 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
       s4 += e[i] * z[i];
     }
   }
-  const float m1 = block_sum(s3, red) * inv_d;
-  const float m2 = block_sum(s4, red) * inv_d;
+  float moments[2] = {s3, s4};
+  block_sums<2>(moments, red2);
+  const float m1 = moments[0] * inv_d, m2 = moments[1] * inv_d;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int d = threadIdx.x + i * kThreads;

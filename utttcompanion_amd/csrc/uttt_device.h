@@ -457,6 +457,22 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
   return scratch[0] + scratch[1] + scratch[2] + scratch[3];
 }
 
+// N block sums at once (one pair of barriers); each sum as block_sum would form it
+template <int N>
+__device__ __forceinline__ void block_sums(float (&v)[N], float* scratch /* 4 N floats */) {
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = wave_sum(v[k]);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) scratch[4 * k + w] = v[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = scratch[4 * k] + scratch[4 * k + 1] + scratch[4 * k + 2] + scratch[4 * k + 3];
+}
+
 __device__ __forceinline__ float block_max(float v, float* scratch) {
   v = wave_max(v);
   const int w = threadIdx.x >> 6;
