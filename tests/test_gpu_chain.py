@@ -244,3 +244,34 @@ def test_chain_with_shared_products_equals_plain_chain():
     for a, b_ in zip(cps_a, cps_b):
         assert torch.equal(a, b_)
     assert torch.equal(surprise_a, surprise_b)
+
+
+BF16_TAIL_CASES = [
+    dict(L=5, b=3, c=40, d=192, f=320, mask=True, copies=True),   # tail chunk, masked rows, bf16 copies
+    dict(L=3, b=2, c=17, d=128, f=192, mask=False, copies=True),  # short chunk
+    dict(L=4, b=9, c=64, d=64, f=128, mask=True, copies=False),   # more rows than XCDs, fp32 masters
+]
+
+
+@pytest.mark.parametrize("case", BF16_TAIL_CASES)
+def test_chain_bf16_tail_chunks_within_tolerance(case):
+    """bf16 chains over partial chunks (rows past C are zero in every operand) and masked rows,
+    against the fp32 oracle's sequential steps."""
+    print(f"bf16 tail case {case}", flush=True)
+    layers, w, s, ln_w, ln_b = make_layers(case["L"], case["b"], case["c"], case["d"], case["f"], seed=61 + case["c"],
+                                           w_scale=0.03)
+    mask = None
+    if case["mask"]:
+        mask = torch.ones(case["b"], case["c"])
+        mask[0, case["c"] // 2:] = 0
+        mask[case["b"] - 1] = 0  # a row with no valid token keeps W and S through every layer
+    ref, ref_s = oracle_chain(layers, w, s, ln_w, ln_b, mask, 0.9, 1.0, True)
+    got, got_s, _, _ = run_chain(layers, w, s, ln_w, ln_b, mask, 0.9, 1.0, True, torch.bfloat16,
+                                 copies=case["copies"])
+    for name, a, e in zip(NAMES, got, ref):
+        err = (a.cpu() - e).abs().max().item()
+        assert err <= 2e-2, f"{name}: max abs err {err:.3e}"
+    assert (got_s.cpu() - ref_s).abs().max().item() <= 2e-2 * max(1.0, ref_s.abs().max().item())
+    if case["mask"]:
+        for a, o in zip(got, w + s):
+            assert torch.equal(a[case["b"] - 1].cpu(), o[case["b"] - 1]), "a row without tokens changed"

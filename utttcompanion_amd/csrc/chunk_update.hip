@@ -20,6 +20,8 @@
 //   6. k_apply        recompute each gradient tile from the small activations and apply
 //                     clip / momentum / decay / inactive-row select to W and S in one pass
 // Steps 1, 2 and 4 alone are the frozen readout.
+#include <algorithm>
+
 #include "update_ln.h"
 #include "uttt_device.h"
 #include "uttt_host.h"
@@ -770,6 +772,138 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   if (want(4)) hipLaunchKernelGGL(k_apply<T>, dim3(3 * (D / 64) * (F / 64), B), blk, 0, st, ap);
 }
 
+// One token per row (decode), bf16 activations: a streaming GEMV.  One workgroup per (row, block
+// of gemv_fb(F) F columns): u and g over all of d (threads split d, partial sums meet in LDS), h
+// rounded to bf16 as the matrix path rounds it, then this block's Z partial over all of D from
+// the block's W_down rows; k_ln_readout sums the blocks.  Every weight row is read as 16-byte
+// (bf16) or 32-byte (fp32) pieces by consecutive threads; fp32 masters are rounded to the bf16
+// operands the matrix path uses, so both weight types give the same readout.
+__host__ __device__ inline int gemv_fb(int64_t F) { return F % 256 == 0 ? 256 : (F % 128 == 0 ? 128 : 64); }
+
+template <typename WT>
+__device__ __forceinline__ void load8(const WT* p, float (&w)[8]) {
+  if constexpr (sizeof(WT) == 2) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = to_f32(v[e]);
+  } else {
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(p), v1 = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w[e] = to_f32(from_f32<bf16>(v0[e]));
+      w[4 + e] = to_f32(from_f32<bf16>(v1[e]));
+    }
+  }
+}
+
+template <int FB, typename WT>
+__global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
+  constexpr int TF = FB / 8;         // threads across one weight row piece (8 columns each)
+  constexpr int DG = kThreads / TF;  // row groups of the u / g loop
+  __shared__ float xs[4096];         // the token's row (D <= 2048 checked by the caller)
+  __shared__ float red[2][DG][FB];
+  __shared__ float hs[FB];
+  const int fb = blockIdx.x, b = blockIdx.y, f0 = fb * FB;
+  const bf16* x = static_cast<const bf16*>(a.x[0]) + (int64_t)b * a.x_rs[0];
+  for (int d = threadIdx.x; d < a.D; d += kThreads) xs[d] = to_f32(x[d]);
+  __syncthreads();
+  const WT* gu = static_cast<const WT*>(a.wu[0]) + (int64_t)b * a.w_rs[0] + f0;
+  const WT* gg = static_cast<const WT*>(a.wg[0]) + (int64_t)b * a.w_rs[0] + f0;
+  const int col = (threadIdx.x % TF) * 8, grp = threadIdx.x / TF;
+  const int d_per = (a.D + DG - 1) / DG, d_begin = grp * d_per, d_end = min(a.D, d_begin + d_per);
+  float au[8], ag[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) au[e] = ag[e] = 0.f;
+  int d = d_begin;
+  for (; d + 4 <= d_end; d += 4) {  // four rows of both matrices in flight
+    float pu[4][8], pg[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      load8<WT>(gu + (int64_t)(d + r) * a.F + col, pu[r]);
+      load8<WT>(gg + (int64_t)(d + r) * a.F + col, pg[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float xv = xs[d + r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        au[e] += xv * pu[r][e];
+        ag[e] += xv * pg[r][e];
+      }
+    }
+  }
+  for (; d < d_end; ++d) {
+    float pu[8], pg[8];
+    load8<WT>(gu + (int64_t)d * a.F + col, pu);
+    load8<WT>(gg + (int64_t)d * a.F + col, pg);
+    const float xv = xs[d];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      au[e] += xv * pu[e];
+      ag[e] += xv * pg[e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    red[0][grp][col + e] = au[e];
+    red[1][grp][col + e] = ag[e];
+  }
+  __syncthreads();
+  if (threadIdx.x < FB) {
+    float u = 0.f, g = 0.f;
+#pragma unroll
+    for (int q = 0; q < DG; ++q) {
+      u += red[0][q][threadIdx.x];
+      g += red[1][q][threadIdx.x];
+    }
+    hs[threadIdx.x] = to_f32(from_f32<bf16>((g * sigmoidf_acc(g)) * u));
+  }
+  __syncthreads();
+  // Z partial of this block: thread (column group c, F part p) takes 8 columns of D and a share
+  // of the block's FB rows
+  const WT* gd = static_cast<const WT*>(a.wd[0]) + (int64_t)b * a.w_rs[0] + (int64_t)f0 * a.D;
+  const int ncol = a.D / 8, nparts = kThreads / ncol;
+  float* zp = a.zp + ((int64_t)fb * a.B + b) * a.tok_pad * a.D;
+  const int c = threadIdx.x % ncol, p = threadIdx.x / ncol;
+  float az[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) az[e] = 0.f;
+  if (p < nparts) {
+    const int f_per = FB / nparts + (FB % nparts != 0), fb0 = p * f_per, fb1 = min(FB, fb0 + f_per);
+    int f = fb0;
+    for (; f + 4 <= fb1; f += 4) {
+      float pw[4][8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) load8<WT>(gd + (int64_t)(f + r) * a.D + c * 8, pw[r]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float hv = hs[f + r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) az[e] += hv * pw[r][e];
+      }
+    }
+    for (; f < fb1; ++f) {
+      float pw[8];
+      load8<WT>(gd + (int64_t)f * a.D + c * 8, pw);
+      const float hv = hs[f];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) az[e] += hv * pw[e];
+    }
+  }
+  __syncthreads();  // red is free again: the parts' sums meet there
+  float* zred = &red[0][0][0];  // nparts x D floats (nparts * D <= 2048 <= 2 * DG * FB)
+  if (p < nparts) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) zred[p * a.D + c * 8 + e] = az[e];
+  }
+  __syncthreads();
+  for (int dd = threadIdx.x; dd < a.D; dd += kThreads) {
+    float v = 0.f;
+    for (int q = 0; q < nparts; ++q) v += zred[q * a.D + dd];
+    zp[dd] = v;
+  }
+}
+
 struct ReadoutLayout {
   size_t h, zp, total;
   int nsplit, ntb;
@@ -779,10 +913,12 @@ static ReadoutLayout readout_layout(int64_t B, int64_t T, int64_t D, int64_t F, 
   ReadoutLayout L;
   L.ntb = (int)((T + 63) / 64);
   L.nsplit = pick_nsplit((D / 64) * B * L.ntb, F / 64);
+  // one token: room for the GEMV's F-block partials too
+  const int64_t zsplits = T == 1 ? std::max<int64_t>(L.nsplit, F / gemv_fb(F)) : L.nsplit;
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t at = off; off += align_up(bytes); return at; };
   L.h = take(act_bytes(dtype) * B * L.ntb * 64 * F);
-  L.zp = take(sizeof(float) * L.nsplit * B * L.ntb * 64 * D);
+  L.zp = take(sizeof(float) * zsplits * B * L.ntb * 64 * D);
   L.total = off;
   return L;
 }
@@ -799,6 +935,23 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   f.zp = reinterpret_cast<float*>(ws + L.zp);
   f.kx = a.keys; f.kx_rs = a.keys_row_stride; f.ku = a.key_up_out; f.kg = a.key_gate_out;
   const dim3 blk(kThreads);
+  if constexpr (sizeof(T) == 2) {
+    if (a.tokens == 1 && a.keys == nullptr && D <= 2048 && D % 8 == 0) {  // decode: streaming GEMV
+      const int fbw = gemv_fb(F);
+      if (fbw == 256)
+        hipLaunchKernelGGL((k_readout_gemv<256, WT>), dim3(F / 256, B), blk, 0, st, f);
+      else if (fbw == 128)
+        hipLaunchKernelGGL((k_readout_gemv<128, WT>), dim3(F / 128, B), blk, 0, st, f);
+      else
+        hipLaunchKernelGGL((k_readout_gemv<64, WT>), dim3(F / 64, B), blk, 0, st, f);
+      LnOutArgs o{};
+      o.B = B; o.ntok = 1; o.D = D; o.nsplit = F / fbw; o.tok_pad = f.tok_pad; o.eps = a.eps;
+      o.zp = f.zp; o.x = a.x; o.x_rs = a.x_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
+      o.out = a.out; o.out_rs = a.out_row_stride;
+      launch_ln_readout<T>(dim3(1, B), st, o);
+      return;
+    }
+  }
   // bf16 weights: K tiles of 128 halve the staged steps of these latency-bound loops where the
   // shape allows.  The key block (when asked for) is one more z block: it runs beside the token
   // blocks of the same F tile and row, on the same XCD, so its weight tiles come from that L2.
