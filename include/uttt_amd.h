@@ -314,6 +314,29 @@ int uttt_fast_weight_drift(int64_t batch, int64_t d_model, int64_t d_ff,
                            const float* w0_up, const float* w0_gate, const float* w0_down,
                            float* out6, void* workspace, size_t workspace_bytes, uttt_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * 8. Skinny slow-weight product out = x W^T (+ residual) for a few rows, bf16 operands with
+ *    fp32 accumulation.  Replaces the F.linear calls of the batched decode step
+ *    (engine/inference.py:263-276: the packed q/k/v projection, the uTTT query projection),
+ *    the residual projections h + linear(x) (model/uttt_layer.py:1528-1555) and the LM head
+ *    when one token per request is stepped.  x (m, k), w (n, k) row-major, out (m, n);
+ *    residual (m, n) may be NULL or alias out.  m <= 64, n % 32 == 0, k % 64 == 0.
+ *    x_eps > 0 folds an input RMSNorm in (the block's attn_norm / uttt_norm, the final norm
+ *    before the LM head): each row of x is scaled by 1 / sqrt(mean(x^2) + x_eps) and w must
+ *    carry the norm weight multiplied into its columns.  x_eps = 0: plain product.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t m, n, k;
+  int32_t act_dtype; /* UTTT_DTYPE_BF16 */
+  float x_eps;
+  const void* x; int64_t x_row_stride;
+  const void* w; int64_t w_row_stride;
+  const void* residual; int64_t residual_row_stride;
+  void* out; int64_t out_row_stride;
+} uttt_skinny_linear_args;
+
+int uttt_skinny_linear(const uttt_skinny_linear_args* args, uttt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,7 +42,8 @@ def test_struct_layouts_match_the_c_header(tmp_path):
     structs = {"uttt_chunk_update_args": N.ChunkUpdateArgs, "uttt_readout_args": N.ReadoutArgs,
                "uttt_rope_append_args": N.RopeAppendArgs, "uttt_swa_prefill_args": N.SwaPrefillArgs,
                "uttt_swa_decode_args": N.SwaDecodeArgs, "uttt_elastic_pull_args": N.ElasticPullArgs,
-               "uttt_chunk_chain_args": N.ChunkChainArgs, "uttt_proj_epilogue_args": N.ProjEpilogueArgs}
+               "uttt_chunk_chain_args": N.ChunkChainArgs, "uttt_proj_epilogue_args": N.ProjEpilogueArgs,
+               "uttt_skinny_linear_args": N.SkinnyLinearArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -96,3 +97,13 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     d.head_dim = 96
     assert lib.uttt_swa_decode(C.byref(d), None) == 1
     assert b"head_dim" in lib.uttt_last_error()
+    s = N.SkinnyLinearArgs()
+    s.m, s.n, s.k, s.act_dtype = 65, 64, 64, N.DTYPE_BF16
+    assert lib.uttt_skinny_linear(C.byref(s), None) == 1
+    assert b"m must be in" in lib.uttt_last_error()
+    s.m, s.n = 8, 48
+    assert lib.uttt_skinny_linear(C.byref(s), None) == 1
+    assert b"multiple of 32" in lib.uttt_last_error()
+    s.n, s.act_dtype = 64, N.DTYPE_F32
+    assert lib.uttt_skinny_linear(C.byref(s), None) == 1
+    assert b"bf16" in lib.uttt_last_error()

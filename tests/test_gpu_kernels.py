@@ -402,3 +402,79 @@ def test_proj_epilogue_folded_norm(dtype):
     for name, a, e in zip(("q", "k", "v", "eta", "alpha"), got, ref):
         err = ((a.float().cpu() - e).abs() / e.abs().clamp_min(1e-6)).max().item()
         assert err <= tol, f"{name}: rel err {err:.3e}"
+
+
+# ---------------------------------------------------------------------------
+# skinny slow-weight products of the decode step (out = x W^T (+ residual), bf16 in / out,
+# fp32 accumulation): against the fp32 product of the same bf16 operands.  Bound: half a
+# bf16 unit of the result (2^-9 relative) doubled for the residual's own rounding, plus a
+# small absolute floor for results near zero.
+# ---------------------------------------------------------------------------
+SKINNY_CASES = [  # (m, n, k): decode q/k/v and LM head, two row blocks, a 4-step tail wave, k = F
+    (32, 2304, 768), (1, 32, 64), (40, 768, 768), (64, 32000, 768), (5, 96, 832), (8, 256, 2048)]
+
+
+def check_skinny(got, ref):
+    got, ref = got.double().cpu(), ref.double().cpu()
+    bound = 2.0 ** -8 * ref.abs() + 1e-4
+    bad = (got - ref).abs() > bound
+    assert not bad.any(), f"{int(bad.sum())} entries off, max err {(got - ref).abs().max().item():.3g}"
+
+
+@pytest.mark.parametrize("m,n,k", SKINNY_CASES)
+def test_skinny_linear_matches_fp32_product(m, n, k):
+    from utttcompanion_amd import kernels as K
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) / math.sqrt(k)).to(torch.bfloat16)
+    ref = x.float() @ w.float().t()
+    got = K.skinny_linear(x.to(DEV), w.to(DEV))
+    torch.cuda.synchronize()
+    check_skinny(got, ref)
+
+
+def test_skinny_linear_residual_in_place_and_strided_rows():
+    from utttcompanion_amd import kernels as K
+    g = torch.Generator().manual_seed(11)
+    m, n, k = 24, 768, 768
+    wide = torch.randn(m, 3 * k, generator=g).to(torch.bfloat16)  # x is a column slice of it
+    w = (torch.randn(n, k, generator=g) / math.sqrt(k)).to(torch.bfloat16)
+    h = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    ref = h.float() + wide[:, k:2 * k].float() @ w.float().t()
+    hd = h.to(DEV)
+    xd = wide.to(DEV)[:, k:2 * k]
+    assert xd.stride(0) == 3 * k
+    out = K.skinny_linear(xd, w.to(DEV), out=hd, residual=hd)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == hd.data_ptr()
+    check_skinny(hd, ref)
+    # a separate output leaves the residual untouched
+    h2 = h.to(DEV)
+    out2 = K.skinny_linear(xd, w.to(DEV), residual=h2)
+    torch.cuda.synchronize()
+    assert torch.equal(h2.cpu(), h)
+    assert torch.equal(out2.cpu(), hd.cpu())
+
+
+@pytest.mark.parametrize("m,n,k,with_residual", [(32, 1280, 768, False), (40, 768, 768, True), (3, 64, 2048, False)])
+def test_skinny_linear_folded_rms_norm(m, n, k, with_residual):
+    """x_eps > 0: rows of x RMS-normalised over k, the norm weight already in W's columns."""
+    from utttcompanion_amd import kernels as K
+    g = torch.Generator().manual_seed(m + 3 * n + k)
+    eps = 1e-5
+    x = (3.0 * torch.randn(m, k, generator=g)).to(torch.bfloat16)
+    gain = 1.0 + 0.1 * torch.randn(k, generator=g)
+    w = (torch.randn(n, k, generator=g) / math.sqrt(k))
+    wf = (w * gain[None, :]).to(torch.bfloat16)
+    xf = x.float()
+    ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)) @ wf.float().t()
+    h = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    if with_residual:
+        ref = ref + h.float()
+        hd = h.to(DEV)
+        K.skinny_linear(x.to(DEV), wf.to(DEV), out=hd, residual=hd, x_eps=eps)
+        got = hd
+    else:
+        got = K.skinny_linear(x.to(DEV), wf.to(DEV), x_eps=eps)
+    torch.cuda.synchronize()
+    check_skinny(got, ref)

@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 MAX_CHAIN = 64
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -73,6 +73,16 @@ class ProjEpilogueArgs(C.Structure):
         ("eta", _P), ("alpha", _P),
         ("x", _P), ("x_row_stride", _I64), ("x_eps", _F),
         ("eta_alpha_bias", _P),
+    ]
+
+
+class SkinnyLinearArgs(C.Structure):
+    _fields_ = [
+        ("m", _I64), ("n", _I64), ("k", _I64), ("act_dtype", _I32), ("x_eps", _F),
+        ("x", _P), ("x_row_stride", _I64),
+        ("w", _P), ("w_row_stride", _I64),
+        ("residual", _P), ("residual_row_stride", _I64),
+        ("out", _P), ("out_row_stride", _I64),
     ]
 
 
@@ -165,6 +175,7 @@ SIGNATURES = {
     "uttt_elastic_pull_workspace": (C.c_size_t, [_I64]),
     "uttt_elastic_pull": (C.c_int, [C.POINTER(ElasticPullArgs), _P, C.c_size_t, _P]),
     "uttt_fast_weight_drift": (C.c_int, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P]),
+    "uttt_skinny_linear": (C.c_int, [C.POINTER(SkinnyLinearArgs), _P]),
 }
 
 _lib = None

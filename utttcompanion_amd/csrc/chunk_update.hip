@@ -779,27 +779,34 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
 // (bf16) or 32-byte (fp32) pieces by consecutive threads; fp32 masters are rounded to the bf16
 // operands the matrix path uses, so both weight types give the same readout.
 __host__ __device__ inline int gemv_fb(int64_t F) { return F % 256 == 0 ? 256 : (F % 128 == 0 ? 128 : 64); }
+constexpr int kGemvRowsBf16 = 8;
 
-template <typename WT>
-__device__ __forceinline__ void load8(const WT* p, float (&w)[8]) {
-  if constexpr (sizeof(WT) == 2) {
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) w[e] = to_f32(v[e]);
-  } else {
-    const f32x4 v0 = *reinterpret_cast<const f32x4*>(p), v1 = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      w[e] = to_f32(from_f32<bf16>(v0[e]));
-      w[4 + e] = to_f32(from_f32<bf16>(v1[e]));
-    }
+// raw 8-column pieces of a weight row: bf16 kept packed until used (so that many rows fit in
+// flight), fp32 masters as two 16-byte halves
+template <typename WT> struct Piece8;
+template <> struct Piece8<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ float get(int e) const { return to_f32(v[e]); }
+};
+template <> struct Piece8<float> {
+  f32x4 lo, hi;
+  __device__ __forceinline__ void load(const float* p) {
+    lo = *reinterpret_cast<const f32x4*>(p);
+    hi = *reinterpret_cast<const f32x4*>(p + 4);
   }
-}
+  __device__ __forceinline__ float get(int e) const { return to_f32(from_f32<bf16>(e < 4 ? lo[e] : hi[e - 4])); }
+};
 
-template <int FB, typename WT>
+// rows of each matrix in flight per thread: 8 packed bf16 pieces, 4 fp32 pairs
+template <typename WT> constexpr int gemv_rows() { return sizeof(WT) == 2 ? kGemvRowsBf16 : 4; }
+
+template <int FB, typename WT, int CW>
 __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
   constexpr int TF = FB / 8;         // threads across one weight row piece (8 columns each)
   constexpr int DG = kThreads / TF;  // row groups of the u / g loop
+  constexpr int RB = gemv_rows<WT>();
+  constexpr int NP = CW / 8;         // 8-column pieces per thread in the W_down loop
   __shared__ float xs[4096];         // the token's row (D <= 2048 checked by the caller)
   __shared__ float red[2][DG][FB];
   __shared__ float hs[FB];
@@ -815,32 +822,33 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) au[e] = ag[e] = 0.f;
   int d = d_begin;
-  for (; d + 4 <= d_end; d += 4) {  // four rows of both matrices in flight
-    float pu[4][8], pg[4][8];
+  for (; d + RB <= d_end; d += RB) {  // RB rows of both matrices in flight
+    Piece8<WT> pu[RB], pg[RB];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      load8<WT>(gu + (int64_t)(d + r) * a.F + col, pu[r]);
-      load8<WT>(gg + (int64_t)(d + r) * a.F + col, pg[r]);
+    for (int r = 0; r < RB; ++r) {
+      pu[r].load(gu + (int64_t)(d + r) * a.F + col);
+      pg[r].load(gg + (int64_t)(d + r) * a.F + col);
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < RB; ++r) {
       const float xv = xs[d + r];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        au[e] += xv * pu[r][e];
-        ag[e] += xv * pg[r][e];
+        au[e] += xv * pu[r].get(e);
+        ag[e] += xv * pg[r].get(e);
       }
     }
   }
   for (; d < d_end; ++d) {
-    float pu[8], pg[8];
-    load8<WT>(gu + (int64_t)d * a.F + col, pu);
-    load8<WT>(gg + (int64_t)d * a.F + col, pg);
+    Piece8<WT> pu, pg;
+    pu.load(gu + (int64_t)d * a.F + col);
+    pg.load(gg + (int64_t)d * a.F + col);
     const float xv = xs[d];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      au[e] += xv * pu[e];
-      ag[e] += xv * pg[e];
+      au[e] += xv * pu.get(e);
+      ag[e] += xv * pg.get(e);
     }
   }
 #pragma unroll
@@ -859,42 +867,51 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
     hs[threadIdx.x] = to_f32(from_f32<bf16>((g * sigmoidf_acc(g)) * u));
   }
   __syncthreads();
-  // Z partial of this block: thread (column group c, F part p) takes 8 columns of D and a share
+  // Z partial of this block: thread (column group c, F part p) takes CW columns of D and a share
   // of the block's FB rows
   const WT* gd = static_cast<const WT*>(a.wd[0]) + (int64_t)b * a.w_rs[0] + (int64_t)f0 * a.D;
-  const int ncol = a.D / 8, nparts = kThreads / ncol;
+  const int ncol = a.D / CW, nparts = kThreads / ncol;
   float* zp = a.zp + ((int64_t)fb * a.B + b) * a.tok_pad * a.D;
   const int c = threadIdx.x % ncol, p = threadIdx.x / ncol;
-  float az[8];
+  constexpr int RD = RB / NP > 0 ? RB / NP : 1;  // W_down rows in flight (same loads in flight)
+  float az[CW];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) az[e] = 0.f;
+  for (int e = 0; e < CW; ++e) az[e] = 0.f;
   if (p < nparts) {
     const int f_per = FB / nparts + (FB % nparts != 0), fb0 = p * f_per, fb1 = min(FB, fb0 + f_per);
     int f = fb0;
-    for (; f + 4 <= fb1; f += 4) {
-      float pw[4][8];
+    for (; f + RD <= fb1; f += RD) {
+      Piece8<WT> pw[RD][NP];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) load8<WT>(gd + (int64_t)(f + r) * a.D + c * 8, pw[r]);
+      for (int r = 0; r < RD; ++r)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+        for (int q = 0; q < NP; ++q) pw[r][q].load(gd + (int64_t)(f + r) * a.D + c * CW + q * 8);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < RD; ++r) {
         const float hv = hs[f + r];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) az[e] += hv * pw[r][e];
+        for (int q = 0; q < NP; ++q)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) az[q * 8 + e] += hv * pw[r][q].get(e);
       }
     }
     for (; f < fb1; ++f) {
-      float pw[8];
-      load8<WT>(gd + (int64_t)f * a.D + c * 8, pw);
       const float hv = hs[f];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) az[e] += hv * pw[e];
+      for (int q = 0; q < NP; ++q) {
+        Piece8<WT> pw;
+        pw.load(gd + (int64_t)f * a.D + c * CW + q * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) az[q * 8 + e] += hv * pw.get(e);
+      }
     }
   }
   __syncthreads();  // red is free again: the parts' sums meet there
-  float* zred = &red[0][0][0];  // nparts x D floats (nparts * D <= 2048 <= 2 * DG * FB)
+  float* zred = &red[0][0][0];  // nparts x D floats (nparts * D <= 256 * CW <= 4096 <= 2 * DG * FB)
   if (p < nparts) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) zred[p * a.D + c * 8 + e] = az[e];
+    for (int e = 0; e < CW; ++e) zred[p * a.D + c * CW + e] = az[e];
   }
   __syncthreads();
   for (int dd = threadIdx.x; dd < a.D; dd += kThreads) {
@@ -923,6 +940,16 @@ static ReadoutLayout readout_layout(int64_t B, int64_t T, int64_t D, int64_t F, 
   return L;
 }
 
+template <typename WT, int CW>
+static void launch_gemv(int fbw, dim3 grid, hipStream_t st, const FwdArgs& f) {
+  if (fbw == 256)
+    hipLaunchKernelGGL((k_readout_gemv<256, WT, CW>), grid, dim3(kThreads), 0, st, f);
+  else if (fbw == 128)
+    hipLaunchKernelGGL((k_readout_gemv<128, WT, CW>), grid, dim3(kThreads), 0, st, f);
+  else
+    hipLaunchKernelGGL((k_readout_gemv<64, WT, CW>), grid, dim3(kThreads), 0, st, f);
+}
+
 template <typename T, typename WT>
 static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLayout& L, hipStream_t st) {
   const int B = (int)a.batch, D = (int)a.d_model, F = (int)a.d_ff;
@@ -938,12 +965,10 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   if constexpr (sizeof(T) == 2) {
     if (a.tokens == 1 && a.keys == nullptr && D <= 2048 && D % 8 == 0) {  // decode: streaming GEMV
       const int fbw = gemv_fb(F);
-      if (fbw == 256)
-        hipLaunchKernelGGL((k_readout_gemv<256, WT>), dim3(F / 256, B), blk, 0, st, f);
-      else if (fbw == 128)
-        hipLaunchKernelGGL((k_readout_gemv<128, WT>), dim3(F / 128, B), blk, 0, st, f);
+      if (D % 16 == 0)
+        launch_gemv<WT, 16>(fbw, dim3(F / fbw, B), st, f);
       else
-        hipLaunchKernelGGL((k_readout_gemv<64, WT>), dim3(F / 64, B), blk, 0, st, f);
+        launch_gemv<WT, 8>(fbw, dim3(F / fbw, B), st, f);
       LnOutArgs o{};
       o.B = B; o.ntok = 1; o.D = D; o.nsplit = F / fbw; o.tok_pad = f.tok_pad; o.eps = a.eps;
       o.zp = f.zp; o.x = a.x; o.x_rs = a.x_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;

@@ -72,6 +72,7 @@ class BatchedDecoder:
         self._ws_attn = torch.zeros(1, dtype=torch.uint8, device=dev)
         self._ws_read = torch.zeros(1, dtype=torch.uint8, device=dev)
         self._states = list(states)
+        self._folds = {}
 
     # ------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -98,14 +99,41 @@ class BatchedDecoder:
         return torch.cat(out_logits, dim=0)
 
     # ------------------------------------------------------------------ one step
+    def _folded(self, weight: Tensor, norm) -> Tensor:
+        """W diag(g) for an RMSNorm ``norm`` applied to W's input (formed in fp32, rounded
+        once), rebuilt when either changes."""
+        key = (weight.data_ptr(), weight._version, norm.weight.data_ptr(), norm.weight._version)
+        hit = self._folds.get(id(weight))
+        if hit is None or hit[0] != key:
+            fold = (weight.detach().float() * norm.weight.detach().float()[None, :]).to(weight.dtype).contiguous()
+            hit = (key, fold)
+            self._folds[id(weight)] = hit
+        return hit[1]
+
+    def _linear(self, x: Tensor, weight: Tensor, residual: Optional[Tensor] = None, norm=None) -> Tensor:
+        """norm(x) W^T (+ residual, updated in place): ``uttt_skinny_linear`` for bf16 steps of
+        at most 64 requests (the RMSNorm folded in), the norm and the library GEMM otherwise."""
+        skinny = (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and x.shape[0] <= 64
+                  and weight.shape[0] % 32 == 0 and x.shape[1] % 64 == 0 and x.stride(1) == 1
+                  and weight.is_contiguous() and (norm is None or (norm.eps or 0.0) > 0.0))
+        if skinny:
+            if norm is None:
+                return K.skinny_linear(x, weight, out=residual, residual=residual)
+            return K.skinny_linear(x, self._folded(weight, norm), out=residual, residual=residual,
+                                   x_eps=norm.eps)
+        if norm is not None:
+            x = norm(x)
+        if residual is not None:
+            return linear_residual(residual, x, weight)
+        return F.linear(x, weight)
+
     def _step_body(self) -> None:
         m = self.model
         n = self.n
         h = F.embedding(self.tokens, m.tok_embeddings.weight)  # (N, D)
         for li, block in enumerate(m.layers):
             attn = block.attn
-            x = block.attn_norm(h)
-            qkv = F.linear(x, attn.packed_qkv().to(x.dtype))  # (N, (H + 2 Hkv) hd)
+            qkv = self._linear(h, attn.packed_qkv().to(h.dtype), norm=block.attn_norm)  # (N, (H + 2 Hkv) hd)
             hq = self.heads * self.hd
             hk = self.hkv * self.hd
             q = qkv[:, :hq].view(n, self.heads, self.hd)
@@ -113,14 +141,13 @@ class BatchedDecoder:
             v = qkv[:, hq + hk:].view(n, self.hkv, self.hd)
             kr, vr = self.rings[li]
             att = K.swa_decode(q, k, v, kr, vr, self.positions, self.cos, self.sin, workspace=self._ws_attn)
-            h = linear_residual(h, att.reshape(n, -1), attn.wo.weight)
-            x2 = block.uttt_norm(h)
-            uq = F.rms_norm(F.linear(x2, block.uttt.w_q.weight), (x2.shape[-1],),
-                            block.uttt.q_norm.weight.to(x2.dtype), block.uttt.q_norm.eps)
+            h = self._linear(att.reshape(n, -1), attn.wo.weight, residual=h)
+            uq = F.rms_norm(self._linear(h, block.uttt.w_q.weight, norm=block.uttt_norm), (h.shape[-1],),
+                            block.uttt.q_norm.weight.to(h.dtype), block.uttt.q_norm.eps)
             r = K.swiglu_readout(uq.view(n, 1, -1), self.w_up, self.w_gate, self.w_down, self.ln_weight,
                                  self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read)
-            h = linear_residual(h, r.view(n, -1), block.uttt.w_o.weight)
-        logits = F.linear(m.norm(h), m.lm_head.weight)
+            h = self._linear(r.view(n, -1), block.uttt.w_o.weight, residual=h)
+        logits = self._linear(h, m.lm_head.weight, norm=m.norm)
         self.positions.add_(1)
         work = logits.float()
         work[:, PAD_ID] = float("-inf")

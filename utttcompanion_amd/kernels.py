@@ -526,6 +526,45 @@ def proj_epilogue(y: Tensor, dim: int, q_weight: Tensor, k_weight: Tensor, eps: 
             ea[0].view(*lead, 1), ea[1].view(*lead, 1))
 
 
+def skinny_linear(x: Tensor, weight: Tensor, out: Optional[Tensor] = None,
+                  residual: Optional[Tensor] = None, x_eps: float = 0.0) -> Tensor:
+    """out = x weight^T (+ residual) for at most 64 bf16 rows (``uttt_skinny_linear``): the
+    decode step's projections and LM head (reference engine/inference.py:263-276, the
+    ``h + linear(x)`` residuals of model/uttt_layer.py:1528-1555).  x (m, k) and weight (n, k)
+    with unit column stride; ``residual`` (m, n) may be ``out`` itself (an in-place update).
+    ``x_eps`` > 0 RMS-normalises x's rows first (pass the weight with the norm weight
+    multiplied into its columns)."""
+    if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError(f"x (m, k) and weight (n, k) must agree on k, got {tuple(x.shape)} and {tuple(weight.shape)}")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("skinny_linear takes bf16 x and weight")
+    dev = x.device
+    _require_device(dev, weight, out, residual)
+    _forward_only(x)
+    m, k = x.shape
+    n = weight.shape[0]
+    if x.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("x and weight need unit column stride")
+    if out is None:
+        out = torch.empty((m, n), dtype=x.dtype, device=dev)
+    for name, t in (("out", out), ("residual", residual)):
+        if t is not None and (t.shape != (m, n) or t.dtype != x.dtype or t.stride(1) != 1):
+            raise ValueError(f"{name} must be ({m}, {n}) bf16 with unit column stride")
+    a = N.SkinnyLinearArgs()
+    if not x_eps >= 0.0:
+        raise ValueError("x_eps must be >= 0")
+    a.m, a.n, a.k, a.act_dtype, a.x_eps = m, n, k, N.DTYPE_BF16, float(x_eps)
+    a.x, a.x_row_stride = _p(x), x.stride(0)
+    a.w, a.w_row_stride = _p(weight), weight.stride(0)
+    if residual is not None:
+        a.residual, a.residual_row_stride = _p(residual), residual.stride(0)
+    a.out, a.out_row_stride = _p(out), out.stride(0)
+    lib = N.load_library()
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_skinny_linear(C.byref(a), _stream(dev)), "uttt_skinny_linear")
+    return out
+
+
 def readout_workspace(x: Tensor, w_up: Tensor) -> Tensor:
     """A workspace for ``swiglu_readout`` of x (B, T, D) through weights shaped like ``w_up``,
     reusable by every later call with the same or smaller shapes."""
