@@ -210,6 +210,16 @@ typedef struct {
    * readout's reads of the same chunk-start weights). */
   const void* keys; int64_t keys_row_stride;
   void* key_up_out; void* key_gate_out;
+  /* Optional, one bf16 token per row (tokens == 1, no keys, d_model <= 2048):
+   * x_norm_weight (d_model, activation dtype) reads out RMSNorm(x) with that weight and eps
+   * x_norm_eps instead of x, rounded to the activation dtype as the separate norm rounds it (the
+   * residual term is the normalised row too): the decode step's q_norm before the readout
+   * (reference uTTTLayer's rms_norm of the query projection, model/uttt_layer.py:1528-1555).
+   * row_counters (batch uint32, zero before the first call; every call leaves them zero) lets the
+   * LayerNorm and residual run in each row's last weight block, so the call is one launch;
+   * calls that share counters must not overlap.  NULL: a second launch does the LayerNorm. */
+  const void* x_norm_weight; float x_norm_eps;
+  uint32_t* row_counters;
 } uttt_readout_args;
 
 size_t uttt_readout_workspace(int64_t batch, int64_t tokens, int64_t d_model, int64_t d_ff, int32_t act_dtype);
@@ -336,6 +346,25 @@ typedef struct {
 } uttt_skinny_linear_args;
 
 int uttt_skinny_linear(const uttt_skinny_linear_args* args, uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 9. Greedy next-token selection: per row, argmax of the logits with the excluded ids and the
+ *    ids >= active_limit set to -inf first (torch.argmax semantics: NaN is the largest value,
+ *    ties go to the lowest id).  Replaces the temperature-0 branch of
+ *    uTTTModel.sample_next_token (model/uttt_model.py:1203-1221) as the decode step uses it.
+ *    active_limit < 0 or >= vocab: no limit.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t rows, vocab;
+  int32_t dtype;    /* UTTT_DTYPE_BF16 or UTTT_DTYPE_F32 logits */
+  int32_t n_banned; /* <= 8 */
+  int32_t banned[8];
+  int64_t active_limit;
+  const void* logits; int64_t row_stride;
+  int64_t* out;     /* (rows,) token ids */
+} uttt_greedy_args;
+
+int uttt_greedy_select(const uttt_greedy_args* args, uttt_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -206,6 +206,40 @@ def test_swiglu_readout_with_bf16_weight_copies():
     check_bf16_activation("readout", from_bf16, ref, ref16)
 
 
+@pytest.mark.parametrize("b,d,f", [(32, 768, 2048), (5, 512, 1024), (3, 1536, 640)])
+def test_decode_readout_with_query_norm_in_one_launch(b, d, f):
+    """One token per row: the readout of RMSNorm(y) (q_norm folded into the readout's x staging)
+    equals the readout of torch's normalised rows to the bf16 readout bound, and the one-launch
+    form (row counters: LayerNorm in each row's last weight block) equals the two-launch form
+    bit for bit on two calls in a row; the counters are zero again after each call."""
+    import torch.nn.functional as F
+    K = kernels()
+    g = torch.Generator().manual_seed(b + d + f)
+    eps = 1e-5
+    w = [(torch.randn(b, d, f, generator=g) * 0.03).bfloat16(), (torch.randn(b, d, f, generator=g) * 0.03).bfloat16(),
+         (torch.randn(b, f, d, generator=g) * 0.02).bfloat16()]
+    ln_w, ln_b = 1 + 0.1 * torch.randn(d, generator=g), 0.1 * torch.randn(d, generator=g)
+    qw = (1 + 0.1 * torch.randn(d, generator=g)).bfloat16()
+    dw = to_dev(*w, ln_w, ln_b, qw)
+    counters = torch.zeros(b, dtype=torch.int32, device=DEV)
+    for call in range(2):
+        y = (2.0 * torch.randn(b, 1, d, generator=g)).bfloat16()
+        yd = y.to(DEV)
+        with torch.no_grad():
+            two = K.swiglu_readout(yd, *dw[:5], eps=1e-5, x_norm=(dw[5], eps))
+            one = K.swiglu_readout(yd, *dw[:5], eps=1e-5, x_norm=(dw[5], eps), row_counters=counters)
+            plain = K.swiglu_readout(F.rms_norm(yd, (d,), dw[5], eps), *dw[:5], eps=1e-5)
+        torch.cuda.synchronize()
+        assert torch.equal(one, two), call
+        assert counters.abs().sum().item() == 0
+        yf = y.float()
+        xn = (yf * torch.rsqrt(yf.pow(2).mean(-1, keepdim=True) + eps) * qw.float()).bfloat16()
+        ref = om.swiglu_fast_forward(xn.float(), *(t_.float() for t_ in w), ln_w, ln_b, 1e-5)
+        ref16 = om.swiglu_fast_forward(xn, *w, ln_w, ln_b, 1e-5)
+        check_bf16_activation("fused readout", one, ref, ref16)
+        check_bf16_activation("plain readout", plain, ref, ref16)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_rope_append_is_bit_exact(dtype):
     K = kernels()
@@ -478,3 +512,32 @@ def test_skinny_linear_folded_rms_norm(m, n, k, with_residual):
         got = K.skinny_linear(x.to(DEV), wf.to(DEV), x_eps=eps)
     torch.cuda.synchronize()
     check_skinny(got, ref)
+
+
+@pytest.mark.parametrize("dtype,rows,vocab,limit", [(torch.bfloat16, 32, 32000, 30000), (torch.float32, 5, 1003, None),
+                                                   (torch.bfloat16, 3, 256, 200)])
+def test_greedy_select_matches_masked_argmax(dtype, rows, vocab, limit):
+    """Against the reference's own steps (float copy, -inf at the excluded ids and past the
+    active limit, torch.argmax), including ties, NaN and fully masked rows."""
+    K = kernels()
+    g = torch.Generator().manual_seed(rows + vocab)
+    x = torch.randn(rows, vocab, generator=g).to(dtype)
+    x[0, 1] = 1e4  # an excluded id holding the largest value
+    x[1 % rows, 7] = x[1 % rows, 9] = 50.0  # a tie: the lower id wins
+    if rows > 2:
+        x[2, 5] = float("nan")  # NaN counts as the largest value
+    if limit is not None and rows > 3:
+        x[3, limit + 1:] = 100.0  # past the active vocabulary
+    banned = (0, 1, 2)
+    ref = x.float().clone()
+    ref[:, list(banned)] = float("-inf")
+    if limit is not None:
+        ref[:, limit:] = float("-inf")
+    want = ref.argmax(dim=-1)
+    got = K.greedy_select(x.to(DEV), banned, limit)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want)
+    allmasked = torch.full((2, vocab), float("-inf")).to(dtype)
+    got2 = K.greedy_select(allmasked.to(DEV), banned, limit)
+    torch.cuda.synchronize()
+    assert got2.tolist() == [0, 0]

@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 MAX_CHAIN = 64
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -86,6 +86,15 @@ class SkinnyLinearArgs(C.Structure):
     ]
 
 
+class GreedyArgs(C.Structure):
+    _fields_ = [
+        ("rows", _I64), ("vocab", _I64), ("dtype", _I32), ("n_banned", _I32),
+        ("banned", _I32 * 8), ("active_limit", _I64),
+        ("logits", _P), ("row_stride", _I64),
+        ("out", _P),
+    ]
+
+
 class ReadoutArgs(C.Structure):
     _fields_ = [
         ("batch", _I64), ("tokens", _I64), ("d_model", _I64), ("d_ff", _I64),
@@ -96,6 +105,8 @@ class ReadoutArgs(C.Structure):
         ("out", _P), ("out_row_stride", _I64),
         ("keys", _P), ("keys_row_stride", _I64),
         ("key_up_out", _P), ("key_gate_out", _P),
+        ("x_norm_weight", _P), ("x_norm_eps", _F),
+        ("row_counters", _P),
     ]
 
 
@@ -176,6 +187,7 @@ SIGNATURES = {
     "uttt_elastic_pull": (C.c_int, [C.POINTER(ElasticPullArgs), _P, C.c_size_t, _P]),
     "uttt_fast_weight_drift": (C.c_int, [_I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, C.c_size_t, _P]),
     "uttt_skinny_linear": (C.c_int, [C.POINTER(SkinnyLinearArgs), _P]),
+    "uttt_greedy_select": (C.c_int, [C.POINTER(GreedyArgs), _P]),
 }
 
 _lib = None

@@ -50,6 +50,16 @@ struct FwdArgs {
   int64_t kx_rs;
   void* ku;
   void* kg;
+  // one token per row (the GEMV readout) only: optional RMSNorm of x, and the LN + residual
+  // in each row's last F block when row counters are given
+  const void* xn_w;
+  float xn_eps;
+  unsigned* counters;
+  float ln_eps;
+  const float* ln_w;
+  const float* ln_b;
+  void* out;
+  int64_t out_rs;
 };
 
 // ---------------------------------------------------------------------------
@@ -346,29 +356,49 @@ struct LnOutArgs {
   const float* ln_w;
   const float* ln_b;
   void* out; int64_t out_rs;
+  const void* xn_w;  // optional RMSNorm weight applied to x first (one token per row only)
+  float xn_eps;
 };
 
-// KPER values per thread (D <= KPER * 256); the splits' partial rows are loaded four at a time
-// with all their loads in flight before any is summed.
+// A token row of x into LDS as fp32.  With a norm weight the row becomes RMSNorm(x) with that
+// weight, rounded to T as a separate norm's output would be.  Each thread rewrites only the
+// entries it staged; the caller synchronises before other threads read them.
+template <typename T>
+__device__ __forceinline__ void stage_row(const T* x, int D, const T* nw, float neps, float* xs, float* red) {
+  float ss = 0.f;
+  for (int d = threadIdx.x; d < D; d += kThreads) {
+    const float v = to_f32(x[d]);
+    xs[d] = v;
+    ss += v * v;
+  }
+  if (nw != nullptr) {
+    const float rstd = rsqrtf(block_sum(ss, red) / (float)D + neps);
+    for (int d = threadIdx.x; d < D; d += kThreads) xs[d] = to_f32(from_f32<T>(xs[d] * rstd * to_f32(nw[d])));
+  }
+}
+
+// out = xres + LN(z) for one token row, z the sum of the row's nsplit partials (rows sp_stride
+// floats apart), xres the row's residual (fp32, LDS or global).  KPER values per thread
+// (D <= KPER * 256); the partial rows are loaded four at a time with all their loads in flight
+// before any is summed, and always summed in split order.
 template <typename T, int KPER>
-__global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
-  __shared__ float red[4];
-  const int t = blockIdx.x, b = blockIdx.y;
-  if (t >= a.ntok) return;
-  const float inv_d = 1.0f / (float)a.D;
+__device__ __forceinline__ void ln_readout_row(const float* z0, int64_t sp_stride, int nsplit, int D, float eps,
+                                               const float* ln_w, const float* ln_b, const float* xres, T* o,
+                                               float* red) {
+  const float inv_d = 1.0f / (float)D;
   float z[KPER];
 #pragma unroll
   for (int i = 0; i < KPER; ++i) z[i] = 0.f;
   constexpr int kGroup = 4;
-  for (int sp0 = 0; sp0 < a.nsplit; sp0 += kGroup) {
+  for (int sp0 = 0; sp0 < nsplit; sp0 += kGroup) {
     float v[kGroup][KPER];
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
-      const float* src = a.zp + (((int64_t)(sp0 + u) * a.B + b) * a.tok_pad + t) * a.D;
+      const float* src = z0 + (int64_t)(sp0 + u) * sp_stride;
 #pragma unroll
       for (int i = 0; i < KPER; ++i) {
         const int d = threadIdx.x + i * kThreads;
-        v[u][i] = sp0 + u < a.nsplit && d < a.D ? src[d] : 0.f;
+        v[u][i] = sp0 + u < nsplit && d < D ? src[d] : 0.f;
       }
     }
 #pragma unroll
@@ -384,23 +414,34 @@ __global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
 #pragma unroll
   for (int i = 0; i < KPER; ++i) {
     const int d = threadIdx.x + i * kThreads;
-    if (d < a.D) {
+    if (d < D) {
       const float c = z[i] - mean;
       s2 += c * c;
     }
   }
-  const float rstd = 1.0f / sqrtf(block_sum(s2, red) * inv_d + a.eps);
-  const T* xr = static_cast<const T*>(a.x) + (int64_t)b * a.x_rs + (int64_t)t * a.D;
-  T* o = static_cast<T*>(a.out) + (int64_t)b * a.out_rs + (int64_t)t * a.D;
+  const float rstd = 1.0f / sqrtf(block_sum(s2, red) * inv_d + eps);
 #pragma unroll
   for (int i = 0; i < KPER; ++i) {
     const int d = threadIdx.x + i * kThreads;
-    if (d < a.D) {
-      const float g = to_f32(from_f32<T>(a.ln_w[d]));
-      const float be = to_f32(from_f32<T>(a.ln_b[d]));
-      o[d] = from_f32<T>(to_f32(xr[d]) + ((z[i] - mean) * rstd * g + be));
+    if (d < D) {
+      const float g = to_f32(from_f32<T>(ln_w[d]));
+      const float be = to_f32(from_f32<T>(ln_b[d]));
+      o[d] = from_f32<T>(xres[d] + ((z[i] - mean) * rstd * g + be));
     }
   }
+}
+
+template <typename T, int KPER>
+__global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
+  __shared__ float red[4];
+  __shared__ float xs[KPER * kThreads];
+  const int t = blockIdx.x, b = blockIdx.y;
+  if (t >= a.ntok) return;
+  const T* xr = static_cast<const T*>(a.x) + (int64_t)b * a.x_rs + (int64_t)t * a.D;
+  stage_row<T>(xr, a.D, static_cast<const T*>(a.xn_w), a.xn_eps, xs, red);
+  T* o = static_cast<T*>(a.out) + (int64_t)b * a.out_rs + (int64_t)t * a.D;
+  ln_readout_row<T, KPER>(a.zp + ((int64_t)b * a.tok_pad + t) * a.D, (int64_t)a.B * a.tok_pad * a.D, a.nsplit, a.D,
+                          a.eps, a.ln_w, a.ln_b, xs, o, red);
 }
 
 template <typename T>
@@ -807,12 +848,14 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
   constexpr int DG = kThreads / TF;  // row groups of the u / g loop
   constexpr int RB = gemv_rows<WT>();
   constexpr int NP = CW / 8;         // 8-column pieces per thread in the W_down loop
-  __shared__ float xs[4096];         // the token's row (D <= 2048 checked by the caller)
+  __shared__ float xs[2048];         // the token's row (D <= 2048 checked by the caller)
   __shared__ float red[2][DG][FB];
   __shared__ float hs[FB];
+  __shared__ float sred[4];
+  __shared__ int last;
   const int fb = blockIdx.x, b = blockIdx.y, f0 = fb * FB;
   const bf16* x = static_cast<const bf16*>(a.x[0]) + (int64_t)b * a.x_rs[0];
-  for (int d = threadIdx.x; d < a.D; d += kThreads) xs[d] = to_f32(x[d]);
+  stage_row<bf16>(x, a.D, static_cast<const bf16*>(a.xn_w), a.xn_eps, xs, sred);
   __syncthreads();
   const WT* gu = static_cast<const WT*>(a.wu[0]) + (int64_t)b * a.w_rs[0] + f0;
   const WT* gg = static_cast<const WT*>(a.wg[0]) + (int64_t)b * a.w_rs[0] + f0;
@@ -919,6 +962,28 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
     for (int q = 0; q < nparts; ++q) v += zred[q * a.D + dd];
     zp[dd] = v;
   }
+  if (a.counters == nullptr) return;  // k_ln_readout follows
+  // The row's last block to finish sums the row's partials.  Every thread's partial stores
+  // have reached this CU's L2 before the barrier; one release (L2 write-back) then publishes
+  // them with the count, and only the last block acquires (L2 invalidate) before reading the
+  // other blocks' partials.  It returns the count to zero for the next call.
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(a.counters + b, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == gridDim.x - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  if (!last) return;
+  bf16* o = static_cast<bf16*>(a.out) + (int64_t)b * a.out_rs;
+  const float* z0 = a.zp + (int64_t)b * a.tok_pad * a.D;
+  const int64_t sp_stride = (int64_t)a.B * a.tok_pad * a.D;
+  if (a.D <= 4 * kThreads)
+    ln_readout_row<bf16, 4>(z0, sp_stride, gridDim.x, a.D, a.ln_eps, a.ln_w, a.ln_b, xs, o, sred);
+  else
+    ln_readout_row<bf16, 8>(z0, sp_stride, gridDim.x, a.D, a.ln_eps, a.ln_w, a.ln_b, xs, o, sred);
+  if (threadIdx.x == 0) __hip_atomic_store(a.counters + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct ReadoutLayout {
@@ -961,6 +1026,8 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   f.h[0] = ws + L.h;
   f.zp = reinterpret_cast<float*>(ws + L.zp);
   f.kx = a.keys; f.kx_rs = a.keys_row_stride; f.ku = a.key_up_out; f.kg = a.key_gate_out;
+  f.xn_w = a.x_norm_weight; f.xn_eps = a.x_norm_eps; f.counters = a.row_counters;
+  f.ln_eps = a.eps; f.ln_w = a.ln_weight; f.ln_b = a.ln_bias; f.out = a.out; f.out_rs = a.out_row_stride;
   const dim3 blk(kThreads);
   if constexpr (sizeof(T) == 2) {
     if (a.tokens == 1 && a.keys == nullptr && D <= 2048 && D % 8 == 0) {  // decode: streaming GEMV
@@ -969,10 +1036,12 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
         launch_gemv<WT, 16>(fbw, dim3(F / fbw, B), st, f);
       else
         launch_gemv<WT, 8>(fbw, dim3(F / fbw, B), st, f);
+      if (a.row_counters != nullptr) return;  // the LN ran in each row's last block
       LnOutArgs o{};
       o.B = B; o.ntok = 1; o.D = D; o.nsplit = F / fbw; o.tok_pad = f.tok_pad; o.eps = a.eps;
       o.zp = f.zp; o.x = a.x; o.x_rs = a.x_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
       o.out = a.out; o.out_rs = a.out_row_stride;
+      o.xn_w = a.x_norm_weight; o.xn_eps = a.x_norm_eps;
       launch_ln_readout<T>(dim3(1, B), st, o);
       return;
     }
@@ -1113,6 +1182,11 @@ extern "C" int uttt_swiglu_readout(const uttt_readout_args* a, void* workspace, 
     UTTT_REQUIRE(a->key_up_out != nullptr && a->key_gate_out != nullptr, "key product outputs must be non-NULL");
     UTTT_REQUIRE(aligned16(a->keys) && a->keys_row_stride % 8 == 0,
                  "keys must be 16-byte aligned with a row stride that is a multiple of 16 bytes");
+  }
+  if (a->x_norm_weight != nullptr || a->row_counters != nullptr) {
+    UTTT_REQUIRE(a->tokens == 1 && a->act_dtype == UTTT_DTYPE_BF16 && a->keys == nullptr && a->d_model <= 2048,
+                 "x_norm_weight and row_counters need one bf16 token per row, no keys and d_model <= 2048");
+    UTTT_REQUIRE(a->x_norm_weight == nullptr || a->x_norm_eps > 0.f, "x_norm_eps must be > 0");
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);

@@ -73,6 +73,10 @@ class BatchedDecoder:
         self._ws_read = torch.zeros(1, dtype=torch.uint8, device=dev)
         self._states = list(states)
         self._folds = {}
+        d_model = model.config.d_model
+        self._fused_readout = self.dtype == torch.bfloat16 and d_model <= 2048 and all(
+            (blk.uttt.q_norm.eps or 0.0) > 0.0 for blk in model.layers)
+        self._counters = torch.zeros(self.n, dtype=torch.int32, device=dev)  # left zero by every readout
 
     # ------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -142,21 +146,23 @@ class BatchedDecoder:
             kr, vr = self.rings[li]
             att = K.swa_decode(q, k, v, kr, vr, self.positions, self.cos, self.sin, workspace=self._ws_attn)
             h = self._linear(att.reshape(n, -1), attn.wo.weight, residual=h)
-            uq = F.rms_norm(self._linear(h, block.uttt.w_q.weight, norm=block.uttt_norm), (h.shape[-1],),
-                            block.uttt.q_norm.weight.to(h.dtype), block.uttt.q_norm.eps)
-            r = K.swiglu_readout(uq.view(n, 1, -1), self.w_up, self.w_gate, self.w_down, self.ln_weight,
-                                 self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read)
+            y = self._linear(h, block.uttt.w_q.weight, norm=block.uttt_norm)
+            qn = block.uttt.q_norm
+            if self._fused_readout:  # q_norm, readout, LayerNorm and residual in one launch
+                r = K.swiglu_readout(y.view(n, 1, -1), self.w_up, self.w_gate, self.w_down, self.ln_weight,
+                                     self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read,
+                                     x_norm=(qn.weight, qn.eps), row_counters=self._counters)
+            else:
+                uq = F.rms_norm(y, (h.shape[-1],), qn.weight.to(h.dtype), qn.eps)
+                r = K.swiglu_readout(uq.view(n, 1, -1), self.w_up, self.w_gate, self.w_down, self.ln_weight,
+                                     self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read)
             h = self._linear(r.view(n, -1), block.uttt.w_o.weight, residual=h)
         logits = self._linear(h, m.lm_head.weight, norm=m.norm)
         self.positions.add_(1)
-        work = logits.float()
-        work[:, PAD_ID] = float("-inf")
-        work[:, BOS_ID] = float("-inf")
-        work[:, UNK_ID] = float("-inf")
-        if m.active_vocab_limit < work.shape[-1]:
-            work[:, m.active_vocab_limit:] = float("-inf")
         self.logits = logits
-        self.next_tokens = work.argmax(dim=-1)
+        # temperature-0 selection: PAD / BOS / UNK and ids past the active vocabulary excluded
+        limit = m.active_vocab_limit if m.active_vocab_limit < logits.shape[-1] else None
+        self.next_tokens = K.greedy_select(logits, (PAD_ID, BOS_ID, UNK_ID), limit)
 
     def _warm_workspaces(self) -> None:
         lib_ws_attn = 1 << 20

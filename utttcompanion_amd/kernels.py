@@ -565,6 +565,36 @@ def skinny_linear(x: Tensor, weight: Tensor, out: Optional[Tensor] = None,
     return out
 
 
+def greedy_select(logits: Tensor, banned: Sequence[int] = (), active_limit: Optional[int] = None,
+                  out: Optional[Tensor] = None) -> Tensor:
+    """Greedy next tokens (rows,) int64 from logits (rows, vocab) bf16 / fp32
+    (``uttt_greedy_select``): argmax after setting the ``banned`` ids and the ids at or past
+    ``active_limit`` to -inf (the temperature-0 branch of reference sample_next_token,
+    model/uttt_model.py:1203-1221), one launch."""
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be (rows, vocab) with unit column stride")
+    if len(banned) > 8:
+        raise ValueError("at most 8 excluded ids")
+    dev = logits.device
+    _require_device(dev, out)
+    code = _act_code(logits.dtype)
+    rows, vocab = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=dev)
+    elif out.dtype != torch.int64 or out.numel() != rows or not out.is_contiguous():
+        raise ValueError(f"out must be {rows} contiguous int64 entries")
+    a = N.GreedyArgs()
+    a.rows, a.vocab, a.dtype, a.n_banned = rows, vocab, code, len(banned)
+    for i, t in enumerate(banned):
+        a.banned[i] = int(t)
+    a.active_limit = -1 if active_limit is None else int(active_limit)
+    a.logits, a.row_stride, a.out = _p(logits), logits.stride(0), _p(out)
+    lib = N.load_library()
+    with torch.cuda.device(dev):
+        N.check(lib.uttt_greedy_select(C.byref(a), _stream(dev)), "uttt_greedy_select")
+    return out
+
+
 def readout_workspace(x: Tensor, w_up: Tensor) -> Tensor:
     """A workspace for ``swiglu_readout`` of x (B, T, D) through weights shaped like ``w_up``,
     reusable by every later call with the same or smaller shapes."""
@@ -576,7 +606,9 @@ def readout_workspace(x: Tensor, w_up: Tensor) -> Tensor:
 def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_weight: Tensor,
                    ln_bias: Tensor, eps: float = 1e-5, out: Optional[Tensor] = None,
                    workspace: Optional[Tensor] = None, keys: Optional[Tensor] = None,
-                   key_outputs: Optional[Tuple[Tensor, Tensor]] = None) -> Tensor:
+                   key_outputs: Optional[Tuple[Tensor, Tensor]] = None,
+                   x_norm: Optional[Tuple[Tensor, float]] = None,
+                   row_counters: Optional[Tensor] = None) -> Tensor:
     """f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down) with per-row (or shared) W.
 
     W is read as fp32 masters, or -- when x and all three weights are bf16 -- as bf16 read
@@ -584,7 +616,12 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
     copy yields the same operands at half the bytes).  With ``keys`` (B, T <= 64, D) bf16 the
     same weight reads also give keys W_up and keys W_gate, written to ``key_outputs``
     ((B, 64, d_ff) each, rows past T zero): the layer chain's products with the chunk-start
-    copies (``ChunkChainRun.w_product_outputs``)."""
+    copies (``ChunkChainRun.w_product_outputs``).
+
+    One bf16 token per row only: ``x_norm`` = (weight, eps) reads out RMSNorm(x) with that
+    weight instead of x (the decode step's q_norm), and ``row_counters`` (B,) int32, zero before
+    the first call and left zero by every call, makes the readout a single launch (the
+    LayerNorm runs in each row's last weight block); calls sharing counters must not overlap."""
     if x.dim() != 3:
         raise ValueError(f"x must be (B, T, D), got {tuple(x.shape)}")
     bsz, tokens, dim = x.shape
@@ -633,9 +670,22 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
             raise ValueError(f"key_outputs must be two contiguous ({bsz}, 64, {ff}) {x.dtype} tensors")
         a.keys, a.keys_row_stride = _p(keys), keys.stride(0)
         a.key_up_out, a.key_gate_out = _p(key_outputs[0]), _p(key_outputs[1])
+    keep = None
+    if x_norm is not None:
+        keep = x_norm[0].detach().to(x.dtype).contiguous()
+        if keep.shape != (dim,):
+            raise ValueError(f"the x norm weight must be ({dim},)")
+        _require_device(dev, keep)
+        a.x_norm_weight, a.x_norm_eps = _p(keep), float(x_norm[1])
+    if row_counters is not None:
+        if row_counters.dtype != torch.int32 or row_counters.numel() < bsz or not row_counters.is_contiguous():
+            raise ValueError(f"row_counters must be a contiguous int32 tensor of >= {bsz} entries")
+        _require_device(dev, row_counters)
+        a.row_counters = _p(row_counters)
     with torch.cuda.device(dev):
         N.check(lib.uttt_swiglu_readout(C.byref(a), _p(workspace), workspace.numel(), _stream(dev)),
                 "uttt_swiglu_readout")
+    del keep
     return out
 
 
