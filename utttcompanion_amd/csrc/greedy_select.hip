@@ -16,7 +16,9 @@ namespace {
 
 struct SelectArgs {
   int vocab, limit;
-  int banned[8];
+  uint64_t low;  // excluded ids below 64, as a bit mask
+  int n_high;    // excluded ids of 64 and above
+  int high[8];
   const void* logits;
   int64_t rs;
   int64_t* out;
@@ -46,9 +48,10 @@ constexpr int kSelThreads = 1024;
 constexpr int kSelUnroll = 4;  // loads in flight per thread
 
 __device__ __forceinline__ bool excluded(const SelectArgs& a, int i) {
-  bool m = i >= a.limit;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) m |= i == a.banned[k];  // unused slots hold -1
+  if (i >= a.limit) return true;
+  if (i < 64) return (a.low >> i) & 1;
+  bool m = false;
+  for (int k = 0; k < a.n_high; ++k) m |= i == a.high[k];
   return m;
 }
 
@@ -118,7 +121,12 @@ extern "C" int uttt_greedy_select(const uttt_greedy_args* a, uttt_stream_t strea
   UTTT_REQUIRE(a->row_stride >= a->vocab, "the row stride must cover vocab");
   SelectArgs s{};
   s.vocab = (int)a->vocab;
-  for (int k = 0; k < 8; ++k) s.banned[k] = k < a->n_banned ? a->banned[k] : -1;
+  for (int k = 0; k < a->n_banned; ++k) {
+    if (a->banned[k] < 64)
+      s.low |= uint64_t(1) << a->banned[k];
+    else
+      s.high[s.n_high++] = a->banned[k];
+  }
   s.limit = (int)std::min<int64_t>(a->active_limit < 0 ? a->vocab : a->active_limit, a->vocab);
   s.logits = a->logits;
   s.rs = a->row_stride;
