@@ -21,8 +21,12 @@ namespace uttt {
 namespace {
 
 constexpr int kSkWaves = 4;
-constexpr int kSkRound = 3;  // k steps per load round of a wave (K = 768 is one round)
 constexpr int kSkStepBytes = 8192;  // 32 x rows + 32 W rows of 64 k
+// k steps per load round of a wave: three (K = 768 in one round) where the grid is small and
+// each workgroup's latency is the time; one for wide products (the LM head), so that five
+// workgroups fit in a CU's LDS and the grid runs in about one round
+constexpr int kSkRoundNarrow = 3, kSkRoundWide = 1;
+constexpr int kSkWideBlocks = 512;  // column blocks from which a product counts as wide
 
 struct SkArgs {
   int m, n, k;
@@ -37,8 +41,9 @@ struct SkArgs {
   int64_t os;
 };
 
+template <int kSkRound>
 __global__ void __launch_bounds__(kSkWaves * 64) k_skinny_linear(const SkArgs a) {
-  __shared__ __align__(1024) char lds[kSkWaves * kSkRound * kSkStepBytes];
+  __shared__ __align__(1024) char lds[kSkWaves * kSkRound * kSkStepBytes];  // >= the 12.5 KB of partial sums
   const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -177,7 +182,11 @@ extern "C" int uttt_skinny_linear(const uttt_skinny_linear_args* a, uttt_stream_
   s.rs = a->residual_row_stride;
   s.out = static_cast<bf16*>(a->out);
   s.os = a->out_row_stride;
-  hipLaunchKernelGGL(k_skinny_linear, dim3((unsigned)(a->n / 32), (unsigned)((a->m + 31) / 32)), dim3(kSkWaves * 64),
-                     0, static_cast<hipStream_t>(stream), s);
+  const dim3 grid((unsigned)(a->n / 32), (unsigned)((a->m + 31) / 32));
+  if (a->n / 32 >= kSkWideBlocks)
+    hipLaunchKernelGGL(k_skinny_linear<kSkRoundWide>, grid, dim3(kSkWaves * 64), 0, static_cast<hipStream_t>(stream), s);
+  else
+    hipLaunchKernelGGL(k_skinny_linear<kSkRoundNarrow>, grid, dim3(kSkWaves * 64), 0, static_cast<hipStream_t>(stream),
+                       s);
   return launch_status("uttt_skinny_linear");
 }
