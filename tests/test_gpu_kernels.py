@@ -387,6 +387,46 @@ def test_swa_decode_ring_matches_full_prefix(dtype, hd):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("win,hkv", [(512, 4), (300, 4), (512, 3)])
+def test_swa_decode_wide_windows_bf16(win, hkv):
+    """bf16 head_dim 64 at the decode shapes: windows up to 512 with at most 4 query heads per kv
+    head run as one workgroup per (request, kv head); 5 query heads per kv head take the split
+    form.  Positions before, at and well past the first wrap; one step each."""
+    K = kernels()
+    hd = 64
+    h = 12 if hkv != 3 else 15
+    pos = [0, 37, win - 1, win, 3 * win + 5]
+    n = len(pos)
+    g = torch.Generator().manual_seed(win + hkv)
+    total = max(pos) + 1
+    qs = torch.randn(n, total, h, hd, generator=g).bfloat16()
+    ks = torch.randn(n, total, hkv, hd, generator=g).bfloat16()
+    vs = torch.randn(n, total, hkv, hd, generator=g).bfloat16()
+    cos, sin = om.rope_tables(hd, total)
+    rq = om.apply_rope(qs.transpose(1, 2), cos, sin)
+    rk = om.apply_rope(ks.transpose(1, 2), cos, sin)
+    rv = vs.transpose(1, 2)
+    k_ring = torch.randn(n, hkv, win, hd, generator=g).bfloat16()  # stale slots must not be read
+    v_ring = torch.randn(n, hkv, win, hd, generator=g).bfloat16()
+    for r, p in enumerate(pos):
+        for j in range(max(0, p - win + 1), p):
+            k_ring[r, :, j % win] = rk[r, :, j]
+            v_ring[r, :, j % win] = rv[r, :, j]
+    q = torch.stack([qs[r, p] for r, p in enumerate(pos)])
+    kn = torch.stack([ks[r, p] for r, p in enumerate(pos)])
+    vn = torch.stack([vs[r, p] for r, p in enumerate(pos)])
+    dk, dv = to_dev(k_ring, v_ring)
+    with torch.no_grad():
+        got = K.swa_decode(*to_dev(q, kn, vn), dk, dv, torch.tensor(pos, dtype=torch.int64, device=DEV),
+                           *to_dev(cos, sin))
+    torch.cuda.synchronize()
+    for r, p in enumerate(pos):
+        want = om.sliding_window_attention(rq[r:r + 1, :, p:p + 1].float(), rk[r:r + 1, :, :p + 1].float(),
+                                           rv[r:r + 1, :, :p + 1].float(), win, p)[0, :, 0]
+        assert max_abs(got[r].float().cpu(), want) <= BF16_ABS, f"request {r} at {p}"
+        assert torch.equal(dk[r, :, p % win].cpu(), rk[r, :, p]), "the new key goes to slot pos mod window"
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_proj_epilogue_matches_oracle(dtype):
     """q/k/v RMSNorm and eta/alpha sigmoid of the packed projection (reference

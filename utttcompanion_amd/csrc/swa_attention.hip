@@ -417,30 +417,42 @@ __device__ __forceinline__ void unpack8(float (&dst)[8], const uint4* v) {
   }
 }
 
-// grid (n_req, n_kv_heads, splits of kDecodeKeys slots)
-template <typename T, int HD>
-__global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_decode_args a, float* part) {
+// grid (n_req, n_kv_heads, splits of KEYS slots), NT threads.  Split form (the default: NT 256,
+// KEYS kDecodeKeys, REP kMaxRep): softmax partials per split for k_swa_decode_combine.  WHOLE:
+// one workgroup covers the whole window (one split) and writes the normalised output itself,
+// so a step is one launch (bf16, window <= KEYS, at most REP query heads per kv head).
+template <typename T, int HD, int NT = kThreads, int KEYS = kDecodeKeys, int REP = kMaxRep, bool WHOLE = false>
+__global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_args a, float* part) {
   constexpr int L = HD / 8;                  // lanes per key row (8 elements each)
-  constexpr int KPP = kThreads / L;          // keys per pass
-  constexpr int PASSES = kDecodeKeys / KPP;  // 2 (HD 64) or 4 (HD 128)
+  constexpr int KPP = NT / L;                // keys per pass
+  constexpr int PASSES = KEYS / KPP;         // split form: 2 (HD 64) or 4 (HD 128)
   constexpr int CH = sizeof(T) == 2 ? 1 : 2; // 16-byte chunks per 8 elements
-  __shared__ float qf[kMaxRep * HD];
+  constexpr int NW = NT / 64;                // waves
+  constexpr int KPL = (KEYS + 63) / 64;      // scores per lane in the softmax
+  static_assert(PASSES * KPP == KEYS, "the passes must cover the keys");
+  __shared__ float qf[REP * HD];
   __shared__ float knew[HD], vnew[HD];
-  __shared__ float sc[kMaxRep * kDecodeKeys];
-  __shared__ float wred[4][kMaxRep * HD];
-  __shared__ float stat[kMaxRep][2];
+  __shared__ float sc[REP * KEYS];
+  __shared__ float wred[NW][REP * HD];
+  __shared__ float stat[REP][2];
   const int n = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int rep = (int)(a.n_heads / a.n_kv_heads);
   const int nsplit = gridDim.z;
   const int64_t W = a.window;
   const int64_t pos = a.positions[n];
-  if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) return;  // combine writes NaN
+  if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) {  // the combine writes NaN
+    if constexpr (WHOLE) {  // position outside the RoPE table: loud NaN output, cache untouched
+      T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
+      for (int idx = threadIdx.x; idx < rep * HD; idx += NT) og[idx] = from_f32<T>(NAN);
+    }
+    return;
+  }
   const int64_t slot = pos % W;
   const int valid = (int)min(pos + 1, W);
-  const int j_lo = sp * kDecodeKeys, j_hi = min(valid, j_lo + kDecodeKeys);
+  const int j_lo = sp * KEYS, j_hi = min(valid, j_lo + KEYS);
   float* pr = part + (((int64_t)n * a.n_kv_heads + kvh) * nsplit + sp) * rep * (HD + 2);
   if (j_lo >= j_hi) {
-    for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += kThreads) {
+    for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += NT) {
       const int e = idx % (HD + 2);
       pr[idx] = e == 0 ? -INFINITY : 0.f;
     }
@@ -468,7 +480,7 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
   const bool owns_slot = slot >= j_lo && slot < j_hi;
   constexpr int half = HD / 2;
   // RoPE (activation-dtype rounding as the reference); the split holding the slot writes the ring
-  for (int idx = threadIdx.x; idx < (rep + 1) * half; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < (rep + 1) * half; idx += NT) {
     const int r = idx / half, e = idx - r * half;
     const T* src = r < rep ? qg + r * HD : kn;
     T lo = src[e], hi = src[e + half];
@@ -486,7 +498,7 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
       }
     }
   }
-  for (int e = threadIdx.x; e < HD; e += kThreads) {
+  for (int e = threadIdx.x; e < HD; e += NT) {
     const T v = vn[e];
     vnew[e] = to_f32(v);
     if (owns_slot) vr[slot * HD + e] = v;
@@ -503,9 +515,9 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
     } else {
       unpack8<T>(kv, kraw[p]);
     }
-    float acc[kMaxRep];
+    float acc[REP];
 #pragma unroll
-    for (int r = 0; r < kMaxRep; ++r) {
+    for (int r = 0; r < REP; ++r) {
       float s = 0.f;
       if (r < rep) {
 #pragma unroll
@@ -517,28 +529,41 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
     }
     if (sub == 0 && j < j_hi) {
 #pragma unroll
-      for (int r = 0; r < kMaxRep; ++r)
-        if (r < rep) sc[r * kDecodeKeys + (j - j_lo)] = acc[r] * a.scale;
+      for (int r = 0; r < REP; ++r)
+        if (r < rep) sc[r * KEYS + (j - j_lo)] = acc[r] * a.scale;
     }
   }
   __syncthreads();
   const int cnt = j_hi - j_lo;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int r = wave; r < rep; r += 4) {
-    const float v0 = lane < cnt ? sc[r * kDecodeKeys + lane] : -INFINITY;
-    const float mx = wave_max(v0);
-    const float p0 = lane < cnt ? expf(v0 - mx) : 0.f;
-    if (lane < cnt) sc[r * kDecodeKeys + lane] = p0;
-    const float sum = wave_sum(p0);
+  for (int r = wave; r < rep; r += NW) {
+    float v0[KPL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < KPL; ++t) {
+      const int jj = lane + 64 * t;
+      v0[t] = jj < cnt ? sc[r * KEYS + jj] : -INFINITY;
+      mx = fmaxf(mx, v0[t]);
+    }
+    mx = wave_max(mx);
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < KPL; ++t) {
+      const int jj = lane + 64 * t;
+      const float p0 = jj < cnt ? expf(v0[t] - mx) : 0.f;
+      if (jj < cnt) sc[r * KEYS + jj] = p0;
+      psum += p0;
+    }
+    const float sum = wave_sum(psum);
     if (lane == 0) {
       stat[r][0] = mx;
       stat[r][1] = sum;
     }
   }
   __syncthreads();
-  float o[kMaxRep][8];
+  float o[REP][8];
 #pragma unroll
-  for (int r = 0; r < kMaxRep; ++r)
+  for (int r = 0; r < REP; ++r)
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[r][i] = 0.f;
 #pragma unroll
@@ -553,17 +578,17 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
       unpack8<T>(vv, vraw[p]);
     }
 #pragma unroll
-    for (int r = 0; r < kMaxRep; ++r) {
+    for (int r = 0; r < REP; ++r) {
       if (r < rep) {
-        const float pw = sc[r * kDecodeKeys + (j - j_lo)];
+        const float pw = sc[r * KEYS + (j - j_lo)];
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[r][i] += pw * vv[i];
       }
     }
   }
-  // reduce the key groups of a wave (lanes with equal sub), then across the 4 waves
+  // reduce the key groups of a wave (lanes with equal sub), then across the waves
 #pragma unroll
-  for (int r = 0; r < kMaxRep; ++r) {
+  for (int r = 0; r < REP; ++r) {
     if (r < rep) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -574,7 +599,7 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
   }
   if (lane < L) {
 #pragma unroll
-    for (int r = 0; r < kMaxRep; ++r) {
+    for (int r = 0; r < REP; ++r) {
       if (r < rep) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) wred[wave][r * HD + e0 + i] = o[r][i];
@@ -582,12 +607,20 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_part(const uttt_swa_dec
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < rep * HD; idx += kThreads) {
+  T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
+  for (int idx = threadIdx.x; idx < rep * HD; idx += NT) {
     const int r = idx / HD, e = idx - r * HD;
-    pr[r * (HD + 2) + 2 + e] = wred[0][idx] + wred[1][idx] + wred[2][idx] + wred[3][idx];
-    if (e == 0) {
-      pr[r * (HD + 2)] = stat[r][0];
-      pr[r * (HD + 2) + 1] = stat[r][1];
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) v += wred[q][idx];
+    if constexpr (WHOLE) {
+      og[idx] = from_f32<T>(v / stat[r][1]);
+    } else {
+      pr[r * (HD + 2) + 2 + e] = v;
+      if (e == 0) {
+        pr[r * (HD + 2)] = stat[r][0];
+        pr[r * (HD + 2) + 1] = stat[r][1];
+      }
     }
   }
 }
@@ -655,10 +688,21 @@ static void launch_prefill(const uttt_swa_prefill_args& a, const PrefillPlan& p,
                        dim3(kThreads), 0, st, a, (const float*)part, p.nsplit, p.q_pad);
 }
 
+// whole-window decode: one 1024-thread workgroup per (request, kv head) for bf16 rings of up to
+// kWholeKeys slots, head_dim 64 and at most kWholeRep query heads per kv head
+constexpr int kWholeThreads = 1024, kWholeKeys = 512, kWholeRep = 4;
+
 template <typename T, int HD>
 static void launch_decode(const uttt_swa_decode_args& a, hipStream_t st) {
   const int nsplit = decode_splits(a.window);
   float* part = static_cast<float*>(a.workspace);
+  if constexpr (sizeof(T) == 2 && HD == 64) {
+    if (a.window <= kWholeKeys && a.n_heads / a.n_kv_heads <= kWholeRep) {
+      hipLaunchKernelGGL((k_swa_decode_part<T, HD, kWholeThreads, kWholeKeys, kWholeRep, true>),
+                         dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, 1u), dim3(kWholeThreads), 0, st, a, part);
+      return;
+    }
+  }
   hipLaunchKernelGGL((k_swa_decode_part<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, (unsigned)nsplit),
                      dim3(kThreads), 0, st, a, part);
   hipLaunchKernelGGL((k_swa_decode_combine<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads), dim3(kThreads), 0,
