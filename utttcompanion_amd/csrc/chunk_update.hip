@@ -381,7 +381,9 @@ __device__ __forceinline__ void stage_row(const T* x, int D, const T* nw, float 
 // floats apart), xres the row's residual (fp32, LDS or global).  KPER values per thread
 // (D <= KPER * 256); the partial rows are loaded four at a time with all their loads in flight
 // before any is summed, and always summed in split order.
-template <typename T, int KPER>
+// AGENT: the partials were written by other workgroups of this launch with device-coherent
+// stores; read them the same way (past this CU's L2, which may hold none of them yet)
+template <typename T, int KPER, bool AGENT = false>
 __device__ __forceinline__ void ln_readout_row(const float* z0, int64_t sp_stride, int nsplit, int D, float eps,
                                                const float* ln_w, const float* ln_b, const float* xres, T* o,
                                                float* red) {
@@ -398,7 +400,12 @@ __device__ __forceinline__ void ln_readout_row(const float* z0, int64_t sp_strid
 #pragma unroll
       for (int i = 0; i < KPER; ++i) {
         const int d = threadIdx.x + i * kThreads;
-        v[u][i] = sp0 + u < nsplit && d < D ? src[d] : 0.f;
+        if constexpr (AGENT)
+          v[u][i] = sp0 + u < nsplit && d < D
+                        ? __hip_atomic_load(src + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : 0.f;
+        else
+          v[u][i] = sp0 + u < nsplit && d < D ? src[d] : 0.f;
       }
     }
 #pragma unroll
@@ -957,22 +964,29 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
     for (int e = 0; e < CW; ++e) zred[p * a.D + c * CW + e] = az[e];
   }
   __syncthreads();
+  if (a.counters == nullptr) {  // k_ln_readout follows
+    for (int dd = threadIdx.x; dd < a.D; dd += kThreads) {
+      float v = 0.f;
+      for (int q = 0; q < nparts; ++q) v += zred[q * a.D + dd];
+      zp[dd] = v;
+    }
+    return;
+  }
+  // The row's last block to finish sums the row's partials.  The partials are written with
+  // device-coherent stores (through this CU's L2), every thread waits until its stores are
+  // done, and only then is the row's count raised; the last block reads the partials with
+  // device-coherent loads.  So no cache write-back or invalidate is needed.  The last block
+  // returns the count to zero for the next call.
   for (int dd = threadIdx.x; dd < a.D; dd += kThreads) {
     float v = 0.f;
     for (int q = 0; q < nparts; ++q) v += zred[q * a.D + dd];
-    zp[dd] = v;
+    __hip_atomic_store(zp + dd, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (a.counters == nullptr) return;  // k_ln_readout follows
-  // The row's last block to finish sums the row's partials.  Every thread's partial stores
-  // have reached this CU's L2 before the barrier; one release (L2 write-back) then publishes
-  // them with the count, and only the last block acquires (L2 invalidate) before reading the
-  // other blocks' partials.  It returns the count to zero for the next call.
   wait_vmcnt<0>();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(a.counters + b, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned prev = __hip_atomic_fetch_add(a.counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = prev == gridDim.x - 1;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!last) return;
@@ -980,9 +994,9 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
   const float* z0 = a.zp + (int64_t)b * a.tok_pad * a.D;
   const int64_t sp_stride = (int64_t)a.B * a.tok_pad * a.D;
   if (a.D <= 4 * kThreads)
-    ln_readout_row<bf16, 4>(z0, sp_stride, gridDim.x, a.D, a.ln_eps, a.ln_w, a.ln_b, xs, o, sred);
+    ln_readout_row<bf16, 4, true>(z0, sp_stride, gridDim.x, a.D, a.ln_eps, a.ln_w, a.ln_b, xs, o, sred);
   else
-    ln_readout_row<bf16, 8>(z0, sp_stride, gridDim.x, a.D, a.ln_eps, a.ln_w, a.ln_b, xs, o, sred);
+    ln_readout_row<bf16, 8, true>(z0, sp_stride, gridDim.x, a.D, a.ln_eps, a.ln_w, a.ln_b, xs, o, sred);
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
