@@ -140,6 +140,10 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
     ws_chain = ws_read = None
     main = torch.cuda.current_stream(dev)
     side = model._chain_stream(dev)  # the layer chain runs one layer behind the forward pass
+    # bf16: each layer's readout also forms the chain's products of that layer's keys with W_up /
+    # W_gate (one read of those weights for both), and the chain stage runs in two parts, as in
+    # the model's prefill with writes
+    shared = copies is not None
     for ci in range(n_chunks):
         rows, off = active[ci], ci * c
         end = off + c
@@ -151,7 +155,7 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
                               pool.normalize_loss_by_dim, pool.eps, dt,
                               copies=None if copies is None else [t[:rows] for t in copies],
                               surprise=surprise[ci], row_loss=chunk_rl, min_row_surprise=min_chunk_surprise,
-                              workspace=ws_chain)
+                              workspace=ws_chain, w_products_given=shared)
         ws_chain = run.workspace
         for li, block in enumerate(model.layers):
             attn = block.attn
@@ -165,11 +169,21 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
             ready.record(main)
             if ws_read is None:
                 ws_read = K.readout_workspace(uq, rd[0])
-            hid = linear_residual(hid, K.swiglu_readout(uq, *rd, ln_w, ln_b, pool.eps, workspace=ws_read),
-                                  block.uttt.w_o.weight)
+            r = K.swiglu_readout(uq, *rd, ln_w, ln_b, pool.eps, workspace=ws_read, keys=uk if shared else None,
+                                 key_outputs=run.w_product_outputs(li) if shared else None)
+            if shared:
+                read_done = torch.cuda.Event()
+                read_done.record(main)
+            hid = linear_residual(hid, r, block.uttt.w_o.weight)
             side.wait_event(ready)  # enqueued after the readout it overlaps
             with torch.cuda.stream(side):
-                run.add_layer(uk, uv, eta, alpha)
+                if shared:
+                    layer = run.set_layer(uk, uv, eta, alpha)
+                    run.launch(layer, part=1)
+                    side.wait_event(read_done)
+                    run.launch(layer, part=2)
+                else:
+                    run.add_layer(uk, uv, eta, alpha)
         side.wait_stream(main)
         with torch.cuda.stream(side):
             run.finish()
