@@ -14,12 +14,12 @@ CFG = dict(vocab_size=256, d_model=128, n_layers=3, n_heads=2, n_kv_heads=1, d_f
            sliding_window_size=24, max_seq_len=512)
 
 
-def make(dtype=torch.float32, seed=0, slow_std=0.08):
+def make(dtype=torch.float32, seed=0, slow_std=0.08, cfg=None):
     """``slow_std`` 0.08 (larger than the reference's 0.02 init) makes greedy tokens vary in
     the token-equality test; the bf16 logits test uses the reference init."""
     from utttcompanion_amd import uTTTConfig, uTTTModel
     torch.manual_seed(seed)
-    model = uTTTModel(uTTTConfig(**CFG)).eval()
+    model = uTTTModel(uTTTConfig(**(cfg or CFG))).eval()
     with torch.no_grad():
         for name, p in model.named_parameters():
             if p.dim() == 2 and "fast_weight_pool" not in name and "w_eta" not in name and "w_alpha" not in name:
@@ -37,7 +37,7 @@ def make(dtype=torch.float32, seed=0, slow_std=0.08):
             t.add_(0.05 * torch.randn(t.shape, generator=g).to(DEV))
         states.append(st)
     lengths = [5, 17, 30, 40]
-    prompts = [torch.randint(6, 256, (n,), generator=g) for n in lengths]
+    prompts = [torch.randint(6, (cfg or CFG)["vocab_size"], (n,), generator=g) for n in lengths]
     return model, states, prompts
 
 
@@ -71,13 +71,22 @@ def test_graph_step_equals_eager_step(dtype):
         tok = eager.next_tokens.clone()
 
 
-def test_decoder_logits_match_eager_frozen_forward_bf16():
+# head_dim 128 (split attention form), d_model 1024, d_ff 640 (128-column readout blocks)
+CFG_WIDE = dict(vocab_size=512, d_model=1024, n_layers=2, n_heads=8, n_kv_heads=2, d_ff_fast=640, chunk_size=16,
+                sliding_window_size=24, max_seq_len=512)
+
+
+@pytest.mark.parametrize("cfg,atol", [(None, 0.015), (CFG_WIDE, 0.035)], ids=["c2-like", "wide"])
+def test_decoder_logits_match_eager_frozen_forward_bf16(cfg, atol):
     """bf16 model: batched step logits vs the eager frozen single-request forward, at the
     reference's own bound for ring decode vs eager bf16 logits (atol 0.015, rtol 0.025,
     reference tests/test_inference_cuda_graph.py:54-90): the batched GEMMs and the ring
-    change bf16 reduction orders, so the two need not be bitwise equal."""
+    change bf16 reduction orders, so the two need not be bitwise equal.  The wide model's
+    logits reach |2.5|, where one bf16 unit is 2^-6: there the absolute bound is two such units
+    plus a little (a step through the library GEMMs and separate norms differs from the eager
+    forward by the same 0.02-0.025)."""
     from utttcompanion_amd.decoder import BatchedDecoder
-    model, states, prompts = make(torch.bfloat16, seed=3, slow_std=0.02)
+    model, states, prompts = make(torch.bfloat16, seed=3, slow_std=0.02, cfg=cfg)
     dec = BatchedDecoder(model, states)
     first = dec.prefill(prompts)
     tok = first.float().argmax(-1)
@@ -92,6 +101,6 @@ def test_decoder_logits_match_eager_frozen_forward_bf16():
             out = model(tok[i].view(1, 1), fast_state=st, kv_caches=caches[i], start_pos=pos,
                         update_fast_weights=False)
             caches[i] = out.kv_caches
-            torch.testing.assert_close(got[i], out.logits[0, -1].float(), atol=0.015, rtol=0.025,
+            torch.testing.assert_close(got[i], out.logits[0, -1].float(), atol=atol, rtol=0.025,
                                        msg=f"step {step} request {i}")
         tok = dec.next_tokens.clone()
