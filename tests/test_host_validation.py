@@ -1,0 +1,69 @@
+"""Host-side argument checks of the decode-step entry points (no GPU needed: every case is
+rejected before any device call).  The wrappers raise ValueError like the reference's own
+shape checks; the C ABI returns a status with a message."""
+import ctypes as C
+
+import pytest
+import torch
+
+from utttcompanion_amd import _native as N
+from utttcompanion_amd import kernels as K
+
+
+def test_skinny_linear_rejects_bad_operands():
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="agree on k"):
+        K.skinny_linear(x, torch.zeros(32, 128, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="bf16"):
+        K.skinny_linear(x.float(), torch.zeros(32, 64))
+    with pytest.raises(ValueError, match="no CPU path"):
+        K.skinny_linear(x, torch.zeros(32, 64, dtype=torch.bfloat16))
+
+
+def test_greedy_select_rejects_bad_arguments():
+    logits = torch.zeros(2, 100)
+    with pytest.raises(ValueError, match="at most 8"):
+        K.greedy_select(logits, banned=tuple(range(9)))
+    with pytest.raises(ValueError, match="rows, vocab"):
+        K.greedy_select(torch.zeros(100))
+    with pytest.raises(ValueError, match="no CPU path"):
+        K.greedy_select(logits, banned=(0, 1, 2))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return N.load_library()
+
+
+def _fake(n):  # aligned, never dereferenced: every call below fails its checks first
+    return C.c_void_p(0x100000 + 0x1000 * n)
+
+
+def test_c_abi_rejects_decode_options_outside_one_token_rows(lib):
+    a = N.ReadoutArgs()
+    a.batch, a.tokens, a.d_model, a.d_ff = 2, 2, 256, 512
+    a.act_dtype, a.w_dtype, a.eps = N.DTYPE_BF16, N.DTYPE_BF16, 1e-5
+    a.x, a.w_up, a.w_gate, a.w_down = _fake(1), _fake(2), _fake(3), _fake(4)
+    a.ln_weight, a.ln_bias, a.out = _fake(5), _fake(6), _fake(7)
+    a.x_row_stride, a.out_row_stride = 2 * 256, 2 * 256
+    a.x_norm_weight, a.x_norm_eps = _fake(8), 1e-5
+    rc = lib.uttt_swiglu_readout(C.byref(a), _fake(9), 1 << 40, None)
+    assert rc != 0
+    assert b"one bf16 token per row" in lib.uttt_last_error()
+    a.tokens = 1
+    a.x_norm_eps = 0.0
+    assert lib.uttt_swiglu_readout(C.byref(a), _fake(9), 1 << 40, None) != 0
+    assert b"x_norm_eps" in lib.uttt_last_error()
+
+
+def test_c_abi_rejects_bad_greedy_and_skinny_calls(lib):
+    g = N.GreedyArgs()
+    g.rows, g.vocab, g.dtype, g.n_banned = 2, 100, N.DTYPE_BF16, 1
+    g.banned[0] = -3
+    g.logits, g.row_stride, g.out = _fake(1), 100, _fake(2)
+    assert lib.uttt_greedy_select(C.byref(g), None) != 0
+    assert b"excluded ids must be >= 0" in lib.uttt_last_error()
+    s = N.SkinnyLinearArgs()
+    s.m, s.n, s.k, s.act_dtype, s.x_eps = 4, 64, 64, N.DTYPE_BF16, -1.0
+    assert lib.uttt_skinny_linear(C.byref(s), None) != 0
+    assert b"x_eps" in lib.uttt_last_error()
