@@ -378,14 +378,14 @@ __device__ __forceinline__ void stage_row(const T* x, int D, const T* nw, float 
 }
 
 // out = xres + LN(z) for one token row, z the sum of the row's nsplit partials (rows sp_stride
-// floats apart), xres the row's residual (fp32, LDS or global).  KPER values per thread
+// floats apart), xres the row's residual (the staged fp32 row in LDS, or the row of x itself).  KPER values per thread
 // (D <= KPER * 256); the partial rows are loaded four at a time with all their loads in flight
 // before any is summed, and always summed in split order.
 // AGENT: the partials were written by other workgroups of this launch with device-coherent
 // stores; read them the same way (past this CU's L2, which may hold none of them yet)
-template <typename T, int KPER, bool AGENT = false>
+template <typename T, int KPER, bool AGENT = false, typename XR>
 __device__ __forceinline__ void ln_readout_row(const float* z0, int64_t sp_stride, int nsplit, int D, float eps,
-                                               const float* ln_w, const float* ln_b, const float* xres, T* o,
+                                               const float* ln_w, const float* ln_b, const XR* xres, T* o,
                                                float* red) {
   const float inv_d = 1.0f / (float)D;
   float z[KPER];
@@ -433,7 +433,7 @@ __device__ __forceinline__ void ln_readout_row(const float* z0, int64_t sp_strid
     if (d < D) {
       const float g = to_f32(from_f32<T>(ln_w[d]));
       const float be = to_f32(from_f32<T>(ln_b[d]));
-      o[d] = from_f32<T>(xres[d] + ((z[i] - mean) * rstd * g + be));
+      o[d] = from_f32<T>(to_f32(xres[d]) + ((z[i] - mean) * rstd * g + be));
     }
   }
 }
@@ -445,10 +445,16 @@ __global__ void __launch_bounds__(kThreads) k_ln_readout(const LnOutArgs a) {
   const int t = blockIdx.x, b = blockIdx.y;
   if (t >= a.ntok) return;
   const T* xr = static_cast<const T*>(a.x) + (int64_t)b * a.x_rs + (int64_t)t * a.D;
-  stage_row<T>(xr, a.D, static_cast<const T*>(a.xn_w), a.xn_eps, xs, red);
   T* o = static_cast<T*>(a.out) + (int64_t)b * a.out_rs + (int64_t)t * a.D;
-  ln_readout_row<T, KPER>(a.zp + ((int64_t)b * a.tok_pad + t) * a.D, (int64_t)a.B * a.tok_pad * a.D, a.nsplit, a.D,
-                          a.eps, a.ln_w, a.ln_b, xs, o, red);
+  const float* z0 = a.zp + ((int64_t)b * a.tok_pad + t) * a.D;
+  const int64_t sp_stride = (int64_t)a.B * a.tok_pad * a.D;
+  if (a.xn_w == nullptr) {  // the residual is x itself, read where it is used
+    ln_readout_row<T, KPER>(z0, sp_stride, a.nsplit, a.D, a.eps, a.ln_w, a.ln_b, xr, o, red);
+    return;
+  }
+  stage_row<T>(xr, a.D, static_cast<const T*>(a.xn_w), a.xn_eps, xs, red);
+  __syncthreads();
+  ln_readout_row<T, KPER>(z0, sp_stride, a.nsplit, a.D, a.eps, a.ln_w, a.ln_b, xs, o, red);
 }
 
 template <typename T>
