@@ -162,7 +162,8 @@ class BatchedDecoder:
         self.logits = logits
         # temperature-0 selection: PAD / BOS / UNK and ids past the active vocabulary excluded
         limit = m.active_vocab_limit if m.active_vocab_limit < logits.shape[-1] else None
-        self.next_tokens = K.greedy_select(logits, (PAD_ID, BOS_ID, UNK_ID), limit)
+        # written straight into the next step's input: stepping with `next_tokens` copies nothing
+        self.next_tokens = K.greedy_select(logits, (PAD_ID, BOS_ID, UNK_ID), limit, out=self.tokens)
 
     def _warm_workspaces(self) -> None:
         lib_ws_attn = 1 << 20
@@ -201,7 +202,8 @@ class BatchedDecoder:
         limit = self.cos.shape[0]
         if max(self.host_positions) >= limit:
             raise ValueError("a request reached the end of the RoPE table")
-        self.tokens.copy_(tokens)
+        if tokens.data_ptr() != self.tokens.data_ptr():
+            self.tokens.copy_(tokens)
         if self._graph is not None:
             self._graph.replay()
         else:
@@ -223,6 +225,6 @@ class BatchedDecoder:
         out = [tok]
         for _ in range(steps - 1):
             self.step(tok)
-            tok = self.next_tokens.clone()
-            out.append(tok)
+            tok = self.next_tokens  # already the next step's input
+            out.append(tok.clone())
         return torch.stack(out, dim=1)
