@@ -362,6 +362,8 @@ typedef struct {
   int64_t active_limit;
   const void* logits; int64_t row_stride;
   int64_t* out;     /* (rows,) token ids */
+  int64_t* advance; /* optional (rows,): each entry is incremented by one (a decode step's position
+                     * counters, advanced in the same launch); NULL: none */
 } uttt_greedy_args;
 
 int uttt_greedy_select(const uttt_greedy_args* args, uttt_stream_t stream);

@@ -574,9 +574,11 @@ def test_greedy_select_matches_masked_argmax(dtype, rows, vocab, limit):
     if limit is not None:
         ref[:, limit:] = float("-inf")
     want = ref.argmax(dim=-1)
-    got = K.greedy_select(x.to(DEV), banned, limit)
+    pos = torch.arange(rows, dtype=torch.int64, device=DEV) * 7
+    got = K.greedy_select(x.to(DEV), banned, limit, advance=pos)
     torch.cuda.synchronize()
     assert torch.equal(got.cpu(), want)
+    assert torch.equal(pos.cpu(), torch.arange(rows, dtype=torch.int64) * 7 + 1)  # advanced once
     allmasked = torch.full((2, vocab), float("-inf")).to(dtype)
     got2 = K.greedy_select(allmasked.to(DEV), banned, limit)
     torch.cuda.synchronize()

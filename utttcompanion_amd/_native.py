@@ -11,7 +11,7 @@ import threading
 
 from .build import LIB_PATH
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 MAX_CHAIN = 64
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -91,7 +91,7 @@ class GreedyArgs(C.Structure):
         ("rows", _I64), ("vocab", _I64), ("dtype", _I32), ("n_banned", _I32),
         ("banned", _I32 * 8), ("active_limit", _I64),
         ("logits", _P), ("row_stride", _I64),
-        ("out", _P),
+        ("out", _P), ("advance", _P),
     ]
 
 

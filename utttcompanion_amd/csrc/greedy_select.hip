@@ -22,6 +22,7 @@ struct SelectArgs {
   const void* logits;
   int64_t rs;
   int64_t* out;
+  int64_t* advance;
 };
 
 struct Best {
@@ -102,6 +103,7 @@ __global__ void __launch_bounds__(kSelThreads) k_greedy_select(const SelectArgs 
   if (threadIdx.x == 0) {
     for (int q = 1; q < kSelThreads / 64; ++q) take(b, sv[q], si[q]);
     a.out[row] = (int64_t)b.i;
+    if (a.advance != nullptr) a.advance[row] += 1;
   }
 }
 
@@ -131,6 +133,7 @@ extern "C" int uttt_greedy_select(const uttt_greedy_args* a, uttt_stream_t strea
   s.logits = a->logits;
   s.rs = a->row_stride;
   s.out = a->out;
+  s.advance = a->advance;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)a->rows);
   const bool bf = a->dtype == UTTT_DTYPE_BF16;

@@ -158,12 +158,13 @@ class BatchedDecoder:
                                      self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read)
             h = self._linear(r.view(n, -1), block.uttt.w_o.weight, residual=h)
         logits = self._linear(h, m.lm_head.weight, norm=m.norm)
-        self.positions.add_(1)
         self.logits = logits
         # temperature-0 selection: PAD / BOS / UNK and ids past the active vocabulary excluded
         limit = m.active_vocab_limit if m.active_vocab_limit < logits.shape[-1] else None
-        # written straight into the next step's input: stepping with `next_tokens` copies nothing
-        self.next_tokens = K.greedy_select(logits, (PAD_ID, BOS_ID, UNK_ID), limit, out=self.tokens)
+        # written straight into the next step's input (stepping with `next_tokens` copies
+        # nothing), and the positions advance in the same launch
+        self.next_tokens = K.greedy_select(logits, (PAD_ID, BOS_ID, UNK_ID), limit, out=self.tokens,
+                                           advance=self.positions)
 
     def _warm_workspaces(self) -> None:
         lib_ws_attn = 1 << 20

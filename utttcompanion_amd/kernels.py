@@ -566,11 +566,12 @@ def skinny_linear(x: Tensor, weight: Tensor, out: Optional[Tensor] = None,
 
 
 def greedy_select(logits: Tensor, banned: Sequence[int] = (), active_limit: Optional[int] = None,
-                  out: Optional[Tensor] = None) -> Tensor:
+                  out: Optional[Tensor] = None, advance: Optional[Tensor] = None) -> Tensor:
     """Greedy next tokens (rows,) int64 from logits (rows, vocab) bf16 / fp32
     (``uttt_greedy_select``): argmax after setting the ``banned`` ids and the ids at or past
     ``active_limit`` to -inf (the temperature-0 branch of reference sample_next_token,
-    model/uttt_model.py:1203-1221), one launch."""
+    model/uttt_model.py:1203-1221), one launch.  ``advance`` (rows,) int64, when given, is
+    incremented by one in the same launch (a decode step's position counters)."""
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be (rows, vocab) with unit column stride")
     if len(banned) > 8:
@@ -589,6 +590,11 @@ def greedy_select(logits: Tensor, banned: Sequence[int] = (), active_limit: Opti
         a.banned[i] = int(t)
     a.active_limit = -1 if active_limit is None else int(active_limit)
     a.logits, a.row_stride, a.out = _p(logits), logits.stride(0), _p(out)
+    if advance is not None:
+        if advance.dtype != torch.int64 or advance.numel() != rows or not advance.is_contiguous():
+            raise ValueError(f"advance must be {rows} contiguous int64 entries")
+        _require_device(dev, advance)
+        a.advance = _p(advance)
     lib = N.load_library()
     with torch.cuda.device(dev):
         N.check(lib.uttt_greedy_select(C.byref(a), _stream(dev)), "uttt_greedy_select")
