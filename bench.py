@@ -258,6 +258,48 @@ def bench_decode(iters: int):
     return ms, kv_bytes, dict(requests=N_REQ, heads=H, kv_heads=HKV, head_dim=HD, window=W)
 
 
+def bench_decode_readout(iters: int):
+    """The decode step's dominant kernel at the config-4 shape: the one-launch fast-weight
+    readout (q_norm, GEMV through the 32 requests' bf16 copies, LayerNorm in each request's last
+    block) of one token per request, 12 calls (one per layer, each its own copies) recorded in
+    a HIP graph and replayed ``iters`` times.  Returns (us per call, algorithmic bytes per call)."""
+    import torch
+    from utttcompanion_amd import kernels as K
+    N_REQ, D, F, LAYERS = 32, C2["d_model"], C2["d_ff_fast"], C2["n_layers"]
+    g = torch.Generator(device="cuda").manual_seed(4)
+    xs = [torch.randn(N_REQ, 1, D, device="cuda", generator=g).to(torch.bfloat16) for _ in range(LAYERS)]
+    ws = [[(0.02 * torch.randn(N_REQ, D, F, device="cuda", generator=g)).to(torch.bfloat16),
+           (0.02 * torch.randn(N_REQ, D, F, device="cuda", generator=g)).to(torch.bfloat16),
+           (0.02 * torch.randn(N_REQ, F, D, device="cuda", generator=g)).to(torch.bfloat16)] for _ in range(LAYERS)]
+    ln_w, ln_b = torch.ones(D, device="cuda"), torch.zeros(D, device="cuda")
+    qn = torch.ones(D, device="cuda", dtype=torch.bfloat16)
+    counters = torch.zeros(N_REQ, dtype=torch.int32, device="cuda")
+    ws_read = K.readout_workspace(xs[0], ws[0][0])
+    outs = [torch.empty_like(x) for x in xs]
+
+    def run():
+        for i in range(LAYERS):
+            K.swiglu_readout(xs[i], *ws[i], ln_w, ln_b, 1e-5, out=outs[i], workspace=ws_read,
+                             x_norm=(qn, 1e-5), row_counters=counters)
+
+    with torch.no_grad():
+        run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (iters * LAYERS)
+    return us, 3 * D * F * 2 * N_REQ
+
+
 def bench_decode_step(model, steps: int):
     """Config 4: 32 requests on the config-2 model, each with its own fp32 fast weights
     (W_up/W_gate/W_down ~ N(0, 0.02) drawn from a generator seeded with the request id,
@@ -470,6 +512,13 @@ def main() -> int:
         decode = {"kernel": "k_swa_decode", "us_per_layer_step": round(dec_ms * 1e3, 2),
                   "achieved_gbs": round(dec_gbs, 1), "hbm_frac": round(dec_gbs / PEAK_HBM_GBS, 4), "shape": dec_shape}
         log(f"decode kernel {dec_ms * 1e3:.1f} us -> {dec_gbs:.0f} GB/s")
+        rd_us, rd_bytes = bench_decode_readout(20)
+        rd_gbs = rd_bytes / (rd_us * 1e-6) / 1e9
+        decode["readout"] = {"kernel": "k_readout_gemv", "us_per_layer_step": round(rd_us, 2),
+                             "algorithmic_bytes": rd_bytes, "achieved_gbs": round(rd_gbs, 1),
+                             "hbm_frac": round(rd_gbs / PEAK_HBM_GBS, 4),
+                             "unit_bytes": "3 D F bf16 per request (W_up, W_gate, W_down copies read once)"}
+        log(f"decode readout {rd_us:.1f} us -> {rd_gbs:.0f} GB/s")
         tps, step_ms, info = bench_decode_step(model, args.decode_steps)
         decode.update(decode_tok_s=round(tps, 1), ms_per_decode_step=round(step_ms, 4), workload=info)
         log(f"decode step {step_ms:.3f} ms -> {tps:.0f} tok/s")
