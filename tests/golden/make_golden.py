@@ -11,7 +11,12 @@ seeded inputs, the outputs that no closed form pins:
   schedule with right padding, per-layer surprise aggregation and step count;
 * ``uTTTModel.forward(update_fast_weights=False)`` and greedy ``stream_generate``;
 * ``uTTTModel.test_time_update`` followed by ``apply_elastic_pull`` and
-  ``compute_drift`` (the personalizer's step 2-3 arithmetic).
+  ``compute_drift`` (the personalizer's step 2-3 arithmetic);
+* (``formats``) the two on-disk payloads a deployment loads: a base checkpoint laid out as
+  ``train_5090.py:918-930`` writes it (``slow_weights`` / ``init_fast_weights`` from the
+  reference model's ``state_dict``) and a persona file laid out as
+  ``engine/checkpoint_manager.py:547-557`` writes it (``fast_state`` from the reference's
+  ``FastWeightState.to_state_dict``), with the reference's logits on them.
 
 Weights are drawn here from a seeded generator and loaded into the reference
 modules, so the fixtures hold every input explicitly: nothing depends on the
@@ -80,7 +85,68 @@ def state_arrays(prefix: str, state) -> dict:
             for n in ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")}
 
 
+# the format fixtures also run on the GPU: d_model and d_ff multiples of 64, head_dim 64
+FORMAT_TINY = dict(TINY, d_model=128, n_layers=1, n_heads=2, n_kv_heads=1, d_ff_fast=64)
+
+
+def write_formats() -> dict:
+    """base_tiny.pt, persona_tiny.pt and formats_tiny.npz (see the module docstring)."""
+    sys.path.insert(0, str(REFERENCE))
+    from model.uttt_model import uTTTConfig, uTTTModel  # noqa: E402
+
+    torch.set_num_threads(1)
+    cfg = uTTTConfig(**FORMAT_TINY)
+    model = uTTTModel(cfg).eval()
+    load_into(model, draw_weights(model, 20261202))
+    state = model.state_dict()
+    prefix = "fast_weight_pool."
+    base = {
+        "checkpoint_type": "uTTT_Base_Checkpoint", "version": "1.0.0", "step": 1234,
+        "timestamp": "2026-12-02T00:00:00Z", "config": cfg.to_dict(),
+        "slow_weights": {k: v.detach().clone() for k, v in state.items() if not k.startswith(prefix)},
+        "init_fast_weights": {k[len(prefix):]: v.detach().clone() for k, v in state.items() if k.startswith(prefix)},
+        "metrics": {"loss": 1.5},
+    }
+    torch.save(base, HERE / "base_tiny.pt")
+    gen = torch.Generator().manual_seed(17)
+    turn = torch.randint(6, TINY["vocab_size"], (1, 40), generator=gen)
+    ids = torch.randint(6, TINY["vocab_size"], (1, 33), generator=gen)
+    with torch.no_grad():
+        persona_state, _, _ = model.test_time_update(turn, model.init_fast_state(detach=True))
+        persona = {
+            "checkpoint_type": "uTTT_User_Persona_State", "version": "1.0.0", "user_id": "alice",
+            "base_signature": "tiny", "base_fingerprint": "tiny", "timestamp": "2026-12-02T00:00:00Z",
+            "fast_state": persona_state.to_state_dict(),
+            "drift_metrics": model.fast_weight_pool.compute_drift(persona_state),
+            "metadata": {"user_id": "alice", "turns": 1},
+        }
+        torch.save(persona, HERE / "persona_tiny.pt")
+        frozen = model(ids, fast_state=persona_state, update_fast_weights=False)
+        written = model(ids, fast_state=persona_state, update_fast_weights=True)
+    arrays = {"in/turn": turn.numpy(), "in/ids": ids.numpy(),
+              "out/frozen_logits": frozen.logits.float().numpy(),
+              "out/update_logits": written.logits.float().numpy()}
+    arrays.update(state_arrays("out/persona_state", persona_state))
+    arrays.update(state_arrays("out/update_state", written.fast_state))
+    arrays["out/update_step"] = np.array(written.fast_state.step)
+    np.savez_compressed(HERE / "formats_tiny.npz", **arrays)
+    return {
+        "base_tiny.pt": {"what": "base checkpoint payload (train_5090.py:918-930 layout), weights seed 20261202; "
+                                 "load with torch.load(weights_only=True)", "config": FORMAT_TINY},
+        "persona_tiny.pt": {"what": "persona payload (checkpoint_manager.py:547-557 layout): fast_state = "
+                                    "FastWeightState.to_state_dict() after test_time_update of in/turn"},
+        "formats_tiny.npz": {"what": "reference frozen forward and forward with writes of in/ids (1 x 33) "
+                                     "from the persona state, and the persona state itself"},
+    }
+
+
 def main() -> None:
+    if sys.argv[1:] == ["formats"]:  # only the on-disk payloads, merged into golden.json
+        meta = json.loads((HERE / "golden.json").read_text())
+        meta["files"].update(write_formats())
+        (HERE / "golden.json").write_text(json.dumps(meta, indent=1) + "\n")
+        print("wrote the on-disk format fixtures")
+        return
     sys.path.insert(0, str(REFERENCE))
     from model.uttt_layer import uTTTBlock, uTTTLayer  # noqa: E402
     from model.uttt_model import uTTTConfig, uTTTModel  # noqa: E402
@@ -176,6 +242,7 @@ def main() -> None:
                 "and uTTTBlock.forward with a 20-token frozen-prefill cache at start_pos 20",
         "layer_config": layer_cfg, "seed_weights": 99, "seed_inputs": 11}
 
+    meta["files"].update(write_formats())
     import platform
     meta["generated_with"] = {"torch": torch.__version__, "python": platform.python_version()}
     (HERE / "golden.json").write_text(json.dumps(meta, indent=1) + "\n")

@@ -104,3 +104,52 @@ def test_decoder_logits_match_eager_frozen_forward_bf16(cfg, atol):
             torch.testing.assert_close(got[i], out.logits[0, -1].float(), atol=atol, rtol=0.025,
                                        msg=f"step {step} request {i}")
         tok = dec.next_tokens.clone()
+
+
+def test_stream_generate_graph_route_equals_eager_tokens():
+    """``use_cuda_graph=True`` (one-request ring decoder replayed from a HIP graph) yields the
+    eager tokens; a second call with the same state reuses the captured decoder, and a write
+    to the state's W makes the next call build a new one."""
+    model, states, prompts = make()
+    kw = dict(max_new_tokens=20, temperature=0.0, eos_token_id=None)
+    for st, ids in zip(states[2:], prompts[2:]):  # prompts of 30 and 40 tokens: past the 24 window
+        p = ids.view(1, -1).to(DEV)
+        eager = list(model.stream_generate(p, st, **kw))
+        graph = list(model.stream_generate(p, st, use_cuda_graph=True, **kw))
+        assert graph == eager
+        dec = model._cuda_graph_decoder
+        assert dec is not None and dec._graph is not None
+        assert list(model.stream_generate(p, st, use_cuda_graph=True, **kw)) == eager
+        assert model._cuda_graph_decoder is dec
+    st, p = states[3], prompts[3].view(1, -1).to(DEV)
+    with torch.no_grad():
+        st.w_up.add_(0.05)
+    eager = list(model.stream_generate(p, st, **kw))
+    assert list(model.stream_generate(p, st, use_cuda_graph=True, **kw)) == eager
+    assert model._cuda_graph_decoder is not dec
+
+
+def test_fused_inference_readout_reads_versioned_copies():
+    """``prepare_for_inference()``: frozen readouts of a bf16 model read the state's versioned
+    bf16 copies -- bit for bit the readout of explicit bf16 copies -- and a write to the master
+    refreshes them."""
+    from utttcompanion_amd import kernels as K
+    model, states, _ = make(torch.bfloat16, seed=5, slow_std=0.02)
+    model.prepare_for_inference()
+    pool, st = model.fast_weight_pool, states[0]
+    x = torch.randn(1, 7, CFG["d_model"], device=DEV).bfloat16()
+    with torch.no_grad():
+        got = pool.forward_readout(x, st)
+        want = K.swiglu_readout(x, *(t.bfloat16() for t in (st.w_up, st.w_gate, st.w_down)), st.ln_weight,
+                                st.ln_bias, pool.eps)
+        assert torch.equal(got, want)
+        copies = st._read_copies
+        pool.forward_readout(x, st)
+        assert st._read_copies is copies
+        st.w_down.mul_(1.5)
+        got2 = pool.forward_readout(x, st)
+        want2 = K.swiglu_readout(x, *(t.bfloat16() for t in (st.w_up, st.w_gate, st.w_down)), st.ln_weight,
+                                 st.ln_bias, pool.eps)
+    torch.cuda.synchronize()
+    assert st._read_copies is not copies and torch.equal(got2, want2)
+    model.prepare_for_inference(False)

@@ -236,3 +236,119 @@ def test_chunk_update_row_loss_and_gate_match_oracle(masked):
     counts = mask.sum(1) if masked else torch.full((b,), float(c))
     assert torch.equal(row_loss[:, 1].cpu(), counts)
     assert rel_err(row_loss[:, 0].cpu() / counts, rows) <= 1e-5
+
+
+def _kernel_row_means(row_loss):
+    """The per-chunk gate's input as the kernels form it: sum / max(count, 1) in fp32."""
+    rl = row_loss.detach().float().cpu()
+    return rl[..., 0] / torch.clamp(rl[..., 1], min=1.0)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_chunk_update_gate_is_inclusive_at_the_threshold(masked):
+    """``uttt_chunk_update``: a row whose chunk loss equals the threshold exactly is written
+    (the gate skips a chunk only when its loss is below the threshold); one float step above
+    its loss it keeps W and S.  The threshold is the kernel's own row mean, read from its
+    ``row_loss`` output, so the comparison is exact."""
+    import numpy as np
+    from test_gpu_kernels import make_chunk, to_dev
+    from utttcompanion_amd import kernels as K
+    b, c, d, f = 4, 64, 128, 192
+    q, k, v, eta, alpha, w, s, ln_w, ln_b = make_chunk(b, c, d, f, seed=37)
+    v = v * torch.tensor([0.3, 1.0, 3.0, 10.0]).view(b, 1, 1)
+    mask = None
+    if masked:
+        mask = torch.ones(b, c)
+        mask[2, 30:] = 0
+    dev_in = to_dev(q, k, v, eta, alpha, *w, *s, ln_w, ln_b, mask)
+
+    def run(thr):
+        rl = torch.full((b, 2), float("nan"), device=DEV)
+        with torch.no_grad():
+            out = K.prepare_chunk_update(*dev_in[:13], dev_in[13], 0.9, 1.0, True, 1e-5, row_loss=rl,
+                                         min_row_surprise=thr).launch()
+        torch.cuda.synchronize()
+        return out, rl
+
+    plain, rl = run(0.0)
+    means = _kernel_row_means(rl)
+    for r in (1, 2):
+        thr = float(means[r])
+        for t in (thr, float(np.nextafter(np.float32(thr), np.float32(np.inf)))):
+            got, _ = run(t)
+            for i in range(b):
+                written = bool(means[i] >= np.float32(t))
+                if i == r:
+                    assert written == (t == thr)
+                for a, p, o in zip(got[1:7], plain[1:7], w + s):
+                    if written:
+                        assert torch.equal(a[i], p[i]), (r, t, i)
+                    else:
+                        assert torch.equal(a[i].cpu(), o[i]), (r, t, i)
+
+
+def test_chain_gate_is_inclusive_at_the_threshold():
+    """``uttt_chunk_chain`` (one layer, so the gate reads the chunk-start state): the same
+    boundary as the single update, at the chain's own row mean."""
+    import numpy as np
+    from test_gpu_chain import make_layers
+    from utttcompanion_amd import kernels as K
+    layers, w, s, ln_w, ln_b = make_layers(1, 4, 64, 128, 192, seed=39)
+    layers = [(x[0], x[1] * torch.tensor([0.3, 1.0, 3.0, 10.0]).view(4, 1, 1), x[2], x[3]) for x in layers]
+    k, v, eta, alpha = (t.to(DEV) for t in layers[0])
+
+    def run(thr):
+        state = [t.clone().to(DEV) for t in w + s]
+        rl = torch.full((1, 4, 2), float("nan"), device=DEV)
+        with torch.no_grad():
+            K.chunk_chain([k], [v], [eta], [alpha], state, ln_w.to(DEV), ln_b.to(DEV), None, 0.9, 1.0, True, 1e-5,
+                          row_loss=rl, min_row_surprise=thr)
+        torch.cuda.synchronize()
+        return state, rl
+
+    plain, rl = run(0.0)
+    means = _kernel_row_means(rl[0])
+    thr = float(means[2])
+    for t in (thr, float(np.nextafter(np.float32(thr), np.float32(np.inf)))):
+        got, _ = run(t)
+        for i in range(4):
+            written = bool(means[i] >= np.float32(t))
+            if i == 2:
+                assert written == (t == thr)
+            for a, p, o in zip(got, plain, w + s):
+                if written:
+                    assert torch.equal(a[i], p[i]), (t, i)
+                else:
+                    assert torch.equal(a[i].cpu(), o[i]), (t, i)
+
+
+def test_evolve_batched_turn_gate_at_a_real_surprise():
+    """The turn gate with real HIP surprises: the threshold is one request's surprise
+    exactly, so that request is not written (strict ``>``, personalizer.py:525) while the
+    requests above it are, each after the real elastic pull."""
+    from utttcompanion_amd import evolve
+    model, oracle = build()
+    ids, masks, states, _ = requests(model, oracle, seed=13)
+    dids, dmasks = [t.to(DEV) for t in ids], [m.to(DEV) for m in masks]
+    updates = evolve.ragged_test_time_update(model, dids, states, dmasks)
+    surprises = [u[1] for u in updates]
+    order = sorted(range(len(surprises)), key=surprises.__getitem__)
+    j = order[len(order) // 2]
+    threshold = surprises[j]
+    real = evolve.ragged_test_time_update
+    evolve.ragged_test_time_update = lambda *a, **kw: updates
+    try:
+        res = evolve.evolve_batched(model, dids, states, dmasks, surprise_threshold=threshold, anchor_lambda=0.05,
+                                    max_drift_ratio=None)
+    finally:
+        evolve.ragged_test_time_update = real
+    pool = model.fast_weight_pool
+    for i, r in enumerate(res):
+        assert r.gate_triggered == (surprises[i] > threshold), i
+        if r.gate_triggered:
+            want = pool.apply_elastic_pull(updates[i][0], 0.05, None)
+            for n in ("w_up", "w_gate", "w_down"):
+                assert torch.equal(getattr(r.state, n), getattr(want, n)), (i, n)
+        else:
+            assert r.state is states[i]
+    assert not res[j].gate_triggered and any(r.gate_triggered for r in res)

@@ -67,3 +67,21 @@ def test_c_abi_rejects_bad_greedy_and_skinny_calls(lib):
     s.m, s.n, s.k, s.act_dtype, s.x_eps = 4, 64, 64, N.DTYPE_BF16, -1.0
     assert lib.uttt_skinny_linear(C.byref(s), None) != 0
     assert b"x_eps" in lib.uttt_last_error()
+
+
+@pytest.mark.parametrize("shape", [(2, 1, 1), (2, 1), (1, 16, 1), (2, 15), (2, 16, 2)])
+def test_chunk_update_refuses_broadcast_eta_and_alpha(shape):
+    """The kernels read one eta / alpha per (row, token); shapes the reference would broadcast
+    are refused before any launch (the check runs ahead of the device check, so on the CPU)."""
+    b, c, d, f = 2, 16, 64, 64
+    q = torch.zeros(b, c, d)
+    w = (torch.zeros(b, d, f), torch.zeros(b, d, f), torch.zeros(b, f, d))
+    good = torch.zeros(b, c, 1)
+    for eta, alpha in ((torch.zeros(shape), good), (good, torch.zeros(shape))):
+        with pytest.raises(ValueError, match=r"must be \(2, 16\) or \(2, 16, 1\)"):
+            K.prepare_chunk_update(q, q, q, eta, alpha, *w, *w, torch.ones(d), torch.zeros(d), None, 0.9, 1.0,
+                                   True, 1e-5)
+    for ok in ((b, c), (b, c, 1)):  # accepted shapes get as far as the device check
+        with pytest.raises(ValueError, match="no CPU path"):
+            K.prepare_chunk_update(q, q, q, torch.zeros(ok), torch.zeros(ok), *w, *w, torch.ones(d),
+                                   torch.zeros(d), None, 0.9, 1.0, True, 1e-5)

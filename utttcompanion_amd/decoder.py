@@ -72,6 +72,7 @@ class BatchedDecoder:
         self._ws_attn = torch.zeros(1, dtype=torch.uint8, device=dev)
         self._ws_read = torch.zeros(1, dtype=torch.uint8, device=dev)
         self._states = list(states)
+        self._key = self._state_key(states)
         self._folds = {}
         d_model = model.config.d_model
         self._fused_readout = self.dtype == torch.bfloat16 and d_model <= 2048 and all(
@@ -91,16 +92,59 @@ class BatchedDecoder:
             if ids.shape[1] == 0:
                 raise ValueError("prompts must be non-empty")
             out = self.model(ids, fast_state=st, update_fast_weights=False, logits_to_keep=1)
-            length = ids.shape[1]
-            for (kr, vr), (k, v) in zip(self.rings, out.kv_caches):
-                cached = k.shape[2]
-                slots = torch.arange(length - cached, length, device=self.device) % self.window
-                kr[i].index_copy_(1, slots, k[0])
-                vr[i].index_copy_(1, slots, v[0])
-            self.host_positions[i] = length
+            self._load_request(i, out.kv_caches, ids.shape[1])
             out_logits.append(out.logits[:, -1, :])
         self.positions.copy_(torch.tensor(self.host_positions, dtype=torch.int64))
         return torch.cat(out_logits, dim=0)
+
+    def _load_request(self, i: int, kv_caches, length: int) -> None:
+        """Request i's ring slots from a frozen prefill's per-layer caches (the last <= window
+        rotated keys / values of ``length`` tokens): token p goes to slot p mod window."""
+        if len(kv_caches) != len(self.rings):
+            raise ValueError(f"expected {len(self.rings)} layer caches, got {len(kv_caches)}")
+        for (kr, vr), (k, v) in zip(self.rings, kv_caches):
+            cached = k.shape[2]
+            if (k.shape != (1, self.hkv, cached, self.hd) or v.shape != k.shape or cached > min(length, self.window)
+                    or cached < min(length, self.window - 1)):
+                raise ValueError("a cache must be (1, n_kv_heads, min(length, window) or window - 1, head_dim)")
+            slots = torch.arange(length - cached, length, device=self.device) % self.window
+            kr[i].index_copy_(1, slots, k[0].to(device=self.device, dtype=kr.dtype))
+            vr[i].index_copy_(1, slots, v[0].to(device=self.device, dtype=vr.dtype))
+        self.host_positions[i] = int(length)
+
+    @torch.no_grad()
+    def reset(self, kv_caches_per_request: Sequence, lengths: Sequence[int]) -> None:
+        """Start again from other prompts' frozen-prefill caches (same requests and states):
+        the rings, positions and buffers keep their addresses, so a captured step stays valid."""
+        if len(kv_caches_per_request) != self.n or len(lengths) != self.n:
+            raise ValueError(f"expected caches and lengths for {self.n} requests")
+        for kr, vr in self.rings:
+            kr.zero_()
+            vr.zero_()
+        for i, (caches, length) in enumerate(zip(kv_caches_per_request, lengths)):
+            if length < 1:
+                raise ValueError("a request needs at least one prompt token")
+            self._load_request(i, caches, int(length))
+        self.positions.copy_(torch.tensor(self.host_positions, dtype=torch.int64))
+
+    @torch.no_grad()
+    def export_kv_caches(self, i: int = 0) -> List:
+        """Request i's per-layer caches in the eager layout (the last min(position, window)
+        rotated keys / values in token order), e.g. to continue a decode eagerly."""
+        pos = self.host_positions[i]
+        kept = min(pos, self.window)
+        slots = torch.arange(pos - kept, pos, device=self.device) % self.window
+        return [(kr[i:i + 1].index_select(2, slots), vr[i:i + 1].index_select(2, slots)) for kr, vr in self.rings]
+
+    def matches(self, model: uTTTModel, states: Sequence[FastWeightState]) -> bool:
+        """Whether this decoder's read copies and LayerNorm pair still stand for ``states`` of
+        ``model`` (same tensors, unchanged versions), so it can be ``reset`` and reused."""
+        return model is self.model and len(states) == self.n and self._state_key(states) == self._key
+
+    @staticmethod
+    def _state_key(states: Sequence[FastWeightState]) -> tuple:
+        return tuple((t.data_ptr(), t._version, t.dtype) for st in states
+                     for t in (st.w_up, st.w_gate, st.w_down, st.ln_weight, st.ln_bias))
 
     # ------------------------------------------------------------------ one step
     def _folded(self, weight: Tensor, norm) -> Tensor:

@@ -31,7 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from . import kernels as K
-from .layer import FastWeightState, linear_residual
+from .layer import FastWeightState, linear_residual, require_write_chunk
 from .model import PAD_ID, uTTTModel
 
 Tensor = torch.Tensor
@@ -75,6 +75,7 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
     cfg = model.config
     if cfg.write_schedule != "sequential":
         raise ValueError("Only the causal sequential write schedule is implemented")
+    require_write_chunk(cfg.chunk_size)
     if model.training and torch.is_grad_enabled():
         raise ValueError("the HIP update path is inference-only; call eval() / torch.no_grad()")
     n = len(interactions)

@@ -72,6 +72,13 @@ def _row_vector(x: Tensor, act: torch.dtype) -> Tensor:
     return x
 
 
+def _check_per_token(x: Tensor, bsz: int, tokens: int, name: str) -> None:
+    """eta / alpha must hold one value per (row, token): (B, C) or (B, C, 1).  The kernels
+    read C entries per row, so a broadcastable (B, 1, 1) or (B, 1) is refused, not read past."""
+    if tuple(x.shape) not in ((bsz, tokens), (bsz, tokens, 1)):
+        raise ValueError(f"{name} must be ({bsz}, {tokens}) or ({bsz}, {tokens}, 1), got {tuple(x.shape)}")
+
+
 def _state(t: Tensor, name: str) -> Tensor:
     if t.dtype == torch.float64:
         raise ValueError(f"{name}: float64 fast-weight state is not supported by the HIP path")
@@ -158,6 +165,8 @@ def prepare_chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
             raise ValueError("momentum buffers must match the weight shapes")
     if dim % 64 or ff % 64 or dim > 4096:
         raise ValueError(f"d_model and d_ff must be multiples of 64 (d_model <= 4096); got {dim}, {ff}")
+    _check_per_token(eta, bsz, tokens, "eta")
+    _check_per_token(alpha, bsz, tokens, "alpha")
     _require_device(dev, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias,
                     token_mask, read_w_up, read_w_gate, read_w_down)
     _forward_only(q, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias)
@@ -409,12 +418,12 @@ class ChunkChainRun(PreparedChain):
         act = self._act
         if k.shape != (bsz, tokens, dim) or v.shape != k.shape or k.dtype != act or v.dtype != act:
             raise ValueError(f"layer {l}: k/v must be ({bsz}, {tokens}, {dim}) {act}")
+        _check_per_token(eta, bsz, tokens, f"layer {l}: eta")
+        _check_per_token(alpha, bsz, tokens, f"layer {l}: alpha")
         _require_device(self.device, k, v, eta, alpha)
         _forward_only(k, v, eta, alpha)
         k, v = _rows(k), _rows(v)
         e, al = _row_vector(eta, act), _row_vector(alpha, act)
-        if e.shape != (bsz, tokens) or al.shape != (bsz, tokens):
-            raise ValueError(f"layer {l}: eta/alpha must be ({bsz}, {tokens}) or ({bsz}, {tokens}, 1)")
         a = self.args
         if l == 0:
             a.kv_row_stride, a.ea_row_stride = k.stride(0), e.stride(0)

@@ -27,6 +27,20 @@ from . import kernels as K
 Tensor = torch.Tensor
 _STATE_NAMES = ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")
 
+# Longest chunk the write kernels take: one 64-token tile per chunk and layer.  Frozen reads
+# (update_fast_weights=False, decoding) do not chunk and take any chunk_size.
+MAX_WRITE_CHUNK = 64
+
+
+def require_write_chunk(chunk_size: int) -> None:
+    """Refuse a fast-weight write with chunks the kernels do not take, before any work.  The
+    reference's shipped configs use chunk_size 128 or 512; splitting such a chunk into 64-token
+    pieces would change how many writes happen, so it is not done silently."""
+    if not 1 <= int(chunk_size) <= MAX_WRITE_CHUNK:
+        raise ValueError(f"chunk_size={chunk_size}: fast-weight writes on the HIP path take chunks of 1.."
+                         f"{MAX_WRITE_CHUNK} tokens; frozen reads (update_fast_weights=False, decoding) take "
+                         f"any chunk_size")
+
 
 # ==============================================================================
 # Fast-weight state (reference model/uttt_layer.py:59-205)
@@ -51,6 +65,13 @@ class FastWeightState:
     last_surprise_loss: float = 0.0
     surprise_history: List[float] = field(default_factory=list)
     _shared_readonly: bool = field(default=False, repr=False)
+    # versioned activation-dtype read copies (SharedFastWeightPool.inference_read_weights and
+    # the fused inference readout); disposable, never part of a persona payload
+    _packed_up_gate: Optional[Tensor] = field(default=None, repr=False)
+    _read_w_down: Optional[Tensor] = field(default=None, repr=False)
+    _packed_key: Optional[tuple] = field(default=None, repr=False)
+    _read_copies: Optional[Tuple[Tensor, Tensor, Tensor]] = field(default=None, repr=False)
+    _read_key: Optional[tuple] = field(default=None, repr=False)
 
     def tensors(self) -> Tuple[Tensor, ...]:
         return tuple(getattr(self, n) for n in _STATE_NAMES)
@@ -136,6 +157,9 @@ class SharedFastWeightPool(nn.Module):
     def __init__(self, d_model: int, d_ff: int, momentum_beta: float = 0.90, max_inner_grad_norm: float = 1.0,
                  normalize_loss_by_dim: bool = False, rms_norm_eps: float = 1e-5) -> None:
         super().__init__()
+        # set by uTTTModel.prepare_for_inference: frozen readouts read versioned
+        # activation-dtype copies of W instead of the fp32 masters (reference :677-689)
+        self.fused_inference_readout = False
         self.d_model = d_model
         self.d_ff = d_ff
         self.momentum_beta = momentum_beta
@@ -172,11 +196,51 @@ class SharedFastWeightPool(nn.Module):
         return FastWeightState(up, gate, down, zero.expand_as(up), zero.expand_as(gate), zero.expand_as(down),
                                view(self.ln_weight), view(self.ln_bias), _shared_readonly=True)
 
+    @staticmethod
+    def _read_key(state: FastWeightState, dtype: torch.dtype, device) -> tuple:
+        weights = (state.w_up, state.w_gate, state.w_down)
+        if torch.is_grad_enabled() or any(t.is_inference() for t in weights):
+            raise ValueError("Inference read caches require no-grad, version-tracked weights")
+        return (dtype, torch.device(device), tuple((id(t), t.data_ptr(), t._version, t.device, t.dtype,
+                                                    tuple(t.shape)) for t in weights))
+
+    def inference_read_weights(self, state: FastWeightState, dtype: torch.dtype,
+                               device) -> Tuple[Tensor, Tensor]:
+        """Versioned read copies in the reference's packed layout (reference :648-668):
+        ``(cat(W_up, W_gate) (B, D, 2F), W_down (B, F, D))`` in ``dtype`` on ``device``, rebuilt
+        when any master's storage, version, dtype or shape changes.  Read-only for the caller;
+        needs no-grad mode and version-tracked (non-inference) tensors, like the reference."""
+        key = self._read_key(state, dtype, device)
+        if state._packed_up_gate is None or state._read_w_down is None or state._packed_key != key:
+            state._packed_up_gate = torch.cat((state.w_up.to(device=device, dtype=dtype),
+                                               state.w_gate.to(device=device, dtype=dtype)), dim=-1)
+            state._read_w_down = state.w_down.to(device=device, dtype=dtype)
+            state._packed_key = key
+        return state._packed_up_gate, state._read_w_down
+
+    def inference_read_copies(self, state: FastWeightState, dtype: torch.dtype,
+                              device) -> Tuple[Tensor, Tensor, Tensor]:
+        """The same versioned copies in the layout ``uttt_swiglu_readout`` reads:
+        ``(W_up (B, D, F), W_gate (B, D, F), W_down (B, F, D))``, contiguous, in ``dtype``."""
+        key = self._read_key(state, dtype, device)
+        if state._read_copies is None or state._read_key != key:
+            state._read_copies = tuple(t.to(device=device, dtype=dtype).contiguous()
+                                       for t in (state.w_up, state.w_gate, state.w_down))
+            state._read_key = key
+        return state._read_copies
+
     def forward_readout(self, x: Tensor, state: FastWeightState) -> Tensor:
-        """Frozen readout f_W(x) (reference :670-695); shared W_0 views are read once per launch."""
+        """Frozen readout f_W(x) (reference :670-695); shared W_0 views are read once per launch.
+        With ``fused_inference_readout`` (eval, no grad, 16-bit activations) the readout reads
+        the state's versioned activation-dtype copies: the same operands (the reference casts W
+        to x's dtype for these products) at half the bytes of the fp32 masters."""
         state = state.ensure_batch_size(x.shape[0])
-        return K.swiglu_readout(x, state.w_up, state.w_gate, state.w_down, state.ln_weight, state.ln_bias,
-                                self.eps)
+        weights = (state.w_up, state.w_gate, state.w_down)
+        if (self.fused_inference_readout and not self.training and not torch.is_grad_enabled()
+                and x.dtype != torch.float32 and not state._shared_readonly
+                and not any(t.is_inference() for t in weights)):
+            weights = self.inference_read_copies(state, x.dtype, x.device)
+        return K.swiglu_readout(x, *weights, state.ln_weight, state.ln_bias, self.eps)
 
     def chunk_step(self, state: FastWeightState, q_chunk: Tensor, k_chunk: Tensor, v_chunk: Tensor,
                    eta_chunk: Tensor, alpha_chunk: Tensor, token_mask: Optional[Tensor] = None,
@@ -317,23 +381,51 @@ class SlidingWindowAttention(nn.Module):
         self.wv = nn.Linear(d_model, n_kv_heads * self.head_dim, bias=False)
         self.wo = nn.Linear(n_heads * self.head_dim, d_model, bias=False)
         self.rope = RotaryEmbedding(self.head_dim, max_seq_len=max_seq_len, theta=rope_theta)
-        self._pack: Optional[Tensor] = None
-        self._pack_key = None
+        # [wq; wk; wv] as one weight, outside the checkpoint keys (reference :1000-1001)
+        self.register_buffer("_packed_qkv", None, persistent=False)
+        self._packed_qkv_key = None
+
+    def _projection_key(self):
+        """Identity of the three projection weights; None for inference tensors (no version)."""
+        ws = (self.wq.weight, self.wk.weight, self.wv.weight)
+        if any(t.is_inference() for t in ws):
+            return None
+        return tuple((id(t), t.data_ptr(), t._version, t.device, t.dtype) for t in ws)
+
+    @torch.no_grad()
+    def prepare_for_inference(self) -> None:
+        """Build (or refresh) ``_packed_qkv`` (reference :1008-1018)."""
+        key = self._projection_key()
+        if key is None:
+            self._packed_qkv = None
+            self._packed_qkv_key = None
+            return
+        if self._packed_qkv is None or key != self._packed_qkv_key:
+            self._packed_qkv = torch.cat([t.detach() for t in (self.wq.weight, self.wk.weight, self.wv.weight)],
+                                         dim=0)
+            self._packed_qkv_key = key
+
+    def train(self, mode: bool = True):
+        if mode:  # reference :1020-1024: packs are dropped when training resumes
+            self._packed_qkv = None
+            self._packed_qkv_key = None
+        return super().train(mode)
 
     def packed_qkv(self) -> Tensor:
-        """[wq; wk; wv] as one (H + 2 Hkv) hd x D weight, rebuilt when any weight changes."""
-        ws = (self.wq.weight, self.wk.weight, self.wv.weight)
-        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in ws)
-        if self._pack is None or self._pack_key != key:
-            self._pack = torch.cat([t.detach() for t in ws], dim=0)
-            self._pack_key = key
-        return self._pack
+        """[wq; wk; wv] as one (H + 2 Hkv) hd x D weight (``_packed_qkv``), rebuilt when any
+        weight changes."""
+        key = self._projection_key()
+        if key is None:
+            return torch.cat([t.detach() for t in (self.wq.weight, self.wk.weight, self.wv.weight)], dim=0)
+        if self._packed_qkv is None or self._packed_qkv_key != key:
+            self.prepare_for_inference()
+        return self._packed_qkv
 
     def packed_qkv_folded(self, norm: "RMSNorm") -> Tensor:
         """The packed QKV weight with an input RMSNorm's weight folded into its columns
         (W diag(g), formed in fp32 and rounded once), rebuilt when any of them changes."""
         w = self.packed_qkv()
-        key = (self._pack_key, norm.weight.data_ptr(), norm.weight._version, norm.weight.dtype)
+        key = (self._packed_qkv_key, norm.weight.data_ptr(), norm.weight._version, norm.weight.dtype)
         if getattr(self, "_fold_key", None) != key:
             self._fold = (w.float() * norm.weight.detach().float()[None, :]).to(w.dtype)
             self._fold_key = key
@@ -489,6 +581,7 @@ class uTTTLayer(nn.Module):
             q = fused_fast_q_proj(x, self.w_q.weight, self.q_norm.weight, self.q_norm.eps)
             readout = fast_pool.forward_readout(q, fast_state.ensure_batch_size(bsz))
             return self.w_o(readout), fast_state, x.new_zeros((), dtype=torch.float32)
+        require_write_chunk(self.chunk_size)
         q, k, v, eta, alpha = self.projections(x)
         cur = fast_state.ensure_batch_size(bsz)
         outs, losses = [], []

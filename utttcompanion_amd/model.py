@@ -28,7 +28,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import kernels as K
-from .layer import FastWeightState, RMSNorm, SharedFastWeightPool, linear_residual, uTTTBlock
+from .layer import FastWeightState, RMSNorm, SharedFastWeightPool, linear_residual, require_write_chunk, uTTTBlock
 
 Tensor = torch.Tensor
 _NAMES = ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")
@@ -176,6 +176,28 @@ class uTTTModel(nn.Module):
         for p in self.parameters():
             p.requires_grad_(False)
 
+    def prepare_for_inference(self, enabled: bool = True) -> None:
+        """Build (or drop) the disposable inference packs without changing checkpoint keys
+        (reference uttt_model.py:401-422): each attention's ``_packed_qkv`` and the pool's
+        ``fused_inference_readout`` switch (frozen readouts through versioned activation-dtype
+        copies of W).  A change drops the cached decode graph."""
+        if type(enabled) is not bool:
+            raise ValueError("Inference projection packing must be boolean")
+        if self.training:
+            raise ValueError("Call eval() before preparing inference projections")
+        changed = bool(getattr(self.fast_weight_pool, "fused_inference_readout", False)) != enabled
+        for block in self.layers:
+            previous = block.attn._packed_qkv
+            if enabled:
+                block.attn.prepare_for_inference()
+            else:
+                block.attn._packed_qkv = None
+                block.attn._packed_qkv_key = None
+            changed = changed or previous is not block.attn._packed_qkv
+        self.fast_weight_pool.fused_inference_readout = enabled
+        if changed:
+            self._cuda_graph_decoder = None
+
     def init_fast_state(self, batch_size: int = 1, device=None, dtype=None, detach: bool = False) -> FastWeightState:
         return self.fast_weight_pool.init_state(batch_size=batch_size, device=device, dtype=dtype, detach=detach)
 
@@ -203,6 +225,7 @@ class uTTTModel(nn.Module):
         if cfg.write_schedule != "sequential":
             raise ValueError("Only the causal sequential write schedule is implemented; aggregated writes must "
                              "not be silently treated as sequential")
+        require_write_chunk(cfg.chunk_size)
         bsz, seq = input_ids.shape
         dev = input_ids.device
         h = F.embedding(input_ids, self.tok_embeddings.weight)
@@ -443,24 +466,62 @@ class uTTTModel(nn.Module):
             return si.gather(-1, torch.multinomial(sp, 1, generator=generator)).squeeze(-1)
         return torch.multinomial(probs, 1, generator=generator).squeeze(-1)
 
+    def _graph_decoder_for(self, fast_state: FastWeightState, caches, pos: int):
+        """A one-request ``BatchedDecoder`` holding the prompt's caches, with its step captured in
+        a HIP graph; reused while the model and the state's W are unchanged (the reference keeps
+        its ``CUDAGraphDecoder`` the same way, uttt_model.py:1138-1152).  None (eager decoding)
+        where the decode kernels do not take the model or state."""
+        from .decoder import BatchedDecoder
+        dev = self.tok_embeddings.weight.device
+        if (dev.type != "cuda" or torch.is_inference_mode_enabled() or pos < 1
+                or fast_state.w_up.shape[0] != 1 or fast_state._shared_readonly):
+            return None
+        cached = getattr(self, "_cuda_graph_decoder", None)
+        try:
+            if cached is not None and cached.matches(self, [fast_state]):
+                cached.reset([caches], [pos])
+                return cached
+            self._cuda_graph_decoder = None  # release the previous state's graph first
+            dec = BatchedDecoder(self, [fast_state])
+            dec.reset([caches], [pos])
+            dec.capture()
+            self._cuda_graph_decoder = dec
+            return dec
+        except (RuntimeError, ValueError) as error:
+            import warnings
+            self._cuda_graph_decoder = None
+            warnings.warn(f"HIP graph decode unavailable; using standard decode ({error})")
+            return None
+
     @torch.no_grad()
     def stream_generate(self, input_ids: Tensor, fast_state: FastWeightState, max_new_tokens: int = 128,
                         temperature: float = 0.7, top_p: float = 0.9, eos_token_id: Optional[int] = EOS_ID,
-                        generator: Optional[torch.Generator] = None, **unused: Any) -> Iterator[int]:
-        """Frozen-state streaming generation for one prompt (reference uttt_model.py:966-1179,
-        without the experimental self-speculative branch)."""
+                        speculative_draft_k: Optional[int] = None, dspark_conf_threshold: Optional[float] = None,
+                        use_cuda_graph: bool = False,
+                        generator: Optional[torch.Generator] = None) -> Iterator[int]:
+        """Frozen-state streaming generation for one prompt (reference uttt_model.py:966-1179).
+
+        ``use_cuda_graph`` decodes through a one-request ring-buffer ``BatchedDecoder`` whose
+        step is replayed from a HIP graph (falling back to eager steps where it does not apply,
+        or, with the exact KV history, when a step is refused).  The experimental
+        self-speculative branch is not part of this path: a positive draft length is refused."""
         if max_new_tokens < 0:
             raise ValueError("max_new_tokens must be nonnegative")
         if max_new_tokens == 0:
             return
         if input_ids.ndim != 2 or input_ids.shape[0] != 1 or input_ids.shape[1] == 0:
             raise ValueError("Streaming generation requires one non-empty prompt")
+        draft_k = (speculative_draft_k if speculative_draft_k is not None
+                   else int(getattr(self.config, "dspark_speculative_k", 0)))
+        if draft_k > 0:
+            raise ValueError("self-speculative decoding is not part of the HIP path; use speculative_draft_k=0")
         was = self.training
         self.eval()
         try:
             out = self.forward(input_ids, fast_state=fast_state, update_fast_weights=False, logits_to_keep=1)
             caches, logits = out.kv_caches, out.logits[:, -1, :]
             pos, recent = input_ids.shape[1], []
+            graph, tried = None, False
             while len(recent) < max_new_tokens:
                 tok = self._sample_next_token(logits, temperature, top_p, recent, self.config.repetition_penalty,
                                               self.active_vocab_limit, generator)
@@ -471,6 +532,18 @@ class uTTTModel(nn.Module):
                 yield tid
                 if (eos_token_id is not None and tid == eos_token_id) or len(recent) >= max_new_tokens:
                     break
+                if use_cuda_graph and not tried:  # after the first token, as the reference does
+                    tried = True
+                    graph = self._graph_decoder_for(fast_state, caches, pos)
+                if graph is not None:
+                    try:
+                        logits = graph.step(tok.view(1).to(graph.device))
+                        pos += 1
+                        continue
+                    except ValueError:  # e.g. the RoPE table's end: continue eagerly from the ring
+                        caches = graph.export_kv_caches(0)
+                        graph = None
+                        self._cuda_graph_decoder = None
                 step = self.forward(tok.view(1, 1), fast_state=fast_state, kv_caches=caches, start_pos=pos,
                                     update_fast_weights=False)
                 caches, logits = step.kv_caches, step.logits[:, -1, :]
