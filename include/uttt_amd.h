@@ -29,9 +29,13 @@ typedef void* uttt_stream_t; /* a hipStream_t; NULL = the default stream */
 enum { UTTT_DTYPE_F32 = 0, UTTT_DTYPE_BF16 = 1 };
 enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE = 3 };
 
+/* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
+ * Python binding reads it from this header and refuses a library built from another one. */
+#define UTTT_ABI_VERSION 14
+
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
-/* ABI version of the structures below; the Python binding checks it. */
+/* UTTT_ABI_VERSION of the header the library was built from. */
 int uttt_abi_version(void);
 
 /* ---------------------------------------------------------------------------

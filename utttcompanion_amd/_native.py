@@ -9,9 +9,20 @@ import ctypes as C
 import os
 import threading
 
-from .build import LIB_PATH
+from .build import HEADER_PATH, LIB_PATH
 
-ABI_VERSION = 13
+
+def _header_abi_version(path: str = HEADER_PATH) -> int:
+    """UTTT_ABI_VERSION as include/uttt_amd.h defines it (the library is built from that header)."""
+    import re
+    with open(path, "r", encoding="utf-8") as fh:
+        m = re.search(r"^#define UTTT_ABI_VERSION (\d+)$", fh.read(), re.M)
+    if m is None:
+        raise RuntimeError(f"{path} defines no UTTT_ABI_VERSION")
+    return int(m.group(1))
+
+
+ABI_VERSION = _header_abi_version()
 MAX_CHAIN = 64
 DTYPE_F32 = 0
 DTYPE_BF16 = 1

@@ -17,6 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libuttt_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
+HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "uttt_amd.h")
 ARCH = os.environ.get("UTTT_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -41,7 +42,7 @@ def build(verbose: bool = False) -> str:
     """Compile all kernels into LIB_PATH (atomically replaced).  Returns the path."""
     fd, tmp = tempfile.mkstemp(prefix=LIB_NAME + ".", suffix=".tmp", dir=HERE)
     os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(os.path.dirname(HERE), "include"), *sources(), "-o", tmp]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.dirname(HEADER_PATH), *sources(), "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

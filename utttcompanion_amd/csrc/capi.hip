@@ -9,4 +9,4 @@ char* last_error_buffer() {
 }  // namespace uttt
 
 extern "C" const char* uttt_last_error(void) { return uttt::last_error_buffer(); }
-extern "C" int uttt_abi_version(void) { return 13; }
+extern "C" int uttt_abi_version(void) { return UTTT_ABI_VERSION; }
