@@ -5,7 +5,8 @@
  * Nothing here allocates or frees device memory and no call synchronises the
  * stream; every call only enqueues kernels on the stream it is given, so calls
  * are stream-ordered and safe to record into a HIP graph.  Buffers (including
- * workspace) belong to the caller.  Every entry point returns UTTT_OK (0) or an
+ * workspace) belong to the caller; the one exception is the device-resident scratch
+ * array of uttt_chunk_update_noalloc.  Every entry point returns UTTT_OK (0) or an
  * error code; uttt_last_error() then describes the failure (per host thread).
  *
  * Shapes follow the reference PyTorch modules of Phova/uTTTCompanion
@@ -90,6 +91,18 @@ int uttt_chunk_update(const uttt_chunk_update_args* args, void* workspace, size_
 #define UTTT_UPDATE_PHASES 5
 int uttt_chunk_update_phase(const uttt_chunk_update_args* args, void* workspace, size_t workspace_bytes,
                             int32_t phase, uttt_stream_t stream);
+
+/* The same update with no workspace argument and no device allocation.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The workspace is a
+ * device-resident array of UTTT_NOALLOC_SCRATCH_BYTES inside the library (each GPU the library
+ * runs on holds its own copy until the process ends); shapes whose workspace
+ * (uttt_chunk_update_workspace) exceeds it are refused with UTTT_ERR_INVALID.  The stream's device
+ * must be the current device.  Every call on one GPU uses that GPU's array, so calls that overlap
+ * on one GPU (other streams, other host threads) race: order them.  Results equal
+ * uttt_chunk_update's. */
+#define UTTT_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int uttt_chunk_update_noalloc(const uttt_chunk_update_args* args, uttt_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * 1b. One chunk's updates for all L layers of the chunk-first shared schedule.

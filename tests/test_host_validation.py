@@ -85,3 +85,16 @@ def test_chunk_update_refuses_broadcast_eta_and_alpha(shape):
         with pytest.raises(ValueError, match="no CPU path"):
             K.prepare_chunk_update(q, q, q, torch.zeros(ok), torch.zeros(ok), *w, *w, torch.ones(d),
                                    torch.zeros(d), None, 0.9, 1.0, True, 1e-5)
+
+
+def test_noalloc_update_refuses_shapes_past_its_scratch(lib):
+    """``uttt_chunk_update_noalloc`` checks the shape's workspace against its fixed scratch before
+    any device call: config 5's 16 rows at D 2048 / F 5504 need about 106 MiB."""
+    a = N.ChunkUpdateArgs()
+    a.batch, a.tokens, a.d_model, a.d_ff, a.act_dtype = 16, 64, 2048, 5504, N.DTYPE_BF16
+    need = lib.uttt_chunk_update_workspace(16, 2048, 5504, N.DTYPE_BF16)
+    assert need > (64 << 20)
+    assert lib.uttt_chunk_update_noalloc(C.byref(a), None) == 1  # UTTT_ERR_INVALID
+    msg = lib.uttt_last_error()
+    assert b"device-resident scratch" in msg and str(need).encode() in msg
+    assert lib.uttt_chunk_update_noalloc(None, None) == 1

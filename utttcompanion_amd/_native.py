@@ -180,6 +180,7 @@ SIGNATURES = {
     "uttt_chunk_update_workspace": (C.c_size_t, [_I64, _I64, _I64, _I32]),
     "uttt_chunk_update": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_update_phase": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _I32, _P]),
+    "uttt_chunk_update_noalloc": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P]),
     "uttt_chunk_chain_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_chunk_chain": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_chain_stage": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _P]),

@@ -21,6 +21,7 @@
 //                     clip / momentum / decay / inactive-row select to W and S in one pass
 // Steps 1, 2 and 4 alone are the frozen readout.
 #include <algorithm>
+#include <mutex>
 
 #include "update_ln.h"
 #include "uttt_device.h"
@@ -1169,6 +1170,66 @@ extern "C" int uttt_chunk_update_phase(const uttt_chunk_update_args* a, void* wo
                                        int32_t phase, uttt_stream_t stream) {
   UTTT_REQUIRE(phase >= 0 && phase < UTTT_UPDATE_PHASES, "phase must be in [0, %d)", UTTT_UPDATE_PHASES);
   return run_update(a, workspace, workspace_bytes, stream, phase, phase);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The same update without a caller workspace, for callers that cannot allocate device memory.
+// Its workspace is `scratch`, a device-resident array of the library (each GPU holds its own copy
+// while the process lives).  In host code the array's name is only a stand-in: its device address
+// comes from hipGetSymbolAddress, fetched once per device with that device current and kept in
+// scratch_device_ptr.  Nothing in the update's workspace needs to start at zero (every phase writes
+// what a later phase reads), so the array is not cleared; calls on one GPU share it and must not
+// overlap.
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+static_assert(UTTT_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size must keep 256-byte alignment");
+__device__ __align__(256) unsigned char scratch[UTTT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_device_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the calling thread's current device, which must be the
+// stream's device.
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(UTTT_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return fail(UTTT_ERR_HIP, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    UTTT_REQUIRE(sdev == dev, "the stream's device (%d) must be the current device (%d)", sdev, dev);
+  }
+  UTTT_REQUIRE(dev >= 0 && dev < kMaxDevices, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_device_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(UTTT_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    scratch_device_ptr[dev] = p;
+  }
+  *out = scratch_device_ptr[dev];
+  return UTTT_OK;
+}
+
+}  // namespace
+
+extern "C" int uttt_chunk_update_noalloc(const uttt_chunk_update_args* a, uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  const int rc = check_dims(a->batch, a->d_model, a->d_ff, a->act_dtype);
+  if (rc != UTTT_OK) return rc;
+  const size_t need = update_layout(a->batch, a->d_model, a->d_ff, a->act_dtype).total;
+  UTTT_REQUIRE(need <= UTTT_NOALLOC_SCRATCH_BYTES,
+               "uttt_chunk_update_noalloc: this shape needs %zu bytes of workspace, more than the %llu-byte "
+               "device-resident scratch; use uttt_chunk_update with a workspace",
+               need, (unsigned long long)UTTT_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int src = scratch_address(static_cast<hipStream_t>(stream), &ws);
+  if (src != UTTT_OK) return src;
+  return run_update(a, ws, UTTT_NOALLOC_SCRATCH_BYTES, stream, 0, UTTT_UPDATE_PHASES - 1);
 }
 
 extern "C" size_t uttt_readout_workspace(int64_t batch, int64_t tokens, int64_t d_model, int64_t d_ff, int32_t act_dtype) {

@@ -131,6 +131,15 @@ class PreparedUpdate:
         N.check(rc, "uttt_chunk_update")
         return self.result
 
+    def launch_noalloc(self) -> Tuple[Tensor, ...]:
+        """Enqueue the whole update through ``uttt_chunk_update_noalloc`` (the library's
+        device-resident scratch instead of ``workspace``; calls on one GPU must not overlap)."""
+        lib = N.load_library()
+        with torch.cuda.device(self.device):
+            rc = lib.uttt_chunk_update_noalloc(C.byref(self.args), _stream(self.device))
+        N.check(rc, "uttt_chunk_update_noalloc")
+        return self.result
+
 
 def prepare_chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
                          w_up: Tensor, w_gate: Tensor, w_down: Tensor,
