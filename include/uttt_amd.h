@@ -32,7 +32,7 @@ enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE =
 
 /* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
  * Python binding reads it from this header and refuses a library built from another one. */
-#define UTTT_ABI_VERSION 14
+#define UTTT_ABI_VERSION 15
 
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
@@ -171,6 +171,16 @@ int uttt_chunk_chain_stage(const uttt_chunk_chain_args* args, void* workspace, s
  * w_products_given, part 2 of stage l must follow the caller's writes of layer l's products. */
 int uttt_chunk_chain_stage_part(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
                                 int32_t stage, int32_t part, uttt_stream_t stream);
+/* Some of the launches of a stage part (part 0: the whole stage), e.g. to time single kernels with
+ * events between them: the launches a part makes are numbered 0, 1, ... in enqueue order, and the
+ * call enqueues those numbered in [launch_begin, launch_end) (none when launch_end <=
+ * launch_begin); enqueueing consecutive ranges in order on one stream equals
+ * uttt_chunk_chain_stage_part.  *count (if not NULL) receives the number of launches of the part
+ * and names[i] (i < names_cap) the kernel name of launch i (static strings).  A range past the
+ * count is an error. */
+int uttt_chunk_chain_stage_launch(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
+                                  int32_t stage, int32_t part, int32_t launch_begin, int32_t launch_end,
+                                  const char** names, int32_t names_cap, int32_t* count, uttt_stream_t stream);
 /* Byte offsets in the chain workspace of layer `layer`'s k W_up and k W_gate products
  * ((batch, 64, d_ff) in the activation dtype, row stride 64 * d_ff). */
 int uttt_chunk_chain_w_products(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff, int32_t act_dtype,

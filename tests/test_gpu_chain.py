@@ -304,3 +304,39 @@ def test_chain_bf16_tail_chunks_within_tolerance(case):
     if case["mask"]:
         for a, o in zip(got, w + s):
             assert torch.equal(a[case["b"] - 1].cpu(), o[case["b"] - 1]), "a row without tokens changed"
+
+
+def test_single_launches_with_timer_equal_whole_stages():
+    """``uttt_chunk_chain_stage_launch``: a stage enqueued launch by launch (with events around
+    the followed kernels) equals the stage enqueued at once, bit for bit; the names follow the
+    launch sequence and every followed launch is timed."""
+    from utttcompanion_amd import kernels as K
+    layers, w, s, ln_w, ln_b = make_layers(4, 3, 64, 256, 384, seed=29, w_scale=0.05)
+    run_a, state_a, cps_a = _chain_run(layers, w, s, ln_w, ln_b, shared=False)
+    run_b, state_b, cps_b = _chain_run(layers, w, s, ln_w, ln_b, shared=False)
+    timer = K.KernelTimer(("k_chain_back_lds", "k_chain_apply_lds", "k_chain_gram_lds"))
+    with torch.no_grad():
+        for layer in layers:
+            run_a.add_layer(*_layer_inputs(layer))
+        sa, _ = run_a.finish()
+        for l, layer in enumerate(layers):
+            run_b.set_layer(*_layer_inputs(layer))
+            names = run_b.stage_launches(l)
+            assert names[-1] == "k_chain_back_lds" and "k_chain_up_lds" in names
+            run_b.launch(l, timer=timer)
+        assert run_b.stage_launches(4) == ("k_chain_coef", "k_chain_apply_lds")
+        sb, _ = run_b.launch(4, timer=timer)
+    torch.cuda.synchronize()
+    for name, a, b_ in zip(NAMES, state_a, state_b):
+        assert torch.equal(a, b_), name
+    assert torch.equal(sa, sb)
+    summary = timer.summary()
+    assert summary["k_chain_back_lds"]["launches"] == 4 and summary["k_chain_apply_lds"]["launches"] == 1
+    assert summary["k_chain_gram_lds"]["launches"] == 12  # key Gram, H Gram and dZ Gram per layer
+    assert all(v["mean_ms"] > 0 for v in summary.values())
+    with pytest.raises(RuntimeError, match="out of range"):
+        from utttcompanion_amd import _native as N
+        import ctypes as C
+        N.check(N.load_library().uttt_chunk_chain_stage_launch(C.byref(run_b.args), run_b.workspace.data_ptr(),
+                                                                 run_b.workspace.numel(), 4, 0, 1, 3, None, 0, None,
+                                                                 None), "stage launch")

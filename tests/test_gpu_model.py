@@ -293,6 +293,28 @@ def test_config1_block_fp32_matches_oracle():
     assert rel_err(sur, osur) <= 1e-5
 
 
+def test_prefill_with_kernel_timer_equals_plain_prefill():
+    """The measurement hook (events around chain kernels, stages enqueued launch by launch) leaves
+    the prefill's results unchanged, bit for bit (fp32 and bf16)."""
+    from utttcompanion_amd.kernels import KernelTimer
+    for dtype in (torch.float32, torch.bfloat16):
+        model, _ = build(dtype=dtype)
+        ids, mask = ids_and_mask(2, 80, 256, seed=31)
+        d_ids, d_mask = ids.to(DEV), mask.to(DEV)
+        state = model.init_fast_state(2, device=DEV, dtype=torch.float32, detach=True)
+        timer = KernelTimer(("k_chain_back_lds", "k_chain_back", "k_chain_apply_lds", "k_chain_apply"))
+        with torch.no_grad():
+            a = model.prefill_with_writes(d_ids, state, d_mask)
+            b = model.prefill_with_writes(d_ids, state, d_mask, kernel_timer=timer)
+        torch.cuda.synchronize()
+        assert torch.equal(a[0], b[0]) and torch.equal(a[2], b[2])
+        for x, y in zip(a[1], b[1]):
+            assert torch.equal(x, y)
+        summary = timer.summary()
+        back = "k_chain_back_lds" if dtype == torch.bfloat16 else "k_chain_back"
+        assert summary[back]["launches"] == 5 * SMALL["n_layers"]  # 5 chunks of 16 tokens
+
+
 def test_prefill_graph_replays_match_eager():
     """The whole prefill with writes recorded in one HIP graph; several replays with eager
     work and syncs between them must each equal the eager result."""

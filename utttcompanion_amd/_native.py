@@ -185,6 +185,8 @@ SIGNATURES = {
     "uttt_chunk_chain": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_chain_stage": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _P]),
     "uttt_chunk_chain_stage_part": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _I32, _P]),
+    "uttt_chunk_chain_stage_launch": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _I32, _I32, _I32,
+                                                C.POINTER(C.c_char_p), _I32, C.POINTER(_I32), _P]),
     "uttt_chunk_chain_w_products": (C.c_int, [_I64, _I64, _I64, _I64, _I32, _I32, C.POINTER(C.c_size_t),
                                               C.POINTER(C.c_size_t)]),
     "uttt_proj_epilogue": (C.c_int, [C.POINTER(ProjEpilogueArgs), _P]),

@@ -1769,21 +1769,40 @@ void pq_group(int l, int L, int size, int& g0, int& g1) {
   g1 = min(head, g0 + size);
 }
 
+// Selects which of the launches of a stage part are enqueued: those numbered in [begin, end) in
+// enqueue order (all of them by default).  Every launch site asks next() with its kernel's name,
+// so the numbering and names follow the launch sequence.
+struct LaunchGate {
+  int begin = 0;
+  int end = 1 << 30;
+  int count = 0;
+  const char** names = nullptr;
+  int cap = 0;
+  bool next(const char* name) {
+    if (names != nullptr && count < cap) names[count] = name;
+    const bool go = begin <= count && count < end;
+    ++count;
+    return go;
+  }
+};
+
 // Gram block rows [l0, l1) of every row b
 template <typename T>
-void launch_gram(int B, int l0, int l1, GramArgs g, hipStream_t st) {
+void launch_gram(int B, int l0, int l1, GramArgs g, hipStream_t st, LaunchGate& gate) {
   g.layer = l0;
   g.layer_end = l1;
-  if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL(k_chain_gram_lds, dim3(row_tile_blocks(B, gram_blocks(l0, l1))), dim3(512), 0, st, g);
-  else
+  if constexpr (sizeof(T) == 2) {
+    if (gate.next("k_chain_gram_lds"))
+      hipLaunchKernelGGL(k_chain_gram_lds, dim3(row_tile_blocks(B, gram_blocks(l0, l1))), dim3(512), 0, st, g);
+  } else if (gate.next("k_chain_gram")) {
     hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l0, l1))), dim3(kGramWaves * 64), 0, st, g);
+  }
 }
 
 template <typename T>
 // parts: bit 0 the snapshot products and key Gram rows of the stages, bit 1 the rest
 void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c, hipStream_t st, int first,
-                  int last, int parts) {
+                  int last, int parts, LaunchGate& gate) {
   const int B = (int)a.batch, L = (int)a.layers, C = (int)a.tokens, D = (int)a.d_model, F = (int)a.d_ff;
   const int LL = L * 64, nF = F / 64;
   const dim3 blk(kThreads);
@@ -1819,7 +1838,7 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   auto want = [&](int stage) { return first <= stage && stage <= last; };
   const bool keys_part = parts & 1, rest_part = parts & 2;
   const int ncoef = B * kCoefStride;  // table of layer 0
-  if (want(0) && rest_part)
+  if (want(0) && rest_part && gate.next("k_chain_init"))
     hipLaunchKernelGGL(k_chain_init, dim3((ncoef + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef);
 
   // the chunk-start state the bf16 kernels read: its bf16 copies when given, else the masters
@@ -1878,22 +1897,23 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
       pa.l_begin = g0;
       pa.l_count = g1 - g0;
       if (g1 - g0 == 1) {  // a single layer: one staged K tile, less LDS per workgroup
-        if (sizeof(T) == 2 && bf16_src)
-          hipLaunchKernelGGL(k_chain_pq_lds, pq_grid, blk, 0, st, pa);
-        else if (bf16_src)
-          hipLaunchKernelGGL((k_chain_pq<T, bf16, 1>), pq_grid, blk, 0, st, pa);
-        else
+        if (sizeof(T) == 2 && bf16_src) {
+          if (gate.next("k_chain_pq_lds")) hipLaunchKernelGGL(k_chain_pq_lds, pq_grid, blk, 0, st, pa);
+        } else if (bf16_src) {
+          if (gate.next("k_chain_pq")) hipLaunchKernelGGL((k_chain_pq<T, bf16, 1>), pq_grid, blk, 0, st, pa);
+        } else if (gate.next("k_chain_pq")) {
           hipLaunchKernelGGL((k_chain_pq<T, float, 1>), pq_grid, blk, 0, st, pa);
+        }
       } else if (bf16_src) {
-        hipLaunchKernelGGL((k_chain_pq<T, bf16, kPqGroup>), pq_grid, blk, 0, st, pa);
-      } else {
+        if (gate.next("k_chain_pq")) hipLaunchKernelGGL((k_chain_pq<T, bf16, kPqGroup>), pq_grid, blk, 0, st, pa);
+      } else if (gate.next("k_chain_pq")) {
         hipLaunchKernelGGL((k_chain_pq<T, float, kPqGroup>), pq_grid, blk, 0, st, pa);
       }
     }
     if (l == g0 && keys_part) {  // key Gram rows of the whole group
       ka.layer = g0;
       ka.layer_end = g1;
-      launch_gram<T>(B, g0, g1, ka, st);
+      launch_gram<T>(B, g0, g1, ka, st, gate);
     }
     if (!rest_part) continue;
     const float* cl = table(l);
@@ -1903,26 +1923,28 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     if (l > 0) ua.prev = coef_step(l - 1);
     ua.coef = cl; ua.pq = ws + c.pq; ua.kk = kk; ua.du_all = du_all; ua.dg_all = dg_all;
     ua.u_cur = u_cur; ua.g_cur = g_cur; ua.h_all = h_all;
-    if constexpr (sizeof(T) == 2)
-      hipLaunchKernelGGL(k_chain_up_lds, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
-    else
+    if constexpr (sizeof(T) == 2) {
+      if (gate.next("k_chain_up_lds")) hipLaunchKernelGGL(k_chain_up_lds, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
+    } else if (gate.next("k_chain_up")) {
       hipLaunchKernelGGL(k_chain_up<T>, dim3(row_tile_blocks(B, nF)), blk, 0, st, ua);
+    }
 
     ha.layer = l;
     ha.layer_end = l + 1;
-    launch_gram<T>(B, l, l + 1, ha, st);
+    launch_gram<T>(B, l, l + 1, ha, st, gate);
 
     DownArgs da{};
     da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
     da.coef = cl; da.h_all = h_all; da.wd = wd_src; da.sd = sd_src; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
     const int ncorr = (l + kCorrPerSplit - 1) / kCorrPerSplit;
     const dim3 down_grid(row_tile_blocks(B, (D / 64) * (c.nsplit + ncorr)));
-    if (sizeof(T) == 2 && bf16_src)
-      hipLaunchKernelGGL(k_chain_down_lds, down_grid, blk, 0, st, da);
-    else if (bf16_src)
-      hipLaunchKernelGGL((k_chain_down<T, bf16>), down_grid, blk, 0, st, da);
-    else
+    if (sizeof(T) == 2 && bf16_src) {
+      if (gate.next("k_chain_down_lds")) hipLaunchKernelGGL(k_chain_down_lds, down_grid, blk, 0, st, da);
+    } else if (bf16_src) {
+      if (gate.next("k_chain_down")) hipLaunchKernelGGL((k_chain_down<T, bf16>), down_grid, blk, 0, st, da);
+    } else if (gate.next("k_chain_down")) {
       hipLaunchKernelGGL((k_chain_down<T, float>), down_grid, blk, 0, st, da);
+    }
 
     LnGradArgs g{};
     g.B = B; g.C = C; g.D = D; g.nsplit = c.nsplit + ncorr; g.tok_pad = 64;
@@ -1933,26 +1955,27 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     g.ln_w = a.ln_weight; g.ln_b = a.ln_bias;
     g.dz = static_cast<char*>(dz_all) + e * l * ld;
     g.loss = loss;
-    launch_ln_grad<T>(dim3(64, B), st, g);
+    if (gate.next("k_ln_grad")) launch_ln_grad<T>(dim3(64, B), st, g);
 
     za.layer = l;
     za.layer_end = l + 1;
-    launch_gram<T>(B, l, l + 1, za, st);
+    launch_gram<T>(B, l, l + 1, za, st, gate);
 
     BackArgs ba{};
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
     ba.coef = cl; ba.dz_all = dz_all; ba.wd = wd_src; ba.sd = sd_src; ba.zz = zz; ba.h_all = h_all;
     ba.u_cur = u_cur; ba.g_cur = g_cur; ba.kk = kk; ba.du_all = du_all; ba.dg_all = dg_all; ba.npart = npart;
-    if (sizeof(T) == 2 && bf16_src)
-      hipLaunchKernelGGL(k_chain_back_lds, dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
-    else if (bf16_src)
-      hipLaunchKernelGGL((k_chain_back<T, bf16>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
-    else
+    if (sizeof(T) == 2 && bf16_src) {
+      if (gate.next("k_chain_back_lds")) hipLaunchKernelGGL(k_chain_back_lds, dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
+    } else if (bf16_src) {
+      if (gate.next("k_chain_back")) hipLaunchKernelGGL((k_chain_back<T, bf16>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
+    } else if (gate.next("k_chain_back")) {
       hipLaunchKernelGGL((k_chain_back<T, float>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
+    }
 
   }
 
-  if (want(L) && rest_part) {
+  if (want(L) && rest_part && gate.next("k_chain_coef")) {
     const CoefArgs last = coef_step(L - 1);
     hipLaunchKernelGGL(k_chain_coef<T>, dim3(B), blk, 0, st, last);
   }
@@ -1969,10 +1992,11 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   aa.sc[2] = static_cast<bf16*>(a.s_down_copy);
   if (want(L) && rest_part) {
     const dim3 grid(row_tile_blocks(B, 3 * (D / 64) * nF));
-    if constexpr (sizeof(T) == 2)
-      hipLaunchKernelGGL(k_chain_apply_lds, grid, blk, 0, st, aa);
-    else
+    if constexpr (sizeof(T) == 2) {
+      if (gate.next("k_chain_apply_lds")) hipLaunchKernelGGL(k_chain_apply_lds, grid, blk, 0, st, aa);
+    } else if (gate.next("k_chain_apply")) {
       hipLaunchKernelGGL(k_chain_apply<T>, grid, blk, 0, st, aa);
+    }
   }
 }
 
@@ -2001,7 +2025,7 @@ extern "C" size_t uttt_chunk_chain_workspace(int64_t batch, int64_t layers, int6
 }
 
 static int run_chain(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes, uttt_stream_t stream,
-                     int first, int last, int parts = 3) {
+                     int first, int last, int parts = 3, LaunchGate* gate = nullptr) {
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   int rc = check_chain_dims(a->batch, a->layers, a->d_model, a->d_ff, a->act_dtype);
   if (rc != UTTT_OK) return rc;
@@ -2038,10 +2062,12 @@ static int run_chain(const uttt_chunk_chain_args* a, void* workspace, size_t wor
                c.total, workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
+  LaunchGate every;
+  LaunchGate& g = gate != nullptr ? *gate : every;
   if (a->act_dtype == UTTT_DTYPE_BF16)
-    launch_chain<bf16>(*a, ws, c, st, first, last, parts);
+    launch_chain<bf16>(*a, ws, c, st, first, last, parts, g);
   else
-    launch_chain<float>(*a, ws, c, st, first, last, parts);
+    launch_chain<float>(*a, ws, c, st, first, last, parts, g);
   return launch_status("uttt_chunk_chain");
 }
 
@@ -2063,6 +2089,29 @@ extern "C" int uttt_chunk_chain_stage_part(const uttt_chunk_chain_args* a, void*
   UTTT_REQUIRE(stage >= 0 && stage <= a->layers, "stage must be in [0, layers] (got %d)", stage);
   UTTT_REQUIRE(part >= 0 && part <= 2, "part must be 0 (whole stage), 1 or 2 (got %d)", part);
   return run_chain(a, workspace, workspace_bytes, stream, stage, stage, part == 0 ? 3 : part);
+}
+
+extern "C" int uttt_chunk_chain_stage_launch(const uttt_chunk_chain_args* a, void* workspace, size_t workspace_bytes,
+                                             int32_t stage, int32_t part, int32_t launch_begin, int32_t launch_end,
+                                             const char** names, int32_t names_cap, int32_t* count,
+                                             uttt_stream_t stream) {
+  UTTT_REQUIRE(a != nullptr, "args is NULL");
+  UTTT_REQUIRE(stage >= 0 && stage <= a->layers, "stage must be in [0, layers] (got %d)", stage);
+  UTTT_REQUIRE(part >= 0 && part <= 2, "part must be 0 (whole stage), 1 or 2 (got %d)", part);
+  UTTT_REQUIRE(names_cap >= 0 && (names != nullptr || names_cap == 0), "names_cap must be >= 0 with names");
+  UTTT_REQUIRE(launch_begin >= 0, "launch_begin must be >= 0 (got %d)", launch_begin);
+  LaunchGate gate;
+  gate.begin = launch_begin;
+  gate.end = launch_end;
+  gate.names = names;
+  gate.cap = names_cap;
+  const int rc = run_chain(a, workspace, workspace_bytes, stream, stage, stage, part == 0 ? 3 : part, &gate);
+  if (count != nullptr) *count = gate.count;
+  if (rc != UTTT_OK) return rc;
+  UTTT_REQUIRE(launch_end <= launch_begin || launch_end <= gate.count,
+               "launches [%d, %d) out of range: stage %d part %d makes %d launches", launch_begin, launch_end, stage,
+               part, gate.count);
+  return UTTT_OK;
 }
 
 extern "C" int uttt_chunk_chain_w_products(int64_t batch, int64_t layers, int64_t d_model, int64_t d_ff,

@@ -287,10 +287,56 @@ class PreparedChain:
         self.args, self._keep, self.workspace, self.result, self.device = args, keep, workspace, result, device
         self.n_layers = n_layers
 
-    def launch(self, stage: Optional[int] = None, part: int = 0) -> Tuple[Tensor, Optional[Tensor]]:
-        """Enqueue the whole chain, or one of its ``layers + 1`` stream-ordered stages, or one
-        part of a stage (1: its snapshot products and key Gram rows, 2: the rest)."""
+    _launch_names: dict = {}
+
+    def stage_launches(self, stage: int, part: int = 0) -> Tuple[str, ...]:
+        """Kernel names of the launches stage ``stage`` (part ``part``) makes, in enqueue order
+        (they depend only on the chain's shape and options, so they are kept per shape)."""
+        a = self.args
+        key = (a.batch, a.layers, a.tokens, a.d_model, a.d_ff, a.act_dtype, bool(a.w_up_copy), a.w_products_given,
+               bool(a.token_mask), int(stage), int(part))
+        hit = PreparedChain._launch_names.get(key)
+        if hit is not None:
+            return hit
         lib = N.load_library()
+        names = (C.c_char_p * 64)()
+        count = C.c_int32(0)
+        with torch.cuda.device(self.device):
+            N.check(lib.uttt_chunk_chain_stage_launch(C.byref(a), _p(self.workspace), self.workspace.numel(),
+                                                      int(stage), int(part), 0, 0, names, 64, C.byref(count), None),
+                    "uttt_chunk_chain_stage_launch")
+        out = tuple(names[i].decode() for i in range(min(count.value, 64)))
+        PreparedChain._launch_names[key] = out
+        return out
+
+    def launch(self, stage: Optional[int] = None, part: int = 0,
+               timer: Optional["KernelTimer"] = None) -> Tuple[Tensor, Optional[Tensor]]:
+        """Enqueue the whole chain, or one of its ``layers + 1`` stream-ordered stages, or one
+        part of a stage (1: its snapshot products and key Gram rows, 2: the rest).  With a
+        ``timer``, a stage is enqueued launch by launch, with events around the kernels the timer
+        follows (same kernels, same order)."""
+        lib = N.load_library()
+        if timer is not None and stage is not None:
+            stream = torch.cuda.current_stream(self.device)
+            names = self.stage_launches(stage, part)
+
+            def enqueue(lo: int, hi: int) -> None:
+                if hi > lo:
+                    with torch.cuda.device(self.device):
+                        N.check(lib.uttt_chunk_chain_stage_launch(C.byref(self.args), _p(self.workspace),
+                                                                  self.workspace.numel(), int(stage), int(part), lo, hi,
+                                                                  None, 0, None, _stream(self.device)),
+                                "uttt_chunk_chain_stage_launch")
+            done = 0  # launches between followed kernels go out as one range
+            for i, name in enumerate(names):
+                if name in timer.kernels:
+                    enqueue(done, i)
+                    pair = timer.begin(name, stream)
+                    enqueue(i, i + 1)
+                    timer.end(pair, stream)
+                    done = i + 1
+            enqueue(done, len(names))
+            return self.result
         with torch.cuda.device(self.device):
             if stage is None:
                 rc = lib.uttt_chunk_chain(C.byref(self.args), _p(self.workspace), self.workspace.numel(),
@@ -304,6 +350,42 @@ class PreparedChain:
                                                 int(stage), _stream(self.device))
         N.check(rc, "uttt_chunk_chain")
         return self.result
+
+
+class KernelTimer:
+    """HIP events around chosen kernels of the layer chain, recorded on the stream each kernel
+    is enqueued on: ``kernels`` names the kernels to follow (``ChunkChainRun.stage_launches``
+    names).  ``summary()`` (after a synchronize) gives, per followed kernel, the number of
+    launches and their mean duration in ms."""
+
+    def __init__(self, kernels: Sequence[str]):
+        self.kernels = set(kernels)
+        self.pairs = {k: [] for k in self.kernels}
+
+    def begin(self, name: str, stream) -> Optional[Tuple[str, "torch.cuda.Event"]]:
+        if name not in self.kernels:
+            return None
+        start = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        return name, start
+
+    def end(self, pair, stream) -> None:
+        if pair is None:
+            return
+        stop = torch.cuda.Event(enable_timing=True)
+        stop.record(stream)
+        self.pairs[pair[0]].append((pair[1], stop))
+
+    def reset(self) -> None:
+        self.pairs = {k: [] for k in self.kernels}
+
+    def summary(self) -> dict:
+        out = {}
+        for name, pairs in self.pairs.items():
+            if pairs:
+                ms = [a.elapsed_time(b) for a, b in pairs]
+                out[name] = {"launches": len(ms), "mean_ms": sum(ms) / len(ms)}
+        return out
 
 
 def _inplace_state(t: Tensor, name: str) -> Tensor:

@@ -212,8 +212,10 @@ class uTTTModel(nn.Module):
 
     def prefill_with_writes(self, input_ids: Tensor, state: FastWeightState,
                             attention_mask: Optional[Tensor] = None,
-                            kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0):
+                            kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0,
+                            kernel_timer: Optional["K.KernelTimer"] = None):
         """Chunk-first forward with fast-weight writes, without any host synchronisation.
+        ``kernel_timer`` (measurement only) records events around the chain kernels it follows.
 
         Per chunk: every layer's attention, projections and fast-weight readout run first
         (all readouts read the chunk-start state, reference uttt_model.py:519-608), then one
@@ -307,16 +309,18 @@ class uTTTModel(nn.Module):
                 # graph's executor keeps the forward pass on one in-order queue of its own
                 side.wait_event(ready)
                 with torch.cuda.stream(side):
+                    layer = run.set_layer(uk, uv, eta, alpha)
                     if shared:
-                        layer = run.set_layer(uk, uv, eta, alpha)
-                        run.launch(layer, part=1)
+                        run.launch(layer, part=1, timer=kernel_timer)
                         side.wait_event(read_done)
-                        run.launch(layer, part=2)
+                        run.launch(layer, part=2, timer=kernel_timer)
                     else:
-                        run.add_layer(uk, uv, eta, alpha)
+                        run.launch(layer, timer=kernel_timer)
             side.wait_stream(main)
             with torch.cuda.stream(side):
-                run.finish()
+                if run.layers_added != run.n_layers:
+                    raise ValueError(f"{run.layers_added} of {run.n_layers} layers were given")
+                run.launch(run.n_layers, timer=kernel_timer)
             main.wait_stream(side)
             pieces.append(hid)
         per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
