@@ -279,6 +279,7 @@ BF16_TAIL_CASES = [
     dict(L=5, b=3, c=40, d=192, f=320, mask=True, copies=True),   # tail chunk, masked rows, bf16 copies
     dict(L=3, b=2, c=17, d=128, f=192, mask=False, copies=True),  # short chunk
     dict(L=4, b=9, c=64, d=64, f=128, mask=True, copies=False),   # more rows than XCDs, fp32 masters
+    dict(L=6, b=3, c=40, d=1024, f=1536, mask=True, copies=True),  # Gram features split over 2 and 3 slices
 ]
 
 

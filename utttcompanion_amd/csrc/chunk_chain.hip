@@ -33,6 +33,8 @@
 // stage L: the last layer's recurrence step (coef) and apply (final W, S and their bf16
 // copies).  Stage l reads only layers <= l, so a caller can run it as soon as layer l's keys
 // and values exist.
+#include <algorithm>
+
 #include "update_ln.h"
 #include "uttt_device.h"
 #include "uttt_host.h"
@@ -184,8 +186,11 @@ struct CombRowStage {
 // ---------------------------------------------------------------------------
 // 0. coefficient tables: a = e = 1, everything else 0 (a fill kernel, safe in graphs)
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kThreads) k_chain_init(float* coef, int n) {
+// The coefficient table of layer 0 (a = e = 1, the rest 0), and the Gram counters cleared (every
+// Gram launch leaves them zero; this covers a fresh workspace).
+__global__ void __launch_bounds__(kThreads) k_chain_init(float* coef, int n, unsigned* counters, int ncounters) {
   const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < ncounters) counters[i] = 0u;
   if (i >= n) return;
   const int slot = i % kCoefStride;
   coef[i] = (slot == 0 || slot == 2) ? 1.f : 0.f;
@@ -353,6 +358,12 @@ struct GramArgs {
   LayerPtrs x;
   float* out;      // row b's block row l at out + (b * out_rows + out_r0 + l * out_lstep) * LL
   int out_rows, out_r0, out_lstep;
+  // bf16 path: the feature range is split over `splits` workgroups per block; their partial
+  // blocks (4096 floats each) go to `part` and the last of them, counted in `counters` (one per
+  // row and block of the launch, zero before the launch and left zero), sums them into `out`
+  float* part;
+  unsigned* counters;
+  int splits;
 };
 
 // 32 x 32 quadrant tiles of the block rows [l0, l1): row l has 4 (l + 1) of them
@@ -429,40 +440,46 @@ __global__ void __launch_bounds__(kGramWaves * 64) k_chain_gram(const GramArgs a
   }
 }
 
-// bf16 activations: one workgroup per 64 x 64 block (b, l, j) -- each operand row read once
-// per block, not once per quadrant.  Eight waves: the four 32 x 32 quadrants times two halves of
-// the feature range, each half streaming coalesced 64-wide row tiles of X_l and X_j straight into
-// LDS through its own ring of kGramSlots steps; the halves' sums meet in LDS.
+// bf16 activations: one workgroup per 64 x 64 block (b, l, j) and slice of kGramSplitSteps 64-wide
+// feature steps.  Four waves, one 32 x 32 quadrant each, stream coalesced 64-wide row tiles of X_l
+// and X_j straight into LDS through a ring of kGramSlots steps.  With one slice the block is written
+// directly; otherwise every workgroup stores its partial block with device-coherent stores, waits
+// for them to complete and raises the block's counter, and the workgroup that completes the count
+// reads the partials back with device-coherent loads (no cache write-back or invalidate between
+// XCDs), sums them in slice order (deterministic) and returns the counter to zero.
 constexpr int kGramSlots = 3;
+constexpr int kGramSplitSteps = 8;
 
 __host__ __device__ inline int gram_blocks(int l0, int l1) { return (l1 * (l1 + 1) - l0 * (l0 + 1)) / 2; }
+__host__ __device__ inline int gram_splits(int kd) { return (kd / 64 + kGramSplitSteps - 1) / kGramSplitSteps; }
 
-__global__ void __launch_bounds__(512) k_chain_gram_lds(const GramArgs a) {
+__global__ void __launch_bounds__(kThreads) k_chain_gram_lds(const GramArgs a) {
   constexpr int kSlot = 16384;  // X_l rows, X_j rows (64 x 64 bf16 each)
-  constexpr int kHalf = kGramSlots * kSlot;
-  constexpr int PER = 4;        // 16 row groups per step over the 4 waves of a half
-  __shared__ __align__(1024) char ring[2 * kHalf];
-  const RowTile rt = row_tile(blockIdx.x, a.B, gram_blocks(a.layer, a.layer_end));
+  constexpr int PER = 4;        // 16 row groups per step over 4 waves
+  __shared__ __align__(1024) char ring[kGramSlots * kSlot];
+  __shared__ int last;
+  const int nblk = gram_blocks(a.layer, a.layer_end);
+  const RowTile rt = row_tile(blockIdx.x, a.B, nblk * a.splits);
   if (!rt.valid) return;
-  int l = a.layer, j = rt.tile;
+  const int blk = rt.tile / a.splits, sp = rt.tile % a.splits;
+  int l = a.layer, j = blk;
   while (j >= l + 1) {  // at most layer_end - layer steps
     j -= l + 1;
     ++l;
   }
   const int b = rt.b;
-  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int kh = w >> 2, q = w & 3;
-  const int n = a.kd / 64, nh = (n + 1) / 2;
-  const int s_begin = kh * nh, mine = min(n, s_begin + nh) - s_begin;  // this half's steps
+  const int n = a.kd / 64;
+  const int s_begin = sp * kGramSplitSteps, mine = min(n, s_begin + kGramSplitSteps) - s_begin;
   const bf16* xa = layer_row<bf16>(a.x, l, b, a.rs);
   const bf16* xb = layer_row<bf16>(a.x, j, b, a.rs);
   const int ts = (int)a.ts;
   int voff[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) voff[i] = row_src_off((q + 4 * i) & 7, lane, ts);
-  const uint32_t ring0 = lds_addr(ring) + (uint32_t)(kh * kHalf);
-  auto issue = [&](int t) {  // this half's step t; rows past C are out of the buffer range: zeros
+  const uint32_t ring0 = lds_addr(ring);
+  auto issue = [&](int t) {  // step t of this slice; rows past C are out of the buffer range: zeros
     const int k0 = (s_begin + t) * 64;
     const uint32_t base = ring0 + (uint32_t)((t % kGramSlots) * kSlot);
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(xa + k0, (uint32_t)(a.C * ts * 2));
@@ -482,38 +499,57 @@ __global__ void __launch_bounds__(512) k_chain_gram_lds(const GramArgs a) {
   }
   f32x16 acc;
   zero(acc);
-  for (int t = 0; t < nh; ++t) {  // both halves run nh rounds: the barriers match
-    if (t < mine) wait_steps<PER, kGramSlots - 2>(min(mine - 1, t + kGramSlots - 2) - t);
+  for (int t = 0; t < mine; ++t) {
+    wait_steps<PER, kGramSlots - 2>(min(mine - 1, t + kGramSlots - 2) - t);
     __builtin_amdgcn_s_barrier();
     if (t + kGramSlots - 1 < mine) issue(t + kGramSlots - 1);
-    if (t < mine) {
-      const uint32_t so = (uint32_t)((t % kGramSlots) * kSlot);
-      bf16x8 fa[4], fb[4];
+    const uint32_t so = (uint32_t)((t % kGramSlots) * kSlot);
+    bf16x8 fa[4], fb[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        fa[k] = lds_read_bf16x8<0>(ta[k] + so);
-        fb[k] = lds_read_bf16x8<0>(tb[k] + so);
-      }
-      lds_wait_frags(fa, fb);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fb[k], acc, 0, 0, 0);
+    for (int k = 0; k < 4; ++k) {
+      fa[k] = lds_read_bf16x8<0>(ta[k] + so);
+      fb[k] = lds_read_bf16x8<0>(tb[k] + so);
     }
-  }
-  __builtin_amdgcn_s_barrier();  // every read of the rings is done: half 0's ring takes the sums
-  float* red = reinterpret_cast<float*>(ring);
-  if (kh == 1) {
+    lds_wait_frags(fa, fb);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) red[(q * 16 + i) * 64 + lane] = acc[i];
+    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fb[k], acc, 0, 0, 0);
   }
-  __syncthreads();
-  if (kh == 1) return;
   float* out = a.out + ((int64_t)b * a.out_rows + a.out_r0 + l * a.out_lstep) * a.LL;
   const int c = j * 64 + (q & 1) * 32 + acc_col();
+  if (a.splits == 1) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int row = (q >> 1) * 32 + acc_row(i);
-    out[(int64_t)row * a.LL + c] = acc[i] + red[(q * 16 + i) * 64 + lane];
+    for (int i = 0; i < 16; ++i) out[(int64_t)((q >> 1) * 32 + acc_row(i)) * a.LL + c] = acc[i];
+    return;
   }
+  const int64_t blk_id = (int64_t)b * nblk + blk;
+  float* mine_part = a.part + (blk_id * a.splits + sp) * 4096;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    __hip_atomic_store(mine_part + (q * 16 + i) * 64 + lane, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(a.counters + blk_id, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == (unsigned)(a.splits - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  const float* parts = a.part + blk_id * a.splits * 4096;
+  float sum[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sum[i] = 0.f;
+  for (int u = 0; u < a.splits; ++u) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      v[i] = __hip_atomic_load(parts + (int64_t)u * 4096 + (q * 16 + i) * 64 + lane, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sum[i] += v[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) out[(int64_t)((q >> 1) * 32 + acc_row(i)) * a.LL + c] = sum[i];
+  if (threadIdx.x == 0) __hip_atomic_store(a.counters + blk_id, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -1714,7 +1750,8 @@ size_t act_size(int32_t dtype) { return dtype == UTTT_DTYPE_BF16 ? 2 : 4; }
 
 struct ChainLayout {
   size_t pq, kk, hh, zz, h_all, du_all, dg_all, dz_all, u_cur, g_cur, zp, loss, npart, coef, total;
-  int nsplit;
+  size_t gpart_k, gpart_l, gcnt;  // split-feature Gram partials (key Gram; H / dZ Grams) and counters
+  int nsplit, max_key_blocks, ncounters;
 };
 
 ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dtype) {
@@ -1739,6 +1776,15 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
   c.loss = take(sizeof(float) * B * 64);
   c.npart = take(sizeof(float) * B * nF);
   c.coef = take(sizeof(float) * 2 * B * kCoefStride);  // tables of even / odd layers
+  // a key Gram launch covers one layer group (at most kPqGroup layers of at most L blocks each);
+  // an H or dZ Gram launch one layer's row of blocks.  The two kinds may run at once (the key Gram
+  // of stage l beside the rest of stage l - 1), so they have separate partials and counters.
+  c.max_key_blocks = (int)(kPqGroup * L);
+  const int sk = gram_splits((int)D), sl = std::max(gram_splits((int)D), gram_splits((int)F));
+  c.gpart_k = take(sizeof(float) * 4096 * B * c.max_key_blocks * sk);
+  c.gpart_l = take(sizeof(float) * 4096 * B * L * sl);
+  c.ncounters = (int)(B * (c.max_key_blocks + L));
+  c.gcnt = take(sizeof(unsigned) * c.ncounters);
   c.total = off;
   return c;
 }
@@ -1792,8 +1838,10 @@ void launch_gram(int B, int l0, int l1, GramArgs g, hipStream_t st, LaunchGate& 
   g.layer = l0;
   g.layer_end = l1;
   if constexpr (sizeof(T) == 2) {
+    g.splits = gram_splits(g.kd);
     if (gate.next("k_chain_gram_lds"))
-      hipLaunchKernelGGL(k_chain_gram_lds, dim3(row_tile_blocks(B, gram_blocks(l0, l1))), dim3(512), 0, st, g);
+      hipLaunchKernelGGL(k_chain_gram_lds, dim3(row_tile_blocks(B, gram_blocks(l0, l1) * g.splits)), dim3(kThreads), 0,
+                         st, g);
   } else if (gate.next("k_chain_gram")) {
     hipLaunchKernelGGL(k_chain_gram<T>, dim3(row_tile_blocks(B, gram_tiles(l0, l1))), dim3(kGramWaves * 64), 0, st, g);
   }
@@ -1838,8 +1886,11 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   auto want = [&](int stage) { return first <= stage && stage <= last; };
   const bool keys_part = parts & 1, rest_part = parts & 2;
   const int ncoef = B * kCoefStride;  // table of layer 0
-  if (want(0) && rest_part && gate.next("k_chain_init"))
-    hipLaunchKernelGGL(k_chain_init, dim3((ncoef + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef);
+  unsigned* gcnt = reinterpret_cast<unsigned*>(ws + c.gcnt);
+  if (want(0) && keys_part && gate.next("k_chain_init")) {
+    const int n = std::max(ncoef, c.ncounters);
+    hipLaunchKernelGGL(k_chain_init, dim3((n + kThreads - 1) / kThreads), blk, 0, st, coef, ncoef, gcnt, c.ncounters);
+  }
 
   // the chunk-start state the bf16 kernels read: its bf16 copies when given, else the masters
   const bool bf16_src = a.w_up_copy != nullptr;
@@ -1859,9 +1910,11 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   GramArgs ka{};  // K_l K_j^T rows of the key Gram (B, LL, LL)
   ka.B = B; ka.L = L; ka.C = C; ka.kd = D; ka.LL = LL; ka.rs = a.kv_row_stride; ka.ts = D;
   ka.x = acts.k; ka.out = kk; ka.out_rows = LL; ka.out_r0 = 0; ka.out_lstep = 64;
+  ka.part = reinterpret_cast<float*>(ws + c.gpart_k); ka.counters = gcnt;
 
   GramArgs ha{};  // H_l H_j^T and dZ_l dZ_j^T: the layer buffers have stride 64 rows per row b
   ha.B = B; ha.L = L; ha.C = C; ha.LL = LL; ha.out_rows = 64; ha.out_r0 = 0; ha.out_lstep = 0;
+  ha.part = reinterpret_cast<float*>(ws + c.gpart_l); ha.counters = gcnt + (size_t)B * c.max_key_blocks;
   GramArgs za = ha;
   ha.kd = F; ha.rs = (int64_t)64 * F; ha.ts = F; ha.out = hh;
   za.kd = D; za.rs = (int64_t)64 * D; za.ts = D; za.out = zz;
