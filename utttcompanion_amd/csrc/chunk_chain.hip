@@ -1243,18 +1243,21 @@ __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
 // kBackSlots steps -- D/64 steps of dZ_l rows with the W_down and S_down rows of this F tile
 // (k = d along every row), then l steps of the scaled dZ Gram block (fp32, as in k_chain_up_lds)
 // with the H_j slab (transposing reads).  dZ (a W_d + b S_d)^T is formed as a dZ W_d^T + b dZ S_d^T
-// with two accumulators, the combined weights never rounded to bf16.
-constexpr int kBackSlots = 4;
+// with two accumulators, the combined weights never rounded to bf16.  The cursor values are loaded
+// after the loops and the epilogue's dU / dG tiles reuse the ring, so registers (184) and LDS (72 KB)
+// leave room for two workgroups per CU: one computes while the other's loads are in flight
+// (measured at the config-3 shape: 49 us against 67 us with a four-step ring at one per CU).
+constexpr int kBackSlots = 3;
 
-__global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a) {
+__global__ void __launch_bounds__(kThreads, 2) k_chain_back_lds(const BackArgs a) {
   constexpr int kSlot = 24576;  // dZ, W_d, S_d tiles; or the Gram block (16 KB) and the H slab
   constexpr int PER = 6;        // 24 row groups per step over 4 waves
   constexpr int LD = lds_ld<bf16>();
+  static_assert(2 * 64 * LD * 2 <= kBackSlots * kSlot, "the epilogue tiles fit in the ring");
   __shared__ __align__(1024) char ring[kBackSlots * kSlot];
-  __shared__ __align__(16) bf16 dus[64 * LD];  // [t][f]
-  __shared__ __align__(16) bf16 dgs[64 * LD];
   __shared__ float red[4];
-  const RowTile rt = row_tile(blockIdx.x, a.B, a.F / 64);
+  const int nF = a.F / 64;
+  const RowTile rt = row_tile(blockIdx.x, a.B, nF);
   if (!rt.valid) return;
   const int ft = rt.tile, b = rt.b, f0 = ft * 64;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -1265,16 +1268,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a
       (const __attribute__((address_space(4))) float*)(uintptr_t)(a.coef + (int64_t)b * kCoefStride);
   const float ca = cf[0], cb = cf[1];
   const bool with_s = cb != 0.f;
-  // the epilogue's cursor values go out first
-  const int64_t base = (int64_t)b * 64 * a.F + f0;
   const int f = wc + acc_col();
-  float uc[16], gc[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + f;
-    uc[i] = a.u_cur[base + off];
-    gc[i] = a.g_cur[base + off];
-  }
   const bf16* dz = static_cast<const bf16*>(a.dz_all) + ((int64_t)a.l * a.B + b) * 64 * a.D;
   const int64_t mat = (int64_t)a.F * a.D;
   const bf16* wd = static_cast<const bf16*>(a.wd) + b * mat + (int64_t)f0 * a.D;
@@ -1282,7 +1276,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a
   const float* zz = a.zz + (int64_t)b * 64 * a.LL;  // layer j's block at + 64 j
   const bf16* hsrc = static_cast<const bf16*>(a.h_all) + (int64_t)b * 64 * a.F + f0;
   const int64_t lstride = (int64_t)a.B * 64 * a.F;
-  const int n1 = a.D / 64, nst = n1 + a.l;
+  const int n1 = a.D / 64, ns = n1 + a.l;
   // row group g of a step: phase 1: 0..7 dZ rows, 8..15 W_d rows, 16..23 S_d rows (8 rows each);
   // phase 2: 0..15 Gram rows (4 rows each), 16..23 H rows; wave w takes groups w, w + 4, ...
   int v1[PER], v2[PER];
@@ -1294,7 +1288,8 @@ __global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a
   }
   const uint32_t ring0 = lds_addr(ring);
   auto issue = [&](int step) {
-    const uint32_t slot = ring0 + (uint32_t)((step % kBackSlots) * kSlot);
+    const int t = step;
+    const uint32_t slot = ring0 + (uint32_t)((t % kBackSlots) * kSlot);
     if (step < n1) {
       const int d0 = step * 64;
       const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(dz + d0, (uint32_t)(64 * a.D * 2));
@@ -1318,7 +1313,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a
       }
     }
   };
-  for (int j = 0; j < min(nst, kBackSlots - 1); ++j) issue(j);
+  for (int t = 0; t < min(ns, kBackSlots - 1); ++t) issue(t);
   uint32_t tz[4], tw[4], ts[4], tg[8];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -1335,11 +1330,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a
   zero(accw);
   zero(accs);
   zero(accg);
-  for (int step = 0; step < nst; ++step) {
-    wait_steps<PER, kBackSlots - 2>(min(nst - 1, step + kBackSlots - 2) - step);
+  for (int t = 0; t < ns; ++t) {
+    wait_steps<PER, kBackSlots - 2>(min(ns - 1, t + kBackSlots - 2) - t);
     __builtin_amdgcn_s_barrier();  // every wave's loads of this step landed; the last step's slot is free
-    if (step + kBackSlots - 1 < nst) issue(step + kBackSlots - 1);
-    const uint32_t so = (uint32_t)((step % kBackSlots) * kSlot);
+    if (t + kBackSlots - 1 < ns) issue(t + kBackSlots - 1);
+    const uint32_t so = (uint32_t)((t % kBackSlots) * kSlot);
+    const int step = t;
     if (step < n1) {
       bf16x8 fz[4], fw[4], fs[4];
 #pragma unroll
@@ -1379,16 +1375,23 @@ __global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a
       }
     }
   }
+  float dh[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dh[i] = (ca * accw[i] + cb * accs[i]) + accg[i];
+  // epilogue: dU, dG of this tile, and its share of |g_l|^2; dU / dG tiles in the ring's LDS
+  __builtin_amdgcn_s_barrier();  // every wave is past its last read of the ring
+  bf16* dus = reinterpret_cast<bf16*>(ring);  // [t][f]
+  bf16* dgs = dus + 64 * LD;
+  const int64_t base = (int64_t)b * 64 * a.F + f0;
   const int64_t lbase = ((int64_t)a.l * a.B + b) * 64 * a.F + f0;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int t = wr + acc_row(i);
     const int64_t off = (int64_t)t * a.F + f;
-    const float dh = (ca * accw[i] + cb * accs[i]) + accg[i];
-    const float u = uc[i], g = gc[i];
+    const float u = a.u_cur[base + off], g = a.g_cur[base + off];
     const float sg = sigmoidf_acc(g);
-    const bf16 du = from_f32<bf16>(dh * (g * sg));
-    const bf16 dg = from_f32<bf16>(dh * u * (sg * (1.0f + g * (1.0f - sg))));
+    const bf16 du = from_f32<bf16>(dh[i] * (g * sg));
+    const bf16 dg = from_f32<bf16>(dh[i] * u * (sg * (1.0f + g * (1.0f - sg))));
     static_cast<bf16*>(a.du_all)[lbase + off] = du;
     static_cast<bf16*>(a.dg_all)[lbase + off] = dg;
     dus[t * LD + f] = du;
@@ -1405,7 +1408,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_chain_back_lds(const BackArgs a
 #pragma unroll
   for (int i = 0; i < 16; ++i) part += (gu[i] + gg[i]) * kk[(int64_t)(wr + acc_row(i)) * a.LL + wc + acc_col()];
   const float total = block_sum(part, red);
-  if (threadIdx.x == 0) a.npart[(int64_t)b * (a.F / 64) + ft] = total;
+  if (threadIdx.x == 0) a.npart[(int64_t)b * nF + ft] = total;
 }
 
 // ---------------------------------------------------------------------------
@@ -2019,7 +2022,8 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
     ba.coef = cl; ba.dz_all = dz_all; ba.wd = wd_src; ba.sd = sd_src; ba.zz = zz; ba.h_all = h_all;
     ba.u_cur = u_cur; ba.g_cur = g_cur; ba.kk = kk; ba.du_all = du_all; ba.dg_all = dg_all; ba.npart = npart;
     if (sizeof(T) == 2 && bf16_src) {
-      if (gate.next("k_chain_back_lds")) hipLaunchKernelGGL(k_chain_back_lds, dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
+      if (gate.next("k_chain_back_lds"))
+        hipLaunchKernelGGL(k_chain_back_lds, dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
     } else if (bf16_src) {
       if (gate.next("k_chain_back")) hipLaunchKernelGGL((k_chain_back<T, bf16>), dim3(row_tile_blocks(B, nF)), blk, 0, st, ba);
     } else if (gate.next("k_chain_back")) {
