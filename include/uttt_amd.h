@@ -32,7 +32,7 @@ enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE =
 
 /* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
  * Python binding reads it from this header and refuses a library built from another one. */
-#define UTTT_ABI_VERSION 15
+#define UTTT_ABI_VERSION 16
 
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
@@ -103,6 +103,50 @@ int uttt_chunk_update_phase(const uttt_chunk_update_args* args, void* workspace,
  * uttt_chunk_update's. */
 #define UTTT_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int uttt_chunk_update_noalloc(const uttt_chunk_update_args* args, uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 1a. Every chunk of one standalone layer's forward in one call.
+ *     Replaces the per-chunk chunk_step loop of uTTTLayer.forward
+ *     (model/uttt_layer.py:1451-1478) for one row of fp32 activations: chunk c
+ *     (tokens [c * chunk_size, min(T, (c + 1) * chunk_size))) is the update of
+ *     uttt_chunk_update applied to the state left by chunk c - 1, with the readout
+ *     through that chunk's pre-update state (read_state None).  The updates run in
+ *     persistent launches of up to 16 chunks: each workgroup keeps 8 columns of
+ *     W_up / W_gate and rows of W_down and their momentum on chip from the first
+ *     chunk of a launch to the last, and the workgroups meet at three device-wide
+ *     barriers per chunk, so a launch needs d_ff / 8 workgroups resident at once
+ *     (at most one per CU).  Each launch saves its chunks' query H and W_down for
+ *     the readout, which follows it on the stream.
+ *     q/k/v/out (T, D) row-major; eta/alpha/token_mask (T,); surprise (n_chunks,)
+ *     receives each chunk's surprise.  The state outputs may alias the inputs.
+ *     A barrier that waits past its bound (about a second) sets the flag word at
+ *     uttt_layer_update_resident_flag_offset in the workspace and no later barrier
+ *     waits: the results are then invalid, and the caller should check the flag.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t batch;       /* must be 1 */
+  int64_t tokens;      /* T >= 1 */
+  int64_t d_model;     /* 128, 256 or 512 */
+  int64_t d_ff;        /* a multiple of 64, d_ff / 8 <= the device's CUs */
+  int64_t chunk_size;  /* 1..64 */
+  int32_t normalize_by_dim;
+  float momentum_beta, max_inner_grad_norm, eps;
+  const float* q; const float* k; const float* v;
+  const float* eta; const float* alpha; const float* token_mask; /* token_mask NULL = all valid */
+  const float* w_up; const float* w_gate; const float* w_down;
+  const float* s_up; const float* s_gate; const float* s_down;
+  const float* ln_weight; const float* ln_bias;
+  float* w_up_out; float* w_gate_out; float* w_down_out;
+  float* s_up_out; float* s_gate_out; float* s_down_out;
+  float* out;
+  float* surprise;
+} uttt_layer_update_args;
+
+int uttt_layer_update_resident_supported(int64_t batch, int64_t d_model, int64_t d_ff);
+size_t uttt_layer_update_resident_workspace(int64_t d_model, int64_t d_ff);
+size_t uttt_layer_update_resident_flag_offset(int64_t d_model, int64_t d_ff);
+int uttt_layer_update_resident(const uttt_layer_update_args* args, void* workspace, size_t workspace_bytes,
+                               uttt_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * 1b. One chunk's updates for all L layers of the chunk-first shared schedule.

@@ -1,8 +1,10 @@
-"""Every HIP kernel compiles for gfx950 without register spills or scratch (private memory).
+"""Every HIP kernel compiles for gfx950 without vector-register spills or scratch (private memory).
 
 Scratch shows up when a per-thread array is indexed with a runtime value; it turns register
 traffic into memory traffic and made one kernel 5x slower before this check existed.  The
-check compiles each source with hipcc's resource-usage remarks (no GPU needed).
+check compiles each source with hipcc's resource-usage remarks (no GPU needed).  Scalar-register
+spills are allowed while the kernel has no scratch: they then go to lanes of a vector register
+(v_writelane / v_readlane), not to memory.
 """
 import glob
 import os
@@ -29,7 +31,7 @@ def test_kernels_use_no_scratch_and_do_not_spill(source, tmp_path):
         m = re.search(r"Function Name: (\S+)", line)
         if m:
             current = m.group(1)
-        m = re.search(r"(ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill): (\d+)", line)
+        m = re.search(r"(ScratchSize \[bytes/lane\]|VGPRs Spill): (\d+)", line)
         if m and int(m.group(2)) != 0:
             bad.append(f"{current}: {m.group(1)} = {m.group(2)}")
     assert not bad, "\n".join(bad)

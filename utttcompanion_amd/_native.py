@@ -56,6 +56,23 @@ class ChunkUpdateArgs(C.Structure):
     ]
 
 
+class LayerUpdateArgs(C.Structure):
+    _fields_ = [
+        ("batch", _I64), ("tokens", _I64), ("d_model", _I64), ("d_ff", _I64), ("chunk_size", _I64),
+        ("normalize_by_dim", _I32),
+        ("momentum_beta", _F), ("max_inner_grad_norm", _F), ("eps", _F),
+        ("q", _P), ("k", _P), ("v", _P),
+        ("eta", _P), ("alpha", _P), ("token_mask", _P),
+        ("w_up", _P), ("w_gate", _P), ("w_down", _P),
+        ("s_up", _P), ("s_gate", _P), ("s_down", _P),
+        ("ln_weight", _P), ("ln_bias", _P),
+        ("w_up_out", _P), ("w_gate_out", _P), ("w_down_out", _P),
+        ("s_up_out", _P), ("s_gate_out", _P), ("s_down_out", _P),
+        ("out", _P),
+        ("surprise", _P),
+    ]
+
+
 class ChunkChainArgs(C.Structure):
     _fields_ = [
         ("batch", _I64), ("layers", _I64), ("tokens", _I64), ("d_model", _I64), ("d_ff", _I64),
@@ -181,6 +198,10 @@ SIGNATURES = {
     "uttt_chunk_update": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_update_phase": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _I32, _P]),
     "uttt_chunk_update_noalloc": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P]),
+    "uttt_layer_update_resident_supported": (C.c_int, [_I64, _I64, _I64]),
+    "uttt_layer_update_resident_workspace": (C.c_size_t, [_I64, _I64]),
+    "uttt_layer_update_resident_flag_offset": (C.c_size_t, [_I64, _I64]),
+    "uttt_layer_update_resident": (C.c_int, [C.POINTER(LayerUpdateArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_chain_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_chunk_chain": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_chain_stage": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _P]),

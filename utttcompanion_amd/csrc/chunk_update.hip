@@ -827,6 +827,23 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   if (want(4)) hipLaunchKernelGGL(k_apply<T>, dim3(3 * (D / 64) * (F / 64), B), blk, 0, st, ap);
 }
 
+void launch_saved_readout(int B, int ntok, int D, int F, int nsplit, const float* h, const float* w_down,
+                          int64_t wd_rs, float* zp, const float* x, int64_t x_rs, const float* ln_w,
+                          const float* ln_b, float eps, float* out, int64_t out_rs, hipStream_t st) {
+  FwdArgs f{};
+  f.B = B; f.D = D; f.F = F; f.ntok = ntok; f.ntb = 1; f.tok_pad = 64; f.nsplit = nsplit;
+  f.wd[0] = w_down; f.w_rs[0] = wd_rs;
+  f.h[0] = const_cast<float*>(h);
+  f.zp = zp;
+  hipLaunchKernelGGL((k_down_partial<float, float>), dim3(D / 64, nsplit, B), dim3(kThreads), 0, st, f);
+  LnOutArgs o{};
+  o.B = B; o.ntok = ntok; o.D = D; o.nsplit = nsplit; o.tok_pad = 64; o.eps = eps;
+  o.zp = zp;
+  o.x = x; o.x_rs = x_rs; o.ln_w = ln_w; o.ln_b = ln_b;
+  o.out = out; o.out_rs = out_rs;
+  launch_ln_readout<float>(dim3(ntok, B), st, o);
+}
+
 // One token per row (decode), bf16 activations: a streaming GEMV.  One workgroup per (row, block
 // of gemv_fb(F) F columns): u and g over all of d (threads split d, partial sums meet in LDS), h
 // rounded to bf16 as the matrix path rounds it, then this block's Z partial over all of D from

@@ -35,6 +35,14 @@ inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Readout of B rows of up to 64 tokens from saved H and W_down (chunk_update.hip): row b's
+// out[t] = x[t] + LN(H[b] W_down[b])[t] for t < ntok, fp32 throughout.  h (B, 64, F) (rows past
+// ntok zero), w_down (B, F, D) with row stride wd_rs, zp a (nsplit, B, 64, D) fp32 scratch; x and
+// out rows of D floats, x_rs / out_rs elements apart from one row b to the next.
+void launch_saved_readout(int B, int ntok, int D, int F, int nsplit, const float* h, const float* w_down,
+                          int64_t wd_rs, float* zp, const float* x, int64_t x_rs, const float* ln_w,
+                          const float* ln_b, float eps, float* out, int64_t out_rs, hipStream_t st);
+
 }  // namespace uttt
 
 #define UTTT_REQUIRE(cond, ...)                              \

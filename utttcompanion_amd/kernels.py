@@ -277,6 +277,133 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
 
 
 # ---------------------------------------------------------------------------
+# every chunk of one standalone layer in one launch (uTTTLayer.forward's chunk loop,
+# model/uttt_layer.py:1451-1478)
+# ---------------------------------------------------------------------------
+
+_RESIDENT_DIMS = (128, 256, 512)
+_resident_pending = []  # (event, pinned flag word) of launches whose barrier flag is not yet read
+
+
+def resident_update_eligible(q: Tensor, w_up: Tensor, chunk_size: int) -> bool:
+    """True when ``layer_update_resident`` takes these operands: one fp32 row on the GPU,
+    d_model 128 / 256 / 512, d_ff a multiple of 64 with d_ff / 8 workgroups fitting the CUs,
+    chunks of at most 64 tokens."""
+    if q.device.type != "cuda" or q.dtype != torch.float32 or q.dim() != 3 or q.shape[0] != 1:
+        return False
+    dim, ff = q.shape[2], w_up.shape[-1]
+    if dim not in _RESIDENT_DIMS or ff % 64 or not 1 <= chunk_size <= 64 or q.shape[1] < 1:
+        return False
+    with torch.cuda.device(q.device):
+        return bool(N.load_library().uttt_layer_update_resident_supported(1, dim, ff))
+
+
+def check_resident_flags(wait: bool = False) -> None:
+    """Raise if a finished ``layer_update_resident`` launch reports a device-wide barrier that
+    waited past its bound (its results are then invalid).  ``wait`` blocks on pending launches."""
+    keep = []
+    failed = False
+    for ev, flag in _resident_pending:
+        if wait:
+            ev.synchronize()
+        if ev.query():
+            failed = failed or int(flag[0]) != 0
+        else:
+            keep.append((ev, flag))
+    _resident_pending[:] = keep
+    if failed:
+        raise RuntimeError("uttt_layer_update_resident: a device-wide barrier timed out (the workgroups were not "
+                           "all resident); its results are invalid")
+
+
+def layer_update_resident(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
+                          w_up: Tensor, w_gate: Tensor, w_down: Tensor,
+                          s_up: Tensor, s_gate: Tensor, s_down: Tensor,
+                          ln_weight: Tensor, ln_bias: Tensor, token_mask: Optional[Tensor],
+                          momentum_beta: float, max_inner_grad_norm: float, normalize_by_dim: bool, eps: float,
+                          chunk_size: int = 64, out_state: Optional[Sequence[Tensor]] = None,
+                          workspace: Optional[Tensor] = None) -> Tuple[Tensor, ...]:
+    """All chunks of one layer's forward for one fp32 row (``uttt_layer_update_resident``):
+    chunk c reads the state left by chunk c - 1, its readout goes through its own pre-update
+    state.  ``q/k/v`` (1, T, D); ``eta/alpha`` (1, T) or (1, T, 1); ``token_mask`` (1, T) or
+    None; state (1, D, F) / (1, F, D).  Returns ``(readout (1, T, D), W_up', W_gate', W_down',
+    S_up', S_gate', S_down', surprise (n_chunks,))``; ``out_state`` may be the input state
+    for an in-place update."""
+    if q.dim() != 3 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(f"q/k/v must share one (1, T, D) shape, got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{tuple(v.shape)}")
+    bsz, tokens, dim = q.shape
+    ff = w_up.shape[-1]
+    if not resident_update_eligible(q, w_up, chunk_size) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"the resident layer update takes one fp32 row with d_model in {_RESIDENT_DIMS}, d_ff a "
+                         f"multiple of 64 within the CU count and chunks of 1..64 tokens; got {tuple(q.shape)} "
+                         f"{q.dtype}, d_ff {ff}, chunk {chunk_size}")
+    if w_up.shape != (1, dim, ff) or w_gate.shape != (1, dim, ff) or w_down.shape != (1, ff, dim):
+        raise ValueError(f"state shapes {tuple(w_up.shape)}, {tuple(w_gate.shape)}, {tuple(w_down.shape)} "
+                         f"do not match B=1, D={dim}, F={ff}")
+    for s, w in ((s_up, w_up), (s_gate, w_gate), (s_down, w_down)):
+        if s.shape != w.shape:
+            raise ValueError("momentum buffers must match the weight shapes")
+    _check_per_token(eta, bsz, tokens, "eta")
+    _check_per_token(alpha, bsz, tokens, "alpha")
+    dev = q.device
+    _require_device(dev, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias,
+                    token_mask)
+    _forward_only(q, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias)
+    q, k, v = (t.contiguous() for t in (q, k, v))
+    q, k, v = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (q, k, v))
+    eta = _row_vector(eta, torch.float32).contiguous()
+    alpha = _row_vector(alpha, torch.float32).contiguous()
+    mask = None
+    if token_mask is not None:
+        if token_mask.shape != (bsz, tokens):
+            raise ValueError(f"token_mask must be (1, T) = (1, {tokens})")
+        mask = token_mask.to(torch.float32).contiguous()
+    ws = [_state(t, n) for t, n in ((w_up, "w_up"), (w_gate, "w_gate"), (w_down, "w_down"),
+                                     (s_up, "s_up"), (s_gate, "s_gate"), (s_down, "s_down"))]
+    ln_w = ln_weight.to(torch.float32).contiguous()
+    ln_b = ln_bias.to(torch.float32).contiguous()
+    if ln_w.numel() != dim or ln_b.numel() != dim:
+        raise ValueError("ln_weight / ln_bias must have d_model elements")
+    if out_state is None:
+        outs = [torch.empty_like(t) for t in ws]
+    else:
+        outs = list(out_state)
+        if len(outs) != 6 or any(o.dtype != torch.float32 or not o.is_contiguous() or o.shape != t.shape
+                                 for o, t in zip(outs, ws)):
+            raise ValueError("out_state must be six contiguous fp32 tensors shaped like the state")
+    n_chunks = (tokens + chunk_size - 1) // chunk_size
+    out = torch.empty((1, tokens, dim), dtype=torch.float32, device=dev)
+    surprise = torch.empty((n_chunks,), dtype=torch.float32, device=dev)
+    lib = N.load_library()
+    nbytes = lib.uttt_layer_update_resident_workspace(dim, ff)
+    if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    a = N.LayerUpdateArgs()
+    a.batch, a.tokens, a.d_model, a.d_ff, a.chunk_size = 1, tokens, dim, ff, int(chunk_size)
+    a.normalize_by_dim = int(bool(normalize_by_dim))
+    a.momentum_beta, a.max_inner_grad_norm, a.eps = float(momentum_beta), float(max_inner_grad_norm or 0.0), float(eps)
+    a.q, a.k, a.v = _p(q), _p(k), _p(v)
+    a.eta, a.alpha, a.token_mask = _p(eta), _p(alpha), _p(mask)
+    a.w_up, a.w_gate, a.w_down, a.s_up, a.s_gate, a.s_down = (_p(t) for t in ws)
+    a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
+    a.w_up_out, a.w_gate_out, a.w_down_out, a.s_up_out, a.s_gate_out, a.s_down_out = (_p(t) for t in outs)
+    a.out, a.surprise = _p(out), _p(surprise)
+    check_resident_flags()
+    with torch.cuda.device(dev):
+        rc = lib.uttt_layer_update_resident(C.byref(a), _p(workspace), workspace.numel(), _stream(dev))
+        N.check(rc, "uttt_layer_update_resident")
+        if not torch.cuda.is_current_stream_capturing():
+            off = lib.uttt_layer_update_resident_flag_offset(dim, ff)
+            flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
+            flag.copy_(workspace[off:off + 4].view(torch.int32), non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            _resident_pending.append((ev, flag))
+    return (out, *outs, surprise)
+
+
+# ---------------------------------------------------------------------------
 # one chunk, all layers (the chunk-first shared schedule, model/uttt_model.py:453-608)
 # ---------------------------------------------------------------------------
 

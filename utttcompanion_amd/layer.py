@@ -264,6 +264,24 @@ class SharedFastWeightPool(nn.Module):
                                     state.last_surprise_loss, state.surprise_history)
         return res[0], new_state, res[7]
 
+    def chunk_loop(self, state: FastWeightState, q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
+                   token_mask: Optional[Tensor], chunk_size: int) -> Optional[Tuple[Tensor, FastWeightState, Tensor]]:
+        """Every ``chunk_step`` of one layer's forward (write, readout through each chunk's own
+        pre-update state) in one launch, when ``K.layer_update_resident`` takes the operands
+        (one fp32 row; see ``K.resident_update_eligible``); None otherwise.  Returns the
+        readout, the state after the last chunk and the mean chunk surprise, as the chunk loop
+        of the reference's uTTTLayer.forward does (reference :1451-1478)."""
+        state = state.ensure_batch_size(q.shape[0])
+        if not K.resident_update_eligible(q, state.w_up, chunk_size):
+            return None
+        res = K.layer_update_resident(q, k, v, eta, alpha, *state.tensors(), state.ln_weight, state.ln_bias,
+                                      token_mask, self.momentum_beta, float(self.max_inner_grad_norm or 0.0),
+                                      self.normalize_loss_by_dim, self.eps, chunk_size)
+        n_chunks = res[7].shape[0]
+        new_state = FastWeightState(*res[1:7], state.ln_weight, state.ln_bias, state.step + n_chunks,
+                                    state.last_surprise_loss, state.surprise_history)
+        return res[0], new_state, res[7].sum() / n_chunks
+
     @torch.no_grad()
     def apply_elastic_pull(self, state: FastWeightState, anchor_lambda: float = 0.02,
                            max_drift_ratio: Optional[float] = None) -> FastWeightState:
@@ -584,6 +602,10 @@ class uTTTLayer(nn.Module):
         require_write_chunk(self.chunk_size)
         q, k, v, eta, alpha = self.projections(x)
         cur = fast_state.ensure_batch_size(bsz)
+        if read_state is None:
+            fused = fast_pool.chunk_loop(cur, q, k, v, eta, alpha, attention_mask, self.chunk_size)
+            if fused is not None:
+                return self.w_o(fused[0]), fused[1], fused[2]
         outs, losses = [], []
         n_chunks = (seq + self.chunk_size - 1) // self.chunk_size
         own = None  # buffers this call owns after the first write: later chunks update in place
