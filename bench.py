@@ -522,9 +522,13 @@ def bench_c1_block(iters: int):
     """Config 1: one uTTT block in fp32 (d_model 512, 8 x 64 heads, 4 kv heads, window 256,
     F 1024, chunk 64, inner lr 0.01, weight decay 0.005, random weights N(0, 0.02) as the
     reference initialises them, eta/alpha routers at their reference init), input (1, 1024, 512)
-    ~ N(0, 1): the block forward with 16 chunk updates.  Returns (tok/s, ms per forward, finite)."""
+    ~ N(0, 1): the block forward with 16 chunk updates (the persistent resident update).  Timed
+    eagerly (back-to-back forwards) and as replays of one captured HIP graph of the forward (no
+    per-kernel launch cost).  Returns (tok/s, ms per forward, finite, graph ms per forward,
+    graph replays equal to eager)."""
     import torch
     from utttcompanion_amd import SharedFastWeightPool, uTTTBlock
+    from utttcompanion_amd import kernels as K
     torch.manual_seed(0)
     c = C1
     block = uTTTBlock(0, c["d_model"], c["n_heads"], c["n_kv_heads"], window_size=c["window"], chunk_size=c["chunk"],
@@ -550,8 +554,28 @@ def bench_c1_block(iters: int):
             out = block(x, pool, state)
         end.record()
         torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / iters
-    return c["seq"] / (ms * 1e-3), ms, bool(torch.isfinite(out[0]).all().item())
+        ms = start.elapsed_time(end) / iters
+        eager = out[0].clone()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            block(x, pool, state)  # allocations of the capture's shapes are made once, outside it
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(graph):
+            gout = block(x, pool, state)
+        graph.replay()
+        torch.cuda.synchronize()
+        same = bool(torch.equal(gout[0], eager))
+        start.record()
+        for _ in range(iters):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        gms = start.elapsed_time(end) / iters
+        same = same and bool(torch.equal(gout[0], eager))
+        K.check_resident_flags(wait=True)
+    return c["seq"] / (ms * 1e-3), ms, bool(torch.isfinite(out[0]).all().item()), gms, same
 
 
 def c1_flops() -> int:
@@ -790,14 +814,19 @@ def main() -> int:
 
     cpu_more = {}
     if "c1" in sections:
-        tps, c1_ms, c1_fin = bench_c1_block(20)
+        tps, c1_ms, c1_fin, c1_gms, c1_same = bench_c1_block(20)
         fl = c1_flops()
         tfl = fl / (c1_ms * 1e-3) / 1e12
+        gtfl = fl / (c1_gms * 1e-3) / 1e12
         big["config1_block"] = {"tok_s": round(tps, 1), "ms_per_forward": round(c1_ms, 4), "finite": c1_fin,
+                                "graph_tok_s": round(C1["seq"] / (c1_gms * 1e-3), 1),
+                                "graph_ms_per_forward": round(c1_gms, 4), "graph_equals_eager": c1_same,
                                 "algorithmic_gflop": round(fl / 1e9, 2), "achieved_tflops": round(tfl, 2),
                                 "fp32_mfma_frac": round(tfl / PEAK_FP32_TFLOPS, 4),
+                                "graph_fp32_mfma_frac": round(gtfl / PEAK_FP32_TFLOPS, 4),
                                 "shape": "B1 T1024 D512 8x64 heads (4 kv) W256 F1024 C64, fp32, 16 chunk updates"}
-        log(f"config 1 block {c1_ms:.3f} ms -> {tps:.0f} tok/s ({tfl:.1f} TFLOP/s fp32)")
+        log(f"config 1 block {c1_ms:.3f} ms eager, {c1_gms:.3f} ms graph -> {tps:.0f} / "
+            f"{C1['seq'] / (c1_gms * 1e-3):.0f} tok/s ({tfl:.1f} / {gtfl:.1f} TFLOP/s fp32)")
         if run_cpu:
             cpu_more["config1"] = cpu_baseline_c1()
             log(f"cpu config 1: {cpu_more['config1']['value']} tok/s")

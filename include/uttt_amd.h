@@ -32,7 +32,7 @@ enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE =
 
 /* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
  * Python binding reads it from this header and refuses a library built from another one. */
-#define UTTT_ABI_VERSION 16
+#define UTTT_ABI_VERSION 17
 
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
@@ -140,6 +140,8 @@ typedef struct {
   float* s_up_out; float* s_gate_out; float* s_down_out;
   float* out;
   float* surprise;
+  unsigned* error_word;  /* optional device word (NULL = none): set to 1 when a barrier timed out;
+                            never cleared by the library, so it collects the failures of many calls */
 } uttt_layer_update_args;
 
 int uttt_layer_update_resident_supported(int64_t batch, int64_t d_model, int64_t d_ff);

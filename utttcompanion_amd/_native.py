@@ -70,6 +70,7 @@ class LayerUpdateArgs(C.Structure):
         ("s_up_out", _P), ("s_gate_out", _P), ("s_down_out", _P),
         ("out", _P),
         ("surprise", _P),
+        ("error_word", _P),
     ]
 
 

@@ -46,7 +46,7 @@ namespace {
 
 constexpr int kCols = 8;                   // F columns per workgroup
 constexpr int kUgLd = 17;                  // row stride of the per-wave U | G and dH partials in LDS
-constexpr int kTileLd = 17;                // row stride of the per-wave 64 x 16 transposition tile
+constexpr int kTLd = 68;                   // row stride of the [16][64] transposed tiles (16-byte rows)
 constexpr unsigned kSpinLimit = 1u << 20;  // about a second of polling
 constexpr int kCoherent = 16;              // buffer cache policy sc1: device-coherent, as agent-scope atomics
 
@@ -59,6 +59,7 @@ struct ResArgs {
   float* out;
   float* surprise;    // (chunks,)
   unsigned char* ws;  // workspace, laid out as WsLayout
+  unsigned* error_word;  // optional: set to 1 on a barrier timeout, never cleared here
 };
 
 constexpr int kSegChunks = 16;  // chunks per launch: bounds the saved readout operands
@@ -122,6 +123,7 @@ __device__ void grid_barrier(const ResArgs& a, unsigned round) {
         __builtin_amdgcn_s_sleep(2);
         if (++spins > kSpinLimit) {
           __hip_atomic_store(ws_flag(a), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (a.error_word != nullptr) __hip_atomic_store(a.error_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           break;
         }
       }
@@ -172,12 +174,34 @@ __device__ __forceinline__ void load_rows(const float* x, int D, int d0, int val
   }
 }
 
-// the 64 x 16 tile held by load_rows (row 16 r + col, feature 4 kq + i) into a wave's LDS tile [t][16]
-__device__ __forceinline__ void put_tile(float* tile, int col, int kq, const f32x4 (&v)[4]) {
+// the 64 x 16 tile held by load_rows (row 16 r + col, feature 4 kq + i) into a wave's LDS tile,
+// transposed: [feature][row]
+__device__ __forceinline__ void put_tile_t(float* tile, int col, int kq, const f32x4 (&v)[4]) {
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tile[(16 * r + col) * kTileLd + 4 * kq + i] = v[r][i];
+    for (int i = 0; i < 4; ++i) tile[(4 * kq + i) * kTLd + 16 * r + col] = v[r][i];
+}
+
+// sum over the 64 tokens of A[m][t] B[t][n] with A^T and B^T rows in LDS ([m][t] and [n][t], 16-byte
+// aligned rows of kTLd floats): lane (col, kq) takes tokens 16 kq .. 16 kq + 15 as its k steps, read
+// as float4 from A^T row col and B^T row brow.  b_on false: B's row for this lane is zero.
+__device__ __forceinline__ f32x4 mfma_tokens(const float* at, const float* bt, int brow, bool b_on, int col,
+                                             int kq) {
+  f32x4 acc = zero4();
+  const f32x4* ar = reinterpret_cast<const f32x4*>(at + col * kTLd + 16 * kq);
+  const f32x4* br = reinterpret_cast<const f32x4*>(bt + brow * kTLd + 16 * kq);
+  f32x4 av[4], bv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    av[j] = ar[j];
+    bv[j] = b_on ? br[j] : zero4();
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc = mfma4(av[j][q], bv[j][q], acc);
+  return acc;
 }
 
 // Z of one key row from the partials of every workgroup (fixed order), then LayerNorm, the token
@@ -281,8 +305,9 @@ __global__ void __launch_bounds__(kThreads, 1) k_resident_update(const ResArgs a
   __shared__ float part_lds[4 * 2 * 64 * kUgLd];      // per-wave U | G partials [v][p][t][c]; dH partials; row sums
   __shared__ __align__(16) float hs[2][64 * kCols];   // H of the keys / queries [t][c]
   __shared__ float uk[64 * kCols], gk[64 * kCols];    // U, G of the keys
-  __shared__ float dug[64 * 16];                      // dU | dG [t][c]
-  __shared__ float tiles[4][64 * kTileLd];            // per-wave transposition tile [t][16]
+  __shared__ __align__(16) float hkt[kCols * kTLd];   // H^T of the keys [c][t]
+  __shared__ __align__(16) float dugt[16 * kTLd];     // [dU | dG]^T [c][t]
+  __shared__ __align__(16) float tiles[4][16 * kTLd]; // per-wave transposed tile [feature][t]
   // momentum, element (m, i) of a lane (see below) at [(wave ND + m) 64 + lane] (S_up | S_gate) and
   // [(wave ND + m) 32 + 8 kq + col] (S_down, lanes col < 8) as float4
   __shared__ f32x4 s_ug_lds[4 * ND * 64], s_dn_lds[4 * ND * 32];
@@ -378,10 +403,12 @@ __global__ void __launch_bounds__(kThreads, 1) k_resident_update(const ResArgs a
         u += row[cc];
         g += row[cc + kCols];
       }
-      hs[p][t * kCols + cc] = (g * sigmoidf_acc(g)) * u;
+      const float h = (g * sigmoidf_acc(g)) * u;
+      hs[p][t * kCols + cc] = h;
       if (p == 0) {
         uk[t * kCols + cc] = u;
         gk[t * kCols + cc] = g;
+        hkt[cc * kTLd + t] = h;
       }
     }
     __syncthreads();
@@ -433,29 +460,48 @@ __global__ void __launch_bounds__(kThreads, 1) k_resident_update(const ResArgs a
       f32x4 dh[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) dh[r] = zero4();
-      f32x4 zb[3][4];  // three feature tiles of dZ rows in flight
-      load_rows<kCoherent>(dzp, D, dbase, C, col, kq, zb[0]);
-      if (ND > 1) load_rows<kCoherent>(dzp, D, dbase + 16, C, col, kq, zb[1]);
+      f32x4 zb[4][4];  // four feature tiles of dZ rows in flight
+#pragma unroll
+      for (int m = 0; m < 3 && m < ND; ++m) load_rows<kCoherent>(dzp, D, dbase + 16 * m, C, col, kq, zb[m]);
+      // warm this XCD's L2 with a slice of the next chunk's key and query rows (workgroup w runs on
+      // XCD w mod 8; a wrong guess only costs the warm-up): 16 KB per workgroup
+      f32x4 warm[4];
+      {
+        const int tn = t0 + a.CS, Cn = c + 1 < a.c_end ? min(a.CS, a.T - tn) : 0;
+        const uint32_t kbytes = (uint32_t)Cn * D * 4u;
+        const int piece = (w >> 3) * 16384;  // byte offset in [K rows | Q rows] of the next chunk
+        const bool in_k = piece < 64 * D * 4;
+        const __amdgpu_buffer_rsrc_t rw =
+            buffer_rsrc(in_k ? a.k + (int64_t)tn * D : a.q + (int64_t)tn * D, kbytes);
+        const int off = (in_k ? piece : piece - 64 * D * 4) + threadIdx.x * 16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          warm[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off + j * 4096, 0, 0));
+      }
+      if (w == 0 && threadIdx.x < 64) {  // the chunk's surprise: masked token losses / valid tokens
+        const int l = threadIdx.x;
+        float num = l < C ? ld_agent(ws_loss(a) + l) : 0.f;
+        float den = l < C ? (a.mask != nullptr ? a.mask[t0 + l] : 1.f) : 0.f;
+        num = wave_sum(num);
+        den = wave_sum(den);
+        if (l == 0) a.surprise[c] = a.mask != nullptr ? num / fmaxf(den, 1.f) : num / den;
+      }
 #pragma unroll
       for (int m = 0; m < ND; ++m) {
-        if (m + 2 < ND) load_rows<kCoherent>(dzp, D, dbase + 16 * (m + 2), C, col, kq, zb[(m + 2) % 3]);
-        const f32x4 (&z)[4] = zb[m % 3];
+        if (m + 3 < ND) load_rows<kCoherent>(dzp, D, dbase + 16 * (m + 3), C, col, kq, zb[(m + 3) % 4]);
+        const f32x4 (&z)[4] = zb[m % 4];
         // dH partial [t][c] += dZ[t][d] W_down[c][d] over this tile's features
+        const f32x4 wv = *reinterpret_cast<const f32x4*>(&wdn[(col & 7) * WDLD + dbase + 16 * m + 4 * kq]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float b = col < kCols ? wdn[col * WDLD + dbase + 16 * m + 4 * kq + i] : 0.f;
+          const float b = col < kCols ? wv[i] : 0.f;
 #pragma unroll
           for (int r = 0; r < 4; ++r) dh[r] = mfma4(z[r][i], b, dh[r]);
         }
-        put_tile(tile, col, kq, z);
+        put_tile_t(tile, col, kq, z);
         wave_lds_sync();
         // gradient of W_down[c][d] for this tile's features: sum_t dZ[t][d] H[t][c]
-        f32x4 gd = zero4();
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-          const int t = 4 * s + kq;
-          gd = mfma4(tile[t * kTileLd + col], col < kCols ? hs[0][t * kCols + col] : 0.f, gd);
-        }
+        const f32x4 gd = mfma_tokens(tile, hkt, col & 7, col < kCols, col, kq);
         g_dn[m] = gd;
         if (col < kCols) sq += (gd[0] * gd[0] + gd[1] * gd[1]) + (gd[2] * gd[2] + gd[3] * gd[3]);
         wave_lds_sync();
@@ -479,26 +525,23 @@ __global__ void __launch_bounds__(kThreads, 1) k_resident_update(const ResArgs a
         for (int v = 0; v < 4; ++v) dhs += part_lds[(v * 64 + t) * kUgLd + cc];
         const float u = uk[t * kCols + cc], g = gk[t * kCols + cc];
         const float sg = sigmoidf_acc(g);
-        dug[t * 16 + cc] = dhs * (g * sg);
-        dug[t * 16 + kCols + cc] = dhs * u * (sg * (1.0f + g * (1.0f - sg)));
+        dugt[cc * kTLd + t] = dhs * (g * sg);
+        dugt[(kCols + cc) * kTLd + t] = dhs * u * (sg * (1.0f + g * (1.0f - sg)));
       }
       __syncthreads();
       // gradient of W_up | W_gate: sum_t K[t][d] [dU | dG][t][c]
 #pragma unroll
       for (int m = 0; m < ND; ++m) {
         if (m + 2 < ND) load_rows(xk, D, dbase + 16 * (m + 2), C, col, kq, kb[(m + 2) % 3]);
-        put_tile(tile, col, kq, kb[m % 3]);
+        put_tile_t(tile, col, kq, kb[m % 3]);
         wave_lds_sync();
-        f32x4 gu = zero4();
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-          const int t = 4 * s + kq;
-          gu = mfma4(tile[t * kTileLd + col], dug[t * 16 + col], gu);
-        }
+        const f32x4 gu = mfma_tokens(tile, dugt, col, true, col, kq);
         g_ug[m] = gu;
         sq += (gu[0] * gu[0] + gu[1] * gu[1]) + (gu[2] * gu[2] + gu[3] * gu[3]);
         wave_lds_sync();
       }
+      // the warm-up loads have long completed; consume them so that they are kept
+      asm volatile("" ::"v"(warm[0]), "v"(warm[1]), "v"(warm[2]), "v"(warm[3]));
       const float total = block_sum(sq, red);
       if (threadIdx.x == 0) st_agent(ws_norms(a) + w, total);
     }
@@ -552,14 +595,6 @@ __global__ void __launch_bounds__(kThreads, 1) k_resident_update(const ResArgs a
           s_ug[64 * m] = su;
           if (col < kCols) s_dn[32 * m] = sd;
         }
-      }
-      if (w == 0 && threadIdx.x < 64) {  // the chunk's surprise: masked token losses / valid tokens
-        const int l = threadIdx.x;
-        float num = l < C ? ld_agent(ws_loss(a) + l) : 0.f;
-        float den = l < C ? (a.mask != nullptr ? a.mask[t0 + l] : 1.f) : 0.f;
-        num = wave_sum(num);
-        den = wave_sum(den);
-        if (l == 0) a.surprise[c] = a.mask != nullptr ? num / fmaxf(den, 1.f) : num / den;
       }
       if (c + 1 < a.c_end) {  // the next chunk's first two feature tiles
         const int tn = t0 + a.CS, Cn = min(a.CS, a.T - tn);
@@ -680,6 +715,7 @@ extern "C" int uttt_layer_update_resident(const uttt_layer_update_args* a, void*
   r.out = a->out;
   r.surprise = a->surprise;
   r.ws = static_cast<unsigned char*>(workspace);
+  r.error_word = a->error_word;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const OutPtrs outs{{a->w_up_out, a->w_gate_out, a->w_down_out, a->s_up_out, a->s_gate_out, a->s_down_out}};
   const int D = r.D, F = r.F, CS = r.CS, T = r.T;

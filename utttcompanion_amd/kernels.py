@@ -282,7 +282,28 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
 # ---------------------------------------------------------------------------
 
 _RESIDENT_DIMS = (128, 256, 512)
-_resident_pending = []  # (event, pinned flag word) of launches whose barrier flag is not yet read
+
+
+class _ResidentErrors:
+    """Per device: a sticky device word that every resident launch sets on a barrier timeout, and a
+    pinned host mirror refreshed by an asynchronous copy after each launch (no allocation per call;
+    the mirror lags the device word by at most the calls still in flight)."""
+
+    def __init__(self, device: torch.device):
+        self.word = torch.zeros(1, dtype=torch.int32, device=device)
+        self.mirror = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.event = torch.cuda.Event()
+        self.recorded = False
+
+
+_resident_errors = {}
+
+
+def _errors_for(device: torch.device) -> _ResidentErrors:
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    if key not in _resident_errors:
+        _resident_errors[key] = _ResidentErrors(torch.device("cuda", key))
+    return _resident_errors[key]
 
 
 def resident_update_eligible(q: Tensor, w_up: Tensor, chunk_size: int) -> bool:
@@ -300,20 +321,16 @@ def resident_update_eligible(q: Tensor, w_up: Tensor, chunk_size: int) -> bool:
 
 def check_resident_flags(wait: bool = False) -> None:
     """Raise if a finished ``layer_update_resident`` launch reports a device-wide barrier that
-    waited past its bound (its results are then invalid).  ``wait`` blocks on pending launches."""
-    keep = []
-    failed = False
-    for ev, flag in _resident_pending:
+    waited past its bound (its results are then invalid).  ``wait`` blocks until every launch so
+    far has been accounted for."""
+    for dev, errs in _resident_errors.items():
         if wait:
-            ev.synchronize()
-        if ev.query():
-            failed = failed or int(flag[0]) != 0
-        else:
-            keep.append((ev, flag))
-    _resident_pending[:] = keep
-    if failed:
-        raise RuntimeError("uttt_layer_update_resident: a device-wide barrier timed out (the workgroups were not "
-                           "all resident); its results are invalid")
+            errs.mirror.copy_(errs.word.cpu())
+        elif not (errs.recorded and errs.event.query()):
+            continue
+        if int(errs.mirror[0]) != 0:
+            raise RuntimeError(f"uttt_layer_update_resident on cuda:{dev}: a device-wide barrier timed out (the "
+                               "workgroups were not all resident); its results are invalid")
 
 
 def layer_update_resident(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
@@ -389,17 +406,18 @@ def layer_update_resident(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: T
     a.ln_weight, a.ln_bias = _p(ln_w), _p(ln_b)
     a.w_up_out, a.w_gate_out, a.w_down_out, a.s_up_out, a.s_gate_out, a.s_down_out = (_p(t) for t in outs)
     a.out, a.surprise = _p(out), _p(surprise)
-    check_resident_flags()
+    errs = _errors_for(dev)
+    a.error_word = _p(errs.word)
     with torch.cuda.device(dev):
+        capturing = torch.cuda.is_current_stream_capturing()
+        if not capturing:  # (event queries are not allowed under graph capture)
+            check_resident_flags()
         rc = lib.uttt_layer_update_resident(C.byref(a), _p(workspace), workspace.numel(), _stream(dev))
         N.check(rc, "uttt_layer_update_resident")
-        if not torch.cuda.is_current_stream_capturing():
-            off = lib.uttt_layer_update_resident_flag_offset(dim, ff)
-            flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
-            flag.copy_(workspace[off:off + 4].view(torch.int32), non_blocking=True)
-            ev = torch.cuda.Event()
-            ev.record()
-            _resident_pending.append((ev, flag))
+        if not capturing:
+            errs.mirror.copy_(errs.word, non_blocking=True)
+            errs.event.record()
+            errs.recorded = True
     return (out, *outs, surprise)
 
 
