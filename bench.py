@@ -59,15 +59,19 @@ PHASES = ("k_up_gate", "k_down_partial", "k_ln_grad+k_ln_readout", "k_backward",
 def measured_traffic(kernel: str, config: str = "c2"):
     """HBM bytes per launch of ``kernel`` at a config's shape, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (scaled by a copy kernel of known size), or None when no
-    summary for that kernel is present."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{kernel}_{config}_traffic.md")
-    try:
-        with open(path) as fh:
-            for line in fh:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip())
-    except OSError:
-        return None
+    summary for that kernel is present.  Looks for a ``traffic_bytes_per_launch <kernel>:`` line
+    in ``profiles/chain_<config>_traffic.md``, then a ``traffic_bytes_per_launch:`` line in
+    ``profiles/<kernel>_<config>_traffic.md``."""
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+    for path, prefix in ((os.path.join(here, f"chain_{config}_traffic.md"), f"traffic_bytes_per_launch {kernel}:"),
+                         (os.path.join(here, f"{kernel}_{config}_traffic.md"), "traffic_bytes_per_launch:")):
+        try:
+            with open(path) as fh:
+                for line in fh:
+                    if line.startswith(prefix):
+                        return int(line.split(":", 1)[1].strip())
+        except OSError:
+            continue
     return None
 
 
@@ -374,6 +378,12 @@ def build_c3_model():
 # D F B bytes: the S_up / S_gate products, the W_down / S_down reads of the down and back passes,
 # and the state write (W and S read and written once per row-chunk, fp32)
 CHAIN_STATE_BYTES = {"k_chain_pq_lds": 4, "k_chain_down_lds": 4, "k_chain_back_lds": 4, "k_chain_apply_lds": 48}
+CHAIN_STATE_WHAT = {
+    "k_chain_pq_lds": "4 D F per row (bf16 S_up and S_gate copies read once; the W products come from the readouts)",
+    "k_chain_down_lds": "4 D F per row (bf16 W_down and S_down copies read once)",
+    "k_chain_back_lds": "4 D F per row (bf16 W_down and S_down copies read once)",
+    "k_chain_apply_lds": "48 D F per row (fp32 W and S read and written once)",
+}
 CHAIN_KERNELS = ("k_chain_pq_lds", "k_chain_gram_lds", "k_chain_up_lds", "k_chain_down_lds", "k_ln_grad",
                  "k_chain_back_lds", "k_chain_coef", "k_chain_apply_lds", "k_chain_init")
 
@@ -796,9 +806,7 @@ def main() -> int:
                                        "timing": f"{per_replay} launches (one per layer) at the config-3 chunk shape "
                                                  f"in a HIP graph, replayed 5 times, HIP events around the replays",
                                        "in_prefill_avg_us": table[dom]["mean_us"],
-                                       "unit_bytes": (f"{CHAIN_STATE_BYTES[dom]} D F per row (bf16 W_down and S_down "
-                                                      f"copies read once)" if dom != "k_chain_apply_lds" else
-                                                      "48 D F per row (W and S read and written once)"),
+                                       "unit_bytes": CHAIN_STATE_WHAT[dom],
                                        "shape": {"B": C3_BATCH, "D": D, "F": F, "L": C3["n_layers"]}}}
             log(f"config 3 dominant streaming chain kernel {dom}: {us:.1f} us -> {gbs:.0f} GB/s")
             if run_cpu:
