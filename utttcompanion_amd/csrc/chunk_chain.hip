@@ -1746,6 +1746,216 @@ __global__ void __launch_bounds__(kThreads, kApplyLdsWaves) k_chain_apply_lds(co
   }
 }
 
+// The same state write with wider output tiles: NA x 64 rows by NB x 64 columns (D and F
+// multiples of 64 NA and 64 NB as the matrix needs).  Per layer the workgroup loads 64 token rows
+// of NA + NB 64-column slabs, so each output costs (NA + NB) / (2 NA NB) of the slab bytes of a
+// 64 x 64 tile, and each layer step carries NA NB times the MFMA work between barriers.  Wave
+// (qr, qc) owns rows qr NA 32 .. and columns qc NB 32 .. of the tile as NA x NB MFMA tiles of
+// 32 x 32; each tile's layer product is folded into its W and S sums right away.
+__device__ __forceinline__ void lds_wait_frag_sets(bf16x8 (&a)[4], bf16x8 (&b)[4], bf16x8 (&c)[4],
+                                                   bf16x8 (&d)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]),
+                 "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]));
+}
+
+template <int NA, int NB, int SLOTS>
+constexpr int apply_wide_occupancy() {
+  return (160 * 1024) / (SLOTS * (NA + NB) * 8192) < 1 ? 1 : (160 * 1024) / (SLOTS * (NA + NB) * 8192);
+}
+
+template <int NA, int NB, int SLOTS>
+__global__ void __launch_bounds__(kThreads, (apply_wide_occupancy<NA, NB, SLOTS>() > 4 ? 4 : apply_wide_occupancy<NA, NB, SLOTS>()))
+k_chain_apply_wide(const ApplyChainArgs a) {
+  constexpr int NS = NA + NB;  // 64-column slabs per layer: A halves, then B halves
+  __shared__ __align__(1024) bf16 slab[SLOTS][NS][64 * 64];
+  const int nD = a.D / 64, nF = a.F / 64;
+  // tiles: W_up / W_gate (D x F) take NA 64-row blocks of D by NB of F; W_down (F x D) NA of F by NB of D
+  const int per_ug = (nD / NA) * (nF / NB), per_dn = (nF / NA) * (nD / NB);
+  const RowTile rt = row_tile(blockIdx.x, a.B, 2 * per_ug + per_dn);
+  if (!rt.valid) return;
+  const int m = rt.tile < 2 * per_ug ? rt.tile / per_ug : 2;
+  const int jt = m < 2 ? rt.tile - m * per_ug : rt.tile - 2 * per_ug;
+  const int b = rt.b;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int qr = w >> 1, qc = w & 1;
+  const __attribute__((address_space(4))) float* cf =
+      (const __attribute__((address_space(4))) float*)(uintptr_t)(a.coef + (int64_t)b * kCoefStride);
+  if (cf[3] == 0.f) return;  // no layer updated this row: W and S stay as they are
+  int r0, c0, ld_out;
+  if (m < 2) {
+    const int nct = nF / NB;
+    r0 = (jt / nct) * 64 * NA;
+    c0 = (jt % nct) * 64 * NB;
+    ld_out = a.F;
+  } else {
+    const int nct = nD / NB;
+    r0 = (jt / nct) * 64 * NA;
+    c0 = (jt % nct) * 64 * NB;
+    ld_out = a.D;
+  }
+  const int64_t mat = (int64_t)a.D * a.F;
+  const bf16* a_src;
+  const bf16* b_src;
+  int64_t a_lstride, b_lstride;
+  int a_ld, b_ld, a_rows;
+  if (m < 2) {
+    a_src = nullptr;  // per-layer key pointers
+    a_lstride = 0;
+    a_ld = (int)a.acts.kv_ts;
+    a_rows = a.C;
+    b_src = static_cast<const bf16*>(m == 0 ? a.du_all : a.dg_all) + (int64_t)b * 64 * a.F + c0;
+    b_ld = a.F;
+    b_lstride = (int64_t)a.B * 64 * a.F;
+  } else {
+    a_src = static_cast<const bf16*>(a.h_all) + (int64_t)b * 64 * a.F + r0;
+    a_ld = a.F;
+    a_lstride = (int64_t)a.B * 64 * a.F;
+    a_rows = 64;
+    b_src = static_cast<const bf16*>(a.dz_all) + (int64_t)b * 64 * a.D + c0;
+    b_ld = a.D;
+    b_lstride = (int64_t)a.B * 64 * a.D;
+  }
+  auto a_layer = [&](int j) -> const bf16* {
+    return m < 2 ? layer_row<bf16>(a.acts.k, j, b, a.acts.kv_rs) + r0 : a_src + j * a_lstride;
+  };
+  // this wave's slab loads: row groups w and w + 4 (8 token rows each) of every slab
+  int a_off[2], b_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    a_off[i] = slab_src_off(w + 4 * i, lane, a_ld);
+    b_off[i] = slab_src_off(w + 4 * i, lane, b_ld);
+  }
+  const uint32_t slab0 = lds_addr(&slab[0][0][0]);
+  // layer j's slabs into slot j % SLOTS.  Slab h of a side starts 64 h columns into the row; its
+  // range ends 128 h bytes before the side's, so rows past the valid ones read as zeros (a row
+  // stride of at least 64 (h + 1) elements keeps every valid row inside).  Past the last layer
+  // the buffers have no range.
+  auto issue = [&](int j) {
+    const bool live = j < a.L;
+    const int jj = live ? j : a.L - 1;
+    const uint32_t base = slab0 + (uint32_t)((j % SLOTS) * NS * 8192);
+    const bf16* al = a_layer(jj);
+    const bf16* bl = b_src + jj * b_lstride;
+#pragma unroll
+    for (int h = 0; h < NA; ++h) {
+      const __amdgpu_buffer_rsrc_t ar =
+          buffer_rsrc(al + 64 * h, live ? (uint32_t)(a_rows * a_ld * 2 - 128 * h) : 0u);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        buffer_load_lds_raw(ar, lds_ptr(base + (uint32_t)(h * 8192 + (w + 4 * i) * 1024)), 16, a_off[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int h = 0; h < NB; ++h) {
+      const __amdgpu_buffer_rsrc_t br = buffer_rsrc(bl + 64 * h, live ? (uint32_t)(64 * b_ld * 2 - 128 * h) : 0u);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        buffer_load_lds_raw(br, lds_ptr(base + (uint32_t)((NA + h) * 8192 + (w + 4 * i) * 1024)), 16, b_off[i], 0,
+                            0, 0);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < SLOTS - 1; ++j) issue(j);
+  // this wave's operand columns: A rows qr NA 32 + 32 ra of the tile, B columns qc NB 32 + 32 cb
+  uint32_t ta[NA], tb[NB];
+#pragma unroll
+  for (int ra = 0; ra < NA; ++ra) {
+    const int row = qr * NA * 32 + 32 * ra;
+    ta[ra] = slab_tr_addr(slab0 + (uint32_t)((row >> 6) * 8192), row & 63, lane);
+  }
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+    const int col = qc * NB * 32 + 32 * cb;
+    tb[cb] = slab_tr_addr(slab0 + (uint32_t)((NA + (col >> 6)) * 8192), col & 63, lane);
+  }
+  f32x16 accw[NA][NB], accs[NA][NB];
+#pragma unroll
+  for (int ra = 0; ra < NA; ++ra)
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) {
+      zero(accw[ra][cb]);
+      zero(accs[ra][cb]);
+    }
+  bf16x8 fa[2][4], fb[2][4];  // the second set stays unused (zero) with one 32-row or column block
+  if constexpr (NA == 1)
+    for (int s = 0; s < 4; ++s) fa[1][s] = bf16x8{};
+  if constexpr (NB == 1)
+    for (int s = 0; s < 4; ++s) fb[1][s] = bf16x8{};
+  for (int j = 0; j < a.L; ++j) {
+    // this wave's slab loads of layer j are done once those of the later issued layers remain
+    wait_steps<2 * NS, SLOTS - 2>(min(a.L - 1, j + SLOTS - 2) - j);
+    __builtin_amdgcn_s_barrier();  // every wave's loads of layer j landed; layer j - 1's slot is free
+    if (j + SLOTS - 1 < a.L) issue(j + SLOTS - 1);
+    const uint32_t so = (uint32_t)((j % SLOTS) * NS * 8192);
+#pragma unroll
+    for (int ra = 0; ra < NA; ++ra) slab_frags(ta[ra] + so, fa[ra]);
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) slab_frags(tb[cb] + so, fb[cb]);
+    lds_wait_frag_sets(fa[0], fa[1], fb[0], fb[1]);
+    const float gj = cf[kGam + j], sj = cf[kSig + j];
+#pragma unroll
+    for (int ra = 0; ra < NA; ++ra)
+#pragma unroll
+      for (int cb = 0; cb < NB; ++cb) {
+        f32x16 t;
+        zero(t);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ra][s], fb[cb][s], t, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          accw[ra][cb][i] += gj * t[i];
+          accs[ra][cb][i] += sj * t[i];
+        }
+      }
+  }
+  const uint32_t mat_bytes = (uint32_t)(mat * 4);
+  const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(a.w[m] + b * mat, mat_bytes);
+  const __amdgpu_buffer_rsrc_t sres = buffer_rsrc(a.s[m] + b * mat, mat_bytes);
+  const float ca = cf[0], cb_ = cf[1], ce = cf[2];
+  const bool copies = a.wc[m] != nullptr;
+  const __amdgpu_buffer_rsrc_t wcres = buffer_rsrc(copies ? a.wc[m] + b * mat : nullptr, copies ? mat_bytes / 2 : 0);
+  const __amdgpu_buffer_rsrc_t scres = buffer_rsrc(copies ? a.sc[m] + b * mat : nullptr, copies ? mat_bytes / 2 : 0);
+  auto row_el = [&](int i) { return (8 * (i >> 2) + (i & 3)) * ld_out; };
+#pragma unroll
+  for (int ra = 0; ra < NA; ++ra)
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) {
+      const int64_t tile0 = (int64_t)(r0 + qr * NA * 32 + 32 * ra) * ld_out + c0 + qc * NB * 32 + 32 * cb;
+      const int lane_el = (int)tile0 + 4 * (lane >> 5) * ld_out + acc_col();
+      float wv[16], sv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        wv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wres, lane_el * 4, row_el(i) * 4,
+                                                                               kNonTemporal));
+        sv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sres, lane_el * 4, row_el(i) * 4,
+                                                                               kNonTemporal));
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float w_new = ca * wv[i] + cb_ * sv[i] + accw[ra][cb][i];
+        const float s_new = ce * sv[i] + accs[ra][cb][i];
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, w_new), wres, lane_el * 4, row_el(i) * 4,
+                                              kNonTemporal);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s_new), sres, lane_el * 4, row_el(i) * 4,
+                                              kNonTemporal);
+        if (copies) {
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<bf16>(w_new)), wcres,
+                                                lane_el * 2, row_el(i) * 2, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<bf16>(s_new)), scres,
+                                                lane_el * 2, row_el(i) * 2, 0);
+        }
+      }
+    }
+}
+
+// the wide state write's tile shape (rows x columns in 64-blocks) and ring depth
+constexpr int kApplyNA = 2, kApplyNB = 2, kApplySlotsWide = 2;
+
+inline bool apply_wide_fits(int64_t D, int64_t F) {
+  return D % (64 * kApplyNA) == 0 && D % (64 * kApplyNB) == 0 && F % (64 * kApplyNA) == 0 && F % (64 * kApplyNB) == 0;
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -2050,7 +2260,16 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
   if (want(L) && rest_part) {
     const dim3 grid(row_tile_blocks(B, 3 * (D / 64) * nF));
     if constexpr (sizeof(T) == 2) {
-      if (gate.next("k_chain_apply_lds")) hipLaunchKernelGGL(k_chain_apply_lds, grid, blk, 0, st, aa);
+      if (gate.next("k_chain_apply_lds")) {
+        if (apply_wide_fits(D, F)) {
+          const int tiles = 2 * (int)((D / (64 * kApplyNA)) * (F / (64 * kApplyNB))) +
+                            (int)((F / (64 * kApplyNA)) * (D / (64 * kApplyNB)));
+          hipLaunchKernelGGL((k_chain_apply_wide<kApplyNA, kApplyNB, kApplySlotsWide>), dim3(row_tile_blocks(B, tiles)),
+                             blk, 0, st, aa);
+        } else {
+          hipLaunchKernelGGL(k_chain_apply_lds, grid, blk, 0, st, aa);
+        }
+      }
     } else if (gate.next("k_chain_apply")) {
       hipLaunchKernelGGL(k_chain_apply<T>, grid, blk, 0, st, aa);
     }
