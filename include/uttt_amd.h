@@ -32,7 +32,7 @@ enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE =
 
 /* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
  * Python binding reads it from this header and refuses a library built from another one. */
-#define UTTT_ABI_VERSION 17
+#define UTTT_ABI_VERSION 18
 
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
@@ -364,7 +364,10 @@ typedef struct {
   const void* k_new; const void* v_new; int64_t kv_new_stride_n; /* (N, Hkv, hd) */
   void* k_ring; void* v_ring; int64_t ring_stride_n; /* (N, Hkv, window, hd) */
   void* out; int64_t o_stride_n;                 /* (N, H, hd) */
-  void* workspace; size_t workspace_bytes;       /* >= uttt_swa_decode_workspace(...) */
+  void* workspace; size_t workspace_bytes;       /* >= uttt_swa_decode_workspace(...); zero-filled
+                                                    before its first use: it ends with per-(request,
+                                                    kv head) merge counters that every call leaves
+                                                    at zero, so calls sharing it must be ordered */
 } uttt_swa_decode_args;
 
 size_t uttt_swa_decode_workspace(int64_t n_req, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,

@@ -417,12 +417,71 @@ __device__ __forceinline__ void unpack8(float (&dst)[8], const uint4* v) {
   }
 }
 
+// The merge of one (request, kv head)'s split partials by the last workgroup to arrive.  Every
+// workgroup has stored its partial device-coherently; each thread waits for its own stores, the
+// workgroup synchronises, one thread raises the counter, and the workgroup that completes the
+// count reads every split's partial device-coherently (past its XCD's L2), merges them as
+// k_swa_decode_combine does (splits in order, 16 at a time) and resets the counter to zero.
+template <typename T, int HD, int NT>
+__device__ void decode_merge(const uttt_swa_decode_args& a, const float* pr0, unsigned* counter, int n, int kvh,
+                             int rep, int nsplit) {
+  __shared__ int last;
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == (unsigned)(nsplit - 1);
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
+  for (int idx = threadIdx.x; idx < rep * HD; idx += NT) {
+    const int r = idx / HD, e = idx - r * HD;
+    float mx = -INFINITY, num = 0.f, den = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += 16) {
+      float m[16], l[16], o[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int s = s0 + k;
+        const float* q = pr0 + (s * rep + r) * (HD + 2);
+        m[k] = s < nsplit ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+        l[k] = s < nsplit ? __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+        o[k] = s < nsplit ? __hip_atomic_load(q + 2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      }
+      float cm = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) cm = fmaxf(cm, m[k]);
+      const float nm = fmaxf(mx, cm);
+      const float scale_old = mx == -INFINITY ? 0.f : expf(mx - nm);
+      num *= scale_old;
+      den *= scale_old;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (m[k] != -INFINITY) {
+          const float f = expf(m[k] - nm);
+          den += l[k] * f;
+          num += o[k] * f;
+        }
+      }
+      mx = nm;
+    }
+    og[idx] = from_f32<T>(num / den);
+  }
+}
+
 // grid (n_req, n_kv_heads, splits of KEYS slots), NT threads.  Split form (the default: NT 256,
 // KEYS kDecodeKeys, REP kMaxRep): softmax partials per split for k_swa_decode_combine.  WHOLE:
 // one workgroup covers the whole window (one split) and writes the normalised output itself,
-// so a step is one launch (bf16, window <= KEYS, at most REP query heads per kv head).
-template <typename T, int HD, int NT = kThreads, int KEYS = kDecodeKeys, int REP = kMaxRep, bool WHOLE = false>
-__global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_args a, float* part) {
+// so a step is one launch.  MERGE: split form in one launch: the partials are written
+// device-coherently, each workgroup then raises its (request, kv head) counter, and the one that
+// completes the count merges the splits (read device-coherently) and resets the counter.
+enum DecodeMode { kSplit = 0, kWhole = 1, kMerge = 2 };
+
+template <typename T, int HD, int NT = kThreads, int KEYS = kDecodeKeys, int REP = kMaxRep, int MODE = kSplit>
+__global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_args a, float* part,
+                                                        unsigned* counters) {
+  constexpr bool WHOLE = MODE == kWhole;
   constexpr int L = HD / 8;                  // lanes per key row (8 elements each)
   constexpr int KPP = NT / L;                // keys per pass
   constexpr int PASSES = KEYS / KPP;         // split form: 2 (HD 64) or 4 (HD 128)
@@ -441,7 +500,7 @@ __global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_ar
   const int64_t W = a.window;
   const int64_t pos = a.positions[n];
   if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) {  // the combine writes NaN
-    if constexpr (WHOLE) {  // position outside the RoPE table: loud NaN output, cache untouched
+    if (MODE != kSplit && sp == 0) {  // position outside the RoPE table: loud NaN output, cache untouched
       T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
       for (int idx = threadIdx.x; idx < rep * HD; idx += NT) og[idx] = from_f32<T>(NAN);
     }
@@ -452,9 +511,18 @@ __global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_ar
   const int j_lo = sp * KEYS, j_hi = min(valid, j_lo + KEYS);
   float* pr = part + (((int64_t)n * a.n_kv_heads + kvh) * nsplit + sp) * rep * (HD + 2);
   if (j_lo >= j_hi) {
-    for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += NT) {
-      const int e = idx % (HD + 2);
-      pr[idx] = e == 0 ? -INFINITY : 0.f;
+    if constexpr (MODE == kMerge) {  // an empty split still arrives: its partial is (-inf, 0, 0)
+      for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += NT) {
+        const int e = idx % (HD + 2);
+        __hip_atomic_store(pr + idx, e == 0 ? -INFINITY : 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      decode_merge<T, HD, NT>(a, pr - (int64_t)sp * rep * (HD + 2), counters + (int64_t)n * a.n_kv_heads + kvh,
+                              n, kvh, rep, nsplit);
+    } else {
+      for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += NT) {
+        const int e = idx % (HD + 2);
+        pr[idx] = e == 0 ? -INFINITY : 0.f;
+      }
     }
     return;
   }
@@ -615,6 +683,12 @@ __global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_ar
     for (int q = 0; q < NW; ++q) v += wred[q][idx];
     if constexpr (WHOLE) {
       og[idx] = from_f32<T>(v / stat[r][1]);
+    } else if constexpr (MODE == kMerge) {
+      __hip_atomic_store(pr + r * (HD + 2) + 2 + e, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (e == 0) {
+        __hip_atomic_store(pr + r * (HD + 2), stat[r][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pr + r * (HD + 2) + 1, stat[r][1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     } else {
       pr[r * (HD + 2) + 2 + e] = v;
       if (e == 0) {
@@ -623,6 +697,9 @@ __global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_ar
       }
     }
   }
+  if constexpr (MODE == kMerge)
+    decode_merge<T, HD, NT>(a, pr - (int64_t)sp * rep * (HD + 2), counters + (int64_t)n * a.n_kv_heads + kvh, n,
+                            kvh, rep, nsplit);
 }
 
 constexpr int kMaxDecodeSplits = 64;
@@ -688,23 +765,42 @@ static void launch_prefill(const uttt_swa_prefill_args& a, const PrefillPlan& p,
                        dim3(kThreads), 0, st, a, (const float*)part, p.nsplit, p.q_pad);
 }
 
-// whole-window decode: one 1024-thread workgroup per (request, kv head) for bf16 rings of up to
-// kWholeKeys slots, head_dim 64 and at most kWholeRep query heads per kv head
+// bf16 rings of up to kMergeSlots slots, head_dim 64 and at most kMergeRep query heads per kv
+// head: one launch, the window split into pieces of kMergeKeys slots merged by the last
+// workgroup (512 workgroups at 32 requests x 4 kv heads x 512 slots).  The whole-window form (one
+// 1024-thread workgroup per request and kv head) is kept for comparison (kDecodeWhole).
+constexpr int kMergeKeys = 128, kMergeSlots = 512, kMergeRep = 4;
 constexpr int kWholeThreads = 1024, kWholeKeys = 512, kWholeRep = 4;
+constexpr bool kDecodeWhole = false;
+
+inline size_t decode_partial_bytes(int64_t n_req, int64_t n_heads, int64_t head_dim, int64_t window) {
+  return align_up(sizeof(float) * (size_t)n_req * (size_t)n_heads * (size_t)decode_splits(window) *
+                  (size_t)(head_dim + 2));
+}
 
 template <typename T, int HD>
 static void launch_decode(const uttt_swa_decode_args& a, hipStream_t st) {
   const int nsplit = decode_splits(a.window);
   float* part = static_cast<float*>(a.workspace);
+  unsigned* counters = reinterpret_cast<unsigned*>(static_cast<char*>(a.workspace) +
+                                                   decode_partial_bytes(a.n_req, a.n_heads, HD, a.window));
   if constexpr (sizeof(T) == 2 && HD == 64) {
-    if (a.window <= kWholeKeys && a.n_heads / a.n_kv_heads <= kWholeRep) {
-      hipLaunchKernelGGL((k_swa_decode_part<T, HD, kWholeThreads, kWholeKeys, kWholeRep, true>),
-                         dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, 1u), dim3(kWholeThreads), 0, st, a, part);
+    if (a.window <= kMergeSlots && a.n_heads / a.n_kv_heads <= kMergeRep) {
+      if constexpr (kDecodeWhole) {
+        hipLaunchKernelGGL((k_swa_decode_part<T, HD, kWholeThreads, kWholeKeys, kWholeRep, kWhole>),
+                           dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, 1u), dim3(kWholeThreads), 0, st, a, part,
+                           counters);
+      } else {
+        const int msplit = (int)((a.window + kMergeKeys - 1) / kMergeKeys);
+        hipLaunchKernelGGL((k_swa_decode_part<T, HD, kThreads, kMergeKeys, kMergeRep, kMerge>),
+                           dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, (unsigned)msplit), dim3(kThreads), 0, st, a,
+                           part, counters);
+      }
       return;
     }
   }
   hipLaunchKernelGGL((k_swa_decode_part<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, (unsigned)nsplit),
-                     dim3(kThreads), 0, st, a, part);
+                     dim3(kThreads), 0, st, a, part, counters);
   hipLaunchKernelGGL((k_swa_decode_combine<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads), dim3(kThreads), 0,
                      st, a, (const float*)part, nsplit);
 }
@@ -779,7 +875,7 @@ extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t st
 extern "C" size_t uttt_swa_decode_workspace(int64_t n_req, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
                                             int64_t window) {
   if (n_req < 1 || n_kv_heads < 1 || n_heads < n_kv_heads || window < 1 || head_dim < 1) return 0;
-  return sizeof(float) * (size_t)n_req * (size_t)n_heads * (size_t)decode_splits(window) * (size_t)(head_dim + 2);
+  return decode_partial_bytes(n_req, n_heads, head_dim, window) + sizeof(unsigned) * (size_t)n_req * (size_t)n_kv_heads;
 }
 
 extern "C" int uttt_swa_decode(const uttt_swa_decode_args* a, uttt_stream_t stream) {

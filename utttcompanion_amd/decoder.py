@@ -211,12 +211,12 @@ class BatchedDecoder:
                                            advance=self.positions)
 
     def _warm_workspaces(self) -> None:
-        lib_ws_attn = 1 << 20
-        nbytes = max(lib_ws_attn, self.n * self.heads * ((self.window + 63) // 64) * (self.hd + 2) * 4)
-        self._ws_attn = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        from . import _native as N
+        # zero-filled: the attention workspace ends with merge counters that every step leaves at zero
+        nbytes = N.load_library().uttt_swa_decode_workspace(self.n, self.heads, self.hkv, self.hd, self.window)
+        self._ws_attn = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=self.device)
         d = self.model.config.d_model
         ff = self.model.config.d_ff_fast
-        from . import _native as N
         code = N.DTYPE_BF16 if self.dtype == torch.bfloat16 else N.DTYPE_F32
         self._ws_read = torch.zeros(max(N.load_library().uttt_readout_workspace(self.n, 1, d, ff, code), 1),
                                     dtype=torch.uint8, device=self.device)
