@@ -32,7 +32,7 @@ enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE =
 
 /* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
  * Python binding reads it from this header and refuses a library built from another one. */
-#define UTTT_ABI_VERSION 18
+#define UTTT_ABI_VERSION 19
 
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
@@ -422,6 +422,73 @@ typedef struct {
 } uttt_skinny_linear_args;
 
 int uttt_skinny_linear(const uttt_skinny_linear_args* args, uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 8b. Slow-weight product out = x W^T (+ residual) for many rows, bf16 operands with fp32
+ *     accumulation.  Replaces the F.linear / h + linear(x) calls of the chunk-first forward pass
+ *     (model/uttt_layer.py:1058-1081 the packed QKV projection, :1193-1231 the packed uTTT
+ *     projections, :1528-1555 the block residual projections) at m = rows x chunk tokens.
+ *     x (m, k), w (n, k) row-major with row strides >= k (multiples of 8 elements, 16-byte
+ *     aligned bases), out (m, n); residual (m, n) may be NULL or alias out.  k % 64 == 0.
+ *     Calls that share a workspace must not overlap.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int64_t m, n, k;
+  int32_t act_dtype; /* UTTT_DTYPE_BF16 */
+  const void* x; int64_t x_row_stride;
+  const void* w; int64_t w_row_stride;
+  const void* residual; int64_t residual_row_stride;
+  void* out; int64_t out_row_stride;
+  void* workspace; size_t workspace_bytes; /* zero-filled once; left zero-filled by every call */
+} uttt_linear_args;
+
+/* Workspace bytes uttt_linear needs for this shape on the current device (0: none; the k loop
+ * is split over several workgroups per output tile only when the tiles do not cover the GPU). */
+size_t uttt_linear_workspace(int64_t m, int64_t n, int64_t k);
+int uttt_linear(const uttt_linear_args* args, uttt_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 8c. One chunk of the chunk-first prefill with fast-weight writes in one call.  Replaces the
+ *     per-chunk loop body of uTTTModel's chunk-first forward (model/uttt_model.py:453-608: per
+ *     layer the block forward of model/uttt_layer.py:1528-1555 through the chunk-start fast
+ *     weights, then the chained updates of :519-608).  Per layer l, on main_stream: the packed
+ *     QKV product (attention input norm folded), RoPE + KV append, sliding-window attention,
+ *     the attention output product into the residual rows, the packed uTTT projection product
+ *     and its epilogue, the readout (with the chain's key products) and the uTTT output product
+ *     into the residual rows; on chain_stream: part 1 of chain stage l after layer l's
+ *     epilogue, part 2 after its readout.  Then the state write (stage n_layers) on
+ *     chain_stream after every layer, and main_stream waits for it.  Each layer's calls are
+ *     the argument structs of the entry points above, built once for a prefill; the executor
+ *     sets the per-chunk fields (rope start_pos / kv_offset, attention q_offset / kv_len =
+ *     kv_offset + q_len, the chain's token_mask / mask_row_stride / surprise) in its own copies.
+ *     The chain args must already name every layer's k / v / eta / alpha (the epilogue's
+ *     outputs).  Calls on one device are serialised; a failing call may leave part of the chunk
+ *     enqueued.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  uttt_linear_args qkv;
+  uttt_rope_append_args rope;
+  uttt_swa_prefill_args attn;
+  uttt_linear_args attn_out;
+  uttt_linear_args proj;
+  uttt_proj_epilogue_args epilogue;
+  uttt_readout_args readout;
+  void* readout_workspace; size_t readout_workspace_bytes;
+  uttt_linear_args uttt_out;
+} uttt_prefill_layer_calls;
+
+typedef struct {
+  int32_t n_layers;                        /* == chain->layers */
+  const uttt_prefill_layer_calls* layers;  /* n_layers entries */
+  const uttt_chunk_chain_args* chain;
+  void* chain_workspace; size_t chain_workspace_bytes;
+  int64_t start_pos;                       /* RoPE position of the chunk's first token */
+  int64_t kv_offset;                       /* KV index of the chunk's first token */
+  const float* token_mask; int64_t mask_row_stride; /* (batch, >= tokens) fp32 or NULL */
+  float* surprise;                         /* (n_layers,) */
+} uttt_prefill_chunk_args;
+
+int uttt_prefill_chunk(const uttt_prefill_chunk_args* args, uttt_stream_t main_stream, uttt_stream_t chain_stream);
 
 /* ---------------------------------------------------------------------------
  * 9. Greedy next-token selection: per row, argmax of the logits with the excluded ids and the

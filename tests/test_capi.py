@@ -43,7 +43,9 @@ def test_struct_layouts_match_the_c_header(tmp_path):
                "uttt_rope_append_args": N.RopeAppendArgs, "uttt_swa_prefill_args": N.SwaPrefillArgs,
                "uttt_swa_decode_args": N.SwaDecodeArgs, "uttt_elastic_pull_args": N.ElasticPullArgs,
                "uttt_chunk_chain_args": N.ChunkChainArgs, "uttt_proj_epilogue_args": N.ProjEpilogueArgs,
-               "uttt_skinny_linear_args": N.SkinnyLinearArgs, "uttt_greedy_args": N.GreedyArgs}
+               "uttt_skinny_linear_args": N.SkinnyLinearArgs, "uttt_greedy_args": N.GreedyArgs,
+               "uttt_layer_update_args": N.LayerUpdateArgs, "uttt_linear_args": N.LinearArgs,
+               "uttt_prefill_layer_calls": N.PrefillLayerCalls, "uttt_prefill_chunk_args": N.PrefillChunkArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')

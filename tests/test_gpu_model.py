@@ -303,8 +303,8 @@ def test_prefill_with_kernel_timer_equals_plain_prefill():
         d_ids, d_mask = ids.to(DEV), mask.to(DEV)
         state = model.init_fast_state(2, device=DEV, dtype=torch.float32, detach=True)
         timer = KernelTimer(("k_chain_back_lds", "k_chain_back", "k_chain_apply_lds", "k_chain_apply"))
-        with torch.no_grad():
-            a = model.prefill_with_writes(d_ids, state, d_mask)
+        with torch.no_grad():  # the timer enqueues launch by launch: compare with that path
+            a = model.prefill_with_writes(d_ids, state, d_mask, executor=False)
             b = model.prefill_with_writes(d_ids, state, d_mask, kernel_timer=timer)
         torch.cuda.synchronize()
         assert torch.equal(a[0], b[0]) and torch.equal(a[2], b[2])
@@ -337,4 +337,64 @@ def test_prefill_graph_replays_match_eager():
                 assert torch.equal(a, e), rep
             assert torch.equal(gout[2], eager[2]), rep
             model(d_ids[:, :16], fast_state=state)  # unrelated eager work between replays
+            torch.cuda.synchronize()
+
+
+def test_prefill_chunk_executor_matches_per_call_path():
+    """bf16: one ``uttt_prefill_chunk`` call per chunk (slow-weight products on ``uttt_linear``)
+    against the launch-by-launch path (the same kernels, products on torch), with a token mask,
+    a ragged last chunk (two plans), and a second prefill continuing from the first's KV caches
+    (history offsets and positions).  The two differ only in the products' accumulation order
+    (one bf16 rounding of each product either way, carried through the layers): hidden rows and
+    KV caches within 2e-2 relative (max|diff| / max|ref|; a few bf16 ulps of the largest
+    values), fast-weight state within 2e-2 max-abs (the bf16 bar), surprise within 1e-2
+    relative."""
+    model, _ = build(dtype=torch.bfloat16)
+    ids, mask = ids_and_mask(2, 72, 256, seed=41)  # 4 chunks of 16 + one of 8
+    ids2, mask2 = ids_and_mask(2, 40, 256, seed=42)
+    d_ids, d_mask, d_ids2, d_mask2 = ids.to(DEV), mask.to(DEV), ids2.to(DEV), mask2.to(DEV)
+    state = model.init_fast_state(2, device=DEV, dtype=torch.float32, detach=True)
+    outs = []
+    with torch.no_grad():
+        for executor in (True, False):
+            a = model.prefill_with_writes(d_ids, state, d_mask, executor=executor)
+            nxt = model.init_fast_state(2, device=DEV, dtype=torch.float32, detach=True)
+            for t, n in zip(a[1], NAMES):
+                getattr(nxt, n).copy_(t)
+            b = model.prefill_with_writes(d_ids2, nxt, d_mask2, kv_caches=a[3], start_pos=72, executor=executor)
+            outs.append((a, b))
+    torch.cuda.synchronize()
+    (ea, eb), (pa, pb) = outs
+    for x, y in ((ea, pa), (eb, pb)):
+        assert x[0].dtype == torch.bfloat16 and torch.isfinite(x[0].float()).all()
+        assert rel_err(x[0], y[0]) <= 2e-2
+        for n, t, u in zip(NAMES, x[1], y[1]):
+            assert max_abs(t, u) <= 2e-2, n
+        assert rel_err(x[2], y[2]) <= 1e-2
+        for (k1, v1), (k2, v2) in zip(x[3], y[3]):
+            assert k1.shape == k2.shape and rel_err(k1, k2) <= 2e-2 and rel_err(v1, v2) <= 2e-2
+
+
+def test_prefill_chunk_executor_graph_replays_match_eager():
+    """The executor path (bf16) recorded in one HIP graph: its native events join the chain
+    stream into the capture; replays with eager work between them equal the eager result."""
+    model, _ = build(dtype=torch.bfloat16)
+    ids, mask = ids_and_mask(2, 48, 256, seed=43)
+    d_ids, d_mask = ids.to(DEV), mask.to(DEV)
+    state = model.init_fast_state(2, device=DEV, dtype=torch.float32, detach=True)
+    with torch.no_grad():
+        h, tensors, per_layer, _ = model.prefill_with_writes(d_ids, state, d_mask)
+        eager = (h.clone(), [t.clone() for t in tensors], per_layer.clone())
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gout = model.prefill_with_writes(d_ids, state, d_mask)
+        for rep in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(gout[0], eager[0]), rep
+            for a, e in zip(gout[1], eager[1]):
+                assert torch.equal(a, e), rep
+            assert torch.equal(gout[2], eager[2]), rep
+            model.prefill_with_writes(d_ids[:, :16], state)  # unrelated eager work between replays
             torch.cuda.synchronize()

@@ -74,6 +74,17 @@ class LayerUpdateArgs(C.Structure):
     ]
 
 
+class LinearArgs(C.Structure):
+    _fields_ = [
+        ("m", _I64), ("n", _I64), ("k", _I64), ("act_dtype", _I32),
+        ("x", _P), ("x_row_stride", _I64),
+        ("w", _P), ("w_row_stride", _I64),
+        ("residual", _P), ("residual_row_stride", _I64),
+        ("out", _P), ("out_row_stride", _I64),
+        ("workspace", _P), ("workspace_bytes", C.c_size_t),
+    ]
+
+
 class ChunkChainArgs(C.Structure):
     _fields_ = [
         ("batch", _I64), ("layers", _I64), ("tokens", _I64), ("d_model", _I64), ("d_ff", _I64),
@@ -192,6 +203,23 @@ class ElasticPullArgs(C.Structure):
 
 
 # exported symbol -> (restype, argtypes)
+class PrefillLayerCalls(C.Structure):
+    _fields_ = [
+        ("qkv", LinearArgs), ("rope", RopeAppendArgs), ("attn", SwaPrefillArgs), ("attn_out", LinearArgs),
+        ("proj", LinearArgs), ("epilogue", ProjEpilogueArgs), ("readout", ReadoutArgs),
+        ("readout_workspace", _P), ("readout_workspace_bytes", C.c_size_t), ("uttt_out", LinearArgs),
+    ]
+
+
+class PrefillChunkArgs(C.Structure):
+    _fields_ = [
+        ("n_layers", _I32), ("layers", C.POINTER(PrefillLayerCalls)), ("chain", C.POINTER(ChunkChainArgs)),
+        ("chain_workspace", _P), ("chain_workspace_bytes", C.c_size_t),
+        ("start_pos", _I64), ("kv_offset", _I64),
+        ("token_mask", _P), ("mask_row_stride", _I64), ("surprise", _P),
+    ]
+
+
 SIGNATURES = {
     "uttt_last_error": (C.c_char_p, []),
     "uttt_abi_version": (C.c_int, []),
@@ -203,6 +231,9 @@ SIGNATURES = {
     "uttt_layer_update_resident_workspace": (C.c_size_t, [_I64, _I64]),
     "uttt_layer_update_resident_flag_offset": (C.c_size_t, [_I64, _I64]),
     "uttt_layer_update_resident": (C.c_int, [C.POINTER(LayerUpdateArgs), _P, C.c_size_t, _P]),
+    "uttt_linear": (C.c_int, [C.POINTER(LinearArgs), _P]),
+    "uttt_linear_workspace": (C.c_size_t, [_I64, _I64, _I64]),
+    "uttt_prefill_chunk": (C.c_int, [C.POINTER(PrefillChunkArgs), _P, _P]),
     "uttt_chunk_chain_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_chunk_chain": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_chain_stage": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _P]),

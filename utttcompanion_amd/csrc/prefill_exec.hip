@@ -1,0 +1,117 @@
+// One chunk of the chunk-first prefill with fast-weight writes, enqueued by one host call
+// (reference uTTTModel's chunk-first forward, model/uttt_model.py:453-608: per chunk, every
+// layer's block forward, model/uttt_layer.py:1528-1555, reading the chunk-start fast weights,
+// then the layers' chained updates, :519-608).
+//
+// The work is the same launches the per-call entry points make, in the same order on the same
+// two streams: per layer, the forward pass on the main stream and stage l of the layer chain on
+// the chain stream, part 1 after the layer's projections and part 2 after its readout, then the
+// state write after the last layer, which the main stream waits for.  What changes is the host
+// side: a chunk costs one call into the library instead of one binding call per launch, so the
+// host enqueues a chunk's ~14 launches per layer in far less time than the GPU runs them, and
+// the two streams stay fed.
+#include <mutex>
+#include <vector>
+
+#include "uttt_host.h"
+
+namespace uttt {
+namespace {
+
+// Two events per layer (projections done, readout done) and two for the chunk's joins, created
+// once per device.  One call at a time per device uses them (the mutex), so a record and the
+// wait that follows it are never interleaved with another call's.
+struct ExecEvents {
+  std::mutex lock;
+  std::vector<hipEvent_t> ev;
+  bool ready = false;
+};
+
+constexpr int kMaxDevices = 64;
+constexpr int kEventsPerCall = 2 * UTTT_MAX_CHAIN + 2;
+
+ExecEvents& device_events(int dev) {
+  static ExecEvents pool[kMaxDevices];
+  return pool[dev];
+}
+
+int make_events(ExecEvents& e) {
+  if (e.ready) return UTTT_OK;
+  e.ev.assign(kEventsPerCall, nullptr);
+  for (auto& h : e.ev) {
+    const hipError_t rc = hipEventCreateWithFlags(&h, hipEventDisableTiming);
+    if (rc != hipSuccess) return fail(UTTT_ERR_HIP, "uttt_prefill_chunk: event creation: %s", hipGetErrorString(rc));
+  }
+  e.ready = true;
+  return UTTT_OK;
+}
+
+int hip_status(hipError_t rc, const char* what) {
+  return rc == hipSuccess ? UTTT_OK : fail(UTTT_ERR_HIP, "uttt_prefill_chunk: %s: %s", what, hipGetErrorString(rc));
+}
+
+}  // namespace
+}  // namespace uttt
+
+using namespace uttt;
+
+#define UTTT_TRY(call)            \
+  do {                            \
+    const int rc_ = (call);       \
+    if (rc_ != UTTT_OK) return rc_; \
+  } while (0)
+
+extern "C" int uttt_prefill_chunk(const uttt_prefill_chunk_args* a, uttt_stream_t main_stream,
+                                  uttt_stream_t chain_stream) {
+  UTTT_REQUIRE(a != nullptr && a->layers != nullptr && a->chain != nullptr, "args, layers and chain must be non-NULL");
+  UTTT_REQUIRE(a->n_layers >= 1 && a->n_layers <= UTTT_MAX_CHAIN && a->n_layers == a->chain->layers,
+               "n_layers (%d) must equal the chain's layer count (%lld), 1..%d", (int)a->n_layers,
+               (long long)a->chain->layers, UTTT_MAX_CHAIN);
+  UTTT_REQUIRE(a->start_pos >= 0 && a->kv_offset >= 0, "start_pos and kv_offset must be >= 0");
+  UTTT_REQUIRE(main_stream != chain_stream, "the chain needs a stream of its own");
+  int dev = 0;
+  UTTT_TRY(hip_status(hipGetDevice(&dev), "hipGetDevice"));
+  UTTT_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  ExecEvents& events = device_events(dev);
+  std::lock_guard<std::mutex> guard(events.lock);
+  UTTT_TRY(make_events(events));
+  hipStream_t ms = static_cast<hipStream_t>(main_stream), cs = static_cast<hipStream_t>(chain_stream);
+
+  uttt_chunk_chain_args chain = *a->chain;  // this chunk's mask and surprise row
+  chain.token_mask = a->token_mask;
+  chain.mask_row_stride = a->token_mask != nullptr ? a->mask_row_stride : 0;
+  chain.surprise = a->surprise;
+  const int L = a->n_layers;
+  for (int l = 0; l < L; ++l) {
+    const uttt_prefill_layer_calls& c = a->layers[l];
+    uttt_rope_append_args rope = c.rope;
+    rope.start_pos = a->start_pos;
+    rope.kv_offset = a->kv_offset;
+    uttt_swa_prefill_args attn = c.attn;
+    attn.q_offset = a->kv_offset;
+    attn.kv_len = a->kv_offset + attn.q_len;
+    hipEvent_t projected = events.ev[2 * l], read = events.ev[2 * l + 1];
+    UTTT_TRY(uttt_linear(&c.qkv, ms));
+    UTTT_TRY(uttt_rope_kv_append(&rope, ms));
+    UTTT_TRY(uttt_swa_prefill(&attn, ms));
+    UTTT_TRY(uttt_linear(&c.attn_out, ms));
+    UTTT_TRY(uttt_linear(&c.proj, ms));
+    UTTT_TRY(uttt_proj_epilogue(&c.epilogue, ms));
+    UTTT_TRY(hip_status(hipEventRecord(projected, ms), "hipEventRecord"));
+    UTTT_TRY(uttt_swiglu_readout(&c.readout, c.readout_workspace, c.readout_workspace_bytes, ms));
+    UTTT_TRY(hip_status(hipEventRecord(read, ms), "hipEventRecord"));
+    UTTT_TRY(uttt_linear(&c.uttt_out, ms));
+    UTTT_TRY(hip_status(hipStreamWaitEvent(cs, projected, 0), "hipStreamWaitEvent"));
+    UTTT_TRY(uttt_chunk_chain_stage_part(&chain, a->chain_workspace, a->chain_workspace_bytes, l, 1, cs));
+    UTTT_TRY(hip_status(hipStreamWaitEvent(cs, read, 0), "hipStreamWaitEvent"));
+    UTTT_TRY(uttt_chunk_chain_stage_part(&chain, a->chain_workspace, a->chain_workspace_bytes, l, 2, cs));
+  }
+  // the state write follows every reader of the chunk-start state; the next chunk follows it
+  hipEvent_t fwd_done = events.ev[2 * UTTT_MAX_CHAIN], chain_done = events.ev[2 * UTTT_MAX_CHAIN + 1];
+  UTTT_TRY(hip_status(hipEventRecord(fwd_done, ms), "hipEventRecord"));
+  UTTT_TRY(hip_status(hipStreamWaitEvent(cs, fwd_done, 0), "hipStreamWaitEvent"));
+  UTTT_TRY(uttt_chunk_chain_stage(&chain, a->chain_workspace, a->chain_workspace_bytes, L, cs));
+  UTTT_TRY(hip_status(hipEventRecord(chain_done, cs), "hipEventRecord"));
+  UTTT_TRY(hip_status(hipStreamWaitEvent(ms, chain_done, 0), "hipStreamWaitEvent"));
+  return ok();
+}

@@ -724,13 +724,17 @@ def chunk_chain(*args, **kwargs) -> Tuple[Tensor, Optional[Tensor]]:
 
 def proj_epilogue(y: Tensor, dim: int, q_weight: Tensor, k_weight: Tensor, eps: float, inner_lr: float,
                   weight_decay: float, x: Optional[Tensor] = None, x_eps: float = 0.0,
-                  eta_alpha_bias: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+                  eta_alpha_bias: Optional[Tensor] = None, outs: Optional[Tuple[Tensor, Tensor]] = None,
+                  build_only: bool = False):
     """q, k, v, eta, alpha from the packed slow-projection product y (..., 3 D + 2)
     (``uttt_proj_epilogue``; the RMSNorm / sigmoid part of reference fused_slow_projections,
     model/uttt_layer.py:1193-1231).  Returns q, k, v (..., D) and eta, alpha (..., 1).
     With ``x`` (..., D), the un-normalised rows y was projected from by a weight with the input
     RMSNorm weight folded in and no bias, y's rows are scaled by 1 / sqrt(mean(x^2) + x_eps)
-    and ``eta_alpha_bias`` (2,) is added to its last two entries first."""
+    and ``eta_alpha_bias`` (2,) is added to its last two entries first.  ``outs`` = (qkv, ea),
+    contiguous (3, rows, D) and (2, rows) tensors in y's dtype, receive the results;
+    ``build_only`` returns (``uttt_proj_epilogue_args``, the tensors it points at) without
+    launching."""
     if y.shape[-1] != 3 * dim + 2:
         raise ValueError(f"y must end in 3 * d_model + 2 = {3 * dim + 2} features, got {y.shape[-1]}")
     code = _act_code(y.dtype)
@@ -742,8 +746,15 @@ def proj_epilogue(y: Tensor, dim: int, q_weight: Tensor, k_weight: Tensor, eps: 
     if y2.stride(1) != 1:
         y2 = y2.contiguous()
     rows = y2.shape[0]
-    qkv = torch.empty((3, rows, dim), dtype=y.dtype, device=dev)
-    ea = torch.empty((2, rows), dtype=y.dtype, device=dev)
+    if outs is None:
+        qkv = torch.empty((3, rows, dim), dtype=y.dtype, device=dev)
+        ea = torch.empty((2, rows), dtype=y.dtype, device=dev)
+    else:
+        qkv, ea = outs
+        if qkv.shape != (3, rows, dim) or ea.shape != (2, rows) or not qkv.is_contiguous() \
+                or not ea.is_contiguous() or qkv.dtype != y.dtype or ea.dtype != y.dtype:
+            raise ValueError(f"outs must be contiguous (3, {rows}, {dim}) and (2, {rows}) tensors in y's dtype")
+        _require_device(dev, qkv, ea)
     qw = q_weight.detach().to(y.dtype).contiguous()  # the reference casts the weights to x's dtype
     kw = k_weight.detach().to(y.dtype).contiguous()
     a = N.ProjEpilogueArgs()
@@ -763,6 +774,8 @@ def proj_epilogue(y: Tensor, dim: int, q_weight: Tensor, k_weight: Tensor, eps: 
         keep = eta_alpha_bias.detach().to(y.dtype).contiguous()
         _require_device(dev, x, keep)
         a.x, a.x_row_stride, a.x_eps, a.eta_alpha_bias = _p(x2), x2.stride(0), float(x_eps), _p(keep)
+    if build_only:
+        return a, (y2, qw, kw, keep, qkv, ea)
     lib = N.load_library()
     with torch.cuda.device(dev):
         N.check(lib.uttt_proj_epilogue(C.byref(a), _stream(dev)), "uttt_proj_epilogue")
@@ -808,6 +821,81 @@ def skinny_linear(x: Tensor, weight: Tensor, out: Optional[Tensor] = None,
     with torch.cuda.device(dev):
         N.check(lib.uttt_skinny_linear(C.byref(a), _stream(dev)), "uttt_skinny_linear")
     return out
+
+
+_LINEAR_WS: dict = {}
+
+
+def _linear_workspace(dev: torch.device, nbytes: int) -> Tensor:
+    """The device's zero-filled ``uttt_linear`` workspace, grown to at least ``nbytes`` (every
+    call leaves it zero-filled, so one buffer serves every call made in stream order)."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _LINEAR_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _LINEAR_WS[key] = ws
+    return ws
+
+
+def linear(x: Tensor, weight: Tensor, out: Optional[Tensor] = None, residual: Optional[Tensor] = None,
+           workspace: Optional[Tensor] = None, build_only: bool = False):
+    """out = x weight^T (+ residual) for many bf16 rows (``uttt_linear``): the chunk-first forward
+    pass's slow-weight projections (reference model/uttt_layer.py:1058-1081 the packed QKV
+    projection, :1193-1231 the packed uTTT projections, :1528-1555 the ``h + linear(x)``
+    residuals).  x (m, k) and weight (n, k) with unit column stride, 16-byte aligned, row strides
+    multiples of 8 elements, k a multiple of 64; ``residual`` (m, n) may be ``out`` itself.
+    ``workspace`` (uint8, zero-filled) defaults to one buffer per device shared by every call:
+    calls on concurrent streams must each pass their own.  ``build_only`` returns the validated
+    ``uttt_linear_args`` without launching (``out`` and, when the shape needs one, ``workspace``
+    must then be given)."""
+    if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError(f"x (m, k) and weight (n, k) must agree on k, got {tuple(x.shape)} and {tuple(weight.shape)}")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("linear takes bf16 x and weight")
+    dev = x.device
+    _require_device(dev, weight, out, residual)
+    _forward_only(x)
+    m, k = x.shape
+    n = weight.shape[0]
+    if x.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("x and weight need unit column stride")
+    if out is None:
+        out = torch.empty((m, n), dtype=x.dtype, device=dev)
+    for name, t in (("out", out), ("residual", residual)):
+        if t is not None and (t.shape != (m, n) or t.dtype != x.dtype or t.stride(1) != 1):
+            raise ValueError(f"{name} must be ({m}, {n}) bf16 with unit column stride")
+    a = N.LinearArgs()
+    a.m, a.n, a.k, a.act_dtype = m, n, k, N.DTYPE_BF16
+    a.x, a.x_row_stride = _p(x), x.stride(0)
+    a.w, a.w_row_stride = _p(weight), weight.stride(0)
+    if residual is not None:
+        a.residual, a.residual_row_stride = _p(residual), residual.stride(0)
+    a.out, a.out_row_stride = _p(out), out.stride(0)
+    lib = N.load_library()
+    with torch.cuda.device(dev):
+        need = lib.uttt_linear_workspace(m, n, k)
+        if need:
+            if workspace is None:
+                if build_only:
+                    raise ValueError(f"this shape needs a workspace of {need} bytes")
+                workspace = _linear_workspace(dev, need)
+            _require_device(dev, workspace)
+            if workspace.numel() * workspace.element_size() < need:
+                raise ValueError(f"the workspace holds fewer than the {need} bytes this shape needs")
+            a.workspace, a.workspace_bytes = _p(workspace), workspace.numel() * workspace.element_size()
+        if build_only:
+            return a
+        N.check(lib.uttt_linear(C.byref(a), _stream(dev)), "uttt_linear")
+    return out
+
+
+def linear_fits(x: Tensor, weight: Tensor) -> bool:
+    """Whether ``linear`` takes these operands: bf16, k % 64 == 0, unit column stride, aligned
+    bases and row strides."""
+    return (x.dim() == 2 and weight.dim() == 2 and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+            and x.shape[1] == weight.shape[1] and x.shape[1] % 64 == 0 and x.shape[0] >= 1
+            and x.stride(1) == 1 and weight.stride(1) == 1 and x.stride(0) % 8 == 0 and weight.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
 
 
 def greedy_select(logits: Tensor, banned: Sequence[int] = (), active_limit: Optional[int] = None,
@@ -859,7 +947,7 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
                    workspace: Optional[Tensor] = None, keys: Optional[Tensor] = None,
                    key_outputs: Optional[Tuple[Tensor, Tensor]] = None,
                    x_norm: Optional[Tuple[Tensor, float]] = None,
-                   row_counters: Optional[Tensor] = None) -> Tensor:
+                   row_counters: Optional[Tensor] = None, build_only: bool = False):
     """f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down) with per-row (or shared) W.
 
     W is read as fp32 masters, or -- when x and all three weights are bf16 -- as bf16 read
@@ -872,7 +960,9 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
     One bf16 token per row only: ``x_norm`` = (weight, eps) reads out RMSNorm(x) with that
     weight instead of x (the decode step's q_norm), and ``row_counters`` (B,) int32, zero before
     the first call and left zero by every call, makes the readout a single launch (the
-    LayerNorm runs in each row's last weight block); calls sharing counters must not overlap."""
+    LayerNorm runs in each row's last weight block); calls sharing counters must not overlap.
+    ``build_only`` returns (``uttt_readout_args``, workspace, the tensors they point at) without
+    launching."""
     if x.dim() != 3:
         raise ValueError(f"x must be (B, T, D), got {tuple(x.shape)}")
     bsz, tokens, dim = x.shape
@@ -933,6 +1023,8 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
             raise ValueError(f"row_counters must be a contiguous int32 tensor of >= {bsz} entries")
         _require_device(dev, row_counters)
         a.row_counters = _p(row_counters)
+    if build_only:
+        return a, workspace, (x, parts, ln_w, ln_b, out, keys, keep)
     with torch.cuda.device(dev):
         N.check(lib.uttt_swiglu_readout(C.byref(a), _p(workspace), workspace.numel(), _stream(dev)),
                 "uttt_swiglu_readout")
@@ -946,12 +1038,13 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
 
 def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, start_pos: int,
                    k_cache: Tensor, v_cache: Tensor, kv_offset: int, x: Optional[Tensor] = None,
-                   x_eps: float = 0.0) -> None:
+                   x_eps: float = 0.0, build_only: bool = False):
     """Rotate ``q`` (B, T, H, hd) in place; write rotated ``k`` and ``v`` (B, T, Hkv, hd) into
     ``k_cache``/``v_cache`` (B, Hkv, L, hd) at time ``kv_offset + t``.  RoPE position of
     token t is ``start_pos + t``; cos/sin are fp32 (positions, hd) tables.  With ``x`` (B, T, D),
     the un-normalised input of a projection whose RMSNorm weight was folded into the weight,
-    token t's q / k / v are first scaled by 1 / sqrt(mean(x_t^2) + x_eps)."""
+    token t's q / k / v are first scaled by 1 / sqrt(mean(x_t^2) + x_eps).  ``build_only``
+    returns the validated ``uttt_rope_append_args`` without launching."""
     bsz, tokens, heads, hd = q.shape
     hkv = k.shape[2]
     if k.shape != (bsz, tokens, hkv, hd) or v.shape != k.shape:
@@ -993,6 +1086,8 @@ def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, st
             raise ValueError("a folded norm needs eps > 0")
         _require_device(dev, x)
         a.x, a.x_stride_b, a.x_stride_t, a.x_dim, a.x_eps = _p(x), x.stride(0), x.stride(1), x.shape[2], float(x_eps)
+    if build_only:
+        return a
     lib = N.load_library()
     with torch.cuda.device(dev):
         N.check(lib.uttt_rope_kv_append(C.byref(a), _stream(dev)), "uttt_rope_kv_append")
@@ -1004,10 +1099,12 @@ def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, st
 
 def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
                 out: Optional[Tensor] = None, kv_len: Optional[int] = None,
-                workspace: Optional[Tensor] = None) -> Tensor:
+                workspace: Optional[Tensor] = None, build_only: bool = False):
     """q (B, H, Tq, hd), k/v (B, Hkv, Tkv, hd) (any strides with hd contiguous).  Query i sits
     at key index q_offset + i and sees key j iff 0 <= q_offset + i - j < window.  ``out``
-    (B, H, Tq, hd) may be a strided view, e.g. of a (B, Tq, H, hd) buffer."""
+    (B, H, Tq, hd) may be a strided view, e.g. of a (B, Tq, H, hd) buffer.  ``build_only``
+    returns the validated ``uttt_swa_prefill_args`` without launching (the operands must then
+    be usable as they are, and ``out`` and ``workspace`` given)."""
     bsz, heads, tq, hd = q.shape
     hkv, tkv = k.shape[1], k.shape[2] if kv_len is None else kv_len
     if k.shape[0] != bsz or k.shape[3] != hd or v.shape != k.shape or heads % hkv:
@@ -1026,6 +1123,8 @@ def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
         if t.stride(-1) != 1:
             raise ValueError("the head dimension must be contiguous")
         if t.data_ptr() % 16 or any(st % vec for st in t.stride()[:3]):
+            if build_only:
+                raise ValueError("q/k/v need 16-byte aligned rows for a prepared call")
             t = t.contiguous()  # the kernel reads 16-byte vectors
         fixed.append(t)
     q, k, v = fixed
@@ -1048,6 +1147,8 @@ def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
     if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
         workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     a.workspace, a.workspace_bytes = _p(workspace), workspace.numel()
+    if build_only:
+        return a
     with torch.cuda.device(dev):
         N.check(lib.uttt_swa_prefill(C.byref(a), _stream(dev)), "uttt_swa_prefill")
     return out

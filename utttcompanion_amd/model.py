@@ -28,6 +28,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import kernels as K
+from .prefill_plan import PrefillPlan, plan_supported
 from .layer import FastWeightState, RMSNorm, SharedFastWeightPool, linear_residual, require_write_chunk, uTTTBlock
 
 Tensor = torch.Tensor
@@ -213,9 +214,12 @@ class uTTTModel(nn.Module):
     def prefill_with_writes(self, input_ids: Tensor, state: FastWeightState,
                             attention_mask: Optional[Tensor] = None,
                             kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0,
-                            kernel_timer: Optional["K.KernelTimer"] = None):
+                            kernel_timer: Optional["K.KernelTimer"] = None, executor: bool = True):
         """Chunk-first forward with fast-weight writes, without any host synchronisation.
         ``kernel_timer`` (measurement only) records events around the chain kernels it follows.
+        With bf16 activations each chunk goes to the GPU in one call (``uttt_prefill_chunk``,
+        ``PrefillPlan``); ``executor=False`` (or a ``kernel_timer``) enqueues it launch by launch
+        from here instead, with the slow-weight products on torch.
 
         Per chunk: every layer's attention, projections and fast-weight readout run first
         (all readouts read the chunk-start state, reference uttt_model.py:519-608), then one
@@ -269,6 +273,30 @@ class uTTTModel(nn.Module):
         # readout reads the chunk-start state); the state write joins after the last readout
         main = torch.cuda.current_stream(dev)
         side = self._chain_stream(dev)
+        if executor and kernel_timer is None and plan_supported(self, h, copies):
+            mask_f = None
+            if attention_mask is not None:
+                mask_f = attention_mask.to(device=dev, dtype=torch.float32).contiguous()
+                counts = F.pad(mask_f, (0, n_chunks * c - seq)).view(bsz, n_chunks, c).sum(dim=(0, 2))
+            plans: Dict[int, PrefillPlan] = {}
+            ws_chain = None
+            for ci in range(n_chunks):
+                off = ci * c
+                tokens = min(seq, off + c) - off
+                plan = plans.get(tokens)
+                if plan is None:
+                    run = K.ChunkChainRun(n_layers, tokens, cur, ln_w, ln_b, None, pool.momentum_beta, clip,
+                                          pool.normalize_loss_by_dim, pool.eps, h.dtype, copies=copies,
+                                          surprise=surprises[ci], workspace=ws_chain, w_products_given=True)
+                    ws_chain = run.workspace
+                    plan = PrefillPlan(self, bsz, tokens, dev, k_bufs, v_bufs, hist + seq, start_pos + seq, read,
+                                       ln_w, ln_b, pool.eps, run)
+                    plans[tokens] = plan
+                plan.run(h, off, start_pos + off, hist + off, mask_f, surprises[ci], main, side)
+            per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
+            caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win
+                      else (kb, vb) for kb, vb in zip(k_bufs, v_bufs)]
+            return h, cur, per_layer, caches
         ws_chain = ws_read = None
         # bf16: each layer's readout also forms the chain's products of that layer's keys with
         # W_up / W_gate (one read of those weights for both), and the chain stage runs in two
