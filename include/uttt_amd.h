@@ -213,7 +213,8 @@ int uttt_chunk_chain_stage(const uttt_chunk_chain_args* args, void* workspace, s
 /* One part of stage `stage`: part 1 launches its snapshot products and key Gram rows (they read
  * only the keys of layers <= stage and the chunk-start state), part 2 the rest; part 1 then part
  * 2 on one stream equals uttt_chunk_chain_stage (part 0).  Part 1 of stage l may run beside
- * part 2 of stage l - 1 (on another stream): they touch disjoint workspace slots.  With
+ * part 2 of any stage m < l (on another stream, the parts 1 in order on theirs): they touch
+ * disjoint workspace slots.  With
  * w_products_given, part 2 of stage l must follow the caller's writes of layer l's products. */
 int uttt_chunk_chain_stage_part(const uttt_chunk_chain_args* args, void* workspace, size_t workspace_bytes,
                                 int32_t stage, int32_t part, uttt_stream_t stream);
@@ -339,7 +340,9 @@ typedef struct {
   const void* k; int64_t k_stride_b, k_stride_h, k_stride_t;
   const void* v; int64_t v_stride_b, v_stride_h, v_stride_t;
   void* out; int64_t o_stride_b, o_stride_h, o_stride_t;
-  void* workspace; size_t workspace_bytes; /* >= uttt_swa_prefill_workspace(...) */
+  /* >= uttt_swa_prefill_workspace(...) bytes, zero-filled before the first call; every call
+   * leaves it zero-filled (split counters), so calls sharing it must not overlap */
+  void* workspace; size_t workspace_bytes;
 } uttt_swa_prefill_args;
 
 size_t uttt_swa_prefill_workspace(int64_t batch, int64_t n_heads, int64_t q_len, int64_t kv_len, int64_t head_dim,

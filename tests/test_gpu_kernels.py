@@ -326,20 +326,29 @@ def test_swa_prefill_matches_oracle(case, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_swa_prefill_ignores_stale_workspace_contents(dtype):
-    """Splits with no visible key leave their partial rows unwritten; a workspace full of
-    NaN (reused memory) must not leak into the output.  Single-query steps exercise it."""
+    """Splits with no visible key leave their partial rows unwritten; partial rows full of
+    NaN (reused memory) must not leak into the output.  Single-query steps exercise it.  The
+    split counters at the end of the workspace start at zero (the contract) and are left
+    zero."""
+    from utttcompanion_amd import _native as N
     K = kernels()
+    lib = N.load_library()
     g = torch.Generator().manual_seed(41)
     for tkv, win in ((21, 24), (70, 8), (300, 128)):
         q = torch.randn(1, 1, 2, 64, generator=g).to(dtype).transpose(1, 2)
         k = torch.randn(1, 1, tkv, 64, generator=g).to(dtype)
         v = torch.randn(1, 1, tkv, 64, generator=g).to(dtype)
         ref = om.sliding_window_attention(q.float(), k.float(), v.float(), win, tkv - 1)
+        nbytes = lib.uttt_swa_prefill_workspace(1, 2, 1, tkv, 64, win)
         ws = torch.full((1 << 22,), float("nan"), device=DEV).view(torch.uint8)
+        if nbytes > 16:
+            ws[nbytes - 8:nbytes].zero_()  # one counter per (row, head, q tile): 1 x 2 x 1
         with torch.no_grad():
             got = K.swa_prefill(*to_dev(q, k, v), win, tkv - 1, workspace=ws)
         torch.cuda.synchronize()
         assert torch.isfinite(got).all(), (tkv, win)
+        if nbytes > 16:
+            assert not ws[nbytes - 8:nbytes].any(), "the counters are left zero"
         tol = F32_REL if dtype == torch.float32 else BF16_ABS
         err = rel_err(got, ref) if dtype == torch.float32 else max_abs(got, ref)
         assert err <= tol, (tkv, win, err)
@@ -427,11 +436,23 @@ def test_swa_decode_wide_windows_bf16(win, hkv):
         assert torch.equal(dk[r, :, p % win].cpu(), rk[r, :, p]), "the new key goes to slot pos mod window"
 
 
+def padded(t):
+    """t (..., n) as a view of a buffer whose rows are padded to a whole number of 16-byte
+    vectors: the form the one-wave-per-row epilogue (16-byte accesses) takes."""
+    vec = 16 // t.element_size()
+    n = t.shape[-1]
+    buf = torch.full((*t.shape[:-1], (n + vec - 1) // vec * vec), float("nan"), dtype=t.dtype, device=t.device)
+    buf[..., :n] = t
+    return buf[..., :n]
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_proj_epilogue_matches_oracle(dtype):
+def test_proj_epilogue_matches_oracle(dtype, layout):
     """q/k/v RMSNorm and eta/alpha sigmoid of the packed projection (reference
     fused_slow_projections, model/uttt_layer.py:1193-1231) against the oracle's ops in fp32:
-    fp32 <= 1e-6 relative; bf16 within one bf16 rounding of the fp32 result (2^-8 relative)."""
+    fp32 <= 1e-6 relative; bf16 within one bf16 rounding of the fp32 result (2^-8 relative).
+    ``padded`` rows (16-byte multiples, NaN past the row) take the one-wave-per-row kernel."""
     K = kernels()
     g = torch.Generator().manual_seed(17)
     rows, d = 37, 192
@@ -443,15 +464,19 @@ def test_proj_epilogue_matches_oracle(dtype):
            om.rms_norm(yf[..., 2 * d:3 * d], None, 1e-5), 0.01 * torch.sigmoid(yf[..., 3 * d:3 * d + 1]),
            0.005 * torch.sigmoid(yf[..., 3 * d + 1:]))
     with torch.no_grad():
-        got = K.proj_epilogue(y_in.to(DEV), d, qw.to(DEV, dtype), kw.to(DEV, dtype), 1e-5, 0.01, 0.005)
+        y_dev = y_in.to(DEV)
+        if layout == "padded":
+            y_dev = padded(y_dev)
+        got = K.proj_epilogue(y_dev, d, qw.to(DEV, dtype), kw.to(DEV, dtype), 1e-5, 0.01, 0.005)
     for name, a, e in zip(("q", "k", "v", "eta", "alpha"), got, ref):
         assert a.shape == e.shape and a.dtype == dtype, name
         err = ((a.float().cpu() - e).abs() / e.abs().clamp_min(1e-6)).max().item()
         assert err <= (1e-6 if dtype == torch.float32 else 2.0 ** -8), f"{name}: rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("layout", ["packed", "padded"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_proj_epilogue_folded_norm(dtype):
+def test_proj_epilogue_folded_norm(dtype, layout):
     """With the GEMM input x given, y's rows are scaled by 1 / sqrt(mean(x^2) + eps) and the eta /
     alpha biases added before the q/k/v RMSNorm and the sigmoids: against the same steps in fp32
     from the same (rounded) y, fp32 <= 1e-5 relative, bf16 within 2^-7 relative."""
@@ -470,7 +495,8 @@ def test_proj_epilogue_folded_norm(dtype):
            om.rms_norm(yf[:, 2 * d:3 * d], None, 1e-5), 0.01 * torch.sigmoid(yf[:, 3 * d:3 * d + 1]),
            0.005 * torch.sigmoid(yf[:, 3 * d + 1:]))
     with torch.no_grad():
-        got = K.proj_epilogue(y.to(DEV), d, qw.to(DEV, dtype), kw.to(DEV, dtype), 1e-5, 0.01, 0.005,
+        y_dev = y.to(DEV) if layout == "packed" else padded(y.to(DEV))
+        got = K.proj_epilogue(y_dev, d, qw.to(DEV, dtype), kw.to(DEV, dtype), 1e-5, 0.01, 0.005,
                               x=x.to(DEV), x_eps=1e-5, eta_alpha_bias=bias.to(DEV))
     tol = 1e-5 if dtype == torch.float32 else 2.0 ** -7
     for name, a, e in zip(("q", "k", "v", "eta", "alpha"), got, ref):

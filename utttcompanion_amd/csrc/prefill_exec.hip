@@ -3,13 +3,14 @@
 // layer's block forward, model/uttt_layer.py:1528-1555, reading the chunk-start fast weights,
 // then the layers' chained updates, :519-608).
 //
-// The work is the same launches the per-call entry points make, in the same order on the same
-// two streams: per layer, the forward pass on the main stream and stage l of the layer chain on
-// the chain stream, part 1 after the layer's projections and part 2 after its readout, then the
-// state write after the last layer, which the main stream waits for.  What changes is the host
-// side: a chunk costs one call into the library instead of one binding call per launch, so the
-// host enqueues a chunk's ~14 launches per layer in far less time than the GPU runs them, and
-// the two streams stay fed.
+// The work is the launches the per-call entry points make: per layer, the forward pass on the
+// main stream, part 1 of chain stage l (the snapshot products with the chunk-start S and the
+// key Gram rows, which need only the keys of layers <= l) after the layer's projections, and
+// part 2 (the layer's update) after the layer's readout, both on the chain stream; then the
+// state write after the last layer, which the main stream waits for.  (Part 1 on a third stream, beside part 2 of earlier layers,
+// measured slower at config 3: 621 against 603 ms per prefill, the snapshot products then
+// competing for HBM with the chain's streaming kernels and the readouts.)  The host side costs
+// one call per chunk instead of one binding call per launch.
 #include <mutex>
 #include <vector>
 
@@ -106,7 +107,9 @@ extern "C" int uttt_prefill_chunk(const uttt_prefill_chunk_args* a, uttt_stream_
     UTTT_TRY(hip_status(hipStreamWaitEvent(cs, read, 0), "hipStreamWaitEvent"));
     UTTT_TRY(uttt_chunk_chain_stage_part(&chain, a->chain_workspace, a->chain_workspace_bytes, l, 2, cs));
   }
-  // the state write follows every reader of the chunk-start state; the next chunk follows it
+  // the state write follows every reader of the chunk-start state; the next chunk follows it.
+  // The chain stream's work ends in a join back to the main stream, which keeps the call
+  // capturable in a graph (a capture must not end with a forked stream's work unjoined)
   hipEvent_t fwd_done = events.ev[2 * UTTT_MAX_CHAIN], chain_done = events.ev[2 * UTTT_MAX_CHAIN + 1];
   UTTT_TRY(hip_status(hipEventRecord(fwd_done, ms), "hipEventRecord"));
   UTTT_TRY(hip_status(hipStreamWaitEvent(cs, fwd_done, 0), "hipStreamWaitEvent"));

@@ -101,8 +101,96 @@ __global__ void __launch_bounds__(kThreads) k_proj_epilogue(const ProjArgs a) {
   }
 }
 
+// The same epilogue with one wave per row and 16-byte accesses (rows, weights and outputs
+// 16-byte aligned with row strides in whole vectors): each lane holds KV vectors of every
+// segment, the four sums of squares are reduced inside the wave, and the kernel uses no LDS,
+// so it can share a CU with the other stream's LDS-heavy kernels.  The products and roundings
+// are those of k_proj_epilogue; only the order of the sums of squares differs.
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> { using type = bf16x8; };
+template <> struct Vec16<float> { using type = f32x4; };
+
+template <typename T, int KV>
+__global__ void __launch_bounds__(64) k_proj_epilogue_vec(const ProjArgs a) {
+  using V = typename Vec16<T>::type;
+  constexpr int VEC = 16 / sizeof(T);
+  const int r = blockIdx.x, lane = threadIdx.x;
+  const int nvec = a.D / VEC;
+  const T* y = static_cast<const T*>(a.y) + (int64_t)r * a.y_rs;
+  const T* x = a.x != nullptr ? static_cast<const T*>(a.x) + (int64_t)r * a.x_rs : nullptr;
+  V v[3][KV], xv[KV];
+#pragma unroll
+  for (int i = 0; i < KV; ++i) {
+    const int c = lane + 64 * i;
+    const bool in = c < nvec;
+#pragma unroll
+    for (int seg = 0; seg < 3; ++seg) v[seg][i] = in ? *reinterpret_cast<const V*>(y + seg * a.D + c * VEC) : V{};
+    xv[i] = in && x != nullptr ? *reinterpret_cast<const V*>(x + c * VEC) : V{};
+  }
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < KV; ++i)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+#pragma unroll
+      for (int seg = 0; seg < 3; ++seg) ss[seg] += to_f32(v[seg][i][e]) * to_f32(v[seg][i][e]);
+      ss[3] += to_f32(xv[i][e]) * to_f32(xv[i][e]);
+    }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ss[k] = wave_sum(ss[k]);
+  const float inv_d = 1.0f / (float)a.D;
+  const float xs = x != nullptr ? 1.0f / sqrtf(ss[3] * inv_d + a.x_eps) : 1.0f;
+#pragma unroll
+  for (int seg = 0; seg < 3; ++seg) {
+    const float rstd = 1.0f / sqrtf(xs * xs * ss[seg] * inv_d + a.eps);
+    const T* wt = static_cast<const T*>(seg == 0 ? a.qw : seg == 1 ? a.kw : nullptr);
+    T* o = static_cast<T*>(a.out[seg]) + (int64_t)r * a.out_rs;
+#pragma unroll
+    for (int i = 0; i < KV; ++i) {
+      const int c = lane + 64 * i;
+      if (c >= nvec) continue;
+      V g{};
+      if (wt != nullptr) g = *reinterpret_cast<const V*>(wt + c * VEC);
+      V out;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        out[e] = from_f32<T>(xs * to_f32(v[seg][i][e]) * rstd * (wt != nullptr ? to_f32(g[e]) : 1.0f));
+      *reinterpret_cast<V*>(o + c * VEC) = out;
+    }
+  }
+  if (lane == 0) {
+    const T* eab = static_cast<const T*>(a.ea_bias);
+    const float be = eab != nullptr ? to_f32(eab[0]) : 0.f, ba = eab != nullptr ? to_f32(eab[1]) : 0.f;
+    const float ye = xs * to_f32(y[3 * a.D]) + be, ya = xs * to_f32(y[3 * a.D + 1]) + ba;
+    static_cast<T*>(a.eta)[r] = from_f32<T>(a.lr * sigmoidf_acc(ye));
+    static_cast<T*>(a.alpha)[r] = from_f32<T>(a.wd * sigmoidf_acc(ya));
+  }
+}
+
+template <typename T>
+bool vec_fits(const ProjArgs& p) {
+  constexpr int VEC = 16 / sizeof(T);
+  auto al = [](const void* q) { return q == nullptr || aligned16(q); };
+  return p.D % VEC == 0 && p.D <= 8 * 64 * VEC && p.y_rs % VEC == 0 && p.out_rs % VEC == 0 &&
+         (p.x == nullptr || p.x_rs % VEC == 0) && al(p.y) && al(p.x) && al(p.qw) && al(p.kw) && al(p.out[0]) &&
+         al(p.out[1]) && al(p.out[2]);
+}
+
 template <typename T>
 void launch_epilogue(const ProjArgs& p, hipStream_t st) {
+  if (vec_fits<T>(p)) {
+    constexpr int VEC = 16 / sizeof(T);
+    const int kv = (p.D / VEC + 63) / 64;
+    if (kv <= 1)
+      hipLaunchKernelGGL((k_proj_epilogue_vec<T, 1>), dim3(p.rows), dim3(64), 0, st, p);
+    else if (kv <= 2)
+      hipLaunchKernelGGL((k_proj_epilogue_vec<T, 2>), dim3(p.rows), dim3(64), 0, st, p);
+    else if (kv <= 4)
+      hipLaunchKernelGGL((k_proj_epilogue_vec<T, 4>), dim3(p.rows), dim3(64), 0, st, p);
+    else
+      hipLaunchKernelGGL((k_proj_epilogue_vec<T, 8>), dim3(p.rows), dim3(64), 0, st, p);
+    return;
+  }
   if (p.D <= 4 * kThreads)
     hipLaunchKernelGGL((k_proj_epilogue<T, 4>), dim3(p.rows), dim3(kThreads), 0, st, p);
   else if (p.D <= 8 * kThreads)

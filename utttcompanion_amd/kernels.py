@@ -1100,7 +1100,8 @@ def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, st
 def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
                 out: Optional[Tensor] = None, kv_len: Optional[int] = None,
                 workspace: Optional[Tensor] = None, build_only: bool = False):
-    """q (B, H, Tq, hd), k/v (B, Hkv, Tkv, hd) (any strides with hd contiguous).  Query i sits
+    """q (B, H, Tq, hd), k/v (B, Hkv, Tkv, hd) (any strides with hd contiguous).  ``workspace``
+    (uint8) must be zero-filled before its first use; every call leaves it so.  Query i sits
     at key index q_offset + i and sees key j iff 0 <= q_offset + i - j < window.  ``out``
     (B, H, Tq, hd) may be a strided view, e.g. of a (B, Tq, H, hd) buffer.  ``build_only``
     returns the validated ``uttt_swa_prefill_args`` without launching (the operands must then
@@ -1145,7 +1146,7 @@ def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
     lib = N.load_library()
     nbytes = lib.uttt_swa_prefill_workspace(bsz, heads, tq, tkv, hd, window)
     if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
-        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+        workspace = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=dev)  # split counters start at 0
     a.workspace, a.workspace_bytes = _p(workspace), workspace.numel()
     if build_only:
         return a

@@ -58,7 +58,8 @@ class PrefillPlan:
         self.hid = torch.empty((bsz, tokens, dim), dtype=act, device=dev)
         self.qkv = torch.empty((bsz, tokens, heads + 2 * hkv, hd), dtype=act, device=dev)
         self.att = torch.empty((bsz, tokens, heads, hd), dtype=act, device=dev)
-        self.y = torch.empty((rows, 3 * dim + 2), dtype=act, device=dev)
+        # the projection rows padded to whole 16-byte vectors (the epilogue's vector path)
+        self.y = torch.empty((rows, (3 * dim + 2 + 7) // 8 * 8), dtype=act, device=dev)[:, :3 * dim + 2]
         self.r = torch.empty((bsz, tokens, dim), dtype=act, device=dev)
         # per layer: q, k, v and eta, alpha (the chain reads layers <= l until the state write)
         self.proj_out = [(torch.empty((3, rows, dim), dtype=act, device=dev), torch.empty((2, rows), dtype=act,
@@ -73,7 +74,7 @@ class PrefillPlan:
         # every KV length a chunk of this plan can see
         nbytes = max(lib.uttt_swa_prefill_workspace(bsz, heads, tokens, kv, hd, win)
                      for kv in range(tokens, kv_capacity + 1))
-        self.attn_ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+        self.attn_ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=dev)  # split counters start at 0
         self.read_ws = K.readout_workspace(self.hid, read[0])
         hid2 = self.hid.view(rows, dim)
         q = self.qkv[:, :, :heads]
