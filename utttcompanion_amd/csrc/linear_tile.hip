@@ -192,7 +192,7 @@ __global__ void __launch_bounds__(kLinThreads, 1) k_linear(const LinArgs a) {
   }
 }
 
-constexpr int kSlots128 = 4, kSlots64 = 6;
+constexpr int kSlots128 = 4, kSlots64 = 3;
 constexpr int kMaxSplits = 8;
 // the workspace starts with a fixed counter region, so that one zero-filled buffer serves every
 // shape (a launch's partial tiles never overlap another shape's counters)
