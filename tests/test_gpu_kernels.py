@@ -328,8 +328,8 @@ def test_swa_prefill_matches_oracle(case, dtype):
 def test_swa_prefill_ignores_stale_workspace_contents(dtype):
     """Splits with no visible key leave their partial rows unwritten; partial rows full of
     NaN (reused memory) must not leak into the output.  Single-query steps exercise it.  The
-    split counters at the end of the workspace start at zero (the contract) and are left
-    zero."""
+    split counters (a fixed 4 KB region at the start of the workspace) start at zero (the
+    contract) and are left zero."""
     from utttcompanion_amd import _native as N
     K = kernels()
     lib = N.load_library()
@@ -342,16 +342,37 @@ def test_swa_prefill_ignores_stale_workspace_contents(dtype):
         nbytes = lib.uttt_swa_prefill_workspace(1, 2, 1, tkv, 64, win)
         ws = torch.full((1 << 22,), float("nan"), device=DEV).view(torch.uint8)
         if nbytes > 16:
-            ws[nbytes - 8:nbytes].zero_()  # one counter per (row, head, q tile): 1 x 2 x 1
+            ws[:4096].zero_()
         with torch.no_grad():
             got = K.swa_prefill(*to_dev(q, k, v), win, tkv - 1, workspace=ws)
         torch.cuda.synchronize()
         assert torch.isfinite(got).all(), (tkv, win)
         if nbytes > 16:
-            assert not ws[nbytes - 8:nbytes].any(), "the counters are left zero"
+            assert not ws[:4096].any(), "the counters are left zero"
         tol = F32_REL if dtype == torch.float32 else BF16_ABS
         err = rel_err(got, ref) if dtype == torch.float32 else max_abs(got, ref)
         assert err <= tol, (tkv, win, err)
+
+
+def test_swa_prefill_one_workspace_serves_every_shape():
+    """Calls of different shapes, one after another, sharing one workspace (as the default
+    per-device workspace is shared): each matches its own fresh-workspace result exactly."""
+    K = kernels()
+    g = torch.Generator().manual_seed(43)
+    ws = torch.zeros(1 << 24, dtype=torch.uint8, device=DEV)
+    for b, h, hkv, tq, tkv, hd, win in ((2, 12, 4, 300, 300, 64, 128), (1, 4, 4, 64, 575, 64, 512),
+                                        (1, 16, 4, 130, 400, 128, 1024), (4, 16, 4, 64, 1088, 128, 1024),
+                                        (1, 4, 4, 64, 575, 64, 512)):
+        q = torch.randn(b, tq, h, hd, generator=g).bfloat16().transpose(1, 2)
+        k = torch.randn(b, hkv, tkv, hd, generator=g).bfloat16()
+        v = torch.randn(b, hkv, tkv, hd, generator=g).bfloat16()
+        with torch.no_grad():
+            shared = K.swa_prefill(*to_dev(q, k, v), win, tkv - tq, workspace=ws)
+            fresh = K.swa_prefill(*to_dev(q, k, v), win, tkv - tq,
+                                  workspace=torch.zeros(1 << 24, dtype=torch.uint8, device=DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(shared, fresh), (b, h, tq, tkv)
+        assert not ws[:4096].any()
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -185,6 +185,7 @@ struct PrefillPlan {
 };
 
 constexpr int kMaxPrefillSplits = 16;
+constexpr int64_t kPrefillTarget = 512;  // workgroups the key split aims the grid at
 
 __host__ __device__ __forceinline__ int prefill_max_tiles(int64_t kv_len, int64_t window) {
   const int64_t span = min(kv_len, window + 63);
@@ -197,7 +198,7 @@ static PrefillPlan prefill_plan(int64_t batch, int64_t heads, int64_t q_len, int
   p.q_pad = p.nqt * 64;
   const int64_t base = (int64_t)p.nqt * heads * batch;
   const int max_tiles = prefill_max_tiles(kv_len, window);
-  int64_t ns = (512 + base - 1) / base;
+  int64_t ns = (kPrefillTarget + base - 1) / base;
   if (ns > max_tiles) ns = max_tiles;
   if (ns > kMaxPrefillSplits) ns = kMaxPrefillSplits;
   if (ns < 1) ns = 1;
@@ -768,8 +769,14 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_combine(const uttt_swa_
   }
 }
 
-// workspace: the split partials (nsplit x batch x heads x q_pad rows of HD + 2 floats), then one
-// counter per (row, head, q tile)
+// workspace: one counter per (row, head, q tile) in a fixed region at the start (the key range
+// is split only while the grid has fewer than kPrefillTarget (row, head, q tile) groups, so at
+// most that many counters), then the split partials (nsplit x batch x heads x q_pad rows of
+// HD + 2 floats).  The fixed region lets one zero-filled buffer serve calls of every shape: a
+// call's partials never overlap another shape's counters.
+constexpr size_t kPrefillCounterBytes = 4096;
+static_assert(kPrefillTarget * sizeof(unsigned) <= kPrefillCounterBytes, "a split grid's counters fit the region");
+
 static size_t prefill_partial_bytes(int64_t batch, int64_t heads, int64_t head_dim, const PrefillPlan& p) {
   return align_up(sizeof(float) * (size_t)p.nsplit * (size_t)batch * (size_t)heads * (size_t)p.q_pad *
                   (size_t)(head_dim + 2));
@@ -777,10 +784,8 @@ static size_t prefill_partial_bytes(int64_t batch, int64_t heads, int64_t head_d
 
 template <typename T, int HD>
 static void launch_prefill(const uttt_swa_prefill_args& a, const PrefillPlan& p, hipStream_t st) {
-  float* part = static_cast<float*>(a.workspace);
-  unsigned* counters = p.nsplit > 1 ? reinterpret_cast<unsigned*>(static_cast<char*>(a.workspace) +
-                                                                  prefill_partial_bytes(a.batch, a.n_heads, HD, p))
-                                    : nullptr;
+  float* part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + (p.nsplit > 1 ? kPrefillCounterBytes : 0));
+  unsigned* counters = p.nsplit > 1 ? static_cast<unsigned*>(a.workspace) : nullptr;
   const dim3 grid((unsigned)p.nqt, (unsigned)a.n_heads, (unsigned)(a.batch * p.nsplit));
   hipLaunchKernelGGL((k_swa_prefill<T, HD>), grid, dim3(kThreads), 0, st, a, part, p.nsplit, p.tiles_per_split,
                      p.q_pad, counters);
@@ -857,8 +862,7 @@ extern "C" size_t uttt_swa_prefill_workspace(int64_t batch, int64_t n_heads, int
   if (batch < 1 || n_heads < 1 || q_len < 1 || kv_len < 1 || window < 1 || head_dim < 1) return 0;
   const PrefillPlan p = prefill_plan(batch, n_heads, q_len, kv_len, window);
   if (p.nsplit == 1) return 16;
-  return prefill_partial_bytes(batch, n_heads, head_dim, p) + sizeof(unsigned) * (size_t)batch * (size_t)n_heads *
-                                                                 (size_t)p.nqt;
+  return kPrefillCounterBytes + prefill_partial_bytes(batch, n_heads, head_dim, p);
 }
 
 extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t stream) {

@@ -1097,13 +1097,30 @@ def rope_kv_append(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, st
 # sliding-window attention (reference SDPA / FlexAttention dispatch, model/uttt_layer.py:1119-1165)
 # ---------------------------------------------------------------------------
 
+_ATTN_WS: dict = {}
+
+
+def _attention_workspace(dev: torch.device, nbytes: int) -> Tensor:
+    """The device's zero-filled ``uttt_swa_prefill`` workspace, grown to at least ``nbytes``
+    (every call leaves its split counters zero, so one buffer serves every call made in stream
+    order)."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _ATTN_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _ATTN_WS[key] = ws
+    return ws
+
+
 def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
                 out: Optional[Tensor] = None, kv_len: Optional[int] = None,
                 workspace: Optional[Tensor] = None, build_only: bool = False):
     """q (B, H, Tq, hd), k/v (B, Hkv, Tkv, hd) (any strides with hd contiguous).  ``workspace``
     (uint8) must be zero-filled before its first use; every call leaves it so.  Query i sits
     at key index q_offset + i and sees key j iff 0 <= q_offset + i - j < window.  ``out``
-    (B, H, Tq, hd) may be a strided view, e.g. of a (B, Tq, H, hd) buffer.  ``build_only``
+    (B, H, Tq, hd) may be a strided view, e.g. of a (B, Tq, H, hd) buffer.  Without a
+    ``workspace`` the call uses one zero-filled buffer per device, shared by every call: calls on
+    concurrent streams must each pass their own.  ``build_only``
     returns the validated ``uttt_swa_prefill_args`` without launching (the operands must then
     be usable as they are, and ``out`` and ``workspace`` given)."""
     bsz, heads, tq, hd = q.shape
@@ -1145,8 +1162,10 @@ def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
     a.out, a.o_stride_b, a.o_stride_h, a.o_stride_t = _p(out), out.stride(0), out.stride(1), out.stride(2)
     lib = N.load_library()
     nbytes = lib.uttt_swa_prefill_workspace(bsz, heads, tq, tkv, hd, window)
-    if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
-        workspace = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=dev)  # split counters start at 0
+    if workspace is None:
+        workspace = _attention_workspace(dev, nbytes)
+    elif workspace.numel() < nbytes or workspace.device != dev:
+        raise ValueError(f"the attention workspace must hold {nbytes} bytes on {dev}")
     a.workspace, a.workspace_bytes = _p(workspace), workspace.numel()
     if build_only:
         return a
