@@ -340,9 +340,7 @@ typedef struct {
   const void* k; int64_t k_stride_b, k_stride_h, k_stride_t;
   const void* v; int64_t v_stride_b, v_stride_h, v_stride_t;
   void* out; int64_t o_stride_b, o_stride_h, o_stride_t;
-  /* >= uttt_swa_prefill_workspace(...) bytes, zero-filled before the first call; every call
-   * leaves it zero-filled (split counters), so calls sharing it must not overlap */
-  void* workspace; size_t workspace_bytes;
+  void* workspace; size_t workspace_bytes; /* >= uttt_swa_prefill_workspace(...) */
 } uttt_swa_prefill_args;
 
 size_t uttt_swa_prefill_workspace(int64_t batch, int64_t n_heads, int64_t q_len, int64_t kv_len, int64_t head_dim,

@@ -327,28 +327,19 @@ def test_swa_prefill_matches_oracle(case, dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_swa_prefill_ignores_stale_workspace_contents(dtype):
     """Splits with no visible key leave their partial rows unwritten; partial rows full of
-    NaN (reused memory) must not leak into the output.  Single-query steps exercise it.  The
-    split counters (a fixed 4 KB region at the start of the workspace) start at zero (the
-    contract) and are left zero."""
-    from utttcompanion_amd import _native as N
+    NaN (reused memory) must not leak into the output.  Single-query steps exercise it."""
     K = kernels()
-    lib = N.load_library()
     g = torch.Generator().manual_seed(41)
     for tkv, win in ((21, 24), (70, 8), (300, 128)):
         q = torch.randn(1, 1, 2, 64, generator=g).to(dtype).transpose(1, 2)
         k = torch.randn(1, 1, tkv, 64, generator=g).to(dtype)
         v = torch.randn(1, 1, tkv, 64, generator=g).to(dtype)
         ref = om.sliding_window_attention(q.float(), k.float(), v.float(), win, tkv - 1)
-        nbytes = lib.uttt_swa_prefill_workspace(1, 2, 1, tkv, 64, win)
         ws = torch.full((1 << 22,), float("nan"), device=DEV).view(torch.uint8)
-        if nbytes > 16:
-            ws[:4096].zero_()
         with torch.no_grad():
             got = K.swa_prefill(*to_dev(q, k, v), win, tkv - 1, workspace=ws)
         torch.cuda.synchronize()
         assert torch.isfinite(got).all(), (tkv, win)
-        if nbytes > 16:
-            assert not ws[:4096].any(), "the counters are left zero"
         tol = F32_REL if dtype == torch.float32 else BF16_ABS
         err = rel_err(got, ref) if dtype == torch.float32 else max_abs(got, ref)
         assert err <= tol, (tkv, win, err)
@@ -356,7 +347,9 @@ def test_swa_prefill_ignores_stale_workspace_contents(dtype):
 
 def test_swa_prefill_one_workspace_serves_every_shape():
     """Calls of different shapes, one after another, sharing one workspace (as the default
-    per-device workspace is shared): each matches its own fresh-workspace result exactly."""
+    per-device workspace and the chunk executor's are shared; the split count, and with it the
+    partials' layout, changes with the keys in range): each matches its own fresh-workspace
+    result exactly."""
     K = kernels()
     g = torch.Generator().manual_seed(43)
     ws = torch.zeros(1 << 24, dtype=torch.uint8, device=DEV)
@@ -372,7 +365,6 @@ def test_swa_prefill_one_workspace_serves_every_shape():
                                   workspace=torch.zeros(1 << 24, dtype=torch.uint8, device=DEV))
         torch.cuda.synchronize()
         assert torch.equal(shared, fresh), (b, h, tq, tkv)
-        assert not ws[:4096].any()
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -138,32 +138,37 @@ __global__ void __launch_bounds__(kThreads) k_up_gate(const FwdArgs a) {
 
 // Readout with bf16 activations and weights over one token block (tokens <= 64): the token rows
 // (and key rows) and the W_up / W_gate tiles go straight from global memory into LDS through a
-// ring of kUgSlots k steps of 64, so up to three steps' loads are in flight; the W tiles reach
-// the MFMA through transposing reads.  With keys, 8 waves: waves 0-3 take the token rows, 4-7
-// the key rows, and every W tile in LDS serves both.  The products accumulate over d in the
-// same order as k_up_gate's and the chain's snapshot products.
-constexpr int kUgSlots = 4;
+// ring of k steps of 64 (up to SLOTS - 1 steps' loads in flight); the W tiles reach the MFMA
+// through transposing reads.  With keys, 8 waves: waves 0-3 take the token rows, 4-7 the key
+// rows, and every W tile in LDS serves both.  A workgroup covers NB 64-column slabs of F: with
+// NB = 2 (F a multiple of 128) the config-3 grid is 43 x 4 = 172 workgroups, one round on the
+// GPU's CUs, instead of 86 x 4 = 344 (two rounds at one workgroup per CU), and each token row
+// tile serves twice the weight columns.  The products accumulate over d in the same order as
+// k_up_gate's and the chain's snapshot products for every NB.
+template <int NB> constexpr int ug_slots() { return NB == 1 ? 4 : 3; }
 
-template <bool KEYS>
+template <bool KEYS, int NB>
 __global__ void __launch_bounds__(KEYS ? 512 : 256) k_up_gate_lds(const FwdArgs a) {
   constexpr int NW = KEYS ? 8 : 4;
   constexpr int NA = KEYS ? 2 : 1;            // row tiles per step
-  constexpr int kSlot = (NA + 2) * 8192;       // row tiles, W_up tile, W_gate tile
-  constexpr int PER = (NA * 8 + 16) / NW;      // load instructions per wave per step
-  static_assert((NA * 8 + 16) % NW == 0, "the step's row groups split evenly over the waves");
-  __shared__ __align__(1024) char ring[kUgSlots * kSlot];
-  const int ft = blockIdx.x, b = blockIdx.y, f0 = ft * 64;
+  constexpr int NS = NA + 2 * NB;             // 8 KB tiles per step: row tiles, W_up slabs, W_gate slabs
+  constexpr int SLOTS = ug_slots<NB>();
+  constexpr int kSlot = NS * 8192;
+  constexpr int PER = NS * 8 / NW;            // load instructions per wave per step
+  static_assert((NS * 8) % NW == 0, "the step's row groups split evenly over the waves");
+  __shared__ __align__(1024) char ring[SLOTS * kSlot];
+  const int ft = blockIdx.x, b = blockIdx.y, f0 = ft * 64 * NB;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int set = w >> 2, w4 = w & 3;  // row set: 0 token rows, 1 key rows
-  const int wr = (w4 >> 1) * 32, wc = (w4 & 1) * 32;
+  const int wr = (w4 >> 1) * 32, wc = (w4 & 1) * 32 * NB;
   const int rows = min(64, a.ntok);
   const bf16* xq = static_cast<const bf16*>(a.x[0]) + (int64_t)b * a.x_rs[0];
   const bf16* xk = KEYS ? static_cast<const bf16*>(a.kx) + (int64_t)b * a.kx_rs : xq;
   const bf16* wu = static_cast<const bf16*>(a.wu[0]) + (int64_t)b * a.w_rs[0] + f0;
   const bf16* wg = static_cast<const bf16*>(a.wg[0]) + (int64_t)b * a.w_rs[0] + f0;
-  // row group g of a step: g < 8 NA row tiles (8 rows each), then W_up and W_gate (8 d rows
-  // each); wave w loads groups w, w + NW, ...; its LDS destination is slot + 1 KB g
+  // row group g of a step: g < 8 NA row tiles (8 rows each), then NB W_up slabs and NB W_gate
+  // slabs (8 d rows each); wave w loads groups w, w + NW, ...; its LDS destination is slot + 1 KB g
   int voff[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -174,64 +179,83 @@ __global__ void __launch_bounds__(KEYS ? 512 : 256) k_up_gate_lds(const FwdArgs 
   const int nsteps = a.D / 64;
   auto issue = [&](int step) {
     const int d0 = step * 64;
-    const uint32_t base = ring0 + (uint32_t)((step % kUgSlots) * kSlot);
-    // rows past `rows` are out of the buffer range: zeros
-    const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(xq + d0, (uint32_t)(rows * a.D * 2));
-    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(xk + d0, (uint32_t)(rows * a.D * 2));
-    const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(wu + (int64_t)d0 * a.F, (uint32_t)(64 * a.F * 2));
-    const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(wg + (int64_t)d0 * a.F, (uint32_t)(64 * a.F * 2));
+    const uint32_t base = ring0 + (uint32_t)((step % SLOTS) * kSlot);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int g = w + NW * i;
-      const __amdgpu_buffer_rsrc_t r = g < 8 ? rq : (g < NA * 8 ? rk : (g < NA * 8 + 8 ? ru : rg));
+      const int g = w + NW * i, ti = g / 8;
+      __amdgpu_buffer_rsrc_t r;
+      if (ti < NA) {  // rows past `rows` are out of the buffer range: zeros
+        r = buffer_rsrc((ti == 0 ? xq : xk) + d0, (uint32_t)(rows * a.D * 2));
+      } else {  // slab h of W_up or W_gate: 64 h columns in, its range ends 128 h bytes early
+        const int sl = ti - NA, h = sl % NB;
+        r = buffer_rsrc((sl < NB ? wu : wg) + (int64_t)d0 * a.F + 64 * h, (uint32_t)(64 * a.F * 2 - 128 * h));
+      }
       buffer_load_lds_raw(r, lds_ptr(base + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
     }
   };
-  for (int j = 0; j < min(nsteps, kUgSlots - 1); ++j) issue(j);
-  uint32_t ta[4];
+  for (int j = 0; j < min(nsteps, SLOTS - 1); ++j) issue(j);
+  uint32_t ta[4], tu[NB], tg[NB];
 #pragma unroll
   for (int k = 0; k < 4; ++k) ta[k] = row_frag_addr(ring0 + (uint32_t)(set * 8192), wr, lane, k);
-  const uint32_t tu = slab_tr_addr(ring0 + (uint32_t)(NA * 8192), wc, lane);
-  const uint32_t tg = slab_tr_addr(ring0 + (uint32_t)((NA + 1) * 8192), wc, lane);
-  f32x16 au, ag;
-  zero(au);
-  zero(ag);
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+    const int c = wc + 32 * cb;
+    tu[cb] = slab_tr_addr(ring0 + (uint32_t)((NA + c / 64) * 8192), c % 64, lane);
+    tg[cb] = slab_tr_addr(ring0 + (uint32_t)((NA + NB + c / 64) * 8192), c % 64, lane);
+  }
+  f32x16 au[NB], ag[NB];
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+    zero(au[cb]);
+    zero(ag[cb]);
+  }
   for (int step = 0; step < nsteps; ++step) {
-    wait_steps<PER, kUgSlots - 2>(min(nsteps - 1, step + kUgSlots - 2) - step);
+    wait_steps<PER, SLOTS - 2>(min(nsteps - 1, step + SLOTS - 2) - step);
     __builtin_amdgcn_s_barrier();  // every wave's loads of this step landed; the last step's slot is free
-    if (step + kUgSlots - 1 < nsteps) issue(step + kUgSlots - 1);
-    const uint32_t so = (uint32_t)((step % kUgSlots) * kSlot);
-    bf16x8 fa[4], fu[4], fg[4];
+    if (step + SLOTS - 1 < nsteps) issue(step + SLOTS - 1);
+    const uint32_t so = (uint32_t)((step % SLOTS) * kSlot);
+    bf16x8 fa[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) fa[k] = lds_read_bf16x8<0>(ta[k] + so);
-    slab_frags(tu + so, fu);
-    slab_frags(tg + so, fg);
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fu[0]), "+v"(fu[1]), "+v"(fu[2]),
-                   "+v"(fu[3]), "+v"(fg[0]), "+v"(fg[1]), "+v"(fg[2]), "+v"(fg[3]));
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      au = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fu[k], au, 0, 0, 0);
-      ag = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fg[k], ag, 0, 0, 0);
+    for (int cb = 0; cb < NB; ++cb) {
+      bf16x8 fu[4], fg[4];
+      slab_frags(tu[cb] + so, fu);
+      slab_frags(tg[cb] + so, fg);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fu[0]), "+v"(fu[1]), "+v"(fu[2]),
+                     "+v"(fu[3]), "+v"(fg[0]), "+v"(fg[1]), "+v"(fg[2]), "+v"(fg[3]));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        au[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fu[k], au[cb], 0, 0, 0);
+        ag[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fg[k], ag[cb], 0, 0, 0);
+      }
     }
   }
-  const int col = wc + acc_col();
   if (KEYS && set == 1) {  // both key products, rows past ntok are 0 (zero key rows)
     bf16* ku = static_cast<bf16*>(a.ku) + (int64_t)b * 64 * a.F + f0;
     bf16* kg = static_cast<bf16*>(a.kg) + (int64_t)b * 64 * a.F + f0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
-      ku[off] = from_f32<bf16>(au[i]);
-      kg[off] = from_f32<bf16>(ag[i]);
+    for (int cb = 0; cb < NB; ++cb) {
+      const int col = wc + 32 * cb + acc_col();
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t off = (int64_t)(wr + acc_row(i)) * a.F + col;
+        ku[off] = from_f32<bf16>(au[cb][i]);
+        kg[off] = from_f32<bf16>(ag[cb][i]);
+      }
     }
     return;
   }
   bf16* h = static_cast<bf16*>(a.h[0]) + (int64_t)b * a.tok_pad * a.F + f0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float u = au[i], g = ag[i];
-    h[(int64_t)(wr + acc_row(i)) * a.F + col] = from_f32<bf16>((g * sigmoidf_acc(g)) * u);
+  for (int cb = 0; cb < NB; ++cb) {
+    const int col = wc + 32 * cb + acc_col();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float u = au[cb][i], g = ag[cb][i];
+      h[(int64_t)(wr + acc_row(i)) * a.F + col] = from_f32<bf16>((g * sigmoidf_acc(g)) * u);
+    }
   }
 }
 
@@ -1091,10 +1115,16 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   const dim3 ug_grid(F / 64, B, L.ntb + (a.keys != nullptr ? 1 : 0));
   if constexpr (sizeof(T) == 2 && sizeof(WT) == 2) {
     if (L.ntb == 1) {  // one token block: the LDS-ring kernel
-      if (a.keys != nullptr)
-        hipLaunchKernelGGL(k_up_gate_lds<true>, dim3(F / 64, B), dim3(512), 0, st, f);
-      else
-        hipLaunchKernelGGL(k_up_gate_lds<false>, dim3(F / 64, B), dim3(256), 0, st, f);
+      if (F % 128 == 0) {
+        if (a.keys != nullptr)
+          hipLaunchKernelGGL((k_up_gate_lds<true, 2>), dim3(F / 128, B), dim3(512), 0, st, f);
+        else
+          hipLaunchKernelGGL((k_up_gate_lds<false, 2>), dim3(F / 128, B), dim3(256), 0, st, f);
+      } else if (a.keys != nullptr) {
+        hipLaunchKernelGGL((k_up_gate_lds<true, 1>), dim3(F / 64, B), dim3(512), 0, st, f);
+      } else {
+        hipLaunchKernelGGL((k_up_gate_lds<false, 1>), dim3(F / 64, B), dim3(256), 0, st, f);
+      }
     } else if (D % 128 == 0) {
       hipLaunchKernelGGL((k_up_gate<T, WT, 128>), ug_grid, blk, 0, st, f);
     } else {

@@ -115,12 +115,10 @@ __global__ void __launch_bounds__(kThreads) k_rope_append(const uttt_rope_append
 // ---------------------------------------------------------------------------
 // Prefill.  grid (q tiles of 64, n_heads, batch * nsplit): the key tiles that intersect a
 // q tile's window are divided among `nsplit` workgroups; each wave owns 16 queries.  With
-// nsplit > 1 the workgroups store fp32 partials (row max, row sum, unnormalised output)
-// device-coherently and raise a counter per (row, head, q tile); the workgroup that completes
-// the count merges the splits (prefill_merge) and resets the counter, so the zero-filled
-// counters after the partials stay zero between calls.  Q / K rows are staged with 16-byte
-// loads, V is transposed in registers to [e][key]; the next key tile is loaded while the
-// current one is consumed.
+// nsplit > 1 the workgroups write fp32 partials (row max, row sum, unnormalised output)
+// and k_swa_prefill_combine merges them.  Q / K rows are staged with 16-byte loads, V is
+// transposed in registers to [e][key]; the next key tile is loaded while the current one
+// is consumed.
 // ---------------------------------------------------------------------------
 template <typename T, int HD>
 struct AttnStage {
@@ -185,7 +183,6 @@ struct PrefillPlan {
 };
 
 constexpr int kMaxPrefillSplits = 16;
-constexpr int64_t kPrefillTarget = 512;  // workgroups the key split aims the grid at
 
 __host__ __device__ __forceinline__ int prefill_max_tiles(int64_t kv_len, int64_t window) {
   const int64_t span = min(kv_len, window + 63);
@@ -198,7 +195,7 @@ static PrefillPlan prefill_plan(int64_t batch, int64_t heads, int64_t q_len, int
   p.q_pad = p.nqt * 64;
   const int64_t base = (int64_t)p.nqt * heads * batch;
   const int max_tiles = prefill_max_tiles(kv_len, window);
-  int64_t ns = (kPrefillTarget + base - 1) / base;
+  int64_t ns = (512 + base - 1) / base;
   if (ns > max_tiles) ns = max_tiles;
   if (ns > kMaxPrefillSplits) ns = kMaxPrefillSplits;
   if (ns < 1) ns = 1;
@@ -207,60 +204,9 @@ static PrefillPlan prefill_plan(int64_t batch, int64_t heads, int64_t q_len, int
   return p;
 }
 
-// The merge of one (row, head, q tile)'s split partials by the last of its workgroups to
-// finish: every thread waited for its own partial stores, the workgroup synchronises, one
-// thread raises the counter, and the workgroup that completes the count reads every split's
-// partials device-coherently (past its XCD's L2) and merges them per output element, splits in
-// order, skipping splits without a visible key; it resets the counter to zero.
-template <typename T, int HD>
-__device__ void prefill_merge(const uttt_swa_prefill_args& a, const float* pr0, int64_t sstride, int nsplit,
-                              int b, int h, int q0, int qn, unsigned* counter) {
-  __shared__ int last;
-  wait_vmcnt<0>();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = old == (unsigned)(nsplit - 1);
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last) return;
-  T* og = static_cast<T*>(a.out) + b * a.o_stride_b + h * a.o_stride_h;
-  for (int idx = threadIdx.x; idx < qn * HD; idx += kThreads) {
-    const int r = idx / HD, e = idx - r * HD;
-    const float* row = pr0 + (int64_t)r * (HD + 2);
-    float m[kMaxPrefillSplits], l[kMaxPrefillSplits], o[kMaxPrefillSplits];
-#pragma unroll
-    for (int sp = 0; sp < kMaxPrefillSplits; ++sp) {
-      const float* q = row + sp * sstride;
-      m[sp] = sp < nsplit ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
-      l[sp] = sp < nsplit ? __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-      o[sp] = sp < nsplit && m[sp] != -INFINITY ? __hip_atomic_load(q + 2 + e, __ATOMIC_RELAXED,
-                                                                      __HIP_MEMORY_SCOPE_AGENT)
-                                                : 0.f;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int sp = 0; sp < kMaxPrefillSplits; ++sp) mx = fmaxf(mx, m[sp]);
-    float num = 0.f, den = 0.f;
-    if (mx != -INFINITY) {
-#pragma unroll
-      for (int sp = 0; sp < kMaxPrefillSplits; ++sp) {
-        // a split with no visible key leaves its output partial unwritten: skip it, do not scale it
-        if (m[sp] != -INFINITY) {
-          const float f = expf(m[sp] - mx);
-          den += l[sp] * f;
-          num += o[sp] * f;
-        }
-      }
-    }
-    og[(int64_t)(q0 + r) * a.o_stride_t + e] = from_f32<T>(den > 0.f ? num / den : 0.f);
-  }
-}
-
 template <typename T, int HD>
 __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill_args a, float* part, int nsplit,
-                                                          int tiles_per_split, int q_pad, unsigned* counters) {
+                                                          int tiles_per_split, int q_pad) {
   constexpr int PAD = Mma16<T>::kPad;
   constexpr int LQ = HD + PAD;   // q/k rows [token][e]
   constexpr int LV = 64 + PAD;   // v^T rows [e][key], p rows [query][key]
@@ -282,16 +228,12 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const int64_t sstride = (int64_t)q_pad * (HD + 2);
-  float* pr0 = part + ((((int64_t)b * a.n_heads + h) * nsplit) * q_pad + q0) * (HD + 2);
-  float* pr = pr0 + sp * sstride;
-  unsigned* counter = counters + ((int64_t)b * a.n_heads + h) * ((q_pad + 63) / 64) + qt;
+  float* pr = part + ((((int64_t)b * a.n_heads + h) * nsplit + sp) * q_pad + q0) * (HD + 2);
   if (t_begin >= t_end) {  // nothing in this split's range (only with nsplit > 1)
     for (int idx = threadIdx.x; idx < 64; idx += kThreads) {
-      __hip_atomic_store(pr + idx * (HD + 2), -INFINITY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(pr + idx * (HD + 2) + 1, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pr[idx * (HD + 2)] = -INFINITY;
+      pr[idx * (HD + 2) + 1] = 0.f;
     }
-    prefill_merge<T, HD>(a, pr0, sstride, nsplit, b, h, q0, qn, counter);
     return;
   }
 
@@ -395,15 +337,57 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
       const int r = 16 * w + 4 * g + i;
       float* row = pr + r * (HD + 2);
       if (c == 0) {
-        __hip_atomic_store(row, m_run[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(row + 1, l_run[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        row[0] = m_run[i];
+        row[1] = l_run[i];
       }
 #pragma unroll
-      for (int t = 0; t < HD / 16; ++t)
-        __hip_atomic_store(row + 2 + 16 * t + c, o[t][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int t = 0; t < HD / 16; ++t) row[2 + 16 * t + c] = o[t][i];
     }
-    prefill_merge<T, HD>(a, pr0, sstride, nsplit, b, h, q0, qn, counter);
   }
+}
+
+// grid (q_pad * HD / 256, n_heads, batch): one output element per thread; the split
+// partials of its row are loaded together (at most kMaxPrefillSplits).
+template <typename T, int HD>
+__global__ void __launch_bounds__(kThreads) k_swa_prefill_combine(const uttt_swa_prefill_args a, const float* part,
+                                                                  int nsplit, int q_pad) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int idx = blockIdx.x * kThreads + threadIdx.x;
+  const int qi = idx / HD, e = idx - qi * HD;
+  if (qi >= a.q_len) return;
+  const float* base = part + (((int64_t)b * a.n_heads + h) * nsplit) * q_pad * (HD + 2) + (int64_t)qi * (HD + 2);
+  const int64_t sstride = (int64_t)q_pad * (HD + 2);
+  float m[kMaxPrefillSplits], l[kMaxPrefillSplits], o[kMaxPrefillSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxPrefillSplits; ++s) {
+    if (s < nsplit) {
+      const float* row = base + s * sstride;
+      m[s] = row[0];
+      l[s] = row[1];
+      o[s] = row[2 + e];
+    } else {
+      m[s] = -INFINITY;
+      l[s] = 0.f;
+      o[s] = 0.f;
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxPrefillSplits; ++s) mx = fmaxf(mx, m[s]);
+  float num = 0.f, den = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll
+    for (int s = 0; s < kMaxPrefillSplits; ++s) {
+      // a split with no visible key leaves its output partial unwritten: skip it, do not scale it
+      if (m[s] != -INFINITY) {
+        const float f = expf(m[s] - mx);
+        den += l[s] * f;
+        num += o[s] * f;
+      }
+    }
+  }
+  T* og = static_cast<T*>(a.out) + b * a.o_stride_b + h * a.o_stride_h;
+  og[(int64_t)qi * a.o_stride_t + e] = from_f32<T>(den > 0.f ? num / den : 0.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -769,26 +753,16 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_combine(const uttt_swa_
   }
 }
 
-// workspace: one counter per (row, head, q tile) in a fixed region at the start (the key range
-// is split only while the grid has fewer than kPrefillTarget (row, head, q tile) groups, so at
-// most that many counters), then the split partials (nsplit x batch x heads x q_pad rows of
-// HD + 2 floats).  The fixed region lets one zero-filled buffer serve calls of every shape: a
-// call's partials never overlap another shape's counters.
-constexpr size_t kPrefillCounterBytes = 4096;
-static_assert(kPrefillTarget * sizeof(unsigned) <= kPrefillCounterBytes, "a split grid's counters fit the region");
-
-static size_t prefill_partial_bytes(int64_t batch, int64_t heads, int64_t head_dim, const PrefillPlan& p) {
-  return align_up(sizeof(float) * (size_t)p.nsplit * (size_t)batch * (size_t)heads * (size_t)p.q_pad *
-                  (size_t)(head_dim + 2));
-}
-
 template <typename T, int HD>
 static void launch_prefill(const uttt_swa_prefill_args& a, const PrefillPlan& p, hipStream_t st) {
-  float* part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + (p.nsplit > 1 ? kPrefillCounterBytes : 0));
-  unsigned* counters = p.nsplit > 1 ? static_cast<unsigned*>(a.workspace) : nullptr;
+  float* part = static_cast<float*>(a.workspace);
   const dim3 grid((unsigned)p.nqt, (unsigned)a.n_heads, (unsigned)(a.batch * p.nsplit));
   hipLaunchKernelGGL((k_swa_prefill<T, HD>), grid, dim3(kThreads), 0, st, a, part, p.nsplit, p.tiles_per_split,
-                     p.q_pad, counters);
+                     p.q_pad);
+  if (p.nsplit > 1)
+    hipLaunchKernelGGL((k_swa_prefill_combine<T, HD>),
+                       dim3((unsigned)((int64_t)p.q_pad * HD / kThreads), (unsigned)a.n_heads, (unsigned)a.batch),
+                       dim3(kThreads), 0, st, a, (const float*)part, p.nsplit, p.q_pad);
 }
 
 // bf16 rings of up to kMergeSlots slots, head_dim 64 and at most kMergeRep query heads per kv
@@ -862,7 +836,7 @@ extern "C" size_t uttt_swa_prefill_workspace(int64_t batch, int64_t n_heads, int
   if (batch < 1 || n_heads < 1 || q_len < 1 || kv_len < 1 || window < 1 || head_dim < 1) return 0;
   const PrefillPlan p = prefill_plan(batch, n_heads, q_len, kv_len, window);
   if (p.nsplit == 1) return 16;
-  return kPrefillCounterBytes + prefill_partial_bytes(batch, n_heads, head_dim, p);
+  return sizeof(float) * (size_t)p.nsplit * (size_t)batch * (size_t)n_heads * (size_t)p.q_pad * (size_t)(head_dim + 2);
 }
 
 extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t stream) {

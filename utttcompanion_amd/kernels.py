@@ -1101,13 +1101,12 @@ _ATTN_WS: dict = {}
 
 
 def _attention_workspace(dev: torch.device, nbytes: int) -> Tensor:
-    """The device's zero-filled ``uttt_swa_prefill`` workspace, grown to at least ``nbytes``
-    (every call leaves its split counters zero, so one buffer serves every call made in stream
-    order)."""
+    """The device's ``uttt_swa_prefill`` workspace (split partials, rewritten by every call),
+    grown to at least ``nbytes``: one buffer serves every call made in stream order."""
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     ws = _ATTN_WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _ATTN_WS[key] = ws
     return ws
 
@@ -1115,8 +1114,7 @@ def _attention_workspace(dev: torch.device, nbytes: int) -> Tensor:
 def swa_prefill(q: Tensor, k: Tensor, v: Tensor, window: int, q_offset: int,
                 out: Optional[Tensor] = None, kv_len: Optional[int] = None,
                 workspace: Optional[Tensor] = None, build_only: bool = False):
-    """q (B, H, Tq, hd), k/v (B, Hkv, Tkv, hd) (any strides with hd contiguous).  ``workspace``
-    (uint8) must be zero-filled before its first use; every call leaves it so.  Query i sits
+    """q (B, H, Tq, hd), k/v (B, Hkv, Tkv, hd) (any strides with hd contiguous).  Query i sits
     at key index q_offset + i and sees key j iff 0 <= q_offset + i - j < window.  ``out``
     (B, H, Tq, hd) may be a strided view, e.g. of a (B, Tq, H, hd) buffer.  Without a
     ``workspace`` the call uses one zero-filled buffer per device, shared by every call: calls on

@@ -70,11 +70,11 @@ class PrefillPlan:
         need = max(lib.uttt_linear_workspace(rows, n, k) for n, k in
                    ((n_qkv, dim), (dim, heads * hd), (3 * dim + 2, dim), (dim, dim)))
         self.linear_ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=dev)
-        # the attention's split count (and workspace) depends on the keys in range: size it for
-        # every KV length a chunk of this plan can see
+        # the attention's split count (and partials) depends on the keys in range: size the
+        # workspace for every KV length a chunk of this plan can see
         nbytes = max(lib.uttt_swa_prefill_workspace(bsz, heads, tokens, kv, hd, win)
                      for kv in range(tokens, kv_capacity + 1))
-        self.attn_ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=dev)  # split counters start at 0
+        self.attn_ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
         self.read_ws = K.readout_workspace(self.hid, read[0])
         hid2 = self.hid.view(rows, dim)
         q = self.qkv[:, :, :heads]
