@@ -398,3 +398,28 @@ def test_prefill_chunk_executor_graph_replays_match_eager():
             assert torch.equal(gout[2], eager[2]), rep
             model.prefill_with_writes(d_ids[:, :16], state)  # unrelated eager work between replays
             torch.cuda.synchronize()
+
+
+def test_prefill_chunk_executor_long_window_matches_per_call_path():
+    """bf16, 16 heads x 4 rows with a 1024-token window over 17 chunks of 64: the attention's key
+    split changes with the keys in range (and not monotonically), so the executor's one attention
+    workspace serves calls of several split layouts; the executor stays within the bf16 bar of
+    the launch-by-launch path (hidden rows 2e-2 relative, fast weights 2e-2 max-abs)."""
+    from utttcompanion_amd import uTTTConfig, uTTTModel
+    cfg = uTTTConfig(vocab_size=512, d_model=1024, n_layers=2, n_heads=16, n_kv_heads=4, d_ff_fast=256,
+                     chunk_size=64, sliding_window_size=1024, max_seq_len=2048)
+    torch.manual_seed(7)
+    model = uTTTModel(cfg).eval().to(DEV).to(torch.bfloat16)
+    model.fast_weight_pool.float()
+    g = torch.Generator().manual_seed(44)
+    ids = torch.randint(6, 512, (4, 1088), generator=g).to(DEV)
+    state = model.init_fast_state(4, device=DEV, dtype=torch.float32, detach=True)
+    with torch.no_grad():
+        a = model.prefill_with_writes(ids, state)
+        b = model.prefill_with_writes(ids, state, executor=False)
+    torch.cuda.synchronize()
+    assert torch.isfinite(a[0].float()).all()
+    assert rel_err(a[0], b[0]) <= 2e-2
+    for n, t, u in zip(NAMES, a[1], b[1]):
+        assert max_abs(t, u) <= 2e-2, n
+    assert rel_err(a[2], b[2]) <= 1e-2
