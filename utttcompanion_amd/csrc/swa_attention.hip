@@ -129,19 +129,26 @@ struct AttnStage {
   uint4 kr[kRowChunks];
   uint4 vr[8];
 
+  // Branch-free: rows at or past n lie outside the buffer ranges and read as zeros, so the loads
+  // carry no condition and the compiler has no reason to wait for them before the current tile's
+  // work (a conditional load made it wait for every outstanding load right away).
   __device__ __forceinline__ void load(const T* k, const T* v, int64_t st_k, int64_t st_v, int n) {
+    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(k, (uint32_t)(max(n, 0) * st_k * (int64_t)sizeof(T)));
+    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(v, (uint32_t)(max(n, 0) * st_v * (int64_t)sizeof(T)));
 #pragma unroll
     for (int j = 0; j < kRowChunks; ++j) {
       const int idx = threadIdx.x + j * kThreads;
       const int row = idx / kChunksPerRow, c = idx - row * kChunksPerRow;
-      kr[j] = row < n ? *reinterpret_cast<const uint4*>(k + row * st_k + c * kVec) : make_uint4(0u, 0u, 0u, 0u);
+      kr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rk, (int)((row * st_k + c * kVec) * (int64_t)sizeof(T)), 0, 0));
     }
     if (threadIdx.x < kVUnits) {
       const int kg = threadIdx.x / kChunksPerRow, c = threadIdx.x - kg * kChunksPerRow;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int row = kg * 8 + i;
-        vr[i] = row < n ? *reinterpret_cast<const uint4*>(v + row * st_v + c * kVec) : make_uint4(0u, 0u, 0u, 0u);
+        vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rv, (int)((row * st_v + c * kVec) * (int64_t)sizeof(T)), 0, 0));
       }
     }
   }
@@ -203,6 +210,32 @@ static PrefillPlan prefill_plan(int64_t batch, int64_t heads, int64_t q_len, int
   p.nsplit = (max_tiles + p.tiles_per_split - 1) / p.tiles_per_split;
   return p;
 }
+
+// Reductions over the 16 lanes of a DPP row (the lanes that share a query row of a 16 x 16 score
+// block): rotations by 8, 4, 2 and 1 within the row leave every lane with the row's result.  They
+// run as VALU operations with DPP operands, where cross-lane shuffles (ds_bpermute) would make
+// each step an LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kRowRor8 = 0x128, kRowRor4 = 0x124, kRowRor2 = 0x122, kRowRor1 = 0x121;  // DPP row_ror:n
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_row<kRowRor8>(v));
+  v = fmaxf(v, dpp_row<kRowRor4>(v));
+  v = fmaxf(v, dpp_row<kRowRor2>(v));
+  return fmaxf(v, dpp_row<kRowRor1>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_row<kRowRor8>(v);
+  v += dpp_row<kRowRor4>(v);
+  v += dpp_row<kRowRor2>(v);
+  return v + dpp_row<kRowRor1>(v);
+}
+// e^x for the softmax weights (x <= 0) through the hardware base-2 exponential:
+// e^x = 2^(x log2 e); relative error about |x| 2^-23 from the product's rounding, far inside the
+// fp32 and bf16 tolerances of the attention output
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
 template <typename T, int HD>
 __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill_args a, float* part, int nsplit,
@@ -296,19 +329,17 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
         s[n][i] = val;
         mx = fmaxf(mx, val);
       }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      mx = row16_max(mx);
       const float m_new = fmaxf(m_run[i], mx);
-      const float corr = m_new == -INFINITY ? 1.f : expf(m_run[i] - m_new);
+      const float corr = m_new == -INFINITY ? 1.f : exp_fast(m_run[i] - m_new);
       float rs = 0.f;
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const float pv = s[n][i] == -INFINITY ? 0.f : expf(s[n][i] - m_new);
+        const float pv = s[n][i] == -INFINITY ? 0.f : exp_fast(s[n][i] - m_new);
         s[n][i] = pv;
         rs += pv;
       }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) rs += __shfl_xor(rs, off, 64);
+      rs = row16_sum(rs);
       l_run[i] = l_run[i] * corr + rs;
       m_run[i] = m_new;
 #pragma unroll
@@ -856,6 +887,9 @@ extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t st
                a->k_stride_b % vec == 0 && a->k_stride_h % vec == 0 && a->k_stride_t % vec == 0 &&
                a->v_stride_b % vec == 0 && a->v_stride_h % vec == 0 && a->v_stride_t % vec == 0,
                "q/k/v strides must be multiples of 16 bytes");
+  UTTT_REQUIRE(a->k_stride_t >= a->head_dim && a->v_stride_t >= a->head_dim &&
+                   a->k_stride_t * 64 * 4 <= 0x7fffffffLL && a->v_stride_t * 64 * 4 <= 0x7fffffffLL,
+               "k/v token strides must cover a row and fit a 64-row buffer range");
   const PrefillPlan p = prefill_plan(a->batch, a->n_heads, a->q_len, a->kv_len, a->window);
   UTTT_REQUIRE(a->batch * p.nsplit <= 65535, "batch too large for the attention grid");
   UTTT_REQUIRE(p.nsplit == 1 || (a->workspace != nullptr &&
