@@ -1759,9 +1759,48 @@ __device__ __forceinline__ void lds_wait_frag_sets(bf16x8 (&a)[4], bf16x8 (&b)[4
                  "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]));
 }
 
+typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+
+// four floats rounded to bf16 (round to nearest even, as static_cast<bf16>) in 8 bytes
+__device__ __forceinline__ u32x2v pack_bf16x4(const f32x4& v) {
+  u32x2v r;
+  r[0] = (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(v[0])) |
+         ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(v[1])) << 16);
+  r[1] = (uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(v[2])) |
+         ((uint32_t)__builtin_bit_cast(unsigned short, static_cast<bf16>(v[3])) << 16);
+  return r;
+}
+
 template <int NA, int NB, int SLOTS>
 constexpr int apply_wide_occupancy() {
   return (160 * 1024) / (SLOTS * (NA + NB) * 8192) < 1 ? 1 : (160 * 1024) / (SLOTS * (NA + NB) * 8192);
+}
+
+// Tile order of the wide state write.  Every output tile reads, per layer, the token slabs of its
+// row block and of its column block, and the workgroups resident on one XCD (about 64) share one
+// L2.  The launch's tiles are listed row by row, matrix by matrix, in blocks of kApplyBlock x
+// kApplyBlock tiles, and XCD x takes the x-th contiguous eighth of the list in order (workgroup
+// ids reach the XCDs round-robin).  The resident workgroups of an XCD then cover about one block,
+// 2 kApplyBlock slabs per layer, where tiles dealt round-robin in row-major order spread over ~55
+// slabs per layer at the config-3 shape and missed L2 on more than half of the slab reads.
+constexpr int kApplyBlock = 8;
+
+// the position in that list of workgroup `bid` of a grid of exactly `total` workgroups
+__device__ __forceinline__ int xcd_contiguous(int bid, int total) {
+  const int x = bid % kXcds, base = total / kXcds, extra = total % kXcds;
+  return x * base + min(x, extra) + bid / kXcds;
+}
+
+// tile q of an R x C tile matrix listed in kApplyBlock x kApplyBlock blocks (row-major blocks,
+// row-major inside a block, ragged blocks at the right and bottom edges)
+__device__ __forceinline__ void blocked_tile(int q, int R, int C, int& r, int& c) {
+  const int i = q / (kApplyBlock * C), rem = q - i * kApplyBlock * C;
+  const int h = min(kApplyBlock, R - i * kApplyBlock);
+  const int j = rem / (h * kApplyBlock), rem2 = rem - j * h * kApplyBlock;
+  const int w = min(kApplyBlock, C - j * kApplyBlock);
+  r = i * kApplyBlock + rem2 / w;
+  c = j * kApplyBlock + rem2 % w;
 }
 
 template <int NA, int NB, int SLOTS>
@@ -1772,29 +1811,23 @@ k_chain_apply_wide(const ApplyChainArgs a) {
   const int nD = a.D / 64, nF = a.F / 64;
   // tiles: W_up / W_gate (D x F) take NA 64-row blocks of D by NB of F; W_down (F x D) NA of F by NB of D
   const int per_ug = (nD / NA) * (nF / NB), per_dn = (nF / NA) * (nD / NB);
-  const RowTile rt = row_tile(blockIdx.x, a.B, 2 * per_ug + per_dn);
-  if (!rt.valid) return;
-  const int m = rt.tile < 2 * per_ug ? rt.tile / per_ug : 2;
-  const int jt = m < 2 ? rt.tile - m * per_ug : rt.tile - 2 * per_ug;
-  const int b = rt.b;
+  const int per_row = 2 * per_ug + per_dn;
+  const int q = xcd_contiguous(blockIdx.x, a.B * per_row);  // the grid is B x per_row workgroups
+  const int b = q / per_row, tile = q - b * per_row;
+  const int m = tile < 2 * per_ug ? tile / per_ug : 2;
+  const int jt = m < 2 ? tile - m * per_ug : tile - 2 * per_ug;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int qr = w >> 1, qc = w & 1;
   const __attribute__((address_space(4))) float* cf =
       (const __attribute__((address_space(4))) float*)(uintptr_t)(a.coef + (int64_t)b * kCoefStride);
   if (cf[3] == 0.f) return;  // no layer updated this row: W and S stay as they are
-  int r0, c0, ld_out;
-  if (m < 2) {
-    const int nct = nF / NB;
-    r0 = (jt / nct) * 64 * NA;
-    c0 = (jt % nct) * 64 * NB;
-    ld_out = a.F;
-  } else {
-    const int nct = nD / NB;
-    r0 = (jt / nct) * 64 * NA;
-    c0 = (jt % nct) * 64 * NB;
-    ld_out = a.D;
-  }
+  int rt, ct;
+  if (m < 2)
+    blocked_tile(jt, nD / NA, nF / NB, rt, ct);
+  else
+    blocked_tile(jt, nF / NA, nD / NB, rt, ct);
+  const int r0 = rt * 64 * NA, c0 = ct * 64 * NB, ld_out = m < 2 ? a.F : a.D;
   const int64_t mat = (int64_t)a.D * a.F;
   const bf16* a_src;
   const bf16* b_src;
@@ -1916,37 +1949,67 @@ k_chain_apply_wide(const ApplyChainArgs a) {
   const bool copies = a.wc[m] != nullptr;
   const __amdgpu_buffer_rsrc_t wcres = buffer_rsrc(copies ? a.wc[m] + b * mat : nullptr, copies ? mat_bytes / 2 : 0);
   const __amdgpu_buffer_rsrc_t scres = buffer_rsrc(copies ? a.sc[m] + b * mat : nullptr, copies ? mat_bytes / 2 : 0);
-  auto row_el = [&](int i) { return (8 * (i >> 2) + (i & 3)) * ld_out; };
+  // The accumulators hold column strips (4 consecutive rows of one column per group of 4).  A
+  // transpose through LDS gives each lane 4 consecutive columns of a row instead, so W and S move
+  // in 16-byte accesses (8 lanes per 128-byte row segment) and the bf16 copies in 8-byte ones:
+  // 24 memory instructions per 32 x 32 tile instead of 96, which also keeps the wave's
+  // outstanding memory operations under the 63 the counter tracks.  The W and S loads of tile
+  // u + 2 are issued once tile u is stored.
+  __syncthreads();  // every wave is done with the slab ring: it becomes the transpose space
+  constexpr int XLD = 36;  // padded row of a 32 x 32 transpose tile (rows stay 16-byte aligned)
+  float* xt = reinterpret_cast<float*>(&slab[0][0][0]) + w * 32 * XLD;
+  const int xr = lane >> 3, xc = 4 * (lane & 7);  // row layout: rows xr + 8 k, columns xc .. xc + 3
+  const int acc_r = 4 * (lane >> 5), acc_c = lane & 31;
+  constexpr int NT = NA * NB;
+  auto tile_el = [&](int u) {
+    const int ra = u / NB, cb = u % NB;
+    return (r0 + qr * NA * 32 + 32 * ra + xr) * ld_out + c0 + qc * NB * 32 + 32 * cb + xc;
+  };
+  f32x4 wo[2][4], so[2][4];
+  auto load_tile = [&](int u) {
+    const int el = tile_el(u);
 #pragma unroll
-  for (int ra = 0; ra < NA; ++ra)
+    for (int k = 0; k < 4; ++k) {
+      wo[u & 1][k] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, el * 4, 8 * k * ld_out * 4, kNonTemporal));
+      so[u & 1][k] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(sres, el * 4, 8 * k * ld_out * 4, kNonTemporal));
+    }
+  };
+  auto transpose = [&](const f32x16& acc, f32x4 (&out)[4]) {
 #pragma unroll
-    for (int cb = 0; cb < NB; ++cb) {
-      const int64_t tile0 = (int64_t)(r0 + qr * NA * 32 + 32 * ra) * ld_out + c0 + qc * NB * 32 + 32 * cb;
-      const int lane_el = (int)tile0 + 4 * (lane >> 5) * ld_out + acc_col();
-      float wv[16], sv[16];
+    for (int i = 0; i < 16; ++i) xt[(8 * (i >> 2) + acc_r + (i & 3)) * XLD + acc_c] = acc[i];
+    // the same wave reads back: one wave's LDS operations complete in order
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        wv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wres, lane_el * 4, row_el(i) * 4,
-                                                                               kNonTemporal));
-        sv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sres, lane_el * 4, row_el(i) * 4,
-                                                                               kNonTemporal));
+    for (int k = 0; k < 4; ++k) out[k] = *reinterpret_cast<const f32x4*>(xt + (xr + 8 * k) * XLD + xc);
+  };
+  load_tile(0);
+  if constexpr (NT > 1) load_tile(1);
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    const int ra = u / NB, cb = u % NB, el = tile_el(u);
+    f32x4 gw[4], gs[4];
+    transpose(accw[ra][cb], gw);
+    transpose(accs[ra][cb], gs);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f32x4 wn, sn;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        wn[e] = ca * wo[u & 1][k][e] + cb_ * so[u & 1][k][e] + gw[k][e];
+        sn[e] = ce * so[u & 1][k][e] + gs[k][e];
       }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float w_new = ca * wv[i] + cb_ * sv[i] + accw[ra][cb][i];
-        const float s_new = ce * sv[i] + accs[ra][cb][i];
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, w_new), wres, lane_el * 4, row_el(i) * 4,
-                                              kNonTemporal);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s_new), sres, lane_el * 4, row_el(i) * 4,
-                                              kNonTemporal);
-        if (copies) {
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<bf16>(w_new)), wcres,
-                                                lane_el * 2, row_el(i) * 2, 0);
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<bf16>(s_new)), scres,
-                                                lane_el * 2, row_el(i) * 2, 0);
-        }
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, wn), wres, el * 4, 8 * k * ld_out * 4,
+                                             kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, sn), sres, el * 4, 8 * k * ld_out * 4,
+                                             kNonTemporal);
+      if (copies) {
+        __builtin_amdgcn_raw_buffer_store_b64(pack_bf16x4(wn), wcres, el * 2, 8 * k * ld_out * 2, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(pack_bf16x4(sn), scres, el * 2, 8 * k * ld_out * 2, 0);
       }
     }
+    if (u + 2 < NT) load_tile(u + 2);
+  }
 }
 
 // the wide state write's tile shape (rows x columns in 64-blocks) and ring depth
@@ -2264,8 +2327,8 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
         if (apply_wide_fits(D, F)) {
           const int tiles = 2 * (int)((D / (64 * kApplyNA)) * (F / (64 * kApplyNB))) +
                             (int)((F / (64 * kApplyNA)) * (D / (64 * kApplyNB)));
-          hipLaunchKernelGGL((k_chain_apply_wide<kApplyNA, kApplyNB, kApplySlotsWide>), dim3(row_tile_blocks(B, tiles)),
-                             blk, 0, st, aa);
+          hipLaunchKernelGGL((k_chain_apply_wide<kApplyNA, kApplyNB, kApplySlotsWide>), dim3((int)B * tiles), blk, 0,
+                             st, aa);
         } else {
           hipLaunchKernelGGL(k_chain_apply_lds, grid, blk, 0, st, aa);
         }
