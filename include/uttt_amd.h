@@ -32,7 +32,7 @@ enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE =
 
 /* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
  * Python binding reads it from this header and refuses a library built from another one. */
-#define UTTT_ABI_VERSION 19
+#define UTTT_ABI_VERSION 20
 
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
@@ -487,6 +487,13 @@ typedef struct {
   int64_t kv_offset;                       /* KV index of the chunk's first token */
   const float* token_mask; int64_t mask_row_stride; /* (batch, >= tokens) fp32 or NULL */
   float* surprise;                         /* (n_layers,) */
+  /* nonzero: main_stream does not wait for this chunk's state write; the next call on the
+   * device makes its main_stream wait for it just before layer 0's readout (the state's first
+   * reader), so that call's layer-0 QKV .. epilogue overlap the state write.  The state write
+   * reads layer 0's k / v / eta / alpha: the next call's layer-0 epilogue must write other
+   * buffers (the caller alternates two sets).  A deferred call cannot end a graph capture, and
+   * the last call of a sequence passes 0. */
+  int32_t defer_join;
 } uttt_prefill_chunk_args;
 
 int uttt_prefill_chunk(const uttt_prefill_chunk_args* args, uttt_stream_t main_stream, uttt_stream_t chain_stream);

@@ -216,7 +216,7 @@ class PrefillChunkArgs(C.Structure):
         ("n_layers", _I32), ("layers", C.POINTER(PrefillLayerCalls)), ("chain", C.POINTER(ChunkChainArgs)),
         ("chain_workspace", _P), ("chain_workspace_bytes", C.c_size_t),
         ("start_pos", _I64), ("kv_offset", _I64),
-        ("token_mask", _P), ("mask_row_stride", _I64), ("surprise", _P),
+        ("token_mask", _P), ("mask_row_stride", _I64), ("surprise", _P), ("defer_join", _I32),
     ]
 
 

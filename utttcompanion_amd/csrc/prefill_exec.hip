@@ -26,6 +26,7 @@ struct ExecEvents {
   std::mutex lock;
   std::vector<hipEvent_t> ev;
   bool ready = false;
+  bool join_pending = false;  // the last call deferred the wait for its state write
 };
 
 constexpr int kMaxDevices = 64;
@@ -70,6 +71,7 @@ extern "C" int uttt_prefill_chunk(const uttt_prefill_chunk_args* a, uttt_stream_
                (long long)a->chain->layers, UTTT_MAX_CHAIN);
   UTTT_REQUIRE(a->start_pos >= 0 && a->kv_offset >= 0, "start_pos and kv_offset must be >= 0");
   UTTT_REQUIRE(main_stream != chain_stream, "the chain needs a stream of its own");
+  UTTT_REQUIRE(a->defer_join == 0 || a->defer_join == 1, "defer_join must be 0 or 1");
   int dev = 0;
   UTTT_TRY(hip_status(hipGetDevice(&dev), "hipGetDevice"));
   UTTT_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
@@ -83,6 +85,7 @@ extern "C" int uttt_prefill_chunk(const uttt_prefill_chunk_args* a, uttt_stream_
   chain.mask_row_stride = a->token_mask != nullptr ? a->mask_row_stride : 0;
   chain.surprise = a->surprise;
   const int L = a->n_layers;
+  hipEvent_t fwd_done = events.ev[2 * UTTT_MAX_CHAIN], chain_done = events.ev[2 * UTTT_MAX_CHAIN + 1];
   for (int l = 0; l < L; ++l) {
     const uttt_prefill_layer_calls& c = a->layers[l];
     uttt_rope_append_args rope = c.rope;
@@ -99,6 +102,10 @@ extern "C" int uttt_prefill_chunk(const uttt_prefill_chunk_args* a, uttt_stream_
     UTTT_TRY(uttt_linear(&c.proj, ms));
     UTTT_TRY(uttt_proj_epilogue(&c.epilogue, ms));
     UTTT_TRY(hip_status(hipEventRecord(projected, ms), "hipEventRecord"));
+    if (l == 0 && events.join_pending) {  // the previous chunk's state write, deferred to here
+      UTTT_TRY(hip_status(hipStreamWaitEvent(ms, chain_done, 0), "hipStreamWaitEvent"));
+      events.join_pending = false;
+    }
     UTTT_TRY(uttt_swiglu_readout(&c.readout, c.readout_workspace, c.readout_workspace_bytes, ms));
     UTTT_TRY(hip_status(hipEventRecord(read, ms), "hipEventRecord"));
     UTTT_TRY(uttt_linear(&c.uttt_out, ms));
@@ -107,14 +114,18 @@ extern "C" int uttt_prefill_chunk(const uttt_prefill_chunk_args* a, uttt_stream_
     UTTT_TRY(hip_status(hipStreamWaitEvent(cs, read, 0), "hipStreamWaitEvent"));
     UTTT_TRY(uttt_chunk_chain_stage_part(&chain, a->chain_workspace, a->chain_workspace_bytes, l, 2, cs));
   }
-  // the state write follows every reader of the chunk-start state; the next chunk follows it.
-  // The chain stream's work ends in a join back to the main stream, which keeps the call
-  // capturable in a graph (a capture must not end with a forked stream's work unjoined)
-  hipEvent_t fwd_done = events.ev[2 * UTTT_MAX_CHAIN], chain_done = events.ev[2 * UTTT_MAX_CHAIN + 1];
+  // the state write follows every reader of the chunk-start state; the next chunk's first
+  // reader (layer 0's readout) follows it.  Without defer_join the chain stream's work ends in a
+  // join back to the main stream here, which keeps the call capturable in a graph (a capture
+  // must not end with a forked stream's work unjoined); with it, the next call joins
   UTTT_TRY(hip_status(hipEventRecord(fwd_done, ms), "hipEventRecord"));
   UTTT_TRY(hip_status(hipStreamWaitEvent(cs, fwd_done, 0), "hipStreamWaitEvent"));
   UTTT_TRY(uttt_chunk_chain_stage(&chain, a->chain_workspace, a->chain_workspace_bytes, L, cs));
   UTTT_TRY(hip_status(hipEventRecord(chain_done, cs), "hipEventRecord"));
-  UTTT_TRY(hip_status(hipStreamWaitEvent(ms, chain_done, 0), "hipStreamWaitEvent"));
+  if (a->defer_join) {
+    events.join_pending = true;
+  } else {
+    UTTT_TRY(hip_status(hipStreamWaitEvent(ms, chain_done, 0), "hipStreamWaitEvent"));
+  }
   return ok();
 }

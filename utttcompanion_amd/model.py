@@ -292,7 +292,9 @@ class uTTTModel(nn.Module):
                     plan = PrefillPlan(self, bsz, tokens, dev, k_bufs, v_bufs, hist + seq, start_pos + seq, read,
                                        ln_w, ln_b, pool.eps, run)
                     plans[tokens] = plan
-                plan.run(h, off, start_pos + off, hist + off, mask_f, surprises[ci], main, side)
+                # each chunk's state write overlaps the next chunk's layer-0 projections and attention
+                plan.run(h, off, start_pos + off, hist + off, mask_f, surprises[ci], main, side,
+                         defer_join=ci + 1 < n_chunks)
             per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
             caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win
                       else (kb, vb) for kb, vb in zip(k_bufs, v_bufs)]

@@ -61,10 +61,13 @@ class PrefillPlan:
         # the projection rows padded to whole 16-byte vectors (the epilogue's vector path)
         self.y = torch.empty((rows, (3 * dim + 2 + 7) // 8 * 8), dtype=act, device=dev)[:, :3 * dim + 2]
         self.r = torch.empty((bsz, tokens, dim), dtype=act, device=dev)
-        # per layer: q, k, v and eta, alpha (the chain reads layers <= l until the state write)
-        self.proj_out = [(torch.empty((3, rows, dim), dtype=act, device=dev), torch.empty((2, rows), dtype=act,
-                                                                                          device=dev))
-                         for _ in range(n_layers)]
+        # per layer: q, k, v and eta, alpha (the chain reads layers <= l until the state write);
+        # layer 0 has a second set, used by every other chunk: a chunk's layer-0 epilogue may
+        # run while the previous chunk's state write still reads layer 0's keys
+        new_out = lambda: (torch.empty((3, rows, dim), dtype=act, device=dev),
+                           torch.empty((2, rows), dtype=act, device=dev))
+        self.proj_out = [new_out() for _ in range(n_layers)]
+        self.proj_out0_alt = new_out()
         lib = N.load_library()
         n_qkv = (heads + 2 * hkv) * hd
         need = max(lib.uttt_linear_workspace(rows, n, k) for n, k in
@@ -98,34 +101,63 @@ class PrefillPlan:
             w_proj, eab = uttt.packed_projection_folded(block.uttt_norm)
             w_proj = w_proj.to(act)
             c.proj = K.linear(hid2, w_proj, out=self.y, workspace=self.linear_ws, build_only=True)
-            c.epilogue, kept = K.proj_epilogue(self.y, dim, uttt.q_norm.weight, uttt.k_norm.weight, uttt.q_norm.eps,
-                                               uttt.base_inner_lr, uttt.base_weight_decay, x=self.hid,
-                                               x_eps=block.uttt_norm.eps, eta_alpha_bias=eab.to(act),
-                                               outs=self.proj_out[li], build_only=True)
-            qkv3, ea = self.proj_out[li]
-            uq, uk, uv = (t.view(bsz, tokens, dim) for t in qkv3)
-            eta, alpha = (t.view(bsz, tokens, 1) for t in ea)
-            c.readout, ws, kept_r = K.swiglu_readout(uq, *read, ln_w, ln_b, eps, out=self.r, workspace=self.read_ws,
-                                                     keys=uk, key_outputs=chain.w_product_outputs(li),
-                                                     build_only=True)
-            c.readout_workspace, c.readout_workspace_bytes = ws.data_ptr(), ws.numel()
+            eab = eab.to(act)
+
+            def epilogue_readout(cc, outs):
+                # the epilogue into ``outs`` and the readout of its q / k rows; returns k, v, eta, alpha
+                cc.epilogue, kept = K.proj_epilogue(self.y, dim, uttt.q_norm.weight, uttt.k_norm.weight,
+                                                    uttt.q_norm.eps, uttt.base_inner_lr, uttt.base_weight_decay,
+                                                    x=self.hid, x_eps=block.uttt_norm.eps, eta_alpha_bias=eab,
+                                                    outs=outs, build_only=True)
+                qkv3, ea = outs
+                uq, uk, uv = (t.view(bsz, tokens, dim) for t in qkv3)
+                eta, alpha = (t.view(bsz, tokens, 1) for t in ea)
+                cc.readout, ws, kept_r = K.swiglu_readout(uq, *read, ln_w, ln_b, eps, out=self.r,
+                                                          workspace=self.read_ws, keys=uk,
+                                                          key_outputs=chain.w_product_outputs(li), build_only=True)
+                cc.readout_workspace, cc.readout_workspace_bytes = ws.data_ptr(), ws.numel()
+                keep.extend([kept, kept_r])
+                return uk, uv, eta, alpha
+
+            layer_inputs = epilogue_readout(c, self.proj_out[li])
             w_o = uttt.w_o.weight.detach().to(act)
             c.uttt_out = K.linear(self.r.view(rows, dim), w_o, out=hid2, residual=hid2, workspace=self.linear_ws,
                                   build_only=True)
-            chain.set_layer(uk, uv, eta, alpha)
-            keep += [w_qkv, cos, sin, w_o_attn, w_proj, kept, kept_r, w_o]
-        self.calls, self._keep = calls, keep
-        self.args = N.PrefillChunkArgs()
-        self.args.n_layers = n_layers
-        self.args.layers = C.cast(calls, C.POINTER(N.PrefillLayerCalls))
-        self.args.chain = C.pointer(chain.args)
-        self.args.chain_workspace, self.args.chain_workspace_bytes = chain.workspace.data_ptr(), chain.workspace.numel()
+            chain.set_layer(*layer_inputs)
+            if li == 0:
+                # the same layer-0 calls and chain inputs over the second buffer set
+                calls_alt = (N.PrefillLayerCalls * n_layers)()
+                calls_alt[0] = N.PrefillLayerCalls.from_buffer_copy(c)
+                layer0_alt = epilogue_readout(calls_alt[0], self.proj_out0_alt)
+            keep += [w_qkv, cos, sin, w_o_attn, w_proj, w_o]
+        for li in range(1, n_layers):
+            calls_alt[li] = calls[li]
+        if chain.args.k[0] != self.proj_out[0][0][1].data_ptr():
+            raise RuntimeError("the chain's layer-0 keys are not the epilogue's output rows")
+        chain_alt = N.ChunkChainArgs.from_buffer_copy(chain.args)
+        k0, v0, eta0, alpha0 = layer0_alt
+        chain_alt.k[0], chain_alt.v[0] = k0.data_ptr(), v0.data_ptr()
+        chain_alt.eta[0], chain_alt.alpha[0] = eta0.data_ptr(), alpha0.data_ptr()
+        self.calls, self._keep = (calls, calls_alt), keep
+        self._chain_args = (chain.args, chain_alt)
+        self.args = []
+        for cl, ch in zip(self.calls, self._chain_args):
+            args = N.PrefillChunkArgs()
+            args.n_layers = n_layers
+            args.layers = C.cast(cl, C.POINTER(N.PrefillLayerCalls))
+            args.chain = C.pointer(ch)
+            args.chain_workspace, args.chain_workspace_bytes = chain.workspace.data_ptr(), chain.workspace.numel()
+            self.args.append(args)
+        self._next = 0  # which buffer set the next chunk uses
 
     def run(self, h: Tensor, off: int, start_pos: int, kv_offset: int, mask: Optional[Tensor],
-            surprise: Tensor, main: "torch.cuda.Stream", side: "torch.cuda.Stream") -> None:
+            surprise: Tensor, main: "torch.cuda.Stream", side: "torch.cuda.Stream", defer_join: bool = False) -> None:
         """One chunk: rows ``off .. off + tokens`` of ``h`` (B, T, D) are updated in place through
         every layer, and the chain writes the state; ``mask`` is the fp32 (B, T) token mask (or
-        None) and ``surprise`` this chunk's (layers,) row."""
+        None) and ``surprise`` this chunk's (layers,) row.  ``defer_join``: ``main`` does not wait
+        for the state write; the next executor call on the device does, before its layer-0
+        readout (consecutive chunks of a plan alternate layer 0's buffers for that).  The last
+        chunk of a prefill passes False."""
         end = off + self.tokens
         # the executor sets these per chunk where the wrappers checked them per call
         if not (0 <= kv_offset and kv_offset + self.tokens <= self.kv_capacity and 0 <= start_pos
@@ -136,8 +168,9 @@ class PrefillPlan:
         if surprise.shape != (self.n_layers,) or surprise.dtype != torch.float32 or not surprise.is_contiguous():
             raise ValueError("surprise must be a contiguous fp32 (layers,) tensor")
         self.hid.copy_(h[:, off:end])
-        a = self.args
-        a.start_pos, a.kv_offset = int(start_pos), int(kv_offset)
+        a = self.args[self._next]
+        self._next ^= 1
+        a.start_pos, a.kv_offset, a.defer_join = int(start_pos), int(kv_offset), int(bool(defer_join))
         if mask is not None:
             a.token_mask, a.mask_row_stride = mask.data_ptr() + off * mask.element_size(), mask.stride(0)
         else:
