@@ -280,6 +280,7 @@ BF16_TAIL_CASES = [
     dict(L=3, b=2, c=17, d=128, f=192, mask=False, copies=True),  # short chunk
     dict(L=4, b=9, c=64, d=64, f=128, mask=True, copies=False),   # more rows than XCDs, fp32 masters
     dict(L=6, b=3, c=40, d=1024, f=1536, mask=True, copies=True),  # Gram features split over 2 and 3 slices
+    dict(L=4, b=9, c=64, d=256, f=2048, mask=True, copies=True),   # 288 back-pass tiles: d range split in two
 ]
 
 

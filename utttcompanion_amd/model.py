@@ -280,6 +280,7 @@ class uTTTModel(nn.Module):
                 counts = F.pad(mask_f, (0, n_chunks * c - seq)).view(bsz, n_chunks, c).sum(dim=(0, 2))
             plans: Dict[int, PrefillPlan] = {}
             ws_chain = None
+            capturing = torch.cuda.is_current_stream_capturing()
             for ci in range(n_chunks):
                 off = ci * c
                 tokens = min(seq, off + c) - off
@@ -292,9 +293,11 @@ class uTTTModel(nn.Module):
                     plan = PrefillPlan(self, bsz, tokens, dev, k_bufs, v_bufs, hist + seq, start_pos + seq, read,
                                        ln_w, ln_b, pool.eps, run)
                     plans[tokens] = plan
-                # each chunk's state write overlaps the next chunk's layer-0 projections and attention
+                # each chunk's state write overlaps the next chunk's layer-0 projections and attention;
+                # not in a HIP graph, whose executor runs the chunks' cross joins slower (config 2:
+                # 88 ms against 64.7 ms per prefill with every call joined)
                 plan.run(h, off, start_pos + off, hist + off, mask_f, surprises[ci], main, side,
-                         defer_join=ci + 1 < n_chunks)
+                         defer_join=ci + 1 < n_chunks and not capturing)
             per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
             caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win
                       else (kb, vb) for kb, vb in zip(k_bufs, v_bufs)]
