@@ -734,6 +734,226 @@ __global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_ar
 }
 
 constexpr int kMaxDecodeSplits = 64;
+// bf16, head_dim 64, up to 4 query heads per kv head: one wave per (request, kv head, piece of
+// kPieceKeys ring slots).  The piece's K rows (a row tile: k = head dim along the row) and V rows
+// (token slabs: k = slot down the rows) go straight from the ring into LDS (buffer loads with the
+// lds bit; slots past the valid ones read as zeros), the slot being written this step is
+// replaced by the new (RoPE'd) key and value in LDS, and both products run on MFMA with the
+// query heads as the rows of a 32-row A operand (rows past the heads zero): S = Q K^T over the
+// piece's 128 slots, the softmax row statistics over DPP row rotations, P (bf16) = exp(S - max),
+// O = P V.  The partial (max, sum, unnormalised O) per head goes to the same workspace slots
+// decode_merge reads, and the last wave of a (request, kv head) merges them.  Measured at the
+// config-4 shape: 12.3 us per call against 14.4 us for k_swa_decode_part's merge form (8 lanes
+// per key row, cross-lane reductions); of the 12.3 us, 5.5 pass before the K / V rows are in
+// LDS, 2.4 in the products and softmax, 4.5 in the merge's three device-coherent round trips
+// (partial stores, counter, partial loads).
+constexpr int kPieceKeys = 128;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_rot(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// max / sum over each 32-lane half of the wave (row rotations within 16 lanes, then across the
+// two 16-lane rows of the half)
+__device__ __forceinline__ float half_max(float v) {
+  v = fmaxf(v, dpp_rot<0x128>(v));
+  v = fmaxf(v, dpp_rot<0x124>(v));
+  v = fmaxf(v, dpp_rot<0x122>(v));
+  v = fmaxf(v, dpp_rot<0x121>(v));
+  return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  v += dpp_rot<0x128>(v);
+  v += dpp_rot<0x124>(v);
+  v += dpp_rot<0x122>(v);
+  v += dpp_rot<0x121>(v);
+  return v + __shfl_xor(v, 16, 64);
+}
+
+__global__ void __launch_bounds__(64) k_swa_decode_mfma(const uttt_swa_decode_args a, float* part, unsigned* counters) {
+  constexpr int HD = 64, KEYS = kPieceKeys;
+  // LDS: K row tiles (slots 0-63, 64-127), V slabs (same), Q row tile, P row tiles (keys 0-63, 64-127)
+  __shared__ __align__(1024) bf16 lds[7 * 64 * 64];
+  bf16* kt = lds;
+  bf16* vt = lds + 2 * 4096;
+  bf16* qt = lds + 4 * 4096;
+  bf16* pt = lds + 5 * 4096;
+  const int n = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int rep = (int)(a.n_heads / a.n_kv_heads);
+  const int nsplit = gridDim.z;
+  const int64_t W = a.window;
+  const int64_t pos = a.positions[n];
+  if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) {  // loud NaN output, cache untouched
+    if (sp == 0) {
+      bf16* og = static_cast<bf16*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
+      for (int idx = lane; idx < rep * HD; idx += 64) og[idx] = from_f32<bf16>(NAN);
+    }
+    return;
+  }
+  const int64_t slot = pos % W;
+  const int valid = (int)min(pos + 1, W);
+  const int j_lo = sp * KEYS, j_hi = min(valid, j_lo + KEYS);
+  float* pr = part + (((int64_t)n * a.n_kv_heads + kvh) * nsplit + sp) * rep * (HD + 2);
+  unsigned* counter = counters + (int64_t)n * a.n_kv_heads + kvh;
+  if (j_lo >= j_hi) {  // an empty piece still arrives: its partial is (-inf, 0, 0)
+    for (int idx = lane; idx < rep * (HD + 2); idx += 64) {
+      const int e = idx % (HD + 2);
+      __hip_atomic_store(pr + idx, e == 0 ? -INFINITY : 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    decode_merge<bf16, HD, 64>(a, pr - (int64_t)sp * rep * (HD + 2), counter, n, kvh, rep, nsplit);
+    return;
+  }
+  bf16* kr = static_cast<bf16*>(a.k_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
+  bf16* vr = static_cast<bf16*>(a.v_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
+  const int cnt = j_hi - j_lo;
+  // the piece's K / V rows into LDS: 16 row groups of 8 slots per operand; rows past cnt are out
+  // of the buffer range and read as zeros
+  const uint32_t k0 = lds_addr(kt), v0 = lds_addr(vt);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rows = min(max(cnt - 64 * h, 0), 64);
+    const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kr + (int64_t)(j_lo + 64 * h) * HD, (uint32_t)(rows * HD * 2));
+    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vr + (int64_t)(j_lo + 64 * h) * HD, (uint32_t)(rows * HD * 2));
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      buffer_load_lds_raw(rk, lds_ptr(k0 + (uint32_t)(h * 8192 + g * 1024)), 16, row_src_off(g, lane, HD), 0, 0, 0);
+      buffer_load_lds_raw(rv, lds_ptr(v0 + (uint32_t)(h * 8192 + g * 1024)), 16, slab_src_off(g, lane, HD), 0, 0, 0);
+    }
+  }
+  // Q and P tiles start at zero (rows past the heads stay zero)
+  {
+    uint4* z = reinterpret_cast<uint4*>(qt);
+#pragma unroll
+    for (int i = 0; i < 3 * 4096 * 2 / 16 / 64; ++i) z[lane + 64 * i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  // RoPE of the query heads and the new key (activation-dtype rounding as the reference); the
+  // piece holding this step's slot writes the ring
+  const bf16* qg = static_cast<const bf16*>(a.q) + n * a.q_stride_n + (int64_t)kvh * rep * HD;
+  const bf16* kn = static_cast<const bf16*>(a.k_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
+  const bf16* vn = static_cast<const bf16*>(a.v_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
+  const bool owns_slot = slot >= j_lo && slot < j_hi;
+  const int ts = (int)(slot - j_lo);  // the slot's row in the piece (when owned)
+  constexpr int half = HD / 2;
+  bf16 knew[2], vnew_v;
+  {
+    const int e = lane & (half - 1);
+    const float c = a.cos_table != nullptr ? a.cos_table[pos * HD + e] : 1.f;
+    const float sn = a.cos_table != nullptr ? a.sin_table[pos * HD + e] : 0.f;
+    for (int r = lane >> 5; r <= rep; r += 2) {  // lanes 0-31 even rows, 32-63 odd rows; row rep: the key
+      const bf16* src = r < rep ? qg + r * HD : kn;
+      bf16 lo = src[e], hi = src[e + half];
+      if (a.cos_table != nullptr) rope_pair<bf16>(to_f32(lo), to_f32(hi), c, sn, lo, hi);
+      if (r < rep) {
+        qt[r * 64 + (((e >> 3) ^ row_swz(r)) << 3) + (e & 7)] = lo;
+        qt[r * 64 + ((((e + half) >> 3) ^ row_swz(r)) << 3) + (e & 7)] = hi;
+      } else {
+        knew[0] = lo;
+        knew[1] = hi;
+        if (owns_slot) {
+          kr[slot * HD + e] = lo;
+          kr[slot * HD + e + half] = hi;
+        }
+      }
+    }
+    vnew_v = vn[lane];
+    if (owns_slot) vr[slot * HD + lane] = vnew_v;
+  }
+  const bool key_lane = ((rep & 1) == 0) == (lane < 32);  // the half of the wave that took row rep
+  wait_vmcnt<0>();  // the K / V rows have landed in LDS
+  if (owns_slot) {  // this step's slot: the new key and value replace what the ring held
+    const int h = ts >> 6, t = ts & 63;
+    bf16* krow = kt + h * 4096 + t * 64;
+    bf16* vrow = vt + h * 4096 + t * 64;
+    if (key_lane) {
+      const int e = lane & (half - 1);
+      krow[(((e >> 3) ^ row_swz(t)) << 3) + (e & 7)] = knew[0];
+      krow[((((e + half) >> 3) ^ row_swz(t)) << 3) + (e & 7)] = knew[1];
+    }
+    vrow[(((lane >> 3) ^ slab_swz(t)) << 3) + (lane & 7)] = vnew_v;
+  }
+  __syncthreads();  // orders the LDS writes above before the fragment reads below
+  // S = Q K^T: 4 column tiles of 32 slots, k = head dim in 4 steps of 16
+  const uint32_t q0 = lds_addr(qt), p0 = lds_addr(pt);
+  bf16x8 fq[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) fq[k] = lds_read_bf16x8<0>(row_frag_addr(q0, 0, lane, k));
+  f32x16 sacc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    bf16x8 fk[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) fk[k] = lds_read_bf16x8<0>(row_frag_addr(k0 + (uint32_t)((t >> 1) * 8192), 32 * (t & 1), lane, k));
+    lds_wait_frags(fq, fk);
+    zero(sacc[t]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fq[k], fk[k], sacc[t], 0, 0, 0);
+  }
+  // row r < 4 of S sits in element r of lanes 0-31 (slot 32 t + lane of tile t); lanes 32-63
+  // hold padding rows 4-7 and go through the same steps harmlessly
+  const float scale2 = a.scale * 1.4426950408889634f;  // scores in log2 units
+  float mx[4], sum[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int j = 32 * t + (lane & 31);
+      sacc[t][r] = j < cnt ? sacc[t][r] * scale2 : -INFINITY;
+      m = fmaxf(m, sacc[t][r]);
+    }
+    mx[r] = half_max(m);
+    float l = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const bf16 pb = from_f32<bf16>(__builtin_amdgcn_exp2f(sacc[t][r] - mx[r]));
+      l += to_f32(pb);
+      if (lane < 32 && r < rep) {
+        const int j = 32 * t + lane, c = j & 63;
+        pt[(j >> 6) * 4096 + r * 64 + (((c >> 3) ^ row_swz(r)) << 3) + (c & 7)] = pb;
+      }
+    }
+    sum[r] = half_sum(l);
+  }
+  __syncthreads();  // the P writes before the fragment reads
+  // O = P V: columns 32 cb of the head dim, k = slots in 8 steps of 16
+  f32x16 oacc[2];
+  zero(oacc[0]);
+  zero(oacc[1]);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    bf16x8 fp[4], fv0[4], fv1[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) fp[k] = lds_read_bf16x8<0>(row_frag_addr(p0 + (uint32_t)(h * 8192), 0, lane, k));
+    slab_frags(slab_tr_addr(v0 + (uint32_t)(h * 8192), 0, lane), fv0);
+    slab_frags(slab_tr_addr(v0 + (uint32_t)(h * 8192), 32, lane), fv1);
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fp[0]), "+v"(fp[1]), "+v"(fp[2]), "+v"(fp[3]), "+v"(fv0[0]), "+v"(fv0[1]), "+v"(fv0[2]),
+                   "+v"(fv0[3]), "+v"(fv1[0]), "+v"(fv1[1]), "+v"(fv1[2]), "+v"(fv1[3]));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      oacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp[k], fv0[k], oacc[0], 0, 0, 0);
+      oacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp[k], fv1[k], oacc[1], 0, 0, 0);
+    }
+  }
+  // the partial of head r: max (natural-log units, as decode_merge takes it), sum, O row
+  if (lane < 32) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (r < rep) {
+        float* q = pr + r * (HD + 2);
+        __hip_atomic_store(q + 2 + lane, oacc[0][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(q + 2 + 32 + lane, oacc[1][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+          __hip_atomic_store(q, mx[r] * 0.6931471805599453f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(q + 1, sum[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  }
+  decode_merge<bf16, HD, 64>(a, pr - (int64_t)sp * rep * (HD + 2), counter, n, kvh, rep, nsplit);
+}
+
 
 // grid (n_req, n_kv_heads): one output element per thread, splits loaded together
 template <typename T, int HD>
@@ -797,12 +1017,14 @@ static void launch_prefill(const uttt_swa_prefill_args& a, const PrefillPlan& p,
 }
 
 // bf16 rings of up to kMergeSlots slots, head_dim 64 and at most kMergeRep query heads per kv
-// head: one launch, the window split into pieces of kMergeKeys slots merged by the last
-// workgroup (512 workgroups at 32 requests x 4 kv heads x 512 slots).  The whole-window form (one
-// 1024-thread workgroup per request and kv head) is kept for comparison (kDecodeWhole).
+// head: one launch, the window split into pieces of 128 slots merged by the last workgroup (512
+// workgroups at 32 requests x 4 kv heads x 512 slots), on MFMA (k_swa_decode_mfma, one wave per
+// piece).  The vector form of the same split (kDecodeMfma false) and the whole-window form (one
+// 1024-thread workgroup per request and kv head, kDecodeWhole) are kept for comparison.
 constexpr int kMergeKeys = 128, kMergeSlots = 512, kMergeRep = 4;
 constexpr int kWholeThreads = 1024, kWholeKeys = 512, kWholeRep = 4;
 constexpr bool kDecodeWhole = false;
+constexpr bool kDecodeMfma = true;
 
 inline size_t decode_partial_bytes(int64_t n_req, int64_t n_heads, int64_t head_dim, int64_t window) {
   return align_up(sizeof(float) * (size_t)n_req * (size_t)n_heads * (size_t)decode_splits(window) *
@@ -821,6 +1043,10 @@ static void launch_decode(const uttt_swa_decode_args& a, hipStream_t st) {
         hipLaunchKernelGGL((k_swa_decode_part<T, HD, kWholeThreads, kWholeKeys, kWholeRep, kWhole>),
                            dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, 1u), dim3(kWholeThreads), 0, st, a, part,
                            counters);
+      } else if constexpr (kDecodeMfma) {
+        const int msplit = (int)((a.window + kPieceKeys - 1) / kPieceKeys);
+        hipLaunchKernelGGL(k_swa_decode_mfma, dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, (unsigned)msplit),
+                           dim3(64), 0, st, a, part, counters);
       } else {
         const int msplit = (int)((a.window + kMergeKeys - 1) / kMergeKeys);
         hipLaunchKernelGGL((k_swa_decode_part<T, HD, kThreads, kMergeKeys, kMergeRep, kMerge>),
