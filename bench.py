@@ -377,14 +377,18 @@ def build_c3_model():
 # per-launch algorithmic bytes of the chain kernels that stream the state (bf16 copies), in units of
 # D F B bytes: the S_up / S_gate products, the W_down / S_down reads of the down and back passes,
 # and the state write (W and S read and written once per row-chunk, fp32)
-CHAIN_STATE_BYTES = {"k_chain_pq_lds": 4, "k_chain_down_lds": 4, "k_chain_back_lds": 4, "k_chain_apply_lds": 48}
+CHAIN_STATE_BYTES = {"k_chain_keys_lds": 4, "k_chain_pq_lds": 4, "k_chain_down_lds": 4, "k_chain_back_lds": 4,
+                     "k_chain_apply_lds": 48}
 CHAIN_STATE_WHAT = {
+    "k_chain_keys_lds": "4 D F per row (bf16 S_up and S_gate copies read once, with the key Gram row in the same "
+                        "launch; the W products come from the readouts)",
     "k_chain_pq_lds": "4 D F per row (bf16 S_up and S_gate copies read once; the W products come from the readouts)",
     "k_chain_down_lds": "4 D F per row (bf16 W_down and S_down copies read once)",
     "k_chain_back_lds": "4 D F per row (bf16 W_down and S_down copies read once)",
     "k_chain_apply_lds": "48 D F per row (fp32 W and S read and written once)",
 }
-CHAIN_KERNELS = ("k_chain_pq_lds", "k_chain_gram_lds", "k_chain_up_lds", "k_chain_down_lds", "k_ln_grad",
+CHAIN_KERNELS = ("k_chain_keys_lds", "k_chain_pq_lds", "k_chain_gram_lds", "k_chain_up_lds", "k_chain_down_lds",
+                 "k_ln_grad",
                  "k_chain_back_lds", "k_chain_coef", "k_chain_apply_lds", "k_chain_init")
 
 

@@ -316,7 +316,7 @@ def test_single_launches_with_timer_equal_whole_stages():
     layers, w, s, ln_w, ln_b = make_layers(4, 3, 64, 256, 384, seed=29, w_scale=0.05)
     run_a, state_a, cps_a = _chain_run(layers, w, s, ln_w, ln_b, shared=False)
     run_b, state_b, cps_b = _chain_run(layers, w, s, ln_w, ln_b, shared=False)
-    timer = K.KernelTimer(("k_chain_back_lds", "k_chain_apply_lds", "k_chain_gram_lds"))
+    timer = K.KernelTimer(("k_chain_back_lds", "k_chain_apply_lds", "k_chain_gram_lds", "k_chain_keys_lds"))
     with torch.no_grad():
         for layer in layers:
             run_a.add_layer(*_layer_inputs(layer))
@@ -334,7 +334,8 @@ def test_single_launches_with_timer_equal_whole_stages():
     assert torch.equal(sa, sb)
     summary = timer.summary()
     assert summary["k_chain_back_lds"]["launches"] == 4 and summary["k_chain_apply_lds"]["launches"] == 1
-    assert summary["k_chain_gram_lds"]["launches"] == 12  # key Gram, H Gram and dZ Gram per layer
+    # per layer: the snapshot products with the key Gram row in one launch, then the H and dZ Grams
+    assert summary["k_chain_keys_lds"]["launches"] == 4 and summary["k_chain_gram_lds"]["launches"] == 8
     assert all(v["mean_ms"] > 0 for v in summary.values())
     with pytest.raises(RuntimeError, match="out of range"):
         from utttcompanion_amd import _native as N

@@ -287,12 +287,14 @@ __global__ void __launch_bounds__(kThreads, 2) k_chain_pq(const PqArgs a) {
 // products accumulate over d in the same order as the readout's key products.
 constexpr int kPqSlots = 3;
 
-__global__ void __launch_bounds__(kThreads) k_chain_pq_lds(const PqArgs a) {
+constexpr int kPqRing = kPqSlots * 2 * 8192;  // bytes of LDS: kPqSlots steps of key rows and an X tile
+
+// workgroup `bid` of the snapshot products (ring: kPqRing bytes of LDS, 1 KB aligned)
+__device__ __forceinline__ void pq_lds_tile(const PqArgs& a, int bid, char* ring) {
   constexpr int kSlot = 2 * 8192;  // key rows, X tile
   constexpr int PER = 4;           // 16 row groups per step over 4 waves
-  __shared__ __align__(1024) char ring[kPqSlots * kSlot];
   const int nF = a.F / 64, nm = a.s_only ? 2 : 4;
-  const RowTile rt = row_tile(blockIdx.x, a.B, nm * nF);
+  const RowTile rt = row_tile(bid, a.B, nm * nF);
   if (!rt.valid) return;
   const int mi = rt.tile / nF, ft = rt.tile - mi * nF, b = rt.b;
   const int m = a.s_only ? 2 * mi + 1 : mi, f0 = ft * 64, l = a.l_begin;
@@ -345,6 +347,11 @@ __global__ void __launch_bounds__(kThreads) k_chain_pq_lds(const PqArgs a) {
   const int col = wc + acc_col();
 #pragma unroll
   for (int i = 0; i < 16; ++i) out[(int64_t)(wr + acc_row(i)) * a.F + col] = from_f32<bf16>(acc[i]);
+}
+
+__global__ void __launch_bounds__(kThreads) k_chain_pq_lds(const PqArgs a) {
+  __shared__ __align__(1024) char ring[kPqRing];
+  pq_lds_tile(a, blockIdx.x, ring);
 }
 
 // ---------------------------------------------------------------------------
@@ -453,13 +460,14 @@ constexpr int kGramSplitSteps = 8;
 __host__ __device__ inline int gram_blocks(int l0, int l1) { return (l1 * (l1 + 1) - l0 * (l0 + 1)) / 2; }
 __host__ __device__ inline int gram_splits(int kd) { return (kd / 64 + kGramSplitSteps - 1) / kGramSplitSteps; }
 
-__global__ void __launch_bounds__(kThreads) k_chain_gram_lds(const GramArgs a) {
+constexpr int kGramRing = kGramSlots * 16384;  // bytes of LDS: kGramSlots steps of X_l and X_j rows
+
+// workgroup `bid` of the Gram blocks (ring: kGramRing bytes of LDS; last: an LDS int)
+__device__ __forceinline__ void gram_lds_tile(const GramArgs& a, int bid, char* ring, int& last) {
   constexpr int kSlot = 16384;  // X_l rows, X_j rows (64 x 64 bf16 each)
   constexpr int PER = 4;        // 16 row groups per step over 4 waves
-  __shared__ __align__(1024) char ring[kGramSlots * kSlot];
-  __shared__ int last;
   const int nblk = gram_blocks(a.layer, a.layer_end);
-  const RowTile rt = row_tile(blockIdx.x, a.B, nblk * a.splits);
+  const RowTile rt = row_tile(bid, a.B, nblk * a.splits);
   if (!rt.valid) return;
   const int blk = rt.tile / a.splits, sp = rt.tile % a.splits;
   int l = a.layer, j = blk;
@@ -550,6 +558,26 @@ __global__ void __launch_bounds__(kThreads) k_chain_gram_lds(const GramArgs a) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) out[(int64_t)((q >> 1) * 32 + acc_row(i)) * a.LL + c] = sum[i];
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + blk_id, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ void __launch_bounds__(kThreads) k_chain_gram_lds(const GramArgs a) {
+  __shared__ __align__(1024) char ring[kGramRing];
+  __shared__ int last;
+  gram_lds_tile(a, blockIdx.x, ring, last);
+}
+
+// Part 1 of a single-layer stage in one launch: the snapshot products' workgroups (the first
+// npq ids), then the key Gram row's (both read only layer l's keys and the chunk-start state, so
+// they need no order between them); one launch instead of two per layer.
+static_assert(sizeof(PqArgs) + sizeof(GramArgs) + 16 <= 4096, "the fused launch's arguments fit the kernarg segment");
+
+__global__ void __launch_bounds__(kThreads) k_chain_keys_lds(const PqArgs pa, const GramArgs ga, int npq) {
+  __shared__ __align__(1024) char ring[kPqRing > kGramRing ? kPqRing : kGramRing];
+  __shared__ int last;
+  if ((int)blockIdx.x < npq)
+    pq_lds_tile(pa, blockIdx.x, ring);
+  else
+    gram_lds_tile(ga, (int)blockIdx.x - npq, ring, last);
 }
 
 // ---------------------------------------------------------------------------
@@ -2227,7 +2255,14 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
       pa.l_count = g1 - g0;
       if (g1 - g0 == 1) {  // a single layer: one staged K tile, less LDS per workgroup
         if (sizeof(T) == 2 && bf16_src) {
-          if (gate.next("k_chain_pq_lds")) hipLaunchKernelGGL(k_chain_pq_lds, pq_grid, blk, 0, st, pa);
+          // the snapshot products and the key Gram row in one launch
+          ka.layer = g0;
+          ka.layer_end = g1;
+          ka.splits = gram_splits(ka.kd);
+          const int npq = (int)pq_grid.x;
+          const int ngram = row_tile_blocks(B, gram_blocks(g0, g1) * ka.splits);
+          if (gate.next("k_chain_keys_lds"))
+            hipLaunchKernelGGL(k_chain_keys_lds, dim3(npq + ngram), blk, 0, st, pa, ka, npq);
         } else if (bf16_src) {
           if (gate.next("k_chain_pq")) hipLaunchKernelGGL((k_chain_pq<T, bf16, 1>), pq_grid, blk, 0, st, pa);
         } else if (gate.next("k_chain_pq")) {
@@ -2239,7 +2274,8 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
         hipLaunchKernelGGL((k_chain_pq<T, float, kPqGroup>), pq_grid, blk, 0, st, pa);
       }
     }
-    if (l == g0 && keys_part) {  // key Gram rows of the whole group
+    const bool keys_fused = sizeof(T) == 2 && bf16_src && g1 - g0 == 1;  // launched with the products
+    if (l == g0 && keys_part && !keys_fused) {  // key Gram rows of the whole group
       ka.layer = g0;
       ka.layer_end = g1;
       launch_gram<T>(B, g0, g1, ka, st, gate);
