@@ -365,10 +365,9 @@ typedef struct {
   const void* k_new; const void* v_new; int64_t kv_new_stride_n; /* (N, Hkv, hd) */
   void* k_ring; void* v_ring; int64_t ring_stride_n; /* (N, Hkv, window, hd) */
   void* out; int64_t o_stride_n;                 /* (N, H, hd) */
-  void* workspace; size_t workspace_bytes;       /* >= uttt_swa_decode_workspace(...); zero-filled
-                                                    before its first use: it ends with per-(request,
-                                                    kv head) merge counters that every call leaves
-                                                    at zero, so calls sharing it must be ordered */
+  void* workspace; size_t workspace_bytes;       /* >= uttt_swa_decode_workspace(...): the split
+                                                    partials of the general form (calls sharing it
+                                                    must be ordered) */
 } uttt_swa_decode_args;
 
 size_t uttt_swa_decode_workspace(int64_t n_req, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,

@@ -459,71 +459,11 @@ __device__ __forceinline__ void unpack8(float (&dst)[8], const uint4* v) {
   }
 }
 
-// The merge of one (request, kv head)'s split partials by the last workgroup to arrive.  Every
-// workgroup has stored its partial device-coherently; each thread waits for its own stores, the
-// workgroup synchronises, one thread raises the counter, and the workgroup that completes the
-// count reads every split's partial device-coherently (past its XCD's L2), merges them as
-// k_swa_decode_combine does (splits in order, 16 at a time) and resets the counter to zero.
-template <typename T, int HD, int NT>
-__device__ void decode_merge(const uttt_swa_decode_args& a, const float* pr0, unsigned* counter, int n, int kvh,
-                             int rep, int nsplit) {
-  __shared__ int last;
-  wait_vmcnt<0>();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = old == (unsigned)(nsplit - 1);
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last) return;
-  T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
-  for (int idx = threadIdx.x; idx < rep * HD; idx += NT) {
-    const int r = idx / HD, e = idx - r * HD;
-    float mx = -INFINITY, num = 0.f, den = 0.f;
-    for (int s0 = 0; s0 < nsplit; s0 += 16) {
-      float m[16], l[16], o[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int s = s0 + k;
-        const float* q = pr0 + (s * rep + r) * (HD + 2);
-        m[k] = s < nsplit ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
-        l[k] = s < nsplit ? __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-        o[k] = s < nsplit ? __hip_atomic_load(q + 2 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-      }
-      float cm = -INFINITY;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) cm = fmaxf(cm, m[k]);
-      const float nm = fmaxf(mx, cm);
-      const float scale_old = mx == -INFINITY ? 0.f : expf(mx - nm);
-      num *= scale_old;
-      den *= scale_old;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        if (m[k] != -INFINITY) {
-          const float f = expf(m[k] - nm);
-          den += l[k] * f;
-          num += o[k] * f;
-        }
-      }
-      mx = nm;
-    }
-    og[idx] = from_f32<T>(num / den);
-  }
-}
-
-// grid (n_req, n_kv_heads, splits of KEYS slots), NT threads.  Split form (the default: NT 256,
-// KEYS kDecodeKeys, REP kMaxRep): softmax partials per split for k_swa_decode_combine.  WHOLE:
-// one workgroup covers the whole window (one split) and writes the normalised output itself,
-// so a step is one launch.  MERGE: split form in one launch: the partials are written
-// device-coherently, each workgroup then raises its (request, kv head) counter, and the one that
-// completes the count merges the splits (read device-coherently) and resets the counter.
-enum DecodeMode { kSplit = 0, kWhole = 1, kMerge = 2 };
-
-template <typename T, int HD, int NT = kThreads, int KEYS = kDecodeKeys, int REP = kMaxRep, int MODE = kSplit>
-__global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_args a, float* part,
-                                                        unsigned* counters) {
-  constexpr bool WHOLE = MODE == kWhole;
+// grid (n_req, n_kv_heads, splits of KEYS slots), NT threads: softmax partials per split for
+// k_swa_decode_combine (the general form: any window, head_dim 64 or 128, up to kMaxRep query
+// heads per kv head, bf16 or fp32).
+template <typename T, int HD, int NT = kThreads, int KEYS = kDecodeKeys, int REP = kMaxRep>
+__global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_args a, float* part) {
   constexpr int L = HD / 8;                  // lanes per key row (8 elements each)
   constexpr int KPP = NT / L;                // keys per pass
   constexpr int PASSES = KEYS / KPP;         // split form: 2 (HD 64) or 4 (HD 128)
@@ -541,30 +481,15 @@ __global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_ar
   const int nsplit = gridDim.z;
   const int64_t W = a.window;
   const int64_t pos = a.positions[n];
-  if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) {  // the combine writes NaN
-    if (MODE != kSplit && sp == 0) {  // position outside the RoPE table: loud NaN output, cache untouched
-      T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
-      for (int idx = threadIdx.x; idx < rep * HD; idx += NT) og[idx] = from_f32<T>(NAN);
-    }
-    return;
-  }
+  if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) return;  // the combine writes NaN
   const int64_t slot = pos % W;
   const int valid = (int)min(pos + 1, W);
   const int j_lo = sp * KEYS, j_hi = min(valid, j_lo + KEYS);
   float* pr = part + (((int64_t)n * a.n_kv_heads + kvh) * nsplit + sp) * rep * (HD + 2);
   if (j_lo >= j_hi) {
-    if constexpr (MODE == kMerge) {  // an empty split still arrives: its partial is (-inf, 0, 0)
-      for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += NT) {
-        const int e = idx % (HD + 2);
-        __hip_atomic_store(pr + idx, e == 0 ? -INFINITY : 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      decode_merge<T, HD, NT>(a, pr - (int64_t)sp * rep * (HD + 2), counters + (int64_t)n * a.n_kv_heads + kvh,
-                              n, kvh, rep, nsplit);
-    } else {
-      for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += NT) {
-        const int e = idx % (HD + 2);
-        pr[idx] = e == 0 ? -INFINITY : 0.f;
-      }
+    for (int idx = threadIdx.x; idx < rep * (HD + 2); idx += NT) {
+      const int e = idx % (HD + 2);
+      pr[idx] = e == 0 ? -INFINITY : 0.f;
     }
     return;
   }
@@ -717,47 +642,20 @@ __global__ void __launch_bounds__(NT) k_swa_decode_part(const uttt_swa_decode_ar
     }
   }
   __syncthreads();
-  T* og = static_cast<T*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
   for (int idx = threadIdx.x; idx < rep * HD; idx += NT) {
     const int r = idx / HD, e = idx - r * HD;
     float v = 0.f;
 #pragma unroll
     for (int q = 0; q < NW; ++q) v += wred[q][idx];
-    if constexpr (WHOLE) {
-      og[idx] = from_f32<T>(v / stat[r][1]);
-    } else if constexpr (MODE == kMerge) {
-      __hip_atomic_store(pr + r * (HD + 2) + 2 + e, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (e == 0) {
-        __hip_atomic_store(pr + r * (HD + 2), stat[r][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(pr + r * (HD + 2) + 1, stat[r][1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    } else {
-      pr[r * (HD + 2) + 2 + e] = v;
-      if (e == 0) {
-        pr[r * (HD + 2)] = stat[r][0];
-        pr[r * (HD + 2) + 1] = stat[r][1];
-      }
+    pr[r * (HD + 2) + 2 + e] = v;
+    if (e == 0) {
+      pr[r * (HD + 2)] = stat[r][0];
+      pr[r * (HD + 2) + 1] = stat[r][1];
     }
   }
-  if constexpr (MODE == kMerge)
-    decode_merge<T, HD, NT>(a, pr - (int64_t)sp * rep * (HD + 2), counters + (int64_t)n * a.n_kv_heads + kvh, n,
-                            kvh, rep, nsplit);
 }
 
 constexpr int kMaxDecodeSplits = 64;
-// bf16, head_dim 64, up to 4 query heads per kv head: one wave per (request, kv head, piece of
-// kPieceKeys ring slots).  The piece's K rows (a row tile: k = head dim along the row) and V rows
-// (token slabs: k = slot down the rows) go straight from the ring into LDS (buffer loads with the
-// lds bit; slots past the valid ones read as zeros), the slot being written this step is
-// replaced by the new (RoPE'd) key and value in LDS, and both products run on MFMA with the
-// query heads as the rows of a 32-row A operand (rows past the heads zero): S = Q K^T over the
-// piece's 128 slots, the softmax row statistics over DPP row rotations, P (bf16) = exp(S - max),
-// O = P V.  The partial (max, sum, unnormalised O) per head goes to the same workspace slots
-// decode_merge reads, and the last wave of a (request, kv head) merges them.  Measured at the
-// config-4 shape: 12.3 us per call against 14.4 us for k_swa_decode_part's merge form (8 lanes
-// per key row, cross-lane reductions); of the 12.3 us, 5.5 pass before the K / V rows are in
-// LDS, 2.4 in the products and softmax, 4.5 in the merge's three device-coherent round trips
-// (partial stores, counter, partial loads).
 constexpr int kPieceKeys = 128;
 
 template <int CTRL>
@@ -781,46 +679,48 @@ __device__ __forceinline__ float half_sum(float v) {
   return v + __shfl_xor(v, 16, 64);
 }
 
-__global__ void __launch_bounds__(64) k_swa_decode_mfma(const uttt_swa_decode_args a, float* part, unsigned* counters) {
-  constexpr int HD = 64, KEYS = kPieceKeys;
-  // LDS: K row tiles (slots 0-63, 64-127), V slabs (same), Q row tile, P row tiles (keys 0-63, 64-127)
-  __shared__ __align__(1024) bf16 lds[7 * 64 * 64];
-  bf16* kt = lds;
-  bf16* vt = lds + 2 * 4096;
-  bf16* qt = lds + 4 * 4096;
-  bf16* pt = lds + 5 * 4096;
-  const int n = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
-  const int lane = threadIdx.x;
+
+// bf16 decode with head_dim 64, windows up to kWindowWaves x kPieceKeys slots and up to 4 query
+// heads per kv head: one workgroup per (request, kv head), wave w taking ring slots
+// [128 w, 128 w + 128).  A wave's K rows (a row tile: k = head dim along the row) and V rows
+// (token slabs: k = slot down the rows) go straight from the ring into LDS (buffer loads with
+// the lds bit; slots past the valid ones read as zeros), the slot written this step is replaced
+// there by the new (RoPE'd) key and value, and both products run on MFMA with the query heads as
+// the rows of a 32-row A operand (rows past the heads zero): S = Q K^T over the wave's 128
+// slots, the softmax row statistics over DPP row rotations, P (bf16) = exp(S - max), O = P V.
+// The four waves' partials (max, sum, unnormalised O per head) meet in LDS.  LDS: each wave's K
+// and V rows (32 KB), the shared query tile (rows 0-31 of a row tile, 4 KB), each wave's P for 64
+// slots at a time (4 KB), the partials (4.2 KB): 152 KB, one workgroup per CU.  Measured at the
+// config-4 shape: 8.5 us per call, against 12.4 us for the same products split over one-wave
+// workgroups whose partials a last workgroup merged through device-coherent stores, a counter
+// and loads (4.5 us of round trips), and 14.4 us for that split with 8 lanes per key row and
+// cross-lane reductions.
+constexpr int kWindowWaves = 4;
+
+__global__ void __launch_bounds__(kWindowWaves * 64) k_swa_decode_window(const uttt_swa_decode_args a) {
+  constexpr int HD = 64, KEYS = kPieceKeys, NW = kWindowWaves;
+  __shared__ __align__(1024) bf16 kv[NW][4][64 * 64];  // per wave: K slots 0-63, 64-127, V slots 0-63, 64-127
+  __shared__ __align__(1024) bf16 qt[32 * 64];          // query rows 0-31 of a row tile
+  __shared__ __align__(1024) bf16 pt[NW][32 * 64];      // per wave: P rows 0-31 for 64 slots
+  __shared__ float red[NW][4][HD + 2];                  // per wave and head (<= 4): max, sum, O row
+  const int n = blockIdx.x, kvh = blockIdx.y;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int rep = (int)(a.n_heads / a.n_kv_heads);
-  const int nsplit = gridDim.z;
   const int64_t W = a.window;
   const int64_t pos = a.positions[n];
+  bf16* og = static_cast<bf16*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
   if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) {  // loud NaN output, cache untouched
-    if (sp == 0) {
-      bf16* og = static_cast<bf16*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
-      for (int idx = lane; idx < rep * HD; idx += 64) og[idx] = from_f32<bf16>(NAN);
-    }
+    for (int idx = threadIdx.x; idx < rep * HD; idx += NW * 64) og[idx] = from_f32<bf16>(NAN);
     return;
   }
   const int64_t slot = pos % W;
   const int valid = (int)min(pos + 1, W);
-  const int j_lo = sp * KEYS, j_hi = min(valid, j_lo + KEYS);
-  float* pr = part + (((int64_t)n * a.n_kv_heads + kvh) * nsplit + sp) * rep * (HD + 2);
-  unsigned* counter = counters + (int64_t)n * a.n_kv_heads + kvh;
-  if (j_lo >= j_hi) {  // an empty piece still arrives: its partial is (-inf, 0, 0)
-    for (int idx = lane; idx < rep * (HD + 2); idx += 64) {
-      const int e = idx % (HD + 2);
-      __hip_atomic_store(pr + idx, e == 0 ? -INFINITY : 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    decode_merge<bf16, HD, 64>(a, pr - (int64_t)sp * rep * (HD + 2), counter, n, kvh, rep, nsplit);
-    return;
-  }
+  const int j_lo = w * KEYS, cnt = max(0, min(valid, j_lo + KEYS) - j_lo);  // this wave's slots
   bf16* kr = static_cast<bf16*>(a.k_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
   bf16* vr = static_cast<bf16*>(a.v_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
-  const int cnt = j_hi - j_lo;
-  // the piece's K / V rows into LDS: 16 row groups of 8 slots per operand; rows past cnt are out
-  // of the buffer range and read as zeros
-  const uint32_t k0 = lds_addr(kt), v0 = lds_addr(vt);
+  // this wave's K / V rows into LDS (rows past cnt read as zeros; an empty piece moves nothing)
+  const uint32_t k0 = lds_addr(&kv[w][0][0]), v0 = lds_addr(&kv[w][2][0]);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int rows = min(max(cnt - 64 * h, 0), 64);
@@ -832,50 +732,48 @@ __global__ void __launch_bounds__(64) k_swa_decode_mfma(const uttt_swa_decode_ar
       buffer_load_lds_raw(rv, lds_ptr(v0 + (uint32_t)(h * 8192 + g * 1024)), 16, slab_src_off(g, lane, HD), 0, 0, 0);
     }
   }
-  // Q and P tiles start at zero (rows past the heads stay zero)
-  {
-    uint4* z = reinterpret_cast<uint4*>(qt);
-#pragma unroll
-    for (int i = 0; i < 3 * 4096 * 2 / 16 / 64; ++i) z[lane + 64 * i] = make_uint4(0u, 0u, 0u, 0u);
-  }
-  // RoPE of the query heads and the new key (activation-dtype rounding as the reference); the
-  // piece holding this step's slot writes the ring
+  // the query tile starts at zero (rows past the heads stay zero)
+  reinterpret_cast<uint4*>(qt)[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();
+  // RoPE of the query heads (wave 0 writes them) and of the new key (kept by the wave whose piece
+  // holds this step's slot, which writes the ring)
   const bf16* qg = static_cast<const bf16*>(a.q) + n * a.q_stride_n + (int64_t)kvh * rep * HD;
   const bf16* kn = static_cast<const bf16*>(a.k_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
   const bf16* vn = static_cast<const bf16*>(a.v_new) + n * a.kv_new_stride_n + (int64_t)kvh * HD;
-  const bool owns_slot = slot >= j_lo && slot < j_hi;
-  const int ts = (int)(slot - j_lo);  // the slot's row in the piece (when owned)
+  const bool owns_slot = slot >= j_lo && slot < j_lo + cnt;
+  const int ts = (int)(slot - j_lo);
   constexpr int half = HD / 2;
-  bf16 knew[2], vnew_v;
-  {
+  bf16 knew[2] = {bf16{}, bf16{}}, vnew_v = bf16{};
+  if (w == 0 || owns_slot) {
     const int e = lane & (half - 1);
     const float c = a.cos_table != nullptr ? a.cos_table[pos * HD + e] : 1.f;
     const float sn = a.cos_table != nullptr ? a.sin_table[pos * HD + e] : 0.f;
     for (int r = lane >> 5; r <= rep; r += 2) {  // lanes 0-31 even rows, 32-63 odd rows; row rep: the key
+      if (r < rep && w != 0) continue;
       const bf16* src = r < rep ? qg + r * HD : kn;
       bf16 lo = src[e], hi = src[e + half];
       if (a.cos_table != nullptr) rope_pair<bf16>(to_f32(lo), to_f32(hi), c, sn, lo, hi);
       if (r < rep) {
         qt[r * 64 + (((e >> 3) ^ row_swz(r)) << 3) + (e & 7)] = lo;
         qt[r * 64 + ((((e + half) >> 3) ^ row_swz(r)) << 3) + (e & 7)] = hi;
-      } else {
+      } else if (owns_slot) {
         knew[0] = lo;
         knew[1] = hi;
-        if (owns_slot) {
-          kr[slot * HD + e] = lo;
-          kr[slot * HD + e + half] = hi;
-        }
+        kr[slot * HD + e] = lo;
+        kr[slot * HD + e + half] = hi;
       }
     }
-    vnew_v = vn[lane];
-    if (owns_slot) vr[slot * HD + lane] = vnew_v;
+    if (owns_slot) {
+      vnew_v = vn[lane];
+      vr[slot * HD + lane] = vnew_v;
+    }
   }
   const bool key_lane = ((rep & 1) == 0) == (lane < 32);  // the half of the wave that took row rep
-  wait_vmcnt<0>();  // the K / V rows have landed in LDS
+  wait_vmcnt<0>();  // this wave's K / V rows have landed in LDS
   if (owns_slot) {  // this step's slot: the new key and value replace what the ring held
     const int h = ts >> 6, t = ts & 63;
-    bf16* krow = kt + h * 4096 + t * 64;
-    bf16* vrow = vt + h * 4096 + t * 64;
+    bf16* krow = &kv[w][h][t * 64];
+    bf16* vrow = &kv[w][2 + h][t * 64];
     if (key_lane) {
       const int e = lane & (half - 1);
       krow[(((e >> 3) ^ row_swz(t)) << 3) + (e & 7)] = knew[0];
@@ -883,9 +781,9 @@ __global__ void __launch_bounds__(64) k_swa_decode_mfma(const uttt_swa_decode_ar
     }
     vrow[(((lane >> 3) ^ slab_swz(t)) << 3) + (lane & 7)] = vnew_v;
   }
-  __syncthreads();  // orders the LDS writes above before the fragment reads below
-  // S = Q K^T: 4 column tiles of 32 slots, k = head dim in 4 steps of 16
-  const uint32_t q0 = lds_addr(qt), p0 = lds_addr(pt);
+  __syncthreads();  // the query tile and the replaced slot rows before the fragment reads
+  // S = Q K^T over this wave's 128 slots (4 column tiles of 32), k = head dim in 4 steps of 16
+  const uint32_t q0 = lds_addr(qt), p0 = lds_addr(&pt[w][0]);
   bf16x8 fq[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) fq[k] = lds_read_bf16x8<0>(row_frag_addr(q0, 0, lane, k));
@@ -894,14 +792,16 @@ __global__ void __launch_bounds__(64) k_swa_decode_mfma(const uttt_swa_decode_ar
   for (int t = 0; t < 4; ++t) {
     bf16x8 fk[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) fk[k] = lds_read_bf16x8<0>(row_frag_addr(k0 + (uint32_t)((t >> 1) * 8192), 32 * (t & 1), lane, k));
+    for (int k = 0; k < 4; ++k)
+      fk[k] = lds_read_bf16x8<0>(row_frag_addr(k0 + (uint32_t)((t >> 1) * 8192), 32 * (t & 1), lane, k));
     lds_wait_frags(fq, fk);
     zero(sacc[t]);
 #pragma unroll
     for (int k = 0; k < 4; ++k) sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fq[k], fk[k], sacc[t], 0, 0, 0);
   }
-  // row r < 4 of S sits in element r of lanes 0-31 (slot 32 t + lane of tile t); lanes 32-63
-  // hold padding rows 4-7 and go through the same steps harmlessly
+  // head r < 4 sits in element r of lanes 0-31 (slot 32 t + lane of tile t); lanes 32-63 hold
+  // padding rows and go through the same steps harmlessly.  An empty piece has every slot masked:
+  // its weights are zero and its partial is left out of the merge.
   const float scale2 = a.scale * 1.4426950408889634f;  // scores in log2 units
   float mx[4], sum[4];
 #pragma unroll
@@ -914,28 +814,41 @@ __global__ void __launch_bounds__(64) k_swa_decode_mfma(const uttt_swa_decode_ar
       m = fmaxf(m, sacc[t][r]);
     }
     mx[r] = half_max(m);
-    float l = 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const bf16 pb = from_f32<bf16>(__builtin_amdgcn_exp2f(sacc[t][r] - mx[r]));
-      l += to_f32(pb);
-      if (lane < 32 && r < rep) {
-        const int j = 32 * t + lane, c = j & 63;
-        pt[(j >> 6) * 4096 + r * 64 + (((c >> 3) ^ row_swz(r)) << 3) + (c & 7)] = pb;
-      }
-    }
-    sum[r] = half_sum(l);
   }
-  __syncthreads();  // the P writes before the fragment reads
-  // O = P V: columns 32 cb of the head dim, k = slots in 8 steps of 16
   f32x16 oacc[2];
   zero(oacc[0]);
   zero(oacc[1]);
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int r = 0; r < 4; ++r) sum[r] = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {  // P for slots 64 h .. 64 h + 63, then O += P V over them
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = 2 * h + tt;
+        const float pf = mx[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sacc[t][r] - mx[r]);
+        const bf16 pb = from_f32<bf16>(pf);
+        sum[r] += to_f32(pb);
+        if (lane < 32 && r < rep) {
+          const int c = 32 * tt + lane;
+          pt[w][r * 64 + (((c >> 3) ^ row_swz(r)) << 3) + (c & 7)] = pb;
+        } else if (lane < 32) {
+          const int c = 32 * tt + lane;
+          pt[w][r * 64 + (((c >> 3) ^ row_swz(r)) << 3) + (c & 7)] = bf16{};
+        }
+      }
+    }
+    if (h == 0) {  // rows 4-31 of P stay zero
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        reinterpret_cast<uint4*>(&pt[w][4 * 64])[lane + 64 * i] = make_uint4(0u, 0u, 0u, 0u);
+      if (lane < 32) reinterpret_cast<uint4*>(&pt[w][4 * 64])[lane + 192] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();  // the P writes before the fragment reads
     bf16x8 fp[4], fv0[4], fv1[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) fp[k] = lds_read_bf16x8<0>(row_frag_addr(p0 + (uint32_t)(h * 8192), 0, lane, k));
+    for (int k = 0; k < 4; ++k) fp[k] = lds_read_bf16x8<0>(row_frag_addr(p0, 0, lane, k));
     slab_frags(slab_tr_addr(v0 + (uint32_t)(h * 8192), 0, lane), fv0);
     slab_frags(slab_tr_addr(v0 + (uint32_t)(h * 8192), 32, lane), fv1);
     asm volatile("s_waitcnt lgkmcnt(0)"
@@ -946,23 +859,40 @@ __global__ void __launch_bounds__(64) k_swa_decode_mfma(const uttt_swa_decode_ar
       oacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp[k], fv0[k], oacc[0], 0, 0, 0);
       oacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fp[k], fv1[k], oacc[1], 0, 0, 0);
     }
+    __syncthreads();  // every wave's P reads are done before its P tile is rewritten
   }
-  // the partial of head r: max (natural-log units, as decode_merge takes it), sum, O row
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sum[r] = half_sum(sum[r]);
   if (lane < 32) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       if (r < rep) {
-        float* q = pr + r * (HD + 2);
-        __hip_atomic_store(q + 2 + lane, oacc[0][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(q + 2 + 32 + lane, oacc[1][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        red[w][r][2 + lane] = oacc[0][r];
+        red[w][r][2 + 32 + lane] = oacc[1][r];
         if (lane == 0) {
-          __hip_atomic_store(q, mx[r] * 0.6931471805599453f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(q + 1, sum[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          red[w][r][0] = cnt > 0 ? mx[r] : -INFINITY;  // log2 units
+          red[w][r][1] = sum[r];
         }
       }
     }
   }
-  decode_merge<bf16, HD, 64>(a, pr - (int64_t)sp * rep * (HD + 2), counter, n, kvh, rep, nsplit);
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < rep * HD; idx += NW * 64) {
+    const int r = idx / HD, e = idx - r * HD;
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) m = fmaxf(m, red[u][r][0]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      if (red[u][r][0] != -INFINITY) {
+        const float f = __builtin_amdgcn_exp2f(red[u][r][0] - m);
+        den += red[u][r][1] * f;
+        num += red[u][r][2 + e] * f;
+      }
+    }
+    og[idx] = from_f32<bf16>(num / den);
+  }
 }
 
 
@@ -1028,15 +958,9 @@ static void launch_prefill(const uttt_swa_prefill_args& a, const PrefillPlan& p,
                        dim3(kThreads), 0, st, a, (const float*)part, p.nsplit, p.q_pad);
 }
 
-// bf16 rings of up to kMergeSlots slots, head_dim 64 and at most kMergeRep query heads per kv
-// head: one launch, the window split into pieces of 128 slots merged by the last workgroup (512
-// workgroups at 32 requests x 4 kv heads x 512 slots), on MFMA (k_swa_decode_mfma, one wave per
-// piece).  The vector form of the same split (kDecodeMfma false) and the whole-window form (one
-// 1024-thread workgroup per request and kv head, kDecodeWhole) are kept for comparison.
-constexpr int kMergeKeys = 128, kMergeSlots = 512, kMergeRep = 4;
-constexpr int kWholeThreads = 1024, kWholeKeys = 512, kWholeRep = 4;
-constexpr bool kDecodeWhole = false;
-constexpr bool kDecodeMfma = true;
+// k_swa_decode_window's reach: bf16 rings of up to 512 slots, head_dim 64, at most 4 query
+// heads per kv head; otherwise the split form and its combine launch
+constexpr int kWindowSlots = kWindowWaves * kPieceKeys, kWindowRep = 4;
 
 inline size_t decode_partial_bytes(int64_t n_req, int64_t n_heads, int64_t head_dim, int64_t window) {
   return align_up(sizeof(float) * (size_t)n_req * (size_t)n_heads * (size_t)decode_splits(window) *
@@ -1045,31 +969,17 @@ inline size_t decode_partial_bytes(int64_t n_req, int64_t n_heads, int64_t head_
 
 template <typename T, int HD>
 static void launch_decode(const uttt_swa_decode_args& a, hipStream_t st) {
-  const int nsplit = decode_splits(a.window);
-  float* part = static_cast<float*>(a.workspace);
-  unsigned* counters = reinterpret_cast<unsigned*>(static_cast<char*>(a.workspace) +
-                                                   decode_partial_bytes(a.n_req, a.n_heads, HD, a.window));
   if constexpr (sizeof(T) == 2 && HD == 64) {
-    if (a.window <= kMergeSlots && a.n_heads / a.n_kv_heads <= kMergeRep) {
-      if constexpr (kDecodeWhole) {
-        hipLaunchKernelGGL((k_swa_decode_part<T, HD, kWholeThreads, kWholeKeys, kWholeRep, kWhole>),
-                           dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, 1u), dim3(kWholeThreads), 0, st, a, part,
-                           counters);
-      } else if constexpr (kDecodeMfma) {
-        const int msplit = (int)((a.window + kPieceKeys - 1) / kPieceKeys);
-        hipLaunchKernelGGL(k_swa_decode_mfma, dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, (unsigned)msplit),
-                           dim3(64), 0, st, a, part, counters);
-      } else {
-        const int msplit = (int)((a.window + kMergeKeys - 1) / kMergeKeys);
-        hipLaunchKernelGGL((k_swa_decode_part<T, HD, kThreads, kMergeKeys, kMergeRep, kMerge>),
-                           dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, (unsigned)msplit), dim3(kThreads), 0, st, a,
-                           part, counters);
-      }
+    if (a.window <= kWindowSlots && a.n_heads / a.n_kv_heads <= kWindowRep) {
+      hipLaunchKernelGGL(k_swa_decode_window, dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads), dim3(kWindowWaves * 64),
+                         0, st, a);
       return;
     }
   }
+  const int nsplit = decode_splits(a.window);
+  float* part = static_cast<float*>(a.workspace);
   hipLaunchKernelGGL((k_swa_decode_part<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads, (unsigned)nsplit),
-                     dim3(kThreads), 0, st, a, part, counters);
+                     dim3(kThreads), 0, st, a, part);
   hipLaunchKernelGGL((k_swa_decode_combine<T, HD>), dim3((unsigned)a.n_req, (unsigned)a.n_kv_heads), dim3(kThreads), 0,
                      st, a, (const float*)part, nsplit);
 }
@@ -1147,7 +1057,7 @@ extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t st
 extern "C" size_t uttt_swa_decode_workspace(int64_t n_req, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
                                             int64_t window) {
   if (n_req < 1 || n_kv_heads < 1 || n_heads < n_kv_heads || window < 1 || head_dim < 1) return 0;
-  return decode_partial_bytes(n_req, n_heads, head_dim, window) + sizeof(unsigned) * (size_t)n_req * (size_t)n_kv_heads;
+  return decode_partial_bytes(n_req, n_heads, head_dim, window);
 }
 
 extern "C" int uttt_swa_decode(const uttt_swa_decode_args* a, uttt_stream_t stream) {

@@ -212,9 +212,8 @@ class BatchedDecoder:
 
     def _warm_workspaces(self) -> None:
         from . import _native as N
-        # zero-filled: the attention workspace ends with merge counters that every step leaves at zero
         nbytes = N.load_library().uttt_swa_decode_workspace(self.n, self.heads, self.hkv, self.hd, self.window)
-        self._ws_attn = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=self.device)
+        self._ws_attn = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=self.device)
         d = self.model.config.d_model
         ff = self.model.config.d_ff_fast
         code = N.DTYPE_BF16 if self.dtype == torch.bfloat16 else N.DTYPE_F32

@@ -1213,8 +1213,7 @@ def swa_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_ring: Tensor, v_ring: 
     lib = N.load_library()
     nbytes = lib.uttt_swa_decode_workspace(n, heads, hkv, hd, window)
     if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
-        # zero-filled: the workspace ends with merge counters that every call leaves at zero
-        workspace = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     a.workspace, a.workspace_bytes = _p(workspace), workspace.numel()
     with torch.cuda.device(dev):
         N.check(lib.uttt_swa_decode(C.byref(a), _stream(dev)), "uttt_swa_decode")
