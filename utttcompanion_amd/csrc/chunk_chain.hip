@@ -371,6 +371,11 @@ struct GramArgs {
   float* part;
   unsigned* counters;
   int splits;
+  // optional (bf16 path): block (l, j) also written as bf16(gamma_j * G) to scaled at the same
+  // place (row b's rows at scaled + b * out_rows * LL), gamma_j = coef[b * kCoefStride + kGam + j]:
+  // the back pass's correction operand, rounded as that pass rounded it from the fp32 block
+  bf16* scaled;
+  const float* coef;
 };
 
 // 32 x 32 quadrant tiles of the block rows [l0, l1): row l has 4 (l + 1) of them
@@ -522,11 +527,23 @@ __device__ __forceinline__ void gram_lds_tile(const GramArgs& a, int bid, char* 
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fb[k], acc, 0, 0, 0);
   }
-  float* out = a.out + ((int64_t)b * a.out_rows + a.out_r0 + l * a.out_lstep) * a.LL;
+  const int64_t out_off = ((int64_t)b * a.out_rows + a.out_r0 + l * a.out_lstep) * a.LL;
+  float* out = a.out + out_off;
   const int c = j * 64 + (q & 1) * 32 + acc_col();
-  if (a.splits == 1) {
+  auto write = [&](const float (&v)[16]) {
+    const float gj = a.scaled != nullptr ? a.coef[(int64_t)b * kCoefStride + kGam + j] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) out[(int64_t)((q >> 1) * 32 + acc_row(i)) * a.LL + c] = acc[i];
+    for (int i = 0; i < 16; ++i) {
+      const int64_t o = (int64_t)((q >> 1) * 32 + acc_row(i)) * a.LL + c;
+      out[o] = v[i];
+      if (a.scaled != nullptr) a.scaled[out_off + o] = static_cast<bf16>(gj * v[i]);
+    }
+  };
+  if (a.splits == 1) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = acc[i];
+    write(v);
     return;
   }
   const int64_t blk_id = (int64_t)b * nblk + blk;
@@ -555,8 +572,7 @@ __device__ __forceinline__ void gram_lds_tile(const GramArgs& a, int bid, char* 
 #pragma unroll
     for (int i = 0; i < 16; ++i) sum[i] += v[i];
   }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) out[(int64_t)((q >> 1) * 32 + acc_row(i)) * a.LL + c] = sum[i];
+  write(sum);
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + blk_id, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1140,6 +1156,7 @@ struct BackArgs {
   const void* wd;
   const void* sd;   // fp32 state or its bf16 copies
   const float* zz;  // (B, 64, LL): dZ_l dZ_j^T
+  const bf16* zzb;  // (B, 64, LL): bf16(gamma_j dZ_l dZ_j^T), the bf16 pass's correction operand
   const void* h_all;
   const float* u_cur;
   const float* g_cur;
@@ -1269,8 +1286,8 @@ __global__ void __launch_bounds__(kThreads) k_chain_back(const BackArgs a) {
 
 // bf16 activations and copies: both loops' operands go straight into LDS through one ring of
 // kBackSlots steps -- D/64 steps of dZ_l rows with the W_down and S_down rows of this F tile
-// (k = d along every row), then l steps of the scaled dZ Gram block (fp32, as in k_chain_up_lds)
-// with the H_j slab (transposing reads).  dZ (a W_d + b S_d)^T is formed as a dZ W_d^T + b dZ S_d^T
+// (k = d along every row), then l steps of the dZ Gram block gamma_j dZ_l dZ_j^T (bf16, scaled
+// and rounded by the Gram launch: a row tile read as is) with the H_j slab (transposing reads).  dZ (a W_d + b S_d)^T is formed as a dZ W_d^T + b dZ S_d^T
 // with two accumulators, the combined weights never rounded to bf16.  The cursor values are loaded
 // after the loops and the epilogue's dU / dG tiles reuse the ring, so registers (184) and LDS (72 KB)
 // leave room for two workgroups per CU: one computes while the other's loads are in flight
@@ -1301,18 +1318,19 @@ __global__ void __launch_bounds__(kThreads, 2) k_chain_back_lds(const BackArgs a
   const int64_t mat = (int64_t)a.F * a.D;
   const bf16* wd = static_cast<const bf16*>(a.wd) + b * mat + (int64_t)f0 * a.D;
   const bf16* sd = static_cast<const bf16*>(a.sd) + b * mat + (int64_t)f0 * a.D;
-  const float* zz = a.zz + (int64_t)b * 64 * a.LL;  // layer j's block at + 64 j
+  const bf16* zzb = a.zzb + (int64_t)b * 64 * a.LL;  // layer j's block at + 64 j
   const bf16* hsrc = static_cast<const bf16*>(a.h_all) + (int64_t)b * 64 * a.F + f0;
   const int64_t lstride = (int64_t)a.B * 64 * a.F;
   const int n1 = a.D / 64, ns = n1 + a.l;
-  // row group g of a step: phase 1: 0..7 dZ rows, 8..15 W_d rows, 16..23 S_d rows (8 rows each);
-  // phase 2: 0..15 Gram rows (4 rows each), 16..23 H rows; wave w takes groups w, w + 4, ...
+  // row group g of a step (8 rows each): phase 1: 0..7 dZ rows, 8..15 W_d rows, 16..23 S_d rows;
+  // phase 2: 0..7 Gram rows, 8..15 nothing (no range: they keep the per-step count), 16..23 H
+  // rows; wave w takes groups w, w + 4, ...
   int v1[PER], v2[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int g = w + 4 * i;
     v1[i] = row_src_off(g & 7, lane, a.D);
-    v2[i] = g < 16 ? gram_src_off(g, lane, a.LL) : slab_src_off(g & 7, lane, a.F);
+    v2[i] = g < 8 ? row_src_off(g, lane, a.LL) : (g < 16 ? 0 : slab_src_off(g & 7, lane, a.F));
   }
   const uint32_t ring0 = lds_addr(ring);
   auto issue = [&](int step) {
@@ -1332,27 +1350,25 @@ __global__ void __launch_bounds__(kThreads, 2) k_chain_back_lds(const BackArgs a
       }
     } else {
       const int j = step - n1;
-      const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(zz + 64 * j, (uint32_t)(64 * a.LL * 4));
+      const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(zzb + 64 * j, (uint32_t)(64 * a.LL * 2));
       const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(hsrc + j * lstride, (uint32_t)(64 * a.F * 2));
+      const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(zzb, 0u);
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int g = w + 4 * i;
-        buffer_load_lds_raw(g < 16 ? rg : rh, lds_ptr(slot + (uint32_t)(g * 1024)), 16, v2[i], 0, 0, 0);
+        buffer_load_lds_raw(g < 8 ? rg : (g < 16 ? rn : rh), lds_ptr(slot + (uint32_t)(g * 1024)), 16, v2[i], 0, 0,
+                            0);
       }
     }
   };
   for (int t = 0; t < min(ns, kBackSlots - 1); ++t) issue(t);
-  uint32_t tz[4], tw[4], ts[4], tg[8];
+  uint32_t tz[4], tw[4], ts[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    tz[k] = row_frag_addr(ring0, wr, lane, k);
+    tz[k] = row_frag_addr(ring0, wr, lane, k);  // dZ rows in phase 1, Gram rows in phase 2
     tw[k] = row_frag_addr(ring0 + 8192u, wc, lane, k);
     ts[k] = row_frag_addr(ring0 + 16384u, wc, lane, k);
   }
-  // Gram A fragments: row wr + lane % 32, fp32 pieces 4 s + 2 h and + 1 (h = lane / 32)
-  const int ia = wr + (lane & 31), ha = lane >> 5;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) tg[q] = ring0 + (uint32_t)(ia * 256 + (((2 * q + 2 * ha - (q & 1)) ^ (ia & 15)) * 16));
   const uint32_t th = slab_tr_addr(ring0 + 16384u, wc, lane);
   f32x16 accw, accs, accg;
   zero(accw);
@@ -1381,26 +1397,13 @@ __global__ void __launch_bounds__(kThreads, 2) k_chain_back_lds(const BackArgs a
         if (with_s) accs = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fz[k], fs[k], accs, 0, 0, 0);
       }
     } else {
-      const int j = step - n1;
-      bf16x8 fh[4];
+      bf16x8 fh[4], fa[4];
       slab_frags(th + so, fh);
-      f32x4 kv[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) kv[q] = lds_read_b128(tg[q] + so);
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(fh[0]), "+v"(fh[1]), "+v"(fh[2]), "+v"(fh[3]), "+v"(kv[0]), "+v"(kv[1]), "+v"(kv[2]),
-                     "+v"(kv[3]), "+v"(kv[4]), "+v"(kv[5]), "+v"(kv[6]), "+v"(kv[7]));
-      const float gj = cf[kGam + j];
+      for (int k = 0; k < 4; ++k) fa[k] = lds_read_bf16x8<0>(tz[k] + so);
+      lds_wait_frags(fa, fh);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        bf16x8 fa;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          fa[e] = static_cast<bf16>(gj * kv[2 * k][e]);
-          fa[4 + e] = static_cast<bf16>(gj * kv[2 * k + 1][e]);
-        }
-        accg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fh[k], accg, 0, 0, 0);
-      }
+      for (int k = 0; k < 4; ++k) accg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fh[k], accg, 0, 0, 0);
     }
   }
   float dh[16];
@@ -2053,7 +2056,7 @@ inline bool apply_wide_fits(int64_t D, int64_t F) {
 size_t act_size(int32_t dtype) { return dtype == UTTT_DTYPE_BF16 ? 2 : 4; }
 
 struct ChainLayout {
-  size_t pq, kk, hh, zz, h_all, du_all, dg_all, dz_all, u_cur, g_cur, zp, loss, npart, coef, total;
+  size_t pq, kk, hh, zz, zzb, h_all, du_all, dg_all, dz_all, u_cur, g_cur, zp, loss, npart, coef, total;
   size_t gpart_k, gpart_l, gcnt;  // split-feature Gram partials (key Gram; H / dZ Grams) and counters
   int nsplit, max_key_blocks, ncounters;
 };
@@ -2070,6 +2073,7 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
   c.kk = take(sizeof(float) * B * LL * LL);
   c.hh = take(sizeof(float) * B * 64 * LL);
   c.zz = take(sizeof(float) * B * 64 * LL);
+  c.zzb = take(sizeof(uint16_t) * B * 64 * LL);
   c.h_all = take(e * L * B * 64 * F);
   c.du_all = take(e * L * B * 64 * F);
   c.dg_all = take(e * L * B * 64 * F);
@@ -2324,11 +2328,16 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
     za.layer = l;
     za.layer_end = l + 1;
+    if (sizeof(T) == 2 && bf16_src) {  // the bf16 back pass reads the row scaled by this layer's gammas
+      za.scaled = reinterpret_cast<bf16*>(ws + c.zzb);
+      za.coef = cl;
+    }
     launch_gram<T>(B, l, l + 1, za, st, gate);
 
     BackArgs ba{};
     ba.B = B; ba.L = L; ba.C = C; ba.D = D; ba.F = F; ba.LL = LL; ba.l = l;
     ba.coef = cl; ba.dz_all = dz_all; ba.wd = wd_src; ba.sd = sd_src; ba.zz = zz; ba.h_all = h_all;
+    ba.zzb = reinterpret_cast<const bf16*>(ws + c.zzb);
     ba.u_cur = u_cur; ba.g_cur = g_cur; ba.kk = kk; ba.du_all = du_all; ba.dg_all = dg_all; ba.npart = npart;
     if (sizeof(T) == 2 && bf16_src) {
       if (gate.next("k_chain_back_lds"))
