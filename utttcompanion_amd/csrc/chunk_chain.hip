@@ -936,6 +936,7 @@ struct DownArgs {
   const void* wd;
   const void* sd;  // (B, F, D): fp32 state or its bf16 copies
   const float* hh;  // (B, 64, LL): H_l H_j^T
+  const bf16* hhb;  // (B, 64, LL): bf16(gamma_j H_l H_j^T), the bf16 pass's correction operand
   const void* dz_all;  // (L, B, 64, D)
   float* zp;           // (nsplit + correction splits, B, 64, D)
 };
@@ -1013,9 +1014,9 @@ __global__ void __launch_bounds__(kThreads) k_chain_down(const DownArgs a) {
 
 
 // bf16 activations and copies: a main split streams H_l rows (k = f) with the W_down and S_down
-// tiles of its F range (rows f hold 64 d columns: transposing reads), a correction split the
-// scaled H Gram blocks (fp32, as in k_chain_up_lds) with the dZ_j slabs, straight into LDS
-// through a ring of kDownSlots steps.  H (a W_d + b S_d) is formed as a H W_d + b H S_d.
+// tiles of its F range (rows f hold 64 d columns: transposing reads), a correction split the H
+// Gram blocks gamma_j H_l H_j^T (bf16, scaled and rounded by the Gram launch: row tiles read as
+// is) with the dZ_j slabs, straight into LDS through a ring of kDownSlots steps.  H (a W_d + b S_d) is formed as a H W_d + b H S_d.
 constexpr int kDownSlots = 3;
 
 __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
@@ -1051,14 +1052,15 @@ __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
   const bf16* sd = static_cast<const bf16*>(a.sd) + b * mat + d0;
   const bf16* dsrc = static_cast<const bf16*>(a.dz_all) + (int64_t)b * 64 * a.D + d0;
   const int64_t lstride = (int64_t)a.B * 64 * a.D;
-  const float* hh = a.hh + (int64_t)b * 64 * a.LL;  // layer j's block at + 64 j
+  const bf16* hhb = a.hhb + (int64_t)b * 64 * a.LL;  // layer j's block at + 64 j
   int voff[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int g = w + 4 * i;  // main: 0..7 H rows, 8..15 W_d rows, 16..23 S_d rows;
-                              // correction: 0..15 Gram rows (4 each), 16..23 dZ rows
+    const int g = w + 4 * i;  // main: 0..7 H rows, 8..15 W_d rows, 16..23 S_d rows (8 rows each);
+                              // correction: 0..7 Gram rows, 8..15 nothing (no range: they keep
+                              // the per-step count), 16..23 dZ rows
     voff[i] = main_split ? (g < 8 ? row_src_off(g & 7, lane, a.F) : slab_src_off(g & 7, lane, a.D))
-                         : (g < 16 ? gram_src_off(g, lane, a.LL) : slab_src_off(g & 7, lane, a.D));
+                         : (g < 8 ? row_src_off(g, lane, a.LL) : (g < 16 ? 0 : slab_src_off(g & 7, lane, a.D)));
   }
   const uint32_t ring0 = lds_addr(ring);
   auto issue = [&](int t) {
@@ -1077,22 +1079,21 @@ __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
       }
     } else {
       const int j = s0 + t;
-      const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(hh + 64 * j, (uint32_t)(64 * a.LL * 4));
+      const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(hhb + 64 * j, (uint32_t)(64 * a.LL * 2));
       const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(dsrc + j * lstride, (uint32_t)(64 * a.D * 2));
+      const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(hhb, 0u);
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int g = w + 4 * i;
-        buffer_load_lds_raw(g < 16 ? rg : rz, lds_ptr(slot + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
+        buffer_load_lds_raw(g < 8 ? rg : (g < 16 ? rn : rz), lds_ptr(slot + (uint32_t)(g * 1024)), 16, voff[i], 0, 0,
+                            0);
       }
     }
   };
   for (int t = 0; t < min(nst, kDownSlots - 1); ++t) issue(t);
-  uint32_t th[4], tg[8];
+  uint32_t th[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) th[k] = row_frag_addr(ring0, wr, lane, k);
-  const int ia = wr + (lane & 31), ha = lane >> 5;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) tg[q] = ring0 + (uint32_t)(ia * 256 + (((2 * q + 2 * ha - (q & 1)) ^ (ia & 15)) * 16));
+  for (int k = 0; k < 4; ++k) th[k] = row_frag_addr(ring0, wr, lane, k);  // H rows, or the Gram rows
   const uint32_t tw = slab_tr_addr(ring0 + 8192u, wc, lane), ts = slab_tr_addr(ring0 + 16384u, wc, lane);
   const uint32_t tz = slab_tr_addr(ring0 + 16384u, wc, lane);
   f32x16 accw, accs;
@@ -1118,25 +1119,13 @@ __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
         if (with_s) accs = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fh[k], fs[k], accs, 0, 0, 0);
       }
     } else {
-      bf16x8 fz[4];
+      bf16x8 fz[4], fa[4];
       slab_frags(tz + so, fz);
-      f32x4 kv[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) kv[q] = lds_read_b128(tg[q] + so);
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(fz[0]), "+v"(fz[1]), "+v"(fz[2]), "+v"(fz[3]), "+v"(kv[0]), "+v"(kv[1]), "+v"(kv[2]),
-                     "+v"(kv[3]), "+v"(kv[4]), "+v"(kv[5]), "+v"(kv[6]), "+v"(kv[7]));
-      const float gj = cf[kGam + s0 + t];
+      for (int k = 0; k < 4; ++k) fa[k] = lds_read_bf16x8<0>(th[k] + so);
+      lds_wait_frags(fa, fz);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        bf16x8 fa;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          fa[e] = static_cast<bf16>(gj * kv[2 * k][e]);
-          fa[4 + e] = static_cast<bf16>(gj * kv[2 * k + 1][e]);
-        }
-        accw = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fz[k], accw, 0, 0, 0);
-      }
+      for (int k = 0; k < 4; ++k) accw = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[k], fz[k], accw, 0, 0, 0);
     }
   }
   float* zp = a.zp + (((int64_t)split * a.B + b) * 64) * a.D + d0;
@@ -2056,7 +2045,7 @@ inline bool apply_wide_fits(int64_t D, int64_t F) {
 size_t act_size(int32_t dtype) { return dtype == UTTT_DTYPE_BF16 ? 2 : 4; }
 
 struct ChainLayout {
-  size_t pq, kk, hh, zz, zzb, h_all, du_all, dg_all, dz_all, u_cur, g_cur, zp, loss, npart, coef, total;
+  size_t pq, kk, hh, zz, zzb, hhb, h_all, du_all, dg_all, dz_all, u_cur, g_cur, zp, loss, npart, coef, total;
   size_t gpart_k, gpart_l, gcnt;  // split-feature Gram partials (key Gram; H / dZ Grams) and counters
   int nsplit, max_key_blocks, ncounters;
 };
@@ -2074,6 +2063,7 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
   c.hh = take(sizeof(float) * B * 64 * LL);
   c.zz = take(sizeof(float) * B * 64 * LL);
   c.zzb = take(sizeof(uint16_t) * B * 64 * LL);
+  c.hhb = take(sizeof(uint16_t) * B * 64 * LL);
   c.h_all = take(e * L * B * 64 * F);
   c.du_all = take(e * L * B * 64 * F);
   c.dg_all = take(e * L * B * 64 * F);
@@ -2300,11 +2290,16 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
 
     ha.layer = l;
     ha.layer_end = l + 1;
+    if (sizeof(T) == 2 && bf16_src) {  // the bf16 down pass reads the row scaled by this layer's gammas
+      ha.scaled = reinterpret_cast<bf16*>(ws + c.hhb);
+      ha.coef = cl;
+    }
     launch_gram<T>(B, l, l + 1, ha, st, gate);
 
     DownArgs da{};
     da.B = B; da.L = L; da.C = C; da.D = D; da.F = F; da.LL = LL; da.l = l; da.nsplit = c.nsplit;
     da.coef = cl; da.h_all = h_all; da.wd = wd_src; da.sd = sd_src; da.hh = hh; da.dz_all = dz_all; da.zp = zp;
+    da.hhb = reinterpret_cast<const bf16*>(ws + c.hhb);
     const int ncorr = (l + kCorrPerSplit - 1) / kCorrPerSplit;
     const dim3 down_grid(row_tile_blocks(B, (D / 64) * (c.nsplit + ncorr)));
     if (sizeof(T) == 2 && bf16_src) {
