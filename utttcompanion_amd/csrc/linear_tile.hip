@@ -254,8 +254,11 @@ extern "C" size_t uttt_linear_workspace(int64_t m, int64_t n, int64_t k) {
   return linear_workspace_bytes(plan_linear(m, n, k, device_cus()));
 }
 
-extern "C" int uttt_linear(const uttt_linear_args* a, uttt_stream_t stream) {
+namespace uttt {
+
+int linear_enqueue(const uttt_linear_args* a, hipStream_t st, int tile_rows) {
   UTTT_REQUIRE(a != nullptr, "args is NULL");
+  UTTT_REQUIRE(tile_rows == 0 || tile_rows == 128, "tile_rows must be 0 or 128");
   UTTT_REQUIRE(a->act_dtype == UTTT_DTYPE_BF16, "uttt_linear takes bf16 operands");
   UTTT_REQUIRE(a->m >= 1 && a->n >= 1 && a->k >= 64 && a->k % 64 == 0 && a->m <= (1 << 24) && a->n <= (1 << 24) &&
                    a->k <= (1 << 16),
@@ -269,7 +272,8 @@ extern "C" int uttt_linear(const uttt_linear_args* a, uttt_stream_t stream) {
                "out / residual row strides must be at least n");
   UTTT_REQUIRE((int64_t)64 * a->x_row_stride * 2 <= 0xffffffffLL && (int64_t)64 * a->w_row_stride * 2 <= 0xffffffffLL,
                "row strides too large");
-  const LinPlan p = plan_linear(a->m, a->n, a->k, device_cus());
+  const LinPlan p = tile_rows == 128 ? LinPlan{128, 1, ((a->m + 127) / 128) * ((a->n + kLinNT - 1) / kLinNT)}
+                                     : plan_linear(a->m, a->n, a->k, device_cus());
   UTTT_REQUIRE(p.tiles * p.splits < (1LL << 31) && (p.splits == 1 || p.tiles <= kMaxSplitTiles), "too many tiles");
   const size_t need = linear_workspace_bytes(p);
   UTTT_REQUIRE(a->workspace_bytes >= need && (need == 0 || (a->workspace != nullptr && aligned16(a->workspace))),
@@ -287,11 +291,16 @@ extern "C" int uttt_linear(const uttt_linear_args* a, uttt_stream_t stream) {
     l.counters = static_cast<unsigned*>(a->workspace);
     l.part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + kCounterBytes);
   }
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(p.tiles * p.splits));
   if (p.mt == 128)
     hipLaunchKernelGGL((k_linear<128, kSlots128>), grid, dim3(kLinThreads), 0, st, l);
   else
     hipLaunchKernelGGL((k_linear<64, kSlots64>), grid, dim3(kLinThreads), 0, st, l);
   return launch_status("uttt_linear");
+}
+
+}  // namespace uttt
+
+extern "C" int uttt_linear(const uttt_linear_args* a, uttt_stream_t stream) {
+  return linear_enqueue(a, static_cast<hipStream_t>(stream), 0);
 }

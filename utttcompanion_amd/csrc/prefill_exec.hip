@@ -95,7 +95,11 @@ extern "C" int uttt_prefill_chunk(const uttt_prefill_chunk_args* a, uttt_stream_
     attn.q_offset = a->kv_offset;
     attn.kv_len = a->kv_offset + attn.q_len;
     hipEvent_t projected = events.ev[2 * l], read = events.ev[2 * l + 1];
-    UTTT_TRY(uttt_linear(&c.qkv, ms));
+    // the QKV product in 128-row tiles without a k split (96 workgroups at config 3): alone on
+    // the GPU the planner's 64-row tiles are faster (13.4 against 16.3 us), but here the product
+    // shares the CUs with the chain stream, and the config-3 prefill measured 554 ms against 556
+    // with a k split of 2 and 561-572 with the planner's tiles
+    UTTT_TRY(linear_enqueue(&c.qkv, ms, 128));
     UTTT_TRY(uttt_rope_kv_append(&rope, ms));
     UTTT_TRY(uttt_swa_prefill(&attn, ms));
     UTTT_TRY(uttt_linear(&c.attn_out, ms));

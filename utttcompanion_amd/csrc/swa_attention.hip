@@ -202,7 +202,10 @@ static PrefillPlan prefill_plan(int64_t batch, int64_t heads, int64_t q_len, int
   p.q_pad = p.nqt * 64;
   const int64_t base = (int64_t)p.nqt * heads * batch;
   const int max_tiles = prefill_max_tiles(kv_len, window);
-  int64_t ns = (512 + base - 1) / base;
+  // about 256 workgroups (one per CU): in the chunk-first prefill the attention shares the GPU
+  // with the layer chain, and at config 3 (64 workgroups before the split) 256 measured faster
+  // than 128, 192, 320 or 512 workgroups (prefill 552-556 against 554-561 ms on one box)
+  int64_t ns = (256 + base - 1) / base;
   if (ns > max_tiles) ns = max_tiles;
   if (ns > kMaxPrefillSplits) ns = kMaxPrefillSplits;
   if (ns < 1) ns = 1;

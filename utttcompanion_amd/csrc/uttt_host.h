@@ -43,6 +43,10 @@ void launch_saved_readout(int B, int ntok, int D, int F, int nsplit, const float
                           int64_t wd_rs, float* zp, const float* x, int64_t x_rs, const float* ln_w,
                           const float* ln_b, float eps, float* out, int64_t out_rs, hipStream_t st);
 
+// uttt_linear with the tile shape chosen by the caller: tile_rows 0 plans it from the shape
+// (as uttt_linear does), 128 takes 128-row tiles without a k split (no workspace needed).
+int linear_enqueue(const uttt_linear_args* a, hipStream_t st, int tile_rows);
+
 }  // namespace uttt
 
 #define UTTT_REQUIRE(cond, ...)                              \
