@@ -460,7 +460,9 @@ __global__ void __launch_bounds__(kGramWaves * 64) k_chain_gram(const GramArgs a
 // reads the partials back with device-coherent loads (no cache write-back or invalidate between
 // XCDs), sums them in slice order (deterministic) and returns the counter to zero.
 constexpr int kGramSlots = 3;
-constexpr int kGramSplitSteps = 8;
+// 1024-feature slices: in the chunk-first prefill the chain shares the GPU with the forward
+// pass, and fewer, longer Gram workgroups measured faster there than 512- or 256-feature slices
+constexpr int kGramSplitSteps = 16;
 
 __host__ __device__ inline int gram_blocks(int l0, int l1) { return (l1 * (l1 + 1) - l0 * (l0 + 1)) / 2; }
 __host__ __device__ inline int gram_splits(int kd) { return (kd / 64 + kGramSplitSteps - 1) / kGramSplitSteps; }
@@ -941,7 +943,8 @@ struct DownArgs {
   float* zp;           // (nsplit + correction splits, B, 64, D)
 };
 
-constexpr int kCorrPerSplit = 2;  // layers j per correction split
+// layers j per correction split (3 measured faster in the prefills than 1, 2 or 4)
+constexpr int kCorrPerSplit = 3;
 
 template <typename T, typename WT>
 __global__ void __launch_bounds__(kThreads) k_chain_down(const DownArgs a) {
@@ -2054,7 +2057,9 @@ ChainLayout chain_layout(int64_t B, int64_t L, int64_t D, int64_t F, int32_t dty
   ChainLayout c;
   const size_t e = act_size(dtype);
   const int64_t LL = L * 64, nF = F / 64;
-  int64_t s = (512 + (D / 64) * B - 1) / ((D / 64) * B);
+  // the down pass's F splits: about 256 workgroups before the correction splits (config 3: 2
+  // splits; measured in the prefills against 1, 3, 4 and 8)
+  int64_t s = (256 + (D / 64) * B - 1) / ((D / 64) * B);
   c.nsplit = (int)(s < 1 ? 1 : (s > nF ? nF : s));
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t at = off; off += align_up(bytes); return at; };
