@@ -735,9 +735,9 @@ __global__ void __launch_bounds__(kWindowWaves * 64) k_swa_decode_window(const u
       buffer_load_lds_raw(rv, lds_ptr(v0 + (uint32_t)(h * 8192 + g * 1024)), 16, slab_src_off(g, lane, HD), 0, 0, 0);
     }
   }
-  // the query tile starts at zero (rows past the heads stay zero)
-  reinterpret_cast<uint4*>(qt)[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
-  __syncthreads();
+  // rows past the query heads of the query tile are zero (rows 0 .. rep-1 are written below,
+  // so no barrier is needed between the two writes)
+  if (threadIdx.x >= rep * 8) reinterpret_cast<uint4*>(qt)[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
   // RoPE of the query heads (wave 0 writes them) and of the new key (kept by the wave whose piece
   // holds this step's slot, which writes the ring)
   const bf16* qg = static_cast<const bf16*>(a.q) + n * a.q_stride_n + (int64_t)kvh * rep * HD;
@@ -762,18 +762,21 @@ __global__ void __launch_bounds__(kWindowWaves * 64) k_swa_decode_window(const u
       } else if (owns_slot) {
         knew[0] = lo;
         knew[1] = hi;
-        kr[slot * HD + e] = lo;
-        kr[slot * HD + e + half] = hi;
       }
     }
-    if (owns_slot) {
-      vnew_v = vn[lane];
-      vr[slot * HD + lane] = vnew_v;
-    }
+    if (owns_slot) vnew_v = vn[lane];
   }
   const bool key_lane = ((rep & 1) == 0) == (lane < 32);  // the half of the wave that took row rep
   wait_vmcnt<0>();  // this wave's K / V rows have landed in LDS
   if (owns_slot) {  // this step's slot: the new key and value replace what the ring held
+    // the ring writes go out after the wait (the vector memory counter counts stores too, so
+    // issued earlier they would sit on the wait), and after every load of this piece
+    if (key_lane) {
+      const int e = lane & (half - 1);
+      kr[slot * HD + e] = knew[0];
+      kr[slot * HD + e + half] = knew[1];
+    }
+    vr[slot * HD + lane] = vnew_v;
     const int h = ts >> 6, t = ts & 63;
     bf16* krow = &kv[w][h][t * 64];
     bf16* vrow = &kv[w][2 + h][t * 64];
