@@ -59,6 +59,15 @@ __global__ void __launch_bounds__(kSkWaves * 64) k_skinny_linear(const SkArgs a)
     xo[g] = row_src_off(g, lane, (int)a.xs);
     wo[g] = row_src_off(g, lane, (int)a.ws);
   }
+  // wave 0 writes the output: its residual values load first, beside the operand loads (every
+  // residual load issued before any store: out may alias the residual; each workgroup reads and
+  // writes only its own 32 x 32 block)
+  const int col = n0 + acc_col();
+  float rv[16];
+  if (w == 0 && a.r != nullptr) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) rv[i] = to_f32(a.r[(int64_t)(m0 + min(acc_row(i), rows - 1)) * a.rs + col]);
+  }
   f32x16 acc;
   zero(acc);
   float ss = 0.f;  // sum of squares of this lane's x pieces (row lane & 31)
@@ -111,12 +120,6 @@ __global__ void __launch_bounds__(kSkWaves * 64) k_skinny_linear(const SkArgs a)
   }
   __syncthreads();
   if (w != 0) return;
-  const int col = n0 + acc_col();
-  float rv[16];
-  if (a.r != nullptr) {  // every residual load issued at once, before any store (out may alias it)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) rv[i] = to_f32(a.r[(int64_t)(m0 + min(acc_row(i), rows - 1)) * a.rs + col]);
-  }
   float v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
