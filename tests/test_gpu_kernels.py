@@ -449,6 +449,53 @@ def test_swa_decode_wide_windows_bf16(win, hkv):
         assert torch.equal(dk[r, :, p % win].cpu(), rk[r, :, p]), "the new key goes to slot pos mod window"
 
 
+def test_swa_decode_nan_slots_and_bad_position_bf16():
+    """Ring slots that are not yet valid hold NaN (the kernel reads whole pieces before it knows
+    the position, so their value rows must not reach the output), and a position past the RoPE
+    table gives a NaN output with that request's ring untouched while the others decode."""
+    K = kernels()
+    hd, h, hkv, win = 64, 12, 4, 512
+    pos = [0, 5, 130, 300]
+    n = len(pos)
+    total = 512
+    g = torch.Generator().manual_seed(11)
+    qs = torch.randn(n, total, h, hd, generator=g).bfloat16()
+    ks = torch.randn(n, total, hkv, hd, generator=g).bfloat16()
+    vs = torch.randn(n, total, hkv, hd, generator=g).bfloat16()
+    cos, sin = om.rope_tables(hd, total)
+    rq = om.apply_rope(qs.transpose(1, 2), cos, sin)
+    rk = om.apply_rope(ks.transpose(1, 2), cos, sin)
+    rv = vs.transpose(1, 2)
+    k_ring = torch.full((n, hkv, win, hd), float("nan")).bfloat16()
+    v_ring = torch.full((n, hkv, win, hd), float("nan")).bfloat16()
+    for r, p in enumerate(pos):
+        for j in range(p):
+            k_ring[r, :, j] = rk[r, :, j]
+            v_ring[r, :, j] = rv[r, :, j]
+    q = torch.stack([qs[r, p] for r, p in enumerate(pos)])
+    kn = torch.stack([ks[r, p] for r, p in enumerate(pos)])
+    vn = torch.stack([vs[r, p] for r, p in enumerate(pos)])
+    bad = 2
+    run_pos = list(pos)
+    run_pos[bad] = total  # one past the table
+    dk, dv = to_dev(k_ring, v_ring)
+    with torch.no_grad():
+        got = K.swa_decode(*to_dev(q, kn, vn), dk, dv, torch.tensor(run_pos, dtype=torch.int64, device=DEV),
+                           *to_dev(cos, sin))
+    torch.cuda.synchronize()
+    for r, p in enumerate(pos):
+        if r == bad:
+            assert torch.isnan(got[r].float()).all(), "a position past the RoPE table must give NaN"
+            assert torch.equal(dk[r].cpu().nan_to_num(7.0), k_ring[r].nan_to_num(7.0)), "ring must stay untouched"
+            assert torch.equal(dv[r].cpu().nan_to_num(7.0), v_ring[r].nan_to_num(7.0)), "ring must stay untouched"
+            continue
+        want = om.sliding_window_attention(rq[r:r + 1, :, p:p + 1].float(), rk[r:r + 1, :, :p + 1].float(),
+                                           rv[r:r + 1, :, :p + 1].float(), win, p)[0, :, 0]
+        out = got[r].float().cpu()
+        assert torch.isfinite(out).all(), f"request {r} at {p}: a stale NaN slot reached the output"
+        assert max_abs(out, want) <= BF16_ABS, f"request {r} at {p}"
+
+
 def padded(t):
     """t (..., n) as a view of a buffer whose rows are padded to a whole number of 16-byte
     vectors: the form the one-wave-per-row epilogue (16-byte accesses) takes."""

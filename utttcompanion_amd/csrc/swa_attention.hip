@@ -711,22 +711,16 @@ __global__ void __launch_bounds__(kWindowWaves * 64) k_swa_decode_window(const u
   const int lane = threadIdx.x & 63;
   const int rep = (int)(a.n_heads / a.n_kv_heads);
   const int64_t W = a.window;
-  const int64_t pos = a.positions[n];
-  bf16* og = static_cast<bf16*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
-  if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) {  // loud NaN output, cache untouched
-    for (int idx = threadIdx.x; idx < rep * HD; idx += NW * 64) og[idx] = from_f32<bf16>(NAN);
-    return;
-  }
-  const int64_t slot = pos % W;
-  const int valid = (int)min(pos + 1, W);
-  const int j_lo = w * KEYS, cnt = max(0, min(valid, j_lo + KEYS) - j_lo);  // this wave's slots
+  const int j_lo = w * KEYS;
+  const int span = (int)max((int64_t)0, min(W - j_lo, (int64_t)KEYS));  // ring slots of this wave's piece
   bf16* kr = static_cast<bf16*>(a.k_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
   bf16* vr = static_cast<bf16*>(a.v_ring) + n * a.ring_stride_n + (int64_t)kvh * W * HD;
-  // this wave's K / V rows into LDS (rows past cnt read as zeros; an empty piece moves nothing)
+  // this wave's K / V rows into LDS, issued before the request's position is known (rows past the
+  // ring read as zeros; value rows of slots not yet valid are cleared after the loads land)
   const uint32_t k0 = lds_addr(&kv[w][0][0]), v0 = lds_addr(&kv[w][2][0]);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int rows = min(max(cnt - 64 * h, 0), 64);
+    const int rows = min(max(span - 64 * h, 0), 64);
     const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kr + (int64_t)(j_lo + 64 * h) * HD, (uint32_t)(rows * HD * 2));
     const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(vr + (int64_t)(j_lo + 64 * h) * HD, (uint32_t)(rows * HD * 2));
 #pragma unroll
@@ -735,6 +729,16 @@ __global__ void __launch_bounds__(kWindowWaves * 64) k_swa_decode_window(const u
       buffer_load_lds_raw(rv, lds_ptr(v0 + (uint32_t)(h * 8192 + g * 1024)), 16, slab_src_off(g, lane, HD), 0, 0, 0);
     }
   }
+  const int64_t pos = a.positions[n];
+  bf16* og = static_cast<bf16*>(a.out) + n * a.o_stride_n + (int64_t)kvh * rep * HD;
+  if (pos < 0 || (a.cos_table != nullptr && pos >= a.table_len)) {  // loud NaN output, cache untouched
+    for (int idx = threadIdx.x; idx < rep * HD; idx += NW * 64) og[idx] = from_f32<bf16>(NAN);
+    wait_vmcnt<0>();  // no LDS write of this workgroup's loads outlives it
+    return;
+  }
+  const int64_t slot = pos % W;
+  const int valid = (int)min(pos + 1, W);
+  const int cnt = max(0, min(valid, j_lo + KEYS) - j_lo);  // this wave's valid slots
   // rows past the query heads of the query tile are zero (rows 0 .. rep-1 are written below,
   // so no barrier is needed between the two writes)
   if (threadIdx.x >= rep * 8) reinterpret_cast<uint4*>(qt)[threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
@@ -768,6 +772,15 @@ __global__ void __launch_bounds__(kWindowWaves * 64) k_swa_decode_window(const u
   }
   const bool key_lane = ((rep & 1) == 0) == (lane < 32);  // the half of the wave that took row rep
   wait_vmcnt<0>();  // this wave's K / V rows have landed in LDS
+  // value rows of slots not yet valid: zeros (their weights are zero, and 0 x NaN would not be);
+  // key rows there are masked out of the scores by selection.  A piece with no valid slot is
+  // left out of the merge.
+  if (cnt > 0 && cnt < span) {
+    for (int i = lane; i < (span - cnt) * 8; i += 64) {
+      const int t = cnt + (i >> 3);
+      reinterpret_cast<uint4*>(&kv[w][2 + (t >> 6)][(t & 63) * 64])[i & 7] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
   if (owns_slot) {  // this step's slot: the new key and value replace what the ring held
     // the ring writes go out after the wait (the vector memory counter counts stores too, so
     // issued earlier they would sit on the wait), and after every load of this piece
