@@ -66,6 +66,9 @@ __global__ void __launch_bounds__(kSelThreads) k_greedy_select(const SelectArgs 
   const int row = blockIdx.x;
   const T* x = static_cast<const T*>(a.logits) + (int64_t)row * a.rs;
   Best b{-INFINITY, 0x7fffffff};
+  // the position to advance loads beside the logits, not after the reduction
+  int64_t adv = 0;
+  if (threadIdx.x == 0 && a.advance != nullptr) adv = a.advance[row];
   const int nvec = a.vocab / VEC;
   for (int c0 = threadIdx.x; c0 < nvec; c0 += kSelThreads * kSelUnroll) {
     vec_t v[kSelUnroll];
@@ -103,7 +106,7 @@ __global__ void __launch_bounds__(kSelThreads) k_greedy_select(const SelectArgs 
   if (threadIdx.x == 0) {
     for (int q = 1; q < kSelThreads / 64; ++q) take(b, sv[q], si[q]);
     a.out[row] = (int64_t)b.i;
-    if (a.advance != nullptr) a.advance[row] += 1;
+    if (a.advance != nullptr) a.advance[row] = adv + 1;
   }
 }
 
