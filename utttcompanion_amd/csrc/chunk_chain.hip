@@ -320,7 +320,7 @@ __device__ __forceinline__ void pq_lds_tile(const PqArgs& a, int bid, char* ring
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int g = w + 4 * i;
-      buffer_load_lds_raw(g < 8 ? rk : rx, lds_ptr(base + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
+      buffer_load_lds16(g >= 8, g < 8 ? rk : rx, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
     }
   };
   for (int j = 0; j < min(nsteps, kPqSlots - 1); ++j) issue(j);
@@ -1077,8 +1077,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int g = w + 4 * i;
-        buffer_load_lds_raw(g < 8 ? rh : (g < 16 ? rw : rs), lds_ptr(slot + (uint32_t)(g * 1024)), 16, voff[i], 0,
-                            0, 0);
+        buffer_load_lds16(g >= 8, g < 8 ? rh : (g < 16 ? rw : rs), lds_ptr(slot + (uint32_t)(g * 1024)), voff[i]);
       }
     } else {
       const int j = s0 + t;

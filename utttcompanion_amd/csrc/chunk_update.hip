@@ -190,7 +190,7 @@ __global__ void __launch_bounds__(KEYS ? 512 : 256) k_up_gate_lds(const FwdArgs 
         const int sl = ti - NA, h = sl % NB;
         r = buffer_rsrc((sl < NB ? wu : wg) + (int64_t)d0 * a.F + 64 * h, (uint32_t)(64 * a.F * 2 - 128 * h));
       }
-      buffer_load_lds_raw(r, lds_ptr(base + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
+      buffer_load_lds16(ti >= NA, r, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
     }
   };
   for (int j = 0; j < min(nsteps, SLOTS - 1); ++j) issue(j);
@@ -337,7 +337,7 @@ __global__ void __launch_bounds__(kThreads) k_down_partial_lds(const FwdArgs a, 
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int g = w + 4 * i;
-      buffer_load_lds_raw(g < 8 ? rh : rw, lds_ptr(base + (uint32_t)(g * 1024)), 16, voff[i], 0, 0, 0);
+      buffer_load_lds16(g >= 8, g < 8 ? rh : rw, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
     }
   };
   for (int j = 0; j < min(nsteps, kDpSlots - 1); ++j) issue(j);

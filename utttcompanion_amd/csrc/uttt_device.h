@@ -305,6 +305,17 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 __device__ void buffer_load_lds_raw(__amdgpu_buffer_rsrc_t rsrc, lds_void_ptr lds, int size, int voffset, int soffset,
                                     int offset, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.load.lds");
 
+// a 16-byte-per-lane direct-to-LDS load whose cache policy follows a wave-uniform choice: data
+// streamed once (the state copies) goes non-temporal, so that it does not push out of L2 the
+// slabs that the other tiles of a row re-read; everything else keeps the default policy
+__device__ __forceinline__ void buffer_load_lds16(bool streamed, __amdgpu_buffer_rsrc_t rsrc, lds_void_ptr lds,
+                                                  int voffset) {
+  if (streamed)
+    buffer_load_lds_raw(rsrc, lds, 16, voffset, 0, 0, kNonTemporal);
+  else
+    buffer_load_lds_raw(rsrc, lds, 16, voffset, 0, 0, 0);
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(p);  // the low half of a generic LDS address is its offset
 }
