@@ -312,6 +312,7 @@ __device__ __forceinline__ void pq_lds_tile(const PqArgs& a, int bid, char* ring
   }
   const uint32_t ring0 = lds_addr(ring);
   const int nsteps = a.D / 64;
+  const bool nt = stream_nt(a.B, a.D, a.F);  // the streamed state copies: non-temporal
   auto issue = [&](int step) {  // key rows past C are out of the buffer range: zeros
     const int d0 = step * 64;
     const uint32_t base = ring0 + (uint32_t)((step % kPqSlots) * kSlot);
@@ -320,7 +321,7 @@ __device__ __forceinline__ void pq_lds_tile(const PqArgs& a, int bid, char* ring
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int g = w + 4 * i;
-      buffer_load_lds16(g >= 8, g < 8 ? rk : rx, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
+      buffer_load_lds16(g >= 8 && nt, g < 8 ? rk : rx, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
     }
   };
   for (int j = 0; j < min(nsteps, kPqSlots - 1); ++j) issue(j);
@@ -1066,6 +1067,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
                          : (g < 8 ? row_src_off(g, lane, a.LL) : (g < 16 ? 0 : slab_src_off(g & 7, lane, a.D)));
   }
   const uint32_t ring0 = lds_addr(ring);
+  const bool nt = stream_nt(a.B, a.D, a.F);  // the streamed state copies: non-temporal
   auto issue = [&](int t) {
     const uint32_t slot = ring0 + (uint32_t)((t % kDownSlots) * kSlot);
     if (main_split) {
@@ -1077,7 +1079,7 @@ __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int g = w + 4 * i;
-        buffer_load_lds16(g >= 8, g < 8 ? rh : (g < 16 ? rw : rs), lds_ptr(slot + (uint32_t)(g * 1024)), voff[i]);
+        buffer_load_lds16(g >= 8 && nt, g < 8 ? rh : (g < 16 ? rw : rs), lds_ptr(slot + (uint32_t)(g * 1024)), voff[i]);
       }
     } else {
       const int j = s0 + t;

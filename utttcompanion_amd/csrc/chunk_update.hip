@@ -177,6 +177,7 @@ __global__ void __launch_bounds__(KEYS ? 512 : 256) k_up_gate_lds(const FwdArgs 
   }
   const uint32_t ring0 = lds_addr(ring);
   const int nsteps = a.D / 64;
+  const bool nt = stream_nt(a.B, a.D, a.F);  // the streamed state copies: non-temporal
   auto issue = [&](int step) {
     const int d0 = step * 64;
     const uint32_t base = ring0 + (uint32_t)((step % SLOTS) * kSlot);
@@ -190,7 +191,7 @@ __global__ void __launch_bounds__(KEYS ? 512 : 256) k_up_gate_lds(const FwdArgs 
         const int sl = ti - NA, h = sl % NB;
         r = buffer_rsrc((sl < NB ? wu : wg) + (int64_t)d0 * a.F + 64 * h, (uint32_t)(64 * a.F * 2 - 128 * h));
       }
-      buffer_load_lds16(ti >= NA, r, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
+      buffer_load_lds16(ti >= NA && nt, r, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
     }
   };
   for (int j = 0; j < min(nsteps, SLOTS - 1); ++j) issue(j);
@@ -330,6 +331,7 @@ __global__ void __launch_bounds__(kThreads) k_down_partial_lds(const FwdArgs a, 
     voff[i] = g < 8 ? row_src_off(g & 7, lane, a.F) : slab_src_off(g & 7, lane, a.D);
   }
   const uint32_t ring0 = lds_addr(ring);
+  const bool nt = stream_nt(a.B, a.D, a.F);  // the streamed state copies: non-temporal
   auto issue = [&](int step) {
     const uint32_t base = ring0 + (uint32_t)((step % kDpSlots) * kSlot);
     const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(h + step * 64, (uint32_t)(64 * a.F * 2));
@@ -337,7 +339,7 @@ __global__ void __launch_bounds__(kThreads) k_down_partial_lds(const FwdArgs a, 
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int g = w + 4 * i;
-      buffer_load_lds16(g >= 8, g < 8 ? rh : rw, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
+      buffer_load_lds16(g >= 8 && nt, g < 8 ? rh : rw, lds_ptr(base + (uint32_t)(g * 1024)), voff[i]);
     }
   };
   for (int j = 0; j < min(nsteps, kDpSlots - 1); ++j) issue(j);

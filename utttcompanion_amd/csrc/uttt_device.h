@@ -316,6 +316,17 @@ __device__ __forceinline__ void buffer_load_lds16(bool streamed, __amdgpu_buffer
     buffer_load_lds_raw(rsrc, lds, 16, voffset, 0, 0, 0);
 }
 
+// Whether a pass over the bf16 state copies of B rows (D x F each) streams them non-temporally:
+// only when the two matrices a pass reads (4 B D F bytes) exceed 96 MiB.  Smaller passes keep the
+// default policy, so that the next pass over the same copies (the back pass after the down pass)
+// still finds them in the 256 MB infinity cache: measured, non-temporal loads took the config-2
+// prefill (50 MB per pass) from 59.9 to 62.4 ms while the config-3 prefill (180 MB per pass) went
+// from 544 to 530 ms.
+constexpr int64_t kStreamNtMinElems = 24LL << 20;
+__device__ __forceinline__ bool stream_nt(int B, int D, int F) {
+  return (int64_t)B * D * F > kStreamNtMinElems;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(p);  // the low half of a generic LDS address is its offset
 }
