@@ -1067,7 +1067,6 @@ __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
                          : (g < 8 ? row_src_off(g, lane, a.LL) : (g < 16 ? 0 : slab_src_off(g & 7, lane, a.D)));
   }
   const uint32_t ring0 = lds_addr(ring);
-  const bool nt = stream_nt(a.B, a.D, a.F);  // the streamed state copies: non-temporal
   auto issue = [&](int t) {
     const uint32_t slot = ring0 + (uint32_t)((t % kDownSlots) * kSlot);
     if (main_split) {
@@ -1079,7 +1078,8 @@ __global__ void __launch_bounds__(kThreads) k_chain_down_lds(const DownArgs a) {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int g = w + 4 * i;
-        buffer_load_lds16(g >= 8 && nt, g < 8 ? rh : (g < 16 ? rw : rs), lds_ptr(slot + (uint32_t)(g * 1024)), voff[i]);
+        buffer_load_lds_raw(g < 8 ? rh : (g < 16 ? rw : rs), lds_ptr(slot + (uint32_t)(g * 1024)), 16, voff[i], 0,
+                            0, 0);
       }
     } else {
       const int j = s0 + t;

@@ -317,11 +317,13 @@ __device__ __forceinline__ void buffer_load_lds16(bool streamed, __amdgpu_buffer
 }
 
 // Whether a pass over the bf16 state copies of B rows (D x F each) streams them non-temporally:
-// only when the two matrices a pass reads (4 B D F bytes) exceed 96 MiB.  Smaller passes keep the
-// default policy, so that the next pass over the same copies (the back pass after the down pass)
-// still finds them in the 256 MB infinity cache: measured, non-temporal loads took the config-2
-// prefill (50 MB per pass) from 59.9 to 62.4 ms while the config-3 prefill (180 MB per pass) went
-// from 544 to 530 ms.
+// only when the two matrices a pass reads (4 B D F bytes) exceed 96 MiB, and only in passes whose
+// copies no later pass of the chunk reads again (the snapshot products, the readout).  Smaller
+// passes keep the default policy, and so do the down pass and the back pass at every size: the back
+// pass re-reads the down pass's W_down / S_down copies, and finds them in the 256 MB infinity
+// cache.  Measured: the hint on every pass took the config-2 prefill (50 MB per pass) from 59.9 to
+// 62.4 ms; at config 3 (180 MB per pass) it took the prefill from 544 to 530 ms, and leaving the
+// down pass out of it to 523 ms.
 constexpr int64_t kStreamNtMinElems = 24LL << 20;
 __device__ __forceinline__ bool stream_nt(int B, int D, int F) {
   return (int64_t)B * D * F > kStreamNtMinElems;
