@@ -32,7 +32,7 @@ enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE =
 
 /* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
  * Python binding reads it from this header and refuses a library built from another one. */
-#define UTTT_ABI_VERSION 20
+#define UTTT_ABI_VERSION 22
 
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
@@ -120,8 +120,10 @@ int uttt_chunk_update_noalloc(const uttt_chunk_update_args* args, uttt_stream_t 
  *     q/k/v/out (T, D) row-major; eta/alpha/token_mask (T,); surprise (n_chunks,)
  *     receives each chunk's surprise.  The state outputs may alias the inputs.
  *     A barrier that waits past its bound (about a second) sets the flag word at
- *     uttt_layer_update_resident_flag_offset in the workspace and no later barrier
- *     waits: the results are then invalid, and the caller should check the flag.
+ *     uttt_layer_update_resident_flag_offset in the workspace (cleared by every call)
+ *     and no later barrier waits, so every workgroup still runs to its end; the call's
+ *     results are then invalid, and it writes NaN into its output state, surprise and
+ *     (for the chunks from the failing launch on) readout.
  * ------------------------------------------------------------------------- */
 typedef struct {
   int64_t batch;       /* must be 1 */
@@ -142,6 +144,9 @@ typedef struct {
   float* surprise;
   unsigned* error_word;  /* optional device word (NULL = none): set to 1 when a barrier timed out;
                             never cleared by the library, so it collects the failures of many calls */
+  int32_t force_timeout; /* test hook, normally 0: nonzero runs the call as if its first barrier had
+                            timed out (flag and error word set before the first launch, no barrier
+                            waits, every kernel runs to its end, NaN results) */
 } uttt_layer_update_args;
 
 int uttt_layer_update_resident_supported(int64_t batch, int64_t d_model, int64_t d_ff);
@@ -462,8 +467,10 @@ int uttt_linear(const uttt_linear_args* args, uttt_stream_t stream);
  *     sets the per-chunk fields (rope start_pos / kv_offset, attention q_offset / kv_len =
  *     kv_offset + q_len, the chain's token_mask / mask_row_stride / surprise) in its own copies.
  *     The chain args must already name every layer's k / v / eta / alpha (the epilogue's
- *     outputs).  Calls on one device are serialised; a failing call may leave part of the chunk
- *     enqueued.
+ *     outputs).  The call keeps no state between calls: the events that order the two streams
+ *     belong to the caller (created with uttt_events_create), and a deferred join is handed to
+ *     the next call explicitly (defer_join, wait_event).  Concurrent calls from several host
+ *     threads must use distinct event sets.  A failing call may leave part of the chunk enqueued.
  * ------------------------------------------------------------------------- */
 typedef struct {
   uttt_linear_args qkv;
@@ -486,16 +493,33 @@ typedef struct {
   int64_t kv_offset;                       /* KV index of the chunk's first token */
   const float* token_mask; int64_t mask_row_stride; /* (batch, >= tokens) fp32 or NULL */
   float* surprise;                         /* (n_layers,) */
-  /* nonzero: main_stream does not wait for this chunk's state write; the next call on the
-   * device makes its main_stream wait for it just before layer 0's readout (the state's first
-   * reader), so that call's layer-0 QKV .. epilogue overlap the state write.  The state write
-   * reads layer 0's k / v / eta / alpha: the next call's layer-0 epilogue must write other
-   * buffers (the caller alternates two sets).  A deferred call cannot end a graph capture, and
-   * the last call of a sequence passes 0. */
+  /* nonzero: main_stream does not wait for this chunk's state write (recorded into
+   * events[2 n_layers + 1]); the caller passes that event as the next call's wait_event, whose
+   * main_stream waits for it just before layer 0's readout (the state's first reader), so that
+   * call's layer-0 QKV .. epilogue overlap the state write.  The state write reads layer 0's
+   * k / v / eta / alpha: the next call's layer-0 epilogue must write other buffers (the caller
+   * alternates two sets).  The last call of a sequence passes 0.  Refused (UTTT_ERR_INVALID,
+   * nothing enqueued) while main_stream is capturing: a capture must not end with the chain
+   * stream unjoined. */
   int32_t defer_join;
+  /* caller-owned hipEvent_t handles (uttt_events_create), n_events >= 2 n_layers + 2: two per
+   * layer (projections done, readout done), then the forward's end and the state write */
+  void* const* events; int32_t n_events;
+  /* NULL, or the state-write event of a previous call made with defer_join: main_stream waits
+   * for it before layer 0's readout.  Refused while main_stream is capturing (the event was
+   * recorded outside the capture). */
+  void* wait_event;
 } uttt_prefill_chunk_args;
 
 int uttt_prefill_chunk(const uttt_prefill_chunk_args* args, uttt_stream_t main_stream, uttt_stream_t chain_stream);
+
+/* Event plumbing for uttt_prefill_chunk (no counterpart in the reference: its chunk-first
+ * prefill, model/uttt_model.py:453-608, runs on one stream): n events created on the current
+ * device with timing disabled, destroyed, and a stream made to wait for one (the join a caller
+ * owes the main stream after a deferred call it does not follow up, e.g. on an exception). */
+int uttt_events_create(int32_t n, void** events);
+int uttt_events_destroy(int32_t n, void* const* events);
+int uttt_stream_wait_event(uttt_stream_t stream, void* event);
 
 /* ---------------------------------------------------------------------------
  * 9. Greedy next-token selection: per row, argmax of the logits with the excluded ids and the

@@ -109,3 +109,30 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     s.n, s.act_dtype = 64, N.DTYPE_F32
     assert lib.uttt_skinny_linear(C.byref(s), None) == 1
     assert b"bf16" in lib.uttt_last_error()
+
+
+def test_prefill_chunk_refuses_missing_events_before_any_launch(lib):
+    """The chunk executor keeps no state of its own: the events that order its two streams come
+    from the caller, and a call without a full set is refused before anything is enqueued."""
+    ch = N.ChunkChainArgs()
+    ch.layers = 2
+    calls = (N.PrefillLayerCalls * 2)()
+    a = N.PrefillChunkArgs()
+    a.n_layers, a.layers, a.chain = 2, C.cast(calls, C.POINTER(N.PrefillLayerCalls)), C.pointer(ch)
+    assert lib.uttt_prefill_chunk(C.byref(a), C.c_void_p(1), C.c_void_p(2)) == 1
+    assert b"caller-owned events" in lib.uttt_last_error()
+    ev = (C.c_void_p * 5)(*([C.c_void_p(8)] * 5))
+    a.events, a.n_events = C.cast(ev, C.POINTER(C.c_void_p)), 5  # 2 n_layers + 2 = 6 needed
+    assert lib.uttt_prefill_chunk(C.byref(a), C.c_void_p(1), C.c_void_p(2)) == 1
+    assert b"2 n_layers + 2 = 6" in lib.uttt_last_error()
+    ev6 = (C.c_void_p * 6)(*([C.c_void_p(8)] * 5 + [None]))
+    a.events, a.n_events = C.cast(ev6, C.POINTER(C.c_void_p)), 6
+    assert lib.uttt_prefill_chunk(C.byref(a), C.c_void_p(1), C.c_void_p(2)) == 1
+    assert b"events[5] is NULL" in lib.uttt_last_error()
+    a.defer_join = 2
+    assert lib.uttt_prefill_chunk(C.byref(a), C.c_void_p(1), C.c_void_p(2)) == 1
+    assert b"defer_join must be 0 or 1" in lib.uttt_last_error()
+    assert lib.uttt_events_create(1, None) == 1
+    assert lib.uttt_events_destroy(1, None) == 1
+    assert lib.uttt_stream_wait_event(None, None) == 1
+    assert b"event must be non-NULL" in lib.uttt_last_error()

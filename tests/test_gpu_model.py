@@ -423,3 +423,78 @@ def test_prefill_chunk_executor_long_window_matches_per_call_path():
     for n, t, u in zip(NAMES, a[1], b[1]):
         assert max_abs(t, u) <= 2e-2, n
     assert rel_err(a[2], b[2]) <= 1e-2
+
+
+def test_prefill_chunk_executor_interleaved_prefills_match_separate_runs():
+    """Two bf16 prefills with deferred joins on stream pairs of their own (two models, so two
+    chain streams), their chunk calls interleaved one by one: each equals the same prefill run
+    alone, bit for bit.  The executor keeps no state between calls (each plan owns its events and
+    hands its deferred state write to its own next call), so neither prefill waits on, or skips,
+    the other's state write."""
+    ma, _ = build(dtype=torch.bfloat16)
+    mb, _ = build(dtype=torch.bfloat16, seed=9)
+    ids_a, mask_a = ids_and_mask(2, 72, 256, seed=45)  # 4 chunks of 16 + a tail of 8: two plans
+    ids_b, _ = ids_and_mask(2, 56, 256, seed=46)
+    ids_a, mask_a, ids_b = ids_a.to(DEV), mask_a.to(DEV), ids_b.to(DEV)
+    sa = ma.init_fast_state(2, device=DEV, dtype=torch.float32, detach=True)
+    sb = mb.init_fast_state(2, device=DEV, dtype=torch.float32, detach=True)
+    with torch.no_grad():
+        alone = {"a": ma.prefill_with_writes(ids_a, sa, mask_a), "b": mb.prefill_with_writes(ids_b, sb)}
+        torch.cuda.synchronize()
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        live = {"a": (ma.prefill_steps(ids_a, sa, mask_a), s1), "b": (mb.prefill_steps(ids_b, sb), s2)}
+        together, steps = {}, 0
+        while live:
+            for name in list(live):
+                gen, st = live[name]
+                with torch.cuda.stream(st):
+                    try:
+                        next(gen)
+                        steps += 1
+                    except StopIteration as done:
+                        together[name] = done.value
+                        del live[name]
+        torch.cuda.synchronize()
+    assert steps == 5 + 4
+    for name in ("a", "b"):
+        x, y = together[name], alone[name]
+        assert torch.equal(x[0], y[0]), name
+        for n, t, u in zip(NAMES, x[1], y[1]):
+            assert torch.equal(t, u), (name, n)
+        assert torch.equal(x[2], y[2]), name
+
+
+def test_prefill_chunk_refuses_a_deferred_join_under_capture():
+    """``uttt_prefill_chunk`` with ``defer_join`` or a ``wait_event`` on a capturing stream is
+    refused before it enqueues anything (a deferred join would leave the chain stream unjoined
+    at the end of the capture, and the event to wait for was recorded outside it); the capture
+    then goes on and replays normally."""
+    import ctypes as C
+    from utttcompanion_amd import _native as N
+    lib = N.load_library()
+    ev = (C.c_void_p * 4)()
+    N.check(lib.uttt_events_create(4, ev), "uttt_events_create")
+    ch = N.ChunkChainArgs()
+    ch.layers = 1
+    calls = (N.PrefillLayerCalls * 1)()
+    a = N.PrefillChunkArgs()
+    a.n_layers, a.layers, a.chain = 1, C.cast(calls, C.POINTER(N.PrefillLayerCalls)), C.pointer(ch)
+    a.events, a.n_events = C.cast(ev, C.POINTER(C.c_void_p)), 4
+    side = torch.cuda.Stream()
+    x = torch.zeros(4, device=DEV)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        a.defer_join = 1
+        rc1 = lib.uttt_prefill_chunk(C.byref(a), torch.cuda.current_stream().cuda_stream, side.cuda_stream)
+        err1 = lib.uttt_last_error()
+        a.defer_join, a.wait_event = 0, ev[3]
+        rc2 = lib.uttt_prefill_chunk(C.byref(a), torch.cuda.current_stream().cuda_stream, side.cuda_stream)
+        err2 = lib.uttt_last_error()
+        x.add_(1.0)
+    assert rc1 == 1 and b"graph capture" in err1
+    assert rc2 == 1 and b"graph capture" in err2
+    graph.replay()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(x.cpu(), torch.full((4,), 2.0))
+    N.check(lib.uttt_events_destroy(4, ev), "uttt_events_destroy")

@@ -113,6 +113,36 @@ def test_resident_update_in_place_equals_fresh_outputs_and_repeats():
     assert inplace[1].data_ptr() == state[0].data_ptr()
 
 
+def test_resident_barrier_timeout_is_loud_and_reported_once():
+    """The timeout path, forced from the host (``force_timeout``: the flag is raised before the
+    first launch, so no barrier waits and every kernel runs to its end): every result of that
+    call is NaN (state, surprise, readout, over all three launches of a 33-chunk call), the
+    report is raised once (the sticky device word is cleared with it), and the next call is
+    clean and matches the oracle."""
+    from utttcompanion_amd import kernels as K
+    q, k, v, eta, alpha, w, s, ln_w, ln_b = make_inputs(2100, 256, 256, seed=21, eta_scale=3.0)
+    dev = [t.to(DEV) for t in (q, k, v, eta, alpha, *w, *s, ln_w, ln_b)]
+    K.check_resident_flags(wait=True)  # nothing pending from earlier tests
+    with torch.no_grad():
+        bad = K.layer_update_resident(*dev, None, 0.9, 1.0, True, 1e-5, force_timeout=True)
+    torch.cuda.synchronize()
+    for name, t in zip(("readout",) + NAMES + ("surprise",), bad):
+        assert torch.isnan(t).all(), name
+    with pytest.raises(RuntimeError, match="barrier timed out"):
+        K.check_resident_flags(wait=True)
+    K.check_resident_flags(wait=True)  # reported once
+    ref_out, ref_state, ref_sur = oracle_loop(q[:, :200], k[:, :200], v[:, :200], eta[:, :200], alpha[:, :200], w,
+                                              s, ln_w, ln_b, None, 64, 1.0, True)
+    with torch.no_grad():
+        good = K.layer_update_resident(*(t[:, :200] for t in dev[:5]), *dev[5:], None, 0.9, 1.0, True, 1e-5)
+    torch.cuda.synchronize()
+    K.check_resident_flags(wait=True)
+    assert rel_err(good[0], ref_out) <= F32_REL
+    for name, a, e in zip(NAMES, good[1:7], ref_state):
+        assert rel_err(a, e) <= F32_REL, name
+    assert rel_err(good[7], ref_sur) <= F32_REL
+
+
 def test_layer_forward_takes_the_resident_path_for_one_fp32_row(monkeypatch):
     """uTTTLayer.forward with one fp32 row runs the resident launch (counted) and matches the
     oracle's layer forward; two rows take the per-chunk path and match it too."""

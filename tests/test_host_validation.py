@@ -98,3 +98,13 @@ def test_noalloc_update_refuses_shapes_past_its_scratch(lib):
     msg = lib.uttt_last_error()
     assert b"device-resident scratch" in msg and str(need).encode() in msg
     assert lib.uttt_chunk_update_noalloc(None, None) == 1
+
+
+def test_prefill_plan_refuses_a_deferred_join_under_capture(monkeypatch):
+    """``PrefillPlan.run`` refuses ``defer_join`` and ``wait_event`` while the current stream is
+    capturing, before it touches a buffer or the library (the plan itself is never consulted)."""
+    from utttcompanion_amd.prefill_plan import PrefillPlan
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    for kw in (dict(defer_join=True), dict(wait_event=12345)):
+        with pytest.raises(ValueError, match="graph capture"):
+            PrefillPlan.run(object(), None, 0, 0, 0, None, None, None, None, **kw)

@@ -70,7 +70,7 @@ class LayerUpdateArgs(C.Structure):
         ("s_up_out", _P), ("s_gate_out", _P), ("s_down_out", _P),
         ("out", _P),
         ("surprise", _P),
-        ("error_word", _P),
+        ("error_word", _P), ("force_timeout", _I32),
     ]
 
 
@@ -217,6 +217,7 @@ class PrefillChunkArgs(C.Structure):
         ("chain_workspace", _P), ("chain_workspace_bytes", C.c_size_t),
         ("start_pos", _I64), ("kv_offset", _I64),
         ("token_mask", _P), ("mask_row_stride", _I64), ("surprise", _P), ("defer_join", _I32),
+        ("events", C.POINTER(_P)), ("n_events", _I32), ("wait_event", _P),
     ]
 
 
@@ -234,6 +235,9 @@ SIGNATURES = {
     "uttt_linear": (C.c_int, [C.POINTER(LinearArgs), _P]),
     "uttt_linear_workspace": (C.c_size_t, [_I64, _I64, _I64]),
     "uttt_prefill_chunk": (C.c_int, [C.POINTER(PrefillChunkArgs), _P, _P]),
+    "uttt_events_create": (C.c_int, [_I32, C.POINTER(_P)]),
+    "uttt_events_destroy": (C.c_int, [_I32, C.POINTER(_P)]),
+    "uttt_stream_wait_event": (C.c_int, [_P, _P]),
     "uttt_chunk_chain_workspace": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_chunk_chain": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_chain_stage": (C.c_int, [C.POINTER(ChunkChainArgs), _P, C.c_size_t, _I32, _P]),

@@ -136,12 +136,15 @@ struct OutPtrs {
   float* p[6];  // W_up, W_gate, W_down, S_up, S_gate, S_down
 };
 
-// Before each launch of k_resident_update: the barrier counter restarts; the error flag is cleared
-// by the first launch of a call only, so that it reports a timeout in any of them.
-__global__ void __launch_bounds__(kThreads) k_resident_init(unsigned char* ws, const OutPtrs outs, int clear_flag) {
+// Before each launch of k_resident_update: the barrier counter restarts; the error flag is set by
+// the first launch of a call only (flag_mode 1: cleared, 2: raised, as if a barrier had timed out,
+// with the error word; 0: kept), so that it reports a timeout in any of the call's launches.
+__global__ void __launch_bounds__(kThreads) k_resident_init(unsigned char* ws, const OutPtrs outs, int flag_mode,
+                                                            unsigned* error_word) {
   if (threadIdx.x == 0) {
     *reinterpret_cast<unsigned*>(ws + WsLayout::kCounter) = 0u;
-    if (clear_flag) *reinterpret_cast<unsigned*>(ws + WsLayout::kFlag) = 0u;
+    if (flag_mode != 0) *reinterpret_cast<unsigned*>(ws + WsLayout::kFlag) = flag_mode == 2 ? 1u : 0u;
+    if (flag_mode == 2 && error_word != nullptr) *error_word = 1u;
   }
   if (threadIdx.x < 6) reinterpret_cast<float**>(ws + WsLayout::kOutPtrs)[threadIdx.x] = outs.p[threadIdx.x];
 }
@@ -611,6 +614,11 @@ __global__ void __launch_bounds__(kThreads, 1) k_resident_update(const ResArgs a
   // ---- the final state.  The lane index is re-derived through an empty asm statement so that the
   // compiler recomputes these addresses here instead of keeping the ones of the initial loads live
   // (in registers, or spilled) through the chunk loop.
+  // A barrier of this call that waited past its bound (every workgroup that passed a timed-out
+  // barrier sees the flag by now) leaves the results invalid: they are made loud instead, NaN in
+  // the state, the surprise of this launch's chunks and, through the saved query H, their readout.
+  const bool timed_out = __hip_atomic_load(ws_flag(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+  const float nan = __builtin_nanf("");
   float* const* outs = reinterpret_cast<float* const*>(a.ws + WsLayout::kOutPtrs);
   int lane_f = threadIdx.x & 63;
   asm volatile("" : "+v"(lane_f));
@@ -621,13 +629,24 @@ __global__ void __launch_bounds__(kThreads, 1) k_resident_update(const ResArgs a
     for (int i = 0; i < 4; ++i) {
       const int d = dbase + 16 * m + 4 * kq_f + i;
       const int64_t off = (int64_t)d * a.F + f0 + (col_f & 7);
-      outs[col_f < kCols ? 0 : 1][off] = w_ug[m][i];
-      outs[col_f < kCols ? 3 : 4][off] = s_ug_lds[(wave * ND + m) * 64 + lane_f][i];
-      if (col_f < kCols) outs[5][(int64_t)(f0 + col_f) * D + d] = s_dn_lds[(wave * ND + m) * 32 + 8 * kq_f + col_f][i];
+      outs[col_f < kCols ? 0 : 1][off] = timed_out ? nan : w_ug[m][i];
+      outs[col_f < kCols ? 3 : 4][off] = timed_out ? nan : s_ug_lds[(wave * ND + m) * 64 + lane_f][i];
+      if (col_f < kCols)
+        outs[5][(int64_t)(f0 + col_f) * D + d] = timed_out ? nan : s_dn_lds[(wave * ND + m) * 32 + 8 * kq_f + col_f][i];
     }
   for (int i = threadIdx.x; i < kCols * D; i += kThreads) {
     const int c = i / D, d = i % D;
-    outs[2][(int64_t)(f0 + c) * D + d] = wdn[c * WDLD + d];
+    outs[2][(int64_t)(f0 + c) * D + d] = timed_out ? nan : wdn[c * WDLD + d];
+  }
+  if (timed_out) {
+    const int nseg = a.c_end - a.c_begin;  // this workgroup's 8 columns of each chunk's saved query H
+    const f32x4 nan4{nan, nan, nan, nan};
+    for (int i = threadIdx.x; i < nseg * 64 * 2; i += kThreads) {
+      const int slot = i >> 7, t = (i >> 1) & 63, half = i & 1;
+      *reinterpret_cast<f32x4*>(ws_hq<D>(a) + ((int64_t)slot * 64 + t) * a.F + f0 + 4 * half) = nan4;
+    }
+    if (w == 0)
+      for (int c = a.c_begin + threadIdx.x; c < a.c_end; c += kThreads) a.surprise[c] = nan;
   }
 }
 
@@ -736,7 +755,8 @@ extern "C" int uttt_layer_update_resident(const uttt_layer_update_args* a, void*
         r.s[m] = outs.p[3 + m];
       }
     }
-    hipLaunchKernelGGL(k_resident_init, dim3(1), dim3(kThreads), 0, st, r.ws, outs, c0 == 0 ? 1 : 0);
+    hipLaunchKernelGGL(k_resident_init, dim3(1), dim3(kThreads), 0, st, r.ws, outs,
+                       c0 == 0 ? (a->force_timeout ? 2 : 1) : 0, a->error_word);
     switch (D) {
       case 128: hipLaunchKernelGGL(k_resident_update<2>, grid, blk, 0, st, r); break;
       case 256: hipLaunchKernelGGL(k_resident_update<4>, grid, blk, 0, st, r); break;

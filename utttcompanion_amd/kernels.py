@@ -321,16 +321,22 @@ def resident_update_eligible(q: Tensor, w_up: Tensor, chunk_size: int) -> bool:
 
 def check_resident_flags(wait: bool = False) -> None:
     """Raise if a finished ``layer_update_resident`` launch reports a device-wide barrier that
-    waited past its bound (its results are then invalid).  ``wait`` blocks until every launch so
-    far has been accounted for."""
+    waited past its bound (that call's results are then invalid: it wrote NaN into its state,
+    surprise and readout).  ``wait`` blocks until every launch so far has been accounted for.
+    A report is raised once: the device word and its mirror are cleared first, so later calls
+    are not blamed for it."""
     for dev, errs in _resident_errors.items():
         if wait:
             errs.mirror.copy_(errs.word.cpu())
         elif not (errs.recorded and errs.event.query()):
             continue
         if int(errs.mirror[0]) != 0:
+            with torch.cuda.device(dev):
+                errs.word.zero_()
+                torch.cuda.current_stream().synchronize()
+            errs.mirror.zero_()
             raise RuntimeError(f"uttt_layer_update_resident on cuda:{dev}: a device-wide barrier timed out (the "
-                               "workgroups were not all resident); its results are invalid")
+                               "workgroups were not all resident); that call's results are invalid (NaN)")
 
 
 def layer_update_resident(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
@@ -339,13 +345,15 @@ def layer_update_resident(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: T
                           ln_weight: Tensor, ln_bias: Tensor, token_mask: Optional[Tensor],
                           momentum_beta: float, max_inner_grad_norm: float, normalize_by_dim: bool, eps: float,
                           chunk_size: int = 64, out_state: Optional[Sequence[Tensor]] = None,
-                          workspace: Optional[Tensor] = None) -> Tuple[Tensor, ...]:
+                          workspace: Optional[Tensor] = None, force_timeout: bool = False) -> Tuple[Tensor, ...]:
     """All chunks of one layer's forward for one fp32 row (``uttt_layer_update_resident``):
     chunk c reads the state left by chunk c - 1, its readout goes through its own pre-update
     state.  ``q/k/v`` (1, T, D); ``eta/alpha`` (1, T) or (1, T, 1); ``token_mask`` (1, T) or
     None; state (1, D, F) / (1, F, D).  Returns ``(readout (1, T, D), W_up', W_gate', W_down',
     S_up', S_gate', S_down', surprise (n_chunks,))``; ``out_state`` may be the input state
-    for an in-place update."""
+    for an in-place update.  A device-wide barrier that times out makes every result NaN and is
+    reported by ``check_resident_flags`` (also at the start of a later call);
+    ``force_timeout`` (a test hook) runs the call as if its first barrier had timed out."""
     if q.dim() != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError(f"q/k/v must share one (1, T, D) shape, got {tuple(q.shape)}, {tuple(k.shape)}, "
                          f"{tuple(v.shape)}")
@@ -408,6 +416,7 @@ def layer_update_resident(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: T
     a.out, a.surprise = _p(out), _p(surprise)
     errs = _errors_for(dev)
     a.error_word = _p(errs.word)
+    a.force_timeout = int(bool(force_timeout))
     with torch.cuda.device(dev):
         capturing = torch.cuda.is_current_stream_capturing()
         if not capturing:  # (event queries are not allowed under graph capture)

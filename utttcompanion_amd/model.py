@@ -27,6 +27,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _native as N
 from . import kernels as K
 from .prefill_plan import PrefillPlan, plan_supported
 from .layer import FastWeightState, RMSNorm, SharedFastWeightPool, linear_residual, require_write_chunk, uTTTBlock
@@ -215,7 +216,26 @@ class uTTTModel(nn.Module):
                             attention_mask: Optional[Tensor] = None,
                             kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0,
                             kernel_timer: Optional["K.KernelTimer"] = None, executor: bool = True):
-        """Chunk-first forward with fast-weight writes, without any host synchronisation.
+        """Chunk-first forward with fast-weight writes, without any host synchronisation: every
+        chunk of ``prefill_steps`` enqueued back to back; returns what it returns."""
+        steps = self.prefill_steps(input_ids, state, attention_mask, kv_caches, start_pos, kernel_timer, executor)
+        while True:
+            try:
+                next(steps)
+            except StopIteration as done:
+                return done.value
+
+    def prefill_steps(self, input_ids: Tensor, state: FastWeightState, attention_mask: Optional[Tensor] = None,
+                      kv_caches: Optional[List[Tuple[Tensor, Tensor]]] = None, start_pos: int = 0,
+                      kernel_timer: Optional["K.KernelTimer"] = None, executor: bool = True):
+        """Generator form of ``prefill_with_writes``: yields each chunk's index once the chunk is
+        enqueued (on the stream current at the first step, which every later step must keep
+        current) and returns the result.  Two prefills on different streams may interleave
+        their steps: a prefill's state is its own (the chunk executor's events belong to its
+        plans), and if the generator is abandoned after a chunk whose state write was deferred,
+        the main stream still waits for that write.
+
+        Chunk-first forward with fast-weight writes, without any host synchronisation.
         ``kernel_timer`` (measurement only) records events around the chain kernels it follows.
         With bf16 activations each chunk goes to the GPU in one call (``uttt_prefill_chunk``,
         ``PrefillPlan``); ``executor=False`` (or a ``kernel_timer``) enqueues it launch by launch
@@ -281,23 +301,30 @@ class uTTTModel(nn.Module):
             plans: Dict[int, PrefillPlan] = {}
             ws_chain = None
             capturing = torch.cuda.is_current_stream_capturing()
-            for ci in range(n_chunks):
-                off = ci * c
-                tokens = min(seq, off + c) - off
-                plan = plans.get(tokens)
-                if plan is None:
-                    run = K.ChunkChainRun(n_layers, tokens, cur, ln_w, ln_b, None, pool.momentum_beta, clip,
-                                          pool.normalize_loss_by_dim, pool.eps, h.dtype, copies=copies,
-                                          surprise=surprises[ci], workspace=ws_chain, w_products_given=True)
-                    ws_chain = run.workspace
-                    plan = PrefillPlan(self, bsz, tokens, dev, k_bufs, v_bufs, hist + seq, start_pos + seq, read,
-                                       ln_w, ln_b, pool.eps, run)
-                    plans[tokens] = plan
-                # each chunk's state write overlaps the next chunk's layer-0 projections and attention;
-                # not in a HIP graph, whose executor runs the chunks' cross joins slower (config 2:
-                # 88 ms against 64.7 ms per prefill with every call joined)
-                plan.run(h, off, start_pos + off, hist + off, mask_f, surprises[ci], main, side,
-                         defer_join=ci + 1 < n_chunks and not capturing)
+            pending = None  # the state-write event of a chunk whose join was deferred
+            try:
+                for ci in range(n_chunks):
+                    off = ci * c
+                    tokens = min(seq, off + c) - off
+                    plan = plans.get(tokens)
+                    if plan is None:
+                        run = K.ChunkChainRun(n_layers, tokens, cur, ln_w, ln_b, None, pool.momentum_beta, clip,
+                                              pool.normalize_loss_by_dim, pool.eps, h.dtype, copies=copies,
+                                              surprise=surprises[ci], workspace=ws_chain, w_products_given=True)
+                        ws_chain = run.workspace
+                        plan = PrefillPlan(self, bsz, tokens, dev, k_bufs, v_bufs, hist + seq, start_pos + seq,
+                                           read, ln_w, ln_b, pool.eps, run)
+                        plans[tokens] = plan
+                    # each chunk's state write overlaps the next chunk's layer-0 projections and
+                    # attention; not in a HIP graph, whose executor runs the chunks' cross joins
+                    # slower (config 2: 88 ms against 64.7 ms per prefill with every call joined)
+                    pending = plan.run(h, off, start_pos + off, hist + off, mask_f, surprises[ci], main, side,
+                                       defer_join=ci + 1 < n_chunks and not capturing, wait_event=pending)
+                    yield ci
+            finally:
+                if pending is not None:  # stopped after a deferred chunk: the main stream still joins it
+                    N.check(N.load_library().uttt_stream_wait_event(main.cuda_stream, pending),
+                            "uttt_stream_wait_event")
             per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
             caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win
                       else (kb, vb) for kb, vb in zip(k_bufs, v_bufs)]
@@ -356,6 +383,7 @@ class uTTTModel(nn.Module):
                 run.launch(run.n_layers, timer=kernel_timer)
             main.wait_stream(side)
             pieces.append(hid)
+            yield ci
         per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
         caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win else (kb, vb)
                   for kb, vb in zip(k_bufs, v_bufs)]

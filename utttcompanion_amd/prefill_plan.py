@@ -140,6 +140,14 @@ class PrefillPlan:
         chain_alt.eta[0], chain_alt.alpha[0] = eta0.data_ptr(), alpha0.data_ptr()
         self.calls, self._keep = (calls, calls_alt), keep
         self._chain_args = (chain.args, chain_alt)
+        # the events that order the two streams belong to the plan (no state in the library): two
+        # per layer, the forward's end and the state write, created on this device, destroyed
+        # with the plan
+        self._lib = lib
+        self._n_events = 2 * n_layers + 2
+        self._events = (C.c_void_p * self._n_events)()
+        with torch.cuda.device(dev):
+            N.check(lib.uttt_events_create(self._n_events, self._events), "uttt_events_create")
         self.args = []
         for cl, ch in zip(self.calls, self._chain_args):
             args = N.PrefillChunkArgs()
@@ -147,17 +155,37 @@ class PrefillPlan:
             args.layers = C.cast(cl, C.POINTER(N.PrefillLayerCalls))
             args.chain = C.pointer(ch)
             args.chain_workspace, args.chain_workspace_bytes = chain.workspace.data_ptr(), chain.workspace.numel()
+            args.events, args.n_events = C.cast(self._events, C.POINTER(C.c_void_p)), self._n_events
             self.args.append(args)
         self._next = 0  # which buffer set the next chunk uses
 
+    @property
+    def state_write_event(self) -> int:
+        """Handle of the event the state write of this plan's calls records (what a deferred
+        call hands to the next one)."""
+        return int(self._events[self._n_events - 1])
+
+    def __del__(self) -> None:
+        events = getattr(self, "_events", None)
+        if events is not None and getattr(self, "_lib", None) is not None:
+            # an event whose recorded work is still running is released when that work ends
+            self._lib.uttt_events_destroy(self._n_events, events)
+            self._events = None
+
     def run(self, h: Tensor, off: int, start_pos: int, kv_offset: int, mask: Optional[Tensor],
-            surprise: Tensor, main: "torch.cuda.Stream", side: "torch.cuda.Stream", defer_join: bool = False) -> None:
+            surprise: Tensor, main: "torch.cuda.Stream", side: "torch.cuda.Stream", defer_join: bool = False,
+            wait_event: Optional[int] = None) -> Optional[int]:
         """One chunk: rows ``off .. off + tokens`` of ``h`` (B, T, D) are updated in place through
         every layer, and the chain writes the state; ``mask`` is the fp32 (B, T) token mask (or
         None) and ``surprise`` this chunk's (layers,) row.  ``defer_join``: ``main`` does not wait
-        for the state write; the next executor call on the device does, before its layer-0
-        readout (consecutive chunks of a plan alternate layer 0's buffers for that).  The last
-        chunk of a prefill passes False."""
+        for the state write; the call returns the state write's event handle, which the caller
+        passes as ``wait_event`` to its next call (of this plan or another plan of the same
+        prefill), whose ``main`` waits for it before its layer-0 readout (consecutive chunks of a
+        plan alternate layer 0's buffers for that).  The last chunk of a prefill passes False.
+        Neither is allowed under graph capture (``ValueError``)."""
+        if (defer_join or wait_event is not None) and torch.cuda.is_current_stream_capturing():
+            raise ValueError("a deferred join cannot be part of a graph capture: every captured chunk joins its "
+                             "own state write")
         end = off + self.tokens
         # the executor sets these per chunk where the wrappers checked them per call
         if not (0 <= kv_offset and kv_offset + self.tokens <= self.kv_capacity and 0 <= start_pos
@@ -171,6 +199,7 @@ class PrefillPlan:
         a = self.args[self._next]
         self._next ^= 1
         a.start_pos, a.kv_offset, a.defer_join = int(start_pos), int(kv_offset), int(bool(defer_join))
+        a.wait_event = wait_event
         if mask is not None:
             a.token_mask, a.mask_row_stride = mask.data_ptr() + off * mask.element_size(), mask.stride(0)
         else:
@@ -179,3 +208,4 @@ class PrefillPlan:
         lib = N.load_library()
         N.check(lib.uttt_prefill_chunk(C.byref(a), main.cuda_stream, side.cuda_stream), "uttt_prefill_chunk")
         h[:, off:end].copy_(self.hid)
+        return self.state_write_event if defer_join else None
