@@ -281,8 +281,8 @@ def sliding_window_attention(q: Tensor, k: Tensor, v: Tensor, window: int, q_off
     cdt = _math_dtype(q.dtype)
     kk = k.to(cdt).repeat_interleave(rep, dim=1)
     vv = v.to(cdt).repeat_interleave(rep, dim=1)
-    qi = torch.arange(tq).view(-1, 1) + q_offset
-    kj = torch.arange(k.shape[2]).view(1, -1)
+    qi = torch.arange(tq, device=q.device).view(-1, 1) + q_offset
+    kj = torch.arange(k.shape[2], device=q.device).view(1, -1)
     visible = (qi >= kj) & ((qi - kj) < window)
     scores = torch.matmul(q.to(cdt), kk.transpose(-1, -2)) * (1.0 / math.sqrt(hd))
     scores = scores.masked_fill(~visible, float("-inf"))

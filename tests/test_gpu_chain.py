@@ -343,3 +343,40 @@ def test_single_launches_with_timer_equal_whole_stages():
         N.check(N.load_library().uttt_chunk_chain_stage_launch(C.byref(run_b.args), run_b.workspace.data_ptr(),
                                                                  run_b.workspace.numel(), 4, 0, 1, 3, None, 0, None,
                                                                  None), "stage launch")
+
+
+DEEP_CASES = [
+    dict(b=2, d=1024, f=1536, mask=False),  # one snapshot-product launch per layer
+    dict(b=2, d=2048, f=5504, mask=True),   # config-3 dims: 180 MB per product launch, grouped layers
+]
+
+
+@pytest.mark.parametrize("case", DEEP_CASES, ids=[f"d{c['d']}-f{c['f']}" for c in DEEP_CASES])
+def test_chain_bf16_24_layers_against_both_oracles(case):
+    """The depth of configs 3 and 5: a 24-layer bf16 chain reading bf16 copies of the chunk-start
+    state (the prefill's form), against 24 sequential oracle steps in fp32 (host CPU) and in the
+    reference's bf16 arithmetic (oracle16: bf16 keys, values, eta, alpha and bf16 matmuls with the
+    fp32 masters; run by torch on the GPU).  Bound: 2e-2 max-abs for the fp32 state against
+    either, the surprise within 2e-2 of each (relative above 1)."""
+    b, d, f = case["b"], case["d"], case["f"]
+    print(f"24-layer bf16 chain, B {b}, D {d}, F {f}", flush=True)
+    layers, w, s, ln_w, ln_b = make_layers(24, b, 64, d, f, seed=240 + d, w_scale=0.02)
+    mask = None
+    if case["mask"]:
+        mask = torch.ones(b, 64)
+        mask[1, 40:] = 0
+    ref, ref_s = oracle_chain(layers, w, s, ln_w, ln_b, mask, 0.9, 1.0, True)
+    l16 = [tuple(x.to(DEV, torch.bfloat16) for x in layer) for layer in layers]
+    with torch.no_grad():
+        ref16, ref16_s = oracle_chain(l16, tuple(t.to(DEV) for t in w), tuple(t.to(DEV) for t in s), ln_w.to(DEV),
+                                      ln_b.to(DEV), None if mask is None else mask.to(DEV), 0.9, 1.0, True)
+    got, got_s, cps, _ = run_chain(layers, w, s, ln_w, ln_b, mask, 0.9, 1.0, True, torch.bfloat16, copies=True)
+    for name, a, e, e16 in zip(NAMES, got, ref, ref16):
+        assert torch.isfinite(a).all(), name
+        err, err16 = (a.cpu() - e).abs().max().item(), (a - e16).abs().max().item()
+        print(f"  {name}: vs fp32 {err:.3e}, vs reference bf16 {err16:.3e}", flush=True)
+        assert err <= 2e-2 and err16 <= 2e-2, name
+    for ref_sur in (ref_s, ref16_s.float().cpu()):
+        assert (got_s.cpu() - ref_sur).abs().max().item() <= 2e-2 * max(1.0, ref_sur.abs().max().item())
+    for cp, st in zip(cps, got):
+        assert torch.equal(cp, st.to(torch.bfloat16))

@@ -75,7 +75,9 @@ def build(cfg_kw=SMALL, seed=5, dtype=torch.float32):
     model = model.to(DEV)
     if dtype != torch.float32:
         model.to(dtype)
-        model.fast_weight_pool.float()
+        model.fast_weight_pool.float()  # fp32 masters: reload the pool the cast has rounded
+        pre = "fast_weight_pool."
+        model.fast_weight_pool.load_state_dict({k[len(pre):]: v for k, v in sd.items() if k.startswith(pre)})
     ocfg = om.OracleConfig(**{k: cfg_kw[k] for k in ("d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff_fast",
                                                      "sliding_window_size", "vocab_size", "chunk_size",
                                                      "base_inner_lr", "base_weight_decay")})
@@ -117,7 +119,9 @@ def test_model_forward_with_writes_bf16_within_tolerance():
     weights = {k: v.detach().clone() for k, v in model.state_dict().items()}
     rounded = {k: (v if k.startswith("fast_weight_pool.") else v.bfloat16().float()) for k, v in weights.items()}
     model = model.to(DEV).to(torch.bfloat16)
-    model.fast_weight_pool.float()
+    model.fast_weight_pool.float()  # fp32 masters: reload the pool the cast has rounded
+    pre = "fast_weight_pool."
+    model.fast_weight_pool.load_state_dict({k[len(pre):]: v for k, v in weights.items() if k.startswith(pre)})
     ocfg = om.OracleConfig(**{k: cfg_kw[k] for k in ("d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff_fast",
                                                      "sliding_window_size", "vocab_size", "chunk_size",
                                                      "base_inner_lr", "base_weight_decay")})
