@@ -14,10 +14,13 @@ the layer chain (``uttt_chunk_chain`` stages) that applies the chunk's chained f
 updates on a second stream, one layer behind.
 
 Also reported:
-* ``roofline``: the chain kernel with the largest total time in the timed prefills, timed live
-  with HIP events around each of its launches (on the chain's stream), against its algorithmic
-  bytes per launch (it streams bf16 copies of the state: HBM-bound), with the HBM traffic
-  rocprofv3 measured for it when a summary is committed under profiles/;
+* ``roofline``: the whole config-3 prefill's algorithmic flops over its timed duration against
+  the bf16 MFMA peak (the north star's axis for the update + prefill), its state-byte fractions
+  of the HBM peak, and the HBM traffic per prefill rocprofv3 measured when a summary is committed
+  under profiles/; beside it, ``dominant_kernel``: the chain kernel with the largest total time in
+  a calibration prefill (every chain launch bracketed by HIP events on the chain's stream),
+  against its algorithmic bytes per launch (it streams bf16 copies of the state: HBM-bound), in
+  the prefill and timed alone;
 * ``prefill``: the whole prefill's algorithmic work against the bf16 MFMA peak and its minimum
   state bytes against the HBM peak, and the timed chain kernels;
 * ``config1_block``: BASELINE config 1 (one fp32 uTTT block, B 1 x T 1024, 16 chunk updates)
@@ -75,6 +78,20 @@ def measured_traffic(kernel: str, config: str = "c2"):
     return None
 
 
+def measured_prefill_traffic(config: str = "c3"):
+    """HBM bytes per prefill from the committed rocprofv3 summary
+    ``profiles/prefill_<config>_traffic.md`` (its ``traffic_bytes_per_prefill:`` line), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"prefill_{config}_traffic.md")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_prefill:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -88,7 +105,7 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timings")
     ap.add_argument("--sections", default="c3,c1,prefill,update,chain,decode,evolve,cpu",
                     help="comma list of c3 (the headline), c1, prefill (config 2), update, chain, decode, "
-                         "evolve, cpu, copyref, c3kern (profiling runs pick a subset)")
+                         "evolve, cpu, copyref, c3kern, c3once (profiling runs pick a subset)")
     ap.add_argument("--c2-steps", type=int, default=5, help="timed config-2 prefills")
     ap.add_argument("--evolve-steps", type=int, default=2, help="timed config-5 updates")
     ap.add_argument("--cpu-tokens", type=int, default=256, help="tokens of the config-3 CPU baseline sample")
@@ -776,9 +793,18 @@ def main() -> int:
 
     # ---------------- headline: config 3 prefill with writes
     line_value, c3_ms, finite, roofline, prefill, cpu, big = float("nan"), float("nan"), False, None, None, None, {}
-    if sections & {"c3", "c3kern", "evolve"}:
+    if sections & {"c3", "c3kern", "c3once", "evolve"}:
         log("building the config-3 model on the GPU")
         model3 = build_c3_model()
+        if "c3once" in sections:  # profiling runs: prefills only (no calibration, no isolated kernel)
+            g = torch.Generator().manual_seed(6)
+            ids = torch.randint(0, C3["vocab_size"], (C3_BATCH, C3_SEQ), generator=g).to("cuda")
+            state = model3.init_fast_state(C3_BATCH, device="cuda", dtype=torch.float32, detach=True)
+            with torch.no_grad():
+                for i in range(args.steps):
+                    model3.prefill_with_writes(ids, state)
+                    torch.cuda.synchronize()
+                    log(f"config 3: prefill {i + 1}/{args.steps} done")
         if "c3kern" in sections:  # profiling runs: the isolated kernel timing alone
             us, per_replay = bench_chain_kernel(args.kernel)
             log(f"{args.kernel} at the config-3 chunk shape: {us:.2f} us per launch ({per_replay} per replay)")
@@ -803,16 +829,35 @@ def main() -> int:
                                              "(stages enqueued launch by launch, so slower than the timed prefills)"}
             nbytes_dom = CHAIN_STATE_BYTES[dom] * D * F * C3_BATCH
             gbs = nbytes_dom / (us * 1e-6) / 1e9
-            roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(dom, "c3"),
-                        "kernel": dom,
-                        "per_launch": {"algorithmic_bytes": nbytes_dom, "avg_us": round(us, 2),
-                                       "timing": f"{per_replay} launches (one per layer) at the config-3 chunk shape "
-                                                 f"in a HIP graph, replayed 5 times, HIP events around the replays",
-                                       "in_prefill_avg_us": table[dom]["mean_us"],
-                                       "unit_bytes": CHAIN_STATE_WHAT[dom],
-                                       "shape": {"B": C3_BATCH, "D": D, "F": F, "L": C3["n_layers"]}}}
-            log(f"config 3 dominant streaming chain kernel {dom}: {us:.1f} us -> {gbs:.0f} GB/s")
+            in_us = table[dom]["mean_us"]
+            in_gbs = nbytes_dom / (in_us * 1e-6) / 1e9
+            tfs = flops["total"] / sec / 1e12
+            # the headline's roofline is the whole prefill's: its algorithmic flops against the
+            # bf16 MFMA peak (the north star's axis; the state-byte fractions beside it); the
+            # dominant streaming kernel is reported separately, in the prefill and alone
+            roofline = {"bound": "mfma", "achieved": round(tfs, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tfs / PEAK_BF16_TFLOPS, 4), "traffic": measured_prefill_traffic("c3"),
+                        "scope": "one whole config-3 prefill with writes: algorithmic flops (update + readout "
+                                 "20 D F per token and layer, window attention, slow projections) over the timed "
+                                 "prefill's time; traffic = HBM bytes per prefill (rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                                 "over the library's kernels of one prefill) or null",
+                        "hbm_frac_min_state_bytes": prefill["hbm_frac_min_state_bytes"],
+                        "hbm_frac_design_bytes": prefill["hbm_frac_design_bytes"],
+                        "dominant_kernel": {
+                            "kernel": dom, "unit_bytes": CHAIN_STATE_WHAT[dom], "algorithmic_bytes": nbytes_dom,
+                            "shape": {"B": C3_BATCH, "D": D, "F": F, "L": C3["n_layers"]},
+                            "in_prefill": {"avg_us": in_us, "gbs": round(in_gbs, 1),
+                                           "hbm_frac": round(in_gbs / PEAK_HBM_GBS, 4),
+                                           "timing": "calibration prefill, HIP events around each launch"},
+                            "isolated": {"avg_us": round(us, 2), "gbs": round(gbs, 1),
+                                         "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+                                         "timing": f"{per_replay} launches (one per layer) at the config-3 chunk "
+                                                   f"shape in a HIP graph, replayed 5 times, HIP events around the "
+                                                   f"replays"},
+                            "traffic": measured_traffic(dom, "c3")}}
+            log(f"config 3: {tfs:.1f} TFLOP/s of algorithmic work ({tfs / PEAK_BF16_TFLOPS:.3f} of bf16 peak); "
+                f"dominant streaming chain kernel {dom}: {in_us:.1f} us in the prefill, {us:.1f} us alone -> "
+                f"{gbs:.0f} GB/s")
             if run_cpu:
                 log("timing the CPU oracle on a config-3 sample")
                 cpu = cpu_baseline_c3(model3, args.cpu_tokens)
