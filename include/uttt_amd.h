@@ -32,7 +32,7 @@ enum { UTTT_OK = 0, UTTT_ERR_INVALID = 1, UTTT_ERR_HIP = 2, UTTT_ERR_WORKSPACE =
 
 /* ABI version of the structures and entry points below: uttt_abi_version() returns it, and the
  * Python binding reads it from this header and refuses a library built from another one. */
-#define UTTT_ABI_VERSION 22
+#define UTTT_ABI_VERSION 23
 
 /* Text of the last error on this host thread ("" when none). */
 const char* uttt_last_error(void);
@@ -48,7 +48,9 @@ int uttt_abi_version(void);
  * ------------------------------------------------------------------------- */
 typedef struct {
   int64_t batch;      /* B rows */
-  int64_t tokens;     /* C tokens in this chunk, 1..64 */
+  int64_t tokens;     /* C tokens in this chunk, 1..UTTT_MAX_UPDATE_TOKENS (one write for the whole
+                         chunk; chunks longer than 64 run the 64-token kernels per block and a
+                         separate pass for the chunk's clip norm) */
   int64_t d_model;    /* D, multiple of 64 */
   int64_t d_ff;       /* F, multiple of 64 */
   int32_t act_dtype;  /* UTTT_DTYPE_F32 or UTTT_DTYPE_BF16: q/k/v/eta/alpha/out */
@@ -80,12 +82,18 @@ typedef struct {
 } uttt_chunk_update_args;
 
 size_t uttt_chunk_update_workspace(int64_t batch, int64_t d_model, int64_t d_ff, int32_t act_dtype);
+/* The same for chunks of up to `tokens` tokens (the reference's configs write 128- and 512-token
+ * chunks: configs/5090_config.yaml:31, configs/5090_pretrain_20261029.yaml:28); 0 if invalid. */
+#define UTTT_MAX_UPDATE_TOKENS 512
+size_t uttt_chunk_update_workspace_tokens(int64_t batch, int64_t tokens, int64_t d_model, int64_t d_ff,
+                                          int32_t act_dtype);
 int uttt_chunk_update(const uttt_chunk_update_args* args, void* workspace, size_t workspace_bytes,
                       uttt_stream_t stream);
 
 /* The same update as UTTT_UPDATE_PHASES stream-ordered launches, one per call, in order
  * 0..4 on one stream with one workspace: 0 U/G/H (both paths), 1 Z partial sums,
- * 2 LayerNorm + loss + dZ + readout, 3 dH/dU/dG + gradient-norm partials, 4 clip/momentum/
+ * 2 LayerNorm + loss + dZ + readout, 3 dH/dU/dG + gradient-norm partials (for a chunk of more
+ * than 64 tokens, a second launch forms them from every token block), 4 clip/momentum/
  * decay/select applied to W and S.  Running all five equals uttt_chunk_update; it exists
  * so a caller can place timing events (or other stream work) between the phases. */
 #define UTTT_UPDATE_PHASES 5
@@ -97,7 +105,7 @@ int uttt_chunk_update_phase(const uttt_chunk_update_args* args, void* workspace,
  * capture, tight serving loops, harnesses that forbid hipMalloc).  The workspace is a
  * device-resident array of UTTT_NOALLOC_SCRATCH_BYTES inside the library (each GPU the library
  * runs on holds its own copy until the process ends); shapes whose workspace
- * (uttt_chunk_update_workspace) exceeds it are refused with UTTT_ERR_INVALID.  The stream's device
+ * (uttt_chunk_update_workspace_tokens) exceeds it are refused with UTTT_ERR_INVALID.  The stream's device
  * must be the current device.  Every call on one GPU uses that GPU's array, so calls that overlap
  * on one GPU (other streams, other host threads) race: order them.  Results equal
  * uttt_chunk_update's. */

@@ -7,8 +7,9 @@ reference's serving code uses, and argument refusals that happen before any devi
   tensors are refused.
 * ``SlidingWindowAttention.prepare_for_inference`` / ``_packed_qkv`` (:1002-1024) and
   ``uTTTModel.prepare_for_inference`` (reference uttt_model.py:401-422).
-* Writes with chunk_size > 64 are refused at the write entry points (construction and frozen
-  reads stay valid: the reference's shipped configs use chunk_size 128 / 512).
+* Writes take chunks of up to 512 tokens (the reference's shipped configs use chunk_size 128 /
+  512); longer ones are refused at the write entry points (construction and frozen reads stay
+  valid).
 """
 import pytest
 import torch
@@ -107,8 +108,18 @@ def test_model_prepare_for_inference():
     assert set(model.state_dict()) == set(uTTTModel(uTTTConfig(**TINY)).state_dict())
 
 
-@pytest.mark.parametrize("chunk", [128, 512])
-def test_writes_with_long_chunks_are_refused_before_any_work(chunk):
+def test_write_chunk_limit_takes_the_reference_configs():
+    from utttcompanion_amd.layer import MAX_WRITE_CHUNK, require_write_chunk
+    assert MAX_WRITE_CHUNK == 512
+    for chunk in (1, 64, 128, 512):  # 128 / 512: configs/5090_config.yaml:31, 5090_pretrain_20261029.yaml:28
+        require_write_chunk(chunk)
+    for chunk in (0, 513, 1024):
+        with pytest.raises(ValueError, match=f"chunk_size={chunk}"):
+            require_write_chunk(chunk)
+
+
+@pytest.mark.parametrize("chunk", [513, 1024])
+def test_writes_with_longer_chunks_are_refused_before_any_work(chunk):
     from utttcompanion_amd.evolve import ragged_test_time_update
     model = uTTTModel(uTTTConfig(**dict(TINY, chunk_size=chunk))).eval()  # constructs: frozen reads are valid
     ids = torch.randint(6, 64, (1, 40))

@@ -24,6 +24,7 @@ def _header_abi_version(path: str = HEADER_PATH) -> int:
 
 ABI_VERSION = _header_abi_version()
 MAX_CHAIN = 64
+MAX_UPDATE_TOKENS = 512  # UTTT_MAX_UPDATE_TOKENS: longest chunk one uttt_chunk_update writes
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 UPDATE_PHASES = 5
@@ -225,6 +226,7 @@ SIGNATURES = {
     "uttt_last_error": (C.c_char_p, []),
     "uttt_abi_version": (C.c_int, []),
     "uttt_chunk_update_workspace": (C.c_size_t, [_I64, _I64, _I64, _I32]),
+    "uttt_chunk_update_workspace_tokens": (C.c_size_t, [_I64, _I64, _I64, _I64, _I32]),
     "uttt_chunk_update": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _P]),
     "uttt_chunk_update_phase": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P, C.c_size_t, _I32, _P]),
     "uttt_chunk_update_noalloc": (C.c_int, [C.POINTER(ChunkUpdateArgs), _P]),

@@ -498,16 +498,16 @@ static void launch_ln_readout(dim3 grid, hipStream_t st, const LnOutArgs& o) {
 // 5. dH = dZ W_down^T per F tile; dU, dG; squared-norm partial of all three gradients
 // ---------------------------------------------------------------------------
 struct BwdArgs {
-  int B, C, D, F;
+  int B, C, D, F, ntb, tok_pad;  // ntb token blocks of 64, tok_pad = 64 ntb
   const void* k; int64_t k_rs;
   const float* wd; int64_t w_rs;
   const float* u_store;
   const float* g_store;
-  const void* h;   // K-path H (B, 64, F)
-  const void* dz;  // (B, 64, D)
-  void* du;        // (B, 64, F)
+  const void* h;   // K-path H (B, tok_pad, F)
+  const void* dz;  // (B, tok_pad, D)
+  void* du;        // (B, tok_pad, F)
   void* dg;
-  float* nrm;      // (B, F/64)
+  float* nrm;      // (B, F/64), one token block only (longer chunks: k_apply<.., true>)
 };
 
 template <typename T>
@@ -519,13 +519,13 @@ __global__ void __launch_bounds__(kThreads) k_backward(const BwdArgs a) {
   __shared__ __align__(16) T dus[64 * LD];   // dU^T [f][t]
   __shared__ __align__(16) T dgs[64 * LD];   // dG^T [f][t]
   __shared__ float red[4];
-  const int ft = blockIdx.x, b = blockIdx.y;
+  const int ft = blockIdx.x, b = blockIdx.y, t0 = blockIdx.z * 64;  // token block blockIdx.z
   const int f0 = ft * 64;
   const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
-  const T* dz = static_cast<const T*>(a.dz) + (int64_t)b * 64 * a.D;
+  const T* dz = static_cast<const T*>(a.dz) + ((int64_t)b * a.tok_pad + t0) * a.D;
   const float* wd = a.wd + (int64_t)b * a.w_rs + (int64_t)f0 * a.D;
   const T* kr = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs;
-  const int64_t rowbase = (int64_t)b * 64 * a.F + f0;
+  const int64_t rowbase = ((int64_t)b * a.tok_pad + t0) * a.F + f0;
 
   // dH tile [t][f] over the full D (A = dZ rows, B^T = W_down rows)
   {
@@ -562,6 +562,9 @@ __global__ void __launch_bounds__(kThreads) k_backward(const BwdArgs a) {
       dgs[f * LD + t] = dg;
     }
   }
+  // with several token blocks the gradient norm needs every block's products: a later launch
+  // (k_apply<T, true>) forms it from the whole chunk
+  if (a.ntb > 1) return;
   // H^T for this F tile
   {
     ColStage<T, 64> hst;
@@ -603,7 +606,8 @@ __global__ void __launch_bounds__(kThreads) k_backward(const BwdArgs a) {
 //    S' = beta S - c g, W' = (1 - alpha_bar) W + S', inactive rows copied through.
 // ---------------------------------------------------------------------------
 struct ApplyArgs {
-  int B, C, D, F;
+  int B, C, D, F, ntb, tok_pad;  // ntb token blocks of 64, tok_pad = 64 ntb
+  int n_norm;                     // squared-norm partials per row in nrm
   float beta, max_norm;
   const void* k; int64_t k_rs;
   const void* alpha; int64_t alpha_rs;
@@ -612,7 +616,7 @@ struct ApplyArgs {
   const void* dz;
   const void* du;
   const void* dg;
-  const float* nrm;
+  float* nrm;  // read by the apply; written (one partial per tile) by the norm-only form
   const float* loss;
   const float* w[3];
   const float* s[3];
@@ -623,67 +627,14 @@ struct ApplyArgs {
   float min_row_surprise;  // > 0: rows whose chunk surprise is below it keep W and S
 };
 
+// The last wave of an apply workgroup derives its row's clip factor, decay and active flag (and,
+// in the first workgroups, the row's loss sums and the batch-global surprise).
 template <typename T>
-__global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
-  constexpr int LD = lds_ld<T>();
-  __shared__ __align__(16) T as[64 * LD];
-  __shared__ __align__(16) T bs[64 * LD];
-  __shared__ float row_scalar[3];
-  const int nD = a.D / 64, nF = a.F / 64;
-  const int per = nD * nF;
-  const int m = blockIdx.x / per, j = blockIdx.x - m * per, b = blockIdx.y;
-  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
-
-  int r0, c0, ld_out;
-  const T *asrc, *bsrc;
-  int64_t a_ld, b_ld;
-  int a_valid;
-  if (m < 2) {  // W_up / W_gate tile (d, f) = K^T dU / K^T dG
-    const int dt = j / nF, ft = j - dt * nF;
-    r0 = dt * 64;
-    c0 = ft * 64;
-    ld_out = a.F;
-    asrc = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs + r0;
-    a_ld = a.D;
-    a_valid = a.C;
-    bsrc = static_cast<const T*>(m == 0 ? a.du : a.dg) + (int64_t)b * 64 * a.F + c0;
-    b_ld = a.F;
-  } else {      // W_down tile (f, d) = H^T dZ
-    const int ft = j / nD, dt = j - ft * nD;
-    r0 = ft * 64;
-    c0 = dt * 64;
-    ld_out = a.D;
-    asrc = static_cast<const T*>(a.h) + (int64_t)b * 64 * a.F + r0;
-    a_ld = a.F;
-    a_valid = 64;
-    bsrc = static_cast<const T*>(a.dz) + (int64_t)b * 64 * a.D + c0;
-    b_ld = a.D;
-  }
-  // the state tile is the bulk of the traffic: issue its loads first
-  const int64_t mat = (int64_t)a.D * a.F;
-  const float* wsrc = a.w[m] + b * mat;
-  const float* ssrc = a.s[m] + b * mat;
-  const int col = c0 + wc + acc_col();
-  float wv[16], sv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
-    wv[i] = wsrc[off];
-    sv[i] = ssrc[off];
-  }
-  constexpr int kUnits = ColStage<T, 64>::kUnits;
+__device__ __forceinline__ void apply_row_scalars(const ApplyArgs& a, int b, float* row_scalar) {
   {
-    ColStage<T, 64> cst;
-    const bool a_part = threadIdx.x < kUnits;
-    const int unit = a_part ? threadIdx.x : threadIdx.x - kUnits;
-    cst.load(a_part ? asrc : bsrc, a_part ? a_ld : b_ld, a_part ? a_valid : 64, unit < kUnits ? unit : kUnits);
-    cst.template store<T>(a_part ? as : bs, LD);
-  }
-
-  if (threadIdx.x >= 192) {  // the last wave derives this row's clip / decay / active flag
     const int lane = threadIdx.x - 192;
     float n2 = 0.f;
-    for (int i = lane; i < nF; i += 64) n2 += a.nrm[b * nF + i];
+    for (int i = lane; i < a.n_norm; i += 64) n2 += a.nrm[(int64_t)b * a.n_norm + i];
     n2 = wave_sum(n2);
     float asum = 0.f, msum = 0.f, any = 0.f;
     const T* al = static_cast<const T*>(a.alpha) + (int64_t)b * a.alpha_rs;
@@ -701,7 +652,9 @@ __global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
     msum = wave_sum(msum);
     any = wave_sum(any);
     // this row's chunk surprise (masked mean token loss), for the optional update gate
-    const float lsum = wave_sum(lane < a.C ? a.loss[b * 64 + lane] : 0.f);
+    float lpart = 0.f;
+    for (int t = lane; t < a.C; t += 64) lpart += a.loss[(int64_t)b * a.tok_pad + t];
+    const float lsum = wave_sum(lpart);
     const float row_mean = lsum / fmaxf(a.mask != nullptr ? msum : (float)a.C, 1.f);
     if (lane == 0) {
       const float abar = a.mask != nullptr ? asum / fmaxf(msum, 1.f) : asum / (float)a.C;
@@ -711,8 +664,11 @@ __global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
       row_scalar[2] = ((a.mask == nullptr || any > 0.f) && !gated_off) ? 1.f : 0.f;
     }
     if (blockIdx.x == 0 && a.row_loss != nullptr) {
-      const float lt = lane < a.C ? a.loss[b * 64 + lane] : 0.f;
-      const float mt = lane < a.C ? (a.mask != nullptr ? a.mask[(int64_t)b * a.mask_rs + lane] : 1.f) : 0.f;
+      float lt = 0.f, mt = 0.f;
+      for (int t = lane; t < a.C; t += 64) {
+        lt += a.loss[(int64_t)b * a.tok_pad + t];
+        mt += a.mask != nullptr ? a.mask[(int64_t)b * a.mask_rs + t] : 1.f;
+      }
       const float sl = wave_sum(lt), sm = wave_sum(mt);
       if (lane == 0) {
         a.row_loss[2 * b] = sl;
@@ -722,8 +678,8 @@ __global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
     if (blockIdx.x == 0 && blockIdx.y == 0) {
       // batch-global surprise: sum of masked token losses over all rows / valid tokens
       float num = 0.f, den = 0.f;
-      for (int i = lane; i < a.B * 64; i += 64) {
-        const int bb = i >> 6, t = i & 63;
+      for (int i = lane; i < a.B * a.tok_pad; i += 64) {
+        const int bb = i / a.tok_pad, t = i - bb * a.tok_pad;
         num += a.loss[i];
         if (t < a.C) den += a.mask != nullptr ? a.mask[(int64_t)bb * a.mask_rs + t] : 1.f;
       }
@@ -732,10 +688,88 @@ __global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
       if (lane == 0) *a.surprise = a.mask != nullptr ? num / fmaxf(den, 1.f) : num / den;
     }
   }
-  __syncthreads();
+}
+
+// NORM: instead of applying, write the tile's squared Frobenius norm to nrm (one partial per tile):
+// the clip norm of a chunk longer than one token block, whose gradient tiles sum over its blocks.
+template <typename T, bool NORM = false>
+__global__ void __launch_bounds__(kThreads) k_apply(const ApplyArgs a) {
+  constexpr int LD = lds_ld<T>();
+  __shared__ __align__(16) T as[64 * LD];
+  __shared__ __align__(16) T bs[64 * LD];
+  __shared__ float row_scalar[3];
+  __shared__ float red[4];
+  const int nD = a.D / 64, nF = a.F / 64;
+  const int per = nD * nF;
+  const int m = blockIdx.x / per, j = blockIdx.x - m * per, b = blockIdx.y;
+  const int w = threadIdx.x >> 6, wr = (w >> 1) * 32, wc = (w & 1) * 32;
+
+  int r0, c0, ld_out;
+  const T *asrc, *bsrc;
+  int64_t a_ld, b_ld;
+  int a_valid;
+  if (m < 2) {  // W_up / W_gate tile (d, f) = K^T dU / K^T dG
+    const int dt = j / nF, ft = j - dt * nF;
+    r0 = dt * 64;
+    c0 = ft * 64;
+    ld_out = a.F;
+    asrc = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs + r0;
+    a_ld = a.D;
+    a_valid = a.C;
+    bsrc = static_cast<const T*>(m == 0 ? a.du : a.dg) + (int64_t)b * a.tok_pad * a.F + c0;
+    b_ld = a.F;
+  } else {      // W_down tile (f, d) = H^T dZ
+    const int ft = j / nD, dt = j - ft * nD;
+    r0 = ft * 64;
+    c0 = dt * 64;
+    ld_out = a.D;
+    asrc = static_cast<const T*>(a.h) + (int64_t)b * a.tok_pad * a.F + r0;
+    a_ld = a.F;
+    a_valid = a.tok_pad;  // rows past the chunk are zero
+    bsrc = static_cast<const T*>(a.dz) + (int64_t)b * a.tok_pad * a.D + c0;
+    b_ld = a.D;
+  }
+  // the state tile is the bulk of the traffic: issue its loads first
+  const int64_t mat = (int64_t)a.D * a.F;
+  const float* wsrc = a.w[m] + b * mat;
+  const float* ssrc = a.s[m] + b * mat;
+  const int col = c0 + wc + acc_col();
+  float wv[16], sv[16];
+  if constexpr (!NORM) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t off = (int64_t)(r0 + wr + acc_row(i)) * ld_out + col;
+      wv[i] = wsrc[off];
+      sv[i] = ssrc[off];
+    }
+  }
+  constexpr int kUnits = ColStage<T, 64>::kUnits;
   f32x16 acc;
   zero(acc);
-  wave_mma<T, 64>(acc, as + wr * LD, LD, bs + wc * LD, LD);
+  // the gradient tile: K = the chunk's tokens, one block of 64 per step
+  for (int tb = 0; tb < a.ntb; ++tb) {
+    const int t0 = tb * 64;
+    if (tb > 0) __syncthreads();  // the previous block's products are done with as / bs
+    {
+      ColStage<T, 64> cst;
+      const bool a_part = threadIdx.x < kUnits;
+      const int unit = a_part ? threadIdx.x : threadIdx.x - kUnits;
+      cst.load(a_part ? asrc + (int64_t)t0 * a_ld : bsrc + (int64_t)t0 * b_ld, a_part ? a_ld : b_ld,
+               a_part ? min(64, a_valid - t0) : 64, unit < kUnits ? unit : kUnits);
+      cst.template store<T>(a_part ? as : bs, LD);
+    }
+    if (!NORM && tb == 0 && threadIdx.x >= 192) apply_row_scalars<T>(a, b, row_scalar);
+    __syncthreads();
+    wave_mma<T, 64>(acc, as + wr * LD, LD, bs + wc * LD, LD);
+  }
+  if constexpr (NORM) {
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sq += acc[i] * acc[i];
+    const float total = block_sum(sq, red);
+    if (threadIdx.x == 0) a.nrm[(int64_t)b * a.n_norm + blockIdx.x] = total;
+    return;
+  }
 
   const float clip = row_scalar[0], decay = row_scalar[1];
   const bool active = row_scalar[2] != 0.f;
@@ -770,25 +804,32 @@ static size_t act_bytes(int32_t dtype) { return dtype == UTTT_DTYPE_BF16 ? 2 : 4
 
 struct UpdateLayout {
   size_t u, g, h0, h1, zp, dz, du, dg, loss, nrm, total;
-  int nsplit;
+  int nsplit, ntb, tok_pad, n_norm;
 };
 
-static UpdateLayout update_layout(int64_t B, int64_t D, int64_t F, int32_t dtype) {
+// Workspace of one update of chunks of up to `tokens` tokens: the activations of ntb blocks of 64
+// tokens; with more than one block, one squared-norm partial per gradient tile (the norm of a
+// tile sums over every block) instead of one per F tile.
+static UpdateLayout update_layout(int64_t B, int64_t tokens, int64_t D, int64_t F, int32_t dtype) {
   UpdateLayout L;
   const size_t e = act_bytes(dtype);
-  L.nsplit = pick_nsplit((D / 64) * B * 2, F / 64);
+  L.ntb = (int)std::max<int64_t>(1, (tokens + 63) / 64);
+  L.tok_pad = 64 * L.ntb;
+  L.n_norm = L.ntb > 1 ? (int)(3 * (D / 64) * (F / 64)) : (int)(F / 64);
+  const size_t TP = (size_t)L.tok_pad;
+  L.nsplit = pick_nsplit((D / 64) * B * 2 * L.ntb, F / 64);
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t at = off; off += align_up(bytes); return at; };
-  L.u = take(sizeof(float) * B * 64 * F);
-  L.g = take(sizeof(float) * B * 64 * F);
-  L.h0 = take(e * B * 64 * F);
-  L.h1 = take(e * B * 64 * F);
-  L.zp = take(sizeof(float) * 2 * L.nsplit * B * 64 * D);
-  L.dz = take(e * B * 64 * D);
-  L.du = take(e * B * 64 * F);
-  L.dg = take(e * B * 64 * F);
-  L.loss = take(sizeof(float) * B * 64);
-  L.nrm = take(sizeof(float) * B * (F / 64));
+  L.u = take(sizeof(float) * B * TP * F);
+  L.g = take(sizeof(float) * B * TP * F);
+  L.h0 = take(e * B * TP * F);
+  L.h1 = take(e * B * TP * F);
+  L.zp = take(sizeof(float) * 2 * L.nsplit * B * TP * D);
+  L.dz = take(e * B * TP * D);
+  L.du = take(e * B * TP * F);
+  L.dg = take(e * B * TP * F);
+  L.loss = take(sizeof(float) * B * TP);
+  L.nrm = take(sizeof(float) * B * L.n_norm);
   L.total = off;
   return L;
 }
@@ -797,8 +838,9 @@ template <typename T>
 static void launch_update(const uttt_chunk_update_args& a, char* ws, const UpdateLayout& L, hipStream_t st,
                           int first_phase, int last_phase) {
   const int B = (int)a.batch, C = (int)a.tokens, D = (int)a.d_model, F = (int)a.d_ff;
+  const int ntb = L.ntb, TP = L.tok_pad;
   FwdArgs f{};
-  f.B = B; f.D = D; f.F = F; f.ntok = C; f.ntb = 1; f.tok_pad = 64; f.nsplit = L.nsplit;
+  f.B = B; f.D = D; f.F = F; f.ntok = C; f.ntb = ntb; f.tok_pad = TP; f.nsplit = L.nsplit;
   f.x[0] = a.k; f.x_rs[0] = a.k_row_stride;
   f.x[1] = a.q; f.x_rs[1] = a.q_row_stride;
   f.wu[0] = a.w_up; f.wg[0] = a.w_gate; f.wd[0] = a.w_down; f.w_rs[0] = (int64_t)D * F;
@@ -811,35 +853,34 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   const dim3 blk(kThreads);
   auto want = [&](int phase) { return first_phase <= phase && phase <= last_phase; };
 
-  if (want(0)) hipLaunchKernelGGL((k_up_gate<T, float>), dim3(F / 64, B, 2), blk, 0, st, f);
-  if (want(1)) hipLaunchKernelGGL((k_down_partial<T, float>), dim3(D / 64, L.nsplit, 2 * B), blk, 0, st, f);
+  if (want(0)) hipLaunchKernelGGL((k_up_gate<T, float>), dim3(F / 64, B, 2 * ntb), blk, 0, st, f);
+  if (want(1)) hipLaunchKernelGGL((k_down_partial<T, float>), dim3(D / 64, L.nsplit, 2 * ntb * B), blk, 0, st, f);
 
   LnGradArgs g{};
-  g.B = B; g.C = C; g.D = D; g.nsplit = L.nsplit; g.tok_pad = 64; g.normalize = a.normalize_by_dim;
+  g.B = B; g.C = C; g.D = D; g.nsplit = L.nsplit; g.tok_pad = TP; g.normalize = a.normalize_by_dim;
   g.eps = a.eps; g.zp = f.zp;
   g.k = a.k; g.k_rs = a.k_row_stride; g.v = a.v; g.v_rs = a.v_row_stride;
   g.eta = a.eta; g.eta_rs = a.eta_row_stride; g.mask = a.token_mask; g.mask_rs = a.mask_row_stride;
   g.ln_w = a.ln_weight; g.ln_b = a.ln_bias;
   g.dz = ws + L.dz; g.loss = reinterpret_cast<float*>(ws + L.loss);
   LnOutArgs o{};
-  o.B = B; o.ntok = C; o.D = D; o.nsplit = L.nsplit; o.tok_pad = 64; o.eps = a.eps;
-  o.zp = f.zp + (size_t)L.nsplit * B * 64 * D;
+  o.B = B; o.ntok = C; o.D = D; o.nsplit = L.nsplit; o.tok_pad = TP; o.eps = a.eps;
+  o.zp = f.zp + (size_t)L.nsplit * B * TP * D;
   o.x = a.q; o.x_rs = a.q_row_stride; o.ln_w = a.ln_weight; o.ln_b = a.ln_bias;
   o.out = a.out; o.out_rs = a.out_row_stride;
   if (want(2)) {
-    launch_ln_grad<T>(dim3(64, B), st, g);
+    launch_ln_grad<T>(dim3(TP, B), st, g);
     launch_ln_readout<T>(dim3(C, B), st, o);
   }
 
   BwdArgs bw{};
-  bw.B = B; bw.C = C; bw.D = D; bw.F = F;
+  bw.B = B; bw.C = C; bw.D = D; bw.F = F; bw.ntb = ntb; bw.tok_pad = TP;
   bw.k = a.k; bw.k_rs = a.k_row_stride; bw.wd = a.w_down; bw.w_rs = (int64_t)D * F;
   bw.u_store = f.u_store; bw.g_store = f.g_store; bw.h = f.h[0]; bw.dz = g.dz;
   bw.du = ws + L.du; bw.dg = ws + L.dg; bw.nrm = reinterpret_cast<float*>(ws + L.nrm);
-  if (want(3)) hipLaunchKernelGGL(k_backward<T>, dim3(F / 64, B), blk, 0, st, bw);
-
   ApplyArgs ap{};
-  ap.B = B; ap.C = C; ap.D = D; ap.F = F; ap.beta = a.momentum_beta; ap.max_norm = a.max_inner_grad_norm;
+  ap.B = B; ap.C = C; ap.D = D; ap.F = F; ap.ntb = ntb; ap.tok_pad = TP; ap.n_norm = L.n_norm;
+  ap.beta = a.momentum_beta; ap.max_norm = a.max_inner_grad_norm;
   ap.k = a.k; ap.k_rs = a.k_row_stride; ap.alpha = a.alpha; ap.alpha_rs = a.alpha_row_stride;
   ap.mask = a.token_mask; ap.mask_rs = a.mask_row_stride;
   ap.h = f.h[0]; ap.dz = g.dz; ap.du = bw.du; ap.dg = bw.dg; ap.nrm = bw.nrm; ap.loss = g.loss;
@@ -850,7 +891,13 @@ static void launch_update(const uttt_chunk_update_args& a, char* ws, const Updat
   ap.surprise = a.surprise;
   ap.row_loss = a.row_loss;
   ap.min_row_surprise = a.min_row_surprise;
-  if (want(4)) hipLaunchKernelGGL(k_apply<T>, dim3(3 * (D / 64) * (F / 64), B), blk, 0, st, ap);
+  const dim3 tiles(3 * (D / 64) * (F / 64), B);
+  if (want(3)) {
+    hipLaunchKernelGGL(k_backward<T>, dim3(F / 64, B, ntb), blk, 0, st, bw);
+    // a chunk of several token blocks: each gradient tile's squared norm over the whole chunk
+    if (ntb > 1) hipLaunchKernelGGL((k_apply<T, true>), tiles, blk, 0, st, ap);
+  }
+  if (want(4)) hipLaunchKernelGGL((k_apply<T, false>), tiles, blk, 0, st, ap);
 }
 
 void launch_saved_readout(int B, int ntok, int D, int F, int nsplit, const float* h, const float* w_down,
@@ -1166,7 +1213,14 @@ using namespace uttt;
 
 extern "C" size_t uttt_chunk_update_workspace(int64_t batch, int64_t d_model, int64_t d_ff, int32_t act_dtype) {
   if (check_dims(batch, d_model, d_ff, act_dtype) != UTTT_OK) return 0;
-  return update_layout(batch, d_model, d_ff, act_dtype).total;
+  return update_layout(batch, 64, d_model, d_ff, act_dtype).total;
+}
+
+extern "C" size_t uttt_chunk_update_workspace_tokens(int64_t batch, int64_t tokens, int64_t d_model, int64_t d_ff,
+                                                     int32_t act_dtype) {
+  if (check_dims(batch, d_model, d_ff, act_dtype) != UTTT_OK || tokens < 1 || tokens > UTTT_MAX_UPDATE_TOKENS)
+    return 0;
+  return update_layout(batch, tokens, d_model, d_ff, act_dtype).total;
 }
 
 static int validate_update(const uttt_chunk_update_args* a, void* workspace, size_t workspace_bytes,
@@ -1174,7 +1228,8 @@ static int validate_update(const uttt_chunk_update_args* a, void* workspace, siz
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   int rc = check_dims(a->batch, a->d_model, a->d_ff, a->act_dtype);
   if (rc != UTTT_OK) return rc;
-  UTTT_REQUIRE(a->tokens >= 1 && a->tokens <= 64, "tokens per chunk must be in [1, 64] (got %lld)", (long long)a->tokens);
+  UTTT_REQUIRE(a->tokens >= 1 && a->tokens <= UTTT_MAX_UPDATE_TOKENS, "tokens per chunk must be in [1, %d] (got %lld)",
+               UTTT_MAX_UPDATE_TOKENS, (long long)a->tokens);
   UTTT_REQUIRE(a->q && a->k && a->v && a->eta && a->alpha, "q/k/v/eta/alpha must be non-NULL");
   UTTT_REQUIRE(a->w_up && a->w_gate && a->w_down && a->s_up && a->s_gate && a->s_down, "state pointers must be non-NULL");
   UTTT_REQUIRE(a->r_up && a->r_gate && a->r_down, "read-state pointers must be non-NULL");
@@ -1191,7 +1246,7 @@ static int validate_update(const uttt_chunk_update_args* a, void* workspace, siz
                "activation and state pointers must be 16-byte aligned");
   UTTT_REQUIRE(a->q_row_stride % vec == 0 && a->k_row_stride % vec == 0 && a->v_row_stride % vec == 0,
                "q/k/v row strides must be multiples of 16 bytes");
-  L = update_layout(a->batch, a->d_model, a->d_ff, a->act_dtype);
+  L = update_layout(a->batch, a->tokens, a->d_model, a->d_ff, a->act_dtype);
   UTTT_REQUIRE(workspace != nullptr && workspace_bytes >= L.total,
                "workspace too small: need %zu bytes, got %zu", L.total, workspace_bytes);
   return UTTT_OK;
@@ -1270,7 +1325,9 @@ extern "C" int uttt_chunk_update_noalloc(const uttt_chunk_update_args* a, uttt_s
   UTTT_REQUIRE(a != nullptr, "args is NULL");
   const int rc = check_dims(a->batch, a->d_model, a->d_ff, a->act_dtype);
   if (rc != UTTT_OK) return rc;
-  const size_t need = update_layout(a->batch, a->d_model, a->d_ff, a->act_dtype).total;
+  UTTT_REQUIRE(a->tokens >= 1 && a->tokens <= UTTT_MAX_UPDATE_TOKENS, "tokens per chunk must be in [1, %d] (got %lld)",
+               UTTT_MAX_UPDATE_TOKENS, (long long)a->tokens);
+  const size_t need = update_layout(a->batch, a->tokens, a->d_model, a->d_ff, a->act_dtype).total;
   UTTT_REQUIRE(need <= UTTT_NOALLOC_SCRATCH_BYTES,
                "uttt_chunk_update_noalloc: this shape needs %zu bytes of workspace, more than the %llu-byte "
                "device-resident scratch; use uttt_chunk_update with a workspace",

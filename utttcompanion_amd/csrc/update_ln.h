@@ -23,8 +23,8 @@ struct LnGradArgs {
   const float* mask; int64_t mask_rs;
   const float* ln_w;
   const float* ln_b;
-  void* dz;     // act dtype (B, 64, D)
-  float* loss;  // (B, 64): token loss times its mask value
+  void* dz;     // act dtype (B, tok_pad, D)
+  float* loss;  // (B, tok_pad): token loss times its mask value
 };
 
 // kPer features per thread (D <= 256 kPer); the split partials of a token are read
@@ -33,10 +33,10 @@ template <typename T, int kPer>
 __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
   __shared__ float red[4];
   const int t = blockIdx.x, b = blockIdx.y;
-  T* dz = static_cast<T*>(a.dz) + ((int64_t)b * 64 + t) * a.D;
+  T* dz = static_cast<T*>(a.dz) + ((int64_t)b * a.tok_pad + t) * a.D;
   if (t >= a.C) {
     for (int d = threadIdx.x; d < a.D; d += kThreads) dz[d] = from_f32<T>(0.f);
-    if (threadIdx.x == 0) a.loss[b * 64 + t] = 0.f;
+    if (threadIdx.x == 0) a.loss[b * a.tok_pad + t] = 0.f;
     return;
   }
   const T* kr = static_cast<const T*>(a.k) + (int64_t)b * a.k_rs + (int64_t)t * a.D;
@@ -98,7 +98,10 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
   // the loss and the mask's token count in one reduction
   __shared__ float red2[8];
   const float* mr = a.mask != nullptr ? a.mask + (int64_t)b * a.mask_rs : nullptr;
-  float sums[2] = {se, (mr != nullptr && threadIdx.x < a.C) ? mr[threadIdx.x] : 0.f};
+  float msum = 0.f;  // the chunk's valid tokens (C may exceed the workgroup)
+  if (mr != nullptr)
+    for (int i = threadIdx.x; i < a.C; i += kThreads) msum += mr[i];
+  float sums[2] = {se, msum};
   block_sums<2>(sums, red2);
   const float token_loss = 0.5f * sums[0] * inv_scale;
 
@@ -130,7 +133,7 @@ __global__ void __launch_bounds__(kThreads) k_ln_grad(const LnGradArgs a) {
     const int d = threadIdx.x + i * kThreads;
     if (d < a.D) dz[d] = from_f32<T>(rstd * (e[i] - m1 - z[i] * m2));
   }
-  if (threadIdx.x == 0) a.loss[b * 64 + t] = a.mask != nullptr ? token_loss * m_t : token_loss;
+  if (threadIdx.x == 0) a.loss[b * a.tok_pad + t] = a.mask != nullptr ? token_loss * m_t : token_loss;
 }
 
 // Launch k_ln_grad with the narrowest per-thread width that covers d_model.

@@ -145,6 +145,10 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
     # W_gate (one read of those weights for both), and the chain stage runs in two parts, as in
     # the model's prefill with writes
     shared = copies is not None
+    long_chunks = c > K.MAX_CHAIN_CHUNK
+    if long_chunks:  # one update per layer; two state sets that swap roles per chunk
+        sets = [cur, tuple(torch.empty_like(t) for t in cur)]
+        ws_update = None
     for ci in range(n_chunks):
         rows, off = active[ci], ci * c
         end = off + c
@@ -152,6 +156,29 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
         hid = h[:rows, off:end].contiguous()  # this chunk's residual stream, updated in place
         rd = [t[:rows] for t in read]
         chunk_rl = torch.empty((n_layers, rows, 2), dtype=torch.float32, device=dev)
+        if long_chunks:
+            # chunks longer than the layer chain takes (the reference's configs write 128 and 512):
+            # per layer, the update into the cursor set with the readout through the chunk-start
+            # set (layer 0 writes the chunk-start set into the other one)
+            snap = [t[:rows] for t in sets[ci % 2]]
+            cursor = [t[:rows] for t in sets[(ci + 1) % 2]]
+            for li, block in enumerate(model.layers):
+                attn = block.attn
+                kb, vb = k_bufs[li][:rows], v_bufs[li][:rows]
+                q = attn.project(hid, off, kb, vb, off, norm=block.attn_norm)
+                att = torch.empty((rows, c, attn.n_heads, hd), dtype=dt, device=dev)
+                K.swa_prefill(q.transpose(1, 2), kb, vb, win, off, out=att.transpose(1, 2), kv_len=end)
+                hid = linear_residual(hid, att.view(rows, c, -1), attn.wo.weight)
+                uq, uk, uv, eta, alpha = block.uttt.projections(hid, norm=block.uttt_norm)
+                prep = K.prepare_chunk_update(uq, uk, uv, eta, alpha, *(snap if li == 0 else cursor), ln_w, ln_b,
+                                              cur_mask, pool.momentum_beta, clip, pool.normalize_loss_by_dim,
+                                              pool.eps, read_w_up=snap[0], read_w_gate=snap[1], read_w_down=snap[2],
+                                              out_state=cursor, surprise=surprise[ci, li], workspace=ws_update,
+                                              row_loss=chunk_rl[li], min_row_surprise=min_chunk_surprise)
+                ws_update = prep.workspace
+                hid = linear_residual(hid, prep.launch()[0], block.uttt.w_o.weight)
+            row_loss[:, :rows] += chunk_rl
+            continue
         run = K.ChunkChainRun(n_layers, c, [t[:rows] for t in cur], ln_w, ln_b, cur_mask, pool.momentum_beta, clip,
                               pool.normalize_loss_by_dim, pool.eps, dt,
                               copies=None if copies is None else [t[:rows] for t in copies],
@@ -192,6 +219,11 @@ def ragged_test_time_update(model: uTTTModel, interactions: Sequence[Tensor],
         row_loss[:, :rows] += chunk_rl
 
     final = cur
+    if long_chunks:  # a request's final state is in the set its last chunk wrote
+        for row, i in enumerate(order):
+            if chunks[i] % 2:
+                for dst, src in zip(sets[0], sets[1]):
+                    dst[row].copy_(src[row])
     per_layer = (row_loss[..., 0] / row_loss[..., 1].clamp_min(1.0)).t()  # (N, L)
     floats = per_layer.tolist()  # the reference's end-of-forward read, once for all requests
 

@@ -111,6 +111,11 @@ def _read_weight(t: Tensor, bsz: int, name: str, keep_bf16: bool = False) -> Tup
 # fast-weight chunk update (reference fused_chunk_ttt_step, model/uttt_layer.py:414-534)
 # ---------------------------------------------------------------------------
 
+# Longest chunk the layer chain (uttt_chunk_chain) takes: its Gram blocks and token slabs are one
+# 64-token tile per layer.  Longer write chunks run one uttt_chunk_update per layer.
+MAX_CHAIN_CHUNK = 64
+
+
 class PreparedUpdate:
     """A validated ``uttt_chunk_update`` call: the argument block, the tensors it points to
     and the result tuple.  ``launch()`` enqueues the whole update on the current stream;
@@ -158,8 +163,8 @@ def prepare_chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
     if q.dim() != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError(f"q/k/v must share one (B, C, D) shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     bsz, tokens, dim = q.shape
-    if not 1 <= tokens <= 64:
-        raise ValueError(f"a chunk holds 1..64 tokens on the HIP path, got {tokens}")
+    if not 1 <= tokens <= N.MAX_UPDATE_TOKENS:
+        raise ValueError(f"a chunk update holds 1..{N.MAX_UPDATE_TOKENS} tokens on the HIP path, got {tokens}")
     if q.dtype != k.dtype or q.dtype != v.dtype:
         raise ValueError("q, k and v must share one dtype")
     act = q.dtype
@@ -221,7 +226,7 @@ def prepare_chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
         surprise = torch.empty((), dtype=torch.float32, device=dev)
 
     lib = N.load_library()
-    nbytes = lib.uttt_chunk_update_workspace(bsz, dim, ff, code)
+    nbytes = lib.uttt_chunk_update_workspace_tokens(bsz, tokens, dim, ff, code)
     if workspace is None or workspace.numel() < nbytes or workspace.device != dev:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     a = N.ChunkUpdateArgs()
@@ -267,8 +272,10 @@ def chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Tensor,
     like the reference.  ``out_state`` (six fp32 tensors) receives the new state
     and may be the input state itself for an in-place update; by default new
     tensors are allocated.  ``surprise`` is a 0-d fp32 device tensor (no sync).
-    ``workspace`` (uint8, at least ``uttt_chunk_update_workspace`` bytes) is reused
-    when given; calls that share one workspace must be ordered on one stream.
+    ``workspace`` (uint8, at least ``uttt_chunk_update_workspace_tokens`` bytes) is reused
+    when given; calls that share one workspace must be ordered on one stream.  A chunk
+    may hold up to ``N.MAX_UPDATE_TOKENS`` (512) tokens: one write for the whole chunk, as
+    the reference's chunk loop does with its configs' 128- and 512-token chunks.
     """
     return prepare_chunk_update(q, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight,
                                 ln_bias, token_mask, momentum_beta, max_inner_grad_norm, normalize_by_dim, eps,

@@ -27,15 +27,17 @@ from . import kernels as K
 Tensor = torch.Tensor
 _STATE_NAMES = ("w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down")
 
-# Longest chunk the write kernels take: one 64-token tile per chunk and layer.  Frozen reads
-# (update_fast_weights=False, decoding) do not chunk and take any chunk_size.
-MAX_WRITE_CHUNK = 64
+# Longest chunk one fast-weight write takes (uttt_chunk_update, UTTT_MAX_UPDATE_TOKENS): the
+# reference's shipped configs use 128 and 512.  Chunks of up to 64 tokens also run the fused layer
+# chain and the resident loop.  Frozen reads (update_fast_weights=False, decoding) do not chunk
+# and take any chunk_size.
+MAX_WRITE_CHUNK = 512
 
 
 def require_write_chunk(chunk_size: int) -> None:
-    """Refuse a fast-weight write with chunks the kernels do not take, before any work.  The
-    reference's shipped configs use chunk_size 128 or 512; splitting such a chunk into 64-token
-    pieces would change how many writes happen, so it is not done silently."""
+    """Refuse a fast-weight write with chunks the kernels do not take, before any work (one write
+    per chunk, as the reference's chunk loop does; a longer chunk is never split into several
+    writes)."""
     if not 1 <= int(chunk_size) <= MAX_WRITE_CHUNK:
         raise ValueError(f"chunk_size={chunk_size}: fast-weight writes on the HIP path take chunks of 1.."
                          f"{MAX_WRITE_CHUNK} tokens; frozen reads (update_fast_weights=False, decoding) take "

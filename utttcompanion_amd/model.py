@@ -277,14 +277,17 @@ class uTTTModel(nn.Module):
         cur = tuple(t.detach().to(device=dev, dtype=torch.float32).clone(memory_format=torch.contiguous_format)
                     for t in state.tensors())
         ln_w, ln_b = state.ln_weight, state.ln_bias
-        # bf16 copies of the state on the bf16 path (the reference casts W to the activation
-        # dtype for these matmuls): the readouts and the chain read them; each chain refreshes them
-        copies = [t.to(torch.bfloat16) for t in cur] if h.dtype == torch.bfloat16 else None
-        read = copies[:3] if copies is not None else cur[:3]
         surprises = torch.zeros((n_chunks, n_layers), dtype=torch.float32, device=dev)
         counts = torch.full((n_chunks,), float(bsz * c), dtype=torch.float32, device=dev)
         if seq % c:
             counts[-1:].fill_(float(bsz * (seq % c)))
+        if c > K.MAX_CHAIN_CHUNK:  # longer write chunks: one update per layer (no layer chain)
+            return (yield from self._prefill_per_layer_updates(h, cur, ln_w, ln_b, attention_mask, k_bufs, v_bufs,
+                                                                hist, start_pos, surprises, counts))
+        # bf16 copies of the state on the bf16 path (the reference casts W to the activation
+        # dtype for these matmuls): the readouts and the chain read them; each chain refreshes them
+        copies = [t.to(torch.bfloat16) for t in cur] if h.dtype == torch.bfloat16 else None
+        read = copies[:3] if copies is not None else cur[:3]
         pool = self.fast_weight_pool
         clip = float(pool.max_inner_grad_norm or 0.0)
         pieces = []
@@ -388,6 +391,64 @@ class uTTTModel(nn.Module):
         caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win else (kb, vb)
                   for kb, vb in zip(k_bufs, v_bufs)]
         return torch.cat(pieces, dim=1), cur, per_layer, caches
+
+    def _prefill_per_layer_updates(self, h: Tensor, cur: Tuple[Tensor, ...], ln_w: Tensor, ln_b: Tensor,
+                                   attention_mask: Optional[Tensor], k_bufs: List[Tensor], v_bufs: List[Tensor],
+                                   hist: int, start_pos: int, surprises: Tensor, counts: Tensor):
+        """The chunk-first schedule for write chunks longer than the layer chain takes (the
+        reference's configs write 128- and 512-token chunks): per chunk, layer by layer, the
+        block's attention and projections, then one ``uttt_chunk_update`` that writes the layer's
+        update into the cursor state and reads its readout through the chunk-start state
+        (reference uttt_model.py:519-608 with ``fused_chunk_ttt_step``'s ``read_w_*``,
+        uttt_layer.py:414-534).  The state lives in two buffer sets that swap roles per chunk:
+        layer 0 writes the chunk-start set into the other one, later layers update that one in
+        place, and the chunk-start set is read by every layer's readout.  Each update streams the
+        fp32 state; the layer chain's single state write per chunk does not apply here.  A
+        generator like ``prefill_steps``; returns the same tuple."""
+        cfg = self.config
+        bsz, seq, _ = h.shape
+        c, n_layers = cfg.chunk_size, len(self.layers)
+        n_chunks = (seq + c - 1) // c
+        attn0 = self.layers[0].attn
+        hd, win = attn0.head_dim, attn0.window_size
+        pool = self.fast_weight_pool
+        clip = float(pool.max_inner_grad_norm or 0.0)
+        sets = [tuple(cur), tuple(torch.empty_like(t) for t in cur)]
+        start_set = 0
+        ws = None
+        pieces = []
+        for ci in range(n_chunks):
+            off = ci * c
+            end = min(seq, off + c)
+            mask = attention_mask[:, off:end] if attention_mask is not None else None
+            if mask is not None:
+                mask = mask.to(torch.float32)
+                counts[ci].copy_(mask.sum())
+            snap, cursor = sets[start_set], sets[start_set ^ 1]
+            hid = h[:, off:end].contiguous()
+            for li, block in enumerate(self.layers):
+                attn = block.attn
+                q = attn.project(hid, start_pos + off, k_bufs[li], v_bufs[li], hist + off, norm=block.attn_norm)
+                att = torch.empty((bsz, end - off, attn.n_heads, hd), dtype=h.dtype, device=h.device)
+                K.swa_prefill(q.transpose(1, 2), k_bufs[li], v_bufs[li], win, hist + off, out=att.transpose(1, 2),
+                              kv_len=hist + end)
+                hid = linear_residual(hid, att.view(bsz, end - off, -1), attn.wo.weight)
+                uq, uk, uv, eta, alpha = block.uttt.projections(hid, norm=block.uttt_norm)
+                src = snap if li == 0 else cursor  # layer 0 writes the chunk-start state out of place
+                prep = K.prepare_chunk_update(uq, uk, uv, eta, alpha, *src, ln_w, ln_b, mask, pool.momentum_beta,
+                                              clip, pool.normalize_loss_by_dim, pool.eps, read_w_up=snap[0],
+                                              read_w_gate=snap[1], read_w_down=snap[2], out_state=cursor,
+                                              surprise=surprises[ci, li], workspace=ws)
+                ws = prep.workspace
+                r = prep.launch()[0]
+                hid = linear_residual(hid, r, block.uttt.w_o.weight)
+            start_set ^= 1
+            pieces.append(hid)
+            yield ci
+        per_layer = (surprises * counts[:, None]).sum(dim=0) / counts.sum().clamp_min(1.0)
+        caches = [(kb[:, :, -win:].contiguous(), vb[:, :, -win:].contiguous()) if kb.shape[2] > win else (kb, vb)
+                  for kb, vb in zip(k_bufs, v_bufs)]
+        return torch.cat(pieces, dim=1), sets[start_set], per_layer, caches
 
     def _chain_stream(self, device: torch.device) -> "torch.cuda.Stream":
         """The second stream the layer chain runs on (default priority, created once per device)."""
