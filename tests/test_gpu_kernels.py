@@ -669,3 +669,22 @@ def test_greedy_select_matches_masked_argmax(dtype, rows, vocab, limit):
     got2 = K.greedy_select(allmasked.to(DEV), banned, limit)
     torch.cuda.synchronize()
     assert got2.tolist() == [0, 0]
+
+
+def test_chunk_update_broadcast_eta_alpha_match_oracle():
+    """Per-row eta / alpha of shape (B, 1, 1), and one shared (1, 1, 1) value, broadcast over the
+    chunk as the reference does (model/uttt_layer.py:371-378, :501-511): the same result as the
+    oracle given the same broadcast tensors."""
+    K = kernels()
+    q, k, v, _, _, w, s, ln_w, ln_b = make_chunk(3, 40, 128, 256, seed=31)
+    mask = torch.ones(3, 40)
+    mask[1, 30:] = 0
+    for eta, alpha in ((torch.tensor([0.01, 0.02, 0.005]).view(3, 1, 1), torch.full((1, 1, 1), 0.003)),
+                       (torch.full((1, 1, 1), 0.02), torch.tensor([0.001, 0.004, 0.002]).view(3, 1, 1))):
+        ref = om.fused_chunk_ttt_step(q, k, v, eta, alpha, *w, *s, ln_w, ln_b, mask, 0.9, 1.0, True, 1e-5)
+        with torch.no_grad():
+            got = K.chunk_update(*to_dev(q, k, v, eta, alpha, *w, *s, ln_w, ln_b), mask.to(DEV), 0.9, 1.0, True, 1e-5)
+        torch.cuda.synchronize()
+        for name, a, e in zip(("readout", "w_up", "w_gate", "w_down", "s_up", "s_gate", "s_down", "surprise"), got,
+                              ref):
+            assert rel_err(a, e) <= F32_REL, name

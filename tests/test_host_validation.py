@@ -69,19 +69,20 @@ def test_c_abi_rejects_bad_greedy_and_skinny_calls(lib):
     assert b"x_eps" in lib.uttt_last_error()
 
 
-@pytest.mark.parametrize("shape", [(2, 1, 1), (2, 1), (1, 16, 1), (2, 15), (2, 16, 2)])
-def test_chunk_update_refuses_broadcast_eta_and_alpha(shape):
-    """The kernels read one eta / alpha per (row, token); shapes the reference would broadcast
-    are refused before any launch (the check runs ahead of the device check, so on the CPU)."""
+@pytest.mark.parametrize("shape", [(2, 15), (2, 16, 2), (3, 16, 1), (2, 2, 16, 1)])
+def test_chunk_update_refuses_eta_and_alpha_that_do_not_broadcast(shape):
+    """One eta / alpha per (row, token), or a shape the reference broadcasts against (B, C, 1);
+    anything else is refused before any launch (the check runs ahead of the device check, so on
+    the CPU)."""
     b, c, d, f = 2, 16, 64, 64
     q = torch.zeros(b, c, d)
     w = (torch.zeros(b, d, f), torch.zeros(b, d, f), torch.zeros(b, f, d))
     good = torch.zeros(b, c, 1)
     for eta, alpha in ((torch.zeros(shape), good), (good, torch.zeros(shape))):
-        with pytest.raises(ValueError, match=r"must be \(2, 16\) or \(2, 16, 1\)"):
+        with pytest.raises(ValueError, match=r"must broadcast to \(2, 16, 1\)"):
             K.prepare_chunk_update(q, q, q, eta, alpha, *w, *w, torch.ones(d), torch.zeros(d), None, 0.9, 1.0,
                                    True, 1e-5)
-    for ok in ((b, c), (b, c, 1)):  # accepted shapes get as far as the device check
+    for ok in ((b, c), (b, c, 1), (b, 1, 1), (b, 1), (1, c, 1), (1, 1, 1)):  # get as far as the device check
         with pytest.raises(ValueError, match="no CPU path"):
             K.prepare_chunk_update(q, q, q, torch.zeros(ok), torch.zeros(ok), *w, *w, torch.ones(d),
                                    torch.zeros(d), None, 0.9, 1.0, True, 1e-5)
@@ -108,3 +109,16 @@ def test_prefill_plan_refuses_a_deferred_join_under_capture(monkeypatch):
     for kw in (dict(defer_join=True), dict(wait_event=12345)):
         with pytest.raises(ValueError, match="graph capture"):
             PrefillPlan.run(object(), None, 0, 0, 0, None, None, None, None, **kw)
+
+
+def test_per_token_scalars_broadcast_like_the_reference():
+    """eta / alpha that broadcast against (B, C, 1) are expanded to one value per (row, token);
+    shapes that do not broadcast are refused before any device work."""
+    per = K._per_token(torch.tensor([0.1, 0.2]).view(2, 1, 1), 2, 5, "eta")
+    assert per.shape == (2, 5) and per.is_contiguous() and torch.equal(per[1], torch.full((5,), 0.2))
+    assert K._per_token(torch.tensor(0.3), 2, 5, "eta").shape == (2, 5)
+    same = torch.zeros(2, 5, 1)
+    assert K._per_token(same, 2, 5, "eta") is same
+    for bad in (torch.zeros(3, 5), torch.zeros(2, 4, 1), torch.zeros(2, 5, 2), torch.zeros(1, 2, 5, 1)):
+        with pytest.raises(ValueError, match="broadcast"):
+            K._per_token(bad, 2, 5, "eta")

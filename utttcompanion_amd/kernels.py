@@ -72,11 +72,20 @@ def _row_vector(x: Tensor, act: torch.dtype) -> Tensor:
     return x
 
 
-def _check_per_token(x: Tensor, bsz: int, tokens: int, name: str) -> None:
-    """eta / alpha must hold one value per (row, token): (B, C) or (B, C, 1).  The kernels
-    read C entries per row, so a broadcastable (B, 1, 1) or (B, 1) is refused, not read past."""
-    if tuple(x.shape) not in ((bsz, tokens), (bsz, tokens, 1)):
-        raise ValueError(f"{name} must be ({bsz}, {tokens}) or ({bsz}, {tokens}, 1), got {tuple(x.shape)}")
+def _per_token(x: Tensor, bsz: int, tokens: int, name: str) -> Tensor:
+    """eta / alpha as one value per (row, token): (B, C) or (B, C, 1) pass through; anything the
+    reference broadcasts against (B, C, 1) (model/uttt_layer.py:371-378, :501-511: a per-row
+    (B, 1, 1), a shared (1, 1, 1), a (B, 1) ...) is expanded into a new (B, C) tensor, since the
+    kernels read C entries per row; other shapes raise ``ValueError``."""
+    if tuple(x.shape) in ((bsz, tokens), (bsz, tokens, 1)):
+        return x
+    try:
+        if x.dim() > 3 or (x.dim() == 3 and x.shape[-1] != 1):
+            raise RuntimeError
+        y = x if x.dim() < 3 else x[..., 0]
+        return torch.broadcast_to(y, (bsz, tokens)).contiguous()
+    except RuntimeError:
+        raise ValueError(f"{name} must broadcast to ({bsz}, {tokens}, 1), got {tuple(x.shape)}") from None
 
 
 def _state(t: Tensor, name: str) -> Tensor:
@@ -179,8 +188,8 @@ def prepare_chunk_update(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: Te
             raise ValueError("momentum buffers must match the weight shapes")
     if dim % 64 or ff % 64 or dim > 4096:
         raise ValueError(f"d_model and d_ff must be multiples of 64 (d_model <= 4096); got {dim}, {ff}")
-    _check_per_token(eta, bsz, tokens, "eta")
-    _check_per_token(alpha, bsz, tokens, "alpha")
+    eta = _per_token(eta, bsz, tokens, "eta")
+    alpha = _per_token(alpha, bsz, tokens, "alpha")
     _require_device(dev, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias,
                     token_mask, read_w_up, read_w_gate, read_w_down)
     _forward_only(q, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias)
@@ -376,8 +385,8 @@ def layer_update_resident(q: Tensor, k: Tensor, v: Tensor, eta: Tensor, alpha: T
     for s, w in ((s_up, w_up), (s_gate, w_gate), (s_down, w_down)):
         if s.shape != w.shape:
             raise ValueError("momentum buffers must match the weight shapes")
-    _check_per_token(eta, bsz, tokens, "eta")
-    _check_per_token(alpha, bsz, tokens, "alpha")
+    eta = _per_token(eta, bsz, tokens, "eta")
+    alpha = _per_token(alpha, bsz, tokens, "alpha")
     dev = q.device
     _require_device(dev, k, v, eta, alpha, w_up, w_gate, w_down, s_up, s_gate, s_down, ln_weight, ln_bias,
                     token_mask)
@@ -670,8 +679,8 @@ class ChunkChainRun(PreparedChain):
         act = self._act
         if k.shape != (bsz, tokens, dim) or v.shape != k.shape or k.dtype != act or v.dtype != act:
             raise ValueError(f"layer {l}: k/v must be ({bsz}, {tokens}, {dim}) {act}")
-        _check_per_token(eta, bsz, tokens, f"layer {l}: eta")
-        _check_per_token(alpha, bsz, tokens, f"layer {l}: alpha")
+        eta = _per_token(eta, bsz, tokens, f"layer {l}: eta")
+        alpha = _per_token(alpha, bsz, tokens, f"layer {l}: alpha")
         _require_device(self.device, k, v, eta, alpha)
         _forward_only(k, v, eta, alpha)
         k, v = _rows(k), _rows(v)
