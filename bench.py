@@ -63,11 +63,14 @@ def measured_traffic(kernel: str, config: str = "c2"):
     """HBM bytes per launch of ``kernel`` at a config's shape, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (scaled by a copy kernel of known size), or None when no
     summary for that kernel is present.  Looks for a ``traffic_bytes_per_launch <kernel>:`` line
-    in ``profiles/chain_<config>_traffic.md``, then a ``traffic_bytes_per_launch:`` line in
+    in ``profiles/prefill_<config>_traffic.md`` (the state write's launch of ``k_chain_apply_lds``
+    runs ``k_chain_apply_wide`` at config 3), then a ``traffic_bytes_per_launch:`` line in
     ``profiles/<kernel>_<config>_traffic.md``."""
     here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
-    for path, prefix in ((os.path.join(here, f"chain_{config}_traffic.md"), f"traffic_bytes_per_launch {kernel}:"),
-                         (os.path.join(here, f"{kernel}_{config}_traffic.md"), "traffic_bytes_per_launch:")):
+    names = [kernel] + (["k_chain_apply_wide"] if kernel == "k_chain_apply_lds" else [])
+    candidates = [(os.path.join(here, f"prefill_{config}_traffic.md"), f"traffic_bytes_per_launch {n}:") for n in names]
+    candidates.append((os.path.join(here, f"{kernel}_{config}_traffic.md"), "traffic_bytes_per_launch:"))
+    for path, prefix in candidates:
         try:
             with open(path) as fh:
                 for line in fh:
@@ -832,17 +835,20 @@ def main() -> int:
             in_us = table[dom]["mean_us"]
             in_gbs = nbytes_dom / (in_us * 1e-6) / 1e9
             tfs = flops["total"] / sec / 1e12
+            prefill_traffic = measured_prefill_traffic("c3")
             # the headline's roofline is the whole prefill's: its algorithmic flops against the
             # bf16 MFMA peak (the north star's axis; the state-byte fractions beside it); the
             # dominant streaming kernel is reported separately, in the prefill and alone
             roofline = {"bound": "mfma", "achieved": round(tfs, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(tfs / PEAK_BF16_TFLOPS, 4), "traffic": measured_prefill_traffic("c3"),
+                        "frac": round(tfs / PEAK_BF16_TFLOPS, 4), "traffic": prefill_traffic,
                         "scope": "one whole config-3 prefill with writes: algorithmic flops (update + readout "
                                  "20 D F per token and layer, window attention, slow projections) over the timed "
                                  "prefill's time; traffic = HBM bytes per prefill (rocprofv3 FETCH_SIZE + WRITE_SIZE "
                                  "over the library's kernels of one prefill) or null",
                         "hbm_frac_min_state_bytes": prefill["hbm_frac_min_state_bytes"],
                         "hbm_frac_design_bytes": prefill["hbm_frac_design_bytes"],
+                        "hbm_frac_measured_traffic": (round(prefill_traffic / sec / 1e9 / PEAK_HBM_GBS, 4)
+                                                      if prefill_traffic else None),
                         "dominant_kernel": {
                             "kernel": dom, "unit_bytes": CHAIN_STATE_WHAT[dom], "algorithmic_bytes": nbytes_dom,
                             "shape": {"B": C3_BATCH, "D": D, "F": F, "L": C3["n_layers"]},
