@@ -662,6 +662,10 @@ def bench_evolve(model, steps: int):
             "mean_surprise": round(sum(r.surprise for r in res) / len(res), 4),
             "min_state_bytes_per_step": 48 * D * F * chunks}  # W, S read + written once per row-chunk
     info["state_hbm_gbs"] = round(info["min_state_bytes_per_step"] / (ms * 1e-3) / 1e9, 1)
+    # the design's streamed bytes per row-chunk, as for config 3: every layer's bf16 state copies
+    # (18 D F) and the state write (60 D F)
+    info["design_bytes_per_step"] = (18 * C3["n_layers"] + 60) * D * F * chunks
+    info["design_hbm_frac"] = round(info["design_bytes_per_step"] / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
     return tokens / (ms * 1e-3), ms, info
 
 
