@@ -206,12 +206,14 @@ def test_swiglu_readout_with_bf16_weight_copies():
     check_bf16_activation("readout", from_bf16, ref, ref16)
 
 
-@pytest.mark.parametrize("b,d,f", [(32, 768, 2048), (5, 512, 1024), (3, 1536, 640)])
+@pytest.mark.parametrize("b,d,f", [(32, 768, 2048), (5, 512, 1024), (3, 1536, 640), (3, 576, 640)])
 def test_decode_readout_with_query_norm_in_one_launch(b, d, f):
     """One token per row: the readout of RMSNorm(y) (q_norm folded into the readout's x staging)
     equals the readout of torch's normalised rows to the bf16 readout bound, and the one-launch
     form (row counters: LayerNorm in each row's last weight block) equals the two-launch form
-    bit for bit on two calls in a row; the counters are zero again after each call."""
+    bit for bit on two calls in a row; the counters are zero again after each call.  The
+    descending weight walk (``sweep_reverse``) meets the same bound, in both forms, and repeats
+    bit for bit (576 x 640 leaves partial row batches in both weight loops)."""
     import torch.nn.functional as F
     K = kernels()
     g = torch.Generator().manual_seed(b + d + f)
@@ -229,8 +231,14 @@ def test_decode_readout_with_query_norm_in_one_launch(b, d, f):
             two = K.swiglu_readout(yd, *dw[:5], eps=1e-5, x_norm=(dw[5], eps))
             one = K.swiglu_readout(yd, *dw[:5], eps=1e-5, x_norm=(dw[5], eps), row_counters=counters)
             plain = K.swiglu_readout(F.rms_norm(yd, (d,), dw[5], eps), *dw[:5], eps=1e-5)
+            rev_one = K.swiglu_readout(yd, *dw[:5], eps=1e-5, x_norm=(dw[5], eps), row_counters=counters,
+                                       sweep_reverse=True)
+            rev_two = K.swiglu_readout(yd, *dw[:5], eps=1e-5, x_norm=(dw[5], eps), sweep_reverse=True)
+            rev_again = K.swiglu_readout(yd, *dw[:5], eps=1e-5, x_norm=(dw[5], eps), row_counters=counters,
+                                         sweep_reverse=True)
         torch.cuda.synchronize()
         assert torch.equal(one, two), call
+        assert torch.equal(rev_one, rev_two) and torch.equal(rev_one, rev_again), call
         assert counters.abs().sum().item() == 0
         yf = y.float()
         xn = (yf * torch.rsqrt(yf.pow(2).mean(-1, keepdim=True) + eps) * qw.float()).bfloat16()
@@ -238,6 +246,7 @@ def test_decode_readout_with_query_norm_in_one_launch(b, d, f):
         ref16 = om.swiglu_fast_forward(xn, *w, ln_w, ln_b, 1e-5)
         check_bf16_activation("fused readout", one, ref, ref16)
         check_bf16_activation("plain readout", plain, ref, ref16)
+        check_bf16_activation("reversed readout", rev_one, ref, ref16)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -148,6 +148,7 @@ class ReadoutArgs(C.Structure):
         ("key_up_out", _P), ("key_gate_out", _P),
         ("x_norm_weight", _P), ("x_norm_eps", _F),
         ("row_counters", _P),
+        ("sweep_reverse", _I32),
     ]
 
 

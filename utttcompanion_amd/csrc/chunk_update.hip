@@ -61,6 +61,7 @@ struct FwdArgs {
   const float* ln_b;
   void* out;
   int64_t out_rs;
+  int rev;  // GEMV only: walk the weight rows in descending order
 };
 
 // ---------------------------------------------------------------------------
@@ -968,18 +969,21 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
   float au[8], ag[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) au[e] = ag[e] = 0.f;
-  int d = d_begin;
-  for (; d + RB <= d_end; d += RB) {  // RB rows of both matrices in flight
+  // the i-th row of this thread's range: ascending, or descending with a.rev
+  const int d_n = d_end - d_begin, d_first = a.rev ? d_end - 1 : d_begin, d_step = a.rev ? -1 : 1;
+  int i = 0;
+  for (; i + RB <= d_n; i += RB) {  // RB rows of both matrices in flight
     Piece8<WT> pu[RB], pg[RB];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      pu[r].load(gu + (int64_t)(d + r) * a.F + col);
-      pg[r].load(gg + (int64_t)(d + r) * a.F + col);
+      const int d = d_first + (i + r) * d_step;
+      pu[r].load(gu + (int64_t)d * a.F + col);
+      pg[r].load(gg + (int64_t)d * a.F + col);
     }
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-      const float xv = xs[d + r];
+      const float xv = xs[d_first + (i + r) * d_step];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         au[e] += xv * pu[r].get(e);
@@ -987,7 +991,8 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
       }
     }
   }
-  for (; d < d_end; ++d) {
+  for (; i < d_n; ++i) {
+    const int d = d_first + i * d_step;
     Piece8<WT> pu, pg;
     pu.load(gu + (int64_t)d * a.F + col);
     pg.load(gg + (int64_t)d * a.F + col);
@@ -1026,24 +1031,27 @@ __global__ void __launch_bounds__(kThreads) k_readout_gemv(const FwdArgs a) {
   for (int e = 0; e < CW; ++e) az[e] = 0.f;
   if (p < nparts) {
     const int f_per = FB / nparts + (FB % nparts != 0), fb0 = p * f_per, fb1 = min(FB, fb0 + f_per);
-    int f = fb0;
-    for (; f + RD <= fb1; f += RD) {
+    const int f_n = fb1 - fb0, f_first = a.rev ? fb1 - 1 : fb0, f_step = a.rev ? -1 : 1;
+    int j = 0;
+    for (; j + RD <= f_n; j += RD) {
       Piece8<WT> pw[RD][NP];
 #pragma unroll
       for (int r = 0; r < RD; ++r)
 #pragma unroll
-        for (int q = 0; q < NP; ++q) pw[r][q].load(gd + (int64_t)(f + r) * a.D + c * CW + q * 8);
+        for (int q = 0; q < NP; ++q)
+          pw[r][q].load(gd + (int64_t)(f_first + (j + r) * f_step) * a.D + c * CW + q * 8);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int r = 0; r < RD; ++r) {
-        const float hv = hs[f + r];
+        const float hv = hs[f_first + (j + r) * f_step];
 #pragma unroll
         for (int q = 0; q < NP; ++q)
 #pragma unroll
           for (int e = 0; e < 8; ++e) az[q * 8 + e] += hv * pw[r][q].get(e);
       }
     }
-    for (; f < fb1; ++f) {
+    for (; j < f_n; ++j) {
+      const int f = f_first + j * f_step;
       const float hv = hs[f];
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
@@ -1139,6 +1147,7 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   f.kx = a.keys; f.kx_rs = a.keys_row_stride; f.ku = a.key_up_out; f.kg = a.key_gate_out;
   f.xn_w = a.x_norm_weight; f.xn_eps = a.x_norm_eps; f.counters = a.row_counters;
   f.ln_eps = a.eps; f.ln_w = a.ln_weight; f.ln_b = a.ln_bias; f.out = a.out; f.out_rs = a.out_row_stride;
+  f.rev = a.sweep_reverse != 0;
   const dim3 blk(kThreads);
   if constexpr (sizeof(T) == 2) {
     if (a.tokens == 1 && a.keys == nullptr && D <= 2048 && D % 8 == 0) {  // decode: streaming GEMV

@@ -192,14 +192,18 @@ class BatchedDecoder:
             h = self._linear(att.reshape(n, -1), attn.wo.weight, residual=h)
             y = self._linear(h, block.uttt.w_q.weight, norm=block.uttt_norm)
             qn = block.uttt.q_norm
+            # every layer reads the same per-request copies: odd layers walk them backwards, so
+            # each readout starts on the lines the previous one left in the infinity cache
+            rev = li % 2 == 1
             if self._fused_readout:  # q_norm, readout, LayerNorm and residual in one launch
                 r = K.swiglu_readout(y.view(n, 1, -1), self.w_up, self.w_gate, self.w_down, self.ln_weight,
                                      self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read,
-                                     x_norm=(qn.weight, qn.eps), row_counters=self._counters)
+                                     x_norm=(qn.weight, qn.eps), row_counters=self._counters, sweep_reverse=rev)
             else:
                 uq = F.rms_norm(y, (h.shape[-1],), qn.weight.to(h.dtype), qn.eps)
                 r = K.swiglu_readout(uq.view(n, 1, -1), self.w_up, self.w_gate, self.w_down, self.ln_weight,
-                                     self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read)
+                                     self.ln_bias, m.fast_weight_pool.eps, workspace=self._ws_read,
+                                     sweep_reverse=rev)
             h = self._linear(r.view(n, -1), block.uttt.w_o.weight, residual=h)
         logits = self._linear(h, m.lm_head.weight, norm=m.norm)
         self.logits = logits

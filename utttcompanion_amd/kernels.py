@@ -972,7 +972,8 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
                    workspace: Optional[Tensor] = None, keys: Optional[Tensor] = None,
                    key_outputs: Optional[Tuple[Tensor, Tensor]] = None,
                    x_norm: Optional[Tuple[Tensor, float]] = None,
-                   row_counters: Optional[Tensor] = None, build_only: bool = False):
+                   row_counters: Optional[Tensor] = None, sweep_reverse: bool = False,
+                   build_only: bool = False):
     """f_W(x) = x + LN((SiLU(x W_gate) * x W_up) W_down) with per-row (or shared) W.
 
     W is read as fp32 masters, or -- when x and all three weights are bf16 -- as bf16 read
@@ -986,7 +987,9 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
     weight instead of x (the decode step's q_norm), and ``row_counters`` (B,) int32, zero before
     the first call and left zero by every call, makes the readout a single launch (the
     LayerNorm runs in each row's last weight block); calls sharing counters must not overlap.
-    ``build_only`` returns (``uttt_readout_args``, workspace, the tensors they point at) without
+    ``sweep_reverse`` walks the weight rows in descending order (one-token rows only): successive
+    calls over the same copies that alternate it start on what the infinity cache still holds
+    from the previous call.  ``build_only`` returns (``uttt_readout_args``, workspace, the tensors they point at) without
     launching."""
     if x.dim() != 3:
         raise ValueError(f"x must be (B, T, D), got {tuple(x.shape)}")
@@ -1048,6 +1051,7 @@ def swiglu_readout(x: Tensor, w_up: Tensor, w_gate: Tensor, w_down: Tensor, ln_w
             raise ValueError(f"row_counters must be a contiguous int32 tensor of >= {bsz} entries")
         _require_device(dev, row_counters)
         a.row_counters = _p(row_counters)
+    a.sweep_reverse = int(bool(sweep_reverse))
     if build_only:
         return a, workspace, (x, parts, ln_w, ln_b, out, keys, keep)
     with torch.cuda.device(dev):
