@@ -166,6 +166,36 @@ def test_no_future_leakage_with_writes_on_gpu():
     assert torch.equal(a[:, :20], b[:, :20])
 
 
+def test_trailing_padding_leaves_writes_and_logits_unchanged():
+    """Padding invariance (reference tests/test_shared_schedule_audit.py:95-127): a row padded at
+    the end with masked tokens takes the same writes, and gives the same logits on its valid
+    tokens, as the unpadded row: masked tokens carry no loss, and a chunk without a valid token
+    neither decays the state nor applies momentum.  40 valid tokens (two full chunks of 16 and a
+    partial one) padded to 64: the partial chunk completed with 8 masked tokens, then a fully
+    masked chunk."""
+    model, _ = build()
+    ids, _ = ids_and_mask(1, 40, 256, seed=31)
+    padded = torch.cat([ids, torch.full((1, 24), 7)], 1)
+    mask = torch.cat([torch.ones(1, 40), torch.zeros(1, 24)], 1)
+    plain = model(ids.to(DEV), update_fast_weights=True)
+    pad = model(padded.to(DEV), attention_mask=mask.to(DEV), update_fast_weights=True)
+    assert rel_err(pad.logits[:, :40], plain.logits) <= 1e-5
+    for n in NAMES:
+        assert rel_err(getattr(pad.fast_state, n), getattr(plain.fast_state, n)) <= 1e-5, n
+
+
+def test_writes_reach_only_later_chunks():
+    """Chunk-first schedule (reference tests/test_shared_schedule_audit.py:40-60): a chunk's
+    writes reach later chunks only.  With writes, the first chunk's logits equal those of a
+    forward without writes (every layer of it reads the initial state); later chunks differ."""
+    model, _ = build()
+    ids, _ = ids_and_mask(1, 48, 256, seed=33)
+    written = model(ids.to(DEV), update_fast_weights=True).logits
+    frozen = model(ids.to(DEV), update_fast_weights=False).logits
+    assert rel_err(written[:, :16], frozen[:, :16]) <= 1e-5
+    assert max_abs(written[:, 16:32], frozen[:, 16:32]) > 1e-3
+
+
 def test_test_time_update_pull_and_drift_match_oracle():
     model, oracle = build()
     ids, mask = ids_and_mask(2, 40, 256, seed=12)
