@@ -69,8 +69,11 @@ __device__ __forceinline__ const T* layer_row(const LayerPtrs& lp, int l, int b,
 
 // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2.  With
 // at least 8 rows the row is the fastest-varying part of the id (rows padded to a multiple of
-// 8), so all workgroups of a row run on one XCD and share its activations in one L2; with
-// fewer rows the tiles vary fastest and every XCD works on every row.
+// 8), so all workgroups of a row run on one XCD and share its activations in one L2.  With 1, 2
+// or 4 rows, row b takes the 8 / B XCDs [8 b / B, 8 (b + 1) / B) and its tiles are dealt over
+// them (the grid padded to whole rounds of 8; the padding workgroups return), so a row's
+// activation slabs are fetched into 8 / B L2s instead of all 8; other row counts interleave the
+// rows over every XCD.
 constexpr int kXcds = 8;
 
 struct RowTile {
@@ -83,11 +86,20 @@ __device__ __forceinline__ RowTile row_tile(int bid, int B, int ntiles) {
     const int b8 = (B + kXcds - 1) / kXcds * kXcds;
     return {bid % b8, bid / b8, bid % b8 < B};
   }
+  if (kXcds % B == 0) {
+    const int per = kXcds / B, x = bid % kXcds, tile = (bid / kXcds) * per + x % per;
+    return {x / per, tile, tile < ntiles};
+  }
   return {bid / ntiles, bid % ntiles, true};
 }
 
 inline int row_tile_blocks(int B, int ntiles) {
-  return (B >= kXcds ? (B + kXcds - 1) / kXcds * kXcds : B) * ntiles;
+  if (B >= kXcds) return (B + kXcds - 1) / kXcds * kXcds * ntiles;
+  if (kXcds % B == 0) {
+    const int per = kXcds / B;
+    return kXcds * ((ntiles + per - 1) / per);
+  }
+  return B * ntiles;
 }
 
 
