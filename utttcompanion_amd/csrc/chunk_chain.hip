@@ -67,40 +67,6 @@ __device__ __forceinline__ const T* layer_row(const LayerPtrs& lp, int l, int b,
   return static_cast<const T*>(lp.p[l]) + (int64_t)b * rs;
 }
 
-// Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2.  With
-// at least 8 rows the row is the fastest-varying part of the id (rows padded to a multiple of
-// 8), so all workgroups of a row run on one XCD and share its activations in one L2.  With 1, 2
-// or 4 rows, row b takes the 8 / B XCDs [8 b / B, 8 (b + 1) / B) and its tiles are dealt over
-// them (the grid padded to whole rounds of 8; the padding workgroups return), so a row's
-// activation slabs are fetched into 8 / B L2s instead of all 8; other row counts interleave the
-// rows over every XCD.
-constexpr int kXcds = 8;
-
-struct RowTile {
-  int b, tile;
-  bool valid;
-};
-
-__device__ __forceinline__ RowTile row_tile(int bid, int B, int ntiles) {
-  if (B >= kXcds) {
-    const int b8 = (B + kXcds - 1) / kXcds * kXcds;
-    return {bid % b8, bid / b8, bid % b8 < B};
-  }
-  if (kXcds % B == 0) {
-    const int per = kXcds / B, x = bid % kXcds, tile = (bid / kXcds) * per + x % per;
-    return {x / per, tile, tile < ntiles};
-  }
-  return {bid / ntiles, bid % ntiles, true};
-}
-
-inline int row_tile_blocks(int B, int ntiles) {
-  if (B >= kXcds) return (B + kXcds - 1) / kXcds * kXcds * ntiles;
-  if (kXcds % B == 0) {
-    const int per = kXcds / B;
-    return kXcds * ((ntiles + per - 1) / per);
-  }
-  return B * ntiles;
-}
 
 
 // Store N (4 or 8) consecutive values to LDS as T with one vector write (dst aligned to N * sizeof(T)).
@@ -1820,13 +1786,7 @@ constexpr int apply_wide_occupancy() {
 // ids reach the XCDs round-robin).  The resident workgroups of an XCD then cover about one block,
 // 2 kApplyBlock slabs per layer, where tiles dealt round-robin in row-major order spread over ~55
 // slabs per layer at the config-3 shape and missed L2 on more than half of the slab reads.
-constexpr int kApplyBlock = 8;
-
-// the position in that list of workgroup `bid` of a grid of exactly `total` workgroups
-__device__ __forceinline__ int xcd_contiguous(int bid, int total) {
-  const int x = bid % kXcds, base = total / kXcds, extra = total % kXcds;
-  return x * base + min(x, extra) + bid / kXcds;
-}
+constexpr int kApplyBlock = 8;  // the list's position of a workgroup: xcd_contiguous
 
 // tile q of an R x C tile matrix listed in kApplyBlock x kApplyBlock blocks (row-major blocks,
 // row-major inside a block, ragged blocks at the right and bottom edges)

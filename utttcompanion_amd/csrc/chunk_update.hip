@@ -158,7 +158,9 @@ __global__ void __launch_bounds__(KEYS ? 512 : 256) k_up_gate_lds(const FwdArgs 
   constexpr int PER = NS * 8 / NW;            // load instructions per wave per step
   static_assert((NS * 8) % NW == 0, "the step's row groups split evenly over the waves");
   __shared__ __align__(1024) char ring[SLOTS * kSlot];
-  const int ft = blockIdx.x, b = blockIdx.y, f0 = ft * 64 * NB;
+  const RowTile rt = row_tile(blockIdx.x, a.B, a.F / (64 * NB));  // a row's tiles share its token rows
+  if (!rt.valid) return;
+  const int ft = rt.tile, b = rt.b, f0 = ft * 64 * NB;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int set = w >> 2, w4 = w & 3;  // row set: 0 token rows, 1 key rows
@@ -313,8 +315,12 @@ __global__ void __launch_bounds__(kThreads) k_down_partial_lds(const FwdArgs a, 
   constexpr int kSlot = 2 * 8192;  // H tile, W_down tile
   constexpr int PER = 4;           // 16 row groups per step over 4 waves
   __shared__ __align__(1024) char ring[kDpSlots * kSlot];
-  const int dt = blockIdx.x, split = blockIdx.y;
-  const int b = blockIdx.z % a.B, pt = blockIdx.z / a.B;
+  // groups z = (token block, row) of (D / 64) x nsplit tiles, which share the group's H rows
+  const int nD = a.D / 64;
+  const RowTile rt = row_tile(blockIdx.x, a.ntb * a.B, nD * a.nsplit);
+  if (!rt.valid) return;
+  const int dt = rt.tile % nD, split = rt.tile / nD;
+  const int b = rt.b % a.B, pt = rt.b / a.B;
   const int path = pt / a.ntb, tb = pt - path * a.ntb;
   const int d0 = dt * 64, t0 = tb * 64;
   const int nK = a.F / kb;  // F ranges in whole blocks of kb, as k_down_partial<.., kb>
@@ -1175,13 +1181,13 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
     if (L.ntb == 1) {  // one token block: the LDS-ring kernel
       if (F % 128 == 0) {
         if (a.keys != nullptr)
-          hipLaunchKernelGGL((k_up_gate_lds<true, 2>), dim3(F / 128, B), dim3(512), 0, st, f);
+          hipLaunchKernelGGL((k_up_gate_lds<true, 2>), dim3(row_tile_blocks(B, F / 128)), dim3(512), 0, st, f);
         else
-          hipLaunchKernelGGL((k_up_gate_lds<false, 2>), dim3(F / 128, B), dim3(256), 0, st, f);
+          hipLaunchKernelGGL((k_up_gate_lds<false, 2>), dim3(row_tile_blocks(B, F / 128)), dim3(256), 0, st, f);
       } else if (a.keys != nullptr) {
-        hipLaunchKernelGGL((k_up_gate_lds<true, 1>), dim3(F / 64, B), dim3(512), 0, st, f);
+        hipLaunchKernelGGL((k_up_gate_lds<true, 1>), dim3(row_tile_blocks(B, F / 64)), dim3(512), 0, st, f);
       } else {
-        hipLaunchKernelGGL((k_up_gate_lds<false, 1>), dim3(F / 64, B), dim3(256), 0, st, f);
+        hipLaunchKernelGGL((k_up_gate_lds<false, 1>), dim3(row_tile_blocks(B, F / 64)), dim3(256), 0, st, f);
       }
     } else if (D % 128 == 0) {
       hipLaunchKernelGGL((k_up_gate<T, WT, 128>), ug_grid, blk, 0, st, f);
@@ -1195,7 +1201,8 @@ static void launch_readout(const uttt_readout_args& a, char* ws, const ReadoutLa
   }
   const dim3 dp_grid(D / 64, L.nsplit, L.ntb * B);
   if constexpr (sizeof(T) == 2 && sizeof(WT) == 2)
-    hipLaunchKernelGGL(k_down_partial_lds, dp_grid, blk, 0, st, f, F % 128 == 0 ? 128 : KT);
+    hipLaunchKernelGGL(k_down_partial_lds, dim3(row_tile_blocks(L.ntb * B, (D / 64) * L.nsplit)), blk, 0, st, f,
+                       F % 128 == 0 ? 128 : KT);
   else if (wide && F % 128 == 0)
     hipLaunchKernelGGL((k_down_partial<T, WT, wide ? 128 : KT>), dp_grid, blk, 0, st, f);
   else

@@ -508,4 +508,47 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
 
 __device__ __forceinline__ float sigmoidf_acc(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// ---------------------------------------------------------------------------
+// Tile placement over the XCDs
+// ---------------------------------------------------------------------------
+// Workgroup ids reach the 8 XCDs round-robin, and each XCD has its own L2.  xcd_contiguous lists
+// a grid of exactly `total` workgroups so that XCD x takes the x-th contiguous eighth of the list
+// (workgroup bid's position in it); the eighths differ by at most one workgroup.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int xcd_contiguous(int bid, int total) {
+  const int x = bid % kXcds, base = total / kXcds, extra = total % kXcds;
+  return x * base + min(x, extra) + bid / kXcds;
+}
+
+// B rows of ntiles tiles each, where the tiles of a row share that row's activation slabs.  With
+// 1, 2 or 4 rows, row b takes the 8 / B XCDs [8 b / B, 8 (b + 1) / B), which deal its tiles
+// among themselves side by side (the grid padded to whole rounds of 8; the padding workgroups
+// are not `valid` and return before any work), so a row's slabs reach 8 / B L2s and the XCDs of a
+// row read neighbouring tiles at the same time.  Any other B: the tiles listed row by row and
+// dealt in contiguous eighths (xcd_contiguous; the grid exactly B ntiles workgroups), so a row's
+// tiles run on one or two XCDs and every XCD gets the same number of tiles within one.
+// Measured against rows interleaved over every XCD (1-7 rows) and whole rows per XCD (8 or more):
+// config 5 (1-16 rows per chunk step) 1.17-1.18 against 1.22-1.24 s, config 3 (4 rows) 520-521
+// against 524 ms, config 2 (8 rows) within run-to-run; the contiguous split at 4 rows took the
+// config-3 prefill to 551 ms.
+struct RowTile {
+  int b, tile;
+  bool valid;
+};
+
+__device__ __forceinline__ RowTile row_tile(int bid, int B, int ntiles) {
+  if (B < kXcds && kXcds % B == 0) {
+    const int per = kXcds / B, x = bid % kXcds, tile = (bid / kXcds) * per + x % per;
+    return {x / per, tile, tile < ntiles};
+  }
+  const int q = xcd_contiguous(bid, B * ntiles);
+  return {q / ntiles, q % ntiles, true};
+}
+
+inline int row_tile_blocks(int B, int ntiles) {
+  if (B < kXcds && kXcds % B == 0) return kXcds * ((ntiles + kXcds / B - 1) / (kXcds / B));
+  return B * ntiles;
+}
+
 }  // namespace uttt
