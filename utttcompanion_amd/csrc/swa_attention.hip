@@ -242,7 +242,7 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 
 template <typename T, int HD>
 __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill_args a, float* part, int nsplit,
-                                                          int tiles_per_split, int q_pad) {
+                                                          int tiles_per_split, int q_pad, int nqt) {
   constexpr int PAD = Mma16<T>::kPad;
   constexpr int LQ = HD + PAD;   // q/k rows [token][e]
   constexpr int LV = 64 + PAD;   // v^T rows [e][key], p rows [query][key]
@@ -250,10 +250,14 @@ __global__ void __launch_bounds__(kThreads) k_swa_prefill(const uttt_swa_prefill
   __shared__ __align__(16) T ks[64 * LQ];
   __shared__ __align__(16) T vt[HD * LV];
   __shared__ __align__(16) T ps[64 * LV];
-  const int qt = blockIdx.x, h = blockIdx.y;
-  const int b = blockIdx.z / nsplit, sp = blockIdx.z - b * nsplit;
+  // the workgroups of one (row, kv head) read the same keys and values: they are placed as the
+  // tiles of one row (row_tile), split fastest, then the query heads of the kv head, then q tiles
   const int rep = (int)(a.n_heads / a.n_kv_heads);
-  const int kvh = h / rep;
+  const RowTile rt = row_tile(blockIdx.x, (int)(a.batch * a.n_kv_heads), nqt * rep * nsplit);
+  if (!rt.valid) return;
+  const int b = rt.b / (int)a.n_kv_heads, kvh = rt.b - b * (int)a.n_kv_heads;
+  const int sp = rt.tile % nsplit, qt = rt.tile / (nsplit * rep);
+  const int h = kvh * rep + (rt.tile / nsplit) % rep;
   const int q0 = qt * 64;
   const int qn = (int)min((int64_t)64, a.q_len - q0);
   const int64_t p_first = a.q_offset + q0, p_last = a.q_offset + q0 + qn - 1;
@@ -967,9 +971,9 @@ __global__ void __launch_bounds__(kThreads) k_swa_decode_combine(const uttt_swa_
 template <typename T, int HD>
 static void launch_prefill(const uttt_swa_prefill_args& a, const PrefillPlan& p, hipStream_t st) {
   float* part = static_cast<float*>(a.workspace);
-  const dim3 grid((unsigned)p.nqt, (unsigned)a.n_heads, (unsigned)(a.batch * p.nsplit));
+  const dim3 grid((unsigned)row_tile_blocks((int)(a.batch * a.n_kv_heads), p.nqt * (int)(a.n_heads / a.n_kv_heads) * p.nsplit));
   hipLaunchKernelGGL((k_swa_prefill<T, HD>), grid, dim3(kThreads), 0, st, a, part, p.nsplit, p.tiles_per_split,
-                     p.q_pad);
+                     p.q_pad, p.nqt);
   if (p.nsplit > 1)
     hipLaunchKernelGGL((k_swa_prefill_combine<T, HD>),
                        dim3((unsigned)((int64_t)p.q_pad * HD / (kThreads * kCombineEpt)), (unsigned)a.n_heads,
@@ -1058,7 +1062,8 @@ extern "C" int uttt_swa_prefill(const uttt_swa_prefill_args* a, uttt_stream_t st
                    a->k_stride_t * 64 * 4 <= 0x7fffffffLL && a->v_stride_t * 64 * 4 <= 0x7fffffffLL,
                "k/v token strides must cover a row and fit a 64-row buffer range");
   const PrefillPlan p = prefill_plan(a->batch, a->n_heads, a->q_len, a->kv_len, a->window);
-  UTTT_REQUIRE(a->batch * p.nsplit <= 65535, "batch too large for the attention grid");
+  UTTT_REQUIRE(a->batch * p.nsplit <= 65535 && a->batch * a->n_heads * p.nqt * p.nsplit + 8LL * a->n_heads <= 0x7fffffffLL,
+               "batch too large for the attention grid");
   UTTT_REQUIRE(p.nsplit == 1 || (a->workspace != nullptr &&
                                  a->workspace_bytes >= uttt_swa_prefill_workspace(a->batch, a->n_heads, a->q_len,
                                                                                   a->kv_len, a->head_dim, a->window)),
