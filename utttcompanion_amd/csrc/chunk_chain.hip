@@ -1781,12 +1781,14 @@ constexpr int apply_wide_occupancy() {
 
 // Tile order of the wide state write.  Every output tile reads, per layer, the token slabs of its
 // row block and of its column block, and the workgroups resident on one XCD (about 64) share one
-// L2.  The launch's tiles are listed row by row, matrix by matrix, in blocks of kApplyBlock x
-// kApplyBlock tiles, and XCD x takes the x-th contiguous eighth of the list in order (workgroup
-// ids reach the XCDs round-robin).  The resident workgroups of an XCD then cover about one block,
-// 2 kApplyBlock slabs per layer, where tiles dealt round-robin in row-major order spread over ~55
-// slabs per layer at the config-3 shape and missed L2 on more than half of the slab reads.
-constexpr int kApplyBlock = 8;  // the list's position of a workgroup: xcd_contiguous
+// L2.  A row's tiles are listed matrix by matrix, in blocks of kApplyBlock x kApplyBlock tiles,
+// and placed on the XCDs by row_tile (a row's 8 / B XCDs take neighbouring tiles side by side
+// for 1, 2 or 4 rows, contiguous eighths of the list otherwise).  The resident workgroups of an
+// XCD then cover about one block, 2 kApplyBlock slabs per layer, where tiles dealt round-robin in
+// row-major order spread over ~55 slabs per layer at the config-3 shape and missed L2 on more
+// than half of the slab reads (side by side instead of contiguous halves of a row: config 3
+// 519.4-520.1 against 520.6-521.3 ms).
+constexpr int kApplyBlock = 8;
 
 // tile q of an R x C tile matrix listed in kApplyBlock x kApplyBlock blocks (row-major blocks,
 // row-major inside a block, ragged blocks at the right and bottom edges)
@@ -1808,8 +1810,9 @@ k_chain_apply_wide(const ApplyChainArgs a) {
   // tiles: W_up / W_gate (D x F) take NA 64-row blocks of D by NB of F; W_down (F x D) NA of F by NB of D
   const int per_ug = (nD / NA) * (nF / NB), per_dn = (nF / NA) * (nD / NB);
   const int per_row = 2 * per_ug + per_dn;
-  const int q = xcd_contiguous(blockIdx.x, a.B * per_row);  // the grid is B x per_row workgroups
-  const int b = q / per_row, tile = q - b * per_row;
+  const RowTile pl = row_tile(blockIdx.x, a.B, per_row);  // the grid is row_tile_blocks(B, per_row)
+  if (!pl.valid) return;
+  const int b = pl.b, tile = pl.tile;
   const int m = tile < 2 * per_ug ? tile / per_ug : 2;
   const int jt = m < 2 ? tile - m * per_ug : tile - 2 * per_ug;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -2345,8 +2348,8 @@ void launch_chain(const uttt_chunk_chain_args& a, char* ws, const ChainLayout& c
         if (apply_wide_fits(D, F)) {
           const int tiles = 2 * (int)((D / (64 * kApplyNA)) * (F / (64 * kApplyNB))) +
                             (int)((F / (64 * kApplyNA)) * (D / (64 * kApplyNB)));
-          hipLaunchKernelGGL((k_chain_apply_wide<kApplyNA, kApplyNB, kApplySlotsWide>), dim3((int)B * tiles), blk, 0,
-                             st, aa);
+          hipLaunchKernelGGL((k_chain_apply_wide<kApplyNA, kApplyNB, kApplySlotsWide>), dim3(row_tile_blocks(B, tiles)),
+                             blk, 0, st, aa);
         } else {
           hipLaunchKernelGGL(k_chain_apply_lds, grid, blk, 0, st, aa);
         }
