@@ -67,8 +67,6 @@ __device__ __forceinline__ const T* layer_row(const LayerPtrs& lp, int l, int b,
   return static_cast<const T*>(lp.p[l]) + (int64_t)b * rs;
 }
 
-
-
 // Store N (4 or 8) consecutive values to LDS as T with one vector write (dst aligned to N * sizeof(T)).
 template <typename T, int N>
 __device__ __forceinline__ void store_vec(T* dst, const float* v) {
